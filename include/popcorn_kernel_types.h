@@ -1,0 +1,191 @@
+/*
+ * popcorn_kernel_types.h — kernel parameter blocks shared by the host runtime
+ * and the gfx950 kernels.
+ *
+ * Each struct keeps the field order of its counterpart in the reference's
+ * Sources/PopcornShaderTypes/PopcornKernelTypes.h (cited per struct), so a
+ * caller that packs the reference's constants packs these. Fields this build
+ * adds sit after the reference's fields and default to the reference's
+ * behaviour when zero. Fields are 4 bytes (FillNormalConstants' counters are
+ * 8); none of the structs has padding.
+ */
+#ifndef POPCORN_KERNEL_TYPES_H
+#define POPCORN_KERNEL_TYPES_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* PopcornKernelTypes.h:10-13, plus V (table rows; 0 = unchecked): an id
+ * outside [0, V) yields a zero row instead of an out-of-bounds read. */
+typedef struct {
+    uint32_t N;
+    uint32_t H;
+    uint32_t V;
+} EmbeddingGatherConstants;
+
+/* PopcornKernelTypes.h:15-18 */
+typedef struct {
+    uint32_t count;
+    float scalar;
+} ScalarMulConstants;
+
+/* PopcornKernelTypes.h:20-22 */
+typedef struct {
+    uint32_t count;
+} MulConstants;
+
+/* PopcornKernelTypes.h:24-26 */
+typedef struct {
+    uint32_t count;
+} AddConstants;
+
+/* PopcornKernelTypes.h:33-35 */
+typedef struct {
+    uint32_t count;
+} GeluTanhConstants;
+
+/* PopcornKernelTypes.h:46-51 */
+typedef struct {
+    uint32_t M;
+    uint32_t K;
+    uint32_t N;
+    uint32_t transposeB;
+} MatmulConstants;
+
+/* PopcornKernelTypes.h:53-57 */
+typedef struct {
+    uint32_t K;
+    uint32_t N;
+    uint32_t transposeW;
+} MatvecConstants;
+
+/* PopcornKernelTypes.h:72-77 */
+typedef struct {
+    uint32_t H;
+    uint32_t hasWeight;
+    uint32_t addOneToWeight;
+    float eps;
+} RMSNormConstants;
+
+/* PopcornKernelTypes.h:121-131, plus:
+ *   kvStride       rows between consecutive KV heads in K/V (0 = Sk), so a
+ *                  cache with spare capacity [B, Nkv, Smax, Hd] is read in
+ *                  place;
+ *   P              key partitions per query row (0 = 1);
+ *   keyLenFromPosition  when 1, Sk = position[0] + Sq is read from the bound
+ *                  position tensor (decode under graph replay).           */
+typedef struct {
+    uint32_t B;
+    uint32_t Nq;
+    uint32_t Nkv;
+    uint32_t Sq;
+    uint32_t Sk;
+    uint32_t Hd;
+    uint32_t maskKind;
+    int32_t slidingWindow;
+    float scale;
+    uint32_t kvStride;
+    uint32_t P;
+    uint32_t keyLenFromPosition;
+} FlashAttentionConstants;
+
+/* PopcornKernelTypes.h:133-144 (the reference's MPP tile constants; here the
+ * MFMA prefill kernel's), plus kvStride as above. */
+typedef struct {
+    uint32_t B;
+    uint32_t Nq;
+    uint32_t Nkv;
+    uint32_t Sq;
+    uint32_t Sk;
+    uint32_t Hd;
+    uint32_t qTilesPerHead;
+    uint32_t maskKind;
+    int32_t slidingWindow;
+    float scale;
+    uint32_t kvStride;
+} MPPFlashAttentionConstants;
+
+/* PopcornKernelTypes.h:146-156, plus kvStride, Sq (query rows; 0 = 1) and
+ * keyLenFromPosition as in FlashAttentionConstants. */
+typedef struct {
+    uint32_t B;
+    uint32_t Nq;
+    uint32_t Nkv;
+    uint32_t Sk;
+    uint32_t Hd;
+    uint32_t P;
+    uint32_t maskKind;
+    int32_t slidingWindow;
+    float scale;
+    uint32_t kvStride;
+    uint32_t Sq;
+    uint32_t keyLenFromPosition;
+} FlashDecodingPartialConstants;
+
+/* PopcornKernelTypes.h:158-163, plus Sq (0 = 1). */
+typedef struct {
+    uint32_t B;
+    uint32_t Nq;
+    uint32_t Hd;
+    uint32_t P;
+    uint32_t Sq;
+} FlashDecodingReduceConstants;
+
+/* PopcornKernelTypes.h:165-172, plus offsetFromPosition: when 1 the write
+ * offset is read from the bound position tensor. */
+typedef struct {
+    uint32_t B;
+    uint32_t Nkv;
+    uint32_t Snew;
+    uint32_t Smax;
+    uint32_t Hd;
+    uint32_t offset;
+    uint32_t offsetFromPosition;
+} KVCacheWriteConstants;
+
+/* PopcornKernelTypes.h:197-200, plus slices: the number of row slices the
+ * two-stage argmax splits each row into (stage 1 grid width). */
+typedef struct {
+    uint32_t rows;
+    uint32_t N;
+    uint32_t slices;
+} ArgmaxConstants;
+
+/* No counterpart in the reference: the fused gated-MLP front half
+ * (RMSNorm -> gate and up matvecs -> GELU-tanh(gate) * up), which replaces the
+ * reference's five-dispatch composition. interDataType is the storage dtype of
+ * the reference's intermediates (POPCORN_DTYPE_*): each intermediate is
+ * rounded to it exactly where the reference stores a tensor. */
+typedef struct {
+    uint32_t H;
+    uint32_t F;
+    uint32_t hasWeight;
+    uint32_t addOneToWeight;
+    float eps;
+    uint32_t interDataType;
+} GatedMLPConstants;
+
+/* No counterpart in the reference: device-side fill of synthetic inputs
+ * (counter-based normal generator) for benchmarks. */
+typedef struct {
+    uint64_t seed;
+    uint64_t count;
+    float mean;
+    float stddev;
+} FillNormalConstants;
+
+/* The decode-step position update that closes a captured decode step: the
+ * position tensor is advanced by `delta` (a kernel, so graph replays need no
+ * memset or host write). No counterpart in the reference (GemmaCLI writes the
+ * position from the CPU, Gemma4TextInference.swift:95-99). */
+typedef struct {
+    int32_t delta;
+} PositionAdvanceConstants;
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,161 @@
+// Decode-loop glue: token in (embedding gather), token out (argmax), the
+// position update that closes a captured step, and a device-side normal
+// generator for synthetic benchmark inputs.
+#include "common.hpp"
+
+namespace {
+
+// EmbeddingGather.metal:6-23: out[n, :] = table[ids[n], :]; one thread per
+// 16-byte run of a row. An id outside [0, V) (when V is given) gives zeros.
+template <typename T, typename O>
+__device__ void gather(const int32_t *__restrict__ ids, const typename T::storage *__restrict__ table,
+                       typename O::storage *__restrict__ out, const EmbeddingGatherConstants &p) {
+    constexpr uint32_t kRun = 16 / sizeof(typename T::storage);
+    const uint32_t runs = (p.H + kRun - 1) / kRun;
+    const uint64_t total = (uint64_t)p.N * runs;
+    for (uint64_t r = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; r < total; r += (uint64_t)gridDim.x * blockDim.x) {
+        const uint32_t n = (uint32_t)(r / runs), h0 = (uint32_t)(r % runs) * kRun;
+        const int32_t id = ids[n];
+        const bool ok = id >= 0 && (p.V == 0 || (uint32_t)id < p.V);
+        for (uint32_t h = h0; h < h0 + kRun && h < p.H; ++h) {
+            float v = ok ? T::load(table[(uint64_t)(uint32_t)id * p.H + h]) : 0.0f;
+            out[(uint64_t)n * p.H + h] = O::store(v);
+        }
+    }
+}
+
+// Argmax.metal:7-9: a candidate wins on a larger value, or an equal value at
+// a smaller index.
+__device__ inline bool better(float v, int32_t i, float bv, int32_t bi) { return v > bv || (v == bv && i < bi); }
+
+__device__ inline void wave_best(float &bv, int32_t &bi) {
+    for (int s = 32; s > 0; s >>= 1) {
+        float ov = __shfl_xor(bv, s, 64);
+        int32_t oi = __shfl_xor(bi, s, 64);
+        if (better(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+}
+
+__device__ void block_best(float &bv, int32_t &bi) {
+    __shared__ float sv[16];
+    __shared__ int32_t si[16];
+    wave_best(bv, bi);
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
+    if (lane == 0) {
+        sv[wave] = bv;
+        si[wave] = bi;
+    }
+    __syncthreads();
+    bv = -INFINITY;
+    bi = 0x7fffffff;
+    for (uint32_t w = 0; w < nw; ++w)
+        if (better(sv[w], si[w], bv, bi)) {
+            bv = sv[w];
+            bi = si[w];
+        }
+}
+
+}  // namespace
+
+#define GATHER(name, T, O)                                                                                \
+    POPCORN_KERNEL void __launch_bounds__(256)                                                            \
+        name(const int32_t *ids, const T::storage *table, O::storage *out, EmbeddingGatherConstants p) {  \
+        gather<T, O>(ids, table, out, p);                                                                 \
+    }
+
+using pk::BF16;
+using pk::F16;
+using pk::F32;
+
+GATHER(embedding_gather, F32, F32)
+GATHER(embedding_gather_f16, F16, F16)
+GATHER(embedding_gather_bf16, BF16, BF16)
+GATHER(embedding_gather_bf16_to_f32, BF16, F32)
+
+// Stage 1: block (slice, row) reduces its slice of the row to one candidate.
+// Grid: x = slices, y = rows. A NaN never wins (v > best is false for NaN),
+// as in the reference's sequential loop when the first element is not NaN.
+POPCORN_KERNEL void __launch_bounds__(256)
+    argmax_partial(const float *x, float *pv, int32_t *pi, ArgmaxConstants p) {
+    const uint32_t row = blockIdx.y, slices = gridDim.x;
+    const uint64_t per = ((uint64_t)p.N + slices - 1) / slices;
+    const uint64_t lo = (uint64_t)blockIdx.x * per, hi = min(lo + per, (uint64_t)p.N);
+    const float *xr = x + (uint64_t)row * p.N;
+    float bv = -INFINITY;
+    int32_t bi = 0x7fffffff;
+    for (uint64_t i = lo + threadIdx.x; i < hi; i += blockDim.x) {
+        float v = xr[i];
+        if (better(v, (int32_t)i, bv, bi)) {
+            bv = v;
+            bi = (int32_t)i;
+        }
+    }
+    block_best(bv, bi);
+    if (threadIdx.x == 0) {
+        pv[(uint64_t)row * slices + blockIdx.x] = bv;
+        pi[(uint64_t)row * slices + blockIdx.x] = bi;
+    }
+}
+
+// Stage 2: one block per row merges the p.slices candidates. The reference's
+// loop starts from x[0] (Argmax.metal:20-21), so a NaN at x[0] keeps index 0;
+// a row with no candidate (all NaN) also yields 0.
+POPCORN_KERNEL void __launch_bounds__(256)
+    argmax_finish(const float *x, const float *pv, const int32_t *pi, int32_t *indices, ArgmaxConstants p) {
+    const uint32_t row = blockIdx.x, slices = p.slices;
+    float bv = -INFINITY;
+    int32_t bi = 0x7fffffff;
+    for (uint32_t s = threadIdx.x; s < slices; s += blockDim.x) {
+        float v = pv[(uint64_t)row * slices + s];
+        int32_t i = pi[(uint64_t)row * slices + s];
+        if (better(v, i, bv, bi)) {
+            bv = v;
+            bi = i;
+        }
+    }
+    block_best(bv, bi);
+    if (threadIdx.x == 0) {
+        if (bi == 0x7fffffff || __builtin_isnan(x[(uint64_t)row * p.N])) bi = 0;
+        indices[row] = bi;
+    }
+}
+
+// pos[0] += delta: the last node of a captured decode step.
+POPCORN_KERNEL void position_advance(int32_t *pos, PositionAdvanceConstants p) {
+    if (threadIdx.x == 0 && blockIdx.x == 0) pos[0] += p.delta;
+}
+
+namespace {
+
+__device__ inline uint64_t splitmix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+// Element i takes the pair (i / 2): two uniforms from splitmix64 of the
+// pair index, Box-Muller, cos for even i and sin for odd i.
+template <typename T>
+__device__ void fill_normal(typename T::storage *out, const FillNormalConstants &p) {
+    const float two_pi = 6.283185307179586f;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < p.count; i += (uint64_t)gridDim.x * blockDim.x) {
+        const uint64_t pair = i >> 1;
+        const uint64_t h1 = splitmix64(p.seed * 0xD1B54A32D192ED03ull + 2 * pair);
+        const uint64_t h2 = splitmix64(p.seed * 0xD1B54A32D192ED03ull + 2 * pair + 1);
+        const float u1 = ((float)(h1 >> 40) + 1.0f) * (1.0f / 16777216.0f);  // (0, 1]
+        const float u2 = (float)(h2 >> 40) * (1.0f / 16777216.0f);           // [0, 1)
+        const float r = sqrtf(-2.0f * __logf(u1));
+        const float z = (i & 1) ? r * __sinf(two_pi * u2) : r * __cosf(two_pi * u2);
+        out[i] = T::store(p.mean + p.stddev * z);
+    }
+}
+
+}  // namespace
+
+POPCORN_KERNEL void __launch_bounds__(256) fill_normal_f32(float *out, FillNormalConstants p) { fill_normal<F32>(out, p); }
+POPCORN_KERNEL void __launch_bounds__(256) fill_normal_bf16(uint16_t *out, FillNormalConstants p) { fill_normal<BF16>(out, p); }
+POPCORN_KERNEL void __launch_bounds__(256) fill_normal_f16(_Float16 *out, FillNormalConstants p) { fill_normal<F16>(out, p); }

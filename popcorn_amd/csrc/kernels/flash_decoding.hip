@@ -1,0 +1,430 @@
+// Split-KV attention (FlashDecoding) and its log-sum-exp combine.
+//
+// Algorithm of Sources/Popcorn/Kernels/FlashDecoding.metal:28-231: the keys
+// of each query row are split into P partitions of per = ceil(Sk/P) keys
+// (:56-63); each partition runs the online softmax over its keys with Q
+// pre-scaled (:65-68) and writes unnormalised O with its running max m and
+// sum l (:165-173); the combine merges them with
+//   m* = max m_k, l* = sum exp(m_k - m*) l_k, O = sum exp(m_k - m*) O_k / l*
+// (:202-227). posQ = Sk - Sq + row (:73 for Sq = 1; FlashAttention.metal:72).
+// Partition outputs: O [B, Nq, Sq, P, Hd], m and l [B, Nq, Sq, P] (f32).
+//
+// Layout for gfx950 (fast path, flash_decoding_partial_<t>_l<LPK>_c<CPL>_g<G>):
+//  * one block (4 waves) per (partition, batch x KV head x head group, query
+//    row): the G query heads that share a KV head (GQA) are processed
+//    together, so each K/V byte is read once per block, not once per head;
+//  * a key row is split across LPK lanes, each holding CPL 16-byte chunks, so
+//    one wave-wide load instruction covers 64/LPK whole key rows (1 KB);
+//  * a wave takes TILE = (64/LPK) * U keys per step: U rows of K and of V per
+//    lane in flight, dot products reduced within the LPK-lane group by DPP,
+//    tile max across the wave, then p = exp(s - m) and O += p V on the
+//    lane's own dims; l and O stay group-local until the end of the range;
+//  * waves take interleaved tiles of the partition's key range; the 4 wave
+//    states are merged in LDS and written as the partition's (O, m, l).
+// Keys outside the causal / sliding-window range are skipped by clamping
+// the range; the per-key mask is still applied. A range with no allowed key
+// writes m = -inf, l = 0, O = 0 (FlashDecoding.metal:78-87); a tile whose
+// keys are all masked leaves the state unchanged instead of computing
+// exp(-inf - -inf).
+#include "common.hpp"
+
+namespace {
+
+constexpr int kWaves = 4;
+
+struct FdGeom {
+    uint32_t b, hkv, g0, gcount, qi, Sq, Sk, posQ, jLo, jHi;
+    bool empty;
+};
+
+__device__ inline bool fd_allowed(const FlashDecodingPartialConstants &p, int posQ, int posK) {
+    bool allowed = (p.maskKind == 2u) || (posK <= posQ);
+    if (p.maskKind == 1u) allowed = allowed && ((posQ - posK) < p.slidingWindow);
+    return allowed;
+}
+
+// Grid: x = partition, y = (b * Nkv + hkv) * ngroups + head group, z = row.
+__device__ inline FdGeom fd_geometry(const FlashDecodingPartialConstants &p, const int32_t *position, uint32_t gmax) {
+    FdGeom g;
+    const uint32_t G = p.Nq / p.Nkv;
+    const uint32_t ngroups = (G + gmax - 1) / gmax;
+    const uint32_t hg = blockIdx.y % ngroups;
+    const uint32_t bkv = blockIdx.y / ngroups;
+    g.b = bkv / p.Nkv;
+    g.hkv = bkv % p.Nkv;
+    g.g0 = hg * gmax;
+    g.gcount = min(gmax, G - g.g0);
+    g.qi = blockIdx.z;
+    g.Sq = p.Sq ? p.Sq : 1u;
+    const uint32_t stride = p.kvStride ? p.kvStride : p.Sk;
+    uint32_t Sk = p.Sk;
+    if (p.keyLenFromPosition) {
+        int32_t pos = position[0];
+        Sk = pos < 0 ? 0u : (uint32_t)pos + g.Sq;
+    }
+    if (Sk > stride) Sk = stride;  // never read past the cache
+    g.Sk = Sk;
+    const int posQ = (int)Sk - (int)g.Sq + (int)g.qi;
+    g.posQ = (uint32_t)max(posQ, -1);
+    const uint32_t P = p.P ? p.P : 1u;
+    const uint32_t per = (Sk + P - 1) / P;
+    int lo = (int)(blockIdx.x * per);
+    int hi = min(lo + (int)per, (int)Sk);
+    if (p.maskKind != 2u) hi = min(hi, posQ + 1);
+    if (p.maskKind == 1u) lo = max(lo, posQ - p.slidingWindow + 1);
+    g.empty = hi <= lo;
+    g.jLo = (uint32_t)max(lo, 0);
+    g.jHi = g.empty ? g.jLo : (uint32_t)hi;
+    return g;
+}
+
+// Writes one partition's state for `gcount` heads: wave states sm_* merged.
+template <int GMAX, int HD>
+__device__ void fd_merge_store(const FlashDecodingPartialConstants &p, const FdGeom &geo, float (*sm_m)[GMAX],
+                               float (*sm_l)[GMAX], float (*sm_o)[GMAX][HD], float *pO, float *pM, float *pL) {
+    const uint32_t P = p.P ? p.P : 1u;
+    const uint32_t G = p.Nq / p.Nkv;
+    for (uint32_t idx = threadIdx.x; idx < geo.gcount * HD; idx += blockDim.x) {
+        const uint32_t g = idx / HD, d = idx % HD;
+        float mstar = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) mstar = fmaxf(mstar, sm_m[w][g]);
+        float o = 0.0f, l = 0.0f;
+        if (mstar != -INFINITY) {
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) {
+                float a = pk::fast_exp(sm_m[w][g] - mstar);
+                o += a * sm_o[w][g][d];
+                l += a * sm_l[w][g];
+            }
+        }
+        const uint32_t hq = geo.hkv * G + geo.g0 + g;
+        const uint64_t slot = ((uint64_t)(geo.b * p.Nq + hq) * geo.Sq + geo.qi) * P + blockIdx.x;
+        pO[slot * HD + d] = o;
+        if (d == 0) {
+            pM[slot] = mstar;
+            pL[slot] = l;
+        }
+    }
+}
+
+template <typename T, int LPK, int CPL, int GMAX, int U>
+__device__ void fd_partial_fast(const typename T::storage *__restrict__ Q, const typename T::storage *__restrict__ K,
+                                const typename T::storage *__restrict__ V, float *__restrict__ pO,
+                                float *__restrict__ pM, float *__restrict__ pL, const int32_t *__restrict__ position,
+                                const FlashDecodingPartialConstants &p) {
+    constexpr int kV = pk::Vec<T>::kVec;
+    constexpr int DL = CPL * kV;   // dims per lane
+    constexpr int HD = LPK * DL;   // head dim
+    constexpr int KPW = 64 / LPK;  // key rows per wave-wide load
+    constexpr int TILE = KPW * U;  // keys per wave step
+
+    __shared__ float sm_m[kWaves][GMAX];
+    __shared__ float sm_l[kWaves][GMAX];
+    __shared__ float sm_o[kWaves][GMAX][HD];
+
+    const FdGeom geo = fd_geometry(p, position, GMAX);
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t kg = lane / LPK, dl = lane % LPK;
+    const uint32_t G = p.Nq / p.Nkv;
+    const uint32_t stride = p.kvStride ? p.kvStride : p.Sk;
+
+    float q[GMAX][DL], o[GMAX][DL], m[GMAX], l[GMAX];
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+        m[g] = -INFINITY;
+        l[g] = 0.0f;
+        const uint32_t gg = min((uint32_t)g, geo.gcount - 1);
+        const uint32_t hq = geo.hkv * G + geo.g0 + gg;
+        const typename T::storage *qrow = Q + ((uint64_t)(geo.b * p.Nq + hq) * geo.Sq + geo.qi) * HD;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            pk::Vec<T> v;
+            v.load(qrow + (c * LPK + dl) * kV);
+#pragma unroll
+            for (int e = 0; e < kV; ++e) {
+                q[g][c * kV + e] = v.get(e) * p.scale;
+                o[g][c * kV + e] = 0.0f;
+            }
+        }
+    }
+
+    const uint64_t kvbase = (uint64_t)(geo.b * p.Nkv + geo.hkv) * stride * HD;
+    const typename T::storage *Kh = K + kvbase;
+    const typename T::storage *Vh = V + kvbase;
+    const uint32_t nkeys = geo.jHi - geo.jLo;
+    const uint32_t ntiles = (nkeys + TILE - 1) / TILE;
+
+    for (uint32_t t = wave; t < ntiles; t += kWaves) {
+        const uint32_t j0 = geo.jLo + t * TILE;
+        pk::Vec<T> kv[U][CPL], vv[U][CPL];
+        bool valid[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t j = j0 + u * KPW + kg;
+            valid[u] = j < geo.jHi && fd_allowed(p, (int)geo.posQ, (int)j);
+            const uint32_t jj = j < geo.jHi ? j : geo.jLo;
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) {
+                kv[u][c].load_nt(Kh + (uint64_t)jj * HD + (c * LPK + dl) * kV);
+                vv[u][c].load_nt(Vh + (uint64_t)jj * HD + (c * LPK + dl) * kV);
+            }
+        }
+        float s[GMAX][U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            float kf[DL];
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) {
+#pragma unroll
+                for (int e = 0; e < kV; ++e) kf[c * kV + e] = kv[u][c].get(e);
+            }
+#pragma unroll
+            for (int g = 0; g < GMAX; ++g) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int e = 0; e < DL; ++e) acc += q[g][e] * kf[e];
+                s[g][u] = pk::group_sum<LPK>(acc);
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < GMAX; ++g) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                if (!valid[u]) s[g][u] = -INFINITY;
+                mx = fmaxf(mx, s[g][u]);
+            }
+            if constexpr (KPW > 1) {
+                // all lanes of a key group hold the same scores: reduce across groups
+                mx = pk::wave_max(mx);
+            }
+            const float m_new = fmaxf(m[g], mx);
+            if (m_new == -INFINITY) continue;  // nothing allowed yet
+            const float alpha = pk::fast_exp(m[g] - m_new);
+            float psum = 0.0f;
+            float pu[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                pu[u] = pk::fast_exp(s[g][u] - m_new);
+                psum += pu[u];
+            }
+            l[g] = alpha * l[g] + psum;
+            m[g] = m_new;
+#pragma unroll
+            for (int e = 0; e < DL; ++e) o[g][e] *= alpha;
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) {
+#pragma unroll
+                    for (int e = 0; e < kV; ++e) o[g][c * kV + e] += pu[u] * vv[u][c].get(e);
+                }
+            }
+        }
+    }
+
+    // Merge the key groups of this wave (lanes dl, dl + LPK, ...).
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+        for (int sft = LPK; sft < 64; sft <<= 1) {
+            l[g] += __shfl_xor(l[g], sft, 64);
+#pragma unroll
+            for (int e = 0; e < DL; ++e) o[g][e] += __shfl_xor(o[g][e], sft, 64);
+        }
+    }
+    if (kg == 0) {
+#pragma unroll
+        for (int g = 0; g < GMAX; ++g) {
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) {
+#pragma unroll
+                for (int e = 0; e < kV; ++e) sm_o[wave][g][(c * LPK + dl) * kV + e] = o[g][c * kV + e];
+            }
+            if (dl == 0) {
+                sm_m[wave][g] = m[g];
+                sm_l[wave][g] = l[g];
+            }
+        }
+    }
+    __syncthreads();
+    fd_merge_store<GMAX, HD>(p, geo, sm_m, sm_l, sm_o, pO, pM, pL);
+}
+
+// Any head dim <= 512 and any dtype: one query head per block (GMAX = 1),
+// lanes stride over the head dim, one key at a time per wave.
+template <typename T>
+__device__ void fd_partial_generic(const typename T::storage *__restrict__ Q, const typename T::storage *__restrict__ K,
+                                   const typename T::storage *__restrict__ V, float *__restrict__ pO,
+                                   float *__restrict__ pM, float *__restrict__ pL, const int32_t *__restrict__ position,
+                                   const FlashDecodingPartialConstants &p) {
+    constexpr int kMaxHd = 512, kDL = kMaxHd / 64;
+    __shared__ float sm_m[kWaves][1];
+    __shared__ float sm_l[kWaves][1];
+    __shared__ float sm_o[kWaves][1][kMaxHd];
+    const FdGeom geo = fd_geometry(p, position, 1);
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t Hd = p.Hd;
+    const uint32_t G = p.Nq / p.Nkv;
+    const uint32_t hq = geo.hkv * G + geo.g0;
+    const uint32_t stride = p.kvStride ? p.kvStride : p.Sk;
+    const typename T::storage *qrow = Q + ((uint64_t)(geo.b * p.Nq + hq) * geo.Sq + geo.qi) * Hd;
+    float q[kDL], o[kDL];
+#pragma unroll
+    for (int i = 0; i < kDL; ++i) {
+        uint32_t d = lane + 64 * i;
+        q[i] = d < Hd ? T::load(qrow[d]) * p.scale : 0.0f;
+        o[i] = 0.0f;
+    }
+    float m = -INFINITY, l = 0.0f;
+    const uint64_t kvbase = (uint64_t)(geo.b * p.Nkv + geo.hkv) * stride * Hd;
+    for (uint32_t j = geo.jLo + wave; j < geo.jHi; j += kWaves) {
+        if (!fd_allowed(p, (int)geo.posQ, (int)j)) continue;
+        const typename T::storage *kr = K + kvbase + (uint64_t)j * Hd;
+        const typename T::storage *vr = V + kvbase + (uint64_t)j * Hd;
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kDL; ++i) {
+            uint32_t d = lane + 64 * i;
+            if (d < Hd) acc += q[i] * T::load(kr[d]);
+        }
+        const float s = pk::wave_sum(acc);
+        const float m_new = fmaxf(m, s);
+        const float alpha = pk::fast_exp(m - m_new);
+        const float pj = pk::fast_exp(s - m_new);
+        l = alpha * l + pj;
+        m = m_new;
+#pragma unroll
+        for (int i = 0; i < kDL; ++i) {
+            uint32_t d = lane + 64 * i;
+            o[i] = alpha * o[i] + (d < Hd ? pj * T::load(vr[d]) : 0.0f);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < kDL; ++i) sm_o[wave][0][lane + 64 * i] = o[i];
+    if (lane == 0) {
+        sm_m[wave][0] = m;
+        sm_l[wave][0] = l;
+    }
+    __syncthreads();
+    const uint32_t P = p.P ? p.P : 1u;
+    for (uint32_t d = threadIdx.x; d < Hd; d += blockDim.x) {
+        float mstar = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) mstar = fmaxf(mstar, sm_m[w][0]);
+        float oo = 0.0f, ll = 0.0f;
+        if (mstar != -INFINITY) {
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) {
+                float a = pk::fast_exp(sm_m[w][0] - mstar);
+                oo += a * sm_o[w][0][d];
+                ll += a * sm_l[w][0];
+            }
+        }
+        const uint64_t slot = ((uint64_t)(geo.b * p.Nq + hq) * geo.Sq + geo.qi) * P + blockIdx.x;
+        pO[slot * Hd + d] = oo;
+        if (d == 0) {
+            pM[slot] = mstar;
+            pL[slot] = ll;
+        }
+    }
+}
+
+// LSE combine, FlashDecoding.metal:179-228: one block per (b, hq, row).
+template <typename O>
+__device__ void fd_reduce(const float *__restrict__ pO, const float *__restrict__ pM, const float *__restrict__ pL,
+                          typename O::storage *__restrict__ out, const FlashDecodingReduceConstants &p) {
+    __shared__ float w_sm[1024];
+    __shared__ float red[kWaves];
+    const uint32_t P = p.P, Hd = p.Hd;
+    const uint64_t slot = blockIdx.x;  // (b * Nq + hq) * Sq + row
+    const float *m = pM + slot * P;
+    const float *l = pL + slot * P;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+    float mx = -INFINITY;
+    for (uint32_t k = tid; k < P; k += blockDim.x) mx = fmaxf(mx, m[k]);
+    mx = pk::wave_max(mx);
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    float mstar = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    float ls = 0.0f;
+    for (uint32_t k = tid; k < P; k += blockDim.x) {
+        float w = mstar == -INFINITY ? 0.0f : pk::fast_exp(m[k] - mstar);
+        w_sm[k] = w;
+        ls += w * l[k];
+    }
+    ls = pk::wave_sum(ls);
+    if (lane == 0) red[wave] = ls;
+    __syncthreads();
+    const float lstar = red[0] + red[1] + red[2] + red[3];
+    const float inv = lstar > 0.0f ? 1.0f / lstar : 0.0f;
+    const float *o = pO + slot * P * Hd;
+    for (uint32_t d = tid; d < Hd; d += blockDim.x) {
+        float acc = 0.0f;
+        for (uint32_t k = 0; k < P; ++k) acc += w_sm[k] * o[(uint64_t)k * Hd + d];
+        out[slot * Hd + d] = O::store(acc * inv);
+    }
+}
+
+}  // namespace
+
+#define FD_FAST(name, T, LPK, CPL, G, U)                                                                   \
+    POPCORN_KERNEL void __launch_bounds__(256)                                                             \
+        name(const T::storage *q, const T::storage *k, const T::storage *v, float *pO, float *pM, float *pL, \
+             const int32_t *position, FlashDecodingPartialConstants p) {                                    \
+        fd_partial_fast<T, LPK, CPL, G, U>(q, k, v, pO, pM, pL, position, p);                               \
+    }
+
+#define FD_GENERIC(name, T)                                                                                 \
+    POPCORN_KERNEL void __launch_bounds__(256)                                                             \
+        name(const T::storage *q, const T::storage *k, const T::storage *v, float *pO, float *pM, float *pL, \
+             const int32_t *position, FlashDecodingPartialConstants p) {                                    \
+        fd_partial_generic<T>(q, k, v, pO, pM, pL, position, p);                                            \
+    }
+
+#define FD_REDUCE(name, O)                                                                                  \
+    POPCORN_KERNEL void __launch_bounds__(256)                                                             \
+        name(const float *pO, const float *pM, const float *pL, O::storage *out, FlashDecodingReduceConstants p) { \
+        fd_reduce<O>(pO, pM, pL, out, p);                                                                   \
+    }
+
+using pk::BF16;
+using pk::F16;
+using pk::F32;
+
+FD_GENERIC(flash_decoding_partial_f32, F32)
+FD_GENERIC(flash_decoding_partial_bf16, BF16)
+FD_GENERIC(flash_decoding_partial_f16, F16)
+
+FD_REDUCE(flash_decoding_reduce_f32, F32)
+FD_REDUCE(flash_decoding_reduce_bf16, BF16)
+FD_REDUCE(flash_decoding_reduce_f16, F16)
+
+// Fast path instantiations: 2-byte types (8 dims per 16B chunk):
+// Hd 64 -> LPK 8, Hd 128 -> 16, Hd 256 -> 32, Hd 512 -> 64 (CPL 1).
+// f32 (4 dims per chunk): Hd 64 -> LPK 16, 128 -> 32, 256 -> 64, 512 -> 64 with CPL 2.
+// U (key rows per lane in flight, each for K and V) shrinks as G grows to keep
+// the per-lane state (q, o for G heads) within the register file.
+#define FD_FAST_G4(T, t, LPK, CPL, U1, U2, U4)                                        \
+    FD_FAST(flash_decoding_partial_##t##_l##LPK##_c##CPL##_g1, T, LPK, CPL, 1, U1)    \
+    FD_FAST(flash_decoding_partial_##t##_l##LPK##_c##CPL##_g2, T, LPK, CPL, 2, U2)    \
+    FD_FAST(flash_decoding_partial_##t##_l##LPK##_c##CPL##_g4, T, LPK, CPL, 4, U4)
+#define FD_FAST_G(T, t, LPK, CPL, U1, U2, U4, U8) \
+    FD_FAST_G4(T, t, LPK, CPL, U1, U2, U4)         \
+    FD_FAST(flash_decoding_partial_##t##_l##LPK##_c##CPL##_g8, T, LPK, CPL, 8, U8)
+
+// Head dim 512 stops at G = 4 (the LDS merge buffer is 4 x G x Hd floats).
+FD_FAST_G(BF16, bf16, 8, 1, 2, 2, 2, 1)
+FD_FAST_G(BF16, bf16, 16, 1, 4, 4, 2, 1)
+FD_FAST_G(BF16, bf16, 32, 1, 8, 8, 4, 2)
+FD_FAST_G4(BF16, bf16, 64, 1, 8, 8, 4)
+FD_FAST_G(F16, f16, 8, 1, 2, 2, 2, 1)
+FD_FAST_G(F16, f16, 16, 1, 4, 4, 2, 1)
+FD_FAST_G(F16, f16, 32, 1, 8, 8, 4, 2)
+FD_FAST_G4(F16, f16, 64, 1, 8, 8, 4)
+FD_FAST_G(F32, f32, 16, 1, 2, 2, 2, 1)
+FD_FAST_G(F32, f32, 32, 1, 4, 4, 2, 1)
+FD_FAST_G(F32, f32, 64, 1, 8, 8, 4, 2)
+FD_FAST_G4(F32, f32, 64, 2, 4, 4, 2)

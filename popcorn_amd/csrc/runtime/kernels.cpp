@@ -1,0 +1,663 @@
+// Kernels.* operation descriptors: validation and routing of the reference's
+// Swift descriptors (Sources/Popcorn/Kernels/*.swift, cited per descriptor),
+// with dispatch geometry chosen for wave64 and the device's CU count.
+#include <algorithm>
+#include <cstring>
+
+#include "popcorn.hpp"
+
+namespace popcorn {
+namespace {
+
+constexpr int kBlock = 256;
+
+int deviceCUs() {
+    static thread_local int cached_dev = -1, cached_cus = 256;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        (void)hipGetLastError();
+        return cached_cus;
+    }
+    if (dev != cached_dev) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0) cached_cus = cus;
+        (void)hipGetLastError();
+        cached_dev = dev;
+    }
+    return cached_cus;
+}
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+bool isFloat(DataType t) { return t == DataType::f32 || t == DataType::f16 || t == DataType::bf16; }
+
+void requireElements(const Tensor &t, int64_t n, const char *what) {
+    if (n < 0) throw Error::invalidArgument(std::string(what) + ": negative size");
+    if (n > 0 && !t.data) throw Error::invalidArgument(std::string(what) + ": null data pointer");
+    if (t.shape.elementCount() < n)
+        throw Error::tensorShapeMismatch(std::string(what) + " holds " + std::to_string(t.shape.elementCount()) +
+                                         " elements; the operation reads or writes " + std::to_string(n) + ".");
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// A single dispatch whose function, bindings, constants and geometry are all
+// fixed at init (the common case of the reference's DispatchKernel structs).
+class FixedDispatch : public DispatchKernel {
+public:
+    FixedDispatch(std::string fn, std::vector<Binding> b, std::vector<std::vector<uint8_t>> c, DispatchSize ds)
+        : fn_(std::move(fn)), b_(std::move(b)), c_(std::move(c)), ds_(ds) {}
+    std::string functionName() const override { return fn_; }
+    std::vector<Binding> tensors() const override { return b_; }
+    std::vector<std::vector<uint8_t>> constants() const override { return c_; }
+    DispatchSize dispatchSize(const FunctionAttributes &) const override { return ds_; }
+
+private:
+    std::string fn_;
+    std::vector<Binding> b_;
+    std::vector<std::vector<uint8_t>> c_;
+    DispatchSize ds_;
+};
+
+DispatchSize grid1(int64_t blocks, int threads, size_t lds = 0) {
+    DispatchSize d;
+    d.grid = dim3((unsigned)std::max<int64_t>(blocks, 0), 1, 1);
+    d.block = dim3((unsigned)threads, 1, 1);
+    d.dynamicLds = lds;
+    return d;
+}
+
+const char *tag(DataType t) { return name(t); }
+
+// ---------------------------------------------------------------------------
+// FlashAttention / FlashDecoding (FlashAttention.swift, FlashDecoding.swift)
+// ---------------------------------------------------------------------------
+
+struct AttnDims {
+    int64_t B, Nq, Nkv, Sq, Sk, Hd, cap;
+};
+
+class FlashAttentionKernel : public Kernel {
+public:
+    FlashAttentionKernel(const Tensor &q, const Tensor &k, const Tensor &v, const Tensor &out, AttnDims d, float scale,
+                         AttentionMask mask, const Tensor *position)
+        : q_(q), k_(k), v_(v), out_(out), d_(d), scale_(scale), mask_(mask), hasPos_(position != nullptr) {
+        if (position) pos_ = *position;
+        // FlashAttention.swift:27-36
+        if (d.Nkv <= 0 || d.Nq % d.Nkv != 0)
+            throw Error::tensorShapeMismatch("FlashAttention query heads must be divisible by KV heads; got " +
+                                             std::to_string(d.Nq) + " and " + std::to_string(d.Nkv) + ".");
+        if (d.Hd > 512)
+            throw Error::tensorShapeMismatch("FlashAttention head dim must be <= 512 (kernel limit); got " +
+                                             std::to_string(d.Hd) + ".");
+        if (d.B <= 0 || d.Nq <= 0 || d.Sq <= 0 || d.Hd <= 0 || d.Sk < 0)
+            throw Error::tensorShapeMismatch("FlashAttention dimensions must be positive.");
+        if (d.cap < d.Sk) throw Error::tensorShapeMismatch("FlashAttention key capacity is smaller than the key length.");
+        if (mask.kind > 2) throw Error::invalidArgument("unknown attention mask kind");
+        // FlashDecoding.swift:119-125 and :199-205, FlashAttention.swift:181-190,
+        // extended with f16; Q, K and V share one dtype.
+        if (!(q.dataType == k.dataType && k.dataType == v.dataType && isFloat(q.dataType) && isFloat(out.dataType)))
+            throw Error::unsupportedDataTypeCombination(std::string("Unsupported FlashAttention data type combination: ") +
+                                                        tag(q.dataType) + ", " + tag(k.dataType) + ", " + tag(out.dataType) + ".");
+        requireElements(q, d.B * d.Nq * d.Sq * d.Hd, "FlashAttention q");
+        requireElements(k, d.B * d.Nkv * d.cap * d.Hd, "FlashAttention k");
+        requireElements(v, d.B * d.Nkv * d.cap * d.Hd, "FlashAttention v");
+        requireElements(out, d.B * d.Nq * d.Sq * d.Hd, "FlashAttention out");
+        if (hasPos_) {
+            if (pos_.dataType != DataType::i32) throw Error::unsupportedDataTypeCombination("position tensor must be i32");
+            requireElements(pos_, 1, "position");
+        }
+        path_ = Kernels::route(d.Sq, d.Hd, q.dataType);
+        planSplit();
+    }
+
+    std::vector<Binding> tensors() const override {
+        std::vector<Binding> b = {{q_, kRead}, {k_, kRead}, {v_, kRead}, {out_, kWrite}};
+        if (hasPos_) b.push_back({pos_, kRead});
+        return b;
+    }
+
+    std::string describe() const override { return partialName_ + "," + reduceName_; }
+
+    void encode(KernelCommandEncoder &enc) const override {
+        // FlashDecoding.swift:54-73: borrow partial O, m, l; partial; combine.
+        const int64_t slots = d_.B * d_.Nq * d_.Sq * P_;
+        enc.withTemporaryTensor(ScratchSpec{{slots, d_.Hd}, DataType::f32}, [&](Tensor pO) {
+            enc.withTemporaryTensor(ScratchSpec{{slots}, DataType::f32}, [&](Tensor pM) {
+                enc.withTemporaryTensor(ScratchSpec{{slots}, DataType::f32}, [&](Tensor pL) {
+                    FlashDecodingPartialConstants pc{};
+                    pc.B = (uint32_t)d_.B;
+                    pc.Nq = (uint32_t)d_.Nq;
+                    pc.Nkv = (uint32_t)d_.Nkv;
+                    pc.Sk = (uint32_t)d_.Sk;
+                    pc.Hd = (uint32_t)d_.Hd;
+                    pc.P = (uint32_t)P_;
+                    pc.maskKind = mask_.kind;
+                    pc.slidingWindow = mask_.kind == 1 ? mask_.window : -1;
+                    pc.scale = scale_;
+                    pc.kvStride = (uint32_t)d_.cap;
+                    pc.Sq = (uint32_t)d_.Sq;
+                    pc.keyLenFromPosition = hasPos_ ? 1u : 0u;
+                    DispatchSize ds;
+                    ds.grid = dim3((unsigned)P_, (unsigned)(d_.B * d_.Nkv * ngroups_), (unsigned)d_.Sq);
+                    ds.block = dim3(kBlock, 1, 1);
+                    // the position binding is read only when keyLenFromPosition
+                    Tensor posOrDummy = hasPos_ ? pos_ : q_;
+                    FixedDispatch partial(partialName_,
+                                          {{q_, kRead}, {k_, kRead}, {v_, kRead}, {pO, kWrite}, {pM, kWrite}, {pL, kWrite},
+                                           {posOrDummy, kRead}},
+                                          {bytesOf(pc)}, ds);
+                    enc.dispatch(partial);
+                    FlashDecodingReduceConstants rc{};
+                    rc.B = (uint32_t)d_.B;
+                    rc.Nq = (uint32_t)d_.Nq;
+                    rc.Hd = (uint32_t)d_.Hd;
+                    rc.P = (uint32_t)P_;
+                    rc.Sq = (uint32_t)d_.Sq;
+                    FixedDispatch reduce(reduceName_, {{pO, kRead}, {pM, kRead}, {pL, kRead}, {out_, kWrite}},
+                                         {bytesOf(rc)}, grid1(d_.B * d_.Nq * d_.Sq, kBlock));
+                    enc.dispatch(reduce);
+                });
+            });
+        });
+    }
+
+private:
+    void planSplit() {
+        const DataType t = q_.dataType;
+        const int64_t G = d_.Nq / d_.Nkv;
+        const int es = stride(t);
+        const int kV = 16 / es;
+        int lpk = 0, cpl = 1;
+        const bool alignedOk = aligned16(q_.data) && aligned16(k_.data) && aligned16(v_.data);
+        if (alignedOk && d_.Hd % kV == 0) {
+            const int64_t chunks = d_.Hd / kV;
+            if (chunks == 8 || chunks == 16 || chunks == 32 || chunks == 64) lpk = (int)chunks;
+            if (chunks == 128 && t == DataType::f32) {
+                lpk = 64;
+                cpl = 2;
+            }
+            if (t == DataType::f32 && chunks == 8) lpk = 0;  // f32 Hd 32: generic
+        }
+        int gmax = 1;
+        if (lpk) {
+            gmax = G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : 8;
+            if (d_.Hd == 512 && gmax > 4) gmax = 4;  // 4 waves x G x Hd f32 of LDS stays <= 32 KB
+            partialName_ = std::string("flash_decoding_partial_") + tag(t) + "_l" + std::to_string(lpk) + "_c" +
+                           std::to_string(cpl) + "_g" + std::to_string(gmax);
+        } else {
+            partialName_ = std::string("flash_decoding_partial_") + tag(t);
+        }
+        reduceName_ = std::string("flash_decoding_reduce_") + tag(out_.dataType);
+        ngroups_ = cdiv(G, gmax);
+        // Partitions: enough blocks to cover every CU twice, but at least 64
+        // keys per block (the reference fixes P = 8, FlashDecoding.swift:77).
+        const int64_t keys = std::max<int64_t>(hasPos_ ? d_.cap : d_.Sk, 1);
+        const int64_t base = d_.B * d_.Nkv * ngroups_ * d_.Sq;
+        const int64_t want = cdiv(2 * deviceCUs(), base);
+        const int64_t maxByKeys = cdiv(keys, 64);
+        P_ = std::clamp<int64_t>(std::min(want, maxByKeys), 1, 1024);
+    }
+
+    Tensor q_, k_, v_, out_, pos_;
+    AttnDims d_;
+    float scale_;
+    AttentionMask mask_;
+    bool hasPos_;
+    Kernels::AttentionPath path_ = Kernels::AttentionPath::plain;
+    std::string partialName_, reduceName_;
+    int64_t ngroups_ = 1, P_ = 1;
+};
+
+// ---------------------------------------------------------------------------
+// Matmul (Matmul.swift)
+// ---------------------------------------------------------------------------
+
+std::string matvecNKName(DataType x, DataType w, DataType o) {
+    using D = DataType;
+    // Matmul.swift:362-374, plus f16 triples
+    if (x == D::f32 && w == D::f32 && o == D::f32) return "matvec_nk_simd_f32_f32_f32";
+    if (x == D::f32 && w == D::bf16 && o == D::f32) return "matvec_nk_simd_f32_bf16_f32";
+    if (x == D::bf16 && w == D::bf16 && o == D::f32) return "matvec_nk_simd_bf16_bf16_f32";
+    if (x == D::bf16 && w == D::bf16 && o == D::bf16) return "matvec_nk_simd_bf16_bf16_bf16";
+    if (x == D::f32 && w == D::f16 && o == D::f32) return "matvec_nk_simd_f32_f16_f32";
+    if (x == D::f16 && w == D::f16 && o == D::f32) return "matvec_nk_simd_f16_f16_f32";
+    if (x == D::f16 && w == D::f16 && o == D::f16) return "matvec_nk_simd_f16_f16_f16";
+    return "";
+}
+
+std::string plainName(const char *base, DataType x, DataType w, DataType o) {
+    using D = DataType;
+    std::string b = base;
+    // Matmul.swift:222-229 and :381-388, plus f16 triples
+    if (x == D::f32 && w == D::f32 && o == D::f32) return b;
+    if (x == D::f32 && w == D::f16 && o == D::f32) return b + "_f16";
+    if (x == D::f32 && w == D::bf16 && o == D::f32) return b + "_bf16";
+    if (x == D::bf16 && w == D::bf16 && o == D::f32) return b + "_bf16_bf16_f32";
+    if (x == D::bf16 && w == D::bf16 && o == D::bf16) return b + "_bf16_bf16_bf16";
+    if (x == D::f16 && w == D::f16 && o == D::f32) return b + "_f16_f16_f32";
+    if (x == D::f16 && w == D::f16 && o == D::f16) return b + "_f16_f16_f16";
+    return "";
+}
+
+// Rows per wave for the NK matvec: the largest R in {4, 2, 1} that still
+// launches at least two blocks (of 4 waves) per CU.
+int matvecRows(int64_t N) {
+    const int64_t target = 2 * deviceCUs();
+    for (int R : {4, 2}) {
+        if (cdiv(N, 4 * R) >= target) return R;
+    }
+    return 1;
+}
+
+constexpr int64_t kMaxStagedK = 16384;  // x staged as f32 in 64 KB of LDS
+
+std::unique_ptr<Kernel> makeMatmul(const Tensor &a, const Tensor &b, const Tensor &c, int64_t m, int64_t k, int64_t n,
+                                   bool transposeB) {
+    if (m < 0 || k < 0 || n < 0) throw Error::tensorShapeMismatch("Matmul dimensions must be non-negative.");
+    requireElements(a, m * k, "Matmul a");
+    requireElements(b, k * n, "Matmul b");
+    requireElements(c, m * n, "Matmul c");
+    std::vector<Binding> binds = {{a, kRead}, {b, kRead}, {c, kWrite}};
+    if (m == 1) {
+        // Matmul.swift:233-277
+        MatvecConstants mc{(uint32_t)k, (uint32_t)n, transposeB ? 1u : 0u};
+        if (transposeB) {
+            std::string fn = matvecNKName(a.dataType, b.dataType, c.dataType);
+            if (fn.empty())
+                throw Error::unsupportedDataTypeCombination(std::string("Unsupported matvec data type combination: ") +
+                                                            tag(a.dataType) + ", " + tag(b.dataType) + ", " + tag(c.dataType) + ".");
+            if (k > kMaxStagedK) throw Error::tensorShapeMismatch("matvec K above " + std::to_string(kMaxStagedK) + " is not supported.");
+            const int R = matvecRows(n);
+            if (R != 4) fn += "_r" + std::to_string(R);
+            return std::make_unique<FixedDispatch>(fn, binds, std::vector<std::vector<uint8_t>>{bytesOf(mc)},
+                                                   grid1(cdiv(n, 4 * R), kBlock, (size_t)std::max<int64_t>(k, 1) * 4));
+        }
+        std::string fn = plainName("matvec", a.dataType, b.dataType, c.dataType);
+        if (fn.empty())
+            throw Error::unsupportedDataTypeCombination(std::string("Unsupported matvec data type combination: ") +
+                                                        tag(a.dataType) + ", " + tag(b.dataType) + ", " + tag(c.dataType) + ".");
+        return std::make_unique<FixedDispatch>(fn, binds, std::vector<std::vector<uint8_t>>{bytesOf(mc)}, grid1(cdiv(n, kBlock), kBlock));
+    }
+    std::string fn = plainName("matmul", a.dataType, b.dataType, c.dataType);
+    if (fn.empty())
+        throw Error::unsupportedDataTypeCombination(std::string("Unsupported matmul data type combination: ") +
+                                                    tag(a.dataType) + ", " + tag(b.dataType) + ", " + tag(c.dataType) + ".");
+    MatmulConstants mc{(uint32_t)m, (uint32_t)k, (uint32_t)n, transposeB ? 1u : 0u};
+    DispatchSize ds;
+    ds.grid = dim3((unsigned)cdiv(n, 64), (unsigned)cdiv(m, 64), 1);
+    ds.block = dim3(kBlock, 1, 1);
+    return std::make_unique<FixedDispatch>(fn, binds, std::vector<std::vector<uint8_t>>{bytesOf(mc)}, ds);
+}
+
+// ---------------------------------------------------------------------------
+// Gated MLP (Gemma4TextInference.swift:416-429 as two dispatches)
+// ---------------------------------------------------------------------------
+
+class GatedMLPKernel : public Kernel {
+public:
+    GatedMLPKernel(const Tensor &x, const Tensor *nw, const Tensor &wg, const Tensor &wu, const Tensor &wd, const Tensor &out,
+                   float eps, bool addOne, const Tensor *hidden)
+        : x_(x), wg_(wg), wu_(wu), wd_(wd), out_(out), eps_(eps), addOne_(addOne) {
+        if (nw) {
+            nw_ = *nw;
+            hasNorm_ = true;
+        }
+        if (hidden) {
+            h_ = *hidden;
+            hasHidden_ = true;
+        }
+        if (wg.shape.rank() != 2) throw Error::tensorInvalidRank(2, wg.shape.rank());
+        F_ = wg.shape[0];
+        H_ = wg.shape[1];
+        if (wu.shape != wg.shape) throw Error::tensorShapeMismatch("GatedMLP up weight shape must match gate weight " + wg.shape.str() + ".");
+        if (wd.shape != Shape({H_, F_})) throw Error::tensorShapeMismatch("GatedMLP down weight must be [" + std::to_string(H_) + ", " + std::to_string(F_) + "].");
+        if (x.shape.rank() < 1 || x.shape.dims.back() != H_ || x.shape.elementCount() != H_)
+            throw Error::tensorShapeMismatch("GatedMLP decodes one row: x must hold [" + std::to_string(H_) + "].");
+        if (out.shape != x.shape) throw Error::tensorShapeMismatch("GatedMLP output shape must match x.");
+        const DataType t = x.dataType;
+        if (!isFloat(t) || wg.dataType != t || wu.dataType != t || wd.dataType != t || out.dataType != t)
+            throw Error::unsupportedDataTypeCombination("GatedMLP needs x, weights and out of one float dtype.");
+        if (hasNorm_) {
+            if (nw_.dataType != DataType::f32) throw Error::unsupportedDataTypeCombination("GatedMLP norm weight must be f32.");
+            requireElements(nw_, H_, "GatedMLP norm weight");
+        }
+        if (hasHidden_) {
+            if (h_.dataType != t) throw Error::unsupportedDataTypeCombination("GatedMLP hidden must have x's dtype.");
+            requireElements(h_, F_, "GatedMLP hidden");
+        }
+        if (H_ > kMaxStagedK || F_ > kMaxStagedK) throw Error::tensorShapeMismatch("GatedMLP H and F must be <= 16384.");
+        requireElements(x, H_, "x");
+        requireElements(wg, F_ * H_, "w_gate");
+        requireElements(wu, F_ * H_, "w_up");
+        requireElements(wd, H_ * F_, "w_down");
+        R_ = cdiv(F_, 8) >= 2 * deviceCUs() ? 2 : 1;
+        gateUpName_ = std::string("gated_mlp_gate_up_") + tag(t) + (R_ == 1 ? "_r1" : "");
+        down_ = makeMatmul(wd_, wd_, out_, 1, F_, H_, true);  // name/geometry probe only
+    }
+
+    std::vector<Binding> tensors() const override {
+        std::vector<Binding> b = {{x_, kRead}, {wg_, kRead}, {wu_, kRead}, {wd_, kRead}, {out_, kWrite}};
+        if (hasNorm_) b.push_back({nw_, kRead});
+        if (hasHidden_) b.push_back({h_, kWrite});
+        return b;
+    }
+
+    std::string describe() const override { return gateUpName_ + "," + down_->describe(); }
+
+    void encode(KernelCommandEncoder &enc) const override {
+        auto run = [&](const Tensor &h) {
+            GatedMLPConstants gc{(uint32_t)H_, (uint32_t)F_, hasNorm_ ? 1u : 0u, addOne_ ? 1u : 0u, eps_,
+                                 (uint32_t)x_.dataType};
+            const Tensor normOrDummy = hasNorm_ ? nw_ : x_;
+            FixedDispatch gu(gateUpName_, {{x_, kRead}, {normOrDummy, kRead}, {wg_, kRead}, {wu_, kRead}, {h, kWrite}},
+                             {bytesOf(gc)}, grid1(cdiv(F_, 4 * R_), kBlock, (size_t)H_ * 4));
+            enc.dispatch(gu);
+            auto down = makeMatmul(h, wd_, out_, 1, F_, H_, true);
+            down->encode(enc);
+        };
+        if (hasHidden_) {
+            run(h_);
+        } else {
+            enc.withTemporaryTensor(ScratchSpec{{F_}, x_.dataType}, [&](Tensor h) { run(h); });
+        }
+    }
+
+private:
+    Tensor x_, nw_, wg_, wu_, wd_, out_, h_;
+    float eps_;
+    bool addOne_, hasNorm_ = false, hasHidden_ = false;
+    int64_t H_ = 0, F_ = 0, R_ = 2;
+    std::string gateUpName_;
+    std::unique_ptr<Kernel> down_;
+};
+
+// ---------------------------------------------------------------------------
+// Argmax (Argmax.swift) as two stages over row slices
+// ---------------------------------------------------------------------------
+
+class ArgmaxKernel : public Kernel {
+public:
+    ArgmaxKernel(const Tensor &x, const Tensor &indices, int64_t rows, int64_t n) : x_(x), idx_(indices), rows_(rows), n_(n) {
+        if (x.dataType != DataType::f32) throw Error::unsupportedDataTypeCombination("Argmax reads f32 values.");
+        if (indices.dataType != DataType::i32) throw Error::unsupportedDataTypeCombination("Argmax indices are i32.");
+        if (n <= 0) throw Error::tensorShapeMismatch("Argmax needs a non-empty axis.");
+        requireElements(x, rows * n, "Argmax x");
+        requireElements(indices, rows, "Argmax indices");
+        slices_ = std::clamp<int64_t>(cdiv(n, 4096), 1, 256);
+    }
+    std::vector<Binding> tensors() const override { return {{x_, kRead}, {idx_, kWrite}}; }
+    std::string describe() const override { return "argmax_partial,argmax_finish"; }
+    void encode(KernelCommandEncoder &enc) const override {
+        if (rows_ == 0) return;
+        ArgmaxConstants ac{(uint32_t)rows_, (uint32_t)n_, (uint32_t)slices_};
+        enc.withTemporaryTensor(ScratchSpec{{rows_ * slices_}, DataType::f32}, [&](Tensor pv) {
+            enc.withTemporaryTensor(ScratchSpec{{rows_ * slices_}, DataType::i32}, [&](Tensor pi) {
+                DispatchSize ds;
+                ds.grid = dim3((unsigned)slices_, (unsigned)rows_, 1);
+                ds.block = dim3(kBlock, 1, 1);
+                FixedDispatch s1("argmax_partial", {{x_, kRead}, {pv, kWrite}, {pi, kWrite}}, {bytesOf(ac)}, ds);
+                enc.dispatch(s1);
+                FixedDispatch s2("argmax_finish", {{x_, kRead}, {pv, kRead}, {pi, kRead}, {idx_, kWrite}}, {bytesOf(ac)},
+                                 grid1(rows_, kBlock));
+                enc.dispatch(s2);
+            });
+        });
+    }
+
+private:
+    Tensor x_, idx_;
+    int64_t rows_, n_, slices_ = 1;
+};
+
+std::unique_ptr<Kernel> elementwise(const char *base, const Tensor &a, const Tensor *b, const Tensor &out,
+                                    std::vector<uint8_t> consts) {
+    if (!isFloat(a.dataType)) throw Error::unsupportedDataTypeCombination(std::string("Unsupported ") + base + " data type: " + tag(a.dataType) + ".");
+    if (out.dataType != a.dataType || (b && b->dataType != a.dataType))
+        throw Error::unsupportedDataTypeCombination(std::string(base) + " needs one dtype for inputs and output.");
+    const int64_t count = a.shape.elementCount();
+    requireElements(a, count, base);
+    requireElements(out, count, base);
+    if (b) requireElements(*b, count, base);
+    std::string fn = base;
+    if (a.dataType != DataType::f32) fn += std::string("_") + tag(a.dataType);
+    std::vector<Binding> binds = {{a, kRead}};
+    if (b) binds.push_back({*b, kRead});
+    binds.push_back({out, kWrite});
+    const int64_t blocks = std::clamp<int64_t>(cdiv(cdiv(count, 16 / stride(a.dataType)), kBlock), 1, 8 * deviceCUs());
+    return std::make_unique<FixedDispatch>(fn, binds, std::vector<std::vector<uint8_t>>{std::move(consts)}, grid1(blocks, kBlock));
+}
+
+}  // namespace
+
+namespace Kernels {
+
+// FlashAttention.swift:109-113. `tiled` (MFMA prefill) takes the MPP path's
+// place once it exists for the dtype and head dim; until then plain.
+AttentionPath route(int64_t queryLen, int64_t headDim, DataType qType) {
+    (void)headDim;
+    (void)qType;
+    if (queryLen == 1) return AttentionPath::decoding;
+    return AttentionPath::plain;
+}
+
+// FlashAttention.swift:51-90
+std::unique_ptr<Kernel> FlashAttention(const Tensor &q, const Tensor &k, const Tensor &v, const Tensor &out, float scale,
+                                       AttentionMask mask) {
+    if (q.shape.rank() != 4) throw Error::tensorInvalidRank(4, q.shape.rank());
+    if (k.shape.rank() != 4) throw Error::tensorInvalidRank(4, k.shape.rank());
+    if (v.shape.rank() != 4) throw Error::tensorInvalidRank(4, v.shape.rank());
+    const int64_t B = q.shape[0], Nq = q.shape[1], Sq = q.shape[2], Hd = q.shape[3];
+    const int64_t Nkv = k.shape[1], Sk = k.shape[2];
+    if (k.shape[0] != B || k.shape[3] != Hd)
+        throw Error::tensorShapeMismatch("FlashAttention K shape must match Q batch/headDim; q " + q.shape.str() + ", k " + k.shape.str() + ".");
+    if (v.shape != k.shape)
+        throw Error::tensorShapeMismatch("FlashAttention V shape must match K; v " + v.shape.str() + ", k " + k.shape.str() + ".");
+    if (out.shape != Shape({B, Nq, Sq, Hd}))
+        throw Error::tensorShapeMismatch("FlashAttention output shape must be " + Shape({B, Nq, Sq, Hd}).str() + "; got " + out.shape.str() + ".");
+    return std::make_unique<FlashAttentionKernel>(q, k, v, out, AttnDims{B, Nq, Nkv, Sq, Sk, Hd, Sk}, scale, mask, nullptr);
+}
+
+// FlashAttention.swift:13-49, plus key capacity and position
+std::unique_ptr<Kernel> FlashAttention(const Tensor &q, const Tensor &k, const Tensor &v, const Tensor &out, int64_t batch,
+                                       int64_t queryHeads, int64_t kvHeads, int64_t queryLen, int64_t keyLen, int64_t headDim,
+                                       float scale, AttentionMask mask, int64_t keyCapacity, const Tensor *position) {
+    const int64_t cap = keyCapacity > 0 ? keyCapacity : keyLen;
+    return std::make_unique<FlashAttentionKernel>(q, k, v, out, AttnDims{batch, queryHeads, kvHeads, queryLen, keyLen, headDim, cap},
+                                                  scale, mask, position);
+}
+
+// Matmul.swift:68-93
+std::unique_ptr<Kernel> Matmul(const Tensor &a, const Tensor &b, const Tensor &c, bool transposeB) {
+    if (a.shape.rank() != 2) throw Error::tensorInvalidRank(2, a.shape.rank());
+    if (b.shape.rank() != 2) throw Error::tensorInvalidRank(2, b.shape.rank());
+    if (c.shape.rank() != 2) throw Error::tensorInvalidRank(2, c.shape.rank());
+    const int64_t m = a.shape[0], k = a.shape[1];
+    const int64_t n = transposeB ? b.shape[0] : b.shape[1];
+    const Shape expectedB = transposeB ? Shape({n, k}) : Shape({k, n});
+    if (b.shape != expectedB)
+        throw Error::tensorShapeMismatch("Matmul RHS shape mismatch: expected " + expectedB.str() + ", got " + b.shape.str() + ".");
+    if (c.shape != Shape({m, n}))
+        throw Error::tensorShapeMismatch("Matmul output shape mismatch: expected " + Shape({m, n}).str() + ", got " + c.shape.str() + ".");
+    return makeMatmul(a, b, c, m, k, n, transposeB);
+}
+
+std::unique_ptr<Kernel> Matmul(const Tensor &a, const Tensor &b, const Tensor &c, int64_t m, int64_t k, int64_t n, bool transposeB) {
+    return makeMatmul(a, b, c, m, k, n, transposeB);
+}
+
+// RMSNorm.swift:10-37
+std::unique_ptr<Kernel> RMSNorm(const Tensor &x, const Tensor *weight, const Tensor &out, int64_t rowCount, int64_t hiddenSize,
+                                float eps, bool addOneToWeight) {
+    const char *fn = nullptr;
+    switch (x.dataType) {
+    case DataType::f32: fn = "rmsnorm"; break;
+    case DataType::f16: fn = "rmsnorm_f16"; break;
+    case DataType::bf16: fn = "rmsnorm_bf16"; break;
+    default: throw Error::unsupportedDataTypeCombination(std::string("Unsupported RMSNorm data type: ") + tag(x.dataType) + ".");
+    }
+    if (out.dataType != x.dataType) throw Error::unsupportedDataTypeCombination("RMSNorm output must have the input's dtype.");
+    if (weight && weight->dataType != DataType::f32)
+        throw Error::unsupportedDataTypeCombination("RMSNorm weight must be f32 (RMSNorm.metal:42-46 reads it as float).");
+    if (hiddenSize <= 0 || rowCount < 0) throw Error::tensorShapeMismatch("RMSNorm needs a positive hidden size.");
+    requireElements(x, rowCount * hiddenSize, "RMSNorm x");
+    requireElements(out, rowCount * hiddenSize, "RMSNorm out");
+    if (weight) requireElements(*weight, hiddenSize, "RMSNorm weight");
+    RMSNormConstants rc{(uint32_t)hiddenSize, weight ? 1u : 0u, addOneToWeight ? 1u : 0u, eps};
+    // One block per row; a lone row spreads over more lanes (latency), many
+    // rows use 256 threads.
+    const int64_t nvec = cdiv(hiddenSize, 16 / stride(x.dataType));
+    int threads = kBlock;
+    if (rowCount < deviceCUs()) threads = (int)std::clamp<int64_t>(cdiv(nvec, 64) * 64, 64, 1024);
+    const Tensor &w = weight ? *weight : x;  // RMSNorm.swift:21: x bound as the absent weight
+    return std::make_unique<FixedDispatch>(fn, std::vector<Binding>{{x, kRead}, {w, kRead}, {out, kWrite}},
+                                           std::vector<std::vector<uint8_t>>{bytesOf(rc)}, grid1(rowCount, threads));
+}
+
+// RMSNorm.swift:39-70
+std::unique_ptr<Kernel> RMSNorm(const Tensor &x, const Tensor *weight, const Tensor &out, int axis, float eps, bool addOneToWeight) {
+    const int rank = x.shape.rank();
+    const int norm = axis < 0 ? rank + axis : axis;
+    if (norm != rank - 1 || rank <= 0) throw Error::tensorInvalidAxis(axis, rank);
+    if (x.shape != out.shape)
+        throw Error::tensorShapeMismatch("RMSNorm output shape must match input; got " + out.shape.str() + ", expected " + x.shape.str() + ".");
+    const int64_t H = x.shape[norm];
+    const int64_t rows = H ? x.shape.elementCount() / H : 0;
+    if (weight && !(weight->shape == Shape({H}) || weight->shape == x.shape))
+        throw Error::tensorShapeMismatch("RMSNorm weight shape must be [" + std::to_string(H) + "] or " + x.shape.str() + "; got " +
+                                         weight->shape.str() + ".");
+    return RMSNorm(x, weight, out, rows, H, eps, addOneToWeight);
+}
+
+// KVCacheWrite.swift:7-35, plus f16 and a run-time position
+std::unique_ptr<Kernel> KVCacheWrite(const Tensor &source, const Tensor &cache, int64_t batch, int64_t kvHeads, int64_t newLen,
+                                     int64_t maxLen, int64_t headDim, int64_t offset, const Tensor *position) {
+    using D = DataType;
+    const D s = source.dataType, c = cache.dataType;
+    const char *fn = nullptr;
+    if (s == D::f32 && c == D::f32) fn = "kv_cache_write";
+    else if (s == D::bf16 && c == D::bf16) fn = "kv_cache_write_bf16";
+    else if (s == D::f32 && c == D::bf16) fn = "kv_cache_write_f32_to_bf16";
+    else if (s == D::f16 && c == D::f16) fn = "kv_cache_write_f16";
+    else
+        throw Error::unsupportedDataTypeCombination(std::string("Unsupported KV cache data type combination: ") + tag(s) + ", " + tag(c) + ".");
+    if (batch < 0 || kvHeads < 0 || newLen < 0 || headDim <= 0 || maxLen < 0)
+        throw Error::tensorShapeMismatch("KV cache write dimensions must be non-negative.");
+    if (!position && (offset < 0 || offset + newLen > maxLen))
+        throw Error::tensorShapeMismatch("KV cache write range " + std::to_string(offset) + "..<" + std::to_string(offset + newLen) +
+                                         " exceeds cache length " + std::to_string(maxLen) + ".");
+    requireElements(source, batch * kvHeads * newLen * headDim, "KV cache source");
+    requireElements(cache, batch * kvHeads * maxLen * headDim, "KV cache");
+    if (position) {
+        if (position->dataType != D::i32) throw Error::unsupportedDataTypeCombination("position tensor must be i32");
+        requireElements(*position, 1, "position");
+    }
+    KVCacheWriteConstants kc{(uint32_t)batch, (uint32_t)kvHeads, (uint32_t)newLen, (uint32_t)maxLen, (uint32_t)headDim,
+                             (uint32_t)std::max<int64_t>(offset, 0), position ? 1u : 0u};
+    const int64_t run = 16 / stride(s);
+    const int64_t runs = batch * kvHeads * newLen * cdiv(headDim, run);
+    const int64_t blocks = std::clamp<int64_t>(cdiv(runs, kBlock), 1, 4096);
+    const Tensor &pos = position ? *position : source;
+    return std::make_unique<FixedDispatch>(fn, std::vector<Binding>{{source, kRead}, {cache, kWrite}, {pos, kRead}},
+                                           std::vector<std::vector<uint8_t>>{bytesOf(kc)}, grid1(runs ? blocks : 0, kBlock));
+}
+
+// KVCacheWrite.swift:37-48
+std::unique_ptr<Kernel> KVCacheWrite(const Tensor &source, const Tensor &cache, int64_t offset) {
+    if (source.shape.rank() != 4) throw Error::tensorInvalidRank(4, source.shape.rank());
+    if (cache.shape.rank() != 4) throw Error::tensorInvalidRank(4, cache.shape.rank());
+    const int64_t B = source.shape[0], Nkv = source.shape[1], Snew = source.shape[2], Hd = source.shape[3];
+    if (cache.shape[0] != B || cache.shape[1] != Nkv || cache.shape[3] != Hd)
+        throw Error::tensorShapeMismatch("KV cache shape must match source batch/heads/headDim; source " + source.shape.str() +
+                                         ", cache " + cache.shape.str() + ".");
+    if (offset < 0 || offset + Snew > cache.shape[2])
+        throw Error::tensorShapeMismatch("KV cache write range " + std::to_string(offset) + "..<" + std::to_string(offset + Snew) +
+                                         " exceeds cache length " + std::to_string(cache.shape[2]) + ".");
+    return KVCacheWrite(source, cache, B, Nkv, Snew, cache.shape[2], Hd, offset, nullptr);
+}
+
+// GeluTanh.swift:28-33
+std::unique_ptr<Kernel> GeluTanh(const Tensor &x, const Tensor &out) {
+    if (x.shape != out.shape)
+        throw Error::tensorShapeMismatch("GeluTanh output shape must match input; got " + out.shape.str() + ", expected " + x.shape.str() + ".");
+    return elementwise("gelu_tanh", x, nullptr, out, bytesOf(GeluTanhConstants{(uint32_t)x.shape.elementCount()}));
+}
+
+// Mul.swift:28-37
+std::unique_ptr<Kernel> Mul(const Tensor &a, const Tensor &b, const Tensor &out) {
+    if (a.shape != b.shape) throw Error::tensorShapeMismatch("Mul requires matching input shapes; got " + a.shape.str() + " and " + b.shape.str() + ".");
+    if (a.shape != out.shape) throw Error::tensorShapeMismatch("Mul output shape must match inputs; got " + out.shape.str() + ", expected " + a.shape.str() + ".");
+    return elementwise("mul", a, &b, out, bytesOf(MulConstants{(uint32_t)a.shape.elementCount()}));
+}
+
+// Add.swift
+std::unique_ptr<Kernel> Add(const Tensor &a, const Tensor &b, const Tensor &out) {
+    if (a.shape != b.shape) throw Error::tensorShapeMismatch("Add requires matching input shapes; got " + a.shape.str() + " and " + b.shape.str() + ".");
+    if (a.shape != out.shape) throw Error::tensorShapeMismatch("Add output shape must match inputs; got " + out.shape.str() + ", expected " + a.shape.str() + ".");
+    return elementwise("add", a, &b, out, bytesOf(AddConstants{(uint32_t)a.shape.elementCount()}));
+}
+
+// ScalarMul.swift
+std::unique_ptr<Kernel> ScalarMul(const Tensor &x, float scalar, const Tensor &out) {
+    if (x.shape != out.shape)
+        throw Error::tensorShapeMismatch("ScalarMul output shape must match input; got " + out.shape.str() + ", expected " + x.shape.str() + ".");
+    return elementwise("scalar_mul", x, nullptr, out, bytesOf(ScalarMulConstants{(uint32_t)x.shape.elementCount(), scalar}));
+}
+
+std::unique_ptr<Kernel> GatedMLP(const Tensor &x, const Tensor *normWeight, const Tensor &wGate, const Tensor &wUp,
+                                 const Tensor &wDown, const Tensor &out, float eps, bool addOneToWeight, const Tensor *hidden) {
+    return std::make_unique<GatedMLPKernel>(x, normWeight, wGate, wUp, wDown, out, eps, addOneToWeight, hidden);
+}
+
+// EmbeddingGather.swift: ids [N] i32, table [V, H], out [N, H]
+std::unique_ptr<Kernel> EmbeddingGather(const Tensor &ids, const Tensor &table, const Tensor &out) {
+    using D = DataType;
+    if (ids.dataType != D::i32) throw Error::unsupportedDataTypeCombination("EmbeddingGather ids must be i32.");
+    if (table.shape.rank() != 2) throw Error::tensorInvalidRank(2, table.shape.rank());
+    const int64_t V = table.shape[0], H = table.shape[1], N = ids.shape.elementCount();
+    const char *fn = nullptr;
+    if (table.dataType == D::f32 && out.dataType == D::f32) fn = "embedding_gather";
+    else if (table.dataType == D::f16 && out.dataType == D::f16) fn = "embedding_gather_f16";
+    else if (table.dataType == D::bf16 && out.dataType == D::bf16) fn = "embedding_gather_bf16";
+    else if (table.dataType == D::bf16 && out.dataType == D::f32) fn = "embedding_gather_bf16_to_f32";
+    else throw Error::unsupportedDataTypeCombination("Unsupported EmbeddingGather data type combination.");
+    requireElements(out, N * H, "EmbeddingGather out");
+    EmbeddingGatherConstants ec{(uint32_t)N, (uint32_t)H, (uint32_t)V};
+    const int64_t runs = N * cdiv(H, 16 / stride(table.dataType));
+    return std::make_unique<FixedDispatch>(fn, std::vector<Binding>{{ids, kRead}, {table, kRead}, {out, kWrite}},
+                                           std::vector<std::vector<uint8_t>>{bytesOf(ec)},
+                                           grid1(runs ? std::clamp<int64_t>(cdiv(runs, kBlock), 1, 4096) : 0, kBlock));
+}
+
+// Argmax.swift:24-37
+std::unique_ptr<Kernel> Argmax(const Tensor &x, const Tensor &indices) {
+    const int rank = x.shape.rank();
+    if (rank <= 0) throw Error::tensorInvalidAxis(-1, rank);
+    const int64_t n = x.shape[rank - 1];
+    const int64_t rows = n ? x.shape.elementCount() / n : 0;
+    if (indices.shape.elementCount() != rows)
+        throw Error::tensorShapeMismatch("Argmax indices must contain " + std::to_string(rows) + " elements; got " +
+                                         std::to_string(indices.shape.elementCount()) + ".");
+    return std::make_unique<ArgmaxKernel>(x, indices, rows, n);
+}
+
+std::unique_ptr<Kernel> Custom(const std::string &functionName, std::vector<Binding> tensors,
+                               std::vector<std::vector<uint8_t>> constants, dim3 grid, dim3 block) {
+    DispatchSize ds;
+    ds.grid = grid;
+    ds.block = block;
+    return std::make_unique<FixedDispatch>(functionName, std::move(tensors), std::move(constants), ds);
+}
+
+std::unique_ptr<Kernel> FillNormal(void *data, DataType dtype, uint64_t count, uint64_t seed, float mean, float stddev) {
+    if (!isFloat(dtype)) throw Error::unsupportedDataTypeCombination("fill_normal writes f32, f16 or bf16.");
+    if (count && !data) throw Error::invalidArgument("fill_normal: null data pointer");
+    FillNormalConstants fc{seed, count, mean, stddev};
+    Tensor t(data, Shape({(int64_t)count}), dtype);
+    const int64_t blocks = std::clamp<int64_t>(cdiv((int64_t)count, kBlock), 1, 16 * deviceCUs());
+    return std::make_unique<FixedDispatch>(std::string("fill_normal_") + tag(dtype), std::vector<Binding>{{t, kWrite}},
+                                           std::vector<std::vector<uint8_t>>{bytesOf(fc)}, grid1(count ? blocks : 0, kBlock));
+}
+
+}  // namespace Kernels
+}  // namespace popcorn

@@ -1,0 +1,569 @@
+"""Python mirror of the reference's Swift API over the C ABI.
+
+Names, argument meaning and errors follow Sources/Popcorn (cited per class):
+``Tensor``, ``Kernels.*``, ``KernelCommandEncoder`` (``encode`` takes one
+kernel or several, the result-builder form), ``KernelLibrary``,
+``ScratchPool`` (a ``KernelScratchAllocator``) and ``PopcornError``. Device
+memory is plain HIP memory owned by ``DeviceBuffer``; host data moves through
+numpy arrays (bf16 as uint16 bit patterns).
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+from typing import Iterable, Optional, Sequence
+
+import numpy as np
+
+from . import _capi
+from ._capi import DTYPES, DTYPE_NAMES, MAX_RANK, TensorDesc, AttentionMaskDesc
+
+
+# ---- errors (PopcornError.swift:23-42) --------------------------------------
+
+class PopcornError(Exception):
+    """Carries the reference's PopcornError.Code raw value in ``code``."""
+
+    CONSTANT_ALLOCATION_FAILED = -1001
+    TENSOR_ALLOCATION_FAILED = -1003
+    KERNEL_FUNCTION_NOT_FOUND = -1006
+    TENSOR_SHAPE_MISMATCH = -1007
+    TENSOR_INVALID_RANK = -1008
+    TENSOR_INVALID_AXIS = -1009
+    UNSUPPORTED_DATA_TYPE_COMBINATION = -1010
+    GPU_OUT_OF_MEMORY = -1013
+    GPU_TIMEOUT = -1014
+    GPU_PAGE_FAULT = -1015
+    GPU_INVALID_RESOURCE = -1016
+    GPU_DEVICE_REMOVED = -1017
+    GPU_INTERNAL = -1019
+    INVALID_ARGUMENT = -1100
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"PopcornError({code}): {message}")
+        self.code = code
+        self.message = message
+
+
+def lib():
+    return _capi.load()
+
+
+def check(status: int) -> None:
+    if status != 0:
+        msg = lib().popcorn_last_error_message()
+        raise PopcornError(int(status), msg.decode() if msg else "")
+
+
+# ---- device ------------------------------------------------------------------
+
+def device_count() -> int:
+    n = C.c_int32(0)
+    check(lib().popcorn_device_count(C.byref(n)))
+    return n.value
+
+
+def device_info(device: int = 0) -> dict:
+    info = _capi.DeviceInfo()
+    check(lib().popcorn_device_info(device, C.byref(info)))
+    return {"name": info.name.decode(), "arch": info.arch.decode(), "compute_units": info.compute_units,
+            "wave_size": info.wave_size, "max_threads_per_block": info.max_threads_per_block,
+            "lds_bytes_per_block": info.lds_bytes_per_block, "global_memory_bytes": info.global_memory_bytes,
+            "l2_bytes": info.l2_bytes, "clock_khz": info.clock_khz}
+
+
+def synchronize() -> None:
+    check(lib().popcorn_device_synchronize())
+
+
+class Stream:
+    """An in-order HIP stream (None = the default stream)."""
+
+    def __init__(self):
+        h = C.c_void_p()
+        check(lib().popcorn_stream_create(C.byref(h)))
+        self.handle = h.value
+
+    def synchronize(self) -> None:
+        check(lib().popcorn_stream_synchronize(self.handle))
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            lib().popcorn_stream_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def _stream_handle(stream) -> Optional[int]:
+    return None if stream is None else stream.handle
+
+
+class Event:
+    def __init__(self):
+        h = C.c_void_p()
+        check(lib().popcorn_event_create(C.byref(h)))
+        self.handle = h.value
+
+    def record(self, stream: Optional[Stream] = None) -> None:
+        check(lib().popcorn_event_record(self.handle, _stream_handle(stream)))
+
+    def synchronize(self) -> None:
+        check(lib().popcorn_event_synchronize(self.handle))
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = C.c_float(0)
+        check(lib().popcorn_event_elapsed_ms(self.handle, end.handle, C.byref(ms)))
+        return ms.value
+
+    def __del__(self):
+        try:
+            if self.handle:
+                lib().popcorn_event_destroy(self.handle)
+        except Exception:
+            pass
+
+
+class DeviceBuffer:
+    """Owned device memory (the MTLBuffer a Tensor views)."""
+
+    def __init__(self, nbytes: int):
+        p = C.c_void_p()
+        check(lib().popcorn_malloc(max(int(nbytes), 1), C.byref(p)))
+        self.ptr = p.value
+        self.nbytes = int(nbytes)
+
+    def __del__(self):
+        try:
+            if self.ptr:
+                lib().popcorn_free(self.ptr)
+        except Exception:
+            pass
+
+
+# ---- tensors (Tensor.swift) ----------------------------------------------------
+
+_NP = {"f32": np.float32, "f16": np.float16, "bf16": np.uint16, "i32": np.int32, "u8": np.uint8,
+       "u16": np.uint16, "u32": np.uint32, "u64": np.uint64, "i8": np.int8, "i16": np.int16, "i64": np.int64}
+
+
+def stride(dtype: str) -> int:
+    return int(lib().popcorn_dtype_stride(DTYPES[dtype]))
+
+
+def _host_array(arr: np.ndarray, dtype: str) -> np.ndarray:
+    """Host storage for `dtype`: uint16 bit patterns are reinterpreted for
+    f16 (never value-converted); other inputs convert to the storage type."""
+    arr = np.asarray(arr)
+    if dtype == "f16" and arr.dtype == np.uint16:
+        return np.ascontiguousarray(arr).view(np.float16)
+    return np.ascontiguousarray(arr, dtype=_NP[dtype])
+
+
+class Tensor:
+    """Tensor{buffer, shape, dataType}: a view of device memory (Tensor.swift:5-22).
+
+    ``ptr`` may be any device address; ``owner`` keeps its buffer alive.
+    """
+
+    def __init__(self, ptr: int, shape: Sequence[int], dtype: str = "f32", owner=None):
+        if dtype not in DTYPES:
+            raise ValueError(f"unknown dtype {dtype}")
+        if len(shape) > MAX_RANK:
+            raise ValueError("rank above 8")
+        self.ptr = int(ptr) if ptr else 0
+        self.shape = tuple(int(s) for s in shape)
+        self.dtype = dtype
+        self.owner = owner
+
+    # construction
+    @classmethod
+    def empty(cls, shape: Sequence[int], dtype: str = "f32") -> "Tensor":
+        n = int(np.prod(shape)) if len(shape) else 1
+        buf = DeviceBuffer(n * stride(dtype))
+        return cls(buf.ptr, shape, dtype, owner=buf)
+
+    @classmethod
+    def from_numpy(cls, arr: np.ndarray, dtype: Optional[str] = None, stream: Optional[Stream] = None) -> "Tensor":
+        """Uploads `arr`. For bf16 pass uint16 bit patterns with dtype='bf16'."""
+        if dtype is None:
+            dtype = {np.dtype(np.float32): "f32", np.dtype(np.float16): "f16", np.dtype(np.int32): "i32"}[arr.dtype]
+        host = _host_array(arr, dtype)
+        t = cls.empty(host.shape, dtype)
+        if host.nbytes:
+            check(lib().popcorn_memcpy_h2d(t.ptr, host.ctypes.data, host.nbytes, _stream_handle(stream)))
+        return t
+
+    def numpy(self, stream: Optional[Stream] = None) -> np.ndarray:
+        out = np.empty(self.shape, dtype=_NP[self.dtype])
+        if out.nbytes:
+            check(lib().popcorn_memcpy_d2h(out.ctypes.data, self.ptr, out.nbytes, _stream_handle(stream)))
+        return out
+
+    def copy_from(self, arr: np.ndarray, stream: Optional[Stream] = None) -> None:
+        host = _host_array(arr, self.dtype)
+        if host.nbytes > self.nbytes:
+            raise ValueError("source larger than tensor")
+        if host.nbytes:
+            check(lib().popcorn_memcpy_h2d(self.ptr, host.ctypes.data, host.nbytes, _stream_handle(stream)))
+
+    def fill_zero(self, stream: Optional[Stream] = None) -> None:
+        check(lib().popcorn_memset(self.ptr, 0, self.nbytes, _stream_handle(stream)))
+
+    def view(self, shape: Sequence[int], dtype: Optional[str] = None, offset_elements: int = 0) -> "Tensor":
+        dt = dtype or self.dtype
+        return Tensor(self.ptr + offset_elements * stride(self.dtype), shape, dt, owner=self.owner or self)
+
+    @property
+    def element_count(self) -> int:
+        return int(np.prod(self.shape)) if self.shape else 1
+
+    @property
+    def nbytes(self) -> int:
+        return self.element_count * stride(self.dtype)
+
+    def desc(self) -> TensorDesc:
+        d = TensorDesc()
+        d.data = self.ptr
+        d.dtype = DTYPES[self.dtype]
+        d.rank = len(self.shape)
+        for i, s in enumerate(self.shape):
+            d.shape[i] = s
+        return d
+
+    def __repr__(self):
+        return f"Tensor(shape={list(self.shape)}, dtype={self.dtype}, ptr=0x{self.ptr:x})"
+
+
+def _d(t: Optional[Tensor]):
+    return None if t is None else C.byref(t.desc())
+
+
+# ---- masks (AttentionMask.swift:17-41) -------------------------------------------
+
+@dataclass(frozen=True)
+class AttentionMask:
+    kind: int = 0
+    window: int = -1
+
+    @staticmethod
+    def causal_sliding_window(window: int) -> "AttentionMask":
+        return AttentionMask(1, int(window))
+
+    def desc(self) -> AttentionMaskDesc:
+        return AttentionMaskDesc(self.kind, self.window if self.kind == 1 else -1)
+
+
+AttentionMask.causal = AttentionMask(0)
+AttentionMask.bidirectional = AttentionMask(2)
+
+
+# ---- library (KernelLibrary.swift) -------------------------------------------------
+
+class KernelFunction:
+    def __init__(self, handle: int, name: str):
+        self.handle = handle
+        self.name = name
+
+    def attributes(self) -> dict:
+        a = _capi.FunctionAttrs()
+        check(lib().popcorn_function_attributes(self.handle, C.byref(a)))
+        return {f: getattr(a, f) for f, _ in a._fields_}
+
+
+class KernelLibrary:
+    """The gfx950 code objects (default: popcorn_amd/lib/kernels)."""
+
+    def __init__(self, path: Optional[str] = None):
+        h = C.c_void_p()
+        check(lib().popcorn_library_load(path.encode() if path else None, C.byref(h)))
+        self.handle = h.value
+
+    def function(self, name: str) -> KernelFunction:
+        """pipelineState(for:): cached; raises PopcornError(-1006) for an unknown name."""
+        h = C.c_void_p()
+        check(lib().popcorn_library_function(self.handle, name.encode(), C.byref(h)))
+        return KernelFunction(h.value, name)
+
+    @property
+    def cached_function_count(self) -> int:
+        return int(lib().popcorn_library_cached_function_count(self.handle))
+
+    def launch(self, name: str, grid, block, buffers: Sequence[int], constants: Sequence[bytes] = (),
+               dynamic_lds: int = 0, stream: Optional[Stream] = None) -> None:
+        """Raw launch: device pointers in order, then constants blocks by value."""
+        fn = self.function(name)
+        g = (C.c_uint32 * 3)(*grid)
+        b = (C.c_uint32 * 3)(*block)
+        bufs = (C.c_void_p * max(len(buffers), 1))(*buffers)
+        keep = [C.create_string_buffer(c, len(c)) for c in constants]
+        cptrs = (C.c_void_p * max(len(keep), 1))(*[C.cast(k, C.c_void_p) for k in keep])
+        sizes = (C.c_size_t * max(len(keep), 1))(*[len(c) for c in constants])
+        check(lib().popcorn_launch(_stream_handle(stream), fn.handle, g, b, bufs, len(buffers), cptrs, sizes,
+                                   len(keep), dynamic_lds))
+
+    def fill_normal(self, t: Tensor, seed: int, mean: float = 0.0, std: float = 1.0,
+                    stream: Optional[Stream] = None) -> None:
+        check(lib().popcorn_fill_normal(self.handle, _stream_handle(stream), t.ptr, DTYPES[t.dtype],
+                                        t.element_count, seed, mean, std))
+
+    def __del__(self):
+        try:
+            if self.handle:
+                lib().popcorn_library_destroy(self.handle)
+        except Exception:
+            pass
+
+
+# ---- scratch (KernelResources.swift) ---------------------------------------------------
+
+class ScratchPool:
+    """Best-fit pool of device buffers for one stream (a KernelScratchAllocator)."""
+
+    def __init__(self):
+        h = C.c_void_p()
+        check(lib().popcorn_scratch_pool_create(C.byref(h)))
+        self.handle = h.value
+
+    def allocator(self) -> _capi.ScratchAllocatorDesc:
+        a = _capi.ScratchAllocatorDesc()
+        check(lib().popcorn_scratch_pool_allocator(self.handle, C.byref(a)))
+        return a
+
+    @property
+    def nbytes(self) -> int:
+        return int(lib().popcorn_scratch_pool_bytes(self.handle))
+
+    def __del__(self):
+        try:
+            if self.handle:
+                lib().popcorn_scratch_pool_destroy(self.handle)
+        except Exception:
+            pass
+
+
+class KernelScratchAllocator:
+    """Base for Python allocators: override borrow(length) -> (ptr, was_reused) and release(ptr)."""
+
+    def borrow(self, length: int):
+        raise NotImplementedError
+
+    def release(self, ptr: int) -> None:
+        pass
+
+    def allocator(self) -> _capi.ScratchAllocatorDesc:
+        def _borrow(ctx, length, out, reused):
+            try:
+                ptr, was_reused = self.borrow(int(length))
+                out[0] = ptr
+                if reused:
+                    reused[0] = 1 if was_reused else 0
+                return 0
+            except Exception:
+                return PopcornError.TENSOR_ALLOCATION_FAILED
+
+        def _release(ctx, ptr):
+            self.release(ptr)
+
+        self._cb = (_capi.BORROW_FN(_borrow), _capi.RELEASE_FN(_release))
+        return _capi.ScratchAllocatorDesc(None, self._cb[0], self._cb[1])
+
+
+def scratch_spec_byte_count(shape: Sequence[int], dtype: str) -> int:
+    arr = (C.c_int64 * max(len(shape), 1))(*shape)
+    return int(lib().popcorn_scratch_spec_byte_count(arr, len(shape), DTYPES[dtype]))
+
+
+# ---- kernels (Kernel.swift + Kernels/*.swift) -----------------------------------------
+
+class Kernel:
+    """A validated operation descriptor; encode it with a KernelCommandEncoder."""
+
+    def __init__(self, handle: int, refs: Iterable = ()):
+        self.handle = handle
+        self._refs = list(refs)  # tensors the descriptor points at
+
+    def describe(self) -> str:
+        buf = C.create_string_buffer(512)
+        check(lib().popcorn_kernel_describe(self.handle, buf, 512))
+        return buf.value.decode()
+
+    @property
+    def function_names(self):
+        return self.describe().split(",")
+
+    def __del__(self):
+        try:
+            if self.handle:
+                lib().popcorn_kernel_destroy(self.handle)
+        except Exception:
+            pass
+
+
+def _make(fn, *args, refs=()):
+    h = C.c_void_p()
+    check(fn(*args, C.byref(h)))
+    return Kernel(h.value, refs)
+
+
+class Kernels:
+    """The operation descriptors of the decode hot path."""
+
+    @staticmethod
+    def route(query_len: int, head_dim: int, q_dtype: str = "bf16") -> str:
+        r = lib().popcorn_flash_attention_route(query_len, head_dim, DTYPES[q_dtype])
+        return {0: "plain", 1: "tiled", 2: "decoding"}[r]
+
+    @staticmethod
+    def FlashAttention(q: Tensor, k: Tensor, v: Tensor, into: Optional[Tensor] = None, *, scale: float,
+                       mask: AttentionMask = AttentionMask(0), out: Optional[Tensor] = None,
+                       batch: Optional[int] = None, query_heads: int = 0, kv_heads: int = 0, query_len: int = 0,
+                       key_len: int = 0, head_dim: int = 0, key_capacity: int = 0,
+                       position: Optional[Tensor] = None) -> Kernel:
+        """FlashAttention(q:k:v:into:scale:mask:) (FlashAttention.swift:51-90), or with
+        batch=... the explicit-dims init (:13-49) plus key_capacity / position."""
+        o = into if into is not None else out
+        refs = (q, k, v, o, position)
+        if batch is None:
+            return _make(lib().popcorn_kernel_flash_attention, _d(q), _d(k), _d(v), _d(o), scale, mask.desc(),
+                         refs=refs)
+        return _make(lib().popcorn_kernel_flash_attention_dims, _d(q), _d(k), _d(v), _d(o), batch, query_heads,
+                     kv_heads, query_len, key_len, head_dim, scale, mask.desc(), key_capacity, _d(position),
+                     refs=refs)
+
+    @staticmethod
+    def Matmul(a: Tensor, b: Tensor, into: Tensor, transpose_b: bool = False, *, m: Optional[int] = None,
+               k: int = 0, n: int = 0) -> Kernel:
+        """Matmul(_:_:into:transposeB:) (Matmul.swift:68-93) or, with m=..., the dims init (:9-66)."""
+        if m is None:
+            return _make(lib().popcorn_kernel_matmul, _d(a), _d(b), _d(into), int(transpose_b), refs=(a, b, into))
+        return _make(lib().popcorn_kernel_matmul_dims, _d(a), _d(b), _d(into), m, k, n, int(transpose_b),
+                     refs=(a, b, into))
+
+    @staticmethod
+    def RMSNorm(x: Tensor, weight: Optional[Tensor] = None, into: Optional[Tensor] = None, *, axis: int = -1,
+                eps: float, add_one_to_weight: bool = False, row_count: Optional[int] = None,
+                hidden_size: int = 0) -> Kernel:
+        """RMSNorm(_:weight:into:axis:eps:addOneToWeight:) (RMSNorm.swift:39-70), or with
+        row_count=... the explicit init (:10-37)."""
+        if row_count is None:
+            return _make(lib().popcorn_kernel_rmsnorm, _d(x), _d(weight), _d(into), axis, eps,
+                         int(add_one_to_weight), refs=(x, weight, into))
+        return _make(lib().popcorn_kernel_rmsnorm_dims, _d(x), _d(weight), _d(into), row_count, hidden_size, eps,
+                     int(add_one_to_weight), refs=(x, weight, into))
+
+    @staticmethod
+    def KVCacheWrite(source: Tensor, cache: Tensor, offset: int = 0, *, batch: Optional[int] = None,
+                     kv_heads: int = 0, new_len: int = 0, max_len: int = 0, head_dim: int = 0,
+                     position: Optional[Tensor] = None) -> Kernel:
+        """KVCacheWrite(source:cache:offset:) (KVCacheWrite.swift:37-48) or the dims init (:7-35)."""
+        if batch is None and position is None:
+            return _make(lib().popcorn_kernel_kv_cache_write, _d(source), _d(cache), offset, refs=(source, cache))
+        if batch is None:
+            batch, kv_heads, new_len, head_dim = source.shape
+            max_len = cache.shape[2]
+        return _make(lib().popcorn_kernel_kv_cache_write_dims, _d(source), _d(cache), batch, kv_heads, new_len,
+                     max_len, head_dim, offset, _d(position), refs=(source, cache, position))
+
+    @staticmethod
+    def GeluTanh(x: Tensor, into: Tensor) -> Kernel:
+        return _make(lib().popcorn_kernel_gelu_tanh, _d(x), _d(into), refs=(x, into))
+
+    @staticmethod
+    def Mul(a: Tensor, b: Tensor, into: Tensor) -> Kernel:
+        return _make(lib().popcorn_kernel_mul, _d(a), _d(b), _d(into), refs=(a, b, into))
+
+    @staticmethod
+    def Add(a: Tensor, b: Tensor, into: Tensor) -> Kernel:
+        return _make(lib().popcorn_kernel_add, _d(a), _d(b), _d(into), refs=(a, b, into))
+
+    @staticmethod
+    def ScalarMul(x: Tensor, by: float, into: Tensor) -> Kernel:
+        return _make(lib().popcorn_kernel_scalar_mul, _d(x), by, _d(into), refs=(x, into))
+
+    @staticmethod
+    def GatedMLP(x: Tensor, norm_weight: Optional[Tensor], w_gate: Tensor, w_up: Tensor, w_down: Tensor,
+                 into: Tensor, *, eps: float, add_one_to_weight: bool = False,
+                 hidden: Optional[Tensor] = None) -> Kernel:
+        """RMSNorm -> gate, up -> GeluTanh(gate) * up -> down (Gemma4TextInference.swift:416-429)."""
+        return _make(lib().popcorn_kernel_gated_mlp, _d(x), _d(norm_weight), _d(w_gate), _d(w_up), _d(w_down),
+                     _d(into), eps, int(add_one_to_weight), _d(hidden),
+                     refs=(x, norm_weight, w_gate, w_up, w_down, into, hidden))
+
+    @staticmethod
+    def EmbeddingGather(ids: Tensor, table: Tensor, into: Tensor) -> Kernel:
+        return _make(lib().popcorn_kernel_embedding_gather, _d(ids), _d(table), _d(into), refs=(ids, table, into))
+
+    @staticmethod
+    def Argmax(x: Tensor, indices: Tensor) -> Kernel:
+        return _make(lib().popcorn_kernel_argmax, _d(x), _d(indices), refs=(x, indices))
+
+    @staticmethod
+    def Custom(function_name: str, tensors: Sequence[Tensor], access: Sequence[int], constants: Sequence[bytes],
+               grid, block) -> Kernel:
+        """A caller-built DispatchKernel (Kernel.swift:54-70); access 1 read, 2 write, 3 both."""
+        n = len(tensors)
+        descs = (TensorDesc * max(n, 1))(*[t.desc() for t in tensors])
+        acc = (C.c_uint8 * max(n, 1))(*access)
+        keep = [C.create_string_buffer(c, len(c)) for c in constants]
+        cptrs = (C.c_void_p * max(len(keep), 1))(*[C.cast(k, C.c_void_p) for k in keep])
+        sizes = (C.c_size_t * max(len(keep), 1))(*[len(c) for c in constants])
+        g = (C.c_uint32 * 3)(*grid)
+        b = (C.c_uint32 * 3)(*block)
+        return _make(lib().popcorn_kernel_custom, function_name.encode(), descs, acc, n, cptrs, sizes, len(keep),
+                     g, b, refs=list(tensors))
+
+
+# ---- encoder (KernelCommandEncoder.swift) ------------------------------------------------
+
+class KernelCommandEncoder:
+    """Encodes kernels in order on one stream; scratch from `scratch` (a ScratchPool
+    or KernelScratchAllocator) or an internal pool."""
+
+    def __init__(self, library: KernelLibrary, stream: Optional[Stream] = None, scratch=None):
+        self.library = library
+        self.stream = stream
+        self._scratch = scratch
+        alloc = scratch.allocator() if scratch is not None else None
+        self._alloc = alloc
+        h = C.c_void_p()
+        check(lib().popcorn_encoder_create(library.handle, _stream_handle(stream),
+                                           C.byref(alloc) if alloc is not None else None, C.byref(h)))
+        self.handle = h.value
+
+    def encode(self, *kernels) -> None:
+        """encode(kernel), or several in order: the result-builder form encode { k1; k2 }."""
+        flat = []
+        for k in kernels:
+            if isinstance(k, (list, tuple)):
+                flat.extend(x for x in k if x is not None)
+            elif k is not None:
+                flat.append(k)
+        if len(flat) == 1:
+            check(lib().popcorn_encoder_encode(self.handle, flat[0].handle))
+        elif flat:
+            arr = (C.c_void_p * len(flat))(*[k.handle for k in flat])
+            check(lib().popcorn_encoder_encode_all(self.handle, arr, len(flat)))
+
+    def barrier(self) -> None:
+        check(lib().popcorn_encoder_barrier(self.handle))
+
+    def stats(self) -> dict:
+        s = _capi.EncoderStats()
+        check(lib().popcorn_encoder_stats(self.handle, C.byref(s)))
+        return {"dispatches": s.dispatches, "hazards": s.hazards, "scratch_borrows": s.scratch_borrows}
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            check(lib().popcorn_encoder_destroy(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,170 @@
+"""CPU tests of the C ABI: the library loads, exports every function that
+include/*.h declares, and the descriptors validate and route without a GPU
+(fake device addresses: nothing is launched)."""
+import os
+import re
+
+import pytest
+
+import popcorn_amd as pa
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+FAKE = 0x7F0000000000  # never dereferenced: descriptors only validate
+
+
+def declared_functions():
+    names = set()
+    inc = os.path.join(ROOT, "include")
+    for f in os.listdir(inc):
+        if f.endswith(".h"):
+            text = open(os.path.join(inc, f)).read()
+            text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+            names |= set(re.findall(r"\b(popcorn_[a-z0-9_]+)\s*\(", text))
+    return sorted(n for n in names if not n.endswith("_t"))  # types in function-pointer fields
+
+
+def test_every_declared_symbol_is_exported():
+    lib = pa.lib()
+    names = declared_functions()
+    assert len(names) > 50
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_bindings_cover_the_header():
+    from popcorn_amd._capi import PROTOTYPES
+
+    assert set(declared_functions()) <= set(PROTOTYPES)
+
+
+def T(shape, dtype="bf16", ptr=FAKE):
+    return pa.Tensor(ptr, shape, dtype)
+
+
+def test_dtype_stride_and_scratch_spec():
+    # Tensor.swift:152-159, ScratchSpec.swift / KernelResourceTests.swift:5-8
+    assert [pa.stride(d) for d in ("u8", "bf16", "f16", "f32", "i32", "i64")] == [1, 2, 2, 4, 4, 8]
+    assert pa.scratch_spec_byte_count([2, 3, 4], "f32") == 96
+    assert pa.scratch_spec_byte_count([], "bf16") == 2
+
+
+def test_status_mapping():
+    lib = pa.lib()
+    assert lib.popcorn_status_from_hip_error(0) == 0
+    assert lib.popcorn_status_from_hip_error(2) == -1013   # out of memory
+    assert lib.popcorn_status_from_hip_error(702) == -1014  # launch timeout
+    assert lib.popcorn_status_from_hip_error(700) == -1015  # illegal address
+    assert lib.popcorn_status_from_hip_error(400) == -1016  # invalid handle
+    assert lib.popcorn_status_from_hip_error(100) == -1017  # no device
+    assert lib.popcorn_status_from_hip_error(999) == -1019
+
+
+def test_route():
+    # FlashAttention.swift:109-113
+    assert pa.Kernels.route(1, 256) == "decoding"
+    assert pa.Kernels.route(2, 256) == "plain"
+
+
+def test_flash_attention_routing_names():
+    q, o = T([1, 8, 1, 256]), T([1, 8, 1, 256])
+    k = T([1, 4, 4352, 256])
+    kern = pa.Kernels.FlashAttention(q, k, k, out=o, scale=1 / 16, batch=1, query_heads=8, kv_heads=4,
+                                     query_len=1, key_len=4097, head_dim=256, key_capacity=4352)
+    assert kern.function_names == ["flash_decoding_partial_bf16_l32_c1_g2", "flash_decoding_reduce_bf16"]
+    f = pa.Kernels.FlashAttention(T([1, 4, 1, 64], "f32"), T([1, 1, 129, 64], "f32"), T([1, 1, 129, 64], "f32"),
+                                  T([1, 4, 1, 64], "f32"), scale=0.125)
+    assert f.function_names[0] == "flash_decoding_partial_f32_l16_c1_g4"
+    g = pa.Kernels.FlashAttention(T([1, 2, 1, 80]), T([1, 1, 9, 80]), T([1, 1, 9, 80]), T([1, 2, 1, 80], "f32"),
+                                  scale=0.1)
+    assert g.function_names == ["flash_decoding_partial_bf16", "flash_decoding_reduce_f32"]
+
+
+def test_flash_attention_validation_codes():
+    E = pa.PopcornError
+    cases = [
+        (lambda: pa.Kernels.FlashAttention(T([1, 3, 1, 64]), T([1, 2, 9, 64]), T([1, 2, 9, 64]), T([1, 3, 1, 64]),
+                                           scale=1.0), E.TENSOR_SHAPE_MISMATCH),  # 3 % 2 != 0
+        (lambda: pa.Kernels.FlashAttention(T([1, 2, 1, 520]), T([1, 2, 9, 520]), T([1, 2, 9, 520]),
+                                           T([1, 2, 1, 520]), scale=1.0), E.TENSOR_SHAPE_MISMATCH),  # Hd > 512
+        (lambda: pa.Kernels.FlashAttention(T([2, 1, 64]), T([1, 2, 9, 64]), T([1, 2, 9, 64]), T([1, 2, 1, 64]),
+                                           scale=1.0), E.TENSOR_INVALID_RANK),
+        (lambda: pa.Kernels.FlashAttention(T([1, 2, 1, 64]), T([1, 2, 9, 64]), T([1, 2, 9, 64]), T([1, 2, 2, 64]),
+                                           scale=1.0), E.TENSOR_SHAPE_MISMATCH),
+        (lambda: pa.Kernels.FlashAttention(T([1, 2, 1, 64], "i32"), T([1, 2, 9, 64], "i32"),
+                                           T([1, 2, 9, 64], "i32"), T([1, 2, 1, 64]), scale=1.0),
+         E.UNSUPPORTED_DATA_TYPE_COMBINATION),
+        # dims init reading past a too-small K tensor is refused
+        (lambda: pa.Kernels.FlashAttention(T([1, 2, 1, 64]), T([1, 2, 9, 64]), T([1, 2, 9, 64]), T([1, 2, 1, 64]),
+                                           scale=1.0, batch=1, query_heads=2, kv_heads=2, query_len=1, key_len=10,
+                                           head_dim=64), E.TENSOR_SHAPE_MISMATCH),
+    ]
+    for make, code in cases:
+        with pytest.raises(pa.PopcornError) as e:
+            make()
+        assert e.value.code == code, e.value
+
+
+def test_matmul_routing_and_validation():
+    x = T([1, 2304])
+    assert pa.Kernels.Matmul(x, T([9216, 2304]), T([1, 9216]), True).describe() == "matvec_nk_simd_bf16_bf16_bf16"
+    assert pa.Kernels.Matmul(T([1, 9216]), T([2304, 9216]), T([1, 2304]), True).describe() == \
+        "matvec_nk_simd_bf16_bf16_bf16_r1"
+    assert pa.Kernels.Matmul(x, T([2304, 300]), T([1, 300]), False).describe() == "matvec_bf16_bf16_bf16"
+    assert pa.Kernels.Matmul(T([4, 8], "f32"), T([8, 3], "f32"), T([4, 3], "f32")).describe() == "matmul"
+    with pytest.raises(pa.PopcornError) as e:  # Matmul.swift:85-87
+        pa.Kernels.Matmul(x, T([9216, 2300]), T([1, 9216]), True)
+    assert e.value.code == pa.PopcornError.TENSOR_SHAPE_MISMATCH
+    with pytest.raises(pa.PopcornError) as e:
+        pa.Kernels.Matmul(T([2304]), T([9216, 2304]), T([1, 9216]), True)
+    assert e.value.code == pa.PopcornError.TENSOR_INVALID_RANK
+    with pytest.raises(pa.PopcornError) as e:
+        pa.Kernels.Matmul(T([1, 8], "i32"), T([8, 8], "i32"), T([1, 8], "i32"), True)
+    assert e.value.code == pa.PopcornError.UNSUPPORTED_DATA_TYPE_COMBINATION
+
+
+def test_rmsnorm_kv_elementwise_validation():
+    E = pa.PopcornError
+    with pytest.raises(E) as e:
+        pa.Kernels.RMSNorm(T([2, 8]), None, T([2, 8]), axis=0, eps=1e-6)
+    assert e.value.code == E.TENSOR_INVALID_AXIS
+    with pytest.raises(E) as e:
+        pa.Kernels.RMSNorm(T([2, 8]), T([8], "bf16"), T([2, 8]), eps=1e-6)  # weight must be f32
+    assert e.value.code == E.UNSUPPORTED_DATA_TYPE_COMBINATION
+    assert pa.Kernels.RMSNorm(T([2, 8]), T([8], "f32"), T([2, 8]), eps=1e-6).describe() == "rmsnorm_bf16"
+    with pytest.raises(E) as e:
+        pa.Kernels.KVCacheWrite(T([1, 4, 1, 256]), T([1, 4, 10, 256]), offset=10)
+    assert e.value.code == E.TENSOR_SHAPE_MISMATCH
+    assert pa.Kernels.KVCacheWrite(T([1, 4, 1, 256], "f32"), T([1, 4, 10, 256]), offset=9).describe() == \
+        "kv_cache_write_f32_to_bf16"
+    with pytest.raises(E) as e:
+        pa.Kernels.Mul(T([4]), T([5]), T([4]))
+    assert e.value.code == E.TENSOR_SHAPE_MISMATCH
+    assert pa.Kernels.GeluTanh(T([7], "f16"), T([7], "f16")).describe() == "gelu_tanh_f16"
+
+
+def test_gated_mlp_validation_and_routing():
+    E = pa.PopcornError
+    k = pa.Kernels.GatedMLP(T([2304]), T([2304], "f32"), T([9216, 2304]), T([9216, 2304]), T([2304, 9216]),
+                            T([2304]), eps=1e-6)
+    assert k.function_names == ["gated_mlp_gate_up_bf16", "matvec_nk_simd_bf16_bf16_bf16_r1"]
+    with pytest.raises(E) as e:
+        pa.Kernels.GatedMLP(T([2304]), None, T([9216, 2304]), T([9216, 2300]), T([2304, 9216]), T([2304]), eps=1e-6)
+    assert e.value.code == E.TENSOR_SHAPE_MISMATCH
+    with pytest.raises(E) as e:
+        pa.Kernels.GatedMLP(T([2304]), None, T([9216, 2304]), T([9216, 2304], "f16"), T([2304, 9216]), T([2304]),
+                            eps=1e-6)
+    assert e.value.code == E.UNSUPPORTED_DATA_TYPE_COMBINATION
+
+
+def test_custom_kernel_rejects_empty_access():
+    # Tensor.swift:208: a binding's access must not be empty
+    with pytest.raises(pa.PopcornError) as e:
+        pa.Kernels.Custom("add", [T([4], "f32")], [0], [], (1, 1, 1), (64, 1, 1))
+    assert e.value.code == pa.PopcornError.INVALID_ARGUMENT
+
+
+def test_no_gpu_paths_fail_loudly_here():
+    if pa.device_count() > 0:
+        pytest.skip("a GPU is visible")
+    with pytest.raises(pa.PopcornError):
+        pa.KernelLibrary()

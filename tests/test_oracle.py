@@ -395,3 +395,17 @@ def test_decoder_layer_vs_float64(oracle):
     a = 0.5 * g * (1 + np.tanh(np.sqrt(2 / np.pi) * (g + 0.044715 * g**3)))
     xx = xx + rms(W64["down"] @ (a * u), W64["post_ffn_norm"])
     assert_approx(x, xx, 1e-4, "decoder layer")
+
+
+def test_half_ulp_tolerance_term():
+    from conftest import half_ulp
+
+    # bf16 keeps 8 significant bits: half an ulp at 1.0 is 2^-8, at 2.27 it is 2^-7
+    assert half_ulp([1.0, 2.27, 0.0], "bf16").tolist() == [2.0**-8, 2.0**-7, 0.0]
+    assert half_ulp([1.0], "f16").tolist() == [2.0**-11]
+    assert half_ulp([3.0], "f32").tolist() == [0.0]
+    # the bound covers exactly the store rounding of an exact value
+    x = np.random.default_rng(0).standard_normal(100000).astype(np.float32) * 10
+    import oracle as O
+    r = O.round_to(x, O.BF16)
+    assert np.all(np.abs(r.astype(np.float64) - x) <= half_ulp(np.maximum(np.abs(r), np.abs(x)), "bf16"))
