@@ -1,0 +1,209 @@
+"""Decode throughput on the Gemma-2-2B shape on one MI355X.
+
+A step is one greedy decode token through the whole model: embedding, 26
+layers of RMSNorm -> QKV matvec -> KV-cache write -> split-KV FlashDecoding
+-> O projection -> residual, gated MLP -> residual, then the final norm,
+the tied LM head (256000 x 2304) and argmax. Weights are random N(0, 0.02)
+bf16 filled on the device, the KV cache holds 4096 synthetic N(0, 1) rows,
+and the timed steps decode positions 4096, 4097, ... from a prompt token
+drawn uniformly from the vocabulary (seed 0). Steps replay a captured HIP
+graph of `graph_steps` tokens; inputs are resident in HBM before timing.
+
+Besides the JSON line's throughput it reports, per kernel, the mean launch
+time measured with HIP events with the kernel launched alone over every
+layer's weights, its algorithmic bytes and the fraction of the 8 TB/s HBM
+peak; `roofline` is the dominant kernel (the fused gate/up matvec).
+`cpu_baseline` is the CPU oracle (scalar C, one core) timed on a bounded
+sample of the same decode: a few layers' steps plus the LM head, scaled to
+26 layers.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+START_POS = 4096
+
+
+def kernel_bytes(cfg, name, pos):
+    """Algorithmic HBM bytes of one launch of `name` in a decode step at `pos`."""
+    H, F, V = cfg.hidden, cfg.ffn, cfg.vocab
+    QW, KW = cfg.query_heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
+    QKV = QW + 2 * KW
+    if name.startswith("gated_mlp_gate_up"):
+        return 2 * F * H * 2 + H * 2 + H * 4 + F * 2  # Wg, Wu, x, norm w, h
+    if name == "matvec_nk_simd_bf16_bf16_bf16_r1":  # down projection (K = F)
+        return H * F * 2 + F * 2 + H * 2
+    if name == "matvec_nk_simd_bf16_bf16_bf16_r2":  # QKV projection
+        return QKV * H * 2 + H * 2 + QKV * 2
+    if name == "matvec_nk_simd_bf16_bf16_bf16":  # output projection (K = QW)
+        return H * QW * 2 + QW * 2 + H * 2
+    if name == "matvec_nk_simd_bf16_bf16_f32":  # LM head
+        return V * H * 2 + H * 2 + V * 4
+    if name.startswith("flash_decoding_partial"):
+        return 2 * KW * (pos + 1) * 2 + 2 * QW * 2  # K and V rows + q
+    return None
+
+
+def cpu_baseline(dec, cfg, stream, token, layers_sample=3, steps_sample=2):
+    """The oracle (scalar C, one thread) on a bounded sample of the decode:
+    `steps_sample` tokens through `layers_sample` layers, plus one LM head,
+    both on this decoder's weights; tok/s extrapolated to all layers."""
+    import oracle as O
+
+    BF = O.BF16
+
+    def host(name, layer=0):
+        t = dec.tensor(name, layer)
+        raw = t.numpy(stream)
+        return raw if t.dtype == "f32" else O.from_bits(raw.view(np.uint16), BF)
+
+    H = cfg.hidden
+    names = [("in_norm", "norm_in"), ("qkv", "w_qkv"), ("o", "w_o"), ("post_attn_norm", "norm_post_attn"),
+             ("pre_ffn_norm", "norm_pre_ffn"), ("gate", "w_gate"), ("up", "w_up"), ("down", "w_down"),
+             ("post_ffn_norm", "norm_post_ffn")]
+    W = [{n: host(t, l) for n, t in names} for l in range(layers_sample)]
+    caches = [(host("k_cache", l)[0].copy(), host("v_cache", l)[0].copy()) for l in range(layers_sample)]
+    emb = host("embedding")
+    x = O.round_to(O.scalar_mul(emb[token], float(np.sqrt(np.float32(H)))), BF)
+    t0 = time.perf_counter()
+    for s in range(steps_sample):
+        for l in range(layers_sample):
+            O.decoder_layer(W[l], x, caches[l][0], caches[l][1], START_POS + s, H=H, Nq=cfg.query_heads,
+                            Nkv=cfg.kv_heads, Hd=cfg.head_dim, F=cfg.ffn, eps=cfg.eps, scale=cfg.attn_scale,
+                            act_tag=BF)
+    t_layers = (time.perf_counter() - t0) / (steps_sample * layers_sample)
+    n = O.round_to(O.rmsnorm(x, host("final_norm"), cfg.eps), BF)
+    t0 = time.perf_counter()
+    logits = O.matmul(n, emb, 1, H, cfg.vocab, True)
+    O.argmax(logits)
+    t_head = time.perf_counter() - t0
+    sec_per_token = cfg.layers * t_layers + t_head
+    return {"value": 1.0 / sec_per_token, "unit": "tok/s", "cores": 1, "kind": "port",
+            "sample": (f"oracle decode of {steps_sample} tokens through {layers_sample} of {cfg.layers} layers at "
+                       f"ctx {START_POS} ({t_layers * 1e3:.0f} ms/layer) + 1 LM head ({t_head * 1e3:.0f} ms), "
+                       f"scaled to {cfg.layers} layers")}
+
+
+def load_traffic(name):
+    """HBM bytes per launch of `name` from the committed rocprofv3 --pmc summary."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        t = json.load(f)
+    return t.get(name, {}).get("bytes_per_launch")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--graph-steps", type=int, default=8)
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kernel-reps", type=int, default=4)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (every GPU box here has one GPU); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import popcorn_amd as pa
+    import popcorn_amd.decoder as D
+
+    if pa.device_count() < 1:
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    lib = pa.KernelLibrary()
+    stream = pa.Stream()
+    cfg = D.DecoderConfig(graph_steps=args.graph_steps)
+    dec = D.Decoder(lib, stream, cfg)
+    dec.randomize(seed=0)
+    token = int(np.random.default_rng(0).integers(cfg.vocab))
+    use_graph = not args.no_graph
+    if START_POS + max(args.steps, args.warmup) > cfg.max_seq:
+        raise SystemExit(f"steps above {cfg.max_seq - START_POS} leave the KV cache")
+
+    # warmup (captures the graph), then the timed region from the same start
+    dec.reset(token, START_POS)
+    dec.step(args.warmup, use_graph=use_graph)
+    stream.synchronize()
+    dec.reset(token, START_POS)
+    pa.synchronize()
+    start, stop = pa.Event(), pa.Event()
+    t0 = time.perf_counter()
+    start.record(stream)
+    dec.step(args.steps, use_graph=use_graph)
+    stop.record(stream)
+    stop.synchronize()
+    pa.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = start.elapsed_ms(stop)
+    elapsed = max(wall, gpu_ms / 1e3)
+    tok, pos = dec.read()
+    assert pos == START_POS + args.steps, (pos, args.steps)
+    tokens_per_s = args.steps / elapsed
+    mean_pos = START_POS + (args.steps - 1) / 2
+    step_bytes = dec.step_bytes(int(mean_pos))
+
+    # per-kernel timing, each kernel alone over all layers' weights
+    names, nd = dec.describe()
+    dec.reset(token, START_POS)
+    kernels = {}
+    for name in dict.fromkeys(names):
+        nbytes = kernel_bytes(cfg, name, START_POS)
+        if nbytes is None:
+            continue
+        ms, launches = dec.time_kernel(name, reps=args.kernel_reps)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        kernels[name] = {"mean_us": round(ms * 1e3, 2), "bytes": nbytes, "GB_s": round(gbs, 1),
+                         "frac": round(gbs / HBM_PEAK_GBS, 3), "launches_timed": launches}
+    dominant = "gated_mlp_gate_up_bf16"
+    dk = kernels[dominant]
+    roofline = {"bound": "hbm", "achieved": dk["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(dk["GB_s"] / HBM_PEAK_GBS, 3), "traffic": load_traffic(dominant),
+                "kernel": dominant, "bytes_per_launch": dk["bytes"], "mean_us": dk["mean_us"]}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(dec, cfg, stream, token)
+
+    line = {
+        "metric": "decode tok/s (Gemma-2B shape, ctx 4K)",
+        "value": round(tokens_per_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(elapsed * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random N(0,0.02) bf16 weights, N(0,1) KV prefix, uniform prompt token; seed 0)",
+        "config": {"workload": "gemma2-2b-shape greedy decode, batch 1, ctx 4096 -> 4096+steps (BASELINE config 4)",
+                   "layers": cfg.layers, "hidden": cfg.hidden, "heads": f"{cfg.query_heads}q/{cfg.kv_heads}kv x {cfg.head_dim}",
+                   "ffn": cfg.ffn, "vocab": cfg.vocab, "graph_steps": cfg.graph_steps if use_graph else 0,
+                   "dispatches_per_step": nd},
+        "hbm_step_GB_s": round(step_bytes * tokens_per_s / 1e9, 1),
+        "hbm_step_frac": round(step_bytes * tokens_per_s / 1e9 / HBM_PEAK_GBS, 3),
+        "roofline": roofline,
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+    }
+    dec.close()
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -177,12 +177,14 @@ typedef struct {
     float stddev;
 } FillNormalConstants;
 
-/* The decode-step position update that closes a captured decode step: the
- * position tensor is advanced by `delta` (a kernel, so graph replays need no
- * memset or host write). No counterpart in the reference (GemmaCLI writes the
- * position from the CPU, Gemma4TextInference.swift:95-99). */
+/* The update that closes a captured decode step: the step's token is stored
+ * in history[position % historyLen] (when historyLen > 0) and the position
+ * tensor advances by `delta` (a kernel, so graph replays need no memset or
+ * host write). No counterpart in the reference (GemmaCLI writes the position
+ * from the CPU, Gemma4TextInference.swift:95-99). */
 typedef struct {
     int32_t delta;
+    uint32_t historyLen;
 } PositionAdvanceConstants;
 
 #ifdef __cplusplus

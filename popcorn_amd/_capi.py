@@ -56,6 +56,13 @@ class ScratchAllocatorDesc(C.Structure):
     _fields_ = [("context", C.c_void_p), ("borrow", BORROW_FN), ("release", RELEASE_FN)]
 
 
+class DecoderConfig(C.Structure):
+    _fields_ = [("layers", C.c_int32), ("hidden", C.c_int32), ("query_heads", C.c_int32),
+                ("kv_heads", C.c_int32), ("head_dim", C.c_int32), ("ffn", C.c_int32), ("vocab", C.c_int32),
+                ("max_seq", C.c_int32), ("eps", C.c_float), ("attn_scale", C.c_float),
+                ("history_len", C.c_int32), ("graph_steps", C.c_int32)]
+
+
 _T = C.POINTER(TensorDesc)
 _K = C.POINTER(C.c_void_p)
 _st = C.c_int32
@@ -129,6 +136,18 @@ PROTOTYPES = {
     "popcorn_kernel_describe": (_st, [C.c_void_p, C.c_char_p, C.c_size_t]),
     "popcorn_fill_normal": (_st, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_uint64, C.c_uint64,
                                   C.c_float, C.c_float]),
+    # include/popcorn_decoder.h
+    "popcorn_decoder_create": (_st, [C.c_void_p, C.c_void_p, C.POINTER(DecoderConfig), C.POINTER(C.c_void_p)]),
+    "popcorn_decoder_destroy": (_st, [C.c_void_p]),
+    "popcorn_decoder_randomize": (_st, [C.c_void_p, C.c_uint64]),
+    "popcorn_decoder_tensor": (_st, [C.c_void_p, C.c_char_p, C.c_int32, _T]),
+    "popcorn_decoder_reset": (_st, [C.c_void_p, C.c_int32, C.c_int32]),
+    "popcorn_decoder_step": (_st, [C.c_void_p, C.c_int32, C.c_int32]),
+    "popcorn_decoder_read": (_st, [C.c_void_p, C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
+    "popcorn_decoder_describe": (_st, [C.c_void_p, C.c_char_p, C.c_size_t, C.POINTER(C.c_int32)]),
+    "popcorn_decoder_step_bytes": (C.c_int64, [C.c_void_p, C.c_int32]),
+    "popcorn_decoder_time_kernel": (_st, [C.c_void_p, C.c_char_p, C.c_int32, C.POINTER(C.c_float),
+                                          C.POINTER(C.c_int32)]),
 }
 
 _lib = None

@@ -123,9 +123,14 @@ POPCORN_KERNEL void __launch_bounds__(256)
     }
 }
 
-// pos[0] += delta: the last node of a captured decode step.
-POPCORN_KERNEL void position_advance(int32_t *pos, PositionAdvanceConstants p) {
-    if (threadIdx.x == 0 && blockIdx.x == 0) pos[0] += p.delta;
+// The last node of a captured decode step: record the step's token, then
+// pos[0] += delta.
+POPCORN_KERNEL void position_advance(const int32_t *token, int32_t *pos, int32_t *history, PositionAdvanceConstants p) {
+    if (threadIdx.x == 0 && blockIdx.x == 0) {
+        const int32_t at = pos[0];
+        if (p.historyLen && at >= 0) history[(uint32_t)at % p.historyLen] = token[0];
+        pos[0] = at + p.delta;
+    }
 }
 
 namespace {

@@ -4,13 +4,10 @@
 #include <cstring>
 #include <new>
 
-#include "popcorn.hpp"
+#include "handles.hpp"
 
 using namespace popcorn;
 
-struct popcorn_library_s {
-    std::unique_ptr<KernelLibrary> lib;
-};
 struct popcorn_function_s {
     const Function *fn;
 };

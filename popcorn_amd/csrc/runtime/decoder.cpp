@@ -1,0 +1,401 @@
+// The batch-1 greedy decode loop (include/popcorn_decoder.h): device state,
+// the per-step kernel list built once from Kernels.* descriptors, and HIP
+// graph capture/replay of whole steps.
+#include <cmath>
+#include <cstring>
+
+#include "handles.hpp"
+#include "popcorn_decoder.h"
+
+using namespace popcorn;
+
+namespace {
+
+struct Buffer {
+    void *p = nullptr;
+    size_t bytes = 0;
+    Buffer() = default;
+    explicit Buffer(size_t n) : bytes(n) {
+        if (hipMalloc(&p, n ? n : 1) != hipSuccess) {
+            (void)hipGetLastError();
+            p = nullptr;
+            throw Error::tensorAllocationFailed(n);
+        }
+    }
+    Buffer(const Buffer &) = delete;
+    Buffer &operator=(const Buffer &) = delete;
+    Buffer(Buffer &&o) noexcept : p(o.p), bytes(o.bytes) { o.p = nullptr; }
+    Buffer &operator=(Buffer &&o) noexcept {
+        std::swap(p, o.p);
+        std::swap(bytes, o.bytes);
+        return *this;
+    }
+    ~Buffer() {
+        if (p) (void)hipFree(p);
+    }
+    template <typename T = uint8_t>
+    T *at(size_t byteOffset) const { return reinterpret_cast<T *>(static_cast<uint8_t *>(p) + byteOffset); }
+};
+
+}  // namespace
+
+struct popcorn_decoder_s {
+    popcorn_decoder_config_t cfg{};
+    KernelLibrary *lib = nullptr;
+    hipStream_t stream = nullptr;
+    ScratchPool pool;
+    std::unique_ptr<KernelCommandEncoder> enc;
+
+    // sizes
+    int64_t L = 0, H = 0, Nq = 0, Nkv = 0, Hd = 0, F = 0, V = 0, S = 0, QW = 0, KW = 0, QKV = 0;
+
+    // weights (bf16 unless noted) and state
+    Buffer embedding, finalNorm /*f32*/, wqkv, wo, wg, wu, wd, norms /*f32 [L][4][H]*/;
+    Buffer kcache, vcache;
+    Buffer x, e, n, qkv, attn, o, t, mlp, hidden, logits /*f32*/, token /*i32*/, position /*i32*/, history /*i32*/;
+
+    std::vector<std::unique_ptr<Kernel>> step;
+    std::vector<std::string> names;
+    hipGraphExec_t graph = nullptr;
+    hipGraph_t graphDef = nullptr;
+    int graphSteps = 1;
+
+    ~popcorn_decoder_s() {
+        if (graph) (void)hipGraphExecDestroy(graph);
+        if (graphDef) (void)hipGraphDestroy(graphDef);
+    }
+
+    Tensor bf(void *p, Shape s) const { return Tensor(p, std::move(s), DataType::bf16); }
+
+    size_t layerOffset(int64_t elemsPerLayer, int64_t l, int es = 2) const { return (size_t)(elemsPerLayer * l) * (size_t)es; }
+
+    Tensor weight(const char *which, int64_t l) const {
+        if (!strcmp(which, "w_qkv")) return bf(wqkv.at(layerOffset(QKV * H, l)), {QKV, H});
+        if (!strcmp(which, "w_o")) return bf(wo.at(layerOffset(H * QW, l)), {H, QW});
+        if (!strcmp(which, "w_gate")) return bf(wg.at(layerOffset(F * H, l)), {F, H});
+        if (!strcmp(which, "w_up")) return bf(wu.at(layerOffset(F * H, l)), {F, H});
+        if (!strcmp(which, "w_down")) return bf(wd.at(layerOffset(H * F, l)), {H, F});
+        if (!strcmp(which, "k_cache")) return bf(kcache.at(layerOffset(Nkv * S * Hd, l)), {1, Nkv, S, Hd});
+        if (!strcmp(which, "v_cache")) return bf(vcache.at(layerOffset(Nkv * S * Hd, l)), {1, Nkv, S, Hd});
+        int slot = !strcmp(which, "norm_in") ? 0 : !strcmp(which, "norm_post_attn") ? 1 : !strcmp(which, "norm_pre_ffn") ? 2
+                 : !strcmp(which, "norm_post_ffn") ? 3 : -1;
+        if (slot >= 0) return Tensor(norms.at(layerOffset(H, l * 4 + slot, 4)), Shape({H}), DataType::f32);
+        throw Error::invalidArgument(std::string("unknown decoder tensor ") + which);
+    }
+
+    void build() {
+        const float eps = cfg.eps;
+        Tensor tx = bf(x.p, {1, H}), te = bf(e.p, {1, H}), tn = bf(n.p, {1, H});
+        Tensor tqkv = bf(qkv.p, {1, QKV});
+        Tensor tq = bf(qkv.p, {1, Nq, 1, Hd});
+        Tensor tk = bf(qkv.at(QW * 2), {1, Nkv, 1, Hd});
+        Tensor tv = bf(qkv.at((QW + KW) * 2), {1, Nkv, 1, Hd});
+        Tensor tattn4 = bf(attn.p, {1, Nq, 1, Hd}), tattn = bf(attn.p, {1, QW});
+        Tensor to = bf(o.p, {1, H}), tt = bf(t.p, {1, H}), tmlp = bf(mlp.p, {1, H}), th = bf(hidden.p, {F});
+        Tensor tpos(position.p, Shape({1}), DataType::i32);
+        Tensor ttok(token.p, Shape({1}), DataType::i32);
+        Tensor temb = bf(embedding.p, {V, H});
+        Tensor tlog(logits.p, Shape({1, V}), DataType::f32);
+        Tensor tfin(finalNorm.p, Shape({H}), DataType::f32);
+
+        auto add = [&](std::unique_ptr<Kernel> k) { step.push_back(std::move(k)); };
+        // Gemma4TextInference.swift:184-185: gather, then scale by sqrt(H)
+        add(Kernels::EmbeddingGather(ttok, temb, te));
+        add(Kernels::ScalarMul(te, std::sqrt((float)H), tx));
+        const AttentionMask causal{0, -1};
+        for (int64_t l = 0; l < L; ++l) {
+            Tensor nin = weight("norm_in", l), npa = weight("norm_post_attn", l);
+            Tensor npf = weight("norm_pre_ffn", l), npo = weight("norm_post_ffn", l);
+            Tensor kc = weight("k_cache", l), vc = weight("v_cache", l);
+            add(Kernels::RMSNorm(tx, &nin, tn, 1, H, eps, false));
+            add(Kernels::Matmul(tn, weight("w_qkv", l), tqkv, true));
+            add(Kernels::KVCacheWrite(tk, kc, 1, Nkv, 1, S, Hd, 0, &tpos));
+            add(Kernels::KVCacheWrite(tv, vc, 1, Nkv, 1, S, Hd, 0, &tpos));
+            add(Kernels::FlashAttention(tq, kc, vc, tattn4, 1, Nq, Nkv, 1, 1, Hd, cfg.attn_scale, causal, S, &tpos));
+            add(Kernels::Matmul(tattn, weight("w_o", l), to, true));
+            add(Kernels::RMSNorm(to, &npa, tt, 1, H, eps, false));
+            add(Kernels::Add(tx, tt, tx));
+            add(Kernels::GatedMLP(tx, &npf, weight("w_gate", l), weight("w_up", l), weight("w_down", l), tmlp, eps, false, &th));
+            add(Kernels::RMSNorm(tmlp, &npo, tt, 1, H, eps, false));
+            add(Kernels::Add(tx, tt, tx));
+        }
+        // Gemma4TextInference.swift:201-206 (the final norm, LM head, argmax)
+        add(Kernels::RMSNorm(tx, &tfin, tn, 1, H, eps, false));
+        add(Kernels::Matmul(tn, temb, tlog, true));
+        add(Kernels::Argmax(tlog, ttok));
+        PositionAdvanceConstants pc{1, (uint32_t)std::max(cfg.history_len, 0)};
+        Tensor thist(history.p, Shape({std::max<int64_t>(cfg.history_len, 1)}), DataType::i32);
+        add(Kernels::Custom("position_advance", {{ttok, kRead}, {tpos, kReadWrite}, {thist, kWrite}}, {bytesOf(pc)},
+                            dim3(1, 1, 1), dim3(64, 1, 1)));
+        for (const auto &k : step) {
+            std::string d = k->describe();
+            size_t s = 0;
+            while (s <= d.size()) {
+                size_t c = d.find(',', s);
+                if (c == std::string::npos) c = d.size();
+                names.push_back(d.substr(s, c - s));
+                s = c + 1;
+            }
+        }
+    }
+
+    void encodeStep() {
+        for (const auto &k : step) enc->encode(*k);
+    }
+
+    void capture() {
+        if (graph) return;
+        // One eager step caches every function and fills the scratch pool, so
+        // the capture allocates nothing; token and position are restored (the
+        // KV row it wrote is rewritten by the first real step).
+        int32_t tok = 0, pos = 0;
+        checkHip(hipMemcpyAsync(&tok, token.p, 4, hipMemcpyDeviceToHost, stream), "read token");
+        checkHip(hipMemcpyAsync(&pos, position.p, 4, hipMemcpyDeviceToHost, stream), "read position");
+        checkHip(hipStreamSynchronize(stream), "sync");
+        encodeStep();
+        checkHip(hipMemcpyAsync(token.p, &tok, 4, hipMemcpyHostToDevice, stream), "restore token");
+        checkHip(hipMemcpyAsync(position.p, &pos, 4, hipMemcpyHostToDevice, stream), "restore position");
+        checkHip(hipStreamSynchronize(stream), "sync");
+        checkHip(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+        try {
+            for (int i = 0; i < graphSteps; ++i) encodeStep();
+        } catch (...) {
+            hipGraph_t g = nullptr;
+            (void)hipStreamEndCapture(stream, &g);
+            if (g) (void)hipGraphDestroy(g);
+            throw;
+        }
+        checkHip(hipStreamEndCapture(stream, &graphDef), "hipStreamEndCapture");
+        checkHip(hipGraphInstantiate(&graph, graphDef, nullptr, nullptr, 0), "hipGraphInstantiate");
+    }
+
+    void run(int32_t steps, bool useGraph) {
+        if (steps < 0) throw Error::invalidArgument("steps must be >= 0");
+        if (!useGraph) {
+            for (int32_t i = 0; i < steps; ++i) encodeStep();
+            return;
+        }
+        capture();
+        int32_t i = 0;
+        for (; i + graphSteps <= steps; i += graphSteps) checkHip(hipGraphLaunch(graph, stream), "hipGraphLaunch");
+        for (; i < steps; ++i) encodeStep();
+    }
+
+    int64_t stepBytes(int32_t pos) const {
+        const int64_t layerW = (QKV * H + H * QW + 3 * F * H) * 2 + 4 * H * 4;
+        const int64_t kv = 2 * Nkv * (int64_t)(pos + 1) * Hd * 2;  // K and V rows read
+        return L * (layerW + kv) + V * H * 2 + H * 4 + V * 4;
+    }
+};
+
+static popcorn_status_t guardedDec(const std::function<void()> &f) {
+    try {
+        f();
+        setLastError("");
+        return POPCORN_OK;
+    } catch (const Error &e) {
+        setLastError(e.what());
+        return e.code();
+    } catch (const std::exception &e) {
+        setLastError(e.what());
+        return POPCORN_ERR_GPU_INTERNAL;
+    }
+}
+
+extern "C" {
+
+popcorn_status_t popcorn_decoder_create(popcorn_library_t library, popcorn_stream_t stream,
+                                        const popcorn_decoder_config_t *config, popcorn_decoder_t *decoder) {
+    return guardedDec([&] {
+        if (!library || !config || !decoder) throw Error::invalidArgument("library, config and decoder must not be NULL");
+        const popcorn_decoder_config_t &c = *config;
+        if (c.layers <= 0 || c.hidden <= 0 || c.query_heads <= 0 || c.kv_heads <= 0 || c.head_dim <= 0 || c.ffn <= 0 ||
+            c.vocab <= 0 || c.max_seq <= 0)
+            throw Error::tensorShapeMismatch("decoder dimensions must be positive");
+        auto d = std::make_unique<popcorn_decoder_s>();
+        d->cfg = c;
+        d->lib = library->lib.get();
+        d->stream = reinterpret_cast<hipStream_t>(stream);
+        d->graphSteps = std::max(1, c.graph_steps);
+        d->L = c.layers;
+        d->H = c.hidden;
+        d->Nq = c.query_heads;
+        d->Nkv = c.kv_heads;
+        d->Hd = c.head_dim;
+        d->F = c.ffn;
+        d->V = c.vocab;
+        d->S = c.max_seq;
+        d->QW = d->Nq * d->Hd;
+        d->KW = d->Nkv * d->Hd;
+        d->QKV = d->QW + 2 * d->KW;
+        const int64_t L = d->L, H = d->H, F = d->F;
+        d->embedding = Buffer((size_t)(d->V * H * 2));
+        d->finalNorm = Buffer((size_t)(H * 4));
+        d->wqkv = Buffer((size_t)(L * d->QKV * H * 2));
+        d->wo = Buffer((size_t)(L * H * d->QW * 2));
+        d->wg = Buffer((size_t)(L * F * H * 2));
+        d->wu = Buffer((size_t)(L * F * H * 2));
+        d->wd = Buffer((size_t)(L * H * F * 2));
+        d->norms = Buffer((size_t)(L * 4 * H * 4));
+        d->kcache = Buffer((size_t)(L * d->Nkv * d->S * d->Hd * 2));
+        d->vcache = Buffer((size_t)(L * d->Nkv * d->S * d->Hd * 2));
+        d->x = Buffer((size_t)(H * 2));
+        d->e = Buffer((size_t)(H * 2));
+        d->n = Buffer((size_t)(H * 2));
+        d->qkv = Buffer((size_t)(d->QKV * 2));
+        d->attn = Buffer((size_t)(d->QW * 2));
+        d->o = Buffer((size_t)(H * 2));
+        d->t = Buffer((size_t)(H * 2));
+        d->mlp = Buffer((size_t)(H * 2));
+        d->hidden = Buffer((size_t)(F * 2));
+        d->logits = Buffer((size_t)(d->V * 4));
+        d->token = Buffer(4);
+        d->position = Buffer(4);
+        d->history = Buffer((size_t)(std::max(c.history_len, 1) * 4));
+        checkHip(hipMemsetAsync(d->token.p, 0, 4, d->stream), "memset");
+        checkHip(hipMemsetAsync(d->position.p, 0, 4, d->stream), "memset");
+        checkHip(hipMemsetAsync(d->history.p, 0xff, d->history.bytes, d->stream), "memset");
+        d->enc = std::make_unique<KernelCommandEncoder>(*d->lib, d->stream, d->pool);
+        d->build();
+        *decoder = d.release();
+    });
+}
+
+popcorn_status_t popcorn_decoder_destroy(popcorn_decoder_t decoder) {
+    return guardedDec([&] {
+        if (!decoder) return;
+        (void)hipStreamSynchronize(decoder->stream);
+        delete decoder;
+    });
+}
+
+popcorn_status_t popcorn_decoder_randomize(popcorn_decoder_t d, uint64_t seed) {
+    return guardedDec([&] {
+        if (!d) throw Error::invalidArgument("decoder must not be NULL");
+        uint64_t s = seed * 1000;
+        auto fill = [&](Buffer &b, DataType t, float mean, float std) {
+            d->enc->encode(*Kernels::FillNormal(b.p, t, b.bytes / (size_t)stride(t), ++s, mean, std));
+        };
+        fill(d->embedding, DataType::bf16, 0.0f, 0.02f);
+        fill(d->finalNorm, DataType::f32, 1.0f, 0.1f);
+        fill(d->wqkv, DataType::bf16, 0.0f, 0.02f);
+        fill(d->wo, DataType::bf16, 0.0f, 0.02f);
+        fill(d->wg, DataType::bf16, 0.0f, 0.02f);
+        fill(d->wu, DataType::bf16, 0.0f, 0.02f);
+        fill(d->wd, DataType::bf16, 0.0f, 0.02f);
+        fill(d->norms, DataType::f32, 1.0f, 0.1f);
+        fill(d->kcache, DataType::bf16, 0.0f, 1.0f);
+        fill(d->vcache, DataType::bf16, 0.0f, 1.0f);
+        checkHip(hipStreamSynchronize(d->stream), "sync");
+    });
+}
+
+popcorn_status_t popcorn_decoder_tensor(popcorn_decoder_t d, const char *name, int32_t layer, popcorn_tensor_t *out) {
+    return guardedDec([&] {
+        if (!d || !name || !out) throw Error::invalidArgument("decoder, name and tensor must not be NULL");
+        Tensor t;
+        std::string n = name;
+        if (n == "embedding") t = d->bf(d->embedding.p, {d->V, d->H});
+        else if (n == "final_norm") t = Tensor(d->finalNorm.p, Shape({d->H}), DataType::f32);
+        else if (n == "x") t = d->bf(d->x.p, {d->H});
+        else if (n == "qkv") t = d->bf(d->qkv.p, {d->QKV});
+        else if (n == "attn") t = d->bf(d->attn.p, {d->QW});
+        else if (n == "o") t = d->bf(d->o.p, {d->H});
+        else if (n == "mlp") t = d->bf(d->mlp.p, {d->H});
+        else if (n == "hidden") t = d->bf(d->hidden.p, {d->F});
+        else if (n == "normed") t = d->bf(d->n.p, {d->H});
+        else if (n == "logits") t = Tensor(d->logits.p, Shape({d->V}), DataType::f32);
+        else if (n == "token") t = Tensor(d->token.p, Shape({1}), DataType::i32);
+        else if (n == "position") t = Tensor(d->position.p, Shape({1}), DataType::i32);
+        else if (n == "history") t = Tensor(d->history.p, Shape({std::max(d->cfg.history_len, 1)}), DataType::i32);
+        else {
+            if (layer < 0 || layer >= d->L) throw Error::invalidArgument("layer out of range");
+            t = d->weight(name, layer);
+        }
+        std::memset(out, 0, sizeof(*out));
+        out->data = t.data;
+        out->dtype = (int32_t)t.dataType;
+        out->rank = t.shape.rank();
+        for (int i = 0; i < t.shape.rank(); ++i) out->shape[i] = t.shape[i];
+    });
+}
+
+popcorn_status_t popcorn_decoder_reset(popcorn_decoder_t d, int32_t token, int32_t position) {
+    return guardedDec([&] {
+        if (!d) throw Error::invalidArgument("decoder must not be NULL");
+        if (token < 0 || token >= d->V) throw Error::invalidArgument("token outside the vocabulary");
+        if (position < 0 || position >= d->S) throw Error::invalidArgument("position outside the KV cache");
+        checkHip(hipMemcpyAsync(d->token.p, &token, 4, hipMemcpyHostToDevice, d->stream), "write token");
+        checkHip(hipMemcpyAsync(d->position.p, &position, 4, hipMemcpyHostToDevice, d->stream), "write position");
+        checkHip(hipStreamSynchronize(d->stream), "sync");
+    });
+}
+
+popcorn_status_t popcorn_decoder_step(popcorn_decoder_t d, int32_t steps, int32_t use_graph) {
+    return guardedDec([&] {
+        if (!d) throw Error::invalidArgument("decoder must not be NULL");
+        d->run(steps, use_graph != 0);
+    });
+}
+
+popcorn_status_t popcorn_decoder_read(popcorn_decoder_t d, int32_t *token, int32_t *position) {
+    return guardedDec([&] {
+        if (!d) throw Error::invalidArgument("decoder must not be NULL");
+        int32_t v[2] = {0, 0};
+        checkHip(hipMemcpyAsync(&v[0], d->token.p, 4, hipMemcpyDeviceToHost, d->stream), "read token");
+        checkHip(hipMemcpyAsync(&v[1], d->position.p, 4, hipMemcpyDeviceToHost, d->stream), "read position");
+        checkHip(hipStreamSynchronize(d->stream), "sync");
+        if (token) *token = v[0];
+        if (position) *position = v[1];
+    });
+}
+
+popcorn_status_t popcorn_decoder_describe(popcorn_decoder_t d, char *buffer, size_t capacity, int32_t *dispatches) {
+    return guardedDec([&] {
+        if (!d) throw Error::invalidArgument("decoder must not be NULL");
+        std::string s;
+        for (size_t i = 0; i < d->names.size(); ++i) s += (i ? "," : "") + d->names[i];
+        if (dispatches) *dispatches = (int32_t)d->names.size();
+        if (buffer && capacity) {
+            std::strncpy(buffer, s.c_str(), capacity - 1);
+            buffer[capacity - 1] = '\0';
+        }
+    });
+}
+
+int64_t popcorn_decoder_step_bytes(popcorn_decoder_t d, int32_t position) { return d ? d->stepBytes(position) : 0; }
+
+popcorn_status_t popcorn_decoder_time_kernel(popcorn_decoder_t d, const char *function_name, int32_t reps,
+                                             float *mean_ms, int32_t *launches) {
+    return guardedDec([&] {
+        if (!d || !function_name || !mean_ms) throw Error::invalidArgument("decoder, name and mean_ms must not be NULL");
+        if (reps <= 0) throw Error::invalidArgument("reps must be positive");
+        int32_t per = 0;
+        for (const std::string &n : d->names) per += (n == function_name) ? 1 : 0;
+        if (per == 0) throw Error::kernelFunctionNotFound(std::string(function_name) + " (not dispatched by a decode step)");
+        hipEvent_t a = nullptr, b = nullptr;
+        checkHip(hipEventCreate(&a), "hipEventCreate");
+        checkHip(hipEventCreate(&b), "hipEventCreate");
+        struct Cleanup {
+            popcorn_decoder_s *d;
+            hipEvent_t a, b;
+            ~Cleanup() {
+                d->enc->setDispatchFilter("");
+                (void)hipEventDestroy(a);
+                (void)hipEventDestroy(b);
+            }
+        } cleanup{d, a, b};
+        d->enc->setDispatchFilter(function_name);
+        d->encodeStep();  // warm: first launch of each
+        checkHip(hipEventRecord(a, d->stream), "hipEventRecord");
+        for (int32_t r = 0; r < reps; ++r) d->encodeStep();
+        checkHip(hipEventRecord(b, d->stream), "hipEventRecord");
+        checkHip(hipEventSynchronize(b), "hipEventSynchronize");
+        float ms = 0;
+        checkHip(hipEventElapsedTime(&ms, a, b), "hipEventElapsedTime");
+        *mean_ms = ms / (float)(per * reps);
+        if (launches) *launches = per * reps;
+    });
+}
+
+}  // extern "C"

@@ -255,6 +255,9 @@ public:
     KernelLibrary &library() { return library_; }
     hipStream_t stream() const { return stream_; }
     popcorn_encoder_stats_t stats() const;
+    // When set, dispatch() launches only kernels with this function name and
+    // skips the rest (used to time one kernel of a composite sequence).
+    void setDispatchFilter(const std::string &functionName) { filter_ = functionName; }
 
 private:
     bool needsBarrier(const std::vector<Binding> &bindings) const;
@@ -265,6 +268,7 @@ private:
     KernelScratchAllocator &scratch_;
     std::map<const void *, uint8_t> accessByBuffer_;
     int64_t dispatches_ = 0, hazards_ = 0, scratchBorrows_ = 0;
+    std::string filter_;
 };
 
 // ---- Kernels.* descriptors --------------------------------------------------

@@ -254,6 +254,7 @@ void KernelCommandEncoder::recordAccesses(const std::vector<Binding> &bindings) 
 void KernelCommandEncoder::barrier() { accessByBuffer_.clear(); }
 
 void KernelCommandEncoder::dispatch(const DispatchKernel &kernel) {
+    if (!filter_.empty() && kernel.functionName() != filter_) return;
     const std::vector<Binding> bindings = kernel.tensors();
     if (needsBarrier(bindings)) {
         // One in-order stream: the previous dispatch's writes are visible to

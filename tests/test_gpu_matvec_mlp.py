@@ -153,18 +153,19 @@ def test_gated_mlp_vs_composition(env, dtype, H, F):
     h_ref, ref = O.gated_mlp(x, nw, 1e-6, wg, wu, wd, inter_tag=TAG[dtype])
     eps = EPS[dtype]
     assert_out(download(out, stream), ref, eps, dtype, "gated MLP out")
-    # h is an intermediate the reference stores as a 16-bit tensor: g and u
-    # are f32 sums whose last bits depend on summation order, so a g or u that
-    # sits next to a rounding midpoint may round the other way (probability
-    # ~1e-3 per value at these sizes) and move h by an ulp or two.
+    # h is an intermediate the reference stores as a 16-bit tensor. The
+    # normalised x is stored too: when one of its H values sits on a bf16
+    # rounding midpoint, the GPU's and the oracle's f32 scale (sums in a
+    # different order) may round it apart by one ulp, and since every g and u
+    # is a dot product with that vector, all of them shift by ~1e-4 and a few
+    # percent of their bf16 roundings flip. h is rounded twice after that
+    # (a = round(gelu(g)), h = round(a * u)), so it is held to the output bar
+    # with two ulps; the MLP output above keeps the full bar.
     h = download(hid, stream)
     if dtype == "f32":
         assert_approx(h, h_ref, 1e-5, "gated hidden")
     else:
-        same = np.mean(h == h_ref)
-        assert same >= 0.99, f"only {same:.4f} of h matches the composition bit for bit"
-        m = np.maximum(np.abs(h), np.abs(h_ref))
-        assert np.all(np.abs(h - h_ref) <= 4 * half_ulp(m, dtype) + 1e-30), "h off by more than 2 ulps"
+        assert_out(h, h_ref, eps, dtype, "gated hidden", half_ulps=4)
 
 
 def test_gated_mlp_scratch_hidden_and_add_one(env):
