@@ -38,16 +38,16 @@ def kernel_bytes(cfg, name, pos):
     H, F, V = cfg.hidden, cfg.ffn, cfg.vocab
     QW, KW = cfg.query_heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
     QKV = QW + 2 * KW
-    if name.startswith("gated_mlp_gate_up"):
-        return 2 * F * H * 2 + H * 2 + H * 4 + F * 2  # Wg, Wu, x, norm w, h
+    if name.startswith("gated_mlp_gate_up"):  # residual + norm, Wg and Wu, h
+        return 2 * F * H * 2 + 3 * H * 2 + 2 * H * 4 + F * 2
     if name == "matvec_nk_simd_bf16_bf16_bf16_r1":  # down projection (K = F)
         return H * F * 2 + F * 2 + H * 2
-    if name == "matvec_nk_simd_bf16_bf16_bf16_r2":  # QKV projection
-        return QKV * H * 2 + H * 2 + QKV * 2
-    if name == "matvec_nk_simd_bf16_bf16_bf16":  # output projection (K = QW)
+    if name in ("decode_matvec_bf16_bf16_r1_f2", "decode_matvec_bf16_bf16_r1_f3"):  # QKV (+ residual), norm, KV scatter
+        return QKV * H * 2 + 3 * H * 2 + 2 * H * 4 + QKV * 2
+    if name == "decode_matvec_bf16_bf16_r1_f0":  # output projection (K = QW)
         return H * QW * 2 + QW * 2 + H * 2
-    if name == "matvec_nk_simd_bf16_bf16_f32":  # LM head
-        return V * H * 2 + H * 2 + V * 4
+    if name == "decode_matvec_bf16_f32_r4_f3":  # residual, final norm, LM head
+        return V * H * 2 + 3 * H * 2 + 2 * H * 4 + V * 4
     if name.startswith("flash_decoding_partial"):
         return 2 * KW * (pos + 1) * 2 + 2 * QW * 2  # K and V rows + q
     return None
@@ -168,7 +168,7 @@ def main():
         gbs = nbytes / (ms * 1e-3) / 1e9
         kernels[name] = {"mean_us": round(ms * 1e3, 2), "bytes": nbytes, "GB_s": round(gbs, 1),
                          "frac": round(gbs / HBM_PEAK_GBS, 3), "launches_timed": launches}
-    dominant = "gated_mlp_gate_up_bf16"
+    dominant = "gated_mlp_gate_up_bf16_r1_res"
     dk = kernels[dominant]
     roofline = {"bound": "hbm", "achieved": dk["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(dk["GB_s"] / HBM_PEAK_GBS, 3), "traffic": load_traffic(dominant),

@@ -58,7 +58,7 @@ popcorn_status_t popcorn_decoder_randomize(popcorn_decoder_t decoder, uint64_t s
  * "w_gate", "w_up", "w_down", "norm_in", "norm_post_attn", "norm_pre_ffn",
  * "norm_post_ffn", "k_cache", "v_cache" (per `layer`), and "x", "logits",
  * "token", "position", "history", plus the last layer's step buffers
- * "normed", "qkv", "attn", "o", "mlp", "hidden". */
+ * "q", "attn", "o", "mlp", "hidden". */
 popcorn_status_t popcorn_decoder_tensor(popcorn_decoder_t decoder, const char *name, int32_t layer,
                                         popcorn_tensor_t *tensor);
 

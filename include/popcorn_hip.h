@@ -321,6 +321,42 @@ popcorn_status_t popcorn_kernel_gated_mlp(const popcorn_tensor_t *x, const popco
                                           float eps, int32_t add_one_to_weight,
                                           const popcorn_tensor_t *hidden, popcorn_kernel_t *kernel);
 
+/* The gated MLP with the attention block's post-norm and residual Add in
+ * front (Gemma4TextInference.swift:400-404 then :416-429):
+ * x = x_in + RMSNorm(delta) * w_post is stored to x_out (which must not alias
+ * x_in), then out = GatedMLP(x). No single counterpart in the reference. */
+popcorn_status_t popcorn_kernel_gated_mlp_residual(const popcorn_tensor_t *x_in, const popcorn_tensor_t *delta,
+                                                   const popcorn_tensor_t *w_post, const popcorn_tensor_t *x_out,
+                                                   const popcorn_tensor_t *norm_weight, const popcorn_tensor_t *w_gate,
+                                                   const popcorn_tensor_t *w_up, const popcorn_tensor_t *w_down,
+                                                   const popcorn_tensor_t *out, float eps, int32_t add_one_to_weight,
+                                                   const popcorn_tensor_t *hidden, popcorn_kernel_t *kernel);
+
+/* The decode-step matvec out = W v (W [N, K], one token) with the layer glue
+ * around it (DecodeMatvecConstants in popcorn_kernel_types.h): with delta,
+ * x = x + RMSNorm(delta) * w_post is formed and stored to x_out; with w_pre,
+ * v = RMSNorm(x) * w_pre, else v = x; with the caches, rows past q_rows are
+ * written to the K then V cache at row position[0] of each KV head. Every
+ * stored intermediate is rounded to the weight dtype. NULL = absent. No
+ * single counterpart in the reference (its RMSNorm, Add, Matmul and
+ * KVCacheWrite dispatches, Gemma4TextInference.swift:334-404). */
+typedef struct {
+    const popcorn_tensor_t *x;
+    const popcorn_tensor_t *delta;
+    const popcorn_tensor_t *w_post;
+    const popcorn_tensor_t *x_out;
+    const popcorn_tensor_t *w_pre;
+    const popcorn_tensor_t *weight;
+    const popcorn_tensor_t *out;
+    const popcorn_tensor_t *k_cache;
+    const popcorn_tensor_t *v_cache;
+    const popcorn_tensor_t *position;
+    int64_t q_rows;
+    float eps;
+} popcorn_decode_matvec_args_t;
+
+popcorn_status_t popcorn_kernel_decode_matvec(const popcorn_decode_matvec_args_t *args, popcorn_kernel_t *kernel);
+
 /* Kernels.EmbeddingGather(ids:table:out:tokenCount:hiddenSize:)
  * (EmbeddingGather.swift) and Kernels.Argmax(_:indices:axis:) (Argmax.swift:24-37):
  * the decode loop's token in / token out. */

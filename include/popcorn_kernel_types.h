@@ -166,7 +166,33 @@ typedef struct {
     uint32_t addOneToWeight;
     float eps;
     uint32_t interDataType;
+    uint32_t residual;  /* 1: x = x_in + RMSNorm(delta; w_post) first (see below) */
 } GatedMLPConstants;
+
+/* No counterpart in the reference: the decode-step matvec y = W x (W [N, K])
+ * with the neighbouring glue of a decoder layer folded in. flags:
+ *   bit 0  residual: x = round(x_in + round(RMSNorm(delta; w_post))), the
+ *          reference's post-norm + residual Add (Gemma4TextInference.swift:
+ *          400-404, :430-434); block 0 stores x to x_out;
+ *   bit 1  pre-norm: the vector multiplied is round(RMSNorm(x; w_pre)), the
+ *          reference's input norm (:334, :416);
+ *   bit 2  KV scatter: rows [qRows, qRows + kvRows) go to the K cache and the
+ *          next kvRows rows to the V cache, at row position[0] of each KV
+ *          head (head = (row - start) / headDim), the reference's KV-cache
+ *          writes (:372-381); rows below qRows go to out.
+ * Rounding points use interDataType (the storage dtype of the reference's
+ * intermediates). */
+typedef struct {
+    uint32_t K;
+    uint32_t N;
+    float eps;
+    uint32_t flags;
+    uint32_t interDataType;
+    uint32_t qRows;
+    uint32_t kvRows;
+    uint32_t headDim;
+    uint32_t kvStride;
+} DecodeMatvecConstants;
 
 /* No counterpart in the reference: device-side fill of synthetic inputs
  * (counter-based normal generator) for benchmarks. */

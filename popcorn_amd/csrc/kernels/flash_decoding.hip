@@ -330,42 +330,70 @@ __device__ void fd_partial_generic(const typename T::storage *__restrict__ Q, co
     }
 }
 
-// LSE combine, FlashDecoding.metal:179-228: one block per (b, hq, row).
+// LSE combine, FlashDecoding.metal:179-228:
+//   m* = max m_k, l* = sum exp(m_k - m*) l_k, O = sum exp(m_k - m*) O_k / l*.
+// Grid: x = (b * Nq + hq) * Sq + row, y = 64-dim slice of the head. Lane =
+// one dim; the 4 waves take interleaved partitions, each folding its
+// partitions in with a running max (so all of a wave's loads are
+// independent and in flight together), then the 4 wave states are merged
+// in LDS. Empty partitions (m = -inf, l = 0) contribute nothing.
+constexpr int kReduceBatch = 8;
+
 template <typename O>
 __device__ void fd_reduce(const float *__restrict__ pO, const float *__restrict__ pM, const float *__restrict__ pL,
                           typename O::storage *__restrict__ out, const FlashDecodingReduceConstants &p) {
-    __shared__ float w_sm[1024];
-    __shared__ float red[kWaves];
+    __shared__ float sm_m[kWaves], sm_l[kWaves];
+    __shared__ float sm_o[kWaves][64];
     const uint32_t P = p.P, Hd = p.Hd;
-    const uint64_t slot = blockIdx.x;  // (b * Nq + hq) * Sq + row
+    const uint64_t slot = blockIdx.x;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t d = blockIdx.y * 64 + lane;
+    const uint32_t dc = min(d, Hd - 1);  // lanes past Hd read a valid dim and store nothing
     const float *m = pM + slot * P;
     const float *l = pL + slot * P;
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float *o = pO + slot * P * Hd + dc;
 
-    float mx = -INFINITY;
-    for (uint32_t k = tid; k < P; k += blockDim.x) mx = fmaxf(mx, m[k]);
-    mx = pk::wave_max(mx);
-    if (lane == 0) red[wave] = mx;
-    __syncthreads();
-    float mstar = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    __syncthreads();
-    float ls = 0.0f;
-    for (uint32_t k = tid; k < P; k += blockDim.x) {
-        float w = mstar == -INFINITY ? 0.0f : pk::fast_exp(m[k] - mstar);
-        w_sm[k] = w;
-        ls += w * l[k];
+    float mr = -INFINITY, lr = 0.0f, acc = 0.0f;
+    for (uint32_t k0 = wave; k0 < P; k0 += kWaves * kReduceBatch) {
+        float mk[kReduceBatch], lk[kReduceBatch], ok[kReduceBatch];
+#pragma unroll
+        for (int i = 0; i < kReduceBatch; ++i) {
+            const uint32_t k = min(k0 + kWaves * i, P - 1);
+            mk[i] = m[k];
+            lk[i] = l[k];
+            ok[i] = o[(uint64_t)k * Hd];
+        }
+#pragma unroll
+        for (int i = 0; i < kReduceBatch; ++i) {
+            if (k0 + kWaves * i >= P || mk[i] == -INFINITY) continue;
+            const float mn = fmaxf(mr, mk[i]);
+            const float a = mr == -INFINITY ? 0.0f : pk::fast_exp(mr - mn);
+            const float b = pk::fast_exp(mk[i] - mn);
+            acc = acc * a + ok[i] * b;
+            lr = lr * a + lk[i] * b;
+            mr = mn;
+        }
     }
-    ls = pk::wave_sum(ls);
-    if (lane == 0) red[wave] = ls;
-    __syncthreads();
-    const float lstar = red[0] + red[1] + red[2] + red[3];
-    const float inv = lstar > 0.0f ? 1.0f / lstar : 0.0f;
-    const float *o = pO + slot * P * Hd;
-    for (uint32_t d = tid; d < Hd; d += blockDim.x) {
-        float acc = 0.0f;
-        for (uint32_t k = 0; k < P; ++k) acc += w_sm[k] * o[(uint64_t)k * Hd + d];
-        out[slot * Hd + d] = O::store(acc * inv);
+    if (lane == 0) {
+        sm_m[wave] = mr;
+        sm_l[wave] = lr;
     }
+    sm_o[wave][lane] = acc;
+    __syncthreads();
+    if (wave != 0) return;
+    float mstar = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) mstar = fmaxf(mstar, sm_m[w]);
+    float ls = 0.0f, os = 0.0f;
+    if (mstar != -INFINITY) {
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const float e = pk::fast_exp(sm_m[w] - mstar);  // 0 for an empty wave (m = -inf)
+            ls += e * sm_l[w];
+            os += e * sm_o[w][lane];
+        }
+    }
+    if (d < Hd) out[slot * Hd + d] = O::store(ls > 0.0f ? os / ls : 0.0f);
 }
 
 }  // namespace

@@ -1,92 +1,82 @@
-// Matrix-vector products for decode (m == 1 of Kernels.Matmul).
-//
+// Matrix-vector products of the decode step (the reference's Matmul with
+// m == 1):
 // matvec_nk_*: y[n] = sum_k x[k] * W[n, k] with W row-major [N, K] (the
 // transposeB layout of Sources/Popcorn/Kernels/Matvec.metal:55-126; host names
-// keep the reference's matvec_nk_simd_<x>_<w>_<out> pattern, with an _r1/_r2
-// suffix for fewer rows per wave).
+// keep the reference's matvec_nk_simd_<x>_<w>_<out> pattern, with an _r1
+// suffix for one row per unit instead of four, and its MatvecConstants).
+// decode_matvec_<t>_<o>_r<R>_f<F>: the same product with the decoder-layer
+// glue folded in (DecodeMatvecConstants): F bit 0 = residual + post-norm in
+// front, bit 1 = pre-norm, compiled in; the KV-cache scatter of the output
+// rows (flags bit 2) is a runtime choice.
 //
-// The kernel is HBM-bound: W is read once, x is reused. A block of 4 waves
-// stages x in LDS as f32, then each wave streams R rows of W with 16-byte
-// non-temporal loads (U chunks per row in flight per lane), accumulates one
-// f32 partial per row per lane, and reduces across the wave with DPP. Rows
-// whose length is not a multiple of the 16-byte vector use a scalar loop
-// (the reference's K % 4 != 0 tail, Matvec.metal:103-115).
+// The kernel is HBM-bound: W is read once, x is reused from LDS. A block of
+// 4 waves stages x (Stage), then every wave streams its units of R rows
+// (RowStream, 16 / R loads of 16 bytes per row and lane in flight). The host
+// sizes the grid so that each wave gets the same number of units, give or
+// take one. Rows whose length is not a multiple of the vector width, or an
+// unaligned W, take a scalar loop (the reference's K % 4 != 0 tail,
+// Matvec.metal:103-115).
 //
 // matvec*: y[n] = sum_k x[k] * W[k, n] (transposeW == 0, Matvec.metal:6-30),
 // one thread per output column; not on the decode path.
-#include "common.hpp"
+#include "stream.hpp"
 
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kUnroll = 4;
+using pk::kStreamWaves;
 
-template <typename X>
-__device__ inline void stage_x(const typename X::storage *__restrict__ x, float *xs, uint32_t K) {
-    for (uint32_t i = threadIdx.x; i < K; i += blockDim.x) xs[i] = X::load(x[i]);
-    __syncthreads();
-}
-
-template <typename X, typename W, typename O, int R>
-__device__ void matvec_nk(const typename X::storage *__restrict__ x, const typename W::storage *__restrict__ w,
-                          typename O::storage *__restrict__ out, const MatvecConstants &p, float *xs) {
+template <typename X, typename W, typename O, int R, bool RES, bool PRE, int J>
+__device__ void matvec_nk(const typename X::storage *__restrict__ x_in, const typename X::storage *__restrict__ delta,
+                          const float *__restrict__ w_post, const float *__restrict__ w_pre,
+                          const typename W::storage *__restrict__ w, typename O::storage *__restrict__ out,
+                          typename X::storage *__restrict__ x_out, typename O::storage *__restrict__ kcache,
+                          typename O::storage *__restrict__ vcache, const int32_t *__restrict__ position,
+                          const DecodeMatvecConstants &p, float *xs) {
+    constexpr int U = 16 / R;
     constexpr int kV = pk::Vec<W>::kVec;
+    __shared__ float red[kStreamWaves];
     const uint32_t K = p.K, N = p.N;
-    stage_x<X>(x, xs, K);
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t row0 = (blockIdx.x * kWaves + wave) * R;
-    if (row0 >= N) return;
-
-    float acc[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-
+    const uint32_t units = (N + R - 1) / R;
+    const uint32_t wave = pk::uniform(threadIdx.x >> 6);
+    const uint32_t first = blockIdx.x * kStreamWaves + wave, stride = gridDim.x * kStreamWaves;
     const bool vec = (K % kV) == 0 && (reinterpret_cast<uintptr_t>(w) % 16) == 0;
-    if (vec) {
-        const uint32_t nchunks = K / kV;
-        const typename W::storage *wr[R];
+    const bool scatter = (p.flags & pk::kKVScatter) != 0;
+    const int32_t pos = scatter ? position[0] : 0;
+    auto rows = [&](uint32_t unit, int s) { return w + (uint64_t)min(unit * R + s, N - 1) * K; };
+
+    using Stage = pk::Stage<X, RES, PRE, J>;
+    auto store = [&](uint32_t unit, const float *sums) {
+        if ((threadIdx.x & 63) != 0) return;
 #pragma unroll
-        for (int r = 0; r < R; ++r) wr[r] = w + (uint64_t)min(row0 + r, N - 1) * K;
-        for (uint32_t c0 = lane; c0 < nchunks; c0 += 64 * kUnroll) {
-            pk::Vec<W> wv[kUnroll][R];
-#pragma unroll
-            for (int u = 0; u < kUnroll; ++u) {
-                uint32_t c = c0 + 64 * u;
-                if (c < nchunks) {
-#pragma unroll
-                    for (int r = 0; r < R; ++r) wv[u][r].load_nt(wr[r] + (uint64_t)c * kV);
+        for (int r = 0; r < R; ++r) {
+            const uint32_t row = unit * R + r;
+            if (row >= N) break;
+            if (scatter && row >= p.qRows) {
+                // K rows then V rows, head-major: cache[(h * kvStride + pos) * headDim + d]
+                uint32_t j = row - p.qRows;
+                const bool isV = j >= p.kvRows;
+                if (isV) j -= p.kvRows;
+                if (pos >= 0 && (uint32_t)pos < p.kvStride) {
+                    const uint64_t at = ((uint64_t)(j / p.headDim) * p.kvStride + (uint32_t)pos) * p.headDim + j % p.headDim;
+                    (isV ? vcache : kcache)[at] = O::store(sums[r]);
                 }
-            }
-#pragma unroll
-            for (int u = 0; u < kUnroll; ++u) {
-                uint32_t c = c0 + 64 * u;
-                if (c < nchunks) {
-                    float xv[kV];
-#pragma unroll
-                    for (int e = 0; e < kV; ++e) xv[e] = xs[c * kV + e];
-#pragma unroll
-                    for (int r = 0; r < R; ++r) {
-#pragma unroll
-                        for (int e = 0; e < kV; ++e) acc[r] += xv[e] * wv[u][r].get(e);
-                    }
-                }
+            } else {
+                out[row] = O::store(sums[r]);
             }
         }
-    } else {
-        for (uint32_t k = lane; k < K; k += 64) {
-            float xv = xs[k];
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                uint32_t row = min(row0 + r, N - 1);
-                acc[r] += xv * W::load(w[(uint64_t)row * K + k]);
-            }
-        }
+    };
+    if (!(vec && K >= (uint32_t)kV && Stage::fast_ok(x_in, delta, w_post, w_pre, x_out, K, 1u))) {
+        Stage::finish_scalar(xs, red, x_in, delta, w_post, w_pre, x_out, K, 1u, p.eps, p.interDataType);
+        pk::stream_rows_scalar<W, R>(xs, K, units, first, stride, rows, store);
+        return;
     }
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        float s = pk::wave_sum(acc[r]);
-        if (lane == 0 && row0 + r < N) out[row0 + r] = O::store(s);
-    }
+    Stage stage;
+    stage.issue(x_in, delta, w_post, w_pre, K);
+    pk::RowStream<W, R, U> rs;
+    rs.init(rows, K, units, first, stride);
+    rs.start(rows);
+    stage.finish(xs, red, x_out, K, 1u, p.eps, p.interDataType);
+    rs.run(xs, rows, store);
 }
 
 template <typename X, typename W, typename O>
@@ -101,17 +91,38 @@ __device__ void matvec_kn(const typename X::storage *__restrict__ x, const typen
 
 }  // namespace
 
-// x is staged in dynamic LDS (K floats).
+// Reference-named matvec: plain product, x staged in dynamic LDS (K floats).
 #define MATVEC_NK(name, X, W, O, R)                                                                   \
     POPCORN_KERNEL void __launch_bounds__(256)                                                        \
         name(const X::storage *x, const W::storage *w, O::storage *out, MatvecConstants p) {          \
         extern __shared__ float xs[];                                                                 \
-        matvec_nk<X, W, O, R>(x, w, out, p, xs);                                                      \
+        DecodeMatvecConstants d{p.K, p.N, 0.0f, 0u, 8u, 0u, 0u, 1u, 1u};                              \
+        matvec_nk<X, W, O, R, false, false, 8>(x, nullptr, nullptr, nullptr, w, out, nullptr, nullptr, \
+                                               nullptr, nullptr, d, xs);                              \
     }
 #define MATVEC_NK_ALL(base, X, W, O) \
     MATVEC_NK(base, X, W, O, 4)      \
-    MATVEC_NK(base##_r2, X, W, O, 2) \
     MATVEC_NK(base##_r1, X, W, O, 1)
+
+// Decode matvec with the layer glue; the plain form stages up to 8 runs of
+// x per thread in registers, the glued forms 2 (K <= 4096 for 16-bit types).
+#define DECODE_MATVEC(name, T, O, R, RES, PRE, J)                                                           \
+    POPCORN_KERNEL void __launch_bounds__(256)                                                              \
+        name(const T::storage *x_in, const T::storage *delta, const float *w_post, const float *w_pre,      \
+             const T::storage *w, O::storage *out, T::storage *x_out, O::storage *kcache, O::storage *vcache, \
+             const int32_t *position, DecodeMatvecConstants p) {                                            \
+        extern __shared__ float xs[];                                                                       \
+        matvec_nk<T, T, O, R, RES, PRE, J>(x_in, delta, w_post, w_pre, w, out, x_out, kcache, vcache,      \
+                                           position, p, xs);                                                \
+    }
+#define DECODE_MATVEC_F(base, T, O, R)                         \
+    DECODE_MATVEC(base##_f0, T, O, R, false, false, 8)         \
+    DECODE_MATVEC(base##_f1, T, O, R, true, false, 2)          \
+    DECODE_MATVEC(base##_f2, T, O, R, false, true, 2)          \
+    DECODE_MATVEC(base##_f3, T, O, R, true, true, 2)
+#define DECODE_MATVEC_R(base, T, O)       \
+    DECODE_MATVEC_F(base##_r4, T, O, 4) \
+    DECODE_MATVEC_F(base##_r1, T, O, 1)
 
 #define MATVEC_KN(name, X, W, O)                                                                    \
     POPCORN_KERNEL void __launch_bounds__(256)                                                      \
@@ -130,6 +141,12 @@ MATVEC_NK_ALL(matvec_nk_simd_bf16_bf16_bf16, BF16, BF16, BF16)
 MATVEC_NK_ALL(matvec_nk_simd_f32_f16_f32, F32, F16, F32)
 MATVEC_NK_ALL(matvec_nk_simd_f16_f16_f32, F16, F16, F32)
 MATVEC_NK_ALL(matvec_nk_simd_f16_f16_f16, F16, F16, F16)
+
+DECODE_MATVEC_R(decode_matvec_bf16_bf16, BF16, BF16)
+DECODE_MATVEC_R(decode_matvec_bf16_f32, BF16, F32)
+DECODE_MATVEC_R(decode_matvec_f16_f16, F16, F16)
+DECODE_MATVEC_R(decode_matvec_f16_f32, F16, F32)
+DECODE_MATVEC_R(decode_matvec_f32_f32, F32, F32)
 
 MATVEC_KN(matvec, F32, F32, F32)
 MATVEC_KN(matvec_f16, F32, F16, F32)

@@ -1,0 +1,368 @@
+// Building blocks of the decode matvecs (matvec.hip, gated_mlp.hip): a block
+// stages the vector it multiplies in LDS as f32 (Stage), then each wave
+// streams the weight rows of its row groups against it (RowStream).
+//
+// Both are shaped by one property of the vector memory pipeline: a wave's
+// loads complete in issue order (vmcnt counts them in order), so waiting
+// for a load also waits for every load issued before it. Stage therefore
+// issues the vector's loads (L2-resident, short latency) before the first
+// weight loads, and computes the layer glue while those weight loads are in
+// flight; RowStream keeps U weight loads per row in flight and refills each
+// slot as soon as it is consumed, so a wave never drains its queue.
+#pragma once
+
+#include "common.hpp"
+
+namespace pk {
+
+constexpr int kStreamThreads = 256;
+constexpr int kStreamWaves = kStreamThreads / 64;
+constexpr uint32_t kKVScatter = 4u;  // DecodeMatvecConstants.flags bit 2 (runtime)
+
+__device__ inline uint32_t uniform(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// Sum over the block (every thread gets it); `red` holds one float per wave.
+__device__ inline float block_sum(float v, float *red) {
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    v = wave_sum(v);
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float t = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kStreamWaves; ++w) t += red[w];
+    __syncthreads();
+    return t;
+}
+
+// E floats -> one 16-byte vector of T storage (E = Vec<T>::kVec).
+template <typename T>
+__device__ inline u32x4 pack16(const float *v);
+
+template <>
+__device__ inline u32x4 pack16<F32>(const float *v) {
+    return u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
+}
+
+template <>
+__device__ inline u32x4 pack16<BF16>(const float *v) {
+    u32x4 r;
+    r.x = (uint32_t)BF16::store(v[0]) | ((uint32_t)BF16::store(v[1]) << 16);
+    r.y = (uint32_t)BF16::store(v[2]) | ((uint32_t)BF16::store(v[3]) << 16);
+    r.z = (uint32_t)BF16::store(v[4]) | ((uint32_t)BF16::store(v[5]) << 16);
+    r.w = (uint32_t)BF16::store(v[6]) | ((uint32_t)BF16::store(v[7]) << 16);
+    return r;
+}
+
+__device__ inline uint32_t f16bits(float x) { return (uint32_t)__builtin_bit_cast(uint16_t, F16::store(x)); }
+
+template <>
+__device__ inline u32x4 pack16<F16>(const float *v) {
+    return u32x4{f16bits(v[0]) | (f16bits(v[1]) << 16), f16bits(v[2]) | (f16bits(v[3]) << 16),
+                 f16bits(v[4]) | (f16bits(v[5]) << 16), f16bits(v[6]) | (f16bits(v[7]) << 16)};
+}
+
+// ---- Stage -------------------------------------------------------------------
+// Builds xs[0..K) (f32, LDS) with the decoder-layer glue chosen at compile
+// time, in the operation order of RMSNorm.metal:32-40 and Add.metal:
+//   RES: x = round(x_in + round((delta * s_d) * w_post)),
+//        s_d = 1 / sqrt(mean(delta^2) + eps); block 0 also stores x to x_out
+//        (the next residual stream);
+//   PRE: v = round((x * s_x) * w'), s_x = 1 / sqrt(mean(x^2) + eps), with
+//        w' = 1 (preMode 0), w_pre (1) or 1 + w_pre (2);
+// round() being the store to the intermediate dtype `inter`. Each thread
+// owns runs of E = 16 / sizeof(X) consecutive elements, run q = tid + 256 j.
+// issue() loads them into registers (J runs per thread); finish() computes,
+// writes LDS and ends with a barrier. Inputs that do not fit (fast_ok())
+// take finish_scalar(), element by element, instead.
+template <typename X, bool RES, bool PRE, int J>
+struct Stage {
+    static constexpr int E = Vec<X>::kVec;
+    static constexpr int EW = E / 4;  // f32 vectors per run of norm weights
+    using S = typename X::storage;
+    Vec<X> xv[J];
+    Vec<X> dv[RES ? J : 1];
+    Vec<F32> wpo[RES ? J : 1][EW];
+    Vec<F32> wpr[PRE ? J : 1][EW];
+
+    // The register path needs whole 16-byte runs, aligned pointers, at most
+    // J runs per thread and, with PRE, a norm weight (preMode != 0).
+    __device__ static bool fast_ok(const S *x_in, const S *delta, const float *w_post, const float *w_pre,
+                                   const S *x_out, uint32_t K, uint32_t preMode) {
+        uintptr_t al = reinterpret_cast<uintptr_t>(x_in);
+        if (RES) al |= reinterpret_cast<uintptr_t>(delta) | reinterpret_cast<uintptr_t>(w_post) |
+                       reinterpret_cast<uintptr_t>(x_out);
+        if (PRE) al |= reinterpret_cast<uintptr_t>(w_pre);
+        return (K % E) == 0 && K / E <= (uint32_t)(kStreamThreads * J) && (al % 16) == 0 && (!PRE || preMode != 0u);
+    }
+
+    // Every thread issues all J runs' loads; runs past K / E re-read the
+    // last run (same addresses as a valid thread) and are not used.
+    __device__ void issue(const S *x_in, const S *delta, const float *w_post, const float *w_pre, uint32_t K) {
+        const uint32_t runs = K / E, tid = threadIdx.x;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const uint64_t at = (uint64_t)min(tid + (uint32_t)(kStreamThreads * j), runs - 1) * E;
+            xv[j].load(x_in + at);
+            if constexpr (RES) {
+                dv[j].load(delta + at);
+#pragma unroll
+                for (int h = 0; h < EW; ++h) wpo[j][h].load(w_post + at + 4 * h);
+            }
+            if constexpr (PRE) {
+#pragma unroll
+                for (int h = 0; h < EW; ++h) wpr[j][h].load(w_pre + at + 4 * h);
+            }
+        }
+    }
+
+    __device__ void finish(float *xs, float *red, S *x_out, uint32_t K, uint32_t preMode, float eps, uint32_t inter) {
+        const uint32_t runs = K / E, tid = threadIdx.x;
+        float ss = 0.0f;
+        if constexpr (RES) {
+            float sd = 0.0f;
+#pragma unroll
+            for (int j = 0; j < J; ++j) {
+                if (tid + (uint32_t)(kStreamThreads * j) < runs) {
+#pragma unroll
+                    for (int e = 0; e < E; ++e) sd += dv[j].get(e) * dv[j].get(e);
+                }
+            }
+            const float s = 1.0f / sqrtf(block_sum(sd, red) / (float)K + eps);
+#pragma unroll
+            for (int j = 0; j < J; ++j) {
+                const uint32_t q = tid + (uint32_t)(kStreamThreads * j);
+                if (q < runs) {
+                    float r[E];
+#pragma unroll
+                    for (int e = 0; e < E; ++e) {
+                        const float t = round_through(inter, (dv[j].get(e) * s) * wpo[j][e / 4].get(e % 4));
+                        r[e] = round_through(inter, xv[j].get(e) + t);
+                        ss += r[e] * r[e];
+                    }
+                    store_lds(xs + (uint64_t)q * E, r);
+                    if (blockIdx.x == 0) *reinterpret_cast<u32x4 *>(x_out + (uint64_t)q * E) = pack16<X>(r);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < J; ++j) {
+                const uint32_t q = tid + (uint32_t)(kStreamThreads * j);
+                if (q < runs) {
+                    float r[E];
+#pragma unroll
+                    for (int e = 0; e < E; ++e) {
+                        r[e] = xv[j].get(e);
+                        ss += r[e] * r[e];
+                    }
+                    store_lds(xs + (uint64_t)q * E, r);
+                }
+            }
+        }
+        if constexpr (PRE) {
+            const float s = 1.0f / sqrtf(block_sum(ss, red) / (float)K + eps);
+#pragma unroll
+            for (int j = 0; j < J; ++j) {
+                const uint32_t q = tid + (uint32_t)(kStreamThreads * j);
+                if (q < runs) {
+                    float r[E];
+                    load_lds(xs + (uint64_t)q * E, r);  // this thread's own writes
+#pragma unroll
+                    for (int e = 0; e < E; ++e) {
+                        float v = r[e] * s;
+                        const float w = wpr[j][e / 4].get(e % 4);
+                        v *= preMode == 2u ? 1.0f + w : w;
+                        r[e] = round_through(inter, v);
+                    }
+                    store_lds(xs + (uint64_t)q * E, r);
+                }
+            }
+        }
+        __syncthreads();
+    }
+
+    __device__ static void store_lds(float *p, const float *r) {
+#pragma unroll
+        for (int h = 0; h < EW; ++h) *reinterpret_cast<float4 *>(p + 4 * h) = float4{r[4 * h], r[4 * h + 1], r[4 * h + 2], r[4 * h + 3]};
+    }
+    __device__ static void load_lds(const float *p, float *r) {
+#pragma unroll
+        for (int h = 0; h < EW; ++h) {
+            const float4 v = *reinterpret_cast<const float4 *>(p + 4 * h);
+            r[4 * h] = v.x;
+            r[4 * h + 1] = v.y;
+            r[4 * h + 2] = v.z;
+            r[4 * h + 3] = v.w;
+        }
+    }
+
+    // Element-wise form of the same computation, any K and alignment.
+    __device__ static void finish_scalar(float *xs, float *red, const S *x_in, const S *delta, const float *w_post,
+                                         const float *w_pre, S *x_out, uint32_t K, uint32_t preMode, float eps,
+                                         uint32_t inter) {
+        const uint32_t tid = threadIdx.x;
+        if constexpr (RES) {
+            float sd = 0.0f;
+            for (uint32_t i = tid; i < K; i += kStreamThreads) {
+                const float d = X::load(delta[i]);
+                xs[i] = d;
+                sd += d * d;
+            }
+            const float s = 1.0f / sqrtf(block_sum(sd, red) / (float)K + eps);
+            for (uint32_t i = tid; i < K; i += kStreamThreads) {
+                const float t = round_through(inter, (xs[i] * s) * w_post[i]);
+                const float r = round_through(inter, X::load(x_in[i]) + t);
+                xs[i] = r;
+                if (blockIdx.x == 0) x_out[i] = X::store(r);
+            }
+        } else {
+            for (uint32_t i = tid; i < K; i += kStreamThreads) xs[i] = X::load(x_in[i]);
+        }
+        if constexpr (PRE) {
+            float ss = 0.0f;
+            for (uint32_t i = tid; i < K; i += kStreamThreads) ss += xs[i] * xs[i];
+            const float s = 1.0f / sqrtf(block_sum(ss, red) / (float)K + eps);
+            for (uint32_t i = tid; i < K; i += kStreamThreads) {
+                float v = xs[i] * s;
+                if (preMode) v *= preMode == 2u ? 1.0f + w_pre[i] : w_pre[i];
+                xs[i] = round_through(inter, v);
+            }
+        }
+        __syncthreads();
+    }
+};
+
+// ---- RowStream -----------------------------------------------------------------
+template <typename W, int S, int U>
+struct RowStream {
+    static constexpr int kV = Vec<W>::kVec;
+    using Ptr = const typename W::storage *;
+    Vec<W> buf[U][S];
+    Ptr iptr[S];
+    uint32_t nchunks, cpl, steps, first, stride;
+    uint32_t is, ii, iu;  // issue cursor: steps issued, step within unit, unit
+
+    template <class Rows>
+    __device__ void init(const Rows &rows, uint32_t K, uint32_t units, uint32_t first_, uint32_t stride_) {
+        nchunks = K / kV;
+        cpl = (nchunks + 63) / 64;
+        first = first_;
+        stride = stride_;
+        const uint32_t nu = first < units ? (units - first + stride - 1) / stride : 0u;
+        steps = nu * cpl;
+        is = 0;
+        ii = 0;
+        iu = first;
+#pragma unroll
+        for (int s = 0; s < S; ++s) iptr[s] = rows(iu, s);
+    }
+
+    // Loads step `is` into `slot`. Once every step is issued it loads the
+    // last step again (lines just fetched), so that every path through the
+    // kernel has the same number of loads in flight and the compiler's wait
+    // counts stay exact.
+    template <class Rows>
+    __device__ inline void issue(int slot, const Rows &rows) {
+        const uint32_t c = min((threadIdx.x & 63) + 64 * ii, nchunks - 1);
+#pragma unroll
+        for (int s = 0; s < S; ++s) buf[slot][s].load_nt(iptr[s] + (uint64_t)c * kV);
+        if (is + 1 < steps) {
+            ++is;
+            if (++ii == cpl) {
+                ii = 0;
+                iu += stride;
+#pragma unroll
+                for (int s = 0; s < S; ++s) iptr[s] = rows(iu, s);
+            }
+        } else {
+            is = steps;
+        }
+    }
+
+    template <class Rows>
+    __device__ void start(const Rows &rows) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) issue(u, rows);
+    }
+
+    template <class Store>
+    __device__ inline void consume(int slot, const float *xs, float (&acc)[S], uint32_t &ci, uint32_t &cu,
+                                   Store &store) {
+        const uint32_t c = (threadIdx.x & 63) + 64 * ci;
+        if (c < nchunks) {
+            float xv[kV];
+#pragma unroll
+            for (int h = 0; h < kV / 4; ++h) {
+                const float4 v = *reinterpret_cast<const float4 *>(xs + (uint64_t)c * kV + 4 * h);
+                xv[4 * h] = v.x;
+                xv[4 * h + 1] = v.y;
+                xv[4 * h + 2] = v.z;
+                xv[4 * h + 3] = v.w;
+            }
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+#pragma unroll
+                for (int e = 0; e < kV; ++e) acc[s] += xv[e] * buf[slot][s].get(e);
+            }
+        }
+        if (++ci == cpl) {
+            float sums[S];
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                sums[s] = wave_sum(acc[s]);
+                acc[s] = 0.0f;
+            }
+            store(cu, sums);
+            ci = 0;
+            cu += stride;
+        }
+    }
+
+    template <class Rows, class Store>
+    __device__ void run(const float *xs, const Rows &rows, Store &store) {
+        float acc[S];
+#pragma unroll
+        for (int s = 0; s < S; ++s) acc[s] = 0.0f;
+        uint32_t cs = 0, ci = 0, cu = first;
+        // steady state: every refill is a real step
+        while (cs + 2 * U <= steps) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                consume(u, xs, acc, ci, cu, store);
+                issue(u, rows);
+            }
+            cs += U;
+        }
+        while (cs < steps) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                if (cs + u < steps) consume(u, xs, acc, ci, cu, store);
+                issue(u, rows);
+            }
+            cs += U;
+        }
+    }
+};
+
+// The same product with scalar loads, for rows whose length is not a
+// multiple of the vector width or whose base is not 16-byte aligned.
+template <typename W, int S, class Rows, class Store>
+__device__ void stream_rows_scalar(const float *xs, uint32_t K, uint32_t units, uint32_t first, uint32_t stride,
+                                   const Rows &rows, Store &store) {
+    const uint32_t lane = threadIdx.x & 63;
+    for (uint32_t unit = first; unit < units; unit += stride) {
+        float acc[S];
+#pragma unroll
+        for (int s = 0; s < S; ++s) acc[s] = 0.0f;
+        for (uint32_t k = lane; k < K; k += 64) {
+            const float x = xs[k];
+#pragma unroll
+            for (int s = 0; s < S; ++s) acc[s] += x * W::load(rows(unit, s)[k]);
+        }
+        float sums[S];
+#pragma unroll
+        for (int s = 0; s < S; ++s) sums[s] = wave_sum(acc[s]);
+        store(unit, sums);
+    }
+}
+
+}  // namespace pk

@@ -537,6 +537,54 @@ popcorn_status_t popcorn_kernel_gated_mlp(const popcorn_tensor_t *x, const popco
     });
 }
 
+popcorn_status_t popcorn_kernel_gated_mlp_residual(const popcorn_tensor_t *x_in, const popcorn_tensor_t *delta,
+                                                   const popcorn_tensor_t *w_post, const popcorn_tensor_t *x_out,
+                                                   const popcorn_tensor_t *norm_weight, const popcorn_tensor_t *w_gate,
+                                                   const popcorn_tensor_t *w_up, const popcorn_tensor_t *w_down,
+                                                   const popcorn_tensor_t *out, float eps, int32_t add_one_to_weight,
+                                                   const popcorn_tensor_t *hidden, popcorn_kernel_t *kernel) {
+    return guarded([&] {
+        Tensor nw, h;
+        if (norm_weight) nw = Tensor::fromC(*norm_weight);
+        if (hidden) h = Tensor::fromC(*hidden);
+        emit(kernel, Kernels::GatedMLPResidual(T(x_in, "x_in"), T(delta, "delta"), T(w_post, "w_post"), T(x_out, "x_out"),
+                                               norm_weight ? &nw : nullptr, T(w_gate, "w_gate"), T(w_up, "w_up"),
+                                               T(w_down, "w_down"), T(out, "out"), eps, add_one_to_weight != 0,
+                                               hidden ? &h : nullptr));
+    });
+}
+
+popcorn_status_t popcorn_kernel_decode_matvec(const popcorn_decode_matvec_args_t *args, popcorn_kernel_t *kernel) {
+    return guarded([&] {
+        need(args, "args");
+        Tensor t[10];
+        const popcorn_tensor_t *src[10] = {args->x, args->delta, args->w_post, args->x_out, args->w_pre,
+                                           args->weight, args->out, args->k_cache, args->v_cache, args->position};
+        const Tensor *p[10];
+        for (int i = 0; i < 10; ++i) {
+            p[i] = nullptr;
+            if (src[i]) {
+                t[i] = Tensor::fromC(*src[i]);
+                p[i] = &t[i];
+            }
+        }
+        Kernels::DecodeMatvecArgs a;
+        a.x = p[0];
+        a.delta = p[1];
+        a.wPost = p[2];
+        a.xOut = p[3];
+        a.wPre = p[4];
+        a.weight = p[5];
+        a.out = p[6];
+        a.kCache = p[7];
+        a.vCache = p[8];
+        a.position = p[9];
+        a.qRows = args->q_rows;
+        a.eps = args->eps;
+        emit(kernel, Kernels::DecodeMatvec(a));
+    });
+}
+
 popcorn_status_t popcorn_kernel_embedding_gather(const popcorn_tensor_t *ids, const popcorn_tensor_t *table,
                                                  const popcorn_tensor_t *out, popcorn_kernel_t *kernel) {
     return guarded([&] { emit(kernel, Kernels::EmbeddingGather(T(ids, "ids"), T(table, "table"), T(out, "out"))); });

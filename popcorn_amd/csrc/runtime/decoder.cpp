@@ -52,7 +52,7 @@ struct popcorn_decoder_s {
     // weights (bf16 unless noted) and state
     Buffer embedding, finalNorm /*f32*/, wqkv, wo, wg, wu, wd, norms /*f32 [L][4][H]*/;
     Buffer kcache, vcache;
-    Buffer x, e, n, qkv, attn, o, t, mlp, hidden, logits /*f32*/, token /*i32*/, position /*i32*/, history /*i32*/;
+    Buffer x, x2, e, qkv, attn, o, mlp, hidden, logits /*f32*/, token /*i32*/, position /*i32*/, history /*i32*/;
 
     std::vector<std::unique_ptr<Kernel>> step;
     std::vector<std::string> names;
@@ -83,15 +83,19 @@ struct popcorn_decoder_s {
         throw Error::invalidArgument(std::string("unknown decoder tensor ") + which);
     }
 
+    // Five dispatches per layer: the QKV matvec (previous layer's post-FFN
+    // norm + residual, this layer's input norm, K/V scattered into the caches),
+    // split-KV attention with its combine, the O projection, the gate/up
+    // matvec (post-attention norm + residual, pre-FFN norm), the down matvec.
+    // The residual stream alternates between x and x2 (blocks of one kernel
+    // read one while block 0 writes the other).
     void build() {
         const float eps = cfg.eps;
-        Tensor tx = bf(x.p, {1, H}), te = bf(e.p, {1, H}), tn = bf(n.p, {1, H});
-        Tensor tqkv = bf(qkv.p, {1, QKV});
-        Tensor tq = bf(qkv.p, {1, Nq, 1, Hd});
-        Tensor tk = bf(qkv.at(QW * 2), {1, Nkv, 1, Hd});
-        Tensor tv = bf(qkv.at((QW + KW) * 2), {1, Nkv, 1, Hd});
+        Tensor tx = bf(x.p, {1, H}), tx2 = bf(x2.p, {1, H}), te = bf(e.p, {1, H});
+        Tensor tq = bf(qkv.p, {1, QW});
+        Tensor tq4 = bf(qkv.p, {1, Nq, 1, Hd});
         Tensor tattn4 = bf(attn.p, {1, Nq, 1, Hd}), tattn = bf(attn.p, {1, QW});
-        Tensor to = bf(o.p, {1, H}), tt = bf(t.p, {1, H}), tmlp = bf(mlp.p, {1, H}), th = bf(hidden.p, {F});
+        Tensor to = bf(o.p, {1, H}), tmlp = bf(mlp.p, {1, H}), th = bf(hidden.p, {F});
         Tensor tpos(position.p, Shape({1}), DataType::i32);
         Tensor ttok(token.p, Shape({1}), DataType::i32);
         Tensor temb = bf(embedding.p, {V, H});
@@ -103,25 +107,52 @@ struct popcorn_decoder_s {
         add(Kernels::EmbeddingGather(ttok, temb, te));
         add(Kernels::ScalarMul(te, std::sqrt((float)H), tx));
         const AttentionMask causal{0, -1};
+        Tensor prevPostFfn;
         for (int64_t l = 0; l < L; ++l) {
             Tensor nin = weight("norm_in", l), npa = weight("norm_post_attn", l);
             Tensor npf = weight("norm_pre_ffn", l), npo = weight("norm_post_ffn", l);
             Tensor kc = weight("k_cache", l), vc = weight("v_cache", l);
-            add(Kernels::RMSNorm(tx, &nin, tn, 1, H, eps, false));
-            add(Kernels::Matmul(tn, weight("w_qkv", l), tqkv, true));
-            add(Kernels::KVCacheWrite(tk, kc, 1, Nkv, 1, S, Hd, 0, &tpos));
-            add(Kernels::KVCacheWrite(tv, vc, 1, Nkv, 1, S, Hd, 0, &tpos));
-            add(Kernels::FlashAttention(tq, kc, vc, tattn4, 1, Nq, Nkv, 1, 1, Hd, cfg.attn_scale, causal, S, &tpos));
-            add(Kernels::Matmul(tattn, weight("w_o", l), to, true));
-            add(Kernels::RMSNorm(to, &npa, tt, 1, H, eps, false));
-            add(Kernels::Add(tx, tt, tx));
-            add(Kernels::GatedMLP(tx, &npf, weight("w_gate", l), weight("w_up", l), weight("w_down", l), tmlp, eps, false, &th));
-            add(Kernels::RMSNorm(tmlp, &npo, tt, 1, H, eps, false));
-            add(Kernels::Add(tx, tt, tx));
+            Tensor wqkv_l = weight("w_qkv", l), wo_l = weight("w_o", l);
+            Kernels::DecodeMatvecArgs qkvArgs;
+            if (l == 0) {
+                qkvArgs.x = &tx;
+            } else {
+                qkvArgs.x = &tx2;
+                qkvArgs.delta = &tmlp;
+                qkvArgs.wPost = &prevPostFfn;
+                qkvArgs.xOut = &tx;
+            }
+            qkvArgs.wPre = &nin;
+            qkvArgs.weight = &wqkv_l;
+            qkvArgs.out = &tq;
+            qkvArgs.kCache = &kc;
+            qkvArgs.vCache = &vc;
+            qkvArgs.position = &tpos;
+            qkvArgs.qRows = QW;
+            qkvArgs.eps = eps;
+            add(Kernels::DecodeMatvec(qkvArgs));
+            add(Kernels::FlashAttention(tq4, kc, vc, tattn4, 1, Nq, Nkv, 1, 1, Hd, cfg.attn_scale, causal, S, &tpos));
+            Kernels::DecodeMatvecArgs oArgs;
+            oArgs.x = &tattn;
+            oArgs.weight = &wo_l;
+            oArgs.out = &to;
+            add(Kernels::DecodeMatvec(oArgs));
+            add(Kernels::GatedMLPResidual(tx, to, npa, tx2, &npf, weight("w_gate", l), weight("w_up", l),
+                                          weight("w_down", l), tmlp, eps, false, &th));
+            prevPostFfn = npo;
         }
-        // Gemma4TextInference.swift:201-206 (the final norm, LM head, argmax)
-        add(Kernels::RMSNorm(tx, &tfin, tn, 1, H, eps, false));
-        add(Kernels::Matmul(tn, temb, tlog, true));
+        // Gemma4TextInference.swift:201-206: the last post-FFN norm + residual,
+        // the final norm and the tied LM head in one matvec, then argmax
+        Kernels::DecodeMatvecArgs head;
+        head.x = &tx2;
+        head.delta = &tmlp;
+        head.wPost = &prevPostFfn;
+        head.xOut = &tx;
+        head.wPre = &tfin;
+        head.weight = &temb;
+        head.out = &tlog;
+        head.eps = eps;
+        add(Kernels::DecodeMatvec(head));
         add(Kernels::Argmax(tlog, ttok));
         PositionAdvanceConstants pc{1, (uint32_t)std::max(cfg.history_len, 0)};
         Tensor thist(history.p, Shape({std::max<int64_t>(cfg.history_len, 1)}), DataType::i32);
@@ -240,12 +271,11 @@ popcorn_status_t popcorn_decoder_create(popcorn_library_t library, popcorn_strea
         d->kcache = Buffer((size_t)(L * d->Nkv * d->S * d->Hd * 2));
         d->vcache = Buffer((size_t)(L * d->Nkv * d->S * d->Hd * 2));
         d->x = Buffer((size_t)(H * 2));
+        d->x2 = Buffer((size_t)(H * 2));
         d->e = Buffer((size_t)(H * 2));
-        d->n = Buffer((size_t)(H * 2));
-        d->qkv = Buffer((size_t)(d->QKV * 2));
+        d->qkv = Buffer((size_t)(d->QW * 2));
         d->attn = Buffer((size_t)(d->QW * 2));
         d->o = Buffer((size_t)(H * 2));
-        d->t = Buffer((size_t)(H * 2));
         d->mlp = Buffer((size_t)(H * 2));
         d->hidden = Buffer((size_t)(F * 2));
         d->logits = Buffer((size_t)(d->V * 4));
@@ -298,12 +328,11 @@ popcorn_status_t popcorn_decoder_tensor(popcorn_decoder_t d, const char *name, i
         if (n == "embedding") t = d->bf(d->embedding.p, {d->V, d->H});
         else if (n == "final_norm") t = Tensor(d->finalNorm.p, Shape({d->H}), DataType::f32);
         else if (n == "x") t = d->bf(d->x.p, {d->H});
-        else if (n == "qkv") t = d->bf(d->qkv.p, {d->QKV});
+        else if (n == "q") t = d->bf(d->qkv.p, {d->QW});
         else if (n == "attn") t = d->bf(d->attn.p, {d->QW});
         else if (n == "o") t = d->bf(d->o.p, {d->H});
         else if (n == "mlp") t = d->bf(d->mlp.p, {d->H});
         else if (n == "hidden") t = d->bf(d->hidden.p, {d->F});
-        else if (n == "normed") t = d->bf(d->n.p, {d->H});
         else if (n == "logits") t = Tensor(d->logits.p, Shape({d->V}), DataType::f32);
         else if (n == "token") t = Tensor(d->token.p, Shape({1}), DataType::i32);
         else if (n == "position") t = Tensor(d->position.p, Shape({1}), DataType::i32);

@@ -2,6 +2,7 @@
 // Swift descriptors (Sources/Popcorn/Kernels/*.swift, cited per descriptor),
 // with dispatch geometry chosen for wave64 and the device's CU count.
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 
 #include "popcorn.hpp"
@@ -154,8 +155,12 @@ public:
                     rc.Hd = (uint32_t)d_.Hd;
                     rc.P = (uint32_t)P_;
                     rc.Sq = (uint32_t)d_.Sq;
+                    // one block per (query row, 64-dim slice of the head)
+                    DispatchSize rs;
+                    rs.grid = dim3((unsigned)(d_.B * d_.Nq * d_.Sq), (unsigned)cdiv(d_.Hd, 64), 1);
+                    rs.block = dim3(kBlock, 1, 1);
                     FixedDispatch reduce(reduceName_, {{pO, kRead}, {pM, kRead}, {pL, kRead}, {out_, kWrite}},
-                                         {bytesOf(rc)}, grid1(d_.B * d_.Nq * d_.Sq, kBlock));
+                                         {bytesOf(rc)}, rs);
                     enc.dispatch(reduce);
                 });
             });
@@ -240,14 +245,30 @@ std::string plainName(const char *base, DataType x, DataType w, DataType o) {
     return "";
 }
 
-// Rows per wave for the NK matvec: the largest R in {4, 2, 1} that still
-// launches at least two blocks (of 4 waves) per CU.
-int matvecRows(int64_t N) {
-    const int64_t target = 2 * deviceCUs();
-    for (int R : {4, 2}) {
-        if (cdiv(N, 4 * R) >= target) return R;
-    }
-    return 1;
+// Rows per unit of the streaming matvecs (stream.hpp): 4 for long outputs
+// (one LDS read of x feeds 4 rows), 1 otherwise (finer units balance better).
+int matvecRows(int64_t N) { return N >= 32768 ? 4 : 1; }
+
+// Waves per CU the streaming kernels are sized for: 8 (two per SIMD) by
+// default; POPCORN_STREAM_WAVES_PER_CU overrides it (1..32) for tuning.
+int streamWavesPerCU() {
+    static const int w = [] {
+        const char *e = std::getenv("POPCORN_STREAM_WAVES_PER_CU");
+        const int v = e ? std::atoi(e) : 0;
+        return v >= 1 && v <= 32 ? v : 8;
+    }();
+    return w;
+}
+
+// Blocks (of 4 waves) for `units` units: each wave's share is
+// ceil(units / maxWaves), and just enough waves are launched to cover the
+// units at that share, so every wave streams the same number of units give
+// or take one.
+int64_t streamBlocks(int64_t units) {
+    if (units <= 0) return 0;
+    const int64_t maxWaves = (int64_t)deviceCUs() * streamWavesPerCU();
+    const int64_t per = cdiv(units, maxWaves);
+    return cdiv(cdiv(units, per), kBlock / 64);
 }
 
 constexpr int64_t kMaxStagedK = 16384;  // x staged as f32 in 64 KB of LDS
@@ -271,7 +292,7 @@ std::unique_ptr<Kernel> makeMatmul(const Tensor &a, const Tensor &b, const Tenso
             const int R = matvecRows(n);
             if (R != 4) fn += "_r" + std::to_string(R);
             return std::make_unique<FixedDispatch>(fn, binds, std::vector<std::vector<uint8_t>>{bytesOf(mc)},
-                                                   grid1(cdiv(n, 4 * R), kBlock, (size_t)std::max<int64_t>(k, 1) * 4));
+                                                   grid1(streamBlocks(cdiv(n, R)), kBlock, (size_t)std::max<int64_t>(k, 1) * 4));
         }
         std::string fn = plainName("matvec", a.dataType, b.dataType, c.dataType);
         if (fn.empty())
@@ -331,27 +352,55 @@ public:
         requireElements(wg, F_ * H_, "w_gate");
         requireElements(wu, F_ * H_, "w_up");
         requireElements(wd, H_ * F_, "w_down");
-        R_ = cdiv(F_, 8) >= 2 * deviceCUs() ? 2 : 1;
-        gateUpName_ = std::string("gated_mlp_gate_up_") + tag(t) + (R_ == 1 ? "_r1" : "");
+        R_ = F_ >= 32768 ? 2 : 1;
         down_ = makeMatmul(wd_, wd_, out_, 1, F_, H_, true);  // name/geometry probe only
+    }
+
+    // Residual form: x_ is the incoming residual stream; x = x_ +
+    // RMSNorm(delta) * wPost is stored to xOut and feeds the MLP.
+    void setResidual(const Tensor &delta, const Tensor &wPost, const Tensor &xOut) {
+        if (delta.dataType != x_.dataType || xOut.dataType != x_.dataType)
+            throw Error::unsupportedDataTypeCombination("GatedMLP residual tensors must have x's dtype.");
+        if (wPost.dataType != DataType::f32) throw Error::unsupportedDataTypeCombination("post-norm weight must be f32.");
+        requireElements(delta, H_, "GatedMLP delta");
+        requireElements(wPost, H_, "GatedMLP post-norm weight");
+        requireElements(xOut, H_, "GatedMLP x_out");
+        if (xOut.data == x_.data) throw Error::invalidArgument("GatedMLP x_out must not alias x (blocks read x while block 0 writes x_out)");
+        delta_ = delta;
+        wPost_ = wPost;
+        xOut_ = xOut;
+        residual_ = true;
     }
 
     std::vector<Binding> tensors() const override {
         std::vector<Binding> b = {{x_, kRead}, {wg_, kRead}, {wu_, kRead}, {wd_, kRead}, {out_, kWrite}};
         if (hasNorm_) b.push_back({nw_, kRead});
         if (hasHidden_) b.push_back({h_, kWrite});
+        if (residual_) {
+            b.push_back({delta_, kRead});
+            b.push_back({wPost_, kRead});
+            b.push_back({xOut_, kWrite});
+        }
         return b;
     }
 
-    std::string describe() const override { return gateUpName_ + "," + down_->describe(); }
+    std::string describe() const override { return gateUpName() + "," + down_->describe(); }
+
+    std::string gateUpName() const {
+        return std::string("gated_mlp_gate_up_") + tag(x_.dataType) + (R_ == 1 ? "_r1" : "") + (residual_ ? "_res" : "");
+    }
 
     void encode(KernelCommandEncoder &enc) const override {
         auto run = [&](const Tensor &h) {
             GatedMLPConstants gc{(uint32_t)H_, (uint32_t)F_, hasNorm_ ? 1u : 0u, addOne_ ? 1u : 0u, eps_,
-                                 (uint32_t)x_.dataType};
+                                 (uint32_t)x_.dataType, residual_ ? 1u : 0u};
             const Tensor normOrDummy = hasNorm_ ? nw_ : x_;
-            FixedDispatch gu(gateUpName_, {{x_, kRead}, {normOrDummy, kRead}, {wg_, kRead}, {wu_, kRead}, {h, kWrite}},
-                             {bytesOf(gc)}, grid1(cdiv(F_, 4 * R_), kBlock, (size_t)H_ * 4));
+            // delta, w_post and x_out are touched only in the residual form
+            const Tensor d = residual_ ? delta_ : x_, w = residual_ ? wPost_ : x_, xo = residual_ ? xOut_ : x_;
+            FixedDispatch gu(gateUpName(),
+                             {{x_, kRead}, {normOrDummy, kRead}, {wg_, kRead}, {wu_, kRead}, {h, kWrite}, {d, kRead},
+                              {w, kRead}, {xo, residual_ ? kWrite : kRead}},
+                             {bytesOf(gc)}, grid1(streamBlocks(cdiv(F_, R_)), kBlock, (size_t)H_ * 4));
             enc.dispatch(gu);
             auto down = makeMatmul(h, wd_, out_, 1, F_, H_, true);
             down->encode(enc);
@@ -364,11 +413,10 @@ public:
     }
 
 private:
-    Tensor x_, nw_, wg_, wu_, wd_, out_, h_;
+    Tensor x_, nw_, wg_, wu_, wd_, out_, h_, delta_, wPost_, xOut_;
     float eps_;
-    bool addOne_, hasNorm_ = false, hasHidden_ = false;
+    bool addOne_, hasNorm_ = false, hasHidden_ = false, residual_ = false;
     int64_t H_ = 0, F_ = 0, R_ = 2;
-    std::string gateUpName_;
     std::unique_ptr<Kernel> down_;
 };
 
@@ -607,6 +655,87 @@ std::unique_ptr<Kernel> ScalarMul(const Tensor &x, float scalar, const Tensor &o
 std::unique_ptr<Kernel> GatedMLP(const Tensor &x, const Tensor *normWeight, const Tensor &wGate, const Tensor &wUp,
                                  const Tensor &wDown, const Tensor &out, float eps, bool addOneToWeight, const Tensor *hidden) {
     return std::make_unique<GatedMLPKernel>(x, normWeight, wGate, wUp, wDown, out, eps, addOneToWeight, hidden);
+}
+
+std::unique_ptr<Kernel> GatedMLPResidual(const Tensor &xIn, const Tensor &delta, const Tensor &wPost, const Tensor &xOut,
+                                         const Tensor *normWeight, const Tensor &wGate, const Tensor &wUp,
+                                         const Tensor &wDown, const Tensor &out, float eps, bool addOneToWeight,
+                                         const Tensor *hidden) {
+    auto k = std::make_unique<GatedMLPKernel>(xIn, normWeight, wGate, wUp, wDown, out, eps, addOneToWeight, hidden);
+    k->setResidual(delta, wPost, xOut);
+    return k;
+}
+
+std::unique_ptr<Kernel> DecodeMatvec(const DecodeMatvecArgs &a) {
+    if (!a.x || !a.weight || !a.out) throw Error::invalidArgument("DecodeMatvec needs x, weight and out");
+    const Tensor &W = *a.weight;
+    if (W.shape.rank() != 2) throw Error::tensorInvalidRank(2, W.shape.rank());
+    const int64_t N = W.shape[0], K = W.shape[1];
+    const DataType t = W.dataType, o = a.out->dataType;
+    if (!isFloat(t) || a.x->dataType != t)
+        throw Error::unsupportedDataTypeCombination("DecodeMatvec needs x and weight of one float dtype.");
+    if (!(o == t || o == DataType::f32)) throw Error::unsupportedDataTypeCombination("DecodeMatvec output is the weight dtype or f32.");
+    if (K <= 0 || N <= 0 || K > kMaxStagedK) throw Error::tensorShapeMismatch("DecodeMatvec needs 0 < K <= 16384 and N > 0.");
+    requireElements(*a.x, K, "DecodeMatvec x");
+    requireElements(W, N * K, "DecodeMatvec weight");
+    uint32_t flags = 0;
+    if (a.delta) {
+        if (!a.wPost || !a.xOut) throw Error::invalidArgument("DecodeMatvec with delta needs wPost and xOut");
+        if (a.delta->dataType != t || a.xOut->dataType != t || a.wPost->dataType != DataType::f32)
+            throw Error::unsupportedDataTypeCombination("DecodeMatvec residual: delta and xOut of x's dtype, wPost f32.");
+        requireElements(*a.delta, K, "DecodeMatvec delta");
+        requireElements(*a.wPost, K, "DecodeMatvec wPost");
+        requireElements(*a.xOut, K, "DecodeMatvec xOut");
+        if (a.xOut->data == a.x->data) throw Error::invalidArgument("DecodeMatvec xOut must not alias x");
+        flags |= 1u;
+    }
+    if (a.wPre) {
+        if (a.wPre->dataType != DataType::f32) throw Error::unsupportedDataTypeCombination("DecodeMatvec wPre must be f32.");
+        requireElements(*a.wPre, K, "DecodeMatvec wPre");
+        flags |= 2u;
+    }
+    DecodeMatvecConstants dc{(uint32_t)K, (uint32_t)N, a.eps, 0u, (uint32_t)t, (uint32_t)N, 0u, 1u, 1u};
+    if (a.kCache || a.vCache) {
+        if (!a.kCache || !a.vCache || !a.position) throw Error::invalidArgument("KV scatter needs both caches and a position");
+        const Tensor &kc = *a.kCache;
+        if (kc.shape != a.vCache->shape) throw Error::tensorShapeMismatch("K and V caches must have one shape.");
+        const int r = kc.shape.rank();
+        if (r < 3 || (r == 4 && kc.shape[0] != 1) || r > 4) throw Error::tensorShapeMismatch("caches must be [1?, Nkv, Smax, Hd].");
+        const int64_t Nkv = kc.shape[r - 3], Smax = kc.shape[r - 2], Hd = kc.shape[r - 1];
+        if (kc.dataType != o || a.vCache->dataType != o || o != t)
+            throw Error::unsupportedDataTypeCombination("KV scatter writes caches of the weight dtype.");
+        if (a.position->dataType != DataType::i32) throw Error::unsupportedDataTypeCombination("position tensor must be i32");
+        requireElements(*a.position, 1, "position");
+        if (a.qRows < 0 || a.qRows + 2 * Nkv * Hd != N)
+            throw Error::tensorShapeMismatch("weight rows must be qRows + 2 * Nkv * Hd for the KV scatter.");
+        requireElements(*a.out, a.qRows, "DecodeMatvec out");
+        flags |= 4u;
+        dc.qRows = (uint32_t)a.qRows;
+        dc.kvRows = (uint32_t)(Nkv * Hd);
+        dc.headDim = (uint32_t)Hd;
+        dc.kvStride = (uint32_t)Smax;
+    } else {
+        requireElements(*a.out, N, "DecodeMatvec out");
+    }
+    dc.flags = flags;
+    const int R = matvecRows(N);
+    const std::string fn = std::string("decode_matvec_") + tag(t) + "_" + tag(o) + "_r" + std::to_string(R) + "_f" +
+                           std::to_string(flags & 3u);
+    const Tensor &x = *a.x;
+    std::vector<Binding> b = {
+        {x, kRead},
+        {a.delta ? *a.delta : x, kRead},
+        {a.wPost ? *a.wPost : x, kRead},
+        {a.wPre ? *a.wPre : x, kRead},
+        {W, kRead},
+        {*a.out, kWrite},
+        {a.xOut ? *a.xOut : x, a.xOut ? kWrite : kRead},
+        {a.kCache ? *a.kCache : *a.out, kWrite},
+        {a.vCache ? *a.vCache : *a.out, kWrite},
+        {a.position ? *a.position : x, kRead},
+    };
+    return std::make_unique<FixedDispatch>(fn, std::move(b), std::vector<std::vector<uint8_t>>{bytesOf(dc)},
+                                           grid1(streamBlocks(cdiv(N, R)), kBlock, (size_t)K * 4));
 }
 
 // EmbeddingGather.swift: ids [N] i32, table [V, H], out [N, H]

@@ -259,6 +259,7 @@ public:
     // skips the rest (used to time one kernel of a composite sequence).
     void setDispatchFilter(const std::string &functionName) { filter_ = functionName; }
 
+
 private:
     bool needsBarrier(const std::vector<Binding> &bindings) const;
     void recordAccesses(const std::vector<Binding> &bindings);
@@ -312,6 +313,31 @@ std::unique_ptr<Kernel> ScalarMul(const Tensor &x, float scalar, const Tensor &o
 std::unique_ptr<Kernel> GatedMLP(const Tensor &x, const Tensor *normWeight, const Tensor &wGate, const Tensor &wUp,
                                  const Tensor &wDown, const Tensor &out, float eps, bool addOneToWeight,
                                  const Tensor *hidden = nullptr);
+
+// The residual form: x = round(xIn + round(RMSNorm(delta) * wPost)) is
+// stored to xOut (the attention block's post-norm and residual Add), then
+// the gated MLP runs on x.
+std::unique_ptr<Kernel> GatedMLPResidual(const Tensor &xIn, const Tensor &delta, const Tensor &wPost, const Tensor &xOut,
+                                         const Tensor *normWeight, const Tensor &wGate, const Tensor &wUp,
+                                         const Tensor &wDown, const Tensor &out, float eps, bool addOneToWeight,
+                                         const Tensor *hidden = nullptr);
+
+// Decode matvec with the decoder-layer glue folded in (DecodeMatvecConstants).
+struct DecodeMatvecArgs {
+    const Tensor *x = nullptr;       // [K] the vector, or the residual stream with delta
+    const Tensor *delta = nullptr;   // [K] sub-layer output: x = x + RMSNorm(delta) * wPost
+    const Tensor *wPost = nullptr;   // [K] f32
+    const Tensor *xOut = nullptr;    // [K] receives the new residual stream
+    const Tensor *wPre = nullptr;    // [K] f32: multiply RMSNorm(x) * wPre
+    const Tensor *weight = nullptr;  // [N, K]
+    const Tensor *out = nullptr;     // [N], or [qRows] with the caches
+    const Tensor *kCache = nullptr;  // [1?, Nkv, Smax, Hd]: rows past qRows scatter here...
+    const Tensor *vCache = nullptr;  // ...and here, at row position[0]
+    const Tensor *position = nullptr;
+    int64_t qRows = 0;
+    float eps = 1e-6f;
+};
+std::unique_ptr<Kernel> DecodeMatvec(const DecodeMatvecArgs &args);
 
 std::unique_ptr<Kernel> EmbeddingGather(const Tensor &ids, const Tensor &table, const Tensor &out);
 std::unique_ptr<Kernel> Argmax(const Tensor &x, const Tensor &indices);

@@ -495,6 +495,31 @@ class Kernels:
                      refs=(x, norm_weight, w_gate, w_up, w_down, into, hidden))
 
     @staticmethod
+    def GatedMLPResidual(x_in: Tensor, delta: Tensor, w_post: Tensor, x_out: Tensor, norm_weight: Optional[Tensor],
+                         w_gate: Tensor, w_up: Tensor, w_down: Tensor, into: Tensor, *, eps: float,
+                         add_one_to_weight: bool = False, hidden: Optional[Tensor] = None) -> Kernel:
+        """x_out = x_in + RMSNorm(delta) * w_post, then into = GatedMLP(x_out)."""
+        return _make(lib().popcorn_kernel_gated_mlp_residual, _d(x_in), _d(delta), _d(w_post), _d(x_out),
+                     _d(norm_weight), _d(w_gate), _d(w_up), _d(w_down), _d(into), eps, int(add_one_to_weight),
+                     _d(hidden), refs=(x_in, delta, w_post, x_out, norm_weight, w_gate, w_up, w_down, into, hidden))
+
+    @staticmethod
+    def DecodeMatvec(x: Tensor, weight: Tensor, into: Tensor, *, delta: Optional[Tensor] = None,
+                     w_post: Optional[Tensor] = None, x_out: Optional[Tensor] = None, w_pre: Optional[Tensor] = None,
+                     k_cache: Optional[Tensor] = None, v_cache: Optional[Tensor] = None,
+                     position: Optional[Tensor] = None, q_rows: int = 0, eps: float = 1e-6) -> Kernel:
+        """Decode matvec with the layer glue (popcorn_decode_matvec_args_t)."""
+        ts = dict(x=x, delta=delta, w_post=w_post, x_out=x_out, w_pre=w_pre, weight=weight, out=into,
+                  k_cache=k_cache, v_cache=v_cache, position=position)
+        descs = {n: (t.desc() if t is not None else None) for n, t in ts.items()}
+        a = _capi.DecodeMatvecArgs()
+        for n, d in descs.items():
+            setattr(a, n, C.pointer(d) if d is not None else None)
+        a.q_rows = q_rows
+        a.eps = eps
+        return _make(lib().popcorn_kernel_decode_matvec, C.byref(a), refs=list(ts.values()))
+
+    @staticmethod
     def EmbeddingGather(ids: Tensor, table: Tensor, into: Tensor) -> Kernel:
         return _make(lib().popcorn_kernel_embedding_gather, _d(ids), _d(table), _d(into), refs=(ids, table, into))
 

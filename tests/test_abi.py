@@ -106,7 +106,9 @@ def test_flash_attention_validation_codes():
 
 def test_matmul_routing_and_validation():
     x = T([1, 2304])
-    assert pa.Kernels.Matmul(x, T([9216, 2304]), T([1, 9216]), True).describe() == "matvec_nk_simd_bf16_bf16_bf16"
+    # 4 rows per unit for long outputs (the LM head), 1 otherwise
+    assert pa.Kernels.Matmul(x, T([32768, 2304]), T([1, 32768]), True).describe() == "matvec_nk_simd_bf16_bf16_bf16"
+    assert pa.Kernels.Matmul(x, T([9216, 2304]), T([1, 9216]), True).describe() == "matvec_nk_simd_bf16_bf16_bf16_r1"
     assert pa.Kernels.Matmul(T([1, 9216]), T([2304, 9216]), T([1, 2304]), True).describe() == \
         "matvec_nk_simd_bf16_bf16_bf16_r1"
     assert pa.Kernels.Matmul(x, T([2304, 300]), T([1, 300]), False).describe() == "matvec_bf16_bf16_bf16"
@@ -146,7 +148,10 @@ def test_gated_mlp_validation_and_routing():
     E = pa.PopcornError
     k = pa.Kernels.GatedMLP(T([2304]), T([2304], "f32"), T([9216, 2304]), T([9216, 2304]), T([2304, 9216]),
                             T([2304]), eps=1e-6)
-    assert k.function_names == ["gated_mlp_gate_up_bf16", "matvec_nk_simd_bf16_bf16_bf16_r1"]
+    assert k.function_names == ["gated_mlp_gate_up_bf16_r1", "matvec_nk_simd_bf16_bf16_bf16_r1"]
+    r = pa.Kernels.GatedMLPResidual(T([2304]), T([2304]), T([2304], "f32"), T([2304], ptr=FAKE + 4096), T([2304], "f32"),
+                                    T([9216, 2304]), T([9216, 2304]), T([2304, 9216]), T([2304]), eps=1e-6)
+    assert r.function_names == ["gated_mlp_gate_up_bf16_r1_res", "matvec_nk_simd_bf16_bf16_bf16_r1"]
     with pytest.raises(E) as e:
         pa.Kernels.GatedMLP(T([2304]), None, T([9216, 2304]), T([9216, 2300]), T([2304, 9216]), T([2304]), eps=1e-6)
     assert e.value.code == E.TENSOR_SHAPE_MISMATCH
@@ -168,3 +173,27 @@ def test_no_gpu_paths_fail_loudly_here():
         pytest.skip("a GPU is visible")
     with pytest.raises(pa.PopcornError):
         pa.KernelLibrary()
+
+
+def test_decode_matvec_routing():
+    # the glue is compiled in: _f<bit0 residual | bit1 pre-norm>; the KV
+    # scatter is a runtime flag; 4 rows per unit for long outputs
+    x, w = T([2304]), T([4096, 2304])
+    norm = T([2304], "f32")
+    caches = dict(k_cache=T([4, 4352, 256], ptr=FAKE + 2 ** 30), v_cache=T([4, 4352, 256], ptr=FAKE + 2 ** 31),
+                  position=T([1], "i32"), q_rows=2048)
+    assert pa.Kernels.DecodeMatvec(x, T([2048, 2304]), T([2048])).function_names == ["decode_matvec_bf16_bf16_r1_f0"]
+    assert pa.Kernels.DecodeMatvec(x, w, T([2048]), w_pre=norm, **caches).function_names == \
+        ["decode_matvec_bf16_bf16_r1_f2"]
+    res = dict(delta=T([2304]), w_post=norm, x_out=T([2304], ptr=FAKE + 2 ** 20))
+    assert pa.Kernels.DecodeMatvec(x, w, T([2048]), w_pre=norm, **res, **caches).function_names == \
+        ["decode_matvec_bf16_bf16_r1_f3"]
+    assert pa.Kernels.DecodeMatvec(x, T([256000, 2304]), T([256000], "f32"), w_pre=norm, **res).function_names == \
+        ["decode_matvec_bf16_f32_r4_f3"]
+    E = pa.PopcornError
+    with pytest.raises(E) as e:  # rows must be q_rows + K rows + V rows
+        pa.Kernels.DecodeMatvec(x, T([4000, 2304]), T([2048]), **caches)
+    assert e.value.code == E.TENSOR_SHAPE_MISMATCH
+    with pytest.raises(E) as e:  # the residual output may not alias x
+        pa.Kernels.DecodeMatvec(x, w, T([4096]), delta=T([2304]), w_post=norm, x_out=x)
+    assert e.value.code == E.INVALID_ARGUMENT

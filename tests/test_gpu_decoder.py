@@ -130,7 +130,7 @@ def test_gemma2_2b_shape_decodes(env):
     dec = D.Decoder(lib, stream, cfg)
     dec.randomize(seed=0)
     names, n = dec.describe()
-    assert n == len(names) and "gated_mlp_gate_up_bf16" in names
+    assert n == len(names) and "gated_mlp_gate_up_bf16_r1_res" in names
     dec.reset(123, 4096)
     dec.step(8, use_graph=True)
     tok, pos = dec.read()
