@@ -103,6 +103,21 @@ def load_traffic(name):
     return t.get(name, {}).get("bytes_per_launch")
 
 
+def copy_calibration(pa, nbytes=1 << 30, copies=3):
+    """A plain copy of known size: its per-dispatch FETCH_SIZE and WRITE_SIZE
+    (KiB) against `nbytes` give the scale of those counters on this GPU."""
+    from popcorn_amd import runtime as R
+
+    src, dst = pa.DeviceBuffer(nbytes), pa.DeviceBuffer(nbytes)
+    stream = pa.Stream()
+    h = R._stream_handle(stream)
+    R.check(R.lib().popcorn_memset(src.ptr, 1, nbytes, h))
+    for _ in range(copies):
+        R.check(R.lib().popcorn_memcpy_d2d(dst.ptr, src.ptr, nbytes, h))
+    stream.synchronize()
+    print(json.dumps({"calibration": "device-to-device copy", "bytes": nbytes, "copies": copies}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -112,6 +127,9 @@ def main():
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=4)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run 3 device-to-device copies of 1 GiB (the known-size kernel that scales the "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE counters) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every GPU box here has one GPU); "
@@ -124,6 +142,9 @@ def main():
     if pa.device_count() < 1:
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
+    if args.copy_calibration:
+        copy_calibration(pa)
+        return
     lib = pa.KernelLibrary()
     stream = pa.Stream()
     cfg = D.DecoderConfig(graph_steps=args.graph_steps)
