@@ -21,6 +21,7 @@
 
 namespace {
 
+using pk::kStreamSteps;
 using pk::kStreamWaves;
 
 template <typename T, int R, bool RES>
@@ -29,7 +30,7 @@ __device__ void gate_up(const typename T::storage *__restrict__ x, const float *
                         typename T::storage *__restrict__ h, const typename T::storage *__restrict__ delta,
                         const float *__restrict__ w_post, typename T::storage *__restrict__ x_out,
                         const GatedMLPConstants &p, float *xs) {
-    constexpr int S = 2 * R, U = 16 / S;
+    constexpr int S = 2 * R, U = kStreamSteps;
     constexpr int kV = pk::Vec<T>::kVec;
     __shared__ float red[kStreamWaves];
     const uint32_t H = p.H, F = p.F;

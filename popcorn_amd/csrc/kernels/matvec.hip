@@ -11,7 +11,7 @@
 //
 // The kernel is HBM-bound: W is read once, x is reused from LDS. A block of
 // 4 waves stages x (Stage), then every wave streams its units of R rows
-// (RowStream, 16 / R loads of 16 bytes per row and lane in flight). The host
+// (RowStream, 4 loads of 16 bytes per row and lane in flight). The host
 // sizes the grid so that each wave gets the same number of units, give or
 // take one. Rows whose length is not a multiple of the vector width, or an
 // unaligned W, take a scalar loop (the reference's K % 4 != 0 tail,
@@ -23,6 +23,7 @@
 
 namespace {
 
+using pk::kStreamSteps;
 using pk::kStreamWaves;
 
 template <typename X, typename W, typename O, int R, bool RES, bool PRE, int J>
@@ -32,7 +33,7 @@ __device__ void matvec_nk(const typename X::storage *__restrict__ x_in, const ty
                           typename X::storage *__restrict__ x_out, typename O::storage *__restrict__ kcache,
                           typename O::storage *__restrict__ vcache, const int32_t *__restrict__ position,
                           const DecodeMatvecConstants &p, float *xs) {
-    constexpr int U = 16 / R;
+    constexpr int U = kStreamSteps;
     constexpr int kV = pk::Vec<W>::kVec;
     __shared__ float red[kStreamWaves];
     const uint32_t K = p.K, N = p.N;

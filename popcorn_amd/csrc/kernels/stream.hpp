@@ -15,6 +15,15 @@
 
 namespace pk {
 
+// Steps in flight in a RowStream (U): each step is one 16-byte load per
+// row of a unit, so a lane has U x S loads in flight. 4, at 12 waves per CU
+// (the host's grid), measured best on MI355X for every decode matvec shape
+// (depth 2..24 x 4..24 waves per CU swept).
+#ifndef POPCORN_STREAM_STEPS
+#define POPCORN_STREAM_STEPS 4
+#endif
+constexpr int kStreamSteps = POPCORN_STREAM_STEPS;
+static_assert(kStreamSteps >= 1, "a RowStream needs at least one step in flight");
 constexpr int kStreamThreads = 256;
 constexpr int kStreamWaves = kStreamThreads / 64;
 constexpr uint32_t kKVScatter = 4u;  // DecodeMatvecConstants.flags bit 2 (runtime)

@@ -249,13 +249,15 @@ std::string plainName(const char *base, DataType x, DataType w, DataType o) {
 // (one LDS read of x feeds 4 rows), 1 otherwise (finer units balance better).
 int matvecRows(int64_t N) { return N >= 32768 ? 4 : 1; }
 
-// Waves per CU the streaming kernels are sized for: 8 (two per SIMD) by
-// default; POPCORN_STREAM_WAVES_PER_CU overrides it (1..32) for tuning.
+// Waves per CU the streaming kernels are sized for: 12 (3 blocks of 4 waves,
+// 3 waves per SIMD), measured best on MI355X for the decode matvecs with 4
+// steps in flight per wave (stream.hpp); POPCORN_STREAM_WAVES_PER_CU
+// overrides it (1..32) for tuning.
 int streamWavesPerCU() {
     static const int w = [] {
         const char *e = std::getenv("POPCORN_STREAM_WAVES_PER_CU");
         const int v = e ? std::atoi(e) : 0;
-        return v >= 1 && v <= 32 ? v : 8;
+        return v >= 1 && v <= 32 ? v : 12;
     }();
     return w;
 }

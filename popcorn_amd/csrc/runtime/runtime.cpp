@@ -3,6 +3,7 @@
 #include <dlfcn.h>
 
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <sstream>
 
@@ -147,7 +148,9 @@ void CScratchAllocator::releaseTemporaryBuffer(const KernelTemporaryBuffer &t) {
 
 // ---- kernel library ----------------------------------------------------------------
 
+// POPCORN_KERNEL_DIR, else the kernels/ directory next to this library.
 std::string KernelLibrary::defaultPath() {
+    if (const char *env = std::getenv("POPCORN_KERNEL_DIR"); env && *env) return env;
     Dl_info info;
     if (dladdr((void *)&popcorn_last_error_message, &info) && info.dli_fname) {
         std::string so = info.dli_fname;
