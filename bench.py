@@ -118,6 +118,46 @@ def copy_calibration(pa, nbytes=1 << 30, copies=3):
     print(json.dumps({"calibration": "device-to-device copy", "bytes": nbytes, "copies": copies}))
 
 
+def fd_sweep(pa, lib, stream, enc):
+    """split-KV FlashDecoding (partial + LSE combine) in f16,
+    Q [B, 8, 1, 256], K/V [B, 4, ctx, 256] N(0, 1), scale 1/16, no mask, over
+    B x ctx. Every launch reads a KV set it has not read for >= 512 MB of other
+    sets (cold in the 256 MB MALL), so the rate is HBM's."""
+    out_rows = []
+    for B in (1, 8, 32):
+        for ctx in (2048, 8192, 32768):
+            kv_elems = B * 4 * ctx * 256
+            nbytes = 2 * kv_elems * 2 + 2 * B * 8 * 256 * 2
+            sets = max(1, min(64, -(-(512 << 20) // (2 * kv_elems * 2))))
+            kpool = pa.Tensor.empty([sets * kv_elems], "f16")
+            vpool = pa.Tensor.empty([sets * kv_elems], "f16")
+            lib.fill_normal(kpool, 1, stream=stream)
+            lib.fill_normal(vpool, 2, stream=stream)
+            q = pa.Tensor.empty([B, 8, 1, 256], "f16")
+            lib.fill_normal(q, 3, stream=stream)
+            o = pa.Tensor.empty([B, 8, 1, 256], "f16")
+            kerns = [pa.Kernels.FlashAttention(q, kpool.view([B, 4, ctx, 256], offset_elements=i * kv_elems),
+                                               vpool.view([B, 4, ctx, 256], offset_elements=i * kv_elems), o,
+                                               scale=1 / 16, mask=pa.AttentionMask(2), batch=B, query_heads=8,
+                                               kv_heads=4, query_len=1, key_len=ctx, head_dim=256)
+                     for i in range(sets)]
+            reps = max(sets, min(256, int(4e9 // nbytes)))
+            enc.encode(*kerns)
+            stream.synchronize()
+            e0, e1 = pa.Event(), pa.Event()
+            e0.record(stream)
+            for r in range(reps):
+                enc.encode(kerns[r % sets])
+            e1.record(stream)
+            e1.synchronize()
+            us = e0.elapsed_ms(e1) * 1e3 / reps
+            gbs = nbytes / (us * 1e-6) / 1e9
+            out_rows.append({"B": B, "ctx": ctx, "us": round(us, 2), "GB_s": round(gbs, 1),
+                             "frac": round(gbs / HBM_PEAK_GBS, 3)})
+            del kerns, kpool, vpool
+    return out_rows
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -127,6 +167,7 @@ def main():
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=4)
+    ap.add_argument("--no-fd-sweep", action="store_true", help="skip the config-2 FlashDecoding sweep")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 3 device-to-device copies of 1 GiB (the known-size kernel that scales the "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -195,6 +236,10 @@ def main():
                 "frac": round(dk["GB_s"] / HBM_PEAK_GBS, 3), "traffic": load_traffic(dominant),
                 "kernel": dominant, "bytes_per_launch": dk["bytes"], "mean_us": dk["mean_us"]}
 
+    fd = None
+    if not args.no_fd_sweep:
+        fd = fd_sweep(pa, lib, stream, pa.KernelCommandEncoder(lib, stream))
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(dec, cfg, stream, token)
@@ -220,6 +265,7 @@ def main():
         "hbm_step_frac": round(step_bytes * tokens_per_s / 1e9 / HBM_PEAK_GBS, 3),
         "roofline": roofline,
         "kernels": kernels,
+        "flash_decoding_config2": fd,
         "cpu_baseline": cpu,
     }
     dec.close()

@@ -74,6 +74,23 @@ const char *tag(DataType t) { return name(t); }
 // FlashAttention / FlashDecoding (FlashAttention.swift, FlashDecoding.swift)
 // ---------------------------------------------------------------------------
 
+// FlashDecoding partition sizing: blocks per CU to aim for (default 2) and
+// the fewest keys a partition takes (default 64); POPCORN_FD_BLOCKS_PER_CU
+// and POPCORN_FD_MIN_KEYS override them for tuning.
+int envInt(const char *name, int lo, int hi, int dflt) {
+    const char *e = std::getenv(name);
+    const int v = e ? std::atoi(e) : 0;
+    return v >= lo && v <= hi ? v : dflt;
+}
+int fdBlocksPerCU() {
+    static const int v = envInt("POPCORN_FD_BLOCKS_PER_CU", 1, 64, 2);
+    return v;
+}
+int fdMinKeys() {
+    static const int v = envInt("POPCORN_FD_MIN_KEYS", 1, 4096, 64);
+    return v;
+}
+
 struct AttnDims {
     int64_t B, Nq, Nkv, Sq, Sk, Hd, cap;
 };
@@ -195,12 +212,13 @@ private:
         }
         reduceName_ = std::string("flash_decoding_reduce_") + tag(out_.dataType);
         ngroups_ = cdiv(G, gmax);
-        // Partitions: enough blocks to cover every CU twice, but at least 64
-        // keys per block (the reference fixes P = 8, FlashDecoding.swift:77).
+        // Partitions: enough blocks to cover every CU fdBlocksPerCU() times,
+        // but at least fdMinKeys() keys per block (the reference fixes P = 8,
+        // FlashDecoding.swift:77).
         const int64_t keys = std::max<int64_t>(hasPos_ ? d_.cap : d_.Sk, 1);
         const int64_t base = d_.B * d_.Nkv * ngroups_ * d_.Sq;
-        const int64_t want = cdiv(2 * deviceCUs(), base);
-        const int64_t maxByKeys = cdiv(keys, 64);
+        const int64_t want = cdiv(fdBlocksPerCU() * deviceCUs(), base);
+        const int64_t maxByKeys = cdiv(keys, fdMinKeys());
         P_ = std::clamp<int64_t>(std::min(want, maxByKeys), 1, 1024);
     }
 
