@@ -158,6 +158,49 @@ def fd_sweep(pa, lib, stream, enc):
     return out_rows
 
 
+MFMA_PEAK_F16_TFLOPS = 2500.0
+
+
+def prefill_config5(pa, lib, stream, enc, reps=8):
+    """BASELINE config 5 (Gemma-7B-shaped single-layer prefill, f16, f32
+    accumulation, seq 2048): the QKV Matmul [2048, 3072] x [9216, 3072]^T and
+    the MLP Matmuls (gate, up [24576, 3072]; down [3072, 24576]) on the MFMA
+    tiles. Activations N(0, 1), weights N(0, 0.02). Each timed over `reps`
+    launches after one warmup."""
+    S, H, F, QKV = 2048, 3072, 24576, 3 * 3072
+    x = pa.Tensor.empty([S, H], "f16")
+    h = pa.Tensor.empty([S, F], "f16")
+    lib.fill_normal(x, 21, stream=stream)
+    lib.fill_normal(h, 22, stream=stream)
+    shapes = {"qkv": (x, QKV, H), "gate": (x, F, H), "up": (x, F, H), "down": (h, H, F)}
+    rows = {}
+    total_flop, total_us = 0.0, 0.0
+    for name, (a, n, k) in shapes.items():
+        w = pa.Tensor.empty([n, k], "f16")
+        lib.fill_normal(w, 30 + len(rows), std=0.02, stream=stream)
+        c = pa.Tensor.empty([S, n], "f16")
+        kern = pa.Kernels.Matmul(a, w, c, True)
+        enc.encode(kern)
+        stream.synchronize()
+        e0, e1 = pa.Event(), pa.Event()
+        e0.record(stream)
+        for _ in range(reps):
+            enc.encode(kern)
+        e1.record(stream)
+        e1.synchronize()
+        us = e0.elapsed_ms(e1) * 1e3 / reps
+        flop = 2.0 * S * n * k
+        total_flop += flop
+        total_us += us
+        rows[name] = {"M": S, "N": n, "K": k, "kernel": kern.function_names[0], "us": round(us, 1),
+                      "TFLOP_s": round(flop / (us * 1e-6) / 1e12, 1),
+                      "frac": round(flop / (us * 1e-6) / 1e12 / MFMA_PEAK_F16_TFLOPS, 3)}
+        del w, c, kern
+    rows["gemm_total"] = {"us": round(total_us, 1), "TFLOP_s": round(total_flop / (total_us * 1e-6) / 1e12, 1),
+                          "frac": round(total_flop / (total_us * 1e-6) / 1e12 / MFMA_PEAK_F16_TFLOPS, 3)}
+    return rows
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -168,6 +211,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=4)
     ap.add_argument("--no-fd-sweep", action="store_true", help="skip the config-2 FlashDecoding sweep")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the config-5 prefill measurement")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 3 device-to-device copies of 1 GiB (the known-size kernel that scales the "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -240,6 +284,10 @@ def main():
     if not args.no_fd_sweep:
         fd = fd_sweep(pa, lib, stream, pa.KernelCommandEncoder(lib, stream))
 
+    prefill = None
+    if not args.no_prefill:
+        prefill = prefill_config5(pa, lib, stream, pa.KernelCommandEncoder(lib, stream))
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(dec, cfg, stream, token)
@@ -266,6 +314,7 @@ def main():
         "roofline": roofline,
         "kernels": kernels,
         "flash_decoding_config2": fd,
+        "prefill_config5": prefill,
         "cpu_baseline": cpu,
     }
     dec.close()

@@ -1,0 +1,176 @@
+// Prefill Matmul on the matrix cores: C[M, N] = A[M, K] . B[N, K]^T
+// (the reference's transposeB layout, Matmul.swift:34-65 and
+// MPPMatmul.metal:19-91, whose MPP tiles this replaces), f16 or bf16 inputs,
+// f32 accumulation, output f32 or the input dtype (popcorn_store rounding).
+//
+// v_mfma_f32_32x32x16_{f16,bf16} lane layout (checked on gfx950):
+//   A fragment: lane l holds A[l % 32][(l / 32) * 8 + i], i < 8
+//   B fragment: lane l holds B[(l / 32) * 8 + i][l % 32]  (= Bt[l % 32][...])
+//   C: lane l, element i is C[(i / 4) * 8 + (l / 32) * 4 + i % 4][l % 32]
+// so both operands are 16-byte runs along K of a row of A or of Bt.
+//
+// A block (4 waves) computes a 128 x 128 tile; each wave a 64 x 64 quarter
+// as 2 x 2 MFMA tiles. K advances 64 at a time through two LDS stages
+// (rows padded to 72 elements, so the 32 rows a fragment load touches fall
+// in distinct banks); the next stage's global loads are in registers while
+// the current stage is multiplied. Tiles are assigned XCD by XCD (blocks
+// are dealt round-robin to the 8 XCDs, so block b runs on XCD b % 8) and,
+// within an XCD's range, in groups of 8 tile rows, so the A and B panels a
+// group shares stay in that XCD's L2.
+#include "common.hpp"
+
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf168 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T>
+struct Mma;
+template <>
+struct Mma<pk::F16> {
+    __device__ static inline f32x16 run(u32x4 a, u32x4 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0,
+                                                      0, 0);
+    }
+};
+template <>
+struct Mma<pk::BF16> {
+    __device__ static inline f32x16 run(u32x4 a, u32x4 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf168, a), __builtin_bit_cast(bf168, b), c,
+                                                       0, 0, 0);
+    }
+};
+
+constexpr int BM = 128, BN = 128, BK = 64;
+constexpr int LDK = BK + 8;                  // padded LDS row, in elements
+constexpr int kThreads = 256;
+constexpr int kChunks = BM * BK / 8 / kThreads;  // 16-byte chunks per thread per operand per stage
+constexpr int kXcds = 8;
+constexpr int kGroupM = 8;
+
+// Tile (pm, pn) of block b: XCD-contiguous ranges, grouped rows within.
+__device__ inline void tile_of(uint32_t b, uint32_t nM, uint32_t nN, uint32_t &pm, uint32_t &pn) {
+    const uint32_t total = nM * nN;
+    uint32_t pid = b;
+    if (total % kXcds == 0) pid = (b % kXcds) * (total / kXcds) + b / kXcds;
+    const uint32_t inGroup = kGroupM * nN;
+    const uint32_t group = pid / inGroup;
+    const uint32_t firstM = group * kGroupM;
+    const uint32_t gm = min(nM - firstM, (uint32_t)kGroupM);
+    pm = firstM + (pid % inGroup) % gm;
+    pn = (pid % inGroup) / gm;
+}
+
+template <typename T, typename O>
+__device__ void gemm_nt(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
+                        typename O::storage *__restrict__ C, const MatmulConstants &p) {
+    __shared__ __attribute__((aligned(16))) uint16_t sA[2][BM * LDK];
+    __shared__ __attribute__((aligned(16))) uint16_t sB[2][BN * LDK];
+    const uint32_t M = p.M, N = p.N, K = p.K;
+    const uint32_t nM = (M + BM - 1) / BM, nN = (N + BN - 1) / BN;
+    uint32_t pm, pn;
+    tile_of(blockIdx.x, nM, nN, pm, pn);
+    const uint32_t bm = pm * BM, bn = pn * BN;
+    const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const uint32_t wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+
+    // Global chunk c of a stage: row c / 8 of the tile, elements (c % 8) * 8 .. +8
+    // of the stage's K range. Rows past M (N) and K past the end read a valid
+    // address and are zeroed when stored to LDS (the mask is applied there,
+    // after the stage's multiply, so the loads stay in flight meanwhile).
+    u32x4 ra[kChunks], rb[kChunks];
+    uint32_t okA = 0, okB = 0;
+    auto gload = [&](uint32_t k0) {
+        okA = okB = 0;
+#pragma unroll
+        for (int i = 0; i < kChunks; ++i) {
+            const uint32_t c = t + i * kThreads, r = c >> 3, k = k0 + (c & 7) * 8;
+            const uint32_t ar = bm + r, br = bn + r;
+            const bool kin = k < K;
+            ra[i] = *reinterpret_cast<const u32x4 *>(A + (uint64_t)min(ar, M - 1) * K + (kin ? k : 0u));
+            rb[i] = *reinterpret_cast<const u32x4 *>(B + (uint64_t)min(br, N - 1) * K + (kin ? k : 0u));
+            okA |= (ar < M && kin) ? 1u << i : 0u;
+            okB |= (br < N && kin) ? 1u << i : 0u;
+        }
+    };
+    auto lstore = [&](int buf) {
+        const u32x4 zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int i = 0; i < kChunks; ++i) {
+            const uint32_t c = t + i * kThreads, r = c >> 3, kc = (c & 7) * 8;
+            *reinterpret_cast<u32x4 *>(&sA[buf][r * LDK + kc]) = (okA >> i) & 1u ? ra[i] : zero;
+            *reinterpret_cast<u32x4 *>(&sB[buf][r * LDK + kc]) = (okB >> i) & 1u ? rb[i] : zero;
+        }
+    };
+
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[mi][ni][i] = 0.0f;
+
+    auto compute = [&](int buf) {
+#pragma unroll
+        for (int kk = 0; kk < BK / 16; ++kk) {
+            const uint32_t ko = kk * 16 + (lane >> 5) * 8;
+            u32x4 fa[2], fb[2];
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi)
+                fa[mi] = *reinterpret_cast<const u32x4 *>(&sA[buf][(wm + mi * 32 + (lane & 31)) * LDK + ko]);
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni)
+                fb[ni] = *reinterpret_cast<const u32x4 *>(&sB[buf][(wn + ni * 32 + (lane & 31)) * LDK + ko]);
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = Mma<T>::run(fa[mi], fb[ni], acc[mi][ni]);
+        }
+    };
+
+    const uint32_t nk = (K + BK - 1) / BK;
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (uint32_t kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+        if (kt + 1 < nk) gload((kt + 1) * BK);
+        compute(cur);
+        if (kt + 1 < nk) lstore(cur ^ 1);
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi) {
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni) {
+            const uint32_t col = bn + wn + ni * 32 + (lane & 31);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const uint32_t row = bm + wm + mi * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+                if (row < M && col < N) C[(uint64_t)row * N + col] = O::store(acc[mi][ni][i]);
+            }
+        }
+    }
+}
+
+}  // namespace
+
+// A, B: 16-bit storage; the host requires K % 8 == 0 and 16-byte aligned A, B.
+#define GEMM_MFMA(name, T, O)                                                                     \
+    POPCORN_KERNEL void __launch_bounds__(256)                                                    \
+        name(const uint16_t *a, const uint16_t *b, O::storage *c, MatmulConstants p) {            \
+        gemm_nt<T, O>(a, b, c, p);                                                                \
+    }
+
+using pk::BF16;
+using pk::F16;
+using pk::F32;
+
+GEMM_MFMA(matmul_mfma_f16_f16_f16, F16, F16)
+GEMM_MFMA(matmul_mfma_f16_f16_f32, F16, F32)
+GEMM_MFMA(matmul_mfma_bf16_bf16_bf16, BF16, BF16)
+GEMM_MFMA(matmul_mfma_bf16_bf16_f32, BF16, F32)

@@ -320,6 +320,19 @@ std::unique_ptr<Kernel> makeMatmul(const Tensor &a, const Tensor &b, const Tenso
                                                         tag(a.dataType) + ", " + tag(b.dataType) + ", " + tag(c.dataType) + ".");
         return std::make_unique<FixedDispatch>(fn, binds, std::vector<std::vector<uint8_t>>{bytesOf(mc)}, grid1(cdiv(n, kBlock), kBlock));
     }
+    // m > 1, transposeB, 16-bit operands: the MFMA tiles (the reference's MPP
+    // GEMM path, Matmul.swift:175-196); 16-byte rows needed (K % 8 == 0).
+    {
+        const DataType t = a.dataType;
+        if (transposeB && (t == DataType::f16 || t == DataType::bf16) && b.dataType == t &&
+            (c.dataType == t || c.dataType == DataType::f32) && k % 8 == 0 && k > 0 && aligned16(a.data) &&
+            aligned16(b.data)) {
+            MatmulConstants mc{(uint32_t)m, (uint32_t)k, (uint32_t)n, 1u};
+            const std::string fn = std::string("matmul_mfma_") + tag(t) + "_" + tag(t) + "_" + tag(c.dataType);
+            return std::make_unique<FixedDispatch>(fn, binds, std::vector<std::vector<uint8_t>>{bytesOf(mc)},
+                                                   grid1(cdiv(m, 128) * cdiv(n, 128), kBlock));
+        }
+    }
     std::string fn = plainName("matmul", a.dataType, b.dataType, c.dataType);
     if (fn.empty())
         throw Error::unsupportedDataTypeCombination(std::string("Unsupported matmul data type combination: ") +
