@@ -9,8 +9,10 @@
 //   C: lane l, element i is C[(i / 4) * 8 + (l / 32) * 4 + i % 4][l % 32]
 // so both operands are 16-byte runs along K of a row of A or of Bt.
 //
-// A block (4 waves) computes a 128 x 128 tile; each wave a 64 x 64 quarter
-// as 2 x 2 MFMA tiles. K advances 64 at a time through two LDS stages
+// A block computes a BM x BN tile (128 or 256 each; 4 or 8 waves, each wave
+// a 64 x 64 or 128 x 64 piece of 32 x 32 MFMA tiles; the host picks the tile
+// shape per GEMM so the tile count fills the 256 CUs evenly). K advances 64
+// at a time through two LDS stages
 // (rows padded to 72 elements, so the 32 rows a fragment load touches fall
 // in distinct banks); the next stage's global loads are in registers while
 // the current stage is multiplied. Tiles are assigned XCD by XCD (blocks
@@ -43,10 +45,8 @@ struct Mma<pk::BF16> {
     }
 };
 
-constexpr int BM = 128, BN = 128, BK = 64;
-constexpr int LDK = BK + 8;                  // padded LDS row, in elements
-constexpr int kThreads = 256;
-constexpr int kChunks = BM * BK / 8 / kThreads;  // 16-byte chunks per thread per operand per stage
+constexpr int BK = 64;
+constexpr int LDK = BK + 8;  // padded LDS row, in elements
 constexpr int kXcds = 8;
 constexpr int kGroupM = 8;
 
@@ -63,53 +63,75 @@ __device__ inline void tile_of(uint32_t b, uint32_t nM, uint32_t nN, uint32_t &p
     pn = (pid % inGroup) / gm;
 }
 
-template <typename T, typename O>
+// BM x BN block tile on WM_N x WN_N waves; each wave a (BM / WM_N) x
+// (BN / WN_N) tile of 32 x 32 MFMA tiles.
+template <typename T, typename O, int BM, int BN, int WM_N, int WN_N>
 __device__ void gemm_nt(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
                         typename O::storage *__restrict__ C, const MatmulConstants &p) {
-    __shared__ __attribute__((aligned(16))) uint16_t sA[2][BM * LDK];
-    __shared__ __attribute__((aligned(16))) uint16_t sB[2][BN * LDK];
+    constexpr int kThreads = 64 * WM_N * WN_N;
+    constexpr int WM = BM / WM_N, WN = BN / WN_N;
+    constexpr int TM = WM / 32, TN = WN / 32;
+    constexpr int kChunksA = BM * BK / 8 / kThreads, kChunksB = BN * BK / 8 / kThreads;
+    static_assert(kChunksA * kThreads * 8 == BM * BK && kChunksB * kThreads * 8 == BN * BK, "tile / thread count");
+    // Two stages of [A rows | B rows], each row LDK elements. The array is
+    // declared here (not passed in) so every access stays an LDS access.
+    constexpr int kStage = (BM + BN) * LDK;
+    __shared__ __attribute__((aligned(16))) uint16_t smem[2 * kStage];
+    auto sA = [&](int buf) { return smem + buf * kStage; };
+    auto sB = [&](int buf) { return smem + buf * kStage + BM * LDK; };
+
     const uint32_t M = p.M, N = p.N, K = p.K;
     const uint32_t nM = (M + BM - 1) / BM, nN = (N + BN - 1) / BN;
     uint32_t pm, pn;
     tile_of(blockIdx.x, nM, nN, pm, pn);
     const uint32_t bm = pm * BM, bn = pn * BN;
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const uint32_t wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const uint32_t wm = (wave / WN_N) * WM, wn = (wave % WN_N) * WN;
 
     // Global chunk c of a stage: row c / 8 of the tile, elements (c % 8) * 8 .. +8
     // of the stage's K range. Rows past M (N) and K past the end read a valid
     // address and are zeroed when stored to LDS (the mask is applied there,
     // after the stage's multiply, so the loads stay in flight meanwhile).
-    u32x4 ra[kChunks], rb[kChunks];
+    u32x4 ra[kChunksA], rb[kChunksB];
     uint32_t okA = 0, okB = 0;
     auto gload = [&](uint32_t k0) {
         okA = okB = 0;
 #pragma unroll
-        for (int i = 0; i < kChunks; ++i) {
+        for (int i = 0; i < kChunksA; ++i) {
             const uint32_t c = t + i * kThreads, r = c >> 3, k = k0 + (c & 7) * 8;
-            const uint32_t ar = bm + r, br = bn + r;
+            const uint32_t ar = bm + r;
             const bool kin = k < K;
             ra[i] = *reinterpret_cast<const u32x4 *>(A + (uint64_t)min(ar, M - 1) * K + (kin ? k : 0u));
-            rb[i] = *reinterpret_cast<const u32x4 *>(B + (uint64_t)min(br, N - 1) * K + (kin ? k : 0u));
             okA |= (ar < M && kin) ? 1u << i : 0u;
+        }
+#pragma unroll
+        for (int i = 0; i < kChunksB; ++i) {
+            const uint32_t c = t + i * kThreads, r = c >> 3, k = k0 + (c & 7) * 8;
+            const uint32_t br = bn + r;
+            const bool kin = k < K;
+            rb[i] = *reinterpret_cast<const u32x4 *>(B + (uint64_t)min(br, N - 1) * K + (kin ? k : 0u));
             okB |= (br < N && kin) ? 1u << i : 0u;
         }
     };
     auto lstore = [&](int buf) {
         const u32x4 zero = {0u, 0u, 0u, 0u};
 #pragma unroll
-        for (int i = 0; i < kChunks; ++i) {
+        for (int i = 0; i < kChunksA; ++i) {
             const uint32_t c = t + i * kThreads, r = c >> 3, kc = (c & 7) * 8;
-            *reinterpret_cast<u32x4 *>(&sA[buf][r * LDK + kc]) = (okA >> i) & 1u ? ra[i] : zero;
-            *reinterpret_cast<u32x4 *>(&sB[buf][r * LDK + kc]) = (okB >> i) & 1u ? rb[i] : zero;
+            *reinterpret_cast<u32x4 *>(&sA(buf)[r * LDK + kc]) = (okA >> i) & 1u ? ra[i] : zero;
+        }
+#pragma unroll
+        for (int i = 0; i < kChunksB; ++i) {
+            const uint32_t c = t + i * kThreads, r = c >> 3, kc = (c & 7) * 8;
+            *reinterpret_cast<u32x4 *>(&sB(buf)[r * LDK + kc]) = (okB >> i) & 1u ? rb[i] : zero;
         }
     };
 
-    f32x16 acc[2][2];
+    f32x16 acc[TM][TN];
 #pragma unroll
-    for (int mi = 0; mi < 2; ++mi)
+    for (int mi = 0; mi < TM; ++mi)
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni)
+        for (int ni = 0; ni < TN; ++ni)
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[mi][ni][i] = 0.0f;
 
@@ -117,17 +139,17 @@ __device__ void gemm_nt(const uint16_t *__restrict__ A, const uint16_t *__restri
 #pragma unroll
         for (int kk = 0; kk < BK / 16; ++kk) {
             const uint32_t ko = kk * 16 + (lane >> 5) * 8;
-            u32x4 fa[2], fb[2];
+            u32x4 fa[TM], fb[TN];
 #pragma unroll
-            for (int mi = 0; mi < 2; ++mi)
-                fa[mi] = *reinterpret_cast<const u32x4 *>(&sA[buf][(wm + mi * 32 + (lane & 31)) * LDK + ko]);
+            for (int mi = 0; mi < TM; ++mi)
+                fa[mi] = *reinterpret_cast<const u32x4 *>(&sA(buf)[(wm + mi * 32 + (lane & 31)) * LDK + ko]);
 #pragma unroll
-            for (int ni = 0; ni < 2; ++ni)
-                fb[ni] = *reinterpret_cast<const u32x4 *>(&sB[buf][(wn + ni * 32 + (lane & 31)) * LDK + ko]);
+            for (int ni = 0; ni < TN; ++ni)
+                fb[ni] = *reinterpret_cast<const u32x4 *>(&sB(buf)[(wn + ni * 32 + (lane & 31)) * LDK + ko]);
 #pragma unroll
-            for (int mi = 0; mi < 2; ++mi)
+            for (int mi = 0; mi < TM; ++mi)
 #pragma unroll
-                for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = Mma<T>::run(fa[mi], fb[ni], acc[mi][ni]);
+                for (int ni = 0; ni < TN; ++ni) acc[mi][ni] = Mma<T>::run(fa[mi], fb[ni], acc[mi][ni]);
         }
     };
 
@@ -144,9 +166,9 @@ __device__ void gemm_nt(const uint16_t *__restrict__ A, const uint16_t *__restri
     }
 
 #pragma unroll
-    for (int mi = 0; mi < 2; ++mi) {
+    for (int mi = 0; mi < TM; ++mi) {
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni) {
+        for (int ni = 0; ni < TN; ++ni) {
             const uint32_t col = bn + wn + ni * 32 + (lane & 31);
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
@@ -160,17 +182,24 @@ __device__ void gemm_nt(const uint16_t *__restrict__ A, const uint16_t *__restri
 }  // namespace
 
 // A, B: 16-bit storage; the host requires K % 8 == 0 and 16-byte aligned A, B.
-#define GEMM_MFMA(name, T, O)                                                                     \
-    POPCORN_KERNEL void __launch_bounds__(256)                                                    \
+// Tile variants: _t<BM>x<BN> on 4 (128 x 128) or 8 waves; LDS is static.
+#define GEMM_MFMA(name, T, O, BM, BN, WMN, WNN)                                                   \
+    POPCORN_KERNEL void __launch_bounds__(64 * WMN * WNN)                                         \
         name(const uint16_t *a, const uint16_t *b, O::storage *c, MatmulConstants p) {            \
-        gemm_nt<T, O>(a, b, c, p);                                                                \
+        gemm_nt<T, O, BM, BN, WMN, WNN>(a, b, c, p);                                              \
     }
+#define GEMM_MFMA_TILES(base, T, O)                          \
+    GEMM_MFMA(base##_t128x128, T, O, 128, 128, 2, 2)         \
+    GEMM_MFMA(base##_t256x128, T, O, 256, 128, 4, 2)         \
+    GEMM_MFMA(base##_t128x256, T, O, 128, 256, 2, 4)         \
+    GEMM_MFMA(base##_t256x256, T, O, 256, 256, 2, 4)         \
+    GEMM_MFMA(base##_t256x256w4, T, O, 256, 256, 2, 2)
 
 using pk::BF16;
 using pk::F16;
 using pk::F32;
 
-GEMM_MFMA(matmul_mfma_f16_f16_f16, F16, F16)
-GEMM_MFMA(matmul_mfma_f16_f16_f32, F16, F32)
-GEMM_MFMA(matmul_mfma_bf16_bf16_bf16, BF16, BF16)
-GEMM_MFMA(matmul_mfma_bf16_bf16_f32, BF16, F32)
+GEMM_MFMA_TILES(matmul_mfma_f16_f16_f16, F16, F16)
+GEMM_MFMA_TILES(matmul_mfma_f16_f16_f32, F16, F32)
+GEMM_MFMA_TILES(matmul_mfma_bf16_bf16_bf16, BF16, BF16)
+GEMM_MFMA_TILES(matmul_mfma_bf16_bf16_f32, BF16, F32)

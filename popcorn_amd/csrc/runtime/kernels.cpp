@@ -291,6 +291,30 @@ int64_t streamBlocks(int64_t units) {
     return cdiv(cdiv(units, per), kBlock / 64);
 }
 
+// MFMA GEMM tile shapes (gemm_mfma.hip): BM x BN and the block size.
+struct GemmTile {
+    int bm, bn, threads;
+    const char *suffix;
+};
+
+GemmTile gemmTile(int64_t m, int64_t n) {
+    static const GemmTile tiles[] = {{256, 256, 512, "256x256"}, {256, 256, 256, "256x256w4"},
+                                     {256, 128, 512, "256x128"}, {128, 256, 512, "128x256"},
+                                     {128, 128, 256, "128x128"}};
+    if (const char *e = std::getenv("POPCORN_GEMM_TILE")) {  // tuning override, e.g. "256x128"
+        for (const GemmTile &t : tiles)
+            if (std::string(t.suffix) == e) return t;
+    }
+    // 256 x 256 on 8 waves reuses each LDS stage for twice the MFMA work of
+    // 128 x 128 (measured: 890 vs 730 TFLOP/s on [2048, 3072] x [24576,
+    // 3072]^T) but runs one block per CU, so it only pays when the tiles fill
+    // the CUs several times over; below that the 128 x 128 grid (two blocks
+    // per CU) balances better (QKV [.., 9216]: 183 vs 202 us).
+    const int64_t big = cdiv(m, 256) * cdiv(n, 256);
+    if (big >= 3 * deviceCUs()) return tiles[0];
+    return tiles[4];
+}
+
 constexpr int64_t kMaxStagedK = 16384;  // x staged as f32 in 64 KB of LDS
 
 std::unique_ptr<Kernel> makeMatmul(const Tensor &a, const Tensor &b, const Tensor &c, int64_t m, int64_t k, int64_t n,
@@ -328,9 +352,11 @@ std::unique_ptr<Kernel> makeMatmul(const Tensor &a, const Tensor &b, const Tenso
             (c.dataType == t || c.dataType == DataType::f32) && k % 8 == 0 && k > 0 && aligned16(a.data) &&
             aligned16(b.data)) {
             MatmulConstants mc{(uint32_t)m, (uint32_t)k, (uint32_t)n, 1u};
-            const std::string fn = std::string("matmul_mfma_") + tag(t) + "_" + tag(t) + "_" + tag(c.dataType);
+            const GemmTile tile = gemmTile(m, n);
+            const std::string fn =
+                std::string("matmul_mfma_") + tag(t) + "_" + tag(t) + "_" + tag(c.dataType) + "_t" + tile.suffix;
             return std::make_unique<FixedDispatch>(fn, binds, std::vector<std::vector<uint8_t>>{bytesOf(mc)},
-                                                   grid1(cdiv(m, 128) * cdiv(n, 128), kBlock));
+                                                   grid1(cdiv(m, tile.bm) * cdiv(n, tile.bn), tile.threads));
         }
     }
     std::string fn = plainName("matmul", a.dataType, b.dataType, c.dataType);
