@@ -1,0 +1,217 @@
+// Prefill FlashAttention on the matrix cores (the reference's MPP path,
+// FlashAttention.swift:236-425 and MPPFlashAttention.metal:38-256, whose
+// role this takes; algorithm of FlashAttention.metal:30-167: online softmax
+// over key tiles with posQ = Sk - Sq + q, FlashAttention.metal:72).
+//
+// A block of 4 waves takes 128 query rows of one (batch, query head); wave w
+// owns rows q0 + 32 w .. +32. Per step of 32 keys:
+//  * the block stages K [32 keys x Hd] row-major and V transposed,
+//    Vt [Hd x 32 keys], in LDS;
+//  * each wave computes S^T = K . Q^T (32 keys x 32 queries) with
+//    v_mfma_f32_32x32x16: A = K rows from LDS, B = Q^T from registers (the
+//    wave's Q rows, loaded once). In the C layout (mfma.hpp) lane l then
+//    holds the 16 scores of query l % 32 for keys (i / 4) * 8 + (l / 32) * 4
+//    + i % 4, so the row max and sum are a lane-local max over 16 values and
+//    one exchange with lane l ^ 32;
+//  * P^T (in the input dtype; for bf16 as a high part plus a bf16 remainder,
+//    two products) is already the B operand of
+//    O^T += Vt . P^T for k-step ks if the 16 key slots of the step are read
+//    in the order the C layout holds them: slot (l / 32) * 8 + j is key
+//    16 ks + (j / 4) * 8 + (l / 32) * 4 + j % 4; the A operand (Vt) is read
+//    in that same order, two runs of 4 keys. O^T accumulates per lane for
+//    one query, so the softmax rescale is lane-local too.
+// Causal / sliding-window keys outside the block's range are not visited;
+// the rest are masked per query. Heavy (late) query tiles start first.
+#include <type_traits>
+
+#include "mfma.hpp"
+
+namespace {
+
+using pk::f32x16;
+using pk::Mma;
+using pk::u32x4;
+
+constexpr int kWaves = 4;
+constexpr int BQ = 32 * kWaves;  // query rows per block
+constexpr int BKV = 32;          // keys per step
+
+__device__ inline bool fa_allowed(const MPPFlashAttentionConstants &p, int posQ, int key) {
+    if (key < 0 || key >= (int)p.Sk) return false;
+    bool ok = (p.maskKind == 2u) || (key <= posQ);
+    if (p.maskKind == 1u) ok = ok && (posQ - key < p.slidingWindow);
+    return ok;
+}
+
+template <typename T, typename O, int HD>
+__device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
+                         const uint16_t *__restrict__ V, typename O::storage *__restrict__ out,
+                         const MPPFlashAttentionConstants &p) {
+    constexpr int KS = HD / 16;  // k-steps of S^T = K . Q^T
+    constexpr int DT = HD / 32;  // 32-row tiles of O^T
+    constexpr int LDK = HD + 8;  // sK row (padded, elements)
+    constexpr int LDV = BKV + 8; // sVt row (padded, elements)
+    constexpr int kChunks = BKV * HD / 8;
+    // softmax weights enter P.V in the input dtype; bf16 (8-bit significand)
+    // carries them as a bf16 pair, f16 (11 bits) as one value
+    constexpr bool kSplitP = std::is_same<T, pk::BF16>::value;
+    __shared__ __attribute__((aligned(16))) uint16_t sK[BKV * LDK];
+    __shared__ __attribute__((aligned(16))) uint16_t sV[HD * LDV];
+
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, c32 = lane & 31;
+    const uint32_t nQT = p.qTilesPerHead;
+    const uint32_t qt = nQT - 1 - blockIdx.x % nQT;
+    const uint32_t bh = blockIdx.x / nQT;  // b * Nq + hq
+    const uint32_t b = bh / p.Nq, hq = bh % p.Nq;
+    const uint32_t hkv = hq / (p.Nq / p.Nkv);
+    const uint32_t stride = p.kvStride ? p.kvStride : p.Sk;
+    const uint16_t *Qh = Q + (uint64_t)bh * p.Sq * HD;
+    const uint64_t kvoff = (uint64_t)(b * p.Nkv + hkv) * stride * HD;
+    const uint16_t *Kh = K + kvoff;
+    const uint16_t *Vh = V + kvoff;
+    const uint32_t myq = qt * BQ + wave * 32 + c32;
+    const int posQ = (int)p.Sk - (int)p.Sq + (int)myq;
+
+    u32x4 qf[KS];
+    {
+        const uint16_t *qrow = Qh + (uint64_t)min(myq, p.Sq - 1) * HD + h * 8;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) qf[s] = *reinterpret_cast<const u32x4 *>(qrow + s * 16);
+    }
+    f32x16 acc[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[dt][i] = 0.0f;
+    float m = -INFINITY, l = 0.0f;
+
+    // keys any query of the block may see
+    const int first = (int)p.Sk - (int)p.Sq + (int)(qt * BQ);
+    const int last = (int)p.Sk - (int)p.Sq + (int)min(qt * BQ + BQ - 1, p.Sq - 1);
+    int kLo = 0, kHi = (int)p.Sk;
+    if (p.maskKind != 2u) kHi = min(kHi, last + 1);
+    if (p.maskKind == 1u) kLo = max(0, first - p.slidingWindow + 1);
+    const uint32_t nSteps = kHi > kLo ? (uint32_t)(kHi - kLo + BKV - 1) / BKV : 0u;
+
+    for (uint32_t it = 0; it < nSteps; ++it) {
+        const uint32_t k0 = (uint32_t)kLo + it * BKV;
+        __syncthreads();  // the previous step's readers are done
+        for (uint32_t c = threadIdx.x; c < (uint32_t)kChunks; c += 64 * kWaves) {
+            const uint32_t key = c / (HD / 8), dc = (c % (HD / 8)) * 8;
+            const uint32_t kk = min(k0 + key, p.Sk - 1);
+            *reinterpret_cast<u32x4 *>(&sK[key * LDK + dc]) = *reinterpret_cast<const u32x4 *>(Kh + (uint64_t)kk * HD + dc);
+        }
+        for (uint32_t c = threadIdx.x; c < (uint32_t)kChunks; c += 64 * kWaves) {
+            const uint32_t key = c % BKV, dc = (c / BKV) * 8;
+            const uint32_t kk = min(k0 + key, p.Sk - 1);
+            const u32x4 v = *reinterpret_cast<const u32x4 *>(Vh + (uint64_t)kk * HD + dc);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t w = v[j];
+                sV[(dc + 2 * j) * LDV + key] = (uint16_t)(w & 0xffffu);
+                sV[(dc + 2 * j + 1) * LDV + key] = (uint16_t)(w >> 16);
+            }
+        }
+        __syncthreads();
+
+        f32x16 st;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) st[i] = 0.0f;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            const u32x4 a = *reinterpret_cast<const u32x4 *>(&sK[c32 * LDK + s * 16 + h * 8]);
+            st = Mma<T>::run(a, qf[s], st);
+        }
+        float sv[16];
+        float mt = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int key = (int)k0 + (i >> 2) * 8 + (int)h * 4 + (i & 3);
+            sv[i] = fa_allowed(p, posQ, key) ? st[i] * p.scale : -INFINITY;
+            mt = fmaxf(mt, sv[i]);
+        }
+        mt = fmaxf(mt, pk::swap32(mt));
+        const float mn = fmaxf(m, mt);
+        float alpha = 1.0f, ps = 0.0f;
+        uint32_t pb[16], pr[16];
+        if (mn == -INFINITY) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) pb[i] = pr[i] = 0u;
+        } else {
+            alpha = pk::fast_exp(m - mn);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float pv = pk::fast_exp(sv[i] - mn);
+                pb[i] = pk::bits16<T>(pv);
+                float w = pk::from_bits16<T>(pb[i]);
+                if constexpr (kSplitP) {
+                    // bf16 keeps 8 bits: the remainder goes in a second product
+                    pr[i] = pk::bits16<T>(pv - w);
+                    w += pk::from_bits16<T>(pr[i]);
+                } else {
+                    pr[i] = 0u;
+                }
+                ps += w;  // the weight the MFMAs apply
+            }
+        }
+        ps += pk::swap32(ps);
+        l = l * alpha + ps;
+        m = mn;
+        u32x4 pf[2], pfr[2];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                pf[ks][j] = pb[ks * 8 + 2 * j] | (pb[ks * 8 + 2 * j + 1] << 16);
+                pfr[ks][j] = pr[ks * 8 + 2 * j] | (pr[ks * 8 + 2 * j + 1] << 16);
+            }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[dt][i] *= alpha;
+            const uint16_t *vrow = &sV[(dt * 32 + c32) * LDV];
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                const uint2 lo = *reinterpret_cast<const uint2 *>(vrow + ks * 16 + h * 4);
+                const uint2 hi = *reinterpret_cast<const uint2 *>(vrow + ks * 16 + 8 + h * 4);
+                const u32x4 a = {lo.x, lo.y, hi.x, hi.y};
+                acc[dt] = Mma<T>::run(a, pf[ks], acc[dt]);
+                if constexpr (kSplitP) acc[dt] = Mma<T>::run(a, pfr[ks], acc[dt]);
+            }
+        }
+    }
+
+    if (myq >= p.Sq) return;
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    typename O::storage *orow = out + ((uint64_t)bh * p.Sq + myq) * HD;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const uint32_t d = dt * 32 + (i >> 2) * 8 + h * 4 + (i & 3);
+            orow[d] = O::store(acc[dt][i] * inv);
+        }
+    }
+}
+
+}  // namespace
+
+#define FA_TILED(name, T, O, HD)                                                                       \
+    POPCORN_KERNEL void __launch_bounds__(256)                                                         \
+        name(const uint16_t *q, const uint16_t *k, const uint16_t *v, O::storage *out,                 \
+             MPPFlashAttentionConstants p) {                                                           \
+        fa_tiled<T, O, HD>(q, k, v, out, p);                                                           \
+    }
+#define FA_TILED_D(t, T, o, O)                                   \
+    FA_TILED(flash_attention_tiled_##t##_##o##_d64, T, O, 64)    \
+    FA_TILED(flash_attention_tiled_##t##_##o##_d128, T, O, 128)  \
+    FA_TILED(flash_attention_tiled_##t##_##o##_d256, T, O, 256)
+
+using pk::BF16;
+using pk::F16;
+using pk::F32;
+
+FA_TILED_D(f16, F16, f16, F16)
+FA_TILED_D(f16, F16, f32, F32)
+FA_TILED_D(bf16, BF16, bf16, BF16)
+FA_TILED_D(bf16, BF16, f32, F32)

@@ -3,11 +3,8 @@
 // MPPMatmul.metal:19-91, whose MPP tiles this replaces), f16 or bf16 inputs,
 // f32 accumulation, output f32 or the input dtype (popcorn_store rounding).
 //
-// v_mfma_f32_32x32x16_{f16,bf16} lane layout (checked on gfx950):
-//   A fragment: lane l holds A[l % 32][(l / 32) * 8 + i], i < 8
-//   B fragment: lane l holds B[(l / 32) * 8 + i][l % 32]  (= Bt[l % 32][...])
-//   C: lane l, element i is C[(i / 4) * 8 + (l / 32) * 4 + i % 4][l % 32]
-// so both operands are 16-byte runs along K of a row of A or of Bt.
+// With the MFMA lane layout of mfma.hpp both operands are 16-byte runs
+// along K of a row of A or of Bt.
 //
 // A block computes a BM x BN tile (128 or 256 each; 4 or 8 waves, each wave
 // a 64 x 64 or 128 x 64 piece of 32 x 32 MFMA tiles; the host picks the tile
@@ -19,31 +16,13 @@
 // are dealt round-robin to the 8 XCDs, so block b runs on XCD b % 8) and,
 // within an XCD's range, in groups of 8 tile rows, so the A and B panels a
 // group shares stay in that XCD's L2.
-#include "common.hpp"
+#include "mfma.hpp"
 
 namespace {
 
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf168 __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-template <typename T>
-struct Mma;
-template <>
-struct Mma<pk::F16> {
-    __device__ static inline f32x16 run(u32x4 a, u32x4 b, f32x16 c) {
-        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0,
-                                                      0, 0);
-    }
-};
-template <>
-struct Mma<pk::BF16> {
-    __device__ static inline f32x16 run(u32x4 a, u32x4 b, f32x16 c) {
-        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf168, a), __builtin_bit_cast(bf168, b), c,
-                                                       0, 0, 0);
-    }
-};
+using pk::f32x16;
+using pk::Mma;
+using pk::u32x4;
 
 constexpr int BK = 64;
 constexpr int LDK = BK + 8;  // padded LDS row, in elements

@@ -1,0 +1,58 @@
+// CDNA4 matrix-core helpers: v_mfma_f32_32x32x16_{f16,bf16} on 16-byte
+// fragments. Lane layout (checked on gfx950 against an exact integer
+// product), for C[32 x 32] += A[32 x 16] . B[16 x 32]:
+//   A fragment: lane l holds A[l % 32][(l / 32) * 8 + i], i < 8
+//   B fragment: lane l holds B[(l / 32) * 8 + i][l % 32]
+//   C (16 floats): lane l, element i is C[(i / 4) * 8 + (l / 32) * 4 + i % 4][l % 32]
+#pragma once
+
+#include "common.hpp"
+
+namespace pk {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf168 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+template <typename T>
+struct Mma;
+template <>
+struct Mma<F16> {
+    __device__ static inline f32x16 run(u32x4 a, u32x4 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0,
+                                                      0, 0);
+    }
+};
+template <>
+struct Mma<BF16> {
+    __device__ static inline f32x16 run(u32x4 a, u32x4 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf168, a), __builtin_bit_cast(bf168, b), c,
+                                                       0, 0, 0);
+    }
+};
+
+// 16-bit storage bits of x in T (f16 IEEE RNE; bf16 the reference's formula).
+template <typename T>
+__device__ inline uint32_t bits16(float x);
+template <>
+__device__ inline uint32_t bits16<F16>(float x) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, F16::store(x));
+}
+template <>
+__device__ inline uint32_t bits16<BF16>(float x) {
+    return (uint32_t)BF16::store(x);
+}
+
+// f32 value of 16-bit storage bits in T.
+template <typename T>
+__device__ inline float from_bits16(uint32_t b);
+template <>
+__device__ inline float from_bits16<F16>(uint32_t b) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)b);
+}
+template <>
+__device__ inline float from_bits16<BF16>(uint32_t b) {
+    return BF16::load((uint16_t)b);
+}
+
+}  // namespace pk

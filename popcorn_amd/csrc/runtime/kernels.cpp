@@ -126,6 +126,15 @@ public:
             requireElements(pos_, 1, "position");
         }
         path_ = Kernels::route(d.Sq, d.Hd, q.dataType);
+        // the tiled kernel reads Q/K/V as 16-byte runs and takes a fixed key
+        // length (no device-side position)
+        if (path_ == Kernels::AttentionPath::tiled &&
+            (hasPos_ || !aligned16(q.data) || !aligned16(k.data) || !aligned16(v.data) ||
+             !(out.dataType == q.dataType || out.dataType == DataType::f32)))
+            path_ = Kernels::AttentionPath::plain;
+        if (path_ == Kernels::AttentionPath::tiled)
+            tiledName_ = std::string("flash_attention_tiled_") + tag(q.dataType) + "_" + tag(out.dataType) + "_d" +
+                         std::to_string(d.Hd);
         planSplit();
     }
 
@@ -135,9 +144,31 @@ public:
         return b;
     }
 
-    std::string describe() const override { return partialName_ + "," + reduceName_; }
+    std::string describe() const override {
+        return path_ == Kernels::AttentionPath::tiled ? tiledName_ : partialName_ + "," + reduceName_;
+    }
 
     void encode(KernelCommandEncoder &enc) const override {
+        if (path_ == Kernels::AttentionPath::tiled) {
+            // MPPFlashAttentionConstants (PopcornKernelTypes.h:133-144): one
+            // block per 128 query rows of each (batch, query head)
+            MPPFlashAttentionConstants c{};
+            c.B = (uint32_t)d_.B;
+            c.Nq = (uint32_t)d_.Nq;
+            c.Nkv = (uint32_t)d_.Nkv;
+            c.Sq = (uint32_t)d_.Sq;
+            c.Sk = (uint32_t)d_.Sk;
+            c.Hd = (uint32_t)d_.Hd;
+            c.qTilesPerHead = (uint32_t)cdiv(d_.Sq, 128);
+            c.maskKind = mask_.kind;
+            c.slidingWindow = mask_.kind == 1 ? mask_.window : -1;
+            c.scale = scale_;
+            c.kvStride = (uint32_t)d_.cap;
+            FixedDispatch fa(tiledName_, {{q_, kRead}, {k_, kRead}, {v_, kRead}, {out_, kWrite}}, {bytesOf(c)},
+                             grid1(d_.B * d_.Nq * (int64_t)c.qTilesPerHead, kBlock));
+            enc.dispatch(fa);
+            return;
+        }
         // FlashDecoding.swift:54-73: borrow partial O, m, l; partial; combine.
         const int64_t slots = d_.B * d_.Nq * d_.Sq * P_;
         enc.withTemporaryTensor(ScratchSpec{{slots, d_.Hd}, DataType::f32}, [&](Tensor pO) {
@@ -228,7 +259,7 @@ private:
     AttentionMask mask_;
     bool hasPos_;
     Kernels::AttentionPath path_ = Kernels::AttentionPath::plain;
-    std::string partialName_, reduceName_;
+    std::string partialName_, reduceName_, tiledName_;
     int64_t ngroups_ = 1, P_ = 1;
 };
 
@@ -541,10 +572,14 @@ namespace Kernels {
 
 // FlashAttention.swift:109-113. `tiled` (MFMA prefill) takes the MPP path's
 // place once it exists for the dtype and head dim; until then plain.
+// FlashAttention.swift:109-113: one query row -> split-KV decoding; 32 rows
+// or more of 16-bit data with a head dim the MFMA kernel has (64, 128, 256)
+// -> the tiled kernel (where the reference takes MPP); otherwise the plain
+// per-row kernel.
 AttentionPath route(int64_t queryLen, int64_t headDim, DataType qType) {
-    (void)headDim;
-    (void)qType;
     if (queryLen == 1) return AttentionPath::decoding;
+    const bool sixteen = qType == DataType::f16 || qType == DataType::bf16;
+    if (queryLen >= 32 && sixteen && (headDim == 64 || headDim == 128 || headDim == 256)) return AttentionPath::tiled;
     return AttentionPath::plain;
 }
 

@@ -197,3 +197,16 @@ def test_decode_matvec_routing():
     with pytest.raises(E) as e:  # the residual output may not alias x
         pa.Kernels.DecodeMatvec(x, w, T([4096]), delta=T([2304]), w_post=norm, x_out=x)
     assert e.value.code == E.INVALID_ARGUMENT
+
+
+def test_prefill_routes_to_tiled():
+    # FlashAttention.swift:109-113 with the MFMA kernel in the MPP role
+    assert pa.Kernels.route(2048, 256, "f16") == "tiled"
+    assert pa.Kernels.route(32, 64, "bf16") == "tiled"
+    assert pa.Kernels.route(31, 64, "bf16") == "plain"
+    assert pa.Kernels.route(2048, 80, "f16") == "plain"
+    assert pa.Kernels.route(2048, 256, "f32") == "plain"
+    assert pa.Kernels.route(1, 256, "f16") == "decoding"
+    q = T([1, 16, 2048, 256], "f16")
+    k = pa.Kernels.FlashAttention(q, q, q, out=T([1, 16, 2048, 256], "f16", ptr=FAKE + 2 ** 32), scale=1 / 16)
+    assert k.function_names == ["flash_attention_tiled_f16_f16_d256"]

@@ -72,3 +72,69 @@ def test_mfma_matmul_config5_shapes_sampled(env, M, K, N):
     got = download(c, stream).reshape(M, N)[rows]
     ref = O.matmul(a, b, len(rows), K, N, True).reshape(len(rows), N)
     assert_out(got, ref, EPS["f16"], "f16", f"config5 {M}x{K}x{N}")
+
+
+# ---- tiled (MFMA) FlashAttention prefill ---------------------------------------
+
+def _attend(env, q, k, v, dtype, out_dtype, scale, mask):
+    pa, lib, stream, enc = env
+    B, Nq, Sq, Hd = q.shape
+    Nkv, cap = k.shape[1], k.shape[2]
+    to = pa.Tensor.empty([B, Nq, Sq, Hd], out_dtype)
+    kern = pa.Kernels.FlashAttention(upload(pa, q, dtype), upload(pa, k, dtype), upload(pa, v, dtype), out=to,
+                                     scale=scale, mask=mask, batch=B, query_heads=Nq, kv_heads=Nkv, query_len=Sq,
+                                     key_len=cap, head_dim=Hd)
+    enc.encode(kern)
+    stream.synchronize()
+    return download(to, stream), kern
+
+
+MASKS = {"causal": (0, -1), "bidirectional": (2, -1), "window40": (1, 40)}
+
+
+@pytest.mark.parametrize("dtype,ot", [("f16", "f16"), ("f16", "f32"), ("bf16", "bf16"), ("bf16", "f32")])
+@pytest.mark.parametrize("B,Nq,Nkv,Sq,Sk,Hd,mask", [
+    (1, 2, 1, 64, 64, 64, "causal"),
+    (2, 4, 2, 130, 200, 128, "causal"),        # Sq < Sk: posQ = Sk - Sq + i; ragged tiles
+    (1, 2, 2, 96, 96, 256, "bidirectional"),
+    (1, 2, 1, 128, 160, 64, "window40"),
+    (1, 1, 1, 32, 32, 256, "causal"),
+])
+def test_tiled_attention_vs_oracle(env, dtype, ot, B, Nq, Nkv, Sq, Sk, Hd, mask):
+    pa = env[0]
+    kind, window = MASKS[mask]
+    q = rounded(O.normal(Sq + Hd, (B, Nq, Sq, Hd)), dtype)
+    k = rounded(O.normal(Sk + Hd + 1, (B, Nkv, Sk, Hd)), dtype)
+    v = rounded(O.normal(Sk + Hd + 2, (B, Nkv, Sk, Hd)), dtype)
+    pm = pa.AttentionMask(kind, window)
+    scale = 1 / np.sqrt(Hd)
+    got, kern = _attend(env, q, k, v, dtype, ot, scale, pm)
+    assert kern.function_names == [f"flash_attention_tiled_{dtype}_{ot}_d{Hd}"]
+    ref = O.attention_naive(q, k, v, scale, mask_kind=kind, window=window)
+    assert not np.isnan(got).any()
+    # softmax weights enter the P.V product in the input dtype (the matrix
+    # cores multiply 16-bit operands: f16 rounds them to 11 bits, bf16 carries
+    # a high part and a remainder); the normaliser sums the same weights
+    assert_out(got, ref, EPS[dtype], ot, f"tiled attention {dtype}->{ot} {mask} Sq={Sq} Sk={Sk} Hd={Hd}")
+
+
+def test_tiled_attention_config5_sampled(env):
+    # BASELINE config 5 attention: [1, 16, 2048, 256] f16, causal, scale 1/16.
+    # A sampled query row r is checked as a single-row query over keys 0..r
+    # (the same posQ = r), against the oracle.
+    pa, lib, stream, enc = env
+    H, S, Hd = 16, 2048, 256
+    tq, tk, tv = (pa.Tensor.empty([1, H, S, Hd], "f16") for _ in range(3))
+    for i, t in enumerate((tq, tk, tv)):
+        lib.fill_normal(t, 40 + i, stream=stream)
+    to = pa.Tensor.empty([1, H, S, Hd], "f16")
+    kern = pa.Kernels.FlashAttention(tq, tk, tv, out=to, scale=1 / 16, batch=1, query_heads=H, kv_heads=H,
+                                     query_len=S, key_len=S, head_dim=Hd)
+    assert kern.function_names == ["flash_attention_tiled_f16_f16_d256"]
+    enc.encode(kern)
+    stream.synchronize()
+    q, k, v = (download(t, stream).reshape(1, H, S, Hd) for t in (tq, tk, tv))
+    got = download(to, stream).reshape(1, H, S, Hd)
+    for r in (0, 1, 127, 128, 1000, 2047):
+        ref = O.attention_naive(q[:, :, r:r + 1], k[:, :, :r + 1].copy(), v[:, :, :r + 1].copy(), 1 / 16)
+        assert_out(got[:, :, r:r + 1], ref, EPS["f16"], "f16", f"config5 row {r}")
