@@ -50,7 +50,7 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
     constexpr int KS = HD / 16;  // k-steps of S^T = K . Q^T
     constexpr int DT = HD / 32;  // 32-row tiles of O^T
     constexpr int LDK = HD + 8;  // sK row (padded, elements)
-    constexpr int LDV = BKV + 8; // sVt row (padded, elements)
+    constexpr int LDV = BKV + 4; // sVt row (padded, elements; 72 bytes spread 8-byte reads over the banks)
     constexpr int kChunks = BKV * HD / 8;
     // softmax weights enter P.V in the input dtype; bf16 (8-bit significand)
     // carries them as a bf16 pair, f16 (11 bits) as one value
@@ -93,26 +93,65 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
     if (p.maskKind == 1u) kLo = max(0, first - p.slidingWindow + 1);
     const uint32_t nSteps = kHi > kLo ? (uint32_t)(kHi - kLo + BKV - 1) / BKV : 0u;
 
+    // Staging of one step: K as 16-byte chunks (row-major), V as 4 keys x 8
+    // dims per thread so its transpose is written as 8-byte runs of 4 keys.
+    // A step's global loads go out before the previous step is computed.
+    constexpr int kKC = (kChunks + 64 * kWaves - 1) / (64 * kWaves);
+    constexpr int kVP = (BKV / 4) * (HD / 8);  // (key quad, dim block) pairs
+    constexpr int kVC = (kVP + 64 * kWaves - 1) / (64 * kWaves);
+    u32x4 kr[kKC], vr[kVC][4];
+    auto gload = [&](uint32_t k0) {
+#pragma unroll
+        for (int i = 0; i < kKC; ++i) {
+            const uint32_t c = threadIdx.x + i * 64 * kWaves;
+            if (c < (uint32_t)kChunks) {
+                const uint32_t key = c / (HD / 8), dc = (c % (HD / 8)) * 8;
+                kr[i] = *reinterpret_cast<const u32x4 *>(Kh + (uint64_t)min(k0 + key, p.Sk - 1) * HD + dc);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kVC; ++i) {
+            const uint32_t pr = threadIdx.x + i * 64 * kWaves;
+            if (pr < (uint32_t)kVP) {
+                const uint32_t kq = pr % (BKV / 4), db = pr / (BKV / 4);
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    vr[i][j] = *reinterpret_cast<const u32x4 *>(Vh + (uint64_t)min(k0 + 4 * kq + j, p.Sk - 1) * HD + db * 8);
+            }
+        }
+    };
+    auto lstore = [&]() {
+#pragma unroll
+        for (int i = 0; i < kKC; ++i) {
+            const uint32_t c = threadIdx.x + i * 64 * kWaves;
+            if (c < (uint32_t)kChunks) {
+                const uint32_t key = c / (HD / 8), dc = (c % (HD / 8)) * 8;
+                *reinterpret_cast<u32x4 *>(&sK[key * LDK + dc]) = kr[i];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kVC; ++i) {
+            const uint32_t pr = threadIdx.x + i * 64 * kWaves;
+            if (pr < (uint32_t)kVP) {
+                const uint32_t kq = pr % (BKV / 4), db = pr / (BKV / 4);
+#pragma unroll
+                for (int d = 0; d < 8; ++d) {
+                    const int sh = (d & 1) * 16;
+                    const uint32_t w0 = (vr[i][0][d >> 1] >> sh) & 0xffffu, w1 = (vr[i][1][d >> 1] >> sh) & 0xffffu;
+                    const uint32_t w2 = (vr[i][2][d >> 1] >> sh) & 0xffffu, w3 = (vr[i][3][d >> 1] >> sh) & 0xffffu;
+                    *reinterpret_cast<uint2 *>(&sV[(db * 8 + d) * LDV + 4 * kq]) = uint2{w0 | (w1 << 16), w2 | (w3 << 16)};
+                }
+            }
+        }
+    };
+
+    if (nSteps > 0) gload((uint32_t)kLo);
     for (uint32_t it = 0; it < nSteps; ++it) {
         const uint32_t k0 = (uint32_t)kLo + it * BKV;
         __syncthreads();  // the previous step's readers are done
-        for (uint32_t c = threadIdx.x; c < (uint32_t)kChunks; c += 64 * kWaves) {
-            const uint32_t key = c / (HD / 8), dc = (c % (HD / 8)) * 8;
-            const uint32_t kk = min(k0 + key, p.Sk - 1);
-            *reinterpret_cast<u32x4 *>(&sK[key * LDK + dc]) = *reinterpret_cast<const u32x4 *>(Kh + (uint64_t)kk * HD + dc);
-        }
-        for (uint32_t c = threadIdx.x; c < (uint32_t)kChunks; c += 64 * kWaves) {
-            const uint32_t key = c % BKV, dc = (c / BKV) * 8;
-            const uint32_t kk = min(k0 + key, p.Sk - 1);
-            const u32x4 v = *reinterpret_cast<const u32x4 *>(Vh + (uint64_t)kk * HD + dc);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint32_t w = v[j];
-                sV[(dc + 2 * j) * LDV + key] = (uint16_t)(w & 0xffffu);
-                sV[(dc + 2 * j + 1) * LDV + key] = (uint16_t)(w >> 16);
-            }
-        }
+        lstore();
         __syncthreads();
+        if (it + 1 < nSteps) gload(k0 + BKV);
 
         f32x16 st;
 #pragma unroll
