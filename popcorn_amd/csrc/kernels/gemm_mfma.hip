@@ -158,6 +158,131 @@ __device__ void gemm_nt(const uint16_t *__restrict__ A, const uint16_t *__restri
     }
 }
 
+// ---- direct-to-LDS pipeline ----------------------------------------------------
+// The same tile product with the operand tiles copied global -> LDS by
+// global_load_lds_dwordx4 (lane l of a wave instruction writes 16 bytes at
+// M0 + 16 l, checked on gfx950), kStagesD stages of BKD = 32 in flight and
+// no staging registers. A stage holds BM + BN rows of 64 bytes (4 chunks);
+// chunk kc of row r sits in slot kc ^ ((r >> 2) & 3), so the 16 rows a
+// fragment read touches (lanes 16 at a time) fall in 16 distinct 4-bank
+// groups. Needs K % 32 == 0 (a chunk past K cannot be zero-filled here).
+constexpr int BKD = 32;
+constexpr int kStagesD = 4;
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+template <int N>
+__device__ inline void wait_vmcnt() {
+    // s_waitcnt vmcnt(N), expcnt and lgkmcnt left at their maximum (no wait)
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <typename T, typename O, int BM, int BN, int WM_N, int WN_N>
+__device__ void gemm_nt_direct(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
+                               typename O::storage *__restrict__ C, const MatmulConstants &p) {
+    constexpr int NW = WM_N * WN_N;
+    constexpr int WM = BM / WM_N, WN = BN / WN_N;
+    constexpr int TM = WM / 32, TN = WN / 32;
+    constexpr int kRowB = BKD * 2;                 // bytes per LDS row
+    constexpr int kStageB = (BM + BN) * kRowB;     // bytes per stage
+    constexpr int kInstA = BM / (16 * NW), kInstB = BN / (16 * NW);  // wave instructions per stage
+    constexpr int kLPS = kInstA + kInstB;          // loads per stage per wave
+    static_assert(kInstA * 16 * NW == BM && kInstB * 16 * NW == BN, "tile rows / waves");
+    __shared__ __attribute__((aligned(16))) uint8_t smem[kStagesD * kStageB];
+
+    const uint32_t M = p.M, N = p.N, K = p.K;
+    const uint32_t nM = (M + BM - 1) / BM, nN = (N + BN - 1) / BN;
+    uint32_t pm, pn;
+    tile_of(blockIdx.x, nM, nN, pm, pn);
+    const uint32_t bm = pm * BM, bn = pn * BN;
+    const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t wm = (wave / WN_N) * WM, wn = (wave % WN_N) * WN;
+
+    // this lane's source rows / chunk for each of its wave's instructions
+    const uint32_t lr = lane >> 2, lpos = lane & 3;
+    auto issue = [&](uint32_t kt) {
+        const uint32_t k0 = kt * BKD;
+        uint8_t *stage = smem + (kt % kStagesD) * kStageB;
+#pragma unroll
+        for (int i = 0; i < kInstA; ++i) {
+            const uint32_t r0 = (i * NW + wave) * 16, r = r0 + lr;
+            const uint32_t kc = lpos ^ ((r >> 2) & 3);
+            const uint16_t *src = A + (uint64_t)min(bm + r, M - 1) * K + k0 + kc * 8;
+            __builtin_amdgcn_global_load_lds(src, (lds_void *)(stage + r0 * kRowB), 16, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < kInstB; ++i) {
+            const uint32_t r0 = (i * NW + wave) * 16, r = r0 + lr;
+            const uint32_t kc = lpos ^ ((r >> 2) & 3);
+            const uint16_t *src = B + (uint64_t)min(bn + r, N - 1) * K + k0 + kc * 8;
+            __builtin_amdgcn_global_load_lds(src, (lds_void *)(stage + (BM + r0) * kRowB), 16, 0, 0);
+        }
+    };
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int mi = 0; mi < TM; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < TN; ++ni)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[mi][ni][i] = 0.0f;
+
+    auto frag = [&](const uint8_t *base, uint32_t row, uint32_t kc) {
+        return *reinterpret_cast<const u32x4 *>(base + row * kRowB + ((kc ^ ((row >> 2) & 3)) << 4));
+    };
+    auto compute = [&](uint32_t kt) {
+        const uint8_t *stage = smem + (kt % kStagesD) * kStageB;
+#pragma unroll
+        for (int kk = 0; kk < BKD / 16; ++kk) {
+            const uint32_t kc = kk * 2 + (lane >> 5);
+            u32x4 fa[TM], fb[TN];
+#pragma unroll
+            for (int mi = 0; mi < TM; ++mi) fa[mi] = frag(stage, wm + mi * 32 + (lane & 31), kc);
+#pragma unroll
+            for (int ni = 0; ni < TN; ++ni) fb[ni] = frag(stage + BM * kRowB, wn + ni * 32 + (lane & 31), kc);
+#pragma unroll
+            for (int mi = 0; mi < TM; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < TN; ++ni) acc[mi][ni] = Mma<T>::run(fa[mi], fb[ni], acc[mi][ni]);
+        }
+    };
+
+    const uint32_t nk = K / BKD;
+#pragma unroll
+    for (int s = 0; s < kStagesD - 1; ++s)
+        if ((uint32_t)s < nk) issue(s);
+    for (uint32_t kt = 0; kt < nk; ++kt) {
+        // stage kt has landed once at most (stages issued after it) x kLPS of
+        // this wave's loads are outstanding; the barrier publishes every
+        // wave's copies and retires the readers of the buffer refilled below
+        const uint32_t after = min((uint32_t)(kStagesD - 2), nk - 1 - kt);
+        if (after >= 2) wait_vmcnt<2 * kLPS>();
+        else if (after == 1) wait_vmcnt<kLPS>();
+        else wait_vmcnt<0>();
+        // a bare barrier: this wave's copies of stage kt have landed (the
+        // wait above) and its reads of the buffer refilled next were consumed
+        // by last step's MFMAs; __syncthreads() would also drain the copies
+        // still in flight
+        __builtin_amdgcn_s_barrier();
+        if (kt + kStagesD - 1 < nk) issue(kt + kStagesD - 1);
+        compute(kt);
+    }
+
+#pragma unroll
+    for (int mi = 0; mi < TM; ++mi) {
+#pragma unroll
+        for (int ni = 0; ni < TN; ++ni) {
+            const uint32_t col = bn + wn + ni * 32 + (lane & 31);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const uint32_t row = bm + wm + mi * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+                if (row < M && col < N) C[(uint64_t)row * N + col] = O::store(acc[mi][ni][i]);
+            }
+        }
+    }
+}
+
 }  // namespace
 
 // A, B: 16-bit storage; the host requires K % 8 == 0 and 16-byte aligned A, B.
@@ -167,7 +292,14 @@ __device__ void gemm_nt(const uint16_t *__restrict__ A, const uint16_t *__restri
         name(const uint16_t *a, const uint16_t *b, O::storage *c, MatmulConstants p) {            \
         gemm_nt<T, O, BM, BN, WMN, WNN>(a, b, c, p);                                              \
     }
+#define GEMM_MFMA_D(name, T, O, BM, BN, WMN, WNN)                                                 \
+    POPCORN_KERNEL void __launch_bounds__(64 * WMN * WNN)                                         \
+        name(const uint16_t *a, const uint16_t *b, O::storage *c, MatmulConstants p) {            \
+        gemm_nt_direct<T, O, BM, BN, WMN, WNN>(a, b, c, p);                                       \
+    }
 #define GEMM_MFMA_TILES(base, T, O)                          \
+    GEMM_MFMA_D(base##_d256x256, T, O, 256, 256, 2, 4)       \
+    GEMM_MFMA_D(base##_d128x128, T, O, 128, 128, 2, 2)       \
     GEMM_MFMA(base##_t128x128, T, O, 128, 128, 2, 2)         \
     GEMM_MFMA(base##_t256x128, T, O, 256, 128, 4, 2)         \
     GEMM_MFMA(base##_t128x256, T, O, 128, 256, 2, 4)         \

@@ -328,22 +328,29 @@ struct GemmTile {
     const char *suffix;
 };
 
-GemmTile gemmTile(int64_t m, int64_t n) {
-    static const GemmTile tiles[] = {{256, 256, 512, "256x256"}, {256, 256, 256, "256x256w4"},
-                                     {256, 128, 512, "256x128"}, {128, 256, 512, "128x256"},
-                                     {128, 128, 256, "128x128"}};
-    if (const char *e = std::getenv("POPCORN_GEMM_TILE")) {  // tuning override, e.g. "256x128"
+// "d" tiles copy operands global -> LDS directly (4 stages of K 32); they
+// need K % 32 == 0.
+GemmTile gemmTile(int64_t m, int64_t n, int64_t k) {
+    static const GemmTile tiles[] = {{256, 256, 512, "t256x256"}, {256, 256, 256, "t256x256w4"},
+                                     {256, 128, 512, "t256x128"}, {128, 256, 512, "t128x256"},
+                                     {128, 128, 256, "t128x128"}, {256, 256, 512, "d256x256"},
+                                     {128, 128, 256, "d128x128"}};
+    if (const char *e = std::getenv("POPCORN_GEMM_TILE")) {  // tuning override, e.g. "t256x128"
         for (const GemmTile &t : tiles)
-            if (std::string(t.suffix) == e) return t;
+            if (std::string(t.suffix) == e && (t.suffix[0] != 'd' || k % 32 == 0)) return t;
     }
     // 256 x 256 on 8 waves reuses each LDS stage for twice the MFMA work of
-    // 128 x 128 (measured: 890 vs 730 TFLOP/s on [2048, 3072] x [24576,
-    // 3072]^T) but runs one block per CU, so it only pays when the tiles fill
-    // the CUs several times over; below that the 128 x 128 grid (two blocks
-    // per CU) balances better (QKV [.., 9216]: 183 vs 202 us).
-    const int64_t big = cdiv(m, 256) * cdiv(n, 256);
-    if (big >= 3 * deviceCUs()) return tiles[0];
-    return tiles[4];
+    // 128 x 128 but runs one block per CU, so it only pays when the tiles
+    // fill the CUs several times over; below that the 128 x 128 grid (two
+    // blocks per CU) balances better. The direct-to-LDS forms beat the
+    // register-staged ones on every config-5 shape (f16, M 2048; us):
+    //                      d256  d128  t256  t128
+    //   QKV  N 9216  K 3072   177   162   203   186
+    //   gate N 24576 K 3072   319   422   375   431
+    //   down N 3072  K 24576  589   430   712   485
+    const bool big = cdiv(m, 256) * cdiv(n, 256) >= 3 * deviceCUs();
+    if (k % 32 == 0) return big ? tiles[5] : tiles[6];
+    return big ? tiles[0] : tiles[4];
 }
 
 constexpr int64_t kMaxStagedK = 16384;  // x staged as f32 in 64 KB of LDS
@@ -383,9 +390,9 @@ std::unique_ptr<Kernel> makeMatmul(const Tensor &a, const Tensor &b, const Tenso
             (c.dataType == t || c.dataType == DataType::f32) && k % 8 == 0 && k > 0 && aligned16(a.data) &&
             aligned16(b.data)) {
             MatmulConstants mc{(uint32_t)m, (uint32_t)k, (uint32_t)n, 1u};
-            const GemmTile tile = gemmTile(m, n);
+            const GemmTile tile = gemmTile(m, n, k);
             const std::string fn =
-                std::string("matmul_mfma_") + tag(t) + "_" + tag(t) + "_" + tag(c.dataType) + "_t" + tile.suffix;
+                std::string("matmul_mfma_") + tag(t) + "_" + tag(t) + "_" + tag(c.dataType) + "_" + tile.suffix;
             return std::make_unique<FixedDispatch>(fn, binds, std::vector<std::vector<uint8_t>>{bytesOf(mc)},
                                                    grid1(cdiv(m, tile.bm) * cdiv(n, tile.bn), tile.threads));
         }

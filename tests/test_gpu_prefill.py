@@ -34,7 +34,7 @@ def test_mfma_matmul_vs_oracle(env, at, ot, M, K, N):
     b = rounded(O.normal(N + K, (N, K), std=0.02), at)
     got, k = _gemm(env, a, b, at, ot)
     if M > 1:
-        assert k.function_names[0].startswith(f"matmul_mfma_{at}_{at}_{ot}_t")
+        assert k.function_names[0].startswith(f"matmul_mfma_{at}_{at}_{ot}_")
     ref = O.matmul(a, b, M, K, N, True).reshape(M, N)
     # inputs exact in their dtype, f32 accumulation in another order: 1e-5
     # for f32 outputs, else the 16-bit bar plus the store's rounding
@@ -65,7 +65,7 @@ def test_mfma_matmul_config5_shapes_sampled(env, M, K, N):
     k = pa.Kernels.Matmul(ta, tb, c, True)
     enc.encode(k)
     stream.synchronize()
-    assert k.function_names[0].startswith("matmul_mfma_f16_f16_f16_t")
+    assert k.function_names[0].startswith("matmul_mfma_f16_f16_f16_")
     rows = [0, 1, 127, 128, M // 2 + 3, M - 1]
     a = download(ta, stream).reshape(M, K)[rows]
     b = download(tb, stream).reshape(N, K)
