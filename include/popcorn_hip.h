@@ -310,6 +310,36 @@ popcorn_status_t popcorn_kernel_add(const popcorn_tensor_t *a, const popcorn_ten
 popcorn_status_t popcorn_kernel_scalar_mul(const popcorn_tensor_t *x, float scalar,
                                            const popcorn_tensor_t *out, popcorn_kernel_t *kernel);
 
+/* Kernels.RopeBuildCosSin(positions:invFreq:cosOut:sinOut:attentionScaling:)
+ * (RopeBuildCosSin.swift:30-50) and the explicit init (:8-28): positions i32
+ * [T], inv_freq f32 [Hd/2] -> cos, sin f32 [T, Hd/2] =
+ * cos/sin(float(position) * inv_freq) * attention_scaling. */
+popcorn_status_t popcorn_kernel_rope_build_cos_sin(const popcorn_tensor_t *positions, const popcorn_tensor_t *inv_freq,
+                                                 const popcorn_tensor_t *cos_out, const popcorn_tensor_t *sin_out,
+                                                 float attention_scaling, popcorn_kernel_t *kernel);
+popcorn_status_t popcorn_kernel_rope_build_cos_sin_dims(const popcorn_tensor_t *positions, const popcorn_tensor_t *inv_freq,
+                                                      const popcorn_tensor_t *cos_out, const popcorn_tensor_t *sin_out,
+                                                      int64_t seq_len, int64_t half_head_dim, float attention_scaling,
+                                                      popcorn_kernel_t *kernel);
+
+/* Kernels.RopeApply(_:cos:sin:into:) (RopeApply.swift:46-60) and the explicit
+ * init (:8-44): half-rotation RoPE of x [B, T, Nh, Hd] with tables [T, Hd/2];
+ * (x, table) dtypes (f32, f32), (bf16, bf16) or (bf16, f32), out of x's dtype. */
+popcorn_status_t popcorn_kernel_rope_apply(const popcorn_tensor_t *x, const popcorn_tensor_t *cos_table,
+                                         const popcorn_tensor_t *sin_table, const popcorn_tensor_t *out,
+                                         popcorn_kernel_t *kernel);
+popcorn_status_t popcorn_kernel_rope_apply_dims(const popcorn_tensor_t *x, const popcorn_tensor_t *cos_table,
+                                              const popcorn_tensor_t *sin_table, const popcorn_tensor_t *out, int64_t batch,
+                                              int64_t seq_len, int64_t head_count, int64_t head_dim,
+                                              popcorn_kernel_t *kernel);
+
+/* Kernels.Transpose12(_:into:) (Transpose12.swift:27-35) and the explicit init
+ * (:8-25): [D0, D1, D2, D3] -> [D0, D2, D1, D3] for f32, f16, bf16. */
+popcorn_status_t popcorn_kernel_transpose12(const popcorn_tensor_t *src, const popcorn_tensor_t *out,
+                                          popcorn_kernel_t *kernel);
+popcorn_status_t popcorn_kernel_transpose12_dims(const popcorn_tensor_t *src, const popcorn_tensor_t *out, int64_t d0,
+                                               int64_t d1, int64_t d2, int64_t d3, popcorn_kernel_t *kernel);
+
 /* The gated MLP of Gemma4TextInference.swift:416-429 (RMSNorm -> gate, up ->
  * GeluTanh(gate) * up -> down) as two dispatches: a fused kernel for
  * everything up to the gated product, then the down matvec. No single

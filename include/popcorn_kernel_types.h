@@ -146,6 +146,30 @@ typedef struct {
     uint32_t offsetFromPosition;
 } KVCacheWriteConstants;
 
+/* PopcornKernelTypes.h:174-178: RoPE tables for T positions and Hd2 = Hd/2
+ * frequencies, both scaled by `scaling`. */
+typedef struct {
+    uint32_t T;
+    uint32_t Hd2;
+    float scaling;
+} RopeBuildCosSinConstants;
+
+/* PopcornKernelTypes.h:180-185: half-rotation RoPE over x [B, T, Nh, 2*Hd2]. */
+typedef struct {
+    uint32_t B;
+    uint32_t T;
+    uint32_t Nh;
+    uint32_t Hd2;
+} RopeApplyConstants;
+
+/* PopcornKernelTypes.h:216-221: [D0, D1, D2, D3] -> [D0, D2, D1, D3]. */
+typedef struct {
+    uint32_t D0;
+    uint32_t D1;
+    uint32_t D2;
+    uint32_t D3;
+} Transpose12Constants;
+
 /* PopcornKernelTypes.h:197-200, plus slices: the number of row slices the
  * two-stage argmax splits each row into (stage 1 grid width). */
 typedef struct {

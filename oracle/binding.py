@@ -68,6 +68,9 @@ def lib():
             C.c_float, C.c_uint32, C.c_int32, _fp, _fp, _fp]
         L.oracle_flash_attention_rows.argtypes = [_fp, _fp, _fp, _fp] + [C.c_uint32] * 8 + [
             C.c_float, C.c_uint32, C.c_int32]
+        L.oracle_rope_build_cos_sin.argtypes = [_i32p, _fp, _fp, _fp, C.c_uint32, C.c_uint32, C.c_float]
+        L.oracle_rope_apply.argtypes = [_fp, _fp, _fp, _fp] + [C.c_uint32] * 4
+        L.oracle_transpose12.argtypes = [_fp, _fp] + [C.c_uint32] * 4
         L.oracle_argmax.argtypes = [_fp, C.c_size_t, C.c_size_t, _i32p]
         L.oracle_embedding_gather.argtypes = [_i32p, _fp, _fp, C.c_size_t, C.c_size_t]
         L.oracle_decoder_layer.argtypes = [C.c_void_p, _fp, _fp, _fp, C.c_uint32]
@@ -240,6 +243,35 @@ def flash_attention_rows(q, k, v, scale, Bc=128, mask_kind=0, window=-1, key_len
     out = np.empty_like(q)
     lib().oracle_flash_attention_rows(_p(q), _p(k), _p(v), _p(out), B, Nq, Nkv, Sq, Sk, cap, Hd, Bc,
                                       scale, mask_kind, window)
+    return out
+
+
+def rope_build_cos_sin(positions, inv_freq, scaling=1.0):
+    """positions i32 [T], inv_freq [Hd2] -> (cos, sin) f32 [T, Hd2]."""
+    pos = np.ascontiguousarray(positions, dtype=np.int32).ravel()
+    inv = _f32(inv_freq).ravel()
+    T, Hd2 = pos.size, inv.size
+    c = np.empty((T, Hd2), np.float32)
+    s = np.empty((T, Hd2), np.float32)
+    lib().oracle_rope_build_cos_sin(pos.ctypes.data_as(_i32p), _p(inv), _p(c), _p(s), T, Hd2, scaling)
+    return c, s
+
+
+def rope_apply(x, cos, sin):
+    """x [B, T, Nh, Hd] with tables [T, Hd/2] -> f32 [B, T, Nh, Hd] (before the output store)."""
+    x, cos, sin = _f32(x), _f32(cos), _f32(sin)
+    B, T, Nh, Hd = x.shape
+    out = np.empty_like(x)
+    lib().oracle_rope_apply(_p(x), _p(cos), _p(sin), _p(out), B, T, Nh, Hd // 2)
+    return out
+
+
+def transpose12(src):
+    """[D0, D1, D2, D3] -> [D0, D2, D1, D3]."""
+    src = _f32(src)
+    D0, D1, D2, D3 = src.shape
+    out = np.empty((D0, D2, D1, D3), np.float32)
+    lib().oracle_transpose12(_p(src), _p(out), D0, D1, D2, D3)
     return out
 
 

@@ -527,6 +527,62 @@ void oracle_flash_attention_rows(const float *q, const float *k, const float *v,
 }
 
 /* ------------------------------------------------------------------------ */
+/* RoPE and head transposes                                                  */
+/* ------------------------------------------------------------------------ */
+
+/* Sources/Popcorn/Kernels/RopeBuildCosSin.metal:17-20:
+ *   angle = float(positions[t]) * inv_freq[i]
+ *   cos_out[t*Hd2+i] = cos(angle) * scaling, sin_out likewise.
+ * The angle is the f32 product; cos/sin of it are taken in double and rounded
+ * once to f32 (the correctly rounded value the GPU's library routine is
+ * within an ulp or two of). */
+void oracle_rope_build_cos_sin(const int32_t *positions, const float *inv_freq, float *cos_out,
+                               float *sin_out, uint32_t T, uint32_t Hd2, float scaling) {
+    for (uint32_t t = 0; t < T; ++t) {
+        for (uint32_t i = 0; i < Hd2; ++i) {
+            float angle = (float)positions[t] * inv_freq[i];
+            float c = (float)cos((double)angle);
+            float s = (float)sin((double)angle);
+            cos_out[(size_t)t * Hd2 + i] = c * scaling;
+            sin_out[(size_t)t * Hd2 + i] = s * scaling;
+        }
+    }
+}
+
+/* Sources/Popcorn/Kernels/RopeApply.metal:15-48: for each (b, t, h) head of
+ * x [B, T, Nh, 2*Hd2] and each i < Hd2, with x1 = x[..., i], x2 =
+ * x[..., Hd2 + i], c = cos[t, i], s = sin[t, i]:
+ *   out[..., i] = x1*c - x2*s,  out[..., Hd2 + i] = x1*s + x2*c.
+ * Values are f32 (widened from the storage dtype); the caller rounds. */
+void oracle_rope_apply(const float *x, const float *cos_tab, const float *sin_tab, float *out,
+                       uint32_t B, uint32_t T, uint32_t Nh, uint32_t Hd2) {
+    for (uint32_t b = 0; b < B; ++b)
+        for (uint32_t t = 0; t < T; ++t)
+            for (uint32_t h = 0; h < Nh; ++h) {
+                size_t base = (((size_t)b * T + t) * Nh + h) * 2 * Hd2;
+                for (uint32_t i = 0; i < Hd2; ++i) {
+                    float x1 = x[base + i], x2 = x[base + Hd2 + i];
+                    float c = cos_tab[(size_t)t * Hd2 + i], s = sin_tab[(size_t)t * Hd2 + i];
+                    float p1 = x1 * c, p2 = x2 * s, p3 = x1 * s, p4 = x2 * c;
+                    out[base + i] = p1 - p2;
+                    out[base + Hd2 + i] = p3 + p4;
+                }
+            }
+}
+
+/* Sources/Popcorn/Kernels/Transpose12.metal:13-24:
+ *   out[((d0*D2 + d2)*D1 + d1)*D3 + d3] = src[((d0*D1 + d1)*D2 + d2)*D3 + d3]. */
+void oracle_transpose12(const float *src, float *out, uint32_t D0, uint32_t D1, uint32_t D2,
+                        uint32_t D3) {
+    for (uint32_t a = 0; a < D0; ++a)
+        for (uint32_t b = 0; b < D1; ++b)
+            for (uint32_t c = 0; c < D2; ++c)
+                for (uint32_t d = 0; d < D3; ++d)
+                    out[(((size_t)a * D2 + c) * D1 + b) * D3 + d] =
+                        src[(((size_t)a * D1 + b) * D2 + c) * D3 + d];
+}
+
+/* ------------------------------------------------------------------------ */
 /* Decode-loop glue                                                          */
 /* ------------------------------------------------------------------------ */
 

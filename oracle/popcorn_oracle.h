@@ -30,6 +30,12 @@
  *                                 same inputs, and to numpy float64
  *   argmax / embedding_gather   - reference KAT (KernelsTests.swift:121-138),
  *                                 tie-break on equal values
+ *   rope_build_cos_sin / rope_apply - reference KAT (KernelsTests.swift:438-489);
+ *                                 cos^2 + sin^2 = scaling^2; rotation keeps each
+ *                                 pair's norm; rotating by +p then -p, and by
+ *                                 p1 then p2 vs p1 + p2 (numpy float64)
+ *   transpose12                 - numpy transpose (0, 2, 1, 3); applied twice
+ *                                 with swapped dims is the identity
  *   decode_step                 - composition of the pinned pieces; numpy
  *                                 float64 forward of a tiny layer
  */
@@ -96,6 +102,13 @@ void oracle_flash_attention_rows(const float *q, const float *k, const float *v,
                                  uint32_t Sq, uint32_t Sk, uint32_t kv_stride,
                                  uint32_t Hd, uint32_t Bc, float scale,
                                  uint32_t mask_kind, int32_t window);
+
+void oracle_rope_build_cos_sin(const int32_t *positions, const float *inv_freq, float *cos_out,
+                               float *sin_out, uint32_t T, uint32_t Hd2, float scaling);
+void oracle_rope_apply(const float *x, const float *cos_tab, const float *sin_tab, float *out,
+                       uint32_t B, uint32_t T, uint32_t Nh, uint32_t Hd2);
+void oracle_transpose12(const float *src, float *out, uint32_t D0, uint32_t D1, uint32_t D2,
+                        uint32_t D3);
 
 void oracle_argmax(const float *x, size_t rows, size_t N, int32_t *indices);
 void oracle_embedding_gather(const int32_t *ids, const float *table, float *out,

@@ -131,6 +131,12 @@ PROTOTYPES = {
     "popcorn_kernel_mul": (_st, [_T, _T, _T, _K]),
     "popcorn_kernel_add": (_st, [_T, _T, _T, _K]),
     "popcorn_kernel_scalar_mul": (_st, [_T, C.c_float, _T, _K]),
+    "popcorn_kernel_rope_build_cos_sin": (_st, [_T, _T, _T, _T, C.c_float, _K]),
+    "popcorn_kernel_rope_build_cos_sin_dims": (_st, [_T, _T, _T, _T, C.c_int64, C.c_int64, C.c_float, _K]),
+    "popcorn_kernel_rope_apply": (_st, [_T, _T, _T, _T, _K]),
+    "popcorn_kernel_rope_apply_dims": (_st, [_T, _T, _T, _T, C.c_int64, C.c_int64, C.c_int64, C.c_int64, _K]),
+    "popcorn_kernel_transpose12": (_st, [_T, _T, _K]),
+    "popcorn_kernel_transpose12_dims": (_st, [_T, _T, C.c_int64, C.c_int64, C.c_int64, C.c_int64, _K]),
     "popcorn_kernel_gated_mlp": (_st, [_T, _T, _T, _T, _T, _T, C.c_float, C.c_int32, _T, _K]),
     "popcorn_kernel_gated_mlp_residual": (_st, [_T, _T, _T, _T, _T, _T, _T, _T, _T, C.c_float, C.c_int32, _T, _K]),
     "popcorn_kernel_decode_matvec": (_st, [C.POINTER(DecodeMatvecArgs), _K]),

@@ -522,6 +522,47 @@ popcorn_status_t popcorn_kernel_scalar_mul(const popcorn_tensor_t *x, float scal
     return guarded([&] { emit(kernel, Kernels::ScalarMul(T(x, "x"), scalar, T(out, "out"))); });
 }
 
+popcorn_status_t popcorn_kernel_rope_build_cos_sin(const popcorn_tensor_t *positions, const popcorn_tensor_t *inv_freq,
+                                                 const popcorn_tensor_t *cos_out, const popcorn_tensor_t *sin_out,
+                                                 float attention_scaling, popcorn_kernel_t *kernel) {
+    return guarded([&] {
+        emit(kernel, Kernels::RopeBuildCosSin(T(positions, "positions"), T(inv_freq, "invFreq"), T(cos_out, "cosOut"),
+                                              T(sin_out, "sinOut"), attention_scaling));
+    });
+}
+popcorn_status_t popcorn_kernel_rope_build_cos_sin_dims(const popcorn_tensor_t *positions, const popcorn_tensor_t *inv_freq,
+                                                      const popcorn_tensor_t *cos_out, const popcorn_tensor_t *sin_out,
+                                                      int64_t seq_len, int64_t half_head_dim, float attention_scaling,
+                                                      popcorn_kernel_t *kernel) {
+    return guarded([&] {
+        emit(kernel, Kernels::RopeBuildCosSin(T(positions, "positions"), T(inv_freq, "invFreq"), T(cos_out, "cosOut"),
+                                              T(sin_out, "sinOut"), seq_len, half_head_dim, attention_scaling));
+    });
+}
+popcorn_status_t popcorn_kernel_rope_apply(const popcorn_tensor_t *x, const popcorn_tensor_t *cos_table,
+                                         const popcorn_tensor_t *sin_table, const popcorn_tensor_t *out,
+                                         popcorn_kernel_t *kernel) {
+    return guarded([&] {
+        emit(kernel, Kernels::RopeApply(T(x, "x"), T(cos_table, "cos"), T(sin_table, "sin"), T(out, "out")));
+    });
+}
+popcorn_status_t popcorn_kernel_rope_apply_dims(const popcorn_tensor_t *x, const popcorn_tensor_t *cos_table,
+                                              const popcorn_tensor_t *sin_table, const popcorn_tensor_t *out, int64_t batch,
+                                              int64_t seq_len, int64_t head_count, int64_t head_dim,
+                                              popcorn_kernel_t *kernel) {
+    return guarded([&] {
+        emit(kernel, Kernels::RopeApply(T(x, "x"), T(cos_table, "cos"), T(sin_table, "sin"), T(out, "out"), batch, seq_len,
+                                        head_count, head_dim));
+    });
+}
+popcorn_status_t popcorn_kernel_transpose12(const popcorn_tensor_t *src, const popcorn_tensor_t *out, popcorn_kernel_t *kernel) {
+    return guarded([&] { emit(kernel, Kernels::Transpose12(T(src, "src"), T(out, "out"))); });
+}
+popcorn_status_t popcorn_kernel_transpose12_dims(const popcorn_tensor_t *src, const popcorn_tensor_t *out, int64_t d0,
+                                               int64_t d1, int64_t d2, int64_t d3, popcorn_kernel_t *kernel) {
+    return guarded([&] { emit(kernel, Kernels::Transpose12(T(src, "src"), T(out, "out"), d0, d1, d2, d3)); });
+}
+
 popcorn_status_t popcorn_kernel_gated_mlp(const popcorn_tensor_t *x, const popcorn_tensor_t *norm_weight,
                                           const popcorn_tensor_t *w_gate, const popcorn_tensor_t *w_up,
                                           const popcorn_tensor_t *w_down, const popcorn_tensor_t *out, float eps,

@@ -753,6 +753,126 @@ std::unique_ptr<Kernel> ScalarMul(const Tensor &x, float scalar, const Tensor &o
     return elementwise("scalar_mul", x, nullptr, out, bytesOf(ScalarMulConstants{(uint32_t)x.shape.elementCount(), scalar}));
 }
 
+// RopeBuildCosSin.swift:8-28: positions i32 [T], inv_freq f32 [Hd2] -> cos,
+// sin f32 [T, Hd2] (the Metal kernel's buffer types, checked here).
+std::unique_ptr<Kernel> RopeBuildCosSin(const Tensor &positions, const Tensor &invFreq, const Tensor &cosOut,
+                                        const Tensor &sinOut, int64_t seqLen, int64_t halfHeadDim, float scaling) {
+    if (positions.dataType != DataType::i32) throw Error::unsupportedDataTypeCombination("RoPE positions must be i32.");
+    if (invFreq.dataType != DataType::f32 || cosOut.dataType != DataType::f32 || sinOut.dataType != DataType::f32)
+        throw Error::unsupportedDataTypeCombination("RoPE invFreq and the cos/sin tables are f32.");
+    if (seqLen < 0 || halfHeadDim < 0 || seqLen > UINT32_MAX || halfHeadDim > UINT32_MAX)
+        throw Error::tensorShapeMismatch("RoPE table dimensions out of range.");
+    requireElements(positions, seqLen, "RoPE positions");
+    requireElements(invFreq, halfHeadDim, "RoPE invFreq");
+    requireElements(cosOut, seqLen * halfHeadDim, "RoPE cos");
+    requireElements(sinOut, seqLen * halfHeadDim, "RoPE sin");
+    RopeBuildCosSinConstants c{(uint32_t)seqLen, (uint32_t)halfHeadDim, scaling};
+    const int64_t n = seqLen * halfHeadDim;
+    const int64_t blocks = n ? std::clamp<int64_t>(cdiv(n, kBlock), 1, 8 * deviceCUs()) : 0;
+    return std::make_unique<FixedDispatch>(
+        "rope_build_cos_sin",
+        std::vector<Binding>{{positions, kRead}, {invFreq, kRead}, {cosOut, kWrite}, {sinOut, kWrite}},
+        std::vector<std::vector<uint8_t>>{bytesOf(c)}, grid1(blocks, kBlock));
+}
+
+// RopeBuildCosSin.swift:30-50
+std::unique_ptr<Kernel> RopeBuildCosSin(const Tensor &positions, const Tensor &invFreq, const Tensor &cosOut,
+                                        const Tensor &sinOut, float scaling) {
+    if (cosOut.shape != sinOut.shape)
+        throw Error::tensorShapeMismatch("RoPE cos and sin output shapes must match; got " + cosOut.shape.str() + " and " +
+                                         sinOut.shape.str() + ".");
+    if (cosOut.shape.rank() != 2) throw Error::tensorInvalidRank(2, cosOut.shape.rank());
+    const int64_t seqLen = cosOut.shape[0], halfHeadDim = cosOut.shape[1];
+    if (positions.shape.elementCount() != seqLen)
+        throw Error::tensorShapeMismatch("RoPE positions count must equal seqLen " + std::to_string(seqLen) + "; got " +
+                                         std::to_string(positions.shape.elementCount()) + ".");
+    if (invFreq.shape.elementCount() != halfHeadDim)
+        throw Error::tensorShapeMismatch("RoPE invFreq count must equal halfHeadDim " + std::to_string(halfHeadDim) +
+                                         "; got " + std::to_string(invFreq.shape.elementCount()) + ".");
+    return RopeBuildCosSin(positions, invFreq, cosOut, sinOut, seqLen, halfHeadDim, scaling);
+}
+
+// RopeApply.swift:8-44: x [B, T, Nh, Hd] with tables [T, Hd/2]; the function
+// is chosen by (x, table) dtypes as the reference does (:25-30); out has x's
+// dtype.
+std::unique_ptr<Kernel> RopeApply(const Tensor &x, const Tensor &cosT, const Tensor &sinT, const Tensor &out,
+                                  int64_t batch, int64_t seqLen, int64_t headCount, int64_t headDim) {
+    if (headDim % 2 != 0)
+        throw Error::tensorShapeMismatch("RoPE head dimension must be even; got " + std::to_string(headDim) + ".");
+    const char *fn = nullptr;
+    if (x.dataType == DataType::f32 && cosT.dataType == DataType::f32) fn = "rope_apply";
+    else if (x.dataType == DataType::bf16 && cosT.dataType == DataType::bf16) fn = "rope_apply_bf16";
+    else if (x.dataType == DataType::bf16 && cosT.dataType == DataType::f32) fn = "rope_apply_f32_tables_bf16";
+    else
+        throw Error::unsupportedDataTypeCombination(std::string("Unsupported RoPE data type combination: ") + tag(x.dataType) +
+                                                    ", " + tag(cosT.dataType) + ".");
+    if (sinT.dataType != cosT.dataType || out.dataType != x.dataType)
+        throw Error::unsupportedDataTypeCombination("RoPE sin table must match cos, and out must match x.");
+    if (batch < 0 || seqLen < 0 || headCount < 0 || headDim < 0 || batch > UINT32_MAX || seqLen > UINT32_MAX ||
+        headCount > UINT32_MAX || headDim > UINT32_MAX)
+        throw Error::tensorShapeMismatch("RoPE dimensions out of range.");
+    const int64_t n = batch * seqLen * headCount * headDim;
+    requireElements(x, n, "RoPE x");
+    requireElements(out, n, "RoPE out");
+    requireElements(cosT, seqLen * (headDim / 2), "RoPE cos");
+    requireElements(sinT, seqLen * (headDim / 2), "RoPE sin");
+    RopeApplyConstants c{(uint32_t)batch, (uint32_t)seqLen, (uint32_t)headCount, (uint32_t)(headDim / 2)};
+    const int64_t items = batch * seqLen * headCount * cdiv(headDim / 2, 8);
+    const int64_t blocks = items ? std::clamp<int64_t>(cdiv(items, kBlock), 1, 8 * deviceCUs()) : 0;
+    return std::make_unique<FixedDispatch>(
+        fn, std::vector<Binding>{{x, kRead}, {cosT, kRead}, {sinT, kRead}, {out, kWrite}},
+        std::vector<std::vector<uint8_t>>{bytesOf(c)}, grid1(blocks, kBlock));
+}
+
+// RopeApply.swift:46-60
+std::unique_ptr<Kernel> RopeApply(const Tensor &x, const Tensor &cosT, const Tensor &sinT, const Tensor &out) {
+    if (x.shape.rank() != 4) throw Error::tensorInvalidRank(4, x.shape.rank());
+    if (x.shape != out.shape)
+        throw Error::tensorShapeMismatch("RoPE output shape must match input; got " + out.shape.str() + ", expected " +
+                                         x.shape.str() + ".");
+    const int64_t batch = x.shape[0], seqLen = x.shape[1], headCount = x.shape[2], headDim = x.shape[3];
+    if (headDim % 2 != 0)
+        throw Error::tensorShapeMismatch("RoPE head dimension must be even; got " + std::to_string(headDim) + ".");
+    const Shape table{seqLen, headDim / 2};
+    if (cosT.shape != table || sinT.shape != table)
+        throw Error::tensorShapeMismatch("RoPE tables must have shape " + table.str() + "; got cos " + cosT.shape.str() +
+                                         ", sin " + sinT.shape.str() + ".");
+    return RopeApply(x, cosT, sinT, out, batch, seqLen, headCount, headDim);
+}
+
+// Transpose12.swift:8-25: [D0, D1, D2, D3] -> [D0, D2, D1, D3].
+std::unique_ptr<Kernel> Transpose12(const Tensor &src, const Tensor &out, int64_t d0, int64_t d1, int64_t d2, int64_t d3) {
+    const char *fn = nullptr;
+    switch (src.dataType) {
+    case DataType::f32: fn = "transpose12"; break;
+    case DataType::f16: fn = "transpose12_f16"; break;
+    case DataType::bf16: fn = "transpose12_bf16"; break;
+    default:
+        throw Error::unsupportedDataTypeCombination(std::string("Unsupported transpose12 data type: ") + tag(src.dataType) + ".");
+    }
+    if (out.dataType != src.dataType) throw Error::unsupportedDataTypeCombination("Transpose12 output must match the source dtype.");
+    for (int64_t d : {d0, d1, d2, d3})
+        if (d < 0 || d > UINT32_MAX) throw Error::tensorShapeMismatch("Transpose12 dimensions out of range.");
+    const int64_t n = d0 * d1 * d2 * d3;
+    requireElements(src, n, "Transpose12 src");
+    requireElements(out, n, "Transpose12 out");
+    Transpose12Constants c{(uint32_t)d0, (uint32_t)d1, (uint32_t)d2, (uint32_t)d3};
+    const int64_t runs = (d3 % (16 / stride(src.dataType)) == 0) ? n / (16 / stride(src.dataType)) : n;
+    const int64_t blocks = runs ? std::clamp<int64_t>(cdiv(runs, kBlock), 1, 8 * deviceCUs()) : 0;
+    return std::make_unique<FixedDispatch>(fn, std::vector<Binding>{{src, kRead}, {out, kWrite}},
+                                           std::vector<std::vector<uint8_t>>{bytesOf(c)}, grid1(blocks, kBlock));
+}
+
+// Transpose12.swift:27-35
+std::unique_ptr<Kernel> Transpose12(const Tensor &src, const Tensor &out) {
+    if (src.shape.rank() != 4) throw Error::tensorInvalidRank(4, src.shape.rank());
+    const int64_t d0 = src.shape[0], d1 = src.shape[1], d2 = src.shape[2], d3 = src.shape[3];
+    const Shape expected{d0, d2, d1, d3};
+    if (out.shape != expected)
+        throw Error::tensorShapeMismatch("Transpose12 output shape must be " + expected.str() + "; got " + out.shape.str() + ".");
+    return Transpose12(src, out, d0, d1, d2, d3);
+}
+
 std::unique_ptr<Kernel> GatedMLP(const Tensor &x, const Tensor *normWeight, const Tensor &wGate, const Tensor &wUp,
                                  const Tensor &wDown, const Tensor &out, float eps, bool addOneToWeight, const Tensor *hidden) {
     return std::make_unique<GatedMLPKernel>(x, normWeight, wGate, wUp, wDown, out, eps, addOneToWeight, hidden);

@@ -310,6 +310,16 @@ std::unique_ptr<Kernel> Mul(const Tensor &a, const Tensor &b, const Tensor &out)
 std::unique_ptr<Kernel> Add(const Tensor &a, const Tensor &b, const Tensor &out);
 std::unique_ptr<Kernel> ScalarMul(const Tensor &x, float scalar, const Tensor &out);
 
+std::unique_ptr<Kernel> RopeBuildCosSin(const Tensor &positions, const Tensor &invFreq, const Tensor &cosOut,
+                                        const Tensor &sinOut, int64_t seqLen, int64_t halfHeadDim, float scaling);
+std::unique_ptr<Kernel> RopeBuildCosSin(const Tensor &positions, const Tensor &invFreq, const Tensor &cosOut,
+                                        const Tensor &sinOut, float scaling);
+std::unique_ptr<Kernel> RopeApply(const Tensor &x, const Tensor &cosT, const Tensor &sinT, const Tensor &out,
+                                  int64_t batch, int64_t seqLen, int64_t headCount, int64_t headDim);
+std::unique_ptr<Kernel> RopeApply(const Tensor &x, const Tensor &cosT, const Tensor &sinT, const Tensor &out);
+std::unique_ptr<Kernel> Transpose12(const Tensor &src, const Tensor &out, int64_t d0, int64_t d1, int64_t d2, int64_t d3);
+std::unique_ptr<Kernel> Transpose12(const Tensor &src, const Tensor &out);
+
 std::unique_ptr<Kernel> GatedMLP(const Tensor &x, const Tensor *normWeight, const Tensor &wGate, const Tensor &wUp,
                                  const Tensor &wDown, const Tensor &out, float eps, bool addOneToWeight,
                                  const Tensor *hidden = nullptr);

@@ -486,6 +486,37 @@ class Kernels:
         return _make(lib().popcorn_kernel_scalar_mul, _d(x), by, _d(into), refs=(x, into))
 
     @staticmethod
+    def RopeBuildCosSin(positions: Tensor, inv_freq: Tensor, cos_out: Tensor, sin_out: Tensor, *,
+                        attention_scaling: float = 1.0, seq_len: Optional[int] = None,
+                        half_head_dim: int = 0) -> Kernel:
+        """RopeBuildCosSin(positions:invFreq:cosOut:sinOut:attentionScaling:) (RopeBuildCosSin.swift:30-50),
+        or with seq_len=... the explicit init (:8-28)."""
+        refs = (positions, inv_freq, cos_out, sin_out)
+        if seq_len is None:
+            return _make(lib().popcorn_kernel_rope_build_cos_sin, _d(positions), _d(inv_freq), _d(cos_out),
+                         _d(sin_out), attention_scaling, refs=refs)
+        return _make(lib().popcorn_kernel_rope_build_cos_sin_dims, _d(positions), _d(inv_freq), _d(cos_out),
+                     _d(sin_out), seq_len, half_head_dim, attention_scaling, refs=refs)
+
+    @staticmethod
+    def RopeApply(x: Tensor, cos: Tensor, sin: Tensor, into: Tensor, *, batch: Optional[int] = None,
+                  seq_len: int = 0, head_count: int = 0, head_dim: int = 0) -> Kernel:
+        """RopeApply(_:cos:sin:into:) (RopeApply.swift:46-60), or with batch=... the explicit init (:8-44)."""
+        refs = (x, cos, sin, into)
+        if batch is None:
+            return _make(lib().popcorn_kernel_rope_apply, _d(x), _d(cos), _d(sin), _d(into), refs=refs)
+        return _make(lib().popcorn_kernel_rope_apply_dims, _d(x), _d(cos), _d(sin), _d(into), batch, seq_len,
+                     head_count, head_dim, refs=refs)
+
+    @staticmethod
+    def Transpose12(src: Tensor, into: Tensor, *, dims: Optional[Sequence[int]] = None) -> Kernel:
+        """Transpose12(_:into:) (Transpose12.swift:27-35), or with dims=(d0, d1, d2, d3) the explicit init (:8-25)."""
+        if dims is None:
+            return _make(lib().popcorn_kernel_transpose12, _d(src), _d(into), refs=(src, into))
+        d0, d1, d2, d3 = dims
+        return _make(lib().popcorn_kernel_transpose12_dims, _d(src), _d(into), d0, d1, d2, d3, refs=(src, into))
+
+    @staticmethod
     def GatedMLP(x: Tensor, norm_weight: Optional[Tensor], w_gate: Tensor, w_up: Tensor, w_down: Tensor,
                  into: Tensor, *, eps: float, add_one_to_weight: bool = False,
                  hidden: Optional[Tensor] = None) -> Kernel:

@@ -144,6 +144,47 @@ def test_rmsnorm_kv_elementwise_validation():
     assert pa.Kernels.GeluTanh(T([7], "f16"), T([7], "f16")).describe() == "gelu_tanh_f16"
 
 
+def test_rope_transpose_validation_and_routing():
+    # RopeBuildCosSin.swift:37-48, RopeApply.swift:18-30 and :47-58, Transpose12.swift:15-20 and :27-35
+    E = pa.PopcornError
+    pos, inv = T([6], "i32"), T([64], "f32")
+    cs = [T([6, 64], "f32", FAKE + 2 ** 20), T([6, 64], "f32", FAKE + 2 ** 21)]
+    assert pa.Kernels.RopeBuildCosSin(pos, inv, *cs).describe() == "rope_build_cos_sin"
+    with pytest.raises(E) as e:
+        pa.Kernels.RopeBuildCosSin(T([5], "i32"), inv, *cs)
+    assert e.value.code == E.TENSOR_SHAPE_MISMATCH and "positions count must equal seqLen 6" in str(e.value)
+    with pytest.raises(E) as e:
+        pa.Kernels.RopeBuildCosSin(pos, inv, T([6, 64], "f32"), T([6, 32], "f32"))
+    assert e.value.code == E.TENSOR_SHAPE_MISMATCH
+    with pytest.raises(E) as e:
+        pa.Kernels.RopeBuildCosSin(pos, inv, T([6, 64, 1], "f32"), T([6, 64, 1], "f32"))
+    assert e.value.code == E.TENSOR_INVALID_RANK
+    x = T([1, 6, 8, 128])
+    for xt, tt, name in (("f32", "f32", "rope_apply"), ("bf16", "bf16", "rope_apply_bf16"),
+                         ("bf16", "f32", "rope_apply_f32_tables_bf16")):
+        k = pa.Kernels.RopeApply(T([1, 6, 8, 128], xt), T([6, 64], tt), T([6, 64], tt),
+                                 T([1, 6, 8, 128], xt, FAKE + 2 ** 24))
+        assert k.describe() == name
+    with pytest.raises(E) as e:
+        pa.Kernels.RopeApply(T([1, 6, 8, 128], "f16"), T([6, 64], "f16"), T([6, 64], "f16"), T([1, 6, 8, 128], "f16"))
+    assert e.value.code == E.UNSUPPORTED_DATA_TYPE_COMBINATION
+    with pytest.raises(E) as e:
+        pa.Kernels.RopeApply(x, T([6, 32], "f32"), T([6, 32], "f32"), T([1, 6, 8, 128]))
+    assert e.value.code == E.TENSOR_SHAPE_MISMATCH and "tables must have shape [6, 64]" in str(e.value)
+    with pytest.raises(E) as e:
+        pa.Kernels.RopeApply(T([1, 6, 8, 7]), T([6, 3]), T([6, 3]), T([1, 6, 8, 7]), batch=1, seq_len=6,
+                             head_count=8, head_dim=7)
+    assert e.value.code == E.TENSOR_SHAPE_MISMATCH and "must be even" in str(e.value)
+    for dt, name in (("f32", "transpose12"), ("f16", "transpose12_f16"), ("bf16", "transpose12_bf16")):
+        assert pa.Kernels.Transpose12(T([1, 6, 8, 128], dt), T([1, 8, 6, 128], dt)).describe() == name
+    with pytest.raises(E) as e:
+        pa.Kernels.Transpose12(T([1, 6, 8, 128]), T([1, 6, 8, 128]))
+    assert e.value.code == E.TENSOR_SHAPE_MISMATCH and "must be [1, 8, 6, 128]" in str(e.value)
+    with pytest.raises(E) as e:
+        pa.Kernels.Transpose12(T([1, 6, 8, 128], "i32"), T([1, 8, 6, 128], "i32"))
+    assert e.value.code == E.UNSUPPORTED_DATA_TYPE_COMBINATION
+
+
 def test_gated_mlp_validation_and_routing():
     E = pa.PopcornError
     k = pa.Kernels.GatedMLP(T([2304]), T([2304], "f32"), T([9216, 2304]), T([9216, 2304]), T([2304, 9216]),

@@ -348,6 +348,75 @@ def test_gated_mlp_bf16_is_composition(oracle):
     np.testing.assert_array_equal(out, oracle.matmul(hh, wd, 1, F, H, True).ravel())
 
 
+# ---- RoPE and head transposes ---------------------------------------------------
+
+def _gemma_inv_freq(hd, base=10_000.0):
+    # Gemma4Workspace.swift:195-197: 1 / base^(2i/Hd), computed in double then f32
+    return np.array([1 / base ** (2 * i / hd) for i in range(hd // 2)], np.float32)
+
+
+def test_rope_reference_kat(oracle):
+    # KernelsTests.swift:438-489 (ropeBuildAndApply), with its approxEqual eps 1e-4
+    c, s = oracle.rope_build_cos_sin([0, 1], [1.0, 0.5])
+    f = np.float32
+    assert_approx(c.ravel(), [1, 1, np.cos(f(1)), np.cos(f(0.5))], 1e-4, "cos")
+    assert_approx(s.ravel(), [0, 0, np.sin(f(1)), np.sin(f(0.5))], 1e-4, "sin")
+    x = np.arange(1, 9, dtype=np.float32).reshape(1, 2, 1, 4)
+    r = oracle.rope_apply(x, c, s).ravel()
+    c0, s0, c1, s1 = np.cos(1.0), np.sin(1.0), np.cos(0.5), np.sin(0.5)
+    assert_approx(r[:4], [1, 2, 3, 4], 1e-4, "t=0 unchanged")
+    assert_approx(r[4:], [5 * c0 - 7 * s0, 6 * c1 - 8 * s1, 5 * s0 + 7 * c0, 6 * s1 + 8 * c1], 1e-4, "t=1")
+
+
+def test_rope_tables_unit_circle_and_scaling(oracle):
+    # cos^2 + sin^2 = scaling^2 at every angle, large positions included; the
+    # t = 0 row is (scaling, 0)
+    inv = _gemma_inv_freq(256)
+    pos = np.array([0, 1, 7, 4096, 131071, 1 << 20], np.int32)
+    for scaling in (1.0, 0.75):
+        c, s = oracle.rope_build_cos_sin(pos, inv, scaling)
+        np.testing.assert_allclose(c.astype(np.float64) ** 2 + s.astype(np.float64) ** 2, scaling ** 2, rtol=1e-6)
+        assert np.all(c[0] == np.float32(scaling)) and np.all(s[0] == 0)
+        # angle is the f32 product float(pos) * inv_freq, then cos/sin in double
+        ang = (pos.astype(np.float32)[:, None] * inv[None, :]).astype(np.float64)
+        np.testing.assert_allclose(c, (np.cos(ang) * scaling).astype(np.float32), atol=2e-7)
+
+
+def test_rope_rotation_properties(oracle):
+    # a rotation of each (x[i], x[i + Hd/2]) pair: norms are kept, rotating by
+    # +p then by -p is the identity, and p1 then p2 equals p1 + p2
+    rng = np.random.default_rng(3)
+    Hd, T = 64, 5
+    inv = _gemma_inv_freq(Hd)
+    x = rng.standard_normal((2, T, 3, Hd)).astype(np.float32)
+    p = np.array([0, 3, 17, 250, 1000], np.int32)
+    c, s = oracle.rope_build_cos_sin(p, inv)
+    y = oracle.rope_apply(x, c, s)
+    h = Hd // 2
+    n_x = x[..., :h].astype(np.float64) ** 2 + x[..., h:].astype(np.float64) ** 2
+    n_y = y[..., :h].astype(np.float64) ** 2 + y[..., h:].astype(np.float64) ** 2
+    np.testing.assert_allclose(n_y, n_x, rtol=1e-5, atol=1e-6)
+    cb, sb = oracle.rope_build_cos_sin(-p, inv)
+    np.testing.assert_allclose(oracle.rope_apply(y, cb, sb), x, atol=1e-5)
+    p2 = np.array([1, 2, 5, 9, 30], np.int32)
+    c2, s2 = oracle.rope_build_cos_sin(p2, inv)
+    c3, s3 = oracle.rope_build_cos_sin(p + p2, inv)
+    np.testing.assert_allclose(oracle.rope_apply(y, c2, s2), oracle.rope_apply(x, c3, s3), atol=5e-5)
+    # only the first half sees -x2*sin: a quarter turn maps (x1, x2) to (-x2, x1)
+    q = np.zeros((1, 1, 1, 4), np.float32)
+    q[..., 0], q[..., 2] = 1.0, 2.0
+    r = oracle.rope_apply(q, np.zeros((1, 2), np.float32), np.ones((1, 2), np.float32)).ravel()
+    assert r.tolist() == [-2.0, 0.0, 1.0, 0.0]
+
+
+@pytest.mark.parametrize("shape", [(1, 2, 3, 4), (2, 5, 1, 7), (1, 1, 6, 256), (3, 4, 2, 1)])
+def test_transpose12_vs_numpy(oracle, shape):
+    x = np.arange(np.prod(shape), dtype=np.float32).reshape(shape)
+    y = oracle.transpose12(x)
+    np.testing.assert_array_equal(y, np.transpose(x, (0, 2, 1, 3)))
+    np.testing.assert_array_equal(oracle.transpose12(y), x)
+
+
 # ---- glue -------------------------------------------------------------------
 
 def test_argmax_and_gather_kats(oracle):
