@@ -387,6 +387,40 @@ typedef struct {
 
 popcorn_status_t popcorn_kernel_decode_matvec(const popcorn_decode_matvec_args_t *args, popcorn_kernel_t *kernel);
 
+/* The attention block of one decode token with its per-head glue folded into
+ * the split-KV kernel (DecodeAttentionConstants in popcorn_kernel_types.h):
+ * qkv [B, (Nq + 2 Nkv) * Hd] holds the raw projections; q_norm / k_norm (f32
+ * [Hd]) apply the per-head RMSNorms, v_norm the weightless one, inv_freq (f32
+ * [Hd/2]) RoPE at position[0] with tables scaled by rope_scaling; the
+ * processed key and value rows are written to the caches [B, Nkv, S, Hd] at
+ * row position[0], and out [B, Nq, 1, Hd] = attention over keys
+ * 0..position[0] (mask as for FlashAttention). Every intermediate is rounded
+ * to the cache dtype where the reference stores a tensor. NULL = absent.
+ * Replaces the reference's RMSNorm, RopeApply, Transpose12, KVCacheWrite and
+ * FlashAttention dispatches of one token (Gemma4TextInference.swift:352-399);
+ * no single counterpart. Needs the fast split-KV path: 16-byte aligned data,
+ * head dim 64/128/256/512 for f16/bf16 (128/256/512 for f32). */
+typedef struct {
+    const popcorn_tensor_t *qkv;
+    const popcorn_tensor_t *k_cache;
+    const popcorn_tensor_t *v_cache;
+    const popcorn_tensor_t *out;
+    const popcorn_tensor_t *position;
+    const popcorn_tensor_t *q_norm;
+    const popcorn_tensor_t *k_norm;
+    const popcorn_tensor_t *inv_freq;
+    int32_t v_norm;
+    int32_t query_heads;
+    int32_t kv_heads;
+    float eps;
+    float scale;
+    float rope_scaling;
+    popcorn_attention_mask_t mask;
+} popcorn_decode_attention_args_t;
+
+popcorn_status_t popcorn_kernel_decode_attention(const popcorn_decode_attention_args_t *args,
+                                                 popcorn_kernel_t *kernel);
+
 /* Kernels.EmbeddingGather(ids:table:out:tokenCount:hiddenSize:)
  * (EmbeddingGather.swift) and Kernels.Argmax(_:indices:axis:) (Argmax.swift:24-37):
  * the decode loop's token in / token out. */

@@ -125,6 +125,26 @@ typedef struct {
     uint32_t keyLenFromPosition;
 } FlashDecodingPartialConstants;
 
+/* No counterpart in the reference: the attention block of one decode token
+ * with the per-head glue folded into the split-KV partial kernel
+ * (flash_decoding_fresh_*). The projections arrive raw in one row per batch
+ * entry of rowStride elements: Nq query heads, then Nkv key heads, then Nkv
+ * value heads, Hd each. flags:
+ *   bit 0  q = RMSNorm(q; w_q) per head   (Gemma4TextInference.swift:353)
+ *   bit 1  k = RMSNorm(k; w_k) per head   (:367)
+ *   bit 2  v = RMSNorm(v) per head, no weight (:368)
+ *   bit 3  RoPE on q and k with angle = float(position) * inv_freq[i],
+ *          tables scaled by ropeScaling (:354, :369; RopeBuildCosSin.metal)
+ * Each step's result is rounded to the storage dtype, as the reference
+ * stores each intermediate. The processed key and value rows are written to
+ * the caches at row `position` and attended as the last key. */
+typedef struct {
+    uint32_t flags;
+    float eps;
+    float ropeScaling;
+    uint32_t rowStride;
+} DecodeAttentionConstants;
+
 /* PopcornKernelTypes.h:158-163, plus Sq (0 = 1). */
 typedef struct {
     uint32_t B;

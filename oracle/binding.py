@@ -299,16 +299,22 @@ class _Layer(C.Structure):
                 ("act_dtype", C.c_int),
                 ("w_in_norm", _fp), ("w_qkv", _fp), ("w_o", _fp), ("w_post_attn_norm", _fp),
                 ("w_pre_ffn_norm", _fp), ("w_gate", _fp), ("w_up", _fp), ("w_down", _fp),
-                ("w_post_ffn_norm", _fp)]
+                ("w_post_ffn_norm", _fp), ("w_q_norm", _fp), ("w_k_norm", _fp), ("v_norm", C.c_int),
+                ("inv_freq", _fp), ("rope_scaling", C.c_float)]
 
 
 def decoder_layer(weights: dict, x: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray, pos: int,
-                  *, H, Nq, Nkv, Hd, F, eps, scale, act_tag) -> None:
-    """In place on x [H], k_cache/v_cache [Nkv, cap, Hd] (f32 storage of act_tag values)."""
-    keep = {n: _f32(w) for n, w in weights.items()}
+                  *, H, Nq, Nkv, Hd, F, eps, scale, act_tag, v_norm=False, rope_scaling=1.0) -> None:
+    """In place on x [H], k_cache/v_cache [Nkv, cap, Hd] (f32 storage of act_tag values).
+    Optional weights "q_norm", "k_norm" [Hd] and "inv_freq" [Hd/2] (with v_norm) make it a
+    real attention block."""
+    keep = {n: _f32(w) for n, w in weights.items() if w is not None}
     assert x.dtype == np.float32 and x.flags["C_CONTIGUOUS"]
     cap = k_cache.shape[1]
+    opt = [_p(keep[n]) if n in keep else None for n in ("q_norm", "k_norm")]
     L = _Layer(H, Nq, Nkv, Hd, F, cap, eps, scale, act_tag,
                *[_p(keep[n]) for n in ("in_norm", "qkv", "o", "post_attn_norm", "pre_ffn_norm",
-                                       "gate", "up", "down", "post_ffn_norm")])
+                                       "gate", "up", "down", "post_ffn_norm")],
+               opt[0], opt[1], int(v_norm), _p(keep["inv_freq"]) if "inv_freq" in keep else None,
+               rope_scaling)
     lib().oracle_decoder_layer(C.byref(L), _p(x), _p(k_cache), _p(v_cache), pos)

@@ -615,14 +615,17 @@ void oracle_embedding_gather(const int32_t *ids, const float *table, float *out,
 
 /* One decoder layer at Sq = 1, following the op order of
  * Examples/GemmaCLI/Sources/GemmaCLI/Gemma4TextInference.swift:334-436 with
- * the per-head q/k norms, RoPE and per-layer inputs left out (no config on
- * this path uses them): RMSNorm -> QKV matvec (one [Nq+2Nkv]*Hd x H weight,
- * row-identical to the three separate projections at :335-343) -> KV-cache
- * write at `pos` (:372-381) -> split-KV attention over pos+1 keys (:394-398)
- * -> O projection -> post-attention RMSNorm -> residual Add (:400-404) ->
- * gated MLP (:416-429) -> post-FFN RMSNorm -> residual Add (:430-434).
- * Every stored tensor is rounded to L->act_dtype; the caches hold act_dtype
- * values in f32 storage here. x is updated in place. */
+ * the per-layer inputs left out: RMSNorm -> QKV matvec (one [Nq+2Nkv]*Hd x H
+ * weight, row-identical to the three separate projections at :335-343) ->
+ * when given, per-head RMSNorm of q (:353), k (:367) and v without weight
+ * (:368) and RoPE of q (:354) and k (:369) at position pos (tables as
+ * RopeBuildCosSin.metal:17-20; the head transposes :355, :370-371 move no
+ * value at one token) -> KV-cache write at `pos` (:372-381) -> attention
+ * over pos+1 keys (:394-398) -> O projection -> post-attention RMSNorm ->
+ * residual Add (:400-404) -> gated MLP (:416-429) -> post-FFN RMSNorm ->
+ * residual Add (:430-434). Every stored tensor is rounded to L->act_dtype;
+ * the caches hold act_dtype values in f32 storage here. x is updated in
+ * place. */
 void oracle_decoder_layer(const oracle_layer_t *L, float *x, float *k_cache,
                           float *v_cache, uint32_t pos) {
     const uint32_t H = L->H, Hd = L->Hd, Nq = L->Nq, Nkv = L->Nkv, F = L->F;
@@ -638,6 +641,28 @@ void oracle_decoder_layer(const oracle_layer_t *L, float *x, float *k_cache,
     round_array(dt, n, H);
     oracle_matmul(n, L->w_qkv, qkv, 1, H, QKV, 1);
     round_array(dt, qkv, QKV);
+    if (L->w_q_norm) {
+        oracle_rmsnorm(qkv, L->w_q_norm, qkv, Nq, Hd, L->eps, 0);
+        round_array(dt, qkv, QW);
+    }
+    if (L->w_k_norm) {
+        oracle_rmsnorm(qkv + QW, L->w_k_norm, qkv + QW, Nkv, Hd, L->eps, 0);
+        round_array(dt, qkv + QW, KW);
+    }
+    if (L->v_norm) {
+        oracle_rmsnorm(qkv + QW + KW, NULL, qkv + QW + KW, Nkv, Hd, L->eps, 0);
+        round_array(dt, qkv + QW + KW, KW);
+    }
+    if (L->inv_freq) {
+        float *cs = (float *)malloc(Hd * sizeof(float));
+        const int32_t p32 = (int32_t)pos;
+        oracle_rope_build_cos_sin(&p32, L->inv_freq, cs, cs + Hd / 2, 1, Hd / 2, L->rope_scaling);
+        oracle_rope_apply(qkv, cs, cs + Hd / 2, qkv, 1, 1, Nq, Hd / 2);
+        round_array(dt, qkv, QW);
+        oracle_rope_apply(qkv + QW, cs, cs + Hd / 2, qkv + QW, 1, 1, Nkv, Hd / 2);
+        round_array(dt, qkv + QW, KW);
+        free(cs);
+    }
     for (uint32_t h = 0; h < Nkv; ++h) {
         for (uint32_t d = 0; d < Hd; ++d) {
             size_t dst = ((size_t)h * L->kv_capacity + pos) * Hd + d;

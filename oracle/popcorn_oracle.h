@@ -37,7 +37,8 @@
  *   transpose12                 - numpy transpose (0, 2, 1, 3); applied twice
  *                                 with swapped dims is the identity
  *   decode_step                 - composition of the pinned pieces; numpy
- *                                 float64 forward of a tiny layer
+ *                                 float64 forward of a tiny layer (with and
+ *                                 without the q/k/v norms and RoPE)
  */
 #ifndef POPCORN_ORACLE_H
 #define POPCORN_ORACLE_H
@@ -129,6 +130,12 @@ typedef struct {
     const float *w_gate, *w_up;    /* [F, H]                                    */
     const float *w_down;      /* [H, F]                                         */
     const float *w_post_ffn_norm;  /* [H]                                       */
+    /* a real attention block (all optional: NULL / 0 = left out) */
+    const float *w_q_norm;    /* [Hd] per-head RMSNorm of q                     */
+    const float *w_k_norm;    /* [Hd] per-head RMSNorm of k                     */
+    int v_norm;               /* 1: per-head RMSNorm of v without weight        */
+    const float *inv_freq;    /* [Hd/2]: RoPE on q and k at position pos        */
+    float rope_scaling;
 } oracle_layer_t;
 
 void oracle_decoder_layer(const oracle_layer_t *L, float *x, float *k_cache,

@@ -69,6 +69,12 @@ _T = C.POINTER(TensorDesc)
 class DecodeMatvecArgs(C.Structure):
     _fields_ = [(n, _T) for n in ("x", "delta", "w_post", "x_out", "w_pre", "weight", "out", "k_cache", "v_cache",
                                   "position")] + [("q_rows", C.c_int64), ("eps", C.c_float)]
+class DecodeAttentionArgs(C.Structure):
+    _fields_ = [(n, _T) for n in ("qkv", "k_cache", "v_cache", "out", "position", "q_norm", "k_norm",
+                                  "inv_freq")] + [("v_norm", C.c_int32), ("query_heads", C.c_int32),
+                                                  ("kv_heads", C.c_int32), ("eps", C.c_float),
+                                                  ("scale", C.c_float), ("rope_scaling", C.c_float),
+                                                  ("mask", AttentionMaskDesc)]
 _K = C.POINTER(C.c_void_p)
 _st = C.c_int32
 
@@ -140,6 +146,7 @@ PROTOTYPES = {
     "popcorn_kernel_gated_mlp": (_st, [_T, _T, _T, _T, _T, _T, C.c_float, C.c_int32, _T, _K]),
     "popcorn_kernel_gated_mlp_residual": (_st, [_T, _T, _T, _T, _T, _T, _T, _T, _T, C.c_float, C.c_int32, _T, _K]),
     "popcorn_kernel_decode_matvec": (_st, [C.POINTER(DecodeMatvecArgs), _K]),
+    "popcorn_kernel_decode_attention": (_st, [C.POINTER(DecodeAttentionArgs), _K]),
     "popcorn_kernel_embedding_gather": (_st, [_T, _T, _T, _K]),
     "popcorn_kernel_argmax": (_st, [_T, _T, _K]),
     "popcorn_kernel_custom": (_st, [C.c_char_p, _T, C.POINTER(C.c_uint8), C.c_int32, C.POINTER(C.c_void_p),

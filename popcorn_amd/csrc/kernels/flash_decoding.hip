@@ -35,6 +35,7 @@ constexpr int kWaves = 4;
 struct FdGeom {
     uint32_t b, hkv, g0, gcount, qi, Sq, Sk, posQ, jLo, jHi;
     bool empty;
+    bool owner;  // fresh-key variant: this block's partition holds key posQ
 };
 
 __device__ inline bool fd_allowed(const FlashDecodingPartialConstants &p, int posQ, int posK) {
@@ -44,7 +45,11 @@ __device__ inline bool fd_allowed(const FlashDecodingPartialConstants &p, int po
 }
 
 // Grid: x = partition, y = (b * Nkv + hkv) * ngroups + head group, z = row.
-__device__ inline FdGeom fd_geometry(const FlashDecodingPartialConstants &p, const int32_t *position, uint32_t gmax) {
+// With freshLast, key posQ is left out of the block's range (the fresh-key
+// variant attends it from its prologue) and `owner` marks the block whose
+// partition holds it.
+__device__ inline FdGeom fd_geometry(const FlashDecodingPartialConstants &p, const int32_t *position, uint32_t gmax,
+                                     bool freshLast = false) {
     FdGeom g;
     const uint32_t G = p.Nq / p.Nkv;
     const uint32_t ngroups = (G + gmax - 1) / gmax;
@@ -70,7 +75,9 @@ __device__ inline FdGeom fd_geometry(const FlashDecodingPartialConstants &p, con
     const uint32_t per = (Sk + P - 1) / P;
     int lo = (int)(blockIdx.x * per);
     int hi = min(lo + (int)per, (int)Sk);
+    g.owner = freshLast && posQ >= 0 && (uint32_t)posQ < stride && lo <= posQ && posQ < hi;
     if (p.maskKind != 2u) hi = min(hi, posQ + 1);
+    if (freshLast) hi = min(hi, posQ);
     if (p.maskKind == 1u) lo = max(lo, posQ - p.slidingWindow + 1);
     g.empty = hi <= lo;
     g.jLo = (uint32_t)max(lo, 0);
@@ -79,7 +86,7 @@ __device__ inline FdGeom fd_geometry(const FlashDecodingPartialConstants &p, con
 }
 
 // Writes one partition's state for `gcount` heads: wave states sm_* merged.
-template <int GMAX, int HD>
+template <int GMAX, int HD, int NSLOTS = kWaves>
 __device__ void fd_merge_store(const FlashDecodingPartialConstants &p, const FdGeom &geo, float (*sm_m)[GMAX],
                                float (*sm_l)[GMAX], float (*sm_o)[GMAX][HD], float *pO, float *pM, float *pL) {
     const uint32_t P = p.P ? p.P : 1u;
@@ -88,11 +95,11 @@ __device__ void fd_merge_store(const FlashDecodingPartialConstants &p, const FdG
         const uint32_t g = idx / HD, d = idx % HD;
         float mstar = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) mstar = fmaxf(mstar, sm_m[w][g]);
+        for (int w = 0; w < NSLOTS; ++w) mstar = fmaxf(mstar, sm_m[w][g]);
         float o = 0.0f, l = 0.0f;
         if (mstar != -INFINITY) {
 #pragma unroll
-            for (int w = 0; w < kWaves; ++w) {
+            for (int w = 0; w < NSLOTS; ++w) {
                 float a = pk::fast_exp(sm_m[w][g] - mstar);
                 o += a * sm_o[w][g][d];
                 l += a * sm_l[w][g];
@@ -108,26 +115,133 @@ __device__ void fd_merge_store(const FlashDecodingPartialConstants &p, const FdG
     }
 }
 
-template <typename T, int LPK, int CPL, int GMAX, int U>
+// The fresh-key variant's extra inputs (DecodeAttentionConstants): the
+// caches again as writable pointers for the new row, the per-head norm
+// weights (f32 [Hd], read when their flag is set) and the RoPE frequencies.
+template <typename T>
+struct FreshArgs {
+    typename T::storage *kw, *vw;
+    const float *wq, *wk, *invFreq;
+    DecodeAttentionConstants c;
+};
+
+struct NoFresh {};
+
+// FRESH: the decode attention block of one token (DecodeAttentionConstants).
+// Q is then the raw projection row; the prologue stages this block's query
+// heads (and, in the block owning key posQ, the key and value heads) in LDS,
+// applies the per-head RMSNorms and RoPE with the reference's rounding after
+// each step, writes the new K/V row to the caches (head group 0 only), and
+// turns the new key into a fifth softmax state (m = q.k, l = 1, O = v) that
+// the merge folds in with the four waves' states. The key loop covers keys
+// below posQ only.
+template <typename T, int LPK, int CPL, int GMAX, int U, bool FRESH = false, typename FA = NoFresh>
 __device__ void fd_partial_fast(const typename T::storage *__restrict__ Q, const typename T::storage *__restrict__ K,
                                 const typename T::storage *__restrict__ V, float *__restrict__ pO,
                                 float *__restrict__ pM, float *__restrict__ pL, const int32_t *__restrict__ position,
-                                const FlashDecodingPartialConstants &p) {
+                                const FlashDecodingPartialConstants &p, const FA &fa = FA{}) {
     constexpr int kV = pk::Vec<T>::kVec;
     constexpr int DL = CPL * kV;   // dims per lane
     constexpr int HD = LPK * DL;   // head dim
     constexpr int KPW = 64 / LPK;  // key rows per wave-wide load
     constexpr int TILE = KPW * U;  // keys per wave step
+    constexpr int NSLOTS = kWaves + (FRESH ? 1 : 0);
+    constexpr int kUnits = FRESH ? GMAX + 2 : 1;  // query heads, key head, value head
 
-    __shared__ float sm_m[kWaves][GMAX];
-    __shared__ float sm_l[kWaves][GMAX];
-    __shared__ float sm_o[kWaves][GMAX][HD];
+    __shared__ float sm_m[NSLOTS][GMAX];
+    __shared__ float sm_l[NSLOTS][GMAX];
+    __shared__ float sm_o[NSLOTS][GMAX][HD];
+    __shared__ float sm_x[kUnits][FRESH ? HD : 1];
+    __shared__ float sm_ss[kUnits];
 
-    const FdGeom geo = fd_geometry(p, position, GMAX);
+    const FdGeom geo = fd_geometry(p, position, GMAX, FRESH);
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t kg = lane / LPK, dl = lane % LPK;
     const uint32_t G = p.Nq / p.Nkv;
     const uint32_t stride = p.kvStride ? p.kvStride : p.Sk;
+    const uint64_t kvbase = (uint64_t)(geo.b * p.Nkv + geo.hkv) * stride * HD;
+
+    if constexpr (FRESH) {
+        const DecodeAttentionConstants &c = fa.c;
+        const typename T::storage *row = Q + (uint64_t)geo.b * c.rowStride;
+        const uint32_t hq0 = geo.hkv * G + geo.g0;
+        auto live = [&](uint32_t u) { return u < (uint32_t)GMAX ? u < geo.gcount : geo.owner; };
+        auto src = [&](uint32_t u) {
+            return u < (uint32_t)GMAX ? row + (uint64_t)(hq0 + u) * HD
+                 : u == (uint32_t)GMAX ? row + (uint64_t)(p.Nq + geo.hkv) * HD
+                                       : row + (uint64_t)(p.Nq + p.Nkv + geo.hkv) * HD;
+        };
+        for (uint32_t idx = threadIdx.x; idx < (uint32_t)(kUnits * HD); idx += blockDim.x) {
+            const uint32_t u = idx / HD, d = idx % HD;
+            if (live(u)) sm_x[u][d] = T::load(src(u)[d]);
+        }
+        __syncthreads();
+        for (uint32_t u = wave; u < (uint32_t)kUnits; u += kWaves) {
+            if (!live(u)) continue;
+            float acc = 0.0f;
+            for (uint32_t d = lane; d < (uint32_t)HD; d += 64) acc += sm_x[u][d] * sm_x[u][d];
+            acc = pk::wave_sum(acc);
+            if (lane == 0) sm_ss[u] = acc;
+        }
+        __syncthreads();
+        // one thread per (unit, rotation pair i, i + Hd/2): reads and writes
+        // only its own two elements
+        constexpr uint32_t H2 = HD / 2;
+        const int32_t pos = (int32_t)geo.posQ;
+        auto rnd = [](float x) { return T::load(T::store(x)); };
+        for (uint32_t idx = threadIdx.x; idx < (uint32_t)kUnits * H2; idx += blockDim.x) {
+            const uint32_t u = idx / H2, i = idx % H2;
+            if (!live(u)) continue;
+            const bool isQ = u < (uint32_t)GMAX, isK = u == (uint32_t)GMAX;
+            float x1 = sm_x[u][i], x2 = sm_x[u][i + H2];
+            if (c.flags & (isQ ? 1u : isK ? 2u : 4u)) {
+                // RMSNorm.metal: (x * rsqrt(mean(x^2) + eps)) * w
+                const float scale = 1.0f / sqrtf(sm_ss[u] / (float)HD + c.eps);
+                x1 *= scale;
+                x2 *= scale;
+                if (isQ || isK) {  // the value norm has no weight
+                    const float *w = isQ ? fa.wq : fa.wk;
+                    x1 *= w[i];
+                    x2 *= w[i + H2];
+                }
+                x1 = rnd(x1);
+                x2 = rnd(x2);
+            }
+            if ((c.flags & 8u) && u <= (uint32_t)GMAX) {
+                // RopeBuildCosSin.metal:17-20, RopeApply.metal:36-37
+                const float angle = (float)pos * fa.invFreq[i];
+                float sn, cs;
+                sincosf(angle, &sn, &cs);
+                cs *= c.ropeScaling;
+                sn *= c.ropeScaling;
+                const float o1 = x1 * cs - x2 * sn, o2 = x1 * sn + x2 * cs;
+                x1 = rnd(o1);
+                x2 = rnd(o2);
+            }
+            sm_x[u][i] = x1;
+            sm_x[u][i + H2] = x2;
+            if (!isQ && geo.g0 == 0) {
+                typename T::storage *dst = (isK ? fa.kw : fa.vw) + kvbase + (uint64_t)pos * HD;
+                dst[i] = T::store(x1);
+                dst[i + H2] = T::store(x2);
+            }
+        }
+        __syncthreads();
+        // the new key's state per query head: m = q.k, l = 1, O = v
+        for (uint32_t g = wave; g < (uint32_t)GMAX; g += kWaves) {
+            const bool has = geo.owner && g < geo.gcount;
+            float acc = 0.0f;
+            if (has) {
+                for (uint32_t d = lane; d < (uint32_t)HD; d += 64) acc += (sm_x[g][d] * p.scale) * sm_x[GMAX][d];
+                acc = pk::wave_sum(acc);
+            }
+            if (lane == 0) {
+                sm_m[kWaves][g] = has ? acc : -INFINITY;
+                sm_l[kWaves][g] = has ? 1.0f : 0.0f;
+            }
+            for (uint32_t d = lane; d < (uint32_t)HD; d += 64) sm_o[kWaves][g][d] = has ? sm_x[GMAX + 1][d] : 0.0f;
+        }
+    }
 
     float q[GMAX][DL], o[GMAX][DL], m[GMAX], l[GMAX];
 #pragma unroll
@@ -135,21 +249,31 @@ __device__ void fd_partial_fast(const typename T::storage *__restrict__ Q, const
         m[g] = -INFINITY;
         l[g] = 0.0f;
         const uint32_t gg = min((uint32_t)g, geo.gcount - 1);
-        const uint32_t hq = geo.hkv * G + geo.g0 + gg;
-        const typename T::storage *qrow = Q + ((uint64_t)(geo.b * p.Nq + hq) * geo.Sq + geo.qi) * HD;
+        if constexpr (FRESH) {
 #pragma unroll
-        for (int c = 0; c < CPL; ++c) {
-            pk::Vec<T> v;
-            v.load(qrow + (c * LPK + dl) * kV);
+            for (int c = 0; c < CPL; ++c) {
 #pragma unroll
-            for (int e = 0; e < kV; ++e) {
-                q[g][c * kV + e] = v.get(e) * p.scale;
-                o[g][c * kV + e] = 0.0f;
+                for (int e = 0; e < kV; ++e) {
+                    q[g][c * kV + e] = sm_x[gg][(c * LPK + dl) * kV + e] * p.scale;
+                    o[g][c * kV + e] = 0.0f;
+                }
+            }
+        } else {
+            const uint32_t hq = geo.hkv * G + geo.g0 + gg;
+            const typename T::storage *qrow = Q + ((uint64_t)(geo.b * p.Nq + hq) * geo.Sq + geo.qi) * HD;
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) {
+                pk::Vec<T> v;
+                v.load(qrow + (c * LPK + dl) * kV);
+#pragma unroll
+                for (int e = 0; e < kV; ++e) {
+                    q[g][c * kV + e] = v.get(e) * p.scale;
+                    o[g][c * kV + e] = 0.0f;
+                }
             }
         }
     }
 
-    const uint64_t kvbase = (uint64_t)(geo.b * p.Nkv + geo.hkv) * stride * HD;
     const typename T::storage *Kh = K + kvbase;
     const typename T::storage *Vh = V + kvbase;
     const uint32_t nkeys = geo.jHi - geo.jLo;
@@ -248,7 +372,7 @@ __device__ void fd_partial_fast(const typename T::storage *__restrict__ Q, const
         }
     }
     __syncthreads();
-    fd_merge_store<GMAX, HD>(p, geo, sm_m, sm_l, sm_o, pO, pM, pL);
+    fd_merge_store<GMAX, HD, NSLOTS>(p, geo, sm_m, sm_l, sm_o, pO, pM, pL);
 }
 
 // Any head dim <= 512 and any dtype: one query head per block (GMAX = 1),
@@ -405,6 +529,15 @@ __device__ void fd_reduce(const float *__restrict__ pO, const float *__restrict_
         fd_partial_fast<T, LPK, CPL, G, U>(q, k, v, pO, pM, pL, position, p);                               \
     }
 
+#define FD_FRESH(name, T, LPK, CPL, G, U)                                                                  \
+    POPCORN_KERNEL void __launch_bounds__(256)                                                             \
+        name(const T::storage *qkv, T::storage *k, T::storage *v, float *pO, float *pM, float *pL,          \
+             const int32_t *position, const float *wq, const float *wk, const float *invFreq,                \
+             FlashDecodingPartialConstants p, DecodeAttentionConstants c) {                                 \
+        FreshArgs<T> fa{k, v, wq, wk, invFreq, c};                                                          \
+        fd_partial_fast<T, LPK, CPL, G, U, true>(qkv, k, v, pO, pM, pL, position, p, fa);                   \
+    }
+
 #define FD_GENERIC(name, T)                                                                                 \
     POPCORN_KERNEL void __launch_bounds__(256)                                                             \
         name(const T::storage *q, const T::storage *k, const T::storage *v, float *pO, float *pM, float *pL, \
@@ -435,13 +568,18 @@ FD_REDUCE(flash_decoding_reduce_f16, F16)
 // f32 (4 dims per chunk): Hd 64 -> LPK 16, 128 -> 32, 256 -> 64, 512 -> 64 with CPL 2.
 // U (key rows per lane in flight, each for K and V) shrinks as G grows to keep
 // the per-lane state (q, o for G heads) within the register file.
-#define FD_FAST_G4(T, t, LPK, CPL, U1, U2, U4)                                        \
-    FD_FAST(flash_decoding_partial_##t##_l##LPK##_c##CPL##_g1, T, LPK, CPL, 1, U1)    \
-    FD_FAST(flash_decoding_partial_##t##_l##LPK##_c##CPL##_g2, T, LPK, CPL, 2, U2)    \
-    FD_FAST(flash_decoding_partial_##t##_l##LPK##_c##CPL##_g4, T, LPK, CPL, 4, U4)
+// Each partial kernel has a fresh-key twin (flash_decoding_fresh_*) for the
+// decode attention block.
+#define FD_BOTH(T, t, LPK, CPL, G, U)                                                \
+    FD_FAST(flash_decoding_partial_##t##_l##LPK##_c##CPL##_g##G, T, LPK, CPL, G, U)  \
+    FD_FRESH(flash_decoding_fresh_##t##_l##LPK##_c##CPL##_g##G, T, LPK, CPL, G, U)
+#define FD_FAST_G4(T, t, LPK, CPL, U1, U2, U4) \
+    FD_BOTH(T, t, LPK, CPL, 1, U1)              \
+    FD_BOTH(T, t, LPK, CPL, 2, U2)              \
+    FD_BOTH(T, t, LPK, CPL, 4, U4)
 #define FD_FAST_G(T, t, LPK, CPL, U1, U2, U4, U8) \
     FD_FAST_G4(T, t, LPK, CPL, U1, U2, U4)         \
-    FD_FAST(flash_decoding_partial_##t##_l##LPK##_c##CPL##_g8, T, LPK, CPL, 8, U8)
+    FD_BOTH(T, t, LPK, CPL, 8, U8)
 
 // Head dim 512 stops at G = 4 (the LDS merge buffer is 4 x G x Hd floats).
 FD_FAST_G(BF16, bf16, 8, 1, 2, 2, 2, 1)

@@ -595,6 +595,40 @@ popcorn_status_t popcorn_kernel_gated_mlp_residual(const popcorn_tensor_t *x_in,
     });
 }
 
+popcorn_status_t popcorn_kernel_decode_attention(const popcorn_decode_attention_args_t *args, popcorn_kernel_t *kernel) {
+    return guarded([&] {
+        need(args, "args");
+        Tensor t[8];
+        const popcorn_tensor_t *src[8] = {args->qkv,    args->k_cache, args->v_cache, args->out,
+                                          args->position, args->q_norm, args->k_norm, args->inv_freq};
+        const Tensor *p[8];
+        for (int i = 0; i < 8; ++i) {
+            p[i] = nullptr;
+            if (src[i]) {
+                t[i] = Tensor::fromC(*src[i]);
+                p[i] = &t[i];
+            }
+        }
+        Kernels::DecodeAttentionArgs a;
+        a.qkv = p[0];
+        a.kCache = p[1];
+        a.vCache = p[2];
+        a.out = p[3];
+        a.position = p[4];
+        a.qNorm = p[5];
+        a.kNorm = p[6];
+        a.invFreq = p[7];
+        a.vNorm = args->v_norm != 0;
+        a.queryHeads = args->query_heads;
+        a.kvHeads = args->kv_heads;
+        a.eps = args->eps;
+        a.scale = args->scale;
+        a.ropeScaling = args->rope_scaling;
+        a.mask = AttentionMask{args->mask.kind, args->mask.window};
+        emit(kernel, Kernels::DecodeAttention(a));
+    });
+}
+
 popcorn_status_t popcorn_kernel_decode_matvec(const popcorn_decode_matvec_args_t *args, popcorn_kernel_t *kernel) {
     return guarded([&] {
         need(args, "args");

@@ -95,6 +95,45 @@ struct AttnDims {
     int64_t B, Nq, Nkv, Sq, Sk, Hd, cap;
 };
 
+// The split-KV launch plan: the fast kernel's lanes per key row (0 = the
+// generic kernel), chunks per lane, query heads per block, head groups per
+// KV head and partitions per query row.
+struct FdPlan {
+    int lpk = 0, cpl = 1, gmax = 1;
+    int64_t ngroups = 1, P = 1;
+    std::string suffix() const {  // "<t>_l<LPK>_c<CPL>_g<G>" without the dtype
+        return "_l" + std::to_string(lpk) + "_c" + std::to_string(cpl) + "_g" + std::to_string(gmax);
+    }
+};
+
+FdPlan fdPlan(DataType t, const AttnDims &d, bool alignedOk, int64_t keys) {
+    FdPlan f;
+    const int64_t G = d.Nq / d.Nkv;
+    const int kV = 16 / stride(t);
+    if (alignedOk && d.Hd % kV == 0) {
+        const int64_t chunks = d.Hd / kV;
+        if (chunks == 8 || chunks == 16 || chunks == 32 || chunks == 64) f.lpk = (int)chunks;
+        if (chunks == 128 && t == DataType::f32) {
+            f.lpk = 64;
+            f.cpl = 2;
+        }
+        if (t == DataType::f32 && chunks == 8) f.lpk = 0;  // f32 Hd 32: generic
+    }
+    if (f.lpk) {
+        f.gmax = G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : 8;
+        if (d.Hd == 512 && f.gmax > 4) f.gmax = 4;  // 4 waves x G x Hd f32 of LDS stays <= 32 KB
+    }
+    f.ngroups = cdiv(G, f.gmax);
+    // Partitions: enough blocks to cover every CU fdBlocksPerCU() times,
+    // but at least fdMinKeys() keys per block (the reference fixes P = 8,
+    // FlashDecoding.swift:77).
+    const int64_t base = d.B * d.Nkv * f.ngroups * d.Sq;
+    const int64_t want = cdiv(fdBlocksPerCU() * deviceCUs(), base);
+    const int64_t maxByKeys = cdiv(std::max<int64_t>(keys, 1), fdMinKeys());
+    f.P = std::clamp<int64_t>(std::min(want, maxByKeys), 1, 1024);
+    return f;
+}
+
 class FlashAttentionKernel : public Kernel {
 public:
     FlashAttentionKernel(const Tensor &q, const Tensor &k, const Tensor &v, const Tensor &out, AttnDims d, float scale,
@@ -218,39 +257,12 @@ public:
 private:
     void planSplit() {
         const DataType t = q_.dataType;
-        const int64_t G = d_.Nq / d_.Nkv;
-        const int es = stride(t);
-        const int kV = 16 / es;
-        int lpk = 0, cpl = 1;
         const bool alignedOk = aligned16(q_.data) && aligned16(k_.data) && aligned16(v_.data);
-        if (alignedOk && d_.Hd % kV == 0) {
-            const int64_t chunks = d_.Hd / kV;
-            if (chunks == 8 || chunks == 16 || chunks == 32 || chunks == 64) lpk = (int)chunks;
-            if (chunks == 128 && t == DataType::f32) {
-                lpk = 64;
-                cpl = 2;
-            }
-            if (t == DataType::f32 && chunks == 8) lpk = 0;  // f32 Hd 32: generic
-        }
-        int gmax = 1;
-        if (lpk) {
-            gmax = G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : 8;
-            if (d_.Hd == 512 && gmax > 4) gmax = 4;  // 4 waves x G x Hd f32 of LDS stays <= 32 KB
-            partialName_ = std::string("flash_decoding_partial_") + tag(t) + "_l" + std::to_string(lpk) + "_c" +
-                           std::to_string(cpl) + "_g" + std::to_string(gmax);
-        } else {
-            partialName_ = std::string("flash_decoding_partial_") + tag(t);
-        }
+        const FdPlan f = fdPlan(t, d_, alignedOk, hasPos_ ? d_.cap : d_.Sk);
+        partialName_ = std::string("flash_decoding_partial_") + tag(t) + (f.lpk ? f.suffix() : std::string());
         reduceName_ = std::string("flash_decoding_reduce_") + tag(out_.dataType);
-        ngroups_ = cdiv(G, gmax);
-        // Partitions: enough blocks to cover every CU fdBlocksPerCU() times,
-        // but at least fdMinKeys() keys per block (the reference fixes P = 8,
-        // FlashDecoding.swift:77).
-        const int64_t keys = std::max<int64_t>(hasPos_ ? d_.cap : d_.Sk, 1);
-        const int64_t base = d_.B * d_.Nkv * ngroups_ * d_.Sq;
-        const int64_t want = cdiv(fdBlocksPerCU() * deviceCUs(), base);
-        const int64_t maxByKeys = cdiv(keys, fdMinKeys());
-        P_ = std::clamp<int64_t>(std::min(want, maxByKeys), 1, 1024);
+        ngroups_ = f.ngroups;
+        P_ = f.P;
     }
 
     Tensor q_, k_, v_, out_, pos_;
@@ -261,6 +273,129 @@ private:
     Kernels::AttentionPath path_ = Kernels::AttentionPath::plain;
     std::string partialName_, reduceName_, tiledName_;
     int64_t ngroups_ = 1, P_ = 1;
+};
+
+// The attention block of one decode token (DecodeAttentionConstants): the
+// fresh-key split-KV partial kernel, then the same LSE combine.
+class DecodeAttentionKernel : public Kernel {
+public:
+    explicit DecodeAttentionKernel(const Kernels::DecodeAttentionArgs &a) {
+        if (!a.qkv || !a.kCache || !a.vCache || !a.out || !a.position)
+            throw Error::invalidArgument("DecodeAttention needs qkv, both caches, out and position");
+        qkv_ = *a.qkv;
+        k_ = *a.kCache;
+        v_ = *a.vCache;
+        out_ = *a.out;
+        pos_ = *a.position;
+        if (k_.shape.rank() != 4) throw Error::tensorInvalidRank(4, k_.shape.rank());
+        if (v_.shape != k_.shape) throw Error::tensorShapeMismatch("DecodeAttention K and V caches must have one shape.");
+        d_.B = k_.shape[0];
+        d_.Nkv = k_.shape[1];
+        d_.cap = k_.shape[2];
+        d_.Hd = k_.shape[3];
+        d_.Nq = a.queryHeads;
+        d_.Sq = 1;
+        d_.Sk = d_.cap;
+        if (d_.Nkv != a.kvHeads) throw Error::tensorShapeMismatch("DecodeAttention kv_heads must match the caches' dim 1.");
+        if (d_.Nkv <= 0 || d_.Nq <= 0 || d_.Nq % d_.Nkv != 0)
+            throw Error::tensorShapeMismatch("DecodeAttention query heads must be a positive multiple of the KV heads.");
+        if (d_.B <= 0 || d_.cap <= 0 || d_.Hd <= 0 || d_.Hd % 2 != 0)
+            throw Error::tensorShapeMismatch("DecodeAttention needs B, capacity > 0 and an even head dim.");
+        if (a.mask.kind > 2) throw Error::invalidArgument("unknown attention mask kind");
+        const DataType t = k_.dataType;
+        if (!isFloat(t) || qkv_.dataType != t || v_.dataType != t || !(out_.dataType == t || out_.dataType == DataType::f32))
+            throw Error::unsupportedDataTypeCombination("DecodeAttention: qkv and the caches of one float dtype, out of it or f32.");
+        if (pos_.dataType != DataType::i32) throw Error::unsupportedDataTypeCombination("position tensor must be i32");
+        requireElements(pos_, 1, "position");
+        const int64_t rowStride = (d_.Nq + 2 * d_.Nkv) * d_.Hd;
+        requireElements(qkv_, d_.B * rowStride, "DecodeAttention qkv");
+        requireElements(k_, d_.B * d_.Nkv * d_.cap * d_.Hd, "DecodeAttention k_cache");
+        requireElements(out_, d_.B * d_.Nq * d_.Hd, "DecodeAttention out");
+        auto f32vec = [&](const Tensor *w, int64_t n, const char *what) {
+            if (!w) return;
+            if (w->dataType != DataType::f32) throw Error::unsupportedDataTypeCombination(std::string(what) + " must be f32.");
+            requireElements(*w, n, what);
+        };
+        f32vec(a.qNorm, d_.Hd, "DecodeAttention q_norm");
+        f32vec(a.kNorm, d_.Hd, "DecodeAttention k_norm");
+        f32vec(a.invFreq, d_.Hd / 2, "DecodeAttention inv_freq");
+        dc_.flags = (a.qNorm ? 1u : 0u) | (a.kNorm ? 2u : 0u) | (a.vNorm ? 4u : 0u) | (a.invFreq ? 8u : 0u);
+        dc_.eps = a.eps;
+        dc_.ropeScaling = a.ropeScaling;
+        dc_.rowStride = (uint32_t)rowStride;
+        const Tensor &dummy = qkv_;  // bound in place of an absent optional input; never read
+        wq_ = a.qNorm ? *a.qNorm : dummy;
+        wk_ = a.kNorm ? *a.kNorm : dummy;
+        invf_ = a.invFreq ? *a.invFreq : dummy;
+        mask_ = a.mask;
+        scale_ = a.scale;
+        const bool alignedOk = aligned16(qkv_.data) && aligned16(k_.data) && aligned16(v_.data) && (rowStride * stride(t)) % 16 == 0;
+        plan_ = fdPlan(t, d_, alignedOk, d_.cap);
+        if (!plan_.lpk)
+            throw Error::unsupportedDataTypeCombination(
+                "DecodeAttention needs 16-byte aligned f16/bf16 data with head dim 64, 128, 256 or 512 (f32: 128, 256, 512).");
+        partialName_ = std::string("flash_decoding_fresh_") + tag(t) + plan_.suffix();
+        reduceName_ = std::string("flash_decoding_reduce_") + tag(out_.dataType);
+    }
+
+    std::vector<Binding> tensors() const override {
+        return {{qkv_, kRead}, {k_, kReadWrite}, {v_, kReadWrite}, {out_, kWrite}, {pos_, kRead},
+                {wq_, kRead}, {wk_, kRead}, {invf_, kRead}};
+    }
+    std::string describe() const override { return partialName_ + "," + reduceName_; }
+
+    void encode(KernelCommandEncoder &enc) const override {
+        const int64_t P = plan_.P;
+        const int64_t slots = d_.B * d_.Nq * P;
+        enc.withTemporaryTensor(ScratchSpec{{slots, d_.Hd}, DataType::f32}, [&](Tensor pO) {
+            enc.withTemporaryTensor(ScratchSpec{{slots}, DataType::f32}, [&](Tensor pM) {
+                enc.withTemporaryTensor(ScratchSpec{{slots}, DataType::f32}, [&](Tensor pL) {
+                    FlashDecodingPartialConstants pc{};
+                    pc.B = (uint32_t)d_.B;
+                    pc.Nq = (uint32_t)d_.Nq;
+                    pc.Nkv = (uint32_t)d_.Nkv;
+                    pc.Sk = (uint32_t)d_.cap;
+                    pc.Hd = (uint32_t)d_.Hd;
+                    pc.P = (uint32_t)P;
+                    pc.maskKind = mask_.kind;
+                    pc.slidingWindow = mask_.kind == 1 ? mask_.window : -1;
+                    pc.scale = scale_;
+                    pc.kvStride = (uint32_t)d_.cap;
+                    pc.Sq = 1;
+                    pc.keyLenFromPosition = 1;
+                    DispatchSize ds;
+                    ds.grid = dim3((unsigned)P, (unsigned)(d_.B * d_.Nkv * plan_.ngroups), 1);
+                    ds.block = dim3(kBlock, 1, 1);
+                    FixedDispatch partial(partialName_,
+                                          {{qkv_, kRead}, {k_, kReadWrite}, {v_, kReadWrite}, {pO, kWrite}, {pM, kWrite},
+                                           {pL, kWrite}, {pos_, kRead}, {wq_, kRead}, {wk_, kRead}, {invf_, kRead}},
+                                          {bytesOf(pc), bytesOf(dc_)}, ds);
+                    enc.dispatch(partial);
+                    FlashDecodingReduceConstants rc{};
+                    rc.B = (uint32_t)d_.B;
+                    rc.Nq = (uint32_t)d_.Nq;
+                    rc.Hd = (uint32_t)d_.Hd;
+                    rc.P = (uint32_t)P;
+                    rc.Sq = 1;
+                    DispatchSize rs;
+                    rs.grid = dim3((unsigned)(d_.B * d_.Nq), (unsigned)cdiv(d_.Hd, 64), 1);
+                    rs.block = dim3(kBlock, 1, 1);
+                    FixedDispatch reduce(reduceName_, {{pO, kRead}, {pM, kRead}, {pL, kRead}, {out_, kWrite}},
+                                         {bytesOf(rc)}, rs);
+                    enc.dispatch(reduce);
+                });
+            });
+        });
+    }
+
+private:
+    Tensor qkv_, k_, v_, out_, pos_, wq_, wk_, invf_;
+    AttnDims d_{};
+    DecodeAttentionConstants dc_{};
+    AttentionMask mask_{0, -1};
+    float scale_ = 1.0f;
+    FdPlan plan_;
+    std::string partialName_, reduceName_;
 };
 
 // ---------------------------------------------------------------------------
@@ -886,6 +1021,8 @@ std::unique_ptr<Kernel> GatedMLPResidual(const Tensor &xIn, const Tensor &delta,
     k->setResidual(delta, wPost, xOut);
     return k;
 }
+
+std::unique_ptr<Kernel> DecodeAttention(const DecodeAttentionArgs &a) { return std::make_unique<DecodeAttentionKernel>(a); }
 
 std::unique_ptr<Kernel> DecodeMatvec(const DecodeMatvecArgs &a) {
     if (!a.x || !a.weight || !a.out) throw Error::invalidArgument("DecodeMatvec needs x, weight and out");

@@ -349,6 +349,25 @@ struct DecodeMatvecArgs {
 };
 std::unique_ptr<Kernel> DecodeMatvec(const DecodeMatvecArgs &args);
 
+// The attention block of one decode token (DecodeAttentionConstants): raw
+// projections in, per-head norms and RoPE, the new K/V row written to the
+// caches at position[0], split-KV attention over keys 0..position[0].
+struct DecodeAttentionArgs {
+    const Tensor *qkv = nullptr;      // [B, (Nq + 2 Nkv) * Hd]
+    const Tensor *kCache = nullptr;   // [B, Nkv, S, Hd]
+    const Tensor *vCache = nullptr;
+    const Tensor *out = nullptr;      // [B, Nq, 1, Hd]
+    const Tensor *position = nullptr; // i32 [1]
+    const Tensor *qNorm = nullptr;    // f32 [Hd] or absent
+    const Tensor *kNorm = nullptr;    // f32 [Hd] or absent
+    const Tensor *invFreq = nullptr;  // f32 [Hd/2] or absent (no RoPE)
+    bool vNorm = false;
+    int64_t queryHeads = 0, kvHeads = 0;
+    float eps = 1e-6f, scale = 1.0f, ropeScaling = 1.0f;
+    AttentionMask mask{0, -1};
+};
+std::unique_ptr<Kernel> DecodeAttention(const DecodeAttentionArgs &args);
+
 std::unique_ptr<Kernel> EmbeddingGather(const Tensor &ids, const Tensor &table, const Tensor &out);
 std::unique_ptr<Kernel> Argmax(const Tensor &x, const Tensor &indices);
 

@@ -551,6 +551,30 @@ class Kernels:
         return _make(lib().popcorn_kernel_decode_matvec, C.byref(a), refs=list(ts.values()))
 
     @staticmethod
+    def DecodeAttention(qkv: Tensor, k_cache: Tensor, v_cache: Tensor, into: Tensor, position: Tensor, *,
+                        query_heads: int, kv_heads: int, scale: float, q_norm: Optional[Tensor] = None,
+                        k_norm: Optional[Tensor] = None, v_norm: bool = False, inv_freq: Optional[Tensor] = None,
+                        rope_scaling: float = 1.0, eps: float = 1e-6,
+                        mask: AttentionMask = AttentionMask(0)) -> Kernel:
+        """One decode token's attention block with its per-head glue (popcorn_decode_attention_args_t):
+        the reference's RMSNorm/RopeApply/Transpose12/KVCacheWrite/FlashAttention sequence
+        (Gemma4TextInference.swift:352-399) as two dispatches."""
+        ts = dict(qkv=qkv, k_cache=k_cache, v_cache=v_cache, out=into, position=position, q_norm=q_norm,
+                  k_norm=k_norm, inv_freq=inv_freq)
+        descs = {n: (t.desc() if t is not None else None) for n, t in ts.items()}
+        a = _capi.DecodeAttentionArgs()
+        for n, d in descs.items():
+            setattr(a, n, C.pointer(d) if d is not None else None)
+        a.v_norm = int(v_norm)
+        a.query_heads = query_heads
+        a.kv_heads = kv_heads
+        a.eps = eps
+        a.scale = scale
+        a.rope_scaling = rope_scaling
+        a.mask = mask.desc()
+        return _make(lib().popcorn_kernel_decode_attention, C.byref(a), refs=list(ts.values()))
+
+    @staticmethod
     def EmbeddingGather(ids: Tensor, table: Tensor, into: Tensor) -> Kernel:
         return _make(lib().popcorn_kernel_embedding_gather, _d(ids), _d(table), _d(into), refs=(ids, table, into))
 

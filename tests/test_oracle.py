@@ -429,7 +429,10 @@ def test_argmax_and_gather_kats(oracle):
     assert oracle.argmax(x).tolist() == [1, 0]
 
 
-def test_decoder_layer_vs_float64(oracle):
+@pytest.mark.parametrize("real_block", [False, True])
+def test_decoder_layer_vs_float64(oracle, real_block):
+    # real_block adds the per-head q/k norms, the weightless v norm and RoPE
+    # (Gemma4TextInference.swift:352-371)
     rng = np.random.default_rng(40)
     H, Nq, Nkv, Hd, F, cap, pos = 64, 4, 2, 16, 128, 12, 9
     W = {
@@ -439,23 +442,38 @@ def test_decoder_layer_vs_float64(oracle):
         "up": 0.1 * rng.standard_normal((F, H)), "down": 0.1 * rng.standard_normal((H, F)),
         "post_ffn_norm": 1 + 0.1 * rng.standard_normal(H),
     }
+    if real_block:
+        W["q_norm"] = 1 + 0.1 * rng.standard_normal(Hd)
+        W["k_norm"] = 1 + 0.1 * rng.standard_normal(Hd)
+        W["inv_freq"] = _gemma_inv_freq(Hd)
     W = {n: w.astype(np.float32) for n, w in W.items()}
     x = rng.standard_normal(H).astype(np.float32)
     kc = rng.standard_normal((Nkv, cap, Hd)).astype(np.float32)
     vc = rng.standard_normal((Nkv, cap, Hd)).astype(np.float32)
     x0, kc0, vc0 = x.copy(), kc.copy(), vc.copy()
     oracle.decoder_layer(W, x, kc, vc, pos, H=H, Nq=Nq, Nkv=Nkv, Hd=Hd, F=F, eps=1e-6, scale=0.25,
-                         act_tag=oracle.F32)
+                         act_tag=oracle.F32, v_norm=real_block, rope_scaling=1.0)
 
-    def rms(t, w):
-        return t / np.sqrt((t**2).mean() + 1e-6) * w
+    def rms(t, w=1.0):
+        return t / np.sqrt((t**2).mean(axis=-1, keepdims=True) + 1e-6) * w
+
+    def rope(t):  # rows [n, Hd]: pair (i, i + Hd/2) turned by pos * inv_freq[i]
+        ang = np.float64(np.float32(pos) * W["inv_freq"])
+        h = Hd // 2
+        a, b = t[:, :h], t[:, h:]
+        return np.concatenate([a * np.cos(ang) - b * np.sin(ang), a * np.sin(ang) + b * np.cos(ang)], axis=1)
 
     W64 = {n: w.astype(np.float64) for n, w in W.items()}
     xx = x0.astype(np.float64)
     qkv = W64["qkv"] @ rms(xx, W64["in_norm"])
-    q = qkv[:Nq * Hd].reshape(1, Nq, 1, Hd)
-    kc0[:, pos] = qkv[Nq * Hd:(Nq + Nkv) * Hd].reshape(Nkv, Hd)
-    vc0[:, pos] = qkv[(Nq + Nkv) * Hd:].reshape(Nkv, Hd)
+    qh = qkv[:Nq * Hd].reshape(Nq, Hd)
+    kh = qkv[Nq * Hd:(Nq + Nkv) * Hd].reshape(Nkv, Hd)
+    vh = qkv[(Nq + Nkv) * Hd:].reshape(Nkv, Hd)
+    if real_block:
+        qh, kh, vh = rope(rms(qh, W64["q_norm"])), rope(rms(kh, W64["k_norm"])), rms(vh)
+    q = qh.reshape(1, Nq, 1, Hd)
+    kc0[:, pos] = kh
+    vc0[:, pos] = vh
     np.testing.assert_allclose(kc[:, :pos + 1], kc0[:, :pos + 1], rtol=1e-5, atol=1e-6)
     att = _attention_f64(q, kc0[None].astype(np.float64), vc0[None].astype(np.float64), 0.25, key_len=pos + 1)
     xx = xx + rms(W64["o"] @ att.ravel(), W64["post_attn_norm"])
