@@ -50,6 +50,8 @@ def kernel_bytes(cfg, name, pos):
         return V * H * 2 + 3 * H * 2 + 2 * H * 4 + V * 4
     if name.startswith("flash_decoding_partial"):
         return 2 * KW * (pos + 1) * 2 + 2 * QW * 2  # K and V rows + q
+    if name.startswith("flash_decoding_fresh"):  # K and V rows, raw q/k/v, new K/V row, norm weights
+        return 2 * KW * pos * 2 + QKV * 2 + 2 * KW * 2 + 2 * cfg.head_dim * 4
     return None
 
 
@@ -227,6 +229,47 @@ def prefill_config5(pa, lib, stream, enc, reps=8):
     return rows
 
 
+def time_decode(pa, dec, stream, token, steps, warmup, use_graph):
+    """Warmup (captures the graph), then `steps` timed decode steps from the
+    same start; seconds, the larger of the wall clock and the HIP events."""
+    dec.reset(token, START_POS)
+    dec.step(warmup, use_graph=use_graph)
+    stream.synchronize()
+    dec.reset(token, START_POS)
+    pa.synchronize()
+    start, stop = pa.Event(), pa.Event()
+    t0 = time.perf_counter()
+    start.record(stream)
+    dec.step(steps, use_graph=use_graph)
+    stop.record(stream)
+    stop.synchronize()
+    pa.synchronize()
+    wall = time.perf_counter() - t0
+    elapsed = max(wall, start.elapsed_ms(stop) / 1e3)
+    tok, pos = dec.read()
+    assert pos == START_POS + steps, (pos, steps)
+    return elapsed
+
+
+def attention_block_decode(pa, lib, stream, D, token, steps, warmup, graph_steps, use_graph, reps):
+    """The same decode with a real attention block (per-head q/k RMSNorm, v
+    RMSNorm, RoPE at theta 10000, Gemma4TextInference.swift:352-371) folded
+    into the attention partial kernel: tok/s and the fused kernel's time."""
+    cfg = D.DecoderConfig(graph_steps=graph_steps, attention_block=1)
+    dec = D.Decoder(lib, stream, cfg)
+    dec.randomize(seed=0)
+    elapsed = time_decode(pa, dec, stream, token, steps, warmup, use_graph)
+    names, nd = dec.describe()
+    fresh = next(n for n in names if n.startswith("flash_decoding_fresh_"))
+    dec.reset(token, START_POS)
+    ms, _ = dec.time_kernel(fresh, reps=reps)
+    nbytes = kernel_bytes(cfg, fresh, START_POS)
+    dec.close()
+    return {"tok_s": round(steps / elapsed, 2), "ms_per_step": round(elapsed * 1e3 / steps, 4),
+            "dispatches_per_step": nd, "attention_kernel": fresh, "attention_us": round(ms * 1e3, 2),
+            "attention_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 3) if nbytes else None}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -238,6 +281,8 @@ def main():
     ap.add_argument("--kernel-reps", type=int, default=4)
     ap.add_argument("--no-fd-sweep", action="store_true", help="skip the config-2 FlashDecoding sweep")
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-5 prefill measurement")
+    ap.add_argument("--no-attention-block", action="store_true",
+                    help="skip the decode with per-head norms and RoPE (a real attention block)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 3 device-to-device copies of 1 GiB (the known-size kernel that scales the "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -266,24 +311,7 @@ def main():
     if START_POS + max(args.steps, args.warmup) > cfg.max_seq:
         raise SystemExit(f"steps above {cfg.max_seq - START_POS} leave the KV cache")
 
-    # warmup (captures the graph), then the timed region from the same start
-    dec.reset(token, START_POS)
-    dec.step(args.warmup, use_graph=use_graph)
-    stream.synchronize()
-    dec.reset(token, START_POS)
-    pa.synchronize()
-    start, stop = pa.Event(), pa.Event()
-    t0 = time.perf_counter()
-    start.record(stream)
-    dec.step(args.steps, use_graph=use_graph)
-    stop.record(stream)
-    stop.synchronize()
-    pa.synchronize()
-    wall = time.perf_counter() - t0
-    gpu_ms = start.elapsed_ms(stop)
-    elapsed = max(wall, gpu_ms / 1e3)
-    tok, pos = dec.read()
-    assert pos == START_POS + args.steps, (pos, args.steps)
+    elapsed = time_decode(pa, dec, stream, token, args.steps, args.warmup, use_graph)
     tokens_per_s = args.steps / elapsed
     mean_pos = START_POS + (args.steps - 1) / 2
     step_bytes = dec.step_bytes(int(mean_pos))
@@ -318,6 +346,11 @@ def main():
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(dec, cfg, stream, token)
 
+    block = None
+    if not args.no_attention_block:
+        block = attention_block_decode(pa, lib, stream, D, token, args.steps, args.warmup, args.graph_steps,
+                                       use_graph, args.kernel_reps)
+
     line = {
         "metric": "decode tok/s (Gemma-2B shape, ctx 4K)",
         "value": round(tokens_per_s, 2),
@@ -341,6 +374,7 @@ def main():
         "kernels": kernels,
         "flash_decoding_config2": fd,
         "prefill_config5": prefill,
+        "decode_attention_block": block,
         "cpu_baseline": cpu,
     }
     dec.close()

@@ -5,16 +5,22 @@
  *
  * It restates the per-token op sequence of the reference's example app
  * (Examples/GemmaCLI/Sources/GemmaCLI/Gemma4TextInference.swift:172-207 for
- * the forward, :312-436 for a layer) without the parts no configuration here
- * uses (per-head q/k norms, RoPE, per-layer inputs, layer scalars):
+ * the forward, :312-436 for a layer) without the per-layer inputs and layer
+ * scalars:
  *
  *   x = EmbeddingGather(token) * sqrt(H)                       (:184-185)
- *   per layer:  n = RMSNorm(x); qkv = n W_qkv^T; KVCacheWrite(k, v) at pos;
+ *   per layer:  n = RMSNorm(x); qkv = n W_qkv^T;
+ *               [attention_block: q = RoPE(RMSNorm_h(q)), k = RoPE(RMSNorm_h(k)),
+ *                v = RMSNorm_h(v) per head                     (:352-371)]
+ *               KVCacheWrite(k, v) at pos;
  *               a = FlashAttention(q, K[:pos+1], V[:pos+1]); o = a W_o^T;
  *               x = x + RMSNorm(o)                             (:334-404)
  *               x = x + RMSNorm(GatedMLP(x))                   (:408-436)
  *   logits = RMSNorm(x) E^T (tied embedding); token = Argmax(logits)
  *                                                              (:201-206)
+ *
+ * With attention_block = 0 the layer is the benchmark layer of the headline
+ * decode configuration (no per-head norms or RoPE).
  *
  * The position and the token live in device memory and the step ends with a
  * kernel that advances the position, so a step (or several) is captured once
@@ -42,6 +48,9 @@ typedef struct {
     float attn_scale;     /* attention scale                                     */
     int32_t history_len;  /* ring of generated tokens kept on the device         */
     int32_t graph_steps;  /* decode steps captured per HIP graph (0 = 1)         */
+    int32_t attention_block; /* 1: per-head q/k RMSNorm (f32 weights), v RMSNorm
+                                without weight and RoPE on q and k              */
+    float rope_theta;     /* RoPE base: inv_freq[i] = theta^(-2i/head_dim)       */
 } popcorn_decoder_config_t;
 
 typedef struct popcorn_decoder_s *popcorn_decoder_t;
@@ -56,9 +65,10 @@ popcorn_status_t popcorn_decoder_randomize(popcorn_decoder_t decoder, uint64_t s
 
 /* A view of an internal tensor: "embedding", "final_norm", "w_qkv", "w_o",
  * "w_gate", "w_up", "w_down", "norm_in", "norm_post_attn", "norm_pre_ffn",
- * "norm_post_ffn", "k_cache", "v_cache" (per `layer`), and "x", "logits",
+ * "norm_post_ffn", "k_cache", "v_cache" and, with attention_block, "q_norm"
+ * and "k_norm" (per `layer`); "inv_freq" (attention_block), "x", "logits",
  * "token", "position", "history", plus the last layer's step buffers
- * "q", "attn", "o", "mlp", "hidden". */
+ * "q", "qkv", "attn", "o", "mlp", "hidden". */
 popcorn_status_t popcorn_decoder_tensor(popcorn_decoder_t decoder, const char *name, int32_t layer,
                                         popcorn_tensor_t *tensor);
 

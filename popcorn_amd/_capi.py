@@ -60,7 +60,8 @@ class DecoderConfig(C.Structure):
     _fields_ = [("layers", C.c_int32), ("hidden", C.c_int32), ("query_heads", C.c_int32),
                 ("kv_heads", C.c_int32), ("head_dim", C.c_int32), ("ffn", C.c_int32), ("vocab", C.c_int32),
                 ("max_seq", C.c_int32), ("eps", C.c_float), ("attn_scale", C.c_float),
-                ("history_len", C.c_int32), ("graph_steps", C.c_int32)]
+                ("history_len", C.c_int32), ("graph_steps", C.c_int32), ("attention_block", C.c_int32),
+                ("rope_theta", C.c_float)]
 
 
 _T = C.POINTER(TensorDesc)
@@ -69,12 +70,16 @@ _T = C.POINTER(TensorDesc)
 class DecodeMatvecArgs(C.Structure):
     _fields_ = [(n, _T) for n in ("x", "delta", "w_post", "x_out", "w_pre", "weight", "out", "k_cache", "v_cache",
                                   "position")] + [("q_rows", C.c_int64), ("eps", C.c_float)]
+
+
 class DecodeAttentionArgs(C.Structure):
     _fields_ = [(n, _T) for n in ("qkv", "k_cache", "v_cache", "out", "position", "q_norm", "k_norm",
                                   "inv_freq")] + [("v_norm", C.c_int32), ("query_heads", C.c_int32),
                                                   ("kv_heads", C.c_int32), ("eps", C.c_float),
                                                   ("scale", C.c_float), ("rope_scaling", C.c_float),
                                                   ("mask", AttentionMaskDesc)]
+
+
 _K = C.POINTER(C.c_void_p)
 _st = C.c_int32
 

@@ -51,6 +51,7 @@ struct popcorn_decoder_s {
 
     // weights (bf16 unless noted) and state
     Buffer embedding, finalNorm /*f32*/, wqkv, wo, wg, wu, wd, norms /*f32 [L][4][H]*/;
+    Buffer headNorms /*f32 [L][2][Hd], attention_block*/, invFreq /*f32 [Hd/2]*/;
     Buffer kcache, vcache;
     Buffer x, x2, e, qkv, attn, o, mlp, hidden, logits /*f32*/, token /*i32*/, position /*i32*/, history /*i32*/;
 
@@ -80,19 +81,25 @@ struct popcorn_decoder_s {
         int slot = !strcmp(which, "norm_in") ? 0 : !strcmp(which, "norm_post_attn") ? 1 : !strcmp(which, "norm_pre_ffn") ? 2
                  : !strcmp(which, "norm_post_ffn") ? 3 : -1;
         if (slot >= 0) return Tensor(norms.at(layerOffset(H, l * 4 + slot, 4)), Shape({H}), DataType::f32);
+        const int head = !strcmp(which, "q_norm") ? 0 : !strcmp(which, "k_norm") ? 1 : -1;
+        if (head >= 0 && headNorms.p) return Tensor(headNorms.at(layerOffset(Hd, l * 2 + head, 4)), Shape({Hd}), DataType::f32);
         throw Error::invalidArgument(std::string("unknown decoder tensor ") + which);
     }
 
-    // Five dispatches per layer: the QKV matvec (previous layer's post-FFN
+    // Six dispatches per layer: the QKV matvec (previous layer's post-FFN
     // norm + residual, this layer's input norm, K/V scattered into the caches),
     // split-KV attention with its combine, the O projection, the gate/up
     // matvec (post-attention norm + residual, pre-FFN norm), the down matvec.
-    // The residual stream alternates between x and x2 (blocks of one kernel
-    // read one while block 0 writes the other).
+    // With attention_block the QKV matvec stores the raw projections and the
+    // attention partial kernel applies the per-head norms and RoPE and writes
+    // the K/V row (DecodeAttention). The residual stream alternates between x
+    // and x2 (blocks of one kernel read one while block 0 writes the other).
     void build() {
         const float eps = cfg.eps;
+        const bool block = cfg.attention_block != 0;
         Tensor tx = bf(x.p, {1, H}), tx2 = bf(x2.p, {1, H}), te = bf(e.p, {1, H});
-        Tensor tq = bf(qkv.p, {1, QW});
+        Tensor tq = bf(qkv.p, {1, QW}), tqkv = bf(qkv.p, {1, QKV});
+        Tensor tinv(invFreq.p, Shape({Hd / 2}), DataType::f32);
         Tensor tq4 = bf(qkv.p, {1, Nq, 1, Hd});
         Tensor tattn4 = bf(attn.p, {1, Nq, 1, Hd}), tattn = bf(attn.p, {1, QW});
         Tensor to = bf(o.p, {1, H}), tmlp = bf(mlp.p, {1, H}), th = bf(hidden.p, {F});
@@ -124,14 +131,36 @@ struct popcorn_decoder_s {
             }
             qkvArgs.wPre = &nin;
             qkvArgs.weight = &wqkv_l;
-            qkvArgs.out = &tq;
-            qkvArgs.kCache = &kc;
-            qkvArgs.vCache = &vc;
-            qkvArgs.position = &tpos;
-            qkvArgs.qRows = QW;
             qkvArgs.eps = eps;
-            add(Kernels::DecodeMatvec(qkvArgs));
-            add(Kernels::FlashAttention(tq4, kc, vc, tattn4, 1, Nq, Nkv, 1, 1, Hd, cfg.attn_scale, causal, S, &tpos));
+            if (block) {
+                qkvArgs.out = &tqkv;
+                add(Kernels::DecodeMatvec(qkvArgs));
+                Tensor wqn = weight("q_norm", l), wkn = weight("k_norm", l);
+                Kernels::DecodeAttentionArgs at;
+                at.qkv = &tqkv;
+                at.kCache = &kc;
+                at.vCache = &vc;
+                at.out = &tattn4;
+                at.position = &tpos;
+                at.qNorm = &wqn;
+                at.kNorm = &wkn;
+                at.invFreq = &tinv;
+                at.vNorm = true;
+                at.queryHeads = Nq;
+                at.kvHeads = Nkv;
+                at.eps = eps;
+                at.scale = cfg.attn_scale;
+                at.mask = causal;
+                add(Kernels::DecodeAttention(at));
+            } else {
+                qkvArgs.out = &tq;
+                qkvArgs.kCache = &kc;
+                qkvArgs.vCache = &vc;
+                qkvArgs.position = &tpos;
+                qkvArgs.qRows = QW;
+                add(Kernels::DecodeMatvec(qkvArgs));
+                add(Kernels::FlashAttention(tq4, kc, vc, tattn4, 1, Nq, Nkv, 1, 1, Hd, cfg.attn_scale, causal, S, &tpos));
+            }
             Kernels::DecodeMatvecArgs oArgs;
             oArgs.x = &tattn;
             oArgs.weight = &wo_l;
@@ -273,7 +302,18 @@ popcorn_status_t popcorn_decoder_create(popcorn_library_t library, popcorn_strea
         d->x = Buffer((size_t)(H * 2));
         d->x2 = Buffer((size_t)(H * 2));
         d->e = Buffer((size_t)(H * 2));
-        d->qkv = Buffer((size_t)(d->QW * 2));
+        d->qkv = Buffer((size_t)(d->QKV * 2));
+        if (c.attention_block) {
+            if (d->Hd % 2 != 0) throw Error::tensorShapeMismatch("attention_block needs an even head dim");
+            if (!(c.rope_theta > 0.0f)) throw Error::invalidArgument("attention_block needs rope_theta > 0");
+            d->headNorms = Buffer((size_t)(L * 2 * d->Hd * 4));
+            // Gemma4Workspace.swift:195-197: inv_freq[i] = 1 / theta^(2i / Hd), in double, stored f32
+            std::vector<float> inv((size_t)(d->Hd / 2));
+            for (size_t i = 0; i < inv.size(); ++i)
+                inv[i] = (float)(1.0 / std::pow((double)c.rope_theta, (double)(2 * i) / (double)d->Hd));
+            d->invFreq = Buffer(inv.size() * 4);
+            checkHip(hipMemcpy(d->invFreq.p, inv.data(), inv.size() * 4, hipMemcpyHostToDevice), "upload inv_freq");
+        }
         d->attn = Buffer((size_t)(d->QW * 2));
         d->o = Buffer((size_t)(H * 2));
         d->mlp = Buffer((size_t)(H * 2));
@@ -314,6 +354,7 @@ popcorn_status_t popcorn_decoder_randomize(popcorn_decoder_t d, uint64_t seed) {
         fill(d->wu, DataType::bf16, 0.0f, 0.02f);
         fill(d->wd, DataType::bf16, 0.0f, 0.02f);
         fill(d->norms, DataType::f32, 1.0f, 0.1f);
+        if (d->headNorms.p) fill(d->headNorms, DataType::f32, 1.0f, 0.1f);
         fill(d->kcache, DataType::bf16, 0.0f, 1.0f);
         fill(d->vcache, DataType::bf16, 0.0f, 1.0f);
         checkHip(hipStreamSynchronize(d->stream), "sync");
@@ -329,6 +370,8 @@ popcorn_status_t popcorn_decoder_tensor(popcorn_decoder_t d, const char *name, i
         else if (n == "final_norm") t = Tensor(d->finalNorm.p, Shape({d->H}), DataType::f32);
         else if (n == "x") t = d->bf(d->x.p, {d->H});
         else if (n == "q") t = d->bf(d->qkv.p, {d->QW});
+        else if (n == "qkv") t = d->bf(d->qkv.p, {d->QKV});
+        else if (n == "inv_freq" && d->invFreq.p) t = Tensor(d->invFreq.p, Shape({d->Hd / 2}), DataType::f32);
         else if (n == "attn") t = d->bf(d->attn.p, {d->QW});
         else if (n == "o") t = d->bf(d->o.p, {d->H});
         else if (n == "mlp") t = d->bf(d->mlp.p, {d->H});

@@ -26,6 +26,8 @@ class DecoderConfig:
     attn_scale: float = 1.0 / 16.0
     history_len: int = 4352
     graph_steps: int = 1
+    attention_block: int = 0      # 1: per-head q/k/v RMSNorm and RoPE (a real attention block)
+    rope_theta: float = 10000.0
 
     def c(self) -> _capi.DecoderConfig:
         return _capi.DecoderConfig(*[getattr(self, f.name) for f in fields(self)])

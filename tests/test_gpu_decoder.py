@@ -16,9 +16,10 @@ def env():
     return gpu_env()
 
 
-def _small(pa_dec, graph_steps=1):
+def _small(pa_dec, graph_steps=1, attention_block=0):
     return pa_dec.DecoderConfig(layers=2, hidden=256, query_heads=4, kv_heads=2, head_dim=64, ffn=512, vocab=1000,
-                                max_seq=64, eps=1e-6, attn_scale=0.125, history_len=64, graph_steps=graph_steps)
+                                max_seq=64, eps=1e-6, attn_scale=0.125, history_len=64, graph_steps=graph_steps,
+                                attention_block=attention_block)
 
 
 def _oracle_step(dec, cfg, caches, token, pos, stream, act=O.BF16):
@@ -32,14 +33,20 @@ def _oracle_step(dec, cfg, caches, token, pos, stream, act=O.BF16):
              [("in_norm", "norm_in"), ("qkv", "w_qkv"), ("o", "w_o"), ("post_attn_norm", "norm_post_attn"),
               ("pre_ffn_norm", "norm_pre_ffn"), ("gate", "w_gate"), ("up", "w_up"), ("down", "w_down"),
               ("post_ffn_norm", "norm_post_ffn")]}
+        if cfg.attention_block:
+            W["q_norm"] = download(dec.tensor("q_norm", l), stream)
+            W["k_norm"] = download(dec.tensor("k_norm", l), stream)
+            W["inv_freq"] = download(dec.tensor("inv_freq"), stream)
         kc, vc = caches[l]
         O.decoder_layer(W, x, kc, vc, pos, H=cfg.hidden, Nq=cfg.query_heads, Nkv=cfg.kv_heads, Hd=cfg.head_dim,
-                        F=cfg.ffn, eps=cfg.eps, scale=cfg.attn_scale, act_tag=act)
+                        F=cfg.ffn, eps=cfg.eps, scale=cfg.attn_scale, act_tag=act,
+                        v_norm=bool(cfg.attention_block))
     n = O.round_to(O.rmsnorm(x, download(dec.tensor("final_norm"), stream), cfg.eps), act)
     return O.matmul(n, emb, 1, cfg.hidden, cfg.vocab, True).ravel()
 
 
-def test_small_decoder_matches_oracle(env):
+@pytest.mark.parametrize("attention_block", [0, 1])
+def test_small_decoder_matches_oracle(env, attention_block):
     # The decode step is a composition of ~10 bf16-stored stages per layer;
     # each stage is pinned to 2e-3 by the kernel tests. Composed, a GPU sum
     # that lands on the other side of a bf16 rounding midpoint than the
@@ -51,9 +58,12 @@ def test_small_decoder_matches_oracle(env):
     pa, lib, stream, enc = env
     import popcorn_amd.decoder as D
 
-    cfg = _small(D)
+    cfg = _small(D, attention_block=attention_block)
     dec = D.Decoder(lib, stream, cfg)
     dec.randomize(seed=1)
+    if attention_block:  # inv_freq of theta 10000 (Gemma4Workspace.swift:195-197)
+        inv = np.array([1 / 10000.0 ** (2 * i / cfg.head_dim) for i in range(cfg.head_dim // 2)], np.float32)
+        np.testing.assert_array_equal(download(dec.tensor("inv_freq"), stream), inv)
     caches = [(download(dec.tensor("k_cache", l), stream)[0].copy(), download(dec.tensor("v_cache", l), stream)[0].copy())
               for l in range(cfg.layers)]
     token, pos = 17, 40
@@ -87,12 +97,12 @@ def test_small_decoder_matches_oracle(env):
     dec.close()
 
 
-@pytest.mark.parametrize("graph_steps,steps", [(1, 5), (3, 7)])
-def test_graph_replay_equals_eager(env, graph_steps, steps):
+@pytest.mark.parametrize("graph_steps,steps,attention_block", [(1, 5, 0), (3, 7, 0), (3, 7, 1)])
+def test_graph_replay_equals_eager(env, graph_steps, steps, attention_block):
     pa, lib, stream, enc = env
     import popcorn_amd.decoder as D
 
-    cfg = _small(D, graph_steps)
+    cfg = _small(D, graph_steps, attention_block)
     dec = D.Decoder(lib, stream, cfg)
     dec.randomize(seed=2)
     k0 = [dec.tensor("k_cache", l).numpy(stream) for l in range(cfg.layers)]
@@ -120,17 +130,20 @@ def test_graph_replay_equals_eager(env, graph_steps, steps):
     dec.close()
 
 
-def test_gemma2_2b_shape_decodes(env):
+@pytest.mark.parametrize("attention_block", [0, 1])
+def test_gemma2_2b_shape_decodes(env, attention_block):
     # BASELINE config 4 shape at full size: 26 layers, H 2304, 8/4 heads of
-    # 256, FFN 9216, vocab 256000, context 4096 -> 4352; random weights
+    # 256, FFN 9216, vocab 256000, context 4096 -> 4352; random weights;
+    # attention_block adds the per-head norms and RoPE of a real block
     pa, lib, stream, enc = env
     import popcorn_amd.decoder as D
 
-    cfg = D.DecoderConfig(graph_steps=4)
+    cfg = D.DecoderConfig(graph_steps=4, attention_block=attention_block)
     dec = D.Decoder(lib, stream, cfg)
     dec.randomize(seed=0)
     names, n = dec.describe()
     assert n == len(names) and "gated_mlp_gate_up_bf16_r1_res" in names
+    assert any(m.startswith("flash_decoding_fresh_") for m in names) == bool(attention_block)
     dec.reset(123, 4096)
     dec.step(8, use_graph=True)
     tok, pos = dec.read()
