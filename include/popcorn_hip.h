@@ -429,6 +429,40 @@ popcorn_status_t popcorn_kernel_embedding_gather(const popcorn_tensor_t *ids, co
 popcorn_status_t popcorn_kernel_argmax(const popcorn_tensor_t *x, const popcorn_tensor_t *indices,
                                        popcorn_kernel_t *kernel);
 
+/* ---- block-affine 4-bit weights (AffineQuantizedTensor.swift:19-84) ------
+ * w = q * scale + bias, q unsigned `bits` wide, packed least-significant
+ * first into little-endian u32 words (AffineQuantizationFormat.swift:24-30),
+ * one scale/bias pair per `group_size` values along the inner axis.
+ * packed_values u32 [..., out, in * bits / 32]; scales and biases
+ * [..., out, in / group_size]; biases.data == NULL for none; shape is the
+ * logical (dequantized) shape, rank >= 2. The kernels take bits 4, group 64,
+ * bf16 scales. */
+typedef struct {
+    popcorn_tensor_t packed_values;
+    popcorn_tensor_t scales;
+    popcorn_tensor_t biases;
+    int32_t rank;
+    int64_t shape[POPCORN_MAX_RANK];
+    int32_t bits;
+    int32_t group_size;
+} popcorn_affine_quantized_tensor_t;
+
+/* AffineQuantizedTensor.init's checks (AffineQuantizedTensor.swift:29-48). */
+popcorn_status_t popcorn_affine_quantized_validate(const popcorn_affine_quantized_tensor_t *tensor);
+
+/* Kernels.Matmul(_:_:into:) with a quantized RHS (Matmul.swift:99-130,
+ * :279-332): c[m, n] = a[m, k] b^T; (a, scales, c) dtypes (bf16, bf16, bf16),
+ * (bf16, bf16, f32) or (f32, bf16, f32); m == 1 runs aq_qmv_fast_*. */
+popcorn_status_t popcorn_kernel_matmul_quantized(const popcorn_tensor_t *a, const popcorn_affine_quantized_tensor_t *b,
+                                                 const popcorn_tensor_t *c, popcorn_kernel_t *kernel);
+
+/* Kernels.EmbeddingGather(ids:table:into:) with a quantized table
+ * (EmbeddingGather.swift:45-88): out[t, :] = dequantize(table[ids[t], :]);
+ * an id outside the table gives a zero row. */
+popcorn_status_t popcorn_kernel_embedding_gather_quantized(const popcorn_tensor_t *ids,
+                                                           const popcorn_affine_quantized_tensor_t *table,
+                                                           const popcorn_tensor_t *out, popcorn_kernel_t *kernel);
+
 /* A DispatchKernel built by the caller (Kernel.swift:54-70): function name,
  * bound tensors with their access (1 read, 2 write, 3 both), constants blocks,
  * and the launch geometry in blocks/threads. */

@@ -190,6 +190,30 @@ typedef struct {
     uint32_t D3;
 } Transpose12Constants;
 
+/* PopcornKernelTypes.h:240-247: y[M, N] = x[M, K] W^T with W block-affine
+ * 4-bit (u32 words of 8 values, lowest index in the lowest bits; one
+ * scale/bias pair per kGroups group of the row), wordsPerRow = K / 8. */
+typedef struct {
+    uint32_t M;
+    uint32_t N;
+    uint32_t K;
+    uint32_t kGroups;
+    uint32_t wordsPerRow;
+    uint32_t hasBias;
+} AffineQMatmulConstants;
+
+/* PopcornKernelTypes.h:249-255: out[T, H] = dequantize(table[ids[t], :]),
+ * plus V (table rows; 0 = unchecked): an id outside [0, V) yields a zero row
+ * instead of an out-of-bounds read. */
+typedef struct {
+    uint32_t T;
+    uint32_t H;
+    uint32_t kGroups;
+    uint32_t wordsPerRow;
+    uint32_t hasBias;
+    uint32_t V;
+} AffineQEmbeddingGatherConstants;
+
 /* PopcornKernelTypes.h:197-200, plus slices: the number of row slices the
  * two-stage argmax splits each row into (stage 1 grid width). */
 typedef struct {

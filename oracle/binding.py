@@ -71,6 +71,12 @@ def lib():
         L.oracle_rope_build_cos_sin.argtypes = [_i32p, _fp, _fp, _fp, C.c_uint32, C.c_uint32, C.c_float]
         L.oracle_rope_apply.argtypes = [_fp, _fp, _fp, _fp] + [C.c_uint32] * 4
         L.oracle_transpose12.argtypes = [_fp, _fp] + [C.c_uint32] * 4
+        _u32p = C.POINTER(C.c_uint32)
+        L.oracle_aq_unpack.restype = C.c_uint32
+        L.oracle_aq_unpack.argtypes = [_u32p, C.c_size_t, C.c_int]
+        L.oracle_aq_matmul.argtypes = [_fp, _u32p, _fp, _fp, _fp] + [C.c_size_t] * 3 + [C.c_int, C.c_int]
+        L.oracle_aq_embedding_gather.argtypes = [_i32p, _u32p, _fp, _fp, _fp, C.c_size_t, C.c_size_t, C.c_int,
+                                                 C.c_int]
         L.oracle_argmax.argtypes = [_fp, C.c_size_t, C.c_size_t, _i32p]
         L.oracle_embedding_gather.argtypes = [_i32p, _fp, _fp, C.c_size_t, C.c_size_t]
         L.oracle_decoder_layer.argtypes = [C.c_void_p, _fp, _fp, _fp, C.c_uint32]
@@ -272,6 +278,40 @@ def transpose12(src):
     D0, D1, D2, D3 = src.shape
     out = np.empty((D0, D2, D1, D3), np.float32)
     lib().oracle_transpose12(_p(src), _p(out), D0, D1, D2, D3)
+    return out
+
+
+def _u32(a):
+    a = np.ascontiguousarray(a, dtype=np.uint32)
+    return a, a.ctypes.data_as(C.POINTER(C.c_uint32))
+
+
+def aq_unpack(words, count: int, bits: int = 4) -> np.ndarray:
+    """Values 0..count-1 of a packed little-endian u32 stream."""
+    w, wp = _u32(words)
+    return np.array([lib().oracle_aq_unpack(wp, i, bits) for i in range(count)], np.uint32)
+
+
+def aq_matmul(x, packed, scales, biases, N: int, K: int, bits: int = 4, group: int = 64) -> np.ndarray:
+    """x [M, K] f32, packed u32 [N, K*bits/32], scales/biases f32 [N, K/group] -> y [M, N]."""
+    x = _f32(x).reshape(-1, K)
+    M = x.shape[0]
+    w, wp = _u32(packed)
+    s = _f32(scales)
+    b = _f32(biases) if biases is not None else None
+    y = np.empty((M, N), np.float32)
+    lib().oracle_aq_matmul(_p(x), wp, _p(s), _p(b) if b is not None else None, _p(y), M, N, K, bits, group)
+    return y
+
+
+def aq_embedding_gather(ids, packed, scales, biases, H: int, bits: int = 4, group: int = 64) -> np.ndarray:
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    w, wp = _u32(packed)
+    s = _f32(scales)
+    b = _f32(biases) if biases is not None else None
+    out = np.empty((ids.size, H), np.float32)
+    lib().oracle_aq_embedding_gather(ids.ctypes.data_as(_i32p), wp, _p(s), _p(b) if b is not None else None, _p(out),
+                                     ids.size, H, bits, group)
     return out
 
 

@@ -583,6 +583,58 @@ void oracle_transpose12(const float *src, float *out, uint32_t D0, uint32_t D1, 
 }
 
 /* ------------------------------------------------------------------------ */
+/* Block-affine quantized weights                                           */
+/* ------------------------------------------------------------------------ */
+
+/* Sources/Popcorn/Quantization/AffineQuantizationFormat.swift:25-29 and
+ * PopcornDTypes.h:55-63: value i of a packed stream sits in bits
+ * (i % vpw) * bits .. + bits of word i / vpw, vpw = 32 / bits. */
+uint32_t oracle_aq_unpack(const uint32_t *words, size_t i, int bits) {
+    const size_t vpw = (size_t)(32 / bits);
+    const uint32_t mask = bits == 32 ? 0xffffffffu : ((1u << bits) - 1u);
+    return (words[i / vpw] >> ((i % vpw) * (size_t)bits)) & mask;
+}
+
+/* Sources/Popcorn/Kernels/Quantized/AffineQuantizedMatmul.metal:34-58
+ * (aq_matvec_simd4): y[m, n] = sum_k x[m, k] * (float(q[n, k]) * s[n, g] +
+ * b[n, g]), g = k / group, summed in k order; biases NULL = no bias
+ * (hasBias 0). Rows of packed values hold K * bits / 32 words. */
+void oracle_aq_matmul(const float *x, const uint32_t *packed, const float *scales, const float *biases,
+                      float *y, size_t M, size_t N, size_t K, int bits, int group) {
+    const size_t words = K * (size_t)bits / 32, groups = K / (size_t)group;
+    for (size_t m = 0; m < M; ++m)
+        for (size_t n = 0; n < N; ++n) {
+            float acc = 0.0f;
+            for (size_t k = 0; k < K; ++k) {
+                const size_t g = k / (size_t)group;
+                const float s = scales[n * groups + g];
+                const float b = biases ? biases[n * groups + g] : 0.0f;
+                const float q = (float)oracle_aq_unpack(packed + n * words, k, bits);
+                const float w = q * s + b;
+                acc += x[m * K + k] * w;
+            }
+            y[m * N + n] = acc;
+        }
+}
+
+/* Sources/Popcorn/Kernels/Quantized/AffineQuantizedEmbeddingGather.metal:16-26:
+ * out[t, h] = float(q[ids[t], h]) * s + b. */
+void oracle_aq_embedding_gather(const int32_t *ids, const uint32_t *packed, const float *scales,
+                                const float *biases, float *out, size_t T, size_t H, int bits,
+                                int group) {
+    const size_t words = H * (size_t)bits / 32, groups = H / (size_t)group;
+    for (size_t t = 0; t < T; ++t) {
+        const size_t row = (size_t)(uint32_t)ids[t];
+        for (size_t h = 0; h < H; ++h) {
+            const size_t g = h / (size_t)group;
+            const float s = scales[row * groups + g];
+            const float b = biases ? biases[row * groups + g] : 0.0f;
+            out[t * H + h] = (float)oracle_aq_unpack(packed + row * words, h, bits) * s + b;
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
 /* Decode-loop glue                                                          */
 /* ------------------------------------------------------------------------ */
 

@@ -36,6 +36,12 @@
  *                                 p1 then p2 vs p1 + p2 (numpy float64)
  *   transpose12                 - numpy transpose (0, 2, 1, 3); applied twice
  *                                 with swapped dims is the identity
+ *   aq_unpack / aq_matmul / aq_embedding_gather - a hand-packed word's bit
+ *                                 layout; numpy float64 of the dequantized
+ *                                 product; exact integer products; the
+ *                                 s*sum(xq) + b*sum(x) identity; numpy f32
+ *                                 dequantization (the reference's tests hold
+ *                                 no quantized case)
  *   decode_step                 - composition of the pinned pieces; numpy
  *                                 float64 forward of a tiny layer (with and
  *                                 without the q/k/v norms and RoPE)
@@ -110,6 +116,13 @@ void oracle_rope_apply(const float *x, const float *cos_tab, const float *sin_ta
                        uint32_t B, uint32_t T, uint32_t Nh, uint32_t Hd2);
 void oracle_transpose12(const float *src, float *out, uint32_t D0, uint32_t D1, uint32_t D2,
                         uint32_t D3);
+
+uint32_t oracle_aq_unpack(const uint32_t *words, size_t i, int bits);
+void oracle_aq_matmul(const float *x, const uint32_t *packed, const float *scales, const float *biases,
+                      float *y, size_t M, size_t N, size_t K, int bits, int group);
+void oracle_aq_embedding_gather(const int32_t *ids, const uint32_t *packed, const float *scales,
+                                const float *biases, float *out, size_t T, size_t H, int bits,
+                                int group);
 
 void oracle_argmax(const float *x, size_t rows, size_t N, int32_t *indices);
 void oracle_embedding_gather(const int32_t *ids, const float *table, float *out,

@@ -7,6 +7,7 @@ Swift API over that ABI.
 """
 from ._capi import LIB_PATH, KERNEL_DIR  # noqa: F401
 from .runtime import (  # noqa: F401
+    AffineQuantizedTensor,
     AttentionMask,
     DeviceBuffer,
     Event,

@@ -31,6 +31,12 @@ class AttentionMaskDesc(C.Structure):
     _fields_ = [("kind", C.c_uint32), ("window", C.c_int32)]
 
 
+class AffineQuantizedDesc(C.Structure):
+    _fields_ = [("packed_values", TensorDesc), ("scales", TensorDesc), ("biases", TensorDesc),
+                ("rank", C.c_int32), ("shape", C.c_int64 * MAX_RANK), ("bits", C.c_int32),
+                ("group_size", C.c_int32)]
+
+
 class DeviceInfo(C.Structure):
     _fields_ = [("name", C.c_char * 64), ("arch", C.c_char * 32), ("compute_units", C.c_int32),
                 ("wave_size", C.c_int32), ("max_threads_per_block", C.c_int32),
@@ -153,6 +159,9 @@ PROTOTYPES = {
     "popcorn_kernel_decode_matvec": (_st, [C.POINTER(DecodeMatvecArgs), _K]),
     "popcorn_kernel_decode_attention": (_st, [C.POINTER(DecodeAttentionArgs), _K]),
     "popcorn_kernel_embedding_gather": (_st, [_T, _T, _T, _K]),
+    "popcorn_affine_quantized_validate": (_st, [C.POINTER(AffineQuantizedDesc)]),
+    "popcorn_kernel_matmul_quantized": (_st, [_T, C.POINTER(AffineQuantizedDesc), _T, _K]),
+    "popcorn_kernel_embedding_gather_quantized": (_st, [_T, C.POINTER(AffineQuantizedDesc), _T, _K]),
     "popcorn_kernel_argmax": (_st, [_T, _T, _K]),
     "popcorn_kernel_custom": (_st, [C.c_char_p, _T, C.POINTER(C.c_uint8), C.c_int32, C.POINTER(C.c_void_p),
                                     C.POINTER(C.c_size_t), C.c_int32, C.POINTER(C.c_uint32),

@@ -1,0 +1,190 @@
+// Block-affine 4-bit matmul and embedding gather (AffineQuantizedMatmul.metal,
+// AffineQuantizedEmbeddingGather.metal): y[m, n] = sum_k x[m, k] (q[n, k] s[n, g]
+// + b[n, g]), g = k / 64; out[t, h] = q[ids[t], h] s + b. Kernel names follow
+// the reference's (Matmul.swift:301-302, EmbeddingGather.swift:80), with the
+// launch shape appended: _l<LPR> lanes per row, _j<J> x octets per thread.
+//
+// A block of 4 waves streams units of 64 / LPR rows per wave (q4.hpp) while
+// the block stages its row of x in LDS; one block row of the grid (blockIdx.y)
+// per row m of x (M == 1 is the decode matvec).
+#include "q4.hpp"
+
+namespace {
+
+using pk::BF16;
+using pk::F32;
+using pk::kQ4Group;
+using pk::Q4Row;
+using pk::Q4Staging;
+using pk::Q4Stream;
+using pk::u32x4;
+
+// J octets per thread stage K <= 2048 J values: LDS holds K/2 pair words
+// (bf16 x) or K floats (f32 x), plus K/64 group sums.
+template <int J>
+constexpr uint32_t maxK() { return 2048u * J; }
+
+// The J octets (8 values) of x this thread stages, loaded into registers
+// before the weight stream starts (loads retire in issue order); octets past
+// the row re-read its last octet and are not used.
+template <typename X, int J>
+struct XOctets {
+    static constexpr int kPieces = sizeof(typename X::storage) * 8 / 16;  // 16-byte loads per octet
+    u32x4 v[J][kPieces];
+    __device__ void issue(const typename X::storage *x, uint32_t K) {
+        const uint32_t octets = K / 8;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const uint32_t o = min(threadIdx.x + pk::kStreamThreads * (uint32_t)j, octets - 1);
+#pragma unroll
+            for (int h = 0; h < kPieces; ++h) v[j][h] = *reinterpret_cast<const u32x4 *>(x + (uint64_t)o * 8 + h * (8 / kPieces));
+        }
+    }
+    __device__ void get(int j, float *out) const {
+        if constexpr (kPieces == 1) {
+            pk::Vec<X> t;
+            t.raw = v[j][0];
+            t.to_float(out);
+        } else {
+#pragma unroll
+            for (int h = 0; h < kPieces; ++h) {
+                pk::Vec<X> t;
+                t.raw = v[j][h];
+                t.to_float(out + h * 4);
+            }
+        }
+    }
+};
+
+template <typename X, typename O, int LPR, int J>
+__device__ void aq_matvec(const uint32_t *__restrict__ W, const uint16_t *__restrict__ Sc, const uint16_t *__restrict__ Bi,
+                          const typename X::storage *__restrict__ x, typename O::storage *__restrict__ y,
+                          const AffineQMatmulConstants &p) {
+    constexpr bool XF32 = sizeof(typename X::storage) == 4;
+    constexpr int kRows = 64 / LPR;
+    __shared__ uint32_t xw[XF32 ? 1 : maxK<J>() / 2];
+    __shared__ float xf[XF32 ? maxK<J>() : 1];
+    __shared__ float gsum[maxK<J>() / kQ4Group];
+
+    const uint32_t m = blockIdx.y;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t units = (p.N + kRows - 1) / kRows;
+    const uint16_t *B = p.hasBias ? Bi : Sc;
+    auto rows = [&](uint32_t unit, int) {
+        const uint32_t r = min(unit * kRows + lane / LPR, p.N - 1);
+        return Q4Row{W + (uint64_t)r * p.wordsPerRow, Sc + (uint64_t)r * p.kGroups, B + (uint64_t)r * p.kGroups};
+    };
+    XOctets<X, J> xo;
+    xo.issue(x + (uint64_t)m * p.K, p.K);
+    Q4Stream<LPR, 1, pk::kStreamSteps, XF32> st;
+    st.init(rows, p.K, units, blockIdx.x * pk::kStreamWaves + wave, gridDim.x * pk::kStreamWaves, p.hasBias != 0);
+    st.start(rows);
+    Q4Staging<XF32>::build(p.K, xw, xf, gsum, [&](uint32_t j, uint32_t, float *v) { xo.get(min(j, (uint32_t)J - 1), v); });
+    auto store = [&](uint32_t unit, const float *sums) {
+        const uint32_t r = unit * kRows + lane / LPR;
+        if (lane % LPR == 0 && r < p.N) y[(uint64_t)m * p.N + r] = O::store(sums[0]);
+    };
+    st.run(xw, xf, gsum, rows, store);
+}
+
+// AffineQuantizedEmbeddingGather.metal:16-26, one thread per packed word (8
+// values of one group) of one token.
+template <typename O>
+__device__ void aq_gather(const int32_t *__restrict__ ids, const uint32_t *__restrict__ W, const uint16_t *__restrict__ Sc,
+                          const uint16_t *__restrict__ Bi, typename O::storage *__restrict__ out,
+                          const AffineQEmbeddingGatherConstants &p) {
+    const uint64_t words = (uint64_t)p.T * p.wordsPerRow;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < words; i += (uint64_t)gridDim.x * blockDim.x) {
+        const uint32_t t = (uint32_t)(i / p.wordsPerRow), wi = (uint32_t)(i % p.wordsPerRow);
+        const uint64_t row = (uint32_t)ids[t];
+        typename O::storage *dst = out + (uint64_t)t * p.H + (uint64_t)wi * 8;
+        if (p.V && row >= p.V) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) dst[e] = O::store(0.0f);
+            continue;
+        }
+        const uint32_t g = wi / pk::kQ4GroupWords;
+        const uint32_t w = W[row * p.wordsPerRow + wi];
+        const float s = pk::bf16_lo(Sc[row * p.kGroups + g]);
+        const float b = p.hasBias ? pk::bf16_lo(Bi[row * p.kGroups + g]) : 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dst[e] = O::store((float)((w >> (4 * e)) & 15u) * s + b);
+    }
+}
+
+// Any alignment and any M (Matmul.swift:321-331 geometry, reworked for wave64):
+// one wave per 4 rows of one x row, lanes strided over K, the form of
+// AffineQuantizedMatmul.metal:34-58.
+template <typename X, typename O>
+__device__ void aq_matvec_any(const uint32_t *__restrict__ W, const uint16_t *__restrict__ Sc,
+                              const uint16_t *__restrict__ Bi, const typename X::storage *__restrict__ x,
+                              typename O::storage *__restrict__ y, const AffineQMatmulConstants &p) {
+    constexpr uint32_t kR = 4;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t row0 = (blockIdx.x * pk::kStreamWaves + (threadIdx.x >> 6)) * kR;
+    const uint32_t m = blockIdx.y;
+    if (row0 >= p.N) return;
+    const typename X::storage *xr = x + (uint64_t)m * p.K;
+    float acc[kR] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t k = lane; k < p.K; k += 64) {
+        const float xv = X::load(xr[k]);
+        const uint32_t g = k / kQ4Group;
+#pragma unroll
+        for (uint32_t r = 0; r < kR; ++r) {
+            const uint64_t row = min(row0 + r, p.N - 1);
+            const float s = pk::bf16_lo(Sc[row * p.kGroups + g]);
+            const float b = p.hasBias ? pk::bf16_lo(Bi[row * p.kGroups + g]) : 0.0f;
+            const uint32_t q = (W[row * p.wordsPerRow + k / 8] >> (4 * (k % 8))) & 15u;
+            acc[r] += xv * ((float)q * s + b);
+        }
+    }
+#pragma unroll
+    for (uint32_t r = 0; r < kR; ++r) {
+        const float sum = pk::wave_sum(acc[r]);
+        if (lane == 0 && row0 + r < p.N) y[(uint64_t)m * p.N + row0 + r] = O::store(sum);
+    }
+}
+
+}  // namespace
+
+#define AQ_MV(prefix, xt, ot, X, O, LPR, J)                                                                         \
+    POPCORN_KERNEL void __launch_bounds__(256) prefix##_##xt##_bf16_##ot##_b4_g64_l##LPR##_j##J(                      \
+        const uint32_t *W, const uint16_t *S, const uint16_t *B, const X::storage *x, O::storage *y,                    \
+        AffineQMatmulConstants p) {                                                                                    \
+        aq_matvec<X, O, LPR, J>(W, S, B, x, y, p);                                                                     \
+    }
+// bf16 x: J 2 (K <= 4096) and 8 (K <= 16384); f32 x: J 2 (K <= 4096, 16 KB
+// of LDS; larger K takes the any-shape kernel)
+#define AQ_MV_L(prefix, xt, ot, X, O, J) \
+    AQ_MV(prefix, xt, ot, X, O, 8, J) AQ_MV(prefix, xt, ot, X, O, 16, J) AQ_MV(prefix, xt, ot, X, O, 32, J)
+#define AQ_MV_ALL(prefix)                                                                  \
+    AQ_MV_L(prefix, bf16, bf16, BF16, BF16, 2) AQ_MV_L(prefix, bf16, bf16, BF16, BF16, 8) \
+    AQ_MV_L(prefix, bf16, f32, BF16, F32, 2) AQ_MV_L(prefix, bf16, f32, BF16, F32, 8)     \
+    AQ_MV_L(prefix, f32, f32, F32, F32, 2)
+
+// Matmul.swift:301 (m == 1 -> aq_qmv_fast, else aq_matvec_simd4) and the
+// dtype triples of Matmul.swift:343-347
+AQ_MV_ALL(aq_qmv_fast)
+AQ_MV_ALL(aq_matvec_simd4)
+
+#define AQ_ANY(xt, ot, X, O)                                                                                  \
+    POPCORN_KERNEL void __launch_bounds__(256) aq_matvec_simd4_##xt##_bf16_##ot##_b4_g64(                          \
+        const uint32_t *W, const uint16_t *S, const uint16_t *B, const X::storage *x, O::storage *y,            \
+        AffineQMatmulConstants p) {                                                                            \
+        aq_matvec_any<X, O>(W, S, B, x, y, p);                                                                 \
+    }
+AQ_ANY(bf16, bf16, BF16, BF16)
+AQ_ANY(bf16, f32, BF16, F32)
+AQ_ANY(f32, f32, F32, F32)
+
+// EmbeddingGather.swift:80 (AffineQuantizedEmbeddingGather.metal:29-30)
+POPCORN_KERNEL void __launch_bounds__(256)
+    aq_embedding_gather_bf16_bf16_b4_g64(const int32_t *ids, const uint32_t *W, const uint16_t *S, const uint16_t *B,
+                                         uint16_t *out, AffineQEmbeddingGatherConstants p) {
+    aq_gather<BF16>(ids, W, S, B, out, p);
+}
+POPCORN_KERNEL void __launch_bounds__(256)
+    aq_embedding_gather_bf16_f32_b4_g64(const int32_t *ids, const uint32_t *W, const uint16_t *S, const uint16_t *B,
+                                        float *out, AffineQEmbeddingGatherConstants p) {
+    aq_gather<F32>(ids, W, S, B, out, p);
+}

@@ -1,0 +1,243 @@
+// Building blocks of the block-affine 4-bit matvecs (affine_quant.hip):
+// weights w = q * scale + bias with q an unsigned 4-bit value, 8 values per
+// little-endian u32 word (value i in bits 4(i % 8) .. 4(i % 8) + 3,
+// AffineQuantizationFormat.swift:25-29) and one bf16 scale/bias pair per group
+// of 64 values along the row (AffineQuantizedTensor.swift:5-17).
+//
+// Per group g of a row: sum_k x_k (q_k s + b) = s * sum_k x_k q_k + b * X_g with
+// X_g = sum_k x_k (the identity the reference's aq_qmv_fast uses,
+// AffineQuantizedMatmul.metal:75-82), so the inner loop is a plain dot product
+// of x with the raw nibbles and the group sums X_g are computed once per block.
+//
+// For bf16 activations the dot product runs on v_dot2_f32_bf16 (two bf16
+// products accumulated in f32 per instruction; bf16 x bf16 products are exact
+// in f32). A nibble pair becomes a bf16 pair with one mask and one OR: bf16
+// 0x4300 is 128.0 and its 7-bit mantissa step is 1, so 0x4300 | q = 128 + q
+// exactly. One AND with 0x000F000F takes nibbles p and p + 4 of a word into
+// the two halves, hence x is staged in LDS as the bf16 pairs (x[8j + p],
+// x[8j + p + 4]). The dot then holds sum x (128 + q) and the group's result is
+// s * dot + (b - 128 s) * X_g.
+#pragma once
+
+#include "stream.hpp"
+
+namespace pk {
+
+constexpr uint32_t kQ4Group = 64;          // values per scale/bias group
+constexpr uint32_t kQ4GroupWords = 8;      // packed u32 words per group
+constexpr uint32_t kQ4PairBase = 0x43004300u;  // bf16 pair (128, 128)
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ inline float dot2_bf16(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+__device__ inline float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
+__device__ inline float bf16_hi(uint32_t v) { return __uint_as_float(v & 0xffff0000u); }
+
+// Staged activations of one row of x for the 4-bit stream, in LDS.
+//   bf16 x (XF32 = false): xw[K / 2] pair words (see above), gsum[K / 64];
+//   f32 x  (XF32 = true):  xf[K] floats, gsum[K / 64].
+// One thread per octet of 8 values: the octet sums meet in groups of 8 lanes.
+template <bool XF32>
+struct Q4Staging {
+    // From 8 f32 values of octet o (already rounded as the caller stores x).
+    __device__ static void put_octet(uint32_t *xw, float *xf, uint32_t o, const float *v) {
+        if constexpr (XF32) {
+            *reinterpret_cast<float4 *>(xf + 8 * o) = float4{v[0], v[1], v[2], v[3]};
+            *reinterpret_cast<float4 *>(xf + 8 * o + 4) = float4{v[4], v[5], v[6], v[7]};
+        } else {
+            u32x4 w;
+            w.x = (__float_as_uint(v[0]) >> 16) | (__float_as_uint(v[4]) & 0xffff0000u);
+            w.y = (__float_as_uint(v[1]) >> 16) | (__float_as_uint(v[5]) & 0xffff0000u);
+            w.z = (__float_as_uint(v[2]) >> 16) | (__float_as_uint(v[6]) & 0xffff0000u);
+            w.w = (__float_as_uint(v[3]) >> 16) | (__float_as_uint(v[7]) & 0xffff0000u);
+            *reinterpret_cast<u32x4 *>(xw + 4 * o) = w;
+        }
+    }
+
+    // Octets o = tid + 256 j (pass j); `get(j, o, v)` fills the 8 values of
+    // octet o. Ends with a barrier. K is a multiple of 64, so every group's 8
+    // octets are 8 consecutive threads of one pass.
+    template <class Get>
+    __device__ static void build(uint32_t K, uint32_t *xw, float *xf, float *gsum, const Get &get) {
+        const uint32_t octets = K / 8;
+        for (uint32_t base = 0, j = 0; base < octets; base += kStreamThreads, ++j) {
+            const uint32_t o = base + threadIdx.x;
+            float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            float s = 0.0f;
+            if (o < octets) {
+                get(j, o, v);
+                put_octet(xw, xf, o, v);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) s += v[e];
+            }
+            s = group_sum<8>(s);
+            if (o < octets && (o & 7u) == 0) gsum[o / 8] = s;
+        }
+        __syncthreads();
+    }
+};
+
+// The rows of a unit as seen by one lane: its row's packed words, scales and
+// biases (biases == scales when the tensor has none; hasBias says so).
+struct Q4Row {
+    const uint32_t *w;
+    const uint16_t *s;
+    const uint16_t *b;
+};
+
+// Streams units of kRows = 64 / LPR rows through a wave: lane l serves row
+// l / LPR of the unit and groups g = l % LPR + LPR i of that row, one group
+// (two 16-byte loads of words, one scale, one bias) per step; NS rows (of NS
+// weight matrices, same row index) per lane. U steps stay in flight and each
+// slot is refilled as soon as it is consumed (in issue order, as in
+// RowStream). A unit's per-row results are summed over its LPR lanes.
+template <int LPR, int NS, int U, bool XF32>
+struct Q4Stream {
+    static_assert(LPR >= 4 && LPR <= 64 && (LPR & (LPR - 1)) == 0, "LPR is a power of two in [4, 64]");
+    static constexpr int kRows = 64 / LPR;
+    u32x4 wv[U][NS][2];
+    uint32_t sb[U][NS];
+    Q4Row ip[NS];
+    uint32_t G, cpl, steps, first, stride, is, ii, iu, gl;
+    bool hasBias;
+
+    template <class Rows>
+    __device__ void init(const Rows &rows, uint32_t K, uint32_t units, uint32_t first_, uint32_t stride_, bool hasBias_) {
+        G = K / kQ4Group;
+        gl = (threadIdx.x & 63) % LPR;
+        cpl = (G + LPR - 1) / LPR;
+        first = first_;
+        stride = stride_;
+        hasBias = hasBias_;
+        const uint32_t nu = first < units ? (units - first + stride - 1) / stride : 0u;
+        steps = nu * cpl;
+        is = 0;
+        ii = 0;
+        iu = first;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) ip[s] = rows(iu, s);
+    }
+
+    // Once every step is issued the last one is loaded again, so every path
+    // has the same loads in flight (exact wait counts, as in RowStream).
+    template <class Rows>
+    __device__ inline void issue(int slot, const Rows &rows) {
+        const uint32_t g = min(gl + LPR * ii, G - 1);
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            const uint32_t *p = ip[s].w + (uint64_t)g * kQ4GroupWords;
+            wv[slot][s][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+            wv[slot][s][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p + 4));
+            sb[slot][s] = (uint32_t)ip[s].s[g] | ((uint32_t)ip[s].b[g] << 16);
+        }
+        if (is + 1 < steps) {
+            ++is;
+            if (++ii == cpl) {
+                ii = 0;
+                iu += stride;
+#pragma unroll
+                for (int s = 0; s < NS; ++s) ip[s] = rows(iu, s);
+            }
+        } else {
+            is = steps;
+        }
+    }
+
+    template <class Rows>
+    __device__ void start(const Rows &rows) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) issue(u, rows);
+    }
+
+    __device__ static inline uint32_t word(const u32x4 (&w)[2], int j) {
+        const u32x4 &h = w[j >> 2];
+        return (j & 3) == 0 ? h.x : (j & 3) == 1 ? h.y : (j & 3) == 2 ? h.z : h.w;
+    }
+
+    template <class Store>
+    __device__ inline void consume(int slot, const uint32_t *xw, const float *xf, const float *gsum, float (&acc)[NS],
+                                   uint32_t &ci, uint32_t &cu, Store &store) {
+        const uint32_t g = gl + LPR * ci;
+        if (g < G) {
+            const float xg = gsum[g];
+            if constexpr (!XF32) {
+                u32x4 xv[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) xv[j] = *reinterpret_cast<const u32x4 *>(xw + (uint64_t)g * 32 + 4 * j);
+#pragma unroll
+                for (int s = 0; s < NS; ++s) {
+                    float d0 = 0.0f, d1 = 0.0f, d2 = 0.0f, d3 = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const uint32_t w = word(wv[slot][s], j);
+                        d0 = dot2_bf16((w & 0x000F000Fu) | kQ4PairBase, xv[j].x, d0);
+                        d1 = dot2_bf16(((w >> 4) & 0x000F000Fu) | kQ4PairBase, xv[j].y, d1);
+                        d2 = dot2_bf16(((w >> 8) & 0x000F000Fu) | kQ4PairBase, xv[j].z, d2);
+                        d3 = dot2_bf16(((w >> 12) & 0x000F000Fu) | kQ4PairBase, xv[j].w, d3);
+                    }
+                    const float dot = (d0 + d1) + (d2 + d3);
+                    const float sc = bf16_lo(sb[slot][s]);
+                    const float bi = hasBias ? bf16_hi(sb[slot][s]) : 0.0f;
+                    acc[s] += sc * dot + (bi - 128.0f * sc) * xg;
+                }
+            } else {
+#pragma unroll
+                for (int s = 0; s < NS; ++s) {
+                    float qd = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const uint32_t w = word(wv[slot][s], j);
+                        const float4 a = *reinterpret_cast<const float4 *>(xf + (uint64_t)g * 64 + 8 * j);
+                        const float4 b = *reinterpret_cast<const float4 *>(xf + (uint64_t)g * 64 + 8 * j + 4);
+                        qd += a.x * (float)(w & 15u) + a.y * (float)((w >> 4) & 15u) + a.z * (float)((w >> 8) & 15u) +
+                              a.w * (float)((w >> 12) & 15u) + b.x * (float)((w >> 16) & 15u) +
+                              b.y * (float)((w >> 20) & 15u) + b.z * (float)((w >> 24) & 15u) + b.w * (float)(w >> 28);
+                    }
+                    const float sc = bf16_lo(sb[slot][s]);
+                    const float bi = hasBias ? bf16_hi(sb[slot][s]) : 0.0f;
+                    acc[s] += sc * qd + bi * xg;
+                }
+            }
+        }
+        if (++ci == cpl) {
+            float sums[NS];
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                sums[s] = group_sum<LPR>(acc[s]);
+                acc[s] = 0.0f;
+            }
+            store(cu, sums);
+            ci = 0;
+            cu += stride;
+        }
+    }
+
+    template <class Rows, class Store>
+    __device__ void run(const uint32_t *xw, const float *xf, const float *gsum, const Rows &rows, Store &store) {
+        float acc[NS];
+#pragma unroll
+        for (int s = 0; s < NS; ++s) acc[s] = 0.0f;
+        uint32_t cs = 0, ci = 0, cu = first;
+        while (cs + 2 * U <= steps) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                consume(u, xw, xf, gsum, acc, ci, cu, store);
+                issue(u, rows);
+            }
+            cs += U;
+        }
+        while (cs < steps) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                if (cs + u < steps) consume(u, xw, xf, gsum, acc, ci, cu, store);
+                issue(u, rows);
+            }
+            cs += U;
+        }
+    }
+};
+
+}  // namespace pk

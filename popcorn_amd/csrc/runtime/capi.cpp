@@ -660,6 +660,38 @@ popcorn_status_t popcorn_kernel_decode_matvec(const popcorn_decode_matvec_args_t
     });
 }
 
+namespace {
+AffineQuantizedTensor quantized(const popcorn_affine_quantized_tensor_t *q, const char *what) {
+    need(q, what);
+    AffineQuantizedTensor t;
+    t.packedValues = Tensor::fromC(q->packed_values);
+    t.scales = Tensor::fromC(q->scales);
+    t.hasBiases = q->biases.data != nullptr;
+    if (t.hasBiases) t.biases = Tensor::fromC(q->biases);
+    if (q->rank < 0 || q->rank > POPCORN_MAX_RANK) throw Error::invalidArgument(std::string(what) + ": rank out of range");
+    std::vector<int64_t> dims(q->shape, q->shape + q->rank);
+    t.shape = Shape(std::move(dims));
+    t.bits = q->bits;
+    t.groupSize = q->group_size;
+    return t;
+}
+}  // namespace
+
+popcorn_status_t popcorn_affine_quantized_validate(const popcorn_affine_quantized_tensor_t *tensor) {
+    return guarded([&] { quantized(tensor, "tensor").validate(); });
+}
+
+popcorn_status_t popcorn_kernel_matmul_quantized(const popcorn_tensor_t *a, const popcorn_affine_quantized_tensor_t *b,
+                                                 const popcorn_tensor_t *c, popcorn_kernel_t *kernel) {
+    return guarded([&] { emit(kernel, Kernels::Matmul(T(a, "a"), quantized(b, "b"), T(c, "c"))); });
+}
+
+popcorn_status_t popcorn_kernel_embedding_gather_quantized(const popcorn_tensor_t *ids,
+                                                           const popcorn_affine_quantized_tensor_t *table,
+                                                           const popcorn_tensor_t *out, popcorn_kernel_t *kernel) {
+    return guarded([&] { emit(kernel, Kernels::EmbeddingGather(T(ids, "ids"), quantized(table, "table"), T(out, "out"))); });
+}
+
 popcorn_status_t popcorn_kernel_embedding_gather(const popcorn_tensor_t *ids, const popcorn_tensor_t *table,
                                                  const popcorn_tensor_t *out, popcorn_kernel_t *kernel) {
     return guarded([&] { emit(kernel, Kernels::EmbeddingGather(T(ids, "ids"), T(table, "table"), T(out, "out"))); });

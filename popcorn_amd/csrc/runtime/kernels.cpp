@@ -710,10 +710,28 @@ std::unique_ptr<Kernel> elementwise(const char *base, const Tensor &a, const Ten
 
 }  // namespace
 
+// AffineQuantizedTensor.swift:29-48, plus the format's own consistency (bits
+// dividing the 32-bit word, a positive group size).
+void AffineQuantizedTensor::validate() const {
+    if (shape.rank() < 2) throw Error::tensorInvalidRank(2, shape.rank());
+    if (hasBiases) {
+        if (biases.dataType != scales.dataType)
+            throw Error::unsupportedDataTypeCombination(std::string("AffineQuantizedTensor scales and biases must share a data type; got ") +
+                                                        name(scales.dataType) + " and " + name(biases.dataType) + ".");
+        if (biases.shape != scales.shape)
+            throw Error::tensorShapeMismatch("AffineQuantizedTensor scales and biases must share a shape; got " + scales.shape.str() +
+                                             " and " + biases.shape.str() + ".");
+    }
+    if (packedValues.dataType != DataType::u32)
+        throw Error::unsupportedDataTypeCombination(
+            std::string("AffineQuantizedTensor packed values must use u32 for packing uint32LittleEndian; got ") +
+            name(packedValues.dataType) + ".");
+    if (bits <= 0 || bits > 32 || 32 % bits != 0 || groupSize <= 0)
+        throw Error::invalidArgument("AffineQuantizedTensor format needs bits dividing 32 and a positive group size.");
+}
+
 namespace Kernels {
 
-// FlashAttention.swift:109-113. `tiled` (MFMA prefill) takes the MPP path's
-// place once it exists for the dtype and head dim; until then plain.
 // FlashAttention.swift:109-113: one query row -> split-KV decoding; 32 rows
 // or more of 16-bit data with a head dim the MFMA kernel has (64, 128, 256)
 // -> the tiled kernel (where the reference takes MPP); otherwise the plain
@@ -1114,6 +1132,129 @@ std::unique_ptr<Kernel> EmbeddingGather(const Tensor &ids, const Tensor &table, 
     return std::make_unique<FixedDispatch>(fn, std::vector<Binding>{{ids, kRead}, {table, kRead}, {out, kWrite}},
                                            std::vector<std::vector<uint8_t>>{bytesOf(ec)},
                                            grid1(runs ? std::clamp<int64_t>(cdiv(runs, kBlock), 1, 4096) : 0, kBlock));
+}
+
+namespace {
+
+// The 4-bit fast kernels' launch shape: lanes per row LPR (a row's K / 64
+// groups are dealt to LPR lanes; the largest LPR that keeps at least 90% of
+// the lanes busy, else the busiest) and x octets per thread J (2 or 8).
+struct Q4Shape {
+    int lpr = 0, j = 0;
+};
+
+Q4Shape q4Shape(int64_t K, bool xF32) {
+    Q4Shape q;
+    const int64_t G = K / 64;
+    const int64_t kMax = xF32 ? 4096 : 16384;
+    if (G <= 0 || K > kMax) return q;
+    q.j = K <= 4096 ? 2 : 8;
+    double best = -1.0;
+    for (int lpr : {32, 16, 8}) {
+        const double eff = (double)G / (double)(lpr * cdiv(G, lpr));
+        if (eff >= 0.9) {
+            q.lpr = lpr;
+            return q;
+        }
+        if (eff > best) {
+            best = eff;
+            q.lpr = lpr;
+        }
+    }
+    return q;
+}
+
+}  // namespace
+
+// Matmul.swift:99-130 and :279-332
+std::unique_ptr<Kernel> Matmul(const Tensor &a, const AffineQuantizedTensor &b, const Tensor &c) {
+    using D = DataType;
+    b.validate();
+    if (a.shape.rank() != 2) throw Error::tensorInvalidRank(2, a.shape.rank());
+    if (c.shape.rank() != 2) throw Error::tensorInvalidRank(2, c.shape.rank());
+    const int64_t m = a.shape[0], k = a.shape[1], n = b.outFeatures();
+    if (b.inFeatures() != k)
+        throw Error::tensorShapeMismatch("Matmul quantized RHS shape mismatch: a.shape=[" + std::to_string(m) + "," +
+                                         std::to_string(k) + "] but b.inFeatures=" + std::to_string(b.inFeatures()) + ".");
+    if (c.shape != Shape{m, n})
+        throw Error::tensorShapeMismatch("Matmul output shape mismatch: expected [" + std::to_string(m) + "," + std::to_string(n) +
+                                         "], got " + c.shape.str() + ".");
+    if (b.groupSize <= 0 || k % b.groupSize != 0)
+        throw Error::tensorShapeMismatch("Matmul quantized RHS: K=" + std::to_string(k) + " is not divisible by groupSize=" +
+                                         std::to_string(b.groupSize) + ".");
+    const D x = a.dataType, sd = b.scales.dataType, o = c.dataType;
+    const bool combo = (x == D::bf16 && sd == D::bf16 && (o == D::bf16 || o == D::f32)) ||
+                       (x == D::f32 && sd == D::bf16 && o == D::f32);
+    if (b.bits != 4 || b.groupSize != 64 || !combo)
+        throw Error::unsupportedDataTypeCombination(
+            "Unsupported affine quantized matmul combination: format=(bits: " + std::to_string(b.bits) + ", groupSize: " +
+            std::to_string(b.groupSize) + "), x=" + tag(x) + ", scales=" + tag(sd) + ", out=" + tag(o) + ".");
+    if (m > UINT32_MAX || n > UINT32_MAX || k > UINT32_MAX) throw Error::tensorShapeMismatch("Matmul dimensions out of range.");
+    requireElements(a, m * k, "Matmul a");
+    requireElements(c, m * n, "Matmul c");
+    requireElements(b.packedValues, n * (k / 8), "Matmul quantized packed values");
+    requireElements(b.scales, n * (k / 64), "Matmul quantized scales");
+    if (b.hasBiases) requireElements(b.biases, n * (k / 64), "Matmul quantized biases");
+    AffineQMatmulConstants qc{(uint32_t)m, (uint32_t)n, (uint32_t)k, (uint32_t)(k / 64), (uint32_t)(k / 8), b.hasBiases ? 1u : 0u};
+    const Tensor &bias = b.hasBiases ? b.biases : b.scales;
+    std::vector<Binding> binds = {{b.packedValues, kRead}, {b.scales, kRead}, {bias, kRead}, {a, kRead}, {c, kWrite}};
+    const std::string combo3 = std::string(tag(x)) + "_bf16_" + tag(o) + "_b4_g64";
+    const Q4Shape q = q4Shape(k, x == D::f32);
+    const bool aligned = aligned16(b.packedValues.data) && aligned16(a.data) &&
+                         (reinterpret_cast<uintptr_t>(b.scales.data) & 1) == 0 && (reinterpret_cast<uintptr_t>(bias.data) & 1) == 0;
+    DispatchSize ds;
+    ds.block = dim3(kBlock, 1, 1);
+    std::string fn;
+    if (q.lpr && aligned && m <= 65535) {
+        fn = std::string(m == 1 ? "aq_qmv_fast_" : "aq_matvec_simd4_") + combo3 + "_l" + std::to_string(q.lpr) + "_j" +
+             std::to_string(q.j);
+        const int64_t units = cdiv(n, 64 / q.lpr);
+        ds.grid = dim3((unsigned)streamBlocks(units), (unsigned)m, 1);
+    } else {
+        if (m > 65535) throw Error::tensorShapeMismatch("quantized Matmul supports at most 65535 rows of a.");
+        fn = "aq_matvec_simd4_" + combo3;  // 4 waves x 4 rows per block
+        ds.grid = dim3((unsigned)cdiv(n, 16), (unsigned)m, 1);
+    }
+    if (m == 0 || n == 0) ds.grid = dim3(0, 1, 1);
+    return std::make_unique<FixedDispatch>(fn, binds, std::vector<std::vector<uint8_t>>{bytesOf(qc)}, ds);
+}
+
+// EmbeddingGather.swift:45-88
+std::unique_ptr<Kernel> EmbeddingGather(const Tensor &ids, const AffineQuantizedTensor &table, const Tensor &out) {
+    using D = DataType;
+    table.validate();
+    if (ids.shape.rank() != 1) throw Error::tensorInvalidRank(1, ids.shape.rank());
+    if (ids.dataType != D::i32)
+        throw Error::unsupportedDataTypeCombination(std::string("EmbeddingGather with quantized table requires i32 ids; got ") +
+                                                    tag(ids.dataType) + ".");
+    if (out.shape.rank() != 2) throw Error::tensorInvalidRank(2, out.shape.rank());
+    const int64_t T = ids.shape[0], H = table.inFeatures(), V = table.outFeatures();
+    if (out.shape != Shape{T, H})
+        throw Error::tensorShapeMismatch("EmbeddingGather output shape mismatch: expected [" + std::to_string(T) + "," +
+                                         std::to_string(H) + "], got " + out.shape.str() + ".");
+    if (table.groupSize <= 0 || H % table.groupSize != 0)
+        throw Error::tensorShapeMismatch("EmbeddingGather quantized table hiddenSize=" + std::to_string(H) +
+                                         " is not divisible by groupSize=" + std::to_string(table.groupSize) + ".");
+    if (table.bits != 4 || table.groupSize != 64)
+        throw Error::unsupportedDataTypeCombination(
+            "EmbeddingGather currently only supports affine quantized tables with bits=4, groupSize=64, "
+            "packing=.uint32LittleEndian.");
+    if (table.scales.dataType != D::bf16 || !(out.dataType == D::bf16 || out.dataType == D::f32))
+        throw Error::unsupportedDataTypeCombination(std::string("Unsupported quantized EmbeddingGather combination: scales ") +
+                                                    tag(table.scales.dataType) + ", out " + tag(out.dataType) + ".");
+    if (V > UINT32_MAX || H > UINT32_MAX || T > UINT32_MAX) throw Error::tensorShapeMismatch("EmbeddingGather dimensions out of range.");
+    requireElements(table.packedValues, V * (H / 8), "EmbeddingGather quantized packed values");
+    requireElements(table.scales, V * (H / 64), "EmbeddingGather quantized scales");
+    if (table.hasBiases) requireElements(table.biases, V * (H / 64), "EmbeddingGather quantized biases");
+    requireElements(out, T * H, "EmbeddingGather out");
+    AffineQEmbeddingGatherConstants gc{(uint32_t)T, (uint32_t)H, (uint32_t)(H / 64), (uint32_t)(H / 8),
+                                       table.hasBiases ? 1u : 0u, (uint32_t)V};
+    const Tensor &bias = table.hasBiases ? table.biases : table.scales;
+    const std::string fn = std::string("aq_embedding_gather_bf16_") + tag(out.dataType) + "_b4_g64";
+    const int64_t words = T * (H / 8);
+    return std::make_unique<FixedDispatch>(
+        fn, std::vector<Binding>{{ids, kRead}, {table.packedValues, kRead}, {table.scales, kRead}, {bias, kRead}, {out, kWrite}},
+        std::vector<std::vector<uint8_t>>{bytesOf(gc)}, grid1(words ? std::clamp<int64_t>(cdiv(words, kBlock), 1, 4096) : 0, kBlock));
 }
 
 // Argmax.swift:24-37

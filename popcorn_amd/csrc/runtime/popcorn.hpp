@@ -279,6 +279,21 @@ struct AttentionMask {
     int32_t window = -1;
 };
 
+// AffineQuantizedTensor (AffineQuantizedTensor.swift:19-84): packed u32
+// values, scales and optional biases [..., out, in / groupSize], logical shape
+// [..., out, in]; MLX-style little-endian packing (the only packing the
+// reference defines, AffineQuantizationFormat.swift:24-30).
+struct AffineQuantizedTensor {
+    Tensor packedValues, scales, biases;
+    bool hasBiases = false;
+    Shape shape;
+    int bits = 4, groupSize = 64;
+    int64_t outFeatures() const { return shape[shape.rank() - 2]; }
+    int64_t inFeatures() const { return shape[shape.rank() - 1]; }
+    // The checks of AffineQuantizedTensor.init (AffineQuantizedTensor.swift:22-54).
+    void validate() const;
+};
+
 namespace Kernels {
 
 enum class AttentionPath { plain = POPCORN_ATTENTION_PLAIN, tiled = POPCORN_ATTENTION_TILED, decoding = POPCORN_ATTENTION_DECODING };
@@ -369,6 +384,10 @@ struct DecodeAttentionArgs {
 std::unique_ptr<Kernel> DecodeAttention(const DecodeAttentionArgs &args);
 
 std::unique_ptr<Kernel> EmbeddingGather(const Tensor &ids, const Tensor &table, const Tensor &out);
+// Matmul(_:_:into:) with a quantized RHS (Matmul.swift:99-130) and
+// EmbeddingGather(ids:table:into:) with a quantized table (EmbeddingGather.swift:45-88).
+std::unique_ptr<Kernel> Matmul(const Tensor &a, const AffineQuantizedTensor &b, const Tensor &c);
+std::unique_ptr<Kernel> EmbeddingGather(const Tensor &ids, const AffineQuantizedTensor &table, const Tensor &out);
 std::unique_ptr<Kernel> Argmax(const Tensor &x, const Tensor &indices);
 
 std::unique_ptr<Kernel> Custom(const std::string &functionName, std::vector<Binding> tensors,

@@ -243,6 +243,44 @@ def _d(t: Optional[Tensor]):
     return None if t is None else C.byref(t.desc())
 
 
+# ---- block-affine quantized weights (AffineQuantizedTensor.swift:19-84) ----------
+
+class AffineQuantizedTensor:
+    """packed_values (u32 [..., out, in * bits / 32]), scales and optional biases
+    ([..., out, in / group_size]) of a logical [..., out, in] tensor:
+    w = q * scale + bias, values packed least-significant first
+    (AffineQuantizationFormat.swift:24-30). Validated as the reference's init is."""
+
+    def __init__(self, packed_values: Tensor, scales: Tensor, biases: Optional[Tensor], shape: Sequence[int],
+                 bits: int = 4, group_size: int = 64):
+        self.packed_values, self.scales, self.biases = packed_values, scales, biases
+        self.shape, self.bits, self.group_size = list(shape), bits, group_size
+        check(lib().popcorn_affine_quantized_validate(C.byref(self.desc())))
+
+    @property
+    def out_features(self) -> int:
+        return self.shape[-2]
+
+    @property
+    def in_features(self) -> int:
+        return self.shape[-1]
+
+    def desc(self) -> _capi.AffineQuantizedDesc:
+        d = _capi.AffineQuantizedDesc()
+        d.packed_values = self.packed_values.desc()
+        d.scales = self.scales.desc()
+        if self.biases is not None:
+            d.biases = self.biases.desc()
+        d.rank = len(self.shape)
+        for i, v in enumerate(self.shape):
+            d.shape[i] = v
+        d.bits, d.group_size = self.bits, self.group_size
+        return d
+
+    def tensors(self):
+        return [t for t in (self.packed_values, self.scales, self.biases) if t is not None]
+
+
 # ---- masks (AttentionMask.swift:17-41) -------------------------------------------
 
 @dataclass(frozen=True)
@@ -436,9 +474,13 @@ class Kernels:
                      refs=refs)
 
     @staticmethod
-    def Matmul(a: Tensor, b: Tensor, into: Tensor, transpose_b: bool = False, *, m: Optional[int] = None,
+    def Matmul(a: Tensor, b, into: Tensor, transpose_b: bool = False, *, m: Optional[int] = None,
                k: int = 0, n: int = 0) -> Kernel:
-        """Matmul(_:_:into:transposeB:) (Matmul.swift:68-93) or, with m=..., the dims init (:9-66)."""
+        """Matmul(_:_:into:transposeB:) (Matmul.swift:68-93) or, with m=..., the dims init (:9-66);
+        with an AffineQuantizedTensor b, Matmul(_:_:into:) (:99-130): c = a b^T."""
+        if isinstance(b, AffineQuantizedTensor):
+            return _make(lib().popcorn_kernel_matmul_quantized, _d(a), C.byref(b.desc()), _d(into),
+                         refs=[a, into] + b.tensors())
         if m is None:
             return _make(lib().popcorn_kernel_matmul, _d(a), _d(b), _d(into), int(transpose_b), refs=(a, b, into))
         return _make(lib().popcorn_kernel_matmul_dims, _d(a), _d(b), _d(into), m, k, n, int(transpose_b),
@@ -575,7 +617,11 @@ class Kernels:
         return _make(lib().popcorn_kernel_decode_attention, C.byref(a), refs=list(ts.values()))
 
     @staticmethod
-    def EmbeddingGather(ids: Tensor, table: Tensor, into: Tensor) -> Kernel:
+    def EmbeddingGather(ids: Tensor, table, into: Tensor) -> Kernel:
+        """EmbeddingGather(ids:table:into:) (EmbeddingGather.swift:29-38, quantized table :45-88)."""
+        if isinstance(table, AffineQuantizedTensor):
+            return _make(lib().popcorn_kernel_embedding_gather_quantized, _d(ids), C.byref(table.desc()), _d(into),
+                         refs=[ids, into] + table.tensors())
         return _make(lib().popcorn_kernel_embedding_gather, _d(ids), _d(table), _d(into), refs=(ids, table, into))
 
     @staticmethod

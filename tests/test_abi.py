@@ -185,6 +185,55 @@ def test_rope_transpose_validation_and_routing():
     assert e.value.code == E.UNSUPPORTED_DATA_TYPE_COMBINATION
 
 
+def _q4(out, inn, scale_dt="bf16", bias=True, packed_dt="u32", bias_shape=None, ptr=FAKE + 2 ** 33, rank2=True):
+    packed = T([out, inn // 8], packed_dt, ptr)
+    scales = T([out, inn // 64], scale_dt, ptr + 2 ** 30)
+    biases = T(bias_shape or [out, inn // 64], scale_dt, ptr + 2 ** 31) if bias else None
+    return pa.AffineQuantizedTensor(packed, scales, biases, [out, inn] if rank2 else [inn])
+
+
+def test_quantized_validation_and_routing():
+    # AffineQuantizedTensor.swift:29-48, Matmul.swift:99-130 / :279-332, EmbeddingGather.swift:45-88
+    E = pa.PopcornError
+    for kw, code in ((dict(packed_dt="f32"), E.UNSUPPORTED_DATA_TYPE_COMBINATION),
+                     (dict(bias_shape=[10, 3]), E.TENSOR_SHAPE_MISMATCH),
+                     (dict(rank2=False), E.TENSOR_INVALID_RANK)):
+        with pytest.raises(E) as e:
+            _q4(9216, 2304, **kw)
+        assert e.value.code == code
+    w = _q4(9216, 2304)
+    out = T([1, 9216], "bf16", FAKE + 2 ** 20)
+    assert pa.Kernels.Matmul(T([1, 2304]), w, out).describe() == "aq_qmv_fast_bf16_bf16_bf16_b4_g64_l8_j2"
+    assert pa.Kernels.Matmul(T([4, 2304]), w, T([4, 9216], "f32")).describe() == "aq_matvec_simd4_bf16_bf16_f32_b4_g64_l8_j2"
+    down = _q4(2304, 9216)
+    assert pa.Kernels.Matmul(T([1, 9216]), down, T([1, 2304])).describe() == "aq_qmv_fast_bf16_bf16_bf16_b4_g64_l32_j8"
+    # unaligned activations or f32 x past 4096 take the any-shape kernel
+    assert pa.Kernels.Matmul(T([1, 2304], ptr=FAKE + 2), w, out).describe() == "aq_matvec_simd4_bf16_bf16_bf16_b4_g64"
+    assert pa.Kernels.Matmul(T([1, 9216], "f32"), down, T([1, 2304], "f32")).describe() == \
+        "aq_matvec_simd4_f32_bf16_f32_b4_g64"
+    with pytest.raises(E) as e:
+        pa.Kernels.Matmul(T([1, 2300]), w, out)
+    assert e.value.code == E.TENSOR_SHAPE_MISMATCH and "b.inFeatures=2304" in str(e.value)
+    with pytest.raises(E) as e:
+        pa.Kernels.Matmul(T([1, 2304], "f16"), w, T([1, 9216], "f16"))
+    assert e.value.code == E.UNSUPPORTED_DATA_TYPE_COMBINATION
+    with pytest.raises(E) as e:
+        pa.Kernels.Matmul(T([1, 2304]), w, T([1, 9215]))
+    assert e.value.code == E.TENSOR_SHAPE_MISMATCH
+    with pytest.raises(E) as e:
+        pa.Kernels.Matmul(T([1, 96]), _q4(8, 96 + 32), T([1, 8]))
+    assert e.value.code == E.TENSOR_SHAPE_MISMATCH
+    emb = _q4(256000, 2304)
+    ids = T([3], "i32")
+    assert pa.Kernels.EmbeddingGather(ids, emb, T([3, 2304])).describe() == "aq_embedding_gather_bf16_bf16_b4_g64"
+    with pytest.raises(E) as e:
+        pa.Kernels.EmbeddingGather(T([3], "i64"), emb, T([3, 2304]))
+    assert e.value.code == E.UNSUPPORTED_DATA_TYPE_COMBINATION
+    with pytest.raises(E) as e:
+        pa.Kernels.EmbeddingGather(ids, emb, T([3, 2300]))
+    assert e.value.code == E.TENSOR_SHAPE_MISMATCH
+
+
 def test_gated_mlp_validation_and_routing():
     E = pa.PopcornError
     k = pa.Kernels.GatedMLP(T([2304]), T([2304], "f32"), T([9216, 2304]), T([9216, 2304]), T([2304, 9216]),

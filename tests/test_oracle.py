@@ -417,6 +417,69 @@ def test_transpose12_vs_numpy(oracle, shape):
     np.testing.assert_array_equal(oracle.transpose12(y), x)
 
 
+# ---- block-affine 4-bit weights ---------------------------------------------------
+# The reference's tests hold no quantized case; the oracle is pinned by the
+# format's bit layout, float64 algebra and exact integer products.
+
+def test_aq_unpack_bit_layout(oracle):
+    # AffineQuantizationFormat.swift:27-28: value i in bits (i % 8) * 4 of word i / 8
+    words = np.array([0x87654321, 0x0000000F], np.uint32)
+    assert oracle.aq_unpack(words, 16).tolist() == [1, 2, 3, 4, 5, 6, 7, 8, 15, 0, 0, 0, 0, 0, 0, 0]
+    from q4util import pack_q4, unpack_q4
+    rng = np.random.default_rng(0)
+    q = rng.integers(0, 16, (3, 64)).astype(np.uint32)
+    packed = pack_q4(q)
+    assert np.array_equal(unpack_q4(packed, 64), q)
+    assert oracle.aq_unpack(packed[1], 64).tolist() == q[1].tolist()
+
+
+@pytest.mark.parametrize("bias", [True, False])
+def test_aq_matmul_vs_float64_dequantized(oracle, bias):
+    from q4util import dequantize_q4, quantize_q4
+    rng = np.random.default_rng(1)
+    M, N, K = 3, 40, 256
+    packed, s, b, q = quantize_q4(0.05 * rng.standard_normal((N, K)), bias=bias)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    y = oracle.aq_matmul(x, packed, s, b, N, K)
+    w64 = q.astype(np.float64) * np.repeat(s, 64, 1).astype(np.float64)
+    if bias:
+        w64 += np.repeat(b, 64, 1)
+    assert_approx(y, x.astype(np.float64) @ w64.T, 1e-5, "aq matmul")
+    # the reference's fast-path algebra: sum_g s_g sum(x q) + b_g sum(x)
+    xg = x.astype(np.float64).reshape(M, K // 64, 64)
+    qg = q.astype(np.float64).reshape(N, K // 64, 64)
+    fast = np.einsum("mgk,ngk->mng", xg, qg) * s[None].astype(np.float64)
+    if bias:
+        fast += xg.sum(-1)[:, None, :] * b[None].astype(np.float64)
+    assert_approx(y, fast.sum(-1), 1e-5, "aq matmul identity")
+    # dequantizing first (q * s + b in f32) gives the same product
+    assert_approx(y, oracle.matmul(x, dequantize_q4(q, s, b), M, K, N, True).reshape(M, N), 1e-5, "dense")
+
+
+def test_aq_matmul_integer_exact(oracle):
+    # x small integers, s a power of two, b an integer: every product and sum is exact
+    from q4util import pack_q4
+    rng = np.random.default_rng(2)
+    M, N, K = 2, 24, 192
+    q = rng.integers(0, 16, (N, K)).astype(np.uint32)
+    s = np.full((N, K // 64), 2.0, np.float32)
+    b = rng.integers(-8, 8, (N, K // 64)).astype(np.float32)
+    x = rng.integers(-3, 4, (M, K)).astype(np.float32)
+    w = q.astype(np.int64) * 2 + np.repeat(b, 64, 1).astype(np.int64)
+    y = oracle.aq_matmul(x, pack_q4(q), s, b, N, K)
+    np.testing.assert_array_equal(y, (x.astype(np.int64) @ w.T).astype(np.float32))
+
+
+def test_aq_embedding_gather_vs_numpy(oracle):
+    from q4util import dequantize_q4, quantize_q4
+    rng = np.random.default_rng(3)
+    V, H = 50, 128
+    packed, s, b, q = quantize_q4(rng.standard_normal((V, H)))
+    ids = np.array([7, 0, 49, 7], np.int32)
+    out = oracle.aq_embedding_gather(ids, packed, s, b, H)
+    np.testing.assert_array_equal(out, dequantize_q4(q, s, b)[ids])
+
+
 # ---- glue -------------------------------------------------------------------
 
 def test_argmax_and_gather_kats(oracle):
