@@ -120,6 +120,53 @@ def copy_calibration(pa, nbytes=1 << 30, copies=3):
     print(json.dumps({"calibration": "device-to-device copy", "bytes": nbytes, "copies": copies}))
 
 
+def timed_launches(pa, stream, enc, kerns):
+    """Mean microseconds per launch of `kerns`, enqueued by one native call
+    (no Python between launches) between two events on `stream`."""
+    e0, e1 = pa.Event(), pa.Event()
+    e0.record(stream)
+    enc.encode(*kerns)
+    e1.record(stream)
+    e1.synchronize()
+    return e0.elapsed_ms(e1) * 1e3 / len(kerns)
+
+
+def q4_sweep(pa, lib, stream, enc):
+    """The 4-bit decode matvec (aq_qmv_fast, bf16 x, bf16 scales and biases,
+    group 64) at the Gemma-2-2B decode shapes; every launch reads a weight set
+    it has not read for >= 512 MB of others (cold in the MALL). Bytes: packed
+    words + scales + biases + x + y."""
+    rows = []
+    for name, N, K in (("qkv", 4096, 2304), ("o_proj", 2304, 2048), ("gate_or_up", 9216, 2304),
+                       ("down", 2304, 9216), ("lm_head", 256000, 2304)):
+        wbytes = N * K // 2 + 2 * N * (K // 64) * 2
+        nbytes = wbytes + K * 2 + N * 2
+        sets = max(1, min(64, -(-(512 << 20) // wbytes)))
+        packed = pa.Tensor.empty([sets * N * K // 8], "u32")
+        scales = pa.Tensor.empty([sets * N * (K // 64)], "bf16")
+        biases = pa.Tensor.empty([sets * N * (K // 64)], "bf16")
+        lib.fill_normal(packed.view([sets * N * K // 8], "f32"), 1, stream=stream)
+        lib.fill_normal(scales, 2, std=0.01, stream=stream)
+        lib.fill_normal(biases, 3, std=0.01, stream=stream)
+        x = pa.Tensor.empty([1, K], "bf16")
+        lib.fill_normal(x, 4, stream=stream)
+        y = pa.Tensor.empty([1, N], "bf16")
+        qts = [pa.AffineQuantizedTensor(packed.view([N, K // 8], offset_elements=i * N * K // 8),
+                                        scales.view([N, K // 64], offset_elements=i * N * (K // 64)),
+                                        biases.view([N, K // 64], offset_elements=i * N * (K // 64)), [N, K])
+               for i in range(sets)]
+        kerns = [pa.Kernels.Matmul(x, q, y) for q in qts]
+        reps = max(sets, min(512, int(4e9 // nbytes)))
+        enc.encode(*kerns)
+        stream.synchronize()
+        us = timed_launches(pa, stream, enc, [kerns[r % sets] for r in range(reps)])
+        gbs = nbytes / (us * 1e-6) / 1e9
+        rows.append({"matvec": name, "N": N, "K": K, "kernel": kerns[0].function_names[0], "us": round(us, 2),
+                     "bytes": nbytes, "GB_s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 3)})
+        del kerns, qts, packed, scales, biases
+    return rows
+
+
 def fd_sweep(pa, lib, stream, enc):
     """split-KV FlashDecoding (partial + LSE combine) in f16,
     Q [B, 8, 1, 256], K/V [B, 4, ctx, 256] N(0, 1), scale 1/16, no mask, over
@@ -146,13 +193,7 @@ def fd_sweep(pa, lib, stream, enc):
             reps = max(sets, min(256, int(4e9 // nbytes)))
             enc.encode(*kerns)
             stream.synchronize()
-            e0, e1 = pa.Event(), pa.Event()
-            e0.record(stream)
-            for r in range(reps):
-                enc.encode(kerns[r % sets])
-            e1.record(stream)
-            e1.synchronize()
-            us = e0.elapsed_ms(e1) * 1e3 / reps
+            us = timed_launches(pa, stream, enc, [kerns[r % sets] for r in range(reps)])
             gbs = nbytes / (us * 1e-6) / 1e9
             out_rows.append({"B": B, "ctx": ctx, "us": round(us, 2), "GB_s": round(gbs, 1),
                              "frac": round(gbs / HBM_PEAK_GBS, 3)})
@@ -281,6 +322,7 @@ def main():
     ap.add_argument("--kernel-reps", type=int, default=4)
     ap.add_argument("--no-fd-sweep", action="store_true", help="skip the config-2 FlashDecoding sweep")
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-5 prefill measurement")
+    ap.add_argument("--no-q4", action="store_true", help="skip the 4-bit matvec measurement")
     ap.add_argument("--no-attention-block", action="store_true",
                     help="skip the decode with per-head norms and RoPE (a real attention block)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -346,6 +388,10 @@ def main():
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(dec, cfg, stream, token)
 
+    q4 = None
+    if not args.no_q4:
+        q4 = q4_sweep(pa, lib, stream, pa.KernelCommandEncoder(lib, stream))
+
     block = None
     if not args.no_attention_block:
         block = attention_block_decode(pa, lib, stream, D, token, args.steps, args.warmup, args.graph_steps,
@@ -375,6 +421,7 @@ def main():
         "flash_decoding_config2": fd,
         "prefill_config5": prefill,
         "decode_attention_block": block,
+        "q4_matvec": q4,
         "cpu_baseline": cpu,
     }
     dec.close()
