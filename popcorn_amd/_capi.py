@@ -37,6 +37,12 @@ class AffineQuantizedDesc(C.Structure):
                 ("group_size", C.c_int32)]
 
 
+class SafetensorsInfo(C.Structure):
+    _fields_ = [("name", C.c_char * 256), ("dtype_name", C.c_char * 16), ("dtype", C.c_int32), ("rank", C.c_int32),
+                ("shape", C.c_int64 * MAX_RANK), ("offset", C.c_uint64), ("nbytes", C.c_uint64),
+                ("index", C.c_int32)]
+
+
 class DeviceInfo(C.Structure):
     _fields_ = [("name", C.c_char * 64), ("arch", C.c_char * 32), ("compute_units", C.c_int32),
                 ("wave_size", C.c_int32), ("max_threads_per_block", C.c_int32),
@@ -170,6 +176,15 @@ PROTOTYPES = {
     "popcorn_kernel_describe": (_st, [C.c_void_p, C.c_char_p, C.c_size_t]),
     "popcorn_fill_normal": (_st, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_uint64, C.c_uint64,
                                   C.c_float, C.c_float]),
+    # include/popcorn_safetensors.h
+    "popcorn_safetensors_open": (_st, [C.c_char_p, C.POINTER(C.c_void_p)]),
+    "popcorn_safetensors_close": (_st, [C.c_void_p]),
+    "popcorn_safetensors_count": (C.c_int32, [C.c_void_p]),
+    "popcorn_safetensors_info": (_st, [C.c_void_p, C.c_int32, C.POINTER(SafetensorsInfo)]),
+    "popcorn_safetensors_find": (_st, [C.c_void_p, C.c_char_p, C.POINTER(SafetensorsInfo)]),
+    "popcorn_safetensors_metadata": (_st, [C.c_void_p, C.c_char_p, C.c_char_p, C.c_size_t]),
+    "popcorn_safetensors_read": (_st, [C.c_void_p, C.c_char_p, C.c_void_p, C.c_size_t]),
+    "popcorn_safetensors_upload": (_st, [C.c_void_p, C.c_char_p, C.c_void_p, C.c_size_t, C.c_void_p]),
     # include/popcorn_decoder.h
     "popcorn_decoder_create": (_st, [C.c_void_p, C.c_void_p, C.POINTER(DecoderConfig), C.POINTER(C.c_void_p)]),
     "popcorn_decoder_destroy": (_st, [C.c_void_p]),

@@ -116,3 +116,54 @@ def test_quantized_embedding_gather(env, ot):
     # q * s + b in f32 (a fused multiply-add may round once where the oracle rounds twice)
     assert_out(got[:4], ref, 1e-6, ot, "aq gather")
     assert not got[4:].any()
+
+
+def _archive(path, entries):
+    """A safetensors file from {name: (dtype name, shape, bytes)} in order."""
+    import json
+    import struct
+    header, blobs, at = {}, [], 0
+    for name, (dt, shape, data) in entries.items():
+        header[name] = {"dtype": dt, "shape": list(shape), "data_offsets": [at, at + len(data)]}
+        blobs.append(data)
+        at += len(data)
+    h = json.dumps(header).encode()
+    h += b" " * (-len(h) % 8)
+    path.write_bytes(struct.pack("<Q", len(h)) + h + b"".join(blobs))
+    return str(path)
+
+
+def test_weight_loader_quantized_matmul_from_archive(env, tmp_path):
+    # An MLX-style archive (Gemma4WeightLoader.swift:80-119): packed U32
+    # "<name>.weight" with BF16 "<name>.scales" and "<name>.biases" -> an
+    # AffineQuantizedTensor on the device; a dense BF16 weight next to it.
+    from popcorn_amd.safetensors import SafeTensors, WeightLoader
+
+    pa, lib, stream, enc = env
+    rng = np.random.default_rng(8)
+    N, K = 512, 2304
+    packed, s, b, q = quantize_q4(0.05 * rng.standard_normal((N, K)).astype(np.float32))
+    dense = rounded(0.05 * rng.standard_normal((64, K)).astype(np.float32), "bf16")
+    pre = "language_model.model.layers.0.mlp."
+    path = _archive(tmp_path / "q.safetensors", {
+        pre + "up_proj.weight": ("U32", packed.shape, packed.tobytes()),
+        pre + "up_proj.scales": ("BF16", s.shape, O.to_bits(s, O.BF16).tobytes()),
+        pre + "up_proj.biases": ("BF16", b.shape, O.to_bits(b, O.BF16).tobytes()),
+        pre + "down_proj.weight": ("BF16", dense.shape, O.to_bits(dense, O.BF16).tobytes()),
+    })
+    wl = WeightLoader(SafeTensors(path), {"bits": 4, "group_size": 64})
+    assert wl.language_model_prefix == "language_model.model"
+    up = wl.linear(wl.layer_prefix(0) + ".mlp.up_proj", stream)
+    down = wl.linear(wl.layer_prefix(0) + ".mlp.down_proj", stream)
+    assert isinstance(up, pa.AffineQuantizedTensor) and up.shape == [N, K]
+    assert isinstance(down, pa.Tensor) and down.dtype == "bf16" and list(down.shape) == [64, K]
+    np.testing.assert_array_equal(up.packed_values.numpy(stream), packed)
+    x = rounded(rng.standard_normal((1, K)).astype(np.float32), "bf16")
+    got, k = _matmul(env, x, up, "bf16", "bf16", N)
+    assert k.function_names[0].startswith("aq_qmv_fast_bf16_bf16_bf16_b4_g64")
+    assert_out(got, O.aq_matmul(x, packed, s, b, N, K), EPS["bf16"], "bf16", "archive q4 matmul")
+    td = pa.Tensor.empty([1, 64], "bf16")
+    enc.encode(pa.Kernels.Matmul(upload(pa, x, "bf16"), down, td, True))
+    stream.synchronize()
+    assert_out(download(td, stream).reshape(1, 64), O.matmul(x, dense, 1, K, 64, True).reshape(1, 64), EPS["bf16"],
+               "bf16", "archive dense matmul")
