@@ -93,6 +93,24 @@ typedef struct {
     int64_t shape[POPCORN_MAX_RANK];
 } popcorn_tensor_t;
 
+/* ---- block-affine 4-bit weights (AffineQuantizedTensor.swift:19-84) ------
+ * w = q * scale + bias, q unsigned `bits` wide, packed least-significant
+ * first into little-endian u32 words (AffineQuantizationFormat.swift:24-30),
+ * one scale/bias pair per `group_size` values along the inner axis.
+ * packed_values u32 [..., out, in * bits / 32]; scales and biases
+ * [..., out, in / group_size]; biases.data == NULL for none; shape is the
+ * logical (dequantized) shape, rank >= 2. The kernels take bits 4, group 64,
+ * bf16 scales. */
+typedef struct {
+    popcorn_tensor_t packed_values;
+    popcorn_tensor_t scales;
+    popcorn_tensor_t biases;
+    int32_t rank;
+    int64_t shape[POPCORN_MAX_RANK];
+    int32_t bits;
+    int32_t group_size;
+} popcorn_affine_quantized_tensor_t;
+
 /* Tensor.DataType.stride (Tensor.swift:152-159); 0 for an unknown tag. */
 int32_t popcorn_dtype_stride(int32_t dtype);
 
@@ -362,6 +380,17 @@ popcorn_status_t popcorn_kernel_gated_mlp_residual(const popcorn_tensor_t *x_in,
                                                    const popcorn_tensor_t *out, float eps, int32_t add_one_to_weight,
                                                    const popcorn_tensor_t *hidden, popcorn_kernel_t *kernel);
 
+/* popcorn_kernel_gated_mlp_residual with block-affine 4-bit gate, up and down
+ * weights (bf16 x/out, bf16 scales, group 64) and an f32 pre-FFN norm weight;
+ * delta, w_post and x_out all NULL for the plain form. No single counterpart
+ * in the reference (its quantized Matmul dispatches, Matmul.swift:99-130, in
+ * the composition of Gemma4TextInference.swift:416-429). */
+popcorn_status_t popcorn_kernel_gated_mlp_residual_quantized(
+    const popcorn_tensor_t *x_in, const popcorn_tensor_t *delta, const popcorn_tensor_t *w_post,
+    const popcorn_tensor_t *x_out, const popcorn_tensor_t *norm_weight, const popcorn_affine_quantized_tensor_t *w_gate,
+    const popcorn_affine_quantized_tensor_t *w_up, const popcorn_affine_quantized_tensor_t *w_down,
+    const popcorn_tensor_t *out, float eps, const popcorn_tensor_t *hidden, popcorn_kernel_t *kernel);
+
 /* The decode-step matvec out = W v (W [N, K], one token) with the layer glue
  * around it (DecodeMatvecConstants in popcorn_kernel_types.h): with delta,
  * x = x + RMSNorm(delta) * w_post is formed and stored to x_out; with w_pre,
@@ -383,6 +412,9 @@ typedef struct {
     const popcorn_tensor_t *position;
     int64_t q_rows;
     float eps;
+    /* in place of `weight`: a block-affine 4-bit weight [N, K] (bf16 x, bf16
+     * scales, group 64, K a multiple of 64 and at most 8192) */
+    const popcorn_affine_quantized_tensor_t *qweight;
 } popcorn_decode_matvec_args_t;
 
 popcorn_status_t popcorn_kernel_decode_matvec(const popcorn_decode_matvec_args_t *args, popcorn_kernel_t *kernel);
@@ -429,23 +461,6 @@ popcorn_status_t popcorn_kernel_embedding_gather(const popcorn_tensor_t *ids, co
 popcorn_status_t popcorn_kernel_argmax(const popcorn_tensor_t *x, const popcorn_tensor_t *indices,
                                        popcorn_kernel_t *kernel);
 
-/* ---- block-affine 4-bit weights (AffineQuantizedTensor.swift:19-84) ------
- * w = q * scale + bias, q unsigned `bits` wide, packed least-significant
- * first into little-endian u32 words (AffineQuantizationFormat.swift:24-30),
- * one scale/bias pair per `group_size` values along the inner axis.
- * packed_values u32 [..., out, in * bits / 32]; scales and biases
- * [..., out, in / group_size]; biases.data == NULL for none; shape is the
- * logical (dequantized) shape, rank >= 2. The kernels take bits 4, group 64,
- * bf16 scales. */
-typedef struct {
-    popcorn_tensor_t packed_values;
-    popcorn_tensor_t scales;
-    popcorn_tensor_t biases;
-    int32_t rank;
-    int64_t shape[POPCORN_MAX_RANK];
-    int32_t bits;
-    int32_t group_size;
-} popcorn_affine_quantized_tensor_t;
 
 /* AffineQuantizedTensor.init's checks (AffineQuantizedTensor.swift:29-48). */
 popcorn_status_t popcorn_affine_quantized_validate(const popcorn_affine_quantized_tensor_t *tensor);

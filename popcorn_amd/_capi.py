@@ -81,7 +81,8 @@ _T = C.POINTER(TensorDesc)
 
 class DecodeMatvecArgs(C.Structure):
     _fields_ = [(n, _T) for n in ("x", "delta", "w_post", "x_out", "w_pre", "weight", "out", "k_cache", "v_cache",
-                                  "position")] + [("q_rows", C.c_int64), ("eps", C.c_float)]
+                                  "position")] + [("q_rows", C.c_int64), ("eps", C.c_float),
+                                                  ("qweight", C.POINTER(AffineQuantizedDesc))]
 
 
 class DecodeAttentionArgs(C.Structure):
@@ -163,6 +164,9 @@ PROTOTYPES = {
     "popcorn_kernel_gated_mlp": (_st, [_T, _T, _T, _T, _T, _T, C.c_float, C.c_int32, _T, _K]),
     "popcorn_kernel_gated_mlp_residual": (_st, [_T, _T, _T, _T, _T, _T, _T, _T, _T, C.c_float, C.c_int32, _T, _K]),
     "popcorn_kernel_decode_matvec": (_st, [C.POINTER(DecodeMatvecArgs), _K]),
+    "popcorn_kernel_gated_mlp_residual_quantized": (_st, [_T, _T, _T, _T, _T, C.POINTER(AffineQuantizedDesc),
+                                                          C.POINTER(AffineQuantizedDesc),
+                                                          C.POINTER(AffineQuantizedDesc), _T, C.c_float, _T, _K]),
     "popcorn_kernel_decode_attention": (_st, [C.POINTER(DecodeAttentionArgs), _K]),
     "popcorn_kernel_embedding_gather": (_st, [_T, _T, _T, _K]),
     "popcorn_affine_quantized_validate": (_st, [C.POINTER(AffineQuantizedDesc)]),

@@ -145,7 +145,163 @@ __device__ void aq_matvec_any(const uint32_t *__restrict__ W, const uint16_t *__
     }
 }
 
+// ---- decode forms with the layer glue (bf16 activations) ---------------------
+// The decoder layer's glue is built by Stage (stream.hpp) into xs (f32, LDS),
+// then turned into the 4-bit staging (pair words + group sums) behind it:
+// dynamic LDS = K floats + K / 2 words + K / 64 floats. Every stored
+// intermediate is rounded to bf16 (interDataType must be bf16, which is what
+// makes the xs values exact bf16 pairs).
+
+template <int LPR, int NS>
+struct Q4Lds {
+    float *xs;
+    uint32_t *xw;
+    float *gsum;
+    __device__ Q4Lds(float *lds, uint32_t K) : xs(lds), xw(reinterpret_cast<uint32_t *>(lds + K)), gsum(lds + K + K / 2) {}
+    __device__ void stage_from_xs(uint32_t K) const {
+        const float *x = xs;
+        Q4Staging<false>::build(K, xw, nullptr, gsum, [&](uint32_t, uint32_t o, float *v) {
+            const float4 a = *reinterpret_cast<const float4 *>(x + 8 * o);
+            const float4 b = *reinterpret_cast<const float4 *>(x + 8 * o + 4);
+            v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+        });
+    }
+};
+
+// DecodeMatvecConstants semantics (flags bits 0-1 compiled in as RES / PRE,
+// bit 2 the KV scatter) with W block-affine 4-bit.
+template <typename O, int LPR, bool RES, bool PRE>
+__device__ void q4_decode_matvec(const uint16_t *__restrict__ x_in, const uint16_t *__restrict__ delta,
+                                 const float *__restrict__ w_post, const float *__restrict__ w_pre,
+                                 const uint32_t *__restrict__ W, const uint16_t *__restrict__ Sc,
+                                 const uint16_t *__restrict__ Bi, typename O::storage *__restrict__ out,
+                                 uint16_t *__restrict__ x_out, typename O::storage *__restrict__ kcache,
+                                 typename O::storage *__restrict__ vcache, const int32_t *__restrict__ position,
+                                 const DecodeMatvecConstants &p, const AffineQMatmulConstants &q) {
+    extern __shared__ float lds[];
+    __shared__ float red[pk::kStreamWaves];
+    constexpr int kRows = 64 / LPR;
+    const uint32_t K = p.K, N = p.N;
+    const Q4Lds<LPR, 1> L(lds, K);
+    const uint32_t lane = threadIdx.x & 63, wave = pk::uniform(threadIdx.x >> 6);
+    const uint32_t units = (N + kRows - 1) / kRows;
+    const uint32_t first = blockIdx.x * pk::kStreamWaves + wave, stride = gridDim.x * pk::kStreamWaves;
+    const uint16_t *B = q.hasBias ? Bi : Sc;
+    auto rows = [&](uint32_t unit, int) {
+        const uint32_t r = min(unit * kRows + lane / LPR, N - 1);
+        return Q4Row{W + (uint64_t)r * q.wordsPerRow, Sc + (uint64_t)r * q.kGroups, B + (uint64_t)r * q.kGroups};
+    };
+    const bool scatter = (p.flags & pk::kKVScatter) != 0;
+    const int32_t pos = scatter ? position[0] : 0;
+    auto store = [&](uint32_t unit, const float *sums) {
+        const uint32_t row = unit * kRows + lane / LPR;
+        if (lane % LPR != 0 || row >= N) return;
+        if (scatter && row >= p.qRows) {
+            uint32_t j = row - p.qRows;
+            const bool isV = j >= p.kvRows;
+            if (isV) j -= p.kvRows;
+            if (pos >= 0 && (uint32_t)pos < p.kvStride) {
+                const uint64_t at = ((uint64_t)(j / p.headDim) * p.kvStride + (uint32_t)pos) * p.headDim + j % p.headDim;
+                (isV ? vcache : kcache)[at] = O::store(sums[0]);
+            }
+        } else {
+            out[row] = O::store(sums[0]);
+        }
+    };
+    using Stage = pk::Stage<BF16, RES, PRE, 2>;
+    Q4Stream<LPR, 1, pk::kStreamSteps, false> st;
+    if (!Stage::fast_ok(x_in, delta, w_post, w_pre, x_out, K, 1u)) {
+        Stage::finish_scalar(L.xs, red, x_in, delta, w_post, w_pre, x_out, K, 1u, p.eps, p.interDataType);
+        L.stage_from_xs(K);
+        st.init(rows, K, units, first, stride, q.hasBias != 0);
+        st.start(rows);
+        st.run(L.xw, nullptr, L.gsum, rows, store);
+        return;
+    }
+    Stage stage;
+    stage.issue(x_in, delta, w_post, w_pre, K);
+    st.init(rows, K, units, first, stride, q.hasBias != 0);
+    st.start(rows);
+    stage.finish(L.xs, red, x_out, K, 1u, p.eps, p.interDataType);
+    L.stage_from_xs(K);
+    st.run(L.xw, nullptr, L.gsum, rows, store);
+}
+
+// The gated-MLP front half (GatedMLPConstants; gated_mlp.hip's semantics)
+// with Wg and Wu block-affine 4-bit: each lane streams the same row of both.
+template <int LPR, bool RES>
+__device__ void q4_gate_up(const uint16_t *__restrict__ x, const float *__restrict__ norm_w,
+                           const uint32_t *__restrict__ Wg, const uint16_t *__restrict__ Sg, const uint16_t *__restrict__ Bg,
+                           const uint32_t *__restrict__ Wu, const uint16_t *__restrict__ Su, const uint16_t *__restrict__ Bu,
+                           uint16_t *__restrict__ h, const uint16_t *__restrict__ delta, const float *__restrict__ w_post,
+                           uint16_t *__restrict__ x_out, const GatedMLPConstants &p, const AffineQMatmulConstants &q) {
+    extern __shared__ float lds[];
+    __shared__ float red[pk::kStreamWaves];
+    constexpr int kRows = 64 / LPR;
+    const uint32_t H = p.H, F = p.F;
+    const Q4Lds<LPR, 2> L(lds, H);
+    const uint32_t lane = threadIdx.x & 63, wave = pk::uniform(threadIdx.x >> 6);
+    const uint32_t units = (F + kRows - 1) / kRows;
+    const uint32_t first = blockIdx.x * pk::kStreamWaves + wave, stride = gridDim.x * pk::kStreamWaves;
+    const uint32_t preMode = p.hasWeight ? (p.addOneToWeight ? 2u : 1u) : 0u;
+    const uint32_t inter = p.interDataType;
+    const uint16_t *BgB = q.hasBias ? Bg : Sg, *BuB = q.hasBias ? Bu : Su;
+    auto rows = [&](uint32_t unit, int s) {
+        const uint64_t r = min(unit * kRows + lane / LPR, F - 1);
+        return s == 0 ? Q4Row{Wg + r * q.wordsPerRow, Sg + r * q.kGroups, BgB + r * q.kGroups}
+                      : Q4Row{Wu + r * q.wordsPerRow, Su + r * q.kGroups, BuB + r * q.kGroups};
+    };
+    auto store = [&](uint32_t unit, const float *sums) {
+        const uint32_t row = unit * kRows + lane / LPR;
+        if (lane % LPR != 0 || row >= F) return;
+        const float g = pk::round_through(inter, sums[0]);
+        const float u = pk::round_through(inter, sums[1]);
+        const float a = pk::round_through(inter, pk::gelu_tanh(g));
+        h[row] = BF16::store(a * u);
+    };
+    using Stage = pk::Stage<BF16, RES, true, 2>;
+    Q4Stream<LPR, 2, pk::kStreamSteps, false> st;
+    if (!Stage::fast_ok(x, delta, w_post, norm_w, x_out, H, preMode)) {
+        Stage::finish_scalar(L.xs, red, x, delta, w_post, norm_w, x_out, H, preMode, p.eps, inter);
+        L.stage_from_xs(H);
+        st.init(rows, H, units, first, stride, q.hasBias != 0);
+        st.start(rows);
+        st.run(L.xw, nullptr, L.gsum, rows, store);
+        return;
+    }
+    Stage stage;
+    stage.issue(x, delta, w_post, norm_w, H);
+    st.init(rows, H, units, first, stride, q.hasBias != 0);
+    st.start(rows);
+    stage.finish(L.xs, red, x_out, H, preMode, p.eps, inter);
+    L.stage_from_xs(H);
+    st.run(L.xw, nullptr, L.gsum, rows, store);
+}
+
 }  // namespace
+
+#define Q4_DMV(ot, O, LPR, F, RES, PRE)                                                                            \
+    POPCORN_KERNEL void __launch_bounds__(256) q4_decode_matvec_bf16_##ot##_l##LPR##_f##F(                          \
+        const uint16_t *x_in, const uint16_t *delta, const float *w_post, const float *w_pre, const uint32_t *W,    \
+        const uint16_t *S, const uint16_t *B, O::storage *out, uint16_t *x_out, O::storage *kcache,               \
+        O::storage *vcache, const int32_t *position, DecodeMatvecConstants p, AffineQMatmulConstants q) {        \
+        q4_decode_matvec<O, LPR, RES, PRE>(x_in, delta, w_post, w_pre, W, S, B, out, x_out, kcache, vcache,       \
+                                           position, p, q);                                                       \
+    }
+#define Q4_DMV_F(ot, O, LPR)                                                                     \
+    Q4_DMV(ot, O, LPR, 0, false, false) Q4_DMV(ot, O, LPR, 1, true, false) Q4_DMV(ot, O, LPR, 2, false, true) \
+    Q4_DMV(ot, O, LPR, 3, true, true)
+#define Q4_GU(LPR, SUFFIX, RES)                                                                                       \
+    POPCORN_KERNEL void __launch_bounds__(256) q4_gate_up_bf16_l##LPR##SUFFIX(                                        \
+        const uint16_t *x, const float *norm_w, const uint32_t *Wg, const uint16_t *Sg, const uint16_t *Bg,           \
+        const uint32_t *Wu, const uint16_t *Su, const uint16_t *Bu, uint16_t *h, const uint16_t *delta,               \
+        const float *w_post, uint16_t *x_out, GatedMLPConstants p, AffineQMatmulConstants q) {                       \
+        q4_gate_up<LPR, RES>(x, norm_w, Wg, Sg, Bg, Wu, Su, Bu, h, delta, w_post, x_out, p, q);                     \
+    }
+#define Q4_ALL(LPR) Q4_DMV_F(bf16, BF16, LPR) Q4_DMV_F(f32, F32, LPR) Q4_GU(LPR, , false) Q4_GU(LPR, _res, true)
+Q4_ALL(8)
+Q4_ALL(16)
+Q4_ALL(32)
 
 #define AQ_MV(prefix, xt, ot, X, O, LPR, J)                                                                         \
     POPCORN_KERNEL void __launch_bounds__(256) prefix##_##xt##_bf16_##ot##_b4_g64_l##LPR##_j##J(                      \

@@ -595,6 +595,23 @@ popcorn_status_t popcorn_kernel_gated_mlp_residual(const popcorn_tensor_t *x_in,
     });
 }
 
+namespace {
+AffineQuantizedTensor quantized(const popcorn_affine_quantized_tensor_t *q, const char *what) {
+    need(q, what);
+    AffineQuantizedTensor t;
+    t.packedValues = Tensor::fromC(q->packed_values);
+    t.scales = Tensor::fromC(q->scales);
+    t.hasBiases = q->biases.data != nullptr;
+    if (t.hasBiases) t.biases = Tensor::fromC(q->biases);
+    if (q->rank < 0 || q->rank > POPCORN_MAX_RANK) throw Error::invalidArgument(std::string(what) + ": rank out of range");
+    std::vector<int64_t> dims(q->shape, q->shape + q->rank);
+    t.shape = Shape(std::move(dims));
+    t.bits = q->bits;
+    t.groupSize = q->group_size;
+    return t;
+}
+}  // namespace
+
 popcorn_status_t popcorn_kernel_decode_attention(const popcorn_decode_attention_args_t *args, popcorn_kernel_t *kernel) {
     return guarded([&] {
         need(args, "args");
@@ -656,26 +673,33 @@ popcorn_status_t popcorn_kernel_decode_matvec(const popcorn_decode_matvec_args_t
         a.position = p[9];
         a.qRows = args->q_rows;
         a.eps = args->eps;
+        AffineQuantizedTensor qw;
+        if (args->qweight) {
+            qw = quantized(args->qweight, "qweight");
+            a.qweight = &qw;
+        }
         emit(kernel, Kernels::DecodeMatvec(a));
     });
 }
 
-namespace {
-AffineQuantizedTensor quantized(const popcorn_affine_quantized_tensor_t *q, const char *what) {
-    need(q, what);
-    AffineQuantizedTensor t;
-    t.packedValues = Tensor::fromC(q->packed_values);
-    t.scales = Tensor::fromC(q->scales);
-    t.hasBiases = q->biases.data != nullptr;
-    if (t.hasBiases) t.biases = Tensor::fromC(q->biases);
-    if (q->rank < 0 || q->rank > POPCORN_MAX_RANK) throw Error::invalidArgument(std::string(what) + ": rank out of range");
-    std::vector<int64_t> dims(q->shape, q->shape + q->rank);
-    t.shape = Shape(std::move(dims));
-    t.bits = q->bits;
-    t.groupSize = q->group_size;
-    return t;
+
+popcorn_status_t popcorn_kernel_gated_mlp_residual_quantized(
+    const popcorn_tensor_t *x_in, const popcorn_tensor_t *delta, const popcorn_tensor_t *w_post,
+    const popcorn_tensor_t *x_out, const popcorn_tensor_t *norm_weight, const popcorn_affine_quantized_tensor_t *w_gate,
+    const popcorn_affine_quantized_tensor_t *w_up, const popcorn_affine_quantized_tensor_t *w_down,
+    const popcorn_tensor_t *out, float eps, const popcorn_tensor_t *hidden, popcorn_kernel_t *kernel) {
+    return guarded([&] {
+        Tensor d, w, xo, h;
+        if (delta) d = Tensor::fromC(*delta);
+        if (w_post) w = Tensor::fromC(*w_post);
+        if (x_out) xo = Tensor::fromC(*x_out);
+        if (hidden) h = Tensor::fromC(*hidden);
+        emit(kernel, Kernels::GatedMLPResidual(T(x_in, "x_in"), delta ? &d : nullptr, w_post ? &w : nullptr,
+                                               x_out ? &xo : nullptr, T(norm_weight, "norm_weight"), quantized(w_gate, "w_gate"),
+                                               quantized(w_up, "w_up"), quantized(w_down, "w_down"), T(out, "out"), eps,
+                                               hidden ? &h : nullptr));
+    });
 }
-}  // namespace
 
 popcorn_status_t popcorn_affine_quantized_validate(const popcorn_affine_quantized_tensor_t *tensor) {
     return guarded([&] { quantized(tensor, "tensor").validate(); });

@@ -457,6 +457,34 @@ int64_t streamBlocks(int64_t units) {
     return cdiv(cdiv(units, per), kBlock / 64);
 }
 
+// The 4-bit fast kernels' launch shape: lanes per row LPR (a row's K / 64
+// groups are dealt to LPR lanes; the largest LPR that keeps at least 90% of
+// the lanes busy, else the busiest) and x octets per thread J (2 or 8).
+struct Q4Shape {
+    int lpr = 0, j = 0;
+};
+
+Q4Shape q4Shape(int64_t K, bool xF32) {
+    Q4Shape q;
+    const int64_t G = K / 64;
+    const int64_t kMax = xF32 ? 4096 : 16384;
+    if (G <= 0 || K > kMax) return q;
+    q.j = K <= 4096 ? 2 : 8;
+    double best = -1.0;
+    for (int lpr : {32, 16, 8}) {
+        const double eff = (double)G / (double)(lpr * cdiv(G, lpr));
+        if (eff >= 0.9) {
+            q.lpr = lpr;
+            return q;
+        }
+        if (eff > best) {
+            best = eff;
+            q.lpr = lpr;
+        }
+    }
+    return q;
+}
+
 // MFMA GEMM tile shapes (gemm_mfma.hip): BM x BN and the block size.
 struct GemmTile {
     int bm, bn, threads;
@@ -650,6 +678,121 @@ private:
     bool addOne_, hasNorm_ = false, hasHidden_ = false, residual_ = false;
     int64_t H_ = 0, F_ = 0, R_ = 2;
     std::unique_ptr<Kernel> down_;
+};
+
+// The gated MLP with block-affine 4-bit gate, up and down weights: the fused
+// front half (q4_gate_up_*) then the 4-bit down matvec (aq_qmv_fast_*).
+// bf16 activations; the post-attention residual in front when delta is given.
+class GatedMLPQ4Kernel : public Kernel {
+public:
+    GatedMLPQ4Kernel(const Tensor &x, const Tensor &nw, const AffineQuantizedTensor &wg, const AffineQuantizedTensor &wu,
+                     const AffineQuantizedTensor &wd, const Tensor &out, float eps, const Tensor *hidden)
+        : x_(x), nw_(nw), wg_(wg), wu_(wu), wd_(wd), out_(out), eps_(eps) {
+        for (const AffineQuantizedTensor *q : {&wg, &wu, &wd}) {
+            q->validate();
+            if (q->bits != 4 || q->groupSize != 64 || q->scales.dataType != DataType::bf16 || q->shape.rank() != 2)
+                throw Error::unsupportedDataTypeCombination("GatedMLP quantized weights are 2-D, 4-bit, group 64, bf16-scaled.");
+            if (!aligned16(q->packedValues.data)) throw Error::invalidArgument("GatedMLP packed values must be 16-byte aligned");
+        }
+        F_ = wg.outFeatures();
+        H_ = wg.inFeatures();
+        if (wu.shape != wg.shape) throw Error::tensorShapeMismatch("GatedMLP up weight shape must match gate weight " + wg.shape.str() + ".");
+        if (wd.shape != Shape({H_, F_}))
+            throw Error::tensorShapeMismatch("GatedMLP down weight must be [" + std::to_string(H_) + ", " + std::to_string(F_) + "].");
+        if (wg.hasBiases != wu.hasBiases) throw Error::invalidArgument("GatedMLP gate and up weights both have biases or neither");
+        if (x.dataType != DataType::bf16 || out.dataType != DataType::bf16 || nw.dataType != DataType::f32)
+            throw Error::unsupportedDataTypeCombination("GatedMLP with quantized weights takes bf16 x and out, an f32 norm weight.");
+        if (H_ % 64 != 0 || F_ % 64 != 0 || H_ > 8192 || F_ > 16384)
+            throw Error::tensorShapeMismatch("GatedMLP quantized: H, F multiples of 64, H <= 8192, F <= 16384.");
+        if (x.shape.elementCount() != H_ || out.shape.elementCount() != H_)
+            throw Error::tensorShapeMismatch("GatedMLP decodes one row: x and out hold [" + std::to_string(H_) + "].");
+        requireElements(x, H_, "x");
+        requireElements(nw, H_, "GatedMLP norm weight");
+        for (const AffineQuantizedTensor *q : {&wg, &wu, &wd}) {
+            const int64_t n = q->outFeatures(), k = q->inFeatures();
+            requireElements(q->packedValues, n * (k / 8), "GatedMLP packed values");
+            requireElements(q->scales, n * (k / 64), "GatedMLP scales");
+            if (q->hasBiases) requireElements(q->biases, n * (k / 64), "GatedMLP biases");
+        }
+        if (hidden) {
+            if (hidden->dataType != DataType::bf16) throw Error::unsupportedDataTypeCombination("GatedMLP hidden must be bf16.");
+            requireElements(*hidden, F_, "GatedMLP hidden");
+            h_ = *hidden;
+            hasHidden_ = true;
+        }
+        lpr_ = q4Shape(H_, false).lpr;
+    }
+
+    void setResidual(const Tensor &delta, const Tensor &wPost, const Tensor &xOut) {
+        if (delta.dataType != DataType::bf16 || xOut.dataType != DataType::bf16 || wPost.dataType != DataType::f32)
+            throw Error::unsupportedDataTypeCombination("GatedMLP residual: delta and x_out bf16, post-norm weight f32.");
+        requireElements(delta, H_, "GatedMLP delta");
+        requireElements(wPost, H_, "GatedMLP post-norm weight");
+        requireElements(xOut, H_, "GatedMLP x_out");
+        if (xOut.data == x_.data) throw Error::invalidArgument("GatedMLP x_out must not alias x (blocks read x while block 0 writes x_out)");
+        delta_ = delta;
+        wPost_ = wPost;
+        xOut_ = xOut;
+        residual_ = true;
+    }
+
+    std::vector<Binding> tensors() const override {
+        std::vector<Binding> b = {{x_, kRead}, {nw_, kRead}, {out_, kWrite}};
+        for (const AffineQuantizedTensor *q : {&wg_, &wu_, &wd_}) {
+            b.push_back({q->packedValues, kRead});
+            b.push_back({q->scales, kRead});
+            if (q->hasBiases) b.push_back({q->biases, kRead});
+        }
+        if (hasHidden_) b.push_back({h_, kWrite});
+        if (residual_) {
+            b.push_back({delta_, kRead});
+            b.push_back({wPost_, kRead});
+            b.push_back({xOut_, kWrite});
+        }
+        return b;
+    }
+
+    std::string gateUpName() const {
+        return "q4_gate_up_bf16_l" + std::to_string(lpr_) + (residual_ ? "_res" : "");
+    }
+
+    std::string describe() const override {
+        Tensor h(x_.data, Shape({1, F_}), DataType::bf16), o(out_.data, Shape({1, H_}), DataType::bf16);
+        return gateUpName() + "," + Kernels::Matmul(h, wd_, o)->describe();
+    }
+
+    void encode(KernelCommandEncoder &enc) const override {
+        auto run = [&](const Tensor &h) {
+            GatedMLPConstants gc{(uint32_t)H_, (uint32_t)F_, 1u, 0u, eps_, (uint32_t)DataType::bf16, residual_ ? 1u : 0u};
+            AffineQMatmulConstants qc{1u, (uint32_t)F_, (uint32_t)H_, (uint32_t)(H_ / 64), (uint32_t)(H_ / 8),
+                                      wg_.hasBiases ? 1u : 0u};
+            const Tensor d = residual_ ? delta_ : x_, w = residual_ ? wPost_ : x_, xo = residual_ ? xOut_ : x_;
+            const size_t lds = (size_t)H_ * 4 + (size_t)H_ * 2 + (size_t)(H_ / 64) * 4;
+            FixedDispatch gu(gateUpName(),
+                             {{x_, kRead}, {nw_, kRead}, {wg_.packedValues, kRead}, {wg_.scales, kRead},
+                              {wg_.hasBiases ? wg_.biases : wg_.scales, kRead}, {wu_.packedValues, kRead}, {wu_.scales, kRead},
+                              {wu_.hasBiases ? wu_.biases : wu_.scales, kRead}, {h, kWrite}, {d, kRead}, {w, kRead},
+                              {xo, residual_ ? kWrite : kRead}},
+                             {bytesOf(gc), bytesOf(qc)}, grid1(streamBlocks(cdiv(F_, 64 / lpr_)), kBlock, lds));
+            enc.dispatch(gu);
+            Tensor hv(h.data, Shape({1, F_}), DataType::bf16), ov(out_.data, Shape({1, H_}), DataType::bf16);
+            Kernels::Matmul(hv, wd_, ov)->encode(enc);
+        };
+        if (hasHidden_) {
+            run(h_);
+        } else {
+            enc.withTemporaryTensor(ScratchSpec{{F_}, DataType::bf16}, [&](Tensor h) { run(h); });
+        }
+    }
+
+private:
+    Tensor x_, nw_;
+    AffineQuantizedTensor wg_, wu_, wd_;
+    Tensor out_, h_, delta_, wPost_, xOut_;
+    float eps_;
+    bool hasHidden_ = false, residual_ = false;
+    int64_t H_ = 0, F_ = 0;
+    int lpr_ = 8;
 };
 
 // ---------------------------------------------------------------------------
@@ -1042,18 +1185,53 @@ std::unique_ptr<Kernel> GatedMLPResidual(const Tensor &xIn, const Tensor &delta,
 
 std::unique_ptr<Kernel> DecodeAttention(const DecodeAttentionArgs &a) { return std::make_unique<DecodeAttentionKernel>(a); }
 
+std::unique_ptr<Kernel> GatedMLPResidual(const Tensor &xIn, const Tensor *delta, const Tensor *wPost, const Tensor *xOut,
+                                         const Tensor &normWeight, const AffineQuantizedTensor &wGate,
+                                         const AffineQuantizedTensor &wUp, const AffineQuantizedTensor &wDown, const Tensor &out,
+                                         float eps, const Tensor *hidden) {
+    auto k = std::make_unique<GatedMLPQ4Kernel>(xIn, normWeight, wGate, wUp, wDown, out, eps, hidden);
+    if (delta || wPost || xOut) {
+        if (!delta || !wPost || !xOut) throw Error::invalidArgument("the residual form needs delta, w_post and x_out");
+        k->setResidual(*delta, *wPost, *xOut);
+    }
+    return k;
+}
+
 std::unique_ptr<Kernel> DecodeMatvec(const DecodeMatvecArgs &a) {
-    if (!a.x || !a.weight || !a.out) throw Error::invalidArgument("DecodeMatvec needs x, weight and out");
-    const Tensor &W = *a.weight;
-    if (W.shape.rank() != 2) throw Error::tensorInvalidRank(2, W.shape.rank());
-    const int64_t N = W.shape[0], K = W.shape[1];
-    const DataType t = W.dataType, o = a.out->dataType;
-    if (!isFloat(t) || a.x->dataType != t)
-        throw Error::unsupportedDataTypeCombination("DecodeMatvec needs x and weight of one float dtype.");
+    if (!a.x || !(a.weight || a.qweight) || !a.out) throw Error::invalidArgument("DecodeMatvec needs x, a weight and out");
+    if (a.weight && a.qweight) throw Error::invalidArgument("DecodeMatvec takes a dense or a quantized weight, not both");
+    const bool q4 = a.qweight != nullptr;
+    int64_t N = 0, K = 0;
+    DataType t;
+    if (q4) {
+        const AffineQuantizedTensor &Q = *a.qweight;
+        Q.validate();
+        N = Q.outFeatures();
+        K = Q.inFeatures();
+        t = a.x->dataType;
+        if (t != DataType::bf16 || Q.bits != 4 || Q.groupSize != 64 || Q.scales.dataType != DataType::bf16)
+            throw Error::unsupportedDataTypeCombination("DecodeMatvec with a quantized weight takes bf16 x and a 4-bit, group-64, "
+                                                        "bf16-scaled weight.");
+        if (K <= 0 || N <= 0 || K % 64 != 0 || K > 8192)
+            throw Error::tensorShapeMismatch("DecodeMatvec with a quantized weight needs K a multiple of 64, 0 < K <= 8192.");
+        requireElements(Q.packedValues, N * (K / 8), "DecodeMatvec packed values");
+        requireElements(Q.scales, N * (K / 64), "DecodeMatvec scales");
+        if (Q.hasBiases) requireElements(Q.biases, N * (K / 64), "DecodeMatvec biases");
+        if (!aligned16(Q.packedValues.data)) throw Error::invalidArgument("DecodeMatvec packed values must be 16-byte aligned");
+    } else {
+        const Tensor &W = *a.weight;
+        if (W.shape.rank() != 2) throw Error::tensorInvalidRank(2, W.shape.rank());
+        N = W.shape[0];
+        K = W.shape[1];
+        t = W.dataType;
+        if (!isFloat(t) || a.x->dataType != t)
+            throw Error::unsupportedDataTypeCombination("DecodeMatvec needs x and weight of one float dtype.");
+        if (K <= 0 || N <= 0 || K > kMaxStagedK) throw Error::tensorShapeMismatch("DecodeMatvec needs 0 < K <= 16384 and N > 0.");
+        requireElements(W, N * K, "DecodeMatvec weight");
+    }
+    const DataType o = a.out->dataType;
     if (!(o == t || o == DataType::f32)) throw Error::unsupportedDataTypeCombination("DecodeMatvec output is the weight dtype or f32.");
-    if (K <= 0 || N <= 0 || K > kMaxStagedK) throw Error::tensorShapeMismatch("DecodeMatvec needs 0 < K <= 16384 and N > 0.");
     requireElements(*a.x, K, "DecodeMatvec x");
-    requireElements(W, N * K, "DecodeMatvec weight");
     uint32_t flags = 0;
     if (a.delta) {
         if (!a.wPost || !a.xOut) throw Error::invalidArgument("DecodeMatvec with delta needs wPost and xOut");
@@ -1094,10 +1272,36 @@ std::unique_ptr<Kernel> DecodeMatvec(const DecodeMatvecArgs &a) {
         requireElements(*a.out, N, "DecodeMatvec out");
     }
     dc.flags = flags;
+    const Tensor &x = *a.x;
+    if (q4) {
+        const AffineQuantizedTensor &Q = *a.qweight;
+        const int lpr = q4Shape(K, false).lpr;
+        const std::string fn = std::string("q4_decode_matvec_bf16_") + tag(o) + "_l" + std::to_string(lpr) + "_f" +
+                               std::to_string(flags & 3u);
+        AffineQMatmulConstants qc{1u, (uint32_t)N, (uint32_t)K, (uint32_t)(K / 64), (uint32_t)(K / 8), Q.hasBiases ? 1u : 0u};
+        std::vector<Binding> b = {
+            {x, kRead},
+            {a.delta ? *a.delta : x, kRead},
+            {a.wPost ? *a.wPost : x, kRead},
+            {a.wPre ? *a.wPre : x, kRead},
+            {Q.packedValues, kRead},
+            {Q.scales, kRead},
+            {Q.hasBiases ? Q.biases : Q.scales, kRead},
+            {*a.out, kWrite},
+            {a.xOut ? *a.xOut : x, a.xOut ? kWrite : kRead},
+            {a.kCache ? *a.kCache : *a.out, kWrite},
+            {a.vCache ? *a.vCache : *a.out, kWrite},
+            {a.position ? *a.position : x, kRead},
+        };
+        // LDS: x as f32, its bf16 pair words, the group sums
+        const size_t lds = (size_t)K * 4 + (size_t)K * 2 + (size_t)(K / 64) * 4;
+        return std::make_unique<FixedDispatch>(fn, std::move(b), std::vector<std::vector<uint8_t>>{bytesOf(dc), bytesOf(qc)},
+                                               grid1(streamBlocks(cdiv(N, 64 / lpr)), kBlock, lds));
+    }
     const int R = matvecRows(N);
     const std::string fn = std::string("decode_matvec_") + tag(t) + "_" + tag(o) + "_r" + std::to_string(R) + "_f" +
                            std::to_string(flags & 3u);
-    const Tensor &x = *a.x;
+    const Tensor &W = *a.weight;
     std::vector<Binding> b = {
         {x, kRead},
         {a.delta ? *a.delta : x, kRead},
@@ -1134,37 +1338,6 @@ std::unique_ptr<Kernel> EmbeddingGather(const Tensor &ids, const Tensor &table, 
                                            grid1(runs ? std::clamp<int64_t>(cdiv(runs, kBlock), 1, 4096) : 0, kBlock));
 }
 
-namespace {
-
-// The 4-bit fast kernels' launch shape: lanes per row LPR (a row's K / 64
-// groups are dealt to LPR lanes; the largest LPR that keeps at least 90% of
-// the lanes busy, else the busiest) and x octets per thread J (2 or 8).
-struct Q4Shape {
-    int lpr = 0, j = 0;
-};
-
-Q4Shape q4Shape(int64_t K, bool xF32) {
-    Q4Shape q;
-    const int64_t G = K / 64;
-    const int64_t kMax = xF32 ? 4096 : 16384;
-    if (G <= 0 || K > kMax) return q;
-    q.j = K <= 4096 ? 2 : 8;
-    double best = -1.0;
-    for (int lpr : {32, 16, 8}) {
-        const double eff = (double)G / (double)(lpr * cdiv(G, lpr));
-        if (eff >= 0.9) {
-            q.lpr = lpr;
-            return q;
-        }
-        if (eff > best) {
-            best = eff;
-            q.lpr = lpr;
-        }
-    }
-    return q;
-}
-
-}  // namespace
 
 // Matmul.swift:99-130 and :279-332
 std::unique_ptr<Kernel> Matmul(const Tensor &a, const AffineQuantizedTensor &b, const Tensor &c) {

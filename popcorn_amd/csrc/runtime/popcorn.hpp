@@ -347,6 +347,13 @@ std::unique_ptr<Kernel> GatedMLPResidual(const Tensor &xIn, const Tensor &delta,
                                          const Tensor &wDown, const Tensor &out, float eps, bool addOneToWeight,
                                          const Tensor *hidden = nullptr);
 
+// The gated MLP with block-affine 4-bit weights (bf16 activations, an f32
+// pre-FFN norm weight); with delta/wPost/xOut the residual form as above.
+std::unique_ptr<Kernel> GatedMLPResidual(const Tensor &xIn, const Tensor *delta, const Tensor *wPost, const Tensor *xOut,
+                                         const Tensor &normWeight, const AffineQuantizedTensor &wGate,
+                                         const AffineQuantizedTensor &wUp, const AffineQuantizedTensor &wDown, const Tensor &out,
+                                         float eps, const Tensor *hidden = nullptr);
+
 // Decode matvec with the decoder-layer glue folded in (DecodeMatvecConstants).
 struct DecodeMatvecArgs {
     const Tensor *x = nullptr;       // [K] the vector, or the residual stream with delta
@@ -361,6 +368,7 @@ struct DecodeMatvecArgs {
     const Tensor *position = nullptr;
     int64_t qRows = 0;
     float eps = 1e-6f;
+    const AffineQuantizedTensor *qweight = nullptr;  // in place of weight: block-affine 4-bit [N, K]
 };
 std::unique_ptr<Kernel> DecodeMatvec(const DecodeMatvecArgs &args);
 

@@ -571,7 +571,14 @@ class Kernels:
     def GatedMLPResidual(x_in: Tensor, delta: Tensor, w_post: Tensor, x_out: Tensor, norm_weight: Optional[Tensor],
                          w_gate: Tensor, w_up: Tensor, w_down: Tensor, into: Tensor, *, eps: float,
                          add_one_to_weight: bool = False, hidden: Optional[Tensor] = None) -> Kernel:
-        """x_out = x_in + RMSNorm(delta) * w_post, then into = GatedMLP(x_out)."""
+        """x_out = x_in + RMSNorm(delta) * w_post, then into = GatedMLP(x_out); with
+        AffineQuantizedTensor weights the 4-bit form (delta, w_post, x_out may then be None)."""
+        if isinstance(w_gate, AffineQuantizedTensor):
+            qs = [w_gate.desc(), w_up.desc(), w_down.desc()]
+            return _make(lib().popcorn_kernel_gated_mlp_residual_quantized, _d(x_in), _d(delta), _d(w_post),
+                         _d(x_out), _d(norm_weight), *[C.byref(q) for q in qs], _d(into), eps, _d(hidden),
+                         refs=[x_in, delta, w_post, x_out, norm_weight, into, hidden] + w_gate.tensors() +
+                         w_up.tensors() + w_down.tensors())
         return _make(lib().popcorn_kernel_gated_mlp_residual, _d(x_in), _d(delta), _d(w_post), _d(x_out),
                      _d(norm_weight), _d(w_gate), _d(w_up), _d(w_down), _d(into), eps, int(add_one_to_weight),
                      _d(hidden), refs=(x_in, delta, w_post, x_out, norm_weight, w_gate, w_up, w_down, into, hidden))
@@ -582,15 +589,21 @@ class Kernels:
                      k_cache: Optional[Tensor] = None, v_cache: Optional[Tensor] = None,
                      position: Optional[Tensor] = None, q_rows: int = 0, eps: float = 1e-6) -> Kernel:
         """Decode matvec with the layer glue (popcorn_decode_matvec_args_t)."""
-        ts = dict(x=x, delta=delta, w_post=w_post, x_out=x_out, w_pre=w_pre, weight=weight, out=into,
-                  k_cache=k_cache, v_cache=v_cache, position=position)
+        qw = weight if isinstance(weight, AffineQuantizedTensor) else None
+        ts = dict(x=x, delta=delta, w_post=w_post, x_out=x_out, w_pre=w_pre, weight=None if qw else weight,
+                  out=into, k_cache=k_cache, v_cache=v_cache, position=position)
         descs = {n: (t.desc() if t is not None else None) for n, t in ts.items()}
         a = _capi.DecodeMatvecArgs()
         for n, d in descs.items():
             setattr(a, n, C.pointer(d) if d is not None else None)
         a.q_rows = q_rows
         a.eps = eps
-        return _make(lib().popcorn_kernel_decode_matvec, C.byref(a), refs=list(ts.values()))
+        refs = list(ts.values())
+        if qw is not None:
+            qd = qw.desc()
+            a.qweight = C.pointer(qd)
+            refs += qw.tensors() + [qd]
+        return _make(lib().popcorn_kernel_decode_matvec, C.byref(a), refs=refs)
 
     @staticmethod
     def DecodeAttention(qkv: Tensor, k_cache: Tensor, v_cache: Tensor, into: Tensor, position: Tensor, *,

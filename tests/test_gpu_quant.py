@@ -167,3 +167,124 @@ def test_weight_loader_quantized_matmul_from_archive(env, tmp_path):
     stream.synchronize()
     assert_out(download(td, stream).reshape(1, 64), O.matmul(x, dense, 1, K, 64, True).reshape(1, 64), EPS["bf16"],
                "bf16", "archive dense matmul")
+
+
+# ---- decode forms with the layer glue -------------------------------------------
+
+def _q4_products(x, w_pre, packed, s, b, N, K):
+    """x W^T (W 4-bit) for each rounding outcome of the pre-norm (or x itself)."""
+    import flips
+    vs = flips.norm_candidates(x, w_pre, 1e-6, O.BF16) if w_pre is not None else [x]
+    return [O.aq_matmul(v[None], packed, s, b, N, K).ravel() for v in vs]
+
+
+@pytest.mark.parametrize("ot", ["bf16", "f32"])
+@pytest.mark.parametrize("residual,prenorm", [(False, False), (True, False), (False, True), (True, True)])
+@pytest.mark.parametrize("K,N", [(2304, 4096), (2048, 2304), (320, 77)])
+def test_q4_decode_matvec_glue(env, ot, residual, prenorm, K, N):
+    import flips
+    pa, lib, stream, enc = env
+    eps = 1e-6
+    rng = np.random.default_rng(K + N)
+    x_in = rounded(rng.standard_normal(K).astype(np.float32), "bf16")
+    delta = rounded(3 * rng.standard_normal(K).astype(np.float32), "bf16")
+    w_post = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    w_pre = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    packed, s, b, q = quantize_q4(0.02 * rng.standard_normal((N, K)).astype(np.float32))
+    out = pa.Tensor.empty([N], ot)
+    x_out = pa.Tensor.empty([K], "bf16")
+    kw = {}
+    if residual:
+        kw.update(delta=upload(pa, delta, "bf16"), w_post=pa.Tensor.from_numpy(w_post), x_out=x_out)
+    if prenorm:
+        kw.update(w_pre=pa.Tensor.from_numpy(w_pre))
+    k = pa.Kernels.DecodeMatvec(upload(pa, x_in, "bf16"), _qtensor(pa, packed, s, b, N, K), out, eps=eps, **kw)
+    f = int(residual) + 2 * int(prenorm)
+    assert k.function_names[0].startswith(f"q4_decode_matvec_bf16_{ot}_l") and k.function_names[0].endswith(f"_f{f}")
+    enc.encode(k)
+    stream.synchronize()
+    x = x_in
+    if residual:
+        x = download(x_out, stream)
+        flips.assert_any(x, flips.residual_candidates(x_in, delta, w_post, eps, O.BF16), EPS["bf16"], "bf16",
+                         "q4 residual stream")
+    flips.assert_any(download(out, stream), _q4_products(x, w_pre if prenorm else None, packed, s, b, N, K),
+                     EPS["bf16"], ot, f"q4 decode matvec r{residual} p{prenorm} {K}x{N}")
+
+
+def test_q4_decode_matvec_kv_scatter(env):
+    import flips
+    pa, lib, stream, enc = env
+    eps, Nq, Nkv, Hd, S, pos, H = 1e-6, 8, 4, 256, 4352, 4096, 2304
+    QW, KW = Nq * Hd, Nkv * Hd
+    N = QW + 2 * KW
+    rng = np.random.default_rng(12)
+    x_in = rounded(rng.standard_normal(H).astype(np.float32), "bf16")
+    delta = rounded(rng.standard_normal(H).astype(np.float32), "bf16")
+    w_post = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+    w_pre = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+    packed, s, b, q = quantize_q4(0.02 * rng.standard_normal((N, H)).astype(np.float32))
+    kc0 = rounded(rng.standard_normal((Nkv, S, Hd)).astype(np.float32), "bf16")
+    vc0 = rounded(rng.standard_normal((Nkv, S, Hd)).astype(np.float32), "bf16")
+    kc, vc = upload(pa, kc0, "bf16"), upload(pa, vc0, "bf16")
+    tq, x_out = pa.Tensor.empty([QW], "bf16"), pa.Tensor.empty([H], "bf16")
+    k = pa.Kernels.DecodeMatvec(upload(pa, x_in, "bf16"), _qtensor(pa, packed, s, b, N, H), tq,
+                                delta=upload(pa, delta, "bf16"), w_post=pa.Tensor.from_numpy(w_post), x_out=x_out,
+                                w_pre=pa.Tensor.from_numpy(w_pre), k_cache=kc, v_cache=vc,
+                                position=pa.Tensor.from_numpy(np.array([pos], np.int32)), q_rows=QW, eps=eps)
+    enc.encode(k)
+    stream.synchronize()
+    x = download(x_out, stream)
+    kg, vg = download(kc, stream).reshape(Nkv, S, Hd), download(vc, stream).reshape(Nkv, S, Hd)
+    got = np.concatenate([download(tq, stream).ravel(), kg[:, pos].ravel(), vg[:, pos].ravel()])
+    flips.assert_any(got, _q4_products(x, w_pre, packed, s, b, N, H), EPS["bf16"], "bf16", "q4 qkv + scatter")
+    others = np.ones(S, bool)
+    others[pos] = False
+    np.testing.assert_array_equal(kg[:, others], kc0[:, others])
+    np.testing.assert_array_equal(vg[:, others], vc0[:, others])
+
+
+@pytest.mark.parametrize("residual", [False, True])
+@pytest.mark.parametrize("H,F", [(2304, 9216), (256, 512)])
+def test_q4_gated_mlp(env, residual, H, F):
+    import flips
+    pa, lib, stream, enc = env
+    eps = 1e-6
+    rng = np.random.default_rng(H + F + int(residual))
+    x_in = rounded(rng.standard_normal(H).astype(np.float32), "bf16")
+    delta = rounded(rng.standard_normal(H).astype(np.float32), "bf16")
+    w_post = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+    nw = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+    gq = quantize_q4(0.02 * rng.standard_normal((F, H)).astype(np.float32))
+    uq = quantize_q4(0.02 * rng.standard_normal((F, H)).astype(np.float32))
+    dq = quantize_q4(0.02 * rng.standard_normal((H, F)).astype(np.float32))
+    out, x_out, hid = pa.Tensor.empty([H], "bf16"), pa.Tensor.empty([H], "bf16"), pa.Tensor.empty([F], "bf16")
+    qt = [_qtensor(pa, p_, s_, b_, n_, k_) for (p_, s_, b_, _), n_, k_ in ((gq, F, H), (uq, F, H), (dq, H, F))]
+    res = dict(delta=upload(pa, delta, "bf16"), w_post=pa.Tensor.from_numpy(w_post), x_out=x_out) if residual \
+        else dict(delta=None, w_post=None, x_out=None)
+    k = pa.Kernels.GatedMLPResidual(upload(pa, x_in, "bf16"), res["delta"], res["w_post"], res["x_out"],
+                                    pa.Tensor.from_numpy(nw), qt[0], qt[1], qt[2], out, eps=eps, hidden=hid)
+    names = k.function_names
+    assert names[0].startswith("q4_gate_up_bf16_l") and names[0].endswith("_res") == residual
+    assert names[1].startswith("aq_qmv_fast_bf16_bf16_bf16_b4_g64")
+    enc.encode(k)
+    stream.synchronize()
+    x = x_in
+    if residual:
+        x = download(x_out, stream)
+        flips.assert_any(x, flips.residual_candidates(x_in, delta, w_post, eps, O.BF16), EPS["bf16"], "bf16",
+                         "q4 mlp residual")
+    got_h, got = download(hid, stream), download(out, stream)
+    errors = []
+    for n in flips.norm_candidates(x, nw, eps, O.BF16):
+        g = O.round_to(O.aq_matmul(n[None], gq[0], gq[1], gq[2], F, H).ravel(), O.BF16)
+        u = O.round_to(O.aq_matmul(n[None], uq[0], uq[1], uq[2], F, H).ravel(), O.BF16)
+        h = O.round_to(O.mul(O.round_to(O.gelu_tanh(g), O.BF16), u), O.BF16)
+        try:
+            assert_out(got_h, h, EPS["bf16"], "bf16", "q4 hidden", half_ulps=2)
+            assert_out(got, O.aq_matmul(got_h[None], dq[0], dq[1], dq[2], H, F).ravel(), EPS["bf16"], "bf16",
+                       "q4 down")
+            return
+        except AssertionError as e:
+            errors.append(str(e))
+    raise AssertionError(" | ".join(errors))
