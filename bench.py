@@ -292,23 +292,29 @@ def time_decode(pa, dec, stream, token, steps, warmup, use_graph):
     return elapsed
 
 
-def attention_block_decode(pa, lib, stream, D, token, steps, warmup, graph_steps, use_graph, reps):
-    """The same decode with a real attention block (per-head q/k RMSNorm, v
-    RMSNorm, RoPE at theta 10000, Gemma4TextInference.swift:352-371) folded
-    into the attention partial kernel: tok/s and the fused kernel's time."""
-    cfg = D.DecoderConfig(graph_steps=graph_steps, attention_block=1)
+def decode_variant(pa, lib, stream, D, token, steps, warmup, graph_steps, use_graph, reps, **variant):
+    """The config-4 decode with another decoder configuration: tok/s, the HBM
+    rate of the whole step, and the mean time of each of the step's kernels.
+    attention_block=1: a real attention block (per-head q/k RMSNorm, v RMSNorm,
+    RoPE at theta 10000, Gemma4TextInference.swift:352-371) folded into the
+    attention partial kernel; weight_bits=4: block-affine 4-bit weights."""
+    cfg = D.DecoderConfig(graph_steps=graph_steps, **variant)
     dec = D.Decoder(lib, stream, cfg)
     dec.randomize(seed=0)
     elapsed = time_decode(pa, dec, stream, token, steps, warmup, use_graph)
     names, nd = dec.describe()
-    fresh = next(n for n in names if n.startswith("flash_decoding_fresh_"))
+    tok_s = steps / elapsed
+    step_bytes = dec.step_bytes(int(START_POS + (steps - 1) / 2))
     dec.reset(token, START_POS)
-    ms, _ = dec.time_kernel(fresh, reps=reps)
-    nbytes = kernel_bytes(cfg, fresh, START_POS)
+    kernels = {}
+    for name in dict.fromkeys(names):
+        if name.startswith(("embedding", "aq_embedding", "argmax", "position", "scalar_mul", "flash_decoding_reduce")):
+            continue
+        ms, _ = dec.time_kernel(name, reps=reps)
+        kernels[name] = round(ms * 1e3, 2)
     dec.close()
-    return {"tok_s": round(steps / elapsed, 2), "ms_per_step": round(elapsed * 1e3 / steps, 4),
-            "dispatches_per_step": nd, "attention_kernel": fresh, "attention_us": round(ms * 1e3, 2),
-            "attention_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 3) if nbytes else None}
+    return {"tok_s": round(tok_s, 2), "ms_per_step": round(elapsed * 1e3 / steps, 4), "dispatches_per_step": nd,
+            "hbm_step_GB_s": round(step_bytes * tok_s / 1e9, 1), "kernel_mean_us": kernels}
 
 
 def main():
@@ -392,10 +398,13 @@ def main():
     if not args.no_q4:
         q4 = q4_sweep(pa, lib, stream, pa.KernelCommandEncoder(lib, stream))
 
-    block = None
+    block = q4dec = None
     if not args.no_attention_block:
-        block = attention_block_decode(pa, lib, stream, D, token, args.steps, args.warmup, args.graph_steps,
-                                       use_graph, args.kernel_reps)
+        block = decode_variant(pa, lib, stream, D, token, args.steps, args.warmup, args.graph_steps, use_graph,
+                               args.kernel_reps, attention_block=1)
+    if not args.no_q4:
+        q4dec = decode_variant(pa, lib, stream, D, token, args.steps, args.warmup, args.graph_steps, use_graph,
+                               args.kernel_reps, weight_bits=4)
 
     line = {
         "metric": "decode tok/s (Gemma-2B shape, ctx 4K)",
@@ -422,6 +431,7 @@ def main():
         "prefill_config5": prefill,
         "decode_attention_block": block,
         "q4_matvec": q4,
+        "decode_q4": q4dec,
         "cpu_baseline": cpu,
     }
     dec.close()

@@ -51,6 +51,9 @@ typedef struct {
     int32_t attention_block; /* 1: per-head q/k RMSNorm (f32 weights), v RMSNorm
                                 without weight and RoPE on q and k              */
     float rope_theta;     /* RoPE base: inv_freq[i] = theta^(-2i/head_dim)       */
+    int32_t weight_bits;  /* 16 (or 0): bf16 weights; 4: block-affine 4-bit, group
+                             64, bf16 scales and biases (the MLX format of
+                             AffineQuantizedTensor.swift), embedding included  */
 } popcorn_decoder_config_t;
 
 typedef struct popcorn_decoder_s *popcorn_decoder_t;
@@ -68,7 +71,9 @@ popcorn_status_t popcorn_decoder_randomize(popcorn_decoder_t decoder, uint64_t s
  * "norm_post_ffn", "k_cache", "v_cache" and, with attention_block, "q_norm"
  * and "k_norm" (per `layer`); "inv_freq" (attention_block), "x", "logits",
  * "token", "position", "history", plus the last layer's step buffers
- * "q", "qkv", "attn", "o", "mlp", "hidden". */
+ * "q", "qkv", "attn", "o", "mlp", "hidden". With weight_bits 4 a weight name
+ * ("embedding", "w_qkv", ...) is its packed u32 values [N, K/8], and
+ * "<name>.scales" / "<name>.biases" its bf16 [N, K/64] groups. */
 popcorn_status_t popcorn_decoder_tensor(popcorn_decoder_t decoder, const char *name, int32_t layer,
                                         popcorn_tensor_t *tensor);
 

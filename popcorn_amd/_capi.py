@@ -73,7 +73,7 @@ class DecoderConfig(C.Structure):
                 ("kv_heads", C.c_int32), ("head_dim", C.c_int32), ("ffn", C.c_int32), ("vocab", C.c_int32),
                 ("max_seq", C.c_int32), ("eps", C.c_float), ("attn_scale", C.c_float),
                 ("history_len", C.c_int32), ("graph_steps", C.c_int32), ("attention_block", C.c_int32),
-                ("rope_theta", C.c_float)]
+                ("rope_theta", C.c_float), ("weight_bits", C.c_int32)]
 
 
 _T = C.POINTER(TensorDesc)

@@ -34,7 +34,8 @@ __device__ inline float dot2_bf16(uint32_t a, uint32_t b, float c) {
 }
 
 __device__ inline float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
-__device__ inline float bf16_hi(uint32_t v) { return __uint_as_float(v & 0xffff0000u); }
+// The bf16 of group g in the word that holds groups g & ~1 and g | 1.
+__device__ inline float bf16_half(uint32_t v, uint32_t g) { return __uint_as_float((g & 1u) ? (v & 0xffff0000u) : (v << 16)); }
 
 // Staged activations of one row of x for the 4-bit stream, in LDS.
 //   bf16 x (XF32 = false): xw[K / 2] pair words (see above), gsum[K / 64];
@@ -81,7 +82,8 @@ struct Q4Staging {
 };
 
 // The rows of a unit as seen by one lane: its row's packed words, scales and
-// biases (biases == scales when the tensor has none; hasBias says so).
+// biases (biases == scales when the tensor has none; hasBias says so). The
+// scale and bias rows start 4-byte aligned (an even number of groups per row).
 struct Q4Row {
     const uint32_t *w;
     const uint16_t *s;
@@ -99,7 +101,13 @@ struct Q4Stream {
     static_assert(LPR >= 4 && LPR <= 64 && (LPR & (LPR - 1)) == 0, "LPR is a power of two in [4, 64]");
     static constexpr int kRows = 64 / LPR;
     u32x4 wv[U][NS][2];
-    uint32_t sb[U][NS];
+    // Scale and bias of the step's group, as the aligned 32-bit word that
+    // holds the bf16 (groups 2i and 2i + 1 share a word; rows hold an even
+    // number of groups, so words never straddle rows). A full-word load
+    // needs no arithmetic at issue time: any (a 16-bit load's zero
+    // extension included) makes the compiler wait for the load right there,
+    // and as loads retire in order the whole queue would drain.
+    uint32_t sv[U][NS], bv[U][NS];
     Q4Row ip[NS];
     uint32_t G, cpl, steps, first, stride, is, ii, iu, gl;
     bool hasBias;
@@ -131,7 +139,8 @@ struct Q4Stream {
             const uint32_t *p = ip[s].w + (uint64_t)g * kQ4GroupWords;
             wv[slot][s][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
             wv[slot][s][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p + 4));
-            sb[slot][s] = (uint32_t)ip[s].s[g] | ((uint32_t)ip[s].b[g] << 16);
+            sv[slot][s] = reinterpret_cast<const uint32_t *>(ip[s].s)[g >> 1];
+            bv[slot][s] = reinterpret_cast<const uint32_t *>(ip[s].b)[g >> 1];
         }
         if (is + 1 < steps) {
             ++is;
@@ -179,8 +188,8 @@ struct Q4Stream {
                         d3 = dot2_bf16(((w >> 12) & 0x000F000Fu) | kQ4PairBase, xv[j].w, d3);
                     }
                     const float dot = (d0 + d1) + (d2 + d3);
-                    const float sc = bf16_lo(sb[slot][s]);
-                    const float bi = hasBias ? bf16_hi(sb[slot][s]) : 0.0f;
+                    const float sc = bf16_half(sv[slot][s], g);
+                    const float bi = hasBias ? bf16_half(bv[slot][s], g) : 0.0f;
                     acc[s] += sc * dot + (bi - 128.0f * sc) * xg;
                 }
             } else {
@@ -196,8 +205,8 @@ struct Q4Stream {
                               a.w * (float)((w >> 12) & 15u) + b.x * (float)((w >> 16) & 15u) +
                               b.y * (float)((w >> 20) & 15u) + b.z * (float)((w >> 24) & 15u) + b.w * (float)(w >> 28);
                     }
-                    const float sc = bf16_lo(sb[slot][s]);
-                    const float bi = hasBias ? bf16_hi(sb[slot][s]) : 0.0f;
+                    const float sc = bf16_half(sv[slot][s], g);
+                    const float bi = hasBias ? bf16_half(bv[slot][s], g) : 0.0f;
                     acc[s] += sc * qd + bi * xg;
                 }
             }

@@ -37,6 +37,38 @@ struct Buffer {
     T *at(size_t byteOffset) const { return reinterpret_cast<T *>(static_cast<uint8_t *>(p) + byteOffset); }
 };
 
+// `count` stacked [N, K] block-affine 4-bit matrices (group 64, bf16 scales
+// and biases): packed u32 [count][N][K / 8], scales and biases [count][N][K / 64].
+struct QMat {
+    Buffer packed, scales, biases;
+    int64_t N = 0, K = 0;
+    void alloc(int64_t n, int64_t k, int64_t count) {
+        N = n;
+        K = k;
+        packed = Buffer((size_t)(count * n * k / 2));
+        scales = Buffer((size_t)(count * n * (k / 64) * 2));
+        biases = Buffer((size_t)(count * n * (k / 64) * 2));
+    }
+    Tensor packedAt(int64_t l) const {
+        return Tensor(packed.at((size_t)(l * N * K / 2)), Shape({N, K / 8}), DataType::u32);
+    }
+    Tensor scalesAt(int64_t l) const {
+        return Tensor(scales.at((size_t)(l * N * (K / 64) * 2)), Shape({N, K / 64}), DataType::bf16);
+    }
+    Tensor biasesAt(int64_t l) const {
+        return Tensor(biases.at((size_t)(l * N * (K / 64) * 2)), Shape({N, K / 64}), DataType::bf16);
+    }
+    AffineQuantizedTensor at(int64_t l) const {
+        AffineQuantizedTensor q;
+        q.packedValues = packedAt(l);
+        q.scales = scalesAt(l);
+        q.biases = biasesAt(l);
+        q.hasBiases = true;
+        q.shape = Shape({N, K});
+        return q;
+    }
+};
+
 }  // namespace
 
 struct popcorn_decoder_s {
@@ -52,6 +84,8 @@ struct popcorn_decoder_s {
     // weights (bf16 unless noted) and state
     Buffer embedding, finalNorm /*f32*/, wqkv, wo, wg, wu, wd, norms /*f32 [L][4][H]*/;
     Buffer headNorms /*f32 [L][2][Hd], attention_block*/, invFreq /*f32 [Hd/2]*/;
+    bool q4 = false;  // weight_bits 4: the matrices below replace the bf16 ones
+    QMat qqkv, qo, qg, qu, qd, qemb;
     Buffer kcache, vcache;
     Buffer x, x2, e, qkv, attn, o, mlp, hidden, logits /*f32*/, token /*i32*/, position /*i32*/, history /*i32*/;
 
@@ -70,7 +104,33 @@ struct popcorn_decoder_s {
 
     size_t layerOffset(int64_t elemsPerLayer, int64_t l, int es = 2) const { return (size_t)(elemsPerLayer * l) * (size_t)es; }
 
+    const QMat *qmat(const std::string &base) const {
+        if (!q4) return nullptr;
+        if (base == "w_qkv") return &qqkv;
+        if (base == "w_o") return &qo;
+        if (base == "w_gate") return &qg;
+        if (base == "w_up") return &qu;
+        if (base == "w_down") return &qd;
+        if (base == "embedding") return &qemb;
+        return nullptr;
+    }
+
+    // "<matrix>", "<matrix>.scales", "<matrix>.biases" of a 4-bit decoder.
+    bool quantizedView(const std::string &name, int64_t l, Tensor &t) const {
+        const size_t dot = name.find('.');
+        const std::string base = name.substr(0, dot), part = dot == std::string::npos ? "" : name.substr(dot + 1);
+        const QMat *m = qmat(base);
+        if (!m) return false;
+        if (part.empty()) t = m->packedAt(l);
+        else if (part == "scales") t = m->scalesAt(l);
+        else if (part == "biases") t = m->biasesAt(l);
+        else return false;
+        return true;
+    }
+
     Tensor weight(const char *which, int64_t l) const {
+        Tensor qt;
+        if (quantizedView(which, l, qt)) return qt;
         if (!strcmp(which, "w_qkv")) return bf(wqkv.at(layerOffset(QKV * H, l)), {QKV, H});
         if (!strcmp(which, "w_o")) return bf(wo.at(layerOffset(H * QW, l)), {H, QW});
         if (!strcmp(which, "w_gate")) return bf(wg.at(layerOffset(F * H, l)), {F, H});
@@ -111,7 +171,8 @@ struct popcorn_decoder_s {
 
         auto add = [&](std::unique_ptr<Kernel> k) { step.push_back(std::move(k)); };
         // Gemma4TextInference.swift:184-185: gather, then scale by sqrt(H)
-        add(Kernels::EmbeddingGather(ttok, temb, te));
+        if (q4) add(Kernels::EmbeddingGather(ttok, qemb.at(0), te));
+        else add(Kernels::EmbeddingGather(ttok, temb, te));
         add(Kernels::ScalarMul(te, std::sqrt((float)H), tx));
         const AttentionMask causal{0, -1};
         Tensor prevPostFfn;
@@ -119,7 +180,9 @@ struct popcorn_decoder_s {
             Tensor nin = weight("norm_in", l), npa = weight("norm_post_attn", l);
             Tensor npf = weight("norm_pre_ffn", l), npo = weight("norm_post_ffn", l);
             Tensor kc = weight("k_cache", l), vc = weight("v_cache", l);
-            Tensor wqkv_l = weight("w_qkv", l), wo_l = weight("w_o", l);
+            Tensor wqkv_l = q4 ? Tensor() : weight("w_qkv", l), wo_l = q4 ? Tensor() : weight("w_o", l);
+            const AffineQuantizedTensor qqkv_l = q4 ? qqkv.at(l) : AffineQuantizedTensor(),
+                                        qo_l = q4 ? qo.at(l) : AffineQuantizedTensor();
             Kernels::DecodeMatvecArgs qkvArgs;
             if (l == 0) {
                 qkvArgs.x = &tx;
@@ -130,7 +193,8 @@ struct popcorn_decoder_s {
                 qkvArgs.xOut = &tx;
             }
             qkvArgs.wPre = &nin;
-            qkvArgs.weight = &wqkv_l;
+            if (q4) qkvArgs.qweight = &qqkv_l;
+            else qkvArgs.weight = &wqkv_l;
             qkvArgs.eps = eps;
             if (block) {
                 qkvArgs.out = &tqkv;
@@ -163,11 +227,15 @@ struct popcorn_decoder_s {
             }
             Kernels::DecodeMatvecArgs oArgs;
             oArgs.x = &tattn;
-            oArgs.weight = &wo_l;
+            if (q4) oArgs.qweight = &qo_l;
+            else oArgs.weight = &wo_l;
             oArgs.out = &to;
             add(Kernels::DecodeMatvec(oArgs));
-            add(Kernels::GatedMLPResidual(tx, to, npa, tx2, &npf, weight("w_gate", l), weight("w_up", l),
-                                          weight("w_down", l), tmlp, eps, false, &th));
+            if (q4)
+                add(Kernels::GatedMLPResidual(tx, &to, &npa, &tx2, npf, qg.at(l), qu.at(l), qd.at(l), tmlp, eps, &th));
+            else
+                add(Kernels::GatedMLPResidual(tx, to, npa, tx2, &npf, weight("w_gate", l), weight("w_up", l),
+                                              weight("w_down", l), tmlp, eps, false, &th));
             prevPostFfn = npo;
         }
         // Gemma4TextInference.swift:201-206: the last post-FFN norm + residual,
@@ -178,7 +246,9 @@ struct popcorn_decoder_s {
         head.wPost = &prevPostFfn;
         head.xOut = &tx;
         head.wPre = &tfin;
-        head.weight = &temb;
+        const AffineQuantizedTensor qemb0 = q4 ? qemb.at(0) : AffineQuantizedTensor();
+        if (q4) head.qweight = &qemb0;
+        else head.weight = &temb;
         head.out = &tlog;
         head.eps = eps;
         add(Kernels::DecodeMatvec(head));
@@ -242,9 +312,11 @@ struct popcorn_decoder_s {
     }
 
     int64_t stepBytes(int32_t pos) const {
-        const int64_t layerW = (QKV * H + H * QW + 3 * F * H) * 2 + 4 * H * 4;
+        // bytes per weight: 2 (bf16), or 1/2 + 2 x 2 / 64 (4-bit values, bf16 scale and bias per 64)
+        auto wbytes = [&](int64_t elems) { return q4 ? elems / 2 + elems / 16 : elems * 2; };
+        const int64_t layerW = wbytes(QKV * H + H * QW + 3 * F * H) + 4 * H * 4;
         const int64_t kv = 2 * Nkv * (int64_t)(pos + 1) * Hd * 2;  // K and V rows read
-        return L * (layerW + kv) + V * H * 2 + H * 4 + V * 4;
+        return L * (layerW + kv) + wbytes(V * H) + H * 4 + V * 4;
     }
 };
 
@@ -289,13 +361,27 @@ popcorn_status_t popcorn_decoder_create(popcorn_library_t library, popcorn_strea
         d->KW = d->Nkv * d->Hd;
         d->QKV = d->QW + 2 * d->KW;
         const int64_t L = d->L, H = d->H, F = d->F;
-        d->embedding = Buffer((size_t)(d->V * H * 2));
+        if (c.weight_bits != 0 && c.weight_bits != 16 && c.weight_bits != 4)
+            throw Error::invalidArgument("weight_bits is 16 (bf16) or 4 (block-affine, group 64)");
+        d->q4 = c.weight_bits == 4;
         d->finalNorm = Buffer((size_t)(H * 4));
-        d->wqkv = Buffer((size_t)(L * d->QKV * H * 2));
-        d->wo = Buffer((size_t)(L * H * d->QW * 2));
-        d->wg = Buffer((size_t)(L * F * H * 2));
-        d->wu = Buffer((size_t)(L * F * H * 2));
-        d->wd = Buffer((size_t)(L * H * F * 2));
+        if (d->q4) {
+            if (H % 128 || F % 128 || d->QW % 128)
+                throw Error::tensorShapeMismatch("4-bit weights need hidden, ffn and query width multiples of 128");
+            d->qemb.alloc(d->V, H, 1);
+            d->qqkv.alloc(d->QKV, H, L);
+            d->qo.alloc(H, d->QW, L);
+            d->qg.alloc(F, H, L);
+            d->qu.alloc(F, H, L);
+            d->qd.alloc(H, F, L);
+        } else {
+            d->embedding = Buffer((size_t)(d->V * H * 2));
+            d->wqkv = Buffer((size_t)(L * d->QKV * H * 2));
+            d->wo = Buffer((size_t)(L * H * d->QW * 2));
+            d->wg = Buffer((size_t)(L * F * H * 2));
+            d->wu = Buffer((size_t)(L * F * H * 2));
+            d->wd = Buffer((size_t)(L * H * F * 2));
+        }
         d->norms = Buffer((size_t)(L * 4 * H * 4));
         d->kcache = Buffer((size_t)(L * d->Nkv * d->S * d->Hd * 2));
         d->vcache = Buffer((size_t)(L * d->Nkv * d->S * d->Hd * 2));
@@ -346,13 +432,23 @@ popcorn_status_t popcorn_decoder_randomize(popcorn_decoder_t d, uint64_t seed) {
         auto fill = [&](Buffer &b, DataType t, float mean, float std) {
             d->enc->encode(*Kernels::FillNormal(b.p, t, b.bytes / (size_t)stride(t), ++s, mean, std));
         };
-        fill(d->embedding, DataType::bf16, 0.0f, 0.02f);
         fill(d->finalNorm, DataType::f32, 1.0f, 0.1f);
-        fill(d->wqkv, DataType::bf16, 0.0f, 0.02f);
-        fill(d->wo, DataType::bf16, 0.0f, 0.02f);
-        fill(d->wg, DataType::bf16, 0.0f, 0.02f);
-        fill(d->wu, DataType::bf16, 0.0f, 0.02f);
-        fill(d->wd, DataType::bf16, 0.0f, 0.02f);
+        if (d->q4) {
+            // values: the bits of N(0, 1) f32 draws; scale ~ 0.02 / 4.6 (the spread
+            // of a 4-bit value), bias ~ -7.5 scale: weights of order N(0, 0.02)
+            for (QMat *m : {&d->qemb, &d->qqkv, &d->qo, &d->qg, &d->qu, &d->qd}) {
+                fill(m->packed, DataType::f32, 0.0f, 1.0f);
+                fill(m->scales, DataType::bf16, 0.0043f, 0.0005f);
+                fill(m->biases, DataType::bf16, -0.032f, 0.003f);
+            }
+        } else {
+            fill(d->embedding, DataType::bf16, 0.0f, 0.02f);
+            fill(d->wqkv, DataType::bf16, 0.0f, 0.02f);
+            fill(d->wo, DataType::bf16, 0.0f, 0.02f);
+            fill(d->wg, DataType::bf16, 0.0f, 0.02f);
+            fill(d->wu, DataType::bf16, 0.0f, 0.02f);
+            fill(d->wd, DataType::bf16, 0.0f, 0.02f);
+        }
         fill(d->norms, DataType::f32, 1.0f, 0.1f);
         if (d->headNorms.p) fill(d->headNorms, DataType::f32, 1.0f, 0.1f);
         fill(d->kcache, DataType::bf16, 0.0f, 1.0f);
@@ -366,7 +462,8 @@ popcorn_status_t popcorn_decoder_tensor(popcorn_decoder_t d, const char *name, i
         if (!d || !name || !out) throw Error::invalidArgument("decoder, name and tensor must not be NULL");
         Tensor t;
         std::string n = name;
-        if (n == "embedding") t = d->bf(d->embedding.p, {d->V, d->H});
+        if (d->quantizedView(n, 0, t) && n.rfind("embedding", 0) == 0) {
+        } else if (n == "embedding") t = d->bf(d->embedding.p, {d->V, d->H});
         else if (n == "final_norm") t = Tensor(d->finalNorm.p, Shape({d->H}), DataType::f32);
         else if (n == "x") t = d->bf(d->x.p, {d->H});
         else if (n == "q") t = d->bf(d->qkv.p, {d->QW});

@@ -468,7 +468,8 @@ Q4Shape q4Shape(int64_t K, bool xF32) {
     Q4Shape q;
     const int64_t G = K / 64;
     const int64_t kMax = xF32 ? 4096 : 16384;
-    if (G <= 0 || K > kMax) return q;
+    // the fast kernels read a row's scales and biases as 32-bit words
+    if (G <= 0 || G % 2 != 0 || K > kMax) return q;
     q.j = K <= 4096 ? 2 : 8;
     double best = -1.0;
     for (int lpr : {32, 16, 8}) {
@@ -692,7 +693,9 @@ public:
             q->validate();
             if (q->bits != 4 || q->groupSize != 64 || q->scales.dataType != DataType::bf16 || q->shape.rank() != 2)
                 throw Error::unsupportedDataTypeCombination("GatedMLP quantized weights are 2-D, 4-bit, group 64, bf16-scaled.");
-            if (!aligned16(q->packedValues.data)) throw Error::invalidArgument("GatedMLP packed values must be 16-byte aligned");
+            if (!aligned16(q->packedValues.data) || (reinterpret_cast<uintptr_t>(q->scales.data) & 3) ||
+                (q->hasBiases && (reinterpret_cast<uintptr_t>(q->biases.data) & 3)))
+                throw Error::invalidArgument("GatedMLP packed values must be 16-byte aligned, scales and biases 4-byte aligned");
         }
         F_ = wg.outFeatures();
         H_ = wg.inFeatures();
@@ -702,8 +705,8 @@ public:
         if (wg.hasBiases != wu.hasBiases) throw Error::invalidArgument("GatedMLP gate and up weights both have biases or neither");
         if (x.dataType != DataType::bf16 || out.dataType != DataType::bf16 || nw.dataType != DataType::f32)
             throw Error::unsupportedDataTypeCombination("GatedMLP with quantized weights takes bf16 x and out, an f32 norm weight.");
-        if (H_ % 64 != 0 || F_ % 64 != 0 || H_ > 8192 || F_ > 16384)
-            throw Error::tensorShapeMismatch("GatedMLP quantized: H, F multiples of 64, H <= 8192, F <= 16384.");
+        if (H_ % 128 != 0 || F_ % 128 != 0 || H_ > 8192 || F_ > 16384)
+            throw Error::tensorShapeMismatch("GatedMLP quantized: H, F multiples of 128, H <= 8192, F <= 16384.");
         if (x.shape.elementCount() != H_ || out.shape.elementCount() != H_)
             throw Error::tensorShapeMismatch("GatedMLP decodes one row: x and out hold [" + std::to_string(H_) + "].");
         requireElements(x, H_, "x");
@@ -757,7 +760,9 @@ public:
     }
 
     std::string describe() const override {
-        Tensor h(x_.data, Shape({1, F_}), DataType::bf16), o(out_.data, Shape({1, H_}), DataType::bf16);
+        // the down matvec reads the hidden tensor, or a 256-byte aligned scratch buffer
+        void *hp = hasHidden_ ? h_.data : reinterpret_cast<void *>(uintptr_t{256});
+        Tensor h(hp, Shape({1, F_}), DataType::bf16), o(out_.data, Shape({1, H_}), DataType::bf16);
         return gateUpName() + "," + Kernels::Matmul(h, wd_, o)->describe();
     }
 
@@ -1212,12 +1217,14 @@ std::unique_ptr<Kernel> DecodeMatvec(const DecodeMatvecArgs &a) {
         if (t != DataType::bf16 || Q.bits != 4 || Q.groupSize != 64 || Q.scales.dataType != DataType::bf16)
             throw Error::unsupportedDataTypeCombination("DecodeMatvec with a quantized weight takes bf16 x and a 4-bit, group-64, "
                                                         "bf16-scaled weight.");
-        if (K <= 0 || N <= 0 || K % 64 != 0 || K > 8192)
-            throw Error::tensorShapeMismatch("DecodeMatvec with a quantized weight needs K a multiple of 64, 0 < K <= 8192.");
+        if (K <= 0 || N <= 0 || K % 128 != 0 || K > 8192)
+            throw Error::tensorShapeMismatch("DecodeMatvec with a quantized weight needs K a multiple of 128, 0 < K <= 8192.");
         requireElements(Q.packedValues, N * (K / 8), "DecodeMatvec packed values");
         requireElements(Q.scales, N * (K / 64), "DecodeMatvec scales");
         if (Q.hasBiases) requireElements(Q.biases, N * (K / 64), "DecodeMatvec biases");
-        if (!aligned16(Q.packedValues.data)) throw Error::invalidArgument("DecodeMatvec packed values must be 16-byte aligned");
+        if (!aligned16(Q.packedValues.data) || (reinterpret_cast<uintptr_t>(Q.scales.data) & 3) ||
+            (Q.hasBiases && (reinterpret_cast<uintptr_t>(Q.biases.data) & 3)))
+            throw Error::invalidArgument("DecodeMatvec packed values must be 16-byte aligned, scales and biases 4-byte aligned");
     } else {
         const Tensor &W = *a.weight;
         if (W.shape.rank() != 2) throw Error::tensorInvalidRank(2, W.shape.rank());
@@ -1374,7 +1381,7 @@ std::unique_ptr<Kernel> Matmul(const Tensor &a, const AffineQuantizedTensor &b, 
     const std::string combo3 = std::string(tag(x)) + "_bf16_" + tag(o) + "_b4_g64";
     const Q4Shape q = q4Shape(k, x == D::f32);
     const bool aligned = aligned16(b.packedValues.data) && aligned16(a.data) &&
-                         (reinterpret_cast<uintptr_t>(b.scales.data) & 1) == 0 && (reinterpret_cast<uintptr_t>(bias.data) & 1) == 0;
+                         (reinterpret_cast<uintptr_t>(b.scales.data) & 3) == 0 && (reinterpret_cast<uintptr_t>(bias.data) & 3) == 0;
     DispatchSize ds;
     ds.block = dim3(kBlock, 1, 1);
     std::string fn;

@@ -28,6 +28,7 @@ class DecoderConfig:
     graph_steps: int = 1
     attention_block: int = 0      # 1: per-head q/k/v RMSNorm and RoPE (a real attention block)
     rope_theta: float = 10000.0
+    weight_bits: int = 16         # 4: block-affine 4-bit weights (group 64, bf16 scales and biases)
 
     def c(self) -> _capi.DecoderConfig:
         return _capi.DecoderConfig(*[getattr(self, f.name) for f in fields(self)])

@@ -16,20 +16,33 @@ def env():
     return gpu_env()
 
 
-def _small(pa_dec, graph_steps=1, attention_block=0):
+def _small(pa_dec, graph_steps=1, attention_block=0, weight_bits=16):
     return pa_dec.DecoderConfig(layers=2, hidden=256, query_heads=4, kv_heads=2, head_dim=64, ffn=512, vocab=1000,
                                 max_seq=64, eps=1e-6, attn_scale=0.125, history_len=64, graph_steps=graph_steps,
-                                attention_block=attention_block)
+                                attention_block=attention_block, weight_bits=weight_bits)
+
+
+def _weight(dec, name, layer, stream):
+    """A decoder weight as f32 values: bf16 as stored, or a 4-bit matrix
+    dequantized (q * scale + bias in f32, AffineQuantizedTensor.swift:5-8)."""
+    t = dec.tensor(name, layer)
+    if t.dtype != "u32":
+        return download(t, stream)
+    from q4util import dequantize_q4, unpack_q4
+    packed = t.numpy(stream)
+    s = download(dec.tensor(name + ".scales", layer), stream)
+    b = download(dec.tensor(name + ".biases", layer), stream)
+    return dequantize_q4(unpack_q4(packed, packed.shape[1] * 8), s, b)
 
 
 def _oracle_step(dec, cfg, caches, token, pos, stream, act=O.BF16):
     """One decode step of the oracle on the decoder's own weights, with every
     stored activation rounded to `act`; caches (f32 copies per layer) are
     updated in place. Returns logits."""
-    emb = download(dec.tensor("embedding"), stream)
+    emb = _weight(dec, "embedding", 0, stream)
     x = O.round_to(O.scalar_mul(emb[token], np.float32(np.sqrt(np.float32(cfg.hidden)))), act)
     for l in range(cfg.layers):
-        W = {n: download(dec.tensor(t, l), stream) for n, t in
+        W = {n: _weight(dec, t, l, stream) for n, t in
              [("in_norm", "norm_in"), ("qkv", "w_qkv"), ("o", "w_o"), ("post_attn_norm", "norm_post_attn"),
               ("pre_ffn_norm", "norm_pre_ffn"), ("gate", "w_gate"), ("up", "w_up"), ("down", "w_down"),
               ("post_ffn_norm", "norm_post_ffn")]}
@@ -45,8 +58,8 @@ def _oracle_step(dec, cfg, caches, token, pos, stream, act=O.BF16):
     return O.matmul(n, emb, 1, cfg.hidden, cfg.vocab, True).ravel()
 
 
-@pytest.mark.parametrize("attention_block", [0, 1])
-def test_small_decoder_matches_oracle(env, attention_block):
+@pytest.mark.parametrize("attention_block,weight_bits", [(0, 16), (1, 16), (0, 4), (1, 4)])
+def test_small_decoder_matches_oracle(env, attention_block, weight_bits):
     # The decode step is a composition of ~10 bf16-stored stages per layer;
     # each stage is pinned to 2e-3 by the kernel tests. Composed, a GPU sum
     # that lands on the other side of a bf16 rounding midpoint than the
@@ -58,7 +71,7 @@ def test_small_decoder_matches_oracle(env, attention_block):
     pa, lib, stream, enc = env
     import popcorn_amd.decoder as D
 
-    cfg = _small(D, attention_block=attention_block)
+    cfg = _small(D, attention_block=attention_block, weight_bits=weight_bits)
     dec = D.Decoder(lib, stream, cfg)
     dec.randomize(seed=1)
     if attention_block:  # inv_freq of theta 10000 (Gemma4Workspace.swift:195-197)
@@ -97,12 +110,13 @@ def test_small_decoder_matches_oracle(env, attention_block):
     dec.close()
 
 
-@pytest.mark.parametrize("graph_steps,steps,attention_block", [(1, 5, 0), (3, 7, 0), (3, 7, 1)])
-def test_graph_replay_equals_eager(env, graph_steps, steps, attention_block):
+@pytest.mark.parametrize("graph_steps,steps,attention_block,weight_bits", [(1, 5, 0, 16), (3, 7, 0, 16), (3, 7, 1, 16),
+                                                                         (3, 7, 1, 4)])
+def test_graph_replay_equals_eager(env, graph_steps, steps, attention_block, weight_bits):
     pa, lib, stream, enc = env
     import popcorn_amd.decoder as D
 
-    cfg = _small(D, graph_steps, attention_block)
+    cfg = _small(D, graph_steps, attention_block, weight_bits)
     dec = D.Decoder(lib, stream, cfg)
     dec.randomize(seed=2)
     k0 = [dec.tensor("k_cache", l).numpy(stream) for l in range(cfg.layers)]
@@ -130,19 +144,21 @@ def test_graph_replay_equals_eager(env, graph_steps, steps, attention_block):
     dec.close()
 
 
-@pytest.mark.parametrize("attention_block", [0, 1])
-def test_gemma2_2b_shape_decodes(env, attention_block):
+@pytest.mark.parametrize("attention_block,weight_bits", [(0, 16), (1, 16), (0, 4)])
+def test_gemma2_2b_shape_decodes(env, attention_block, weight_bits):
     # BASELINE config 4 shape at full size: 26 layers, H 2304, 8/4 heads of
     # 256, FFN 9216, vocab 256000, context 4096 -> 4352; random weights;
-    # attention_block adds the per-head norms and RoPE of a real block
+    # attention_block adds the per-head norms and RoPE of a real block,
+    # weight_bits 4 the block-affine 4-bit weights
     pa, lib, stream, enc = env
     import popcorn_amd.decoder as D
 
-    cfg = D.DecoderConfig(graph_steps=4, attention_block=attention_block)
+    cfg = D.DecoderConfig(graph_steps=4, attention_block=attention_block, weight_bits=weight_bits)
     dec = D.Decoder(lib, stream, cfg)
     dec.randomize(seed=0)
     names, n = dec.describe()
-    assert n == len(names) and "gated_mlp_gate_up_bf16_r1_res" in names
+    assert n == len(names)
+    assert ("q4_gate_up_bf16_l8_res" if weight_bits == 4 else "gated_mlp_gate_up_bf16_r1_res") in names
     assert any(m.startswith("flash_decoding_fresh_") for m in names) == bool(attention_block)
     dec.reset(123, 4096)
     dec.step(8, use_graph=True)
@@ -157,5 +173,5 @@ def test_gemma2_2b_shape_decodes(env, attention_block):
     dec.step(8, use_graph=False)
     np.testing.assert_array_equal(dec.history(4096, 8), hist)
     np.testing.assert_array_equal(dec.tensor("logits").numpy(stream), logits)
-    assert dec.step_bytes(4096) > 5.0e9
+    assert dec.step_bytes(4096) > (5.0e9 if weight_bits == 16 else 1.4e9)
     dec.close()
