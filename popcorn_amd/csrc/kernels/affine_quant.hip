@@ -62,7 +62,7 @@ __device__ void aq_matvec(const uint32_t *__restrict__ W, const uint16_t *__rest
                           const AffineQMatmulConstants &p) {
     constexpr bool XF32 = sizeof(typename X::storage) == 4;
     constexpr int kRows = 64 / LPR;
-    __shared__ uint32_t xw[XF32 ? 1 : maxK<J>() / 2];
+    __shared__ uint32_t xw[XF32 ? 1 : maxK<J>() / kQ4Group * pk::kQ4GroupStride];
     __shared__ float xf[XF32 ? maxK<J>() : 1];
     __shared__ float gsum[maxK<J>() / kQ4Group];
 
@@ -148,7 +148,7 @@ __device__ void aq_matvec_any(const uint32_t *__restrict__ W, const uint16_t *__
 // ---- decode forms with the layer glue (bf16 activations) ---------------------
 // The decoder layer's glue is built by Stage (stream.hpp) into xs (f32, LDS),
 // then turned into the 4-bit staging (pair words + group sums) behind it:
-// dynamic LDS = K floats + K / 2 words + K / 64 floats. Every stored
+// dynamic LDS = K floats + K / 64 groups x 36 words + K / 64 floats. Every stored
 // intermediate is rounded to bf16 (interDataType must be bf16, which is what
 // makes the xs values exact bf16 pairs).
 
@@ -157,7 +157,8 @@ struct Q4Lds {
     float *xs;
     uint32_t *xw;
     float *gsum;
-    __device__ Q4Lds(float *lds, uint32_t K) : xs(lds), xw(reinterpret_cast<uint32_t *>(lds + K)), gsum(lds + K + K / 2) {}
+    __device__ Q4Lds(float *lds, uint32_t K)
+        : xs(lds), xw(reinterpret_cast<uint32_t *>(lds + K)), gsum(lds + K + K / kQ4Group * pk::kQ4GroupStride) {}
     __device__ void stage_from_xs(uint32_t K) const {
         const float *x = xs;
         Q4Staging<false>::build(K, xw, nullptr, gsum, [&](uint32_t, uint32_t o, float *v) {

@@ -26,6 +26,11 @@ namespace pk {
 constexpr uint32_t kQ4Group = 64;          // values per scale/bias group
 constexpr uint32_t kQ4GroupWords = 8;      // packed u32 words per group
 constexpr uint32_t kQ4PairBase = 0x43004300u;  // bf16 pair (128, 128)
+// LDS words per group of staged x: 32 pair words + 4 of padding, so that the
+// 16-byte reads of 8 consecutive groups (8 lanes of one row, or one lane of
+// 8 rows... any 8 lanes served together) start in 8 different 4-bank slots
+// instead of all in the same one (a stride of 32 words is 32 banks).
+constexpr uint32_t kQ4GroupStride = 36;
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
@@ -38,7 +43,8 @@ __device__ inline float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
 __device__ inline float bf16_half(uint32_t v, uint32_t g) { return __uint_as_float((g & 1u) ? (v & 0xffff0000u) : (v << 16)); }
 
 // Staged activations of one row of x for the 4-bit stream, in LDS.
-//   bf16 x (XF32 = false): xw[K / 2] pair words (see above), gsum[K / 64];
+//   bf16 x (XF32 = false): xw[K / 64 * kQ4GroupStride] pair words (see
+//                          above), gsum[K / 64];
 //   f32 x  (XF32 = true):  xf[K] floats, gsum[K / 64].
 // One thread per octet of 8 values: the octet sums meet in groups of 8 lanes.
 template <bool XF32>
@@ -54,7 +60,7 @@ struct Q4Staging {
             w.y = (__float_as_uint(v[1]) >> 16) | (__float_as_uint(v[5]) & 0xffff0000u);
             w.z = (__float_as_uint(v[2]) >> 16) | (__float_as_uint(v[6]) & 0xffff0000u);
             w.w = (__float_as_uint(v[3]) >> 16) | (__float_as_uint(v[7]) & 0xffff0000u);
-            *reinterpret_cast<u32x4 *>(xw + 4 * o) = w;
+            *reinterpret_cast<u32x4 *>(xw + (o / 8) * kQ4GroupStride + 4 * (o % 8)) = w;
         }
     }
 
@@ -111,9 +117,14 @@ struct Q4Stream {
     Q4Row ip[NS];
     uint32_t G, cpl, steps, first, stride, is, ii, iu, gl;
     bool hasBias;
+    // The nibble-pair mask and the bf16 (128, 128) base, held in registers so
+    // that each pair is one v_and_or_b32 (which cannot take two literals).
+    uint32_t pairMask, pairBase;
 
     template <class Rows>
     __device__ void init(const Rows &rows, uint32_t K, uint32_t units, uint32_t first_, uint32_t stride_, bool hasBias_) {
+        asm volatile("v_mov_b32 %0, 0x000f000f" : "=v"(pairMask));
+        asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(pairBase));
         G = K / kQ4Group;
         gl = (threadIdx.x & 63) % LPR;
         cpl = (G + LPR - 1) / LPR;
@@ -175,17 +186,17 @@ struct Q4Stream {
             if constexpr (!XF32) {
                 u32x4 xv[8];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) xv[j] = *reinterpret_cast<const u32x4 *>(xw + (uint64_t)g * 32 + 4 * j);
+                for (int j = 0; j < 8; ++j) xv[j] = *reinterpret_cast<const u32x4 *>(xw + g * kQ4GroupStride + 4 * j);
 #pragma unroll
                 for (int s = 0; s < NS; ++s) {
                     float d0 = 0.0f, d1 = 0.0f, d2 = 0.0f, d3 = 0.0f;
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
                         const uint32_t w = word(wv[slot][s], j);
-                        d0 = dot2_bf16((w & 0x000F000Fu) | kQ4PairBase, xv[j].x, d0);
-                        d1 = dot2_bf16(((w >> 4) & 0x000F000Fu) | kQ4PairBase, xv[j].y, d1);
-                        d2 = dot2_bf16(((w >> 8) & 0x000F000Fu) | kQ4PairBase, xv[j].z, d2);
-                        d3 = dot2_bf16(((w >> 12) & 0x000F000Fu) | kQ4PairBase, xv[j].w, d3);
+                        d0 = dot2_bf16((w & pairMask) | pairBase, xv[j].x, d0);
+                        d1 = dot2_bf16(((w >> 4) & pairMask) | pairBase, xv[j].y, d1);
+                        d2 = dot2_bf16(((w >> 8) & pairMask) | pairBase, xv[j].z, d2);
+                        d3 = dot2_bf16(((w >> 12) & pairMask) | pairBase, xv[j].w, d3);
                     }
                     const float dot = (d0 + d1) + (d2 + d3);
                     const float sc = bf16_half(sv[slot][s], g);

@@ -772,7 +772,7 @@ public:
             AffineQMatmulConstants qc{1u, (uint32_t)F_, (uint32_t)H_, (uint32_t)(H_ / 64), (uint32_t)(H_ / 8),
                                       wg_.hasBiases ? 1u : 0u};
             const Tensor d = residual_ ? delta_ : x_, w = residual_ ? wPost_ : x_, xo = residual_ ? xOut_ : x_;
-            const size_t lds = (size_t)H_ * 4 + (size_t)H_ * 2 + (size_t)(H_ / 64) * 4;
+            const size_t lds = (size_t)H_ * 4 + (size_t)(H_ / 64) * 36 * 4 + (size_t)(H_ / 64) * 4;
             FixedDispatch gu(gateUpName(),
                              {{x_, kRead}, {nw_, kRead}, {wg_.packedValues, kRead}, {wg_.scales, kRead},
                               {wg_.hasBiases ? wg_.biases : wg_.scales, kRead}, {wu_.packedValues, kRead}, {wu_.scales, kRead},
@@ -1300,8 +1300,8 @@ std::unique_ptr<Kernel> DecodeMatvec(const DecodeMatvecArgs &a) {
             {a.vCache ? *a.vCache : *a.out, kWrite},
             {a.position ? *a.position : x, kRead},
         };
-        // LDS: x as f32, its bf16 pair words, the group sums
-        const size_t lds = (size_t)K * 4 + (size_t)K * 2 + (size_t)(K / 64) * 4;
+        // LDS: x as f32, its bf16 pair words (36 words per group of 64), the group sums
+        const size_t lds = (size_t)K * 4 + (size_t)(K / 64) * 36 * 4 + (size_t)(K / 64) * 4;
         return std::make_unique<FixedDispatch>(fn, std::move(b), std::vector<std::vector<uint8_t>>{bytesOf(dc), bytesOf(qc)},
                                                grid1(streamBlocks(cdiv(N, 64 / lpr)), kBlock, lds));
     }
