@@ -457,29 +457,33 @@ int64_t streamBlocks(int64_t units) {
     return cdiv(cdiv(units, per), kBlock / 64);
 }
 
-// The 4-bit fast kernels' launch shape: lanes per row LPR (a row's K / 64
-// groups are dealt to LPR lanes; the largest LPR that keeps at least 90% of
-// the lanes busy, else the busiest) and x octets per thread J (2 or 8).
+// The 4-bit fast kernels' launch shape: lanes per row LPR (8, 16 or 32; a
+// unit is 64 / LPR rows and a row's K / 64 groups are dealt to its LPR
+// lanes, one group per lane and step) and x octets per thread J (2 or 8).
+// LPR minimises the steps of the busiest wave, units per wave x steps per
+// unit, at the grid's waves per CU: short matrices want many small units,
+// long ones full lanes. Ties go to the higher lane occupancy.
 struct Q4Shape {
     int lpr = 0, j = 0;
 };
 
-Q4Shape q4Shape(int64_t K, bool xF32) {
+Q4Shape q4Shape(int64_t N, int64_t K, bool xF32) {
     Q4Shape q;
     const int64_t G = K / 64;
     const int64_t kMax = xF32 ? 4096 : 16384;
     // the fast kernels read a row's scales and biases as 32-bit words
-    if (G <= 0 || G % 2 != 0 || K > kMax) return q;
+    if (N <= 0 || G <= 0 || G % 2 != 0 || K > kMax) return q;
     q.j = K <= 4096 ? 2 : 8;
-    double best = -1.0;
+    const int64_t waves = (int64_t)deviceCUs() * streamWavesPerCU();
+    int64_t bestSteps = INT64_MAX;
+    double bestEff = 0.0;
     for (int lpr : {32, 16, 8}) {
-        const double eff = (double)G / (double)(lpr * cdiv(G, lpr));
-        if (eff >= 0.9) {
-            q.lpr = lpr;
-            return q;
-        }
-        if (eff > best) {
-            best = eff;
+        const int64_t cpl = cdiv(G, lpr);
+        const int64_t steps = cdiv(cdiv(N, 64 / lpr), waves) * cpl;
+        const double eff = (double)G / (double)(lpr * cpl);
+        if (steps < bestSteps || (steps == bestSteps && eff > bestEff)) {
+            bestSteps = steps;
+            bestEff = eff;
             q.lpr = lpr;
         }
     }
@@ -723,7 +727,7 @@ public:
             h_ = *hidden;
             hasHidden_ = true;
         }
-        lpr_ = q4Shape(H_, false).lpr;
+        lpr_ = q4Shape(F_, H_, false).lpr;
     }
 
     void setResidual(const Tensor &delta, const Tensor &wPost, const Tensor &xOut) {
@@ -1282,7 +1286,7 @@ std::unique_ptr<Kernel> DecodeMatvec(const DecodeMatvecArgs &a) {
     const Tensor &x = *a.x;
     if (q4) {
         const AffineQuantizedTensor &Q = *a.qweight;
-        const int lpr = q4Shape(K, false).lpr;
+        const int lpr = q4Shape(N, K, false).lpr;
         const std::string fn = std::string("q4_decode_matvec_bf16_") + tag(o) + "_l" + std::to_string(lpr) + "_f" +
                                std::to_string(flags & 3u);
         AffineQMatmulConstants qc{1u, (uint32_t)N, (uint32_t)K, (uint32_t)(K / 64), (uint32_t)(K / 8), Q.hasBiases ? 1u : 0u};
@@ -1379,7 +1383,7 @@ std::unique_ptr<Kernel> Matmul(const Tensor &a, const AffineQuantizedTensor &b, 
     const Tensor &bias = b.hasBiases ? b.biases : b.scales;
     std::vector<Binding> binds = {{b.packedValues, kRead}, {b.scales, kRead}, {bias, kRead}, {a, kRead}, {c, kWrite}};
     const std::string combo3 = std::string(tag(x)) + "_bf16_" + tag(o) + "_b4_g64";
-    const Q4Shape q = q4Shape(k, x == D::f32);
+    const Q4Shape q = q4Shape(n, k, x == D::f32);
     const bool aligned = aligned16(b.packedValues.data) && aligned16(a.data) &&
                          (reinterpret_cast<uintptr_t>(b.scales.data) & 3) == 0 && (reinterpret_cast<uintptr_t>(bias.data) & 3) == 0;
     DispatchSize ds;
