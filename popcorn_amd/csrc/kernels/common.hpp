@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "popcorn_kernel_types.h"
 
 #define POPCORN_KERNEL extern "C" __global__
@@ -48,6 +50,24 @@ __device__ inline float round_through(uint32_t tag, float x) {
     if (tag == 10u) return BF16::load(BF16::store(x));
     if (tag == 9u) return F16::load(F16::store(x));
     return x;
+}
+
+// The same with the dtype fixed at compile time: straight-line code, for
+// bodies that branch on the tag once (with_round_tag) instead of per element.
+template <uint32_t TAG>
+__device__ inline float round_as(float x) {
+    if constexpr (TAG == 10u) return BF16::load(BF16::store(x));
+    else if constexpr (TAG == 9u) return F16::load(F16::store(x));
+    else return x;
+}
+
+// Calls f(std::integral_constant<uint32_t, TAG>) for the tag's rounding:
+// 10 (bf16), 9 (f16) or 0 (f32, no rounding).
+template <typename Fn>
+__device__ inline void with_round_tag(uint32_t tag, Fn &&f) {
+    if (tag == 10u) f(std::integral_constant<uint32_t, 10u>{});
+    else if (tag == 9u) f(std::integral_constant<uint32_t, 9u>{});
+    else f(std::integral_constant<uint32_t, 0u>{});
 }
 
 // ---- 16-byte vectors -------------------------------------------------------

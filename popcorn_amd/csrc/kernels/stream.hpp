@@ -124,7 +124,15 @@ struct Stage {
         }
     }
 
+    // One straight-line body per rounding dtype: this code runs once per
+    // launch from a cold instruction cache, and a branch on `inter` at every
+    // element made it several times longer (and slower) than the arithmetic.
     __device__ void finish(float *xs, float *red, S *x_out, uint32_t K, uint32_t preMode, float eps, uint32_t inter) {
+        with_round_tag(inter, [&](auto tag) { this->template finish_as<decltype(tag)::value>(xs, red, x_out, K, preMode, eps); });
+    }
+
+    template <uint32_t TAG>
+    __device__ void finish_as(float *xs, float *red, S *x_out, uint32_t K, uint32_t preMode, float eps) {
         const uint32_t runs = K / E, tid = threadIdx.x;
         float ss = 0.0f;
         if constexpr (RES) {
@@ -144,8 +152,8 @@ struct Stage {
                     float r[E];
 #pragma unroll
                     for (int e = 0; e < E; ++e) {
-                        const float t = round_through(inter, (dv[j].get(e) * s) * wpo[j][e / 4].get(e % 4));
-                        r[e] = round_through(inter, xv[j].get(e) + t);
+                        const float t = round_as<TAG>((dv[j].get(e) * s) * wpo[j][e / 4].get(e % 4));
+                        r[e] = round_as<TAG>(xv[j].get(e) + t);
                         ss += r[e] * r[e];
                     }
                     store_lds(xs + (uint64_t)q * E, r);
@@ -180,7 +188,7 @@ struct Stage {
                         float v = r[e] * s;
                         const float w = wpr[j][e / 4].get(e % 4);
                         v *= preMode == 2u ? 1.0f + w : w;
-                        r[e] = round_through(inter, v);
+                        r[e] = round_as<TAG>(v);
                     }
                     store_lds(xs + (uint64_t)q * E, r);
                 }
