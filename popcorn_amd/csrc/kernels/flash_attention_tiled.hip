@@ -71,6 +71,7 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
     const uint16_t *Vh = V + kvoff;
     const uint32_t myq = qt * BQ + wave * 32 + c32;
     const int posQ = (int)p.Sk - (int)p.Sq + (int)myq;
+    const int posQ0 = (int)p.Sk - (int)p.Sq + (int)(qt * BQ + wave * 32);  // the wave's first row
 
     u32x4 qf[KS];
     {
@@ -153,20 +154,35 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
         __syncthreads();
         if (it + 1 < nSteps) gload(k0 + BKV);
 
-        f32x16 st;
+        // Two accumulators over alternate k-steps, their K fragments read
+        // from LDS four at a time, so neither the MFMA chain nor the LDS
+        // reads wait on each other step by step.
+        f32x16 st, st2;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) st[i] = 0.0f;
+        for (int i = 0; i < 16; ++i) st[i] = st2[i] = 0.0f;
 #pragma unroll
-        for (int s = 0; s < KS; ++s) {
-            const u32x4 a = *reinterpret_cast<const u32x4 *>(&sK[c32 * LDK + s * 16 + h * 8]);
-            st = Mma<T>::run(a, qf[s], st);
+        for (int s0 = 0; s0 < KS; s0 += 4) {
+            u32x4 a[4];
+#pragma unroll
+            for (int s = 0; s < 4; ++s) a[s] = *reinterpret_cast<const u32x4 *>(&sK[c32 * LDK + (s0 + s) * 16 + h * 8]);
+#pragma unroll
+            for (int s = 0; s < 4; s += 2) {
+                st = Mma<T>::run(a[s], qf[s0 + s], st);
+                st2 = Mma<T>::run(a[s + 1], qf[s0 + s + 1], st2);
+            }
         }
+        // The whole step is visible to every row of the wave (keys in
+        // range, at or before the wave's first query, inside the window of
+        // its last): no per-key test.
+        const bool full = (int)k0 + BKV <= (int)p.Sk && (p.maskKind == 2u || (int)k0 + BKV - 1 <= posQ0) &&
+                          (p.maskKind != 1u || posQ0 + 31 - (int)k0 < (int)p.slidingWindow);
         float sv[16];
         float mt = -INFINITY;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int key = (int)k0 + (i >> 2) * 8 + (int)h * 4 + (i & 3);
-            sv[i] = fa_allowed(p, posQ, key) ? st[i] * p.scale : -INFINITY;
+            const float v = (st[i] + st2[i]) * p.scale;
+            sv[i] = full || fa_allowed(p, posQ, key) ? v : -INFINITY;
             mt = fmaxf(mt, sv[i]);
         }
         mt = fmaxf(mt, pk::swap32(mt));
@@ -204,18 +220,35 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
                 pf[ks][j] = pb[ks * 8 + 2 * j] | (pb[ks * 8 + 2 * j + 1] << 16);
                 pfr[ks][j] = pr[ks * 8 + 2 * j] | (pr[ks * 8 + 2 * j + 1] << 16);
             }
+        // The running max of most rows stops moving after the first steps:
+        // the rescale (a read-modify-write of every accumulator) runs only
+        // when some row of the wave needs it.
+        if (__ballot(alpha != 1.0f)) {
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[dt][i] *= alpha;
+        }
+        // Vt fragments of tile dt + 1 are read while tile dt multiplies.
+        auto vfrag = [&](int dt, int ks) {
+            const uint16_t *vrow = &sV[(dt * 32 + c32) * LDV];
+            const uint2 lo = *reinterpret_cast<const uint2 *>(vrow + ks * 16 + h * 4);
+            const uint2 hi = *reinterpret_cast<const uint2 *>(vrow + ks * 16 + 8 + h * 4);
+            return u32x4{lo.x, lo.y, hi.x, hi.y};
+        };
+        u32x4 va[2][2];
+        va[0][0] = vfrag(0, 0);
+        va[0][1] = vfrag(0, 1);
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) acc[dt][i] *= alpha;
-            const uint16_t *vrow = &sV[(dt * 32 + c32) * LDV];
+            if (dt + 1 < DT) {
+                va[(dt + 1) & 1][0] = vfrag(dt + 1, 0);
+                va[(dt + 1) & 1][1] = vfrag(dt + 1, 1);
+            }
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
-                const uint2 lo = *reinterpret_cast<const uint2 *>(vrow + ks * 16 + h * 4);
-                const uint2 hi = *reinterpret_cast<const uint2 *>(vrow + ks * 16 + 8 + h * 4);
-                const u32x4 a = {lo.x, lo.y, hi.x, hi.y};
-                acc[dt] = Mma<T>::run(a, pf[ks], acc[dt]);
-                if constexpr (kSplitP) acc[dt] = Mma<T>::run(a, pfr[ks], acc[dt]);
+                acc[dt] = Mma<T>::run(va[dt & 1][ks], pf[ks], acc[dt]);
+                if constexpr (kSplitP) acc[dt] = Mma<T>::run(va[dt & 1][ks], pfr[ks], acc[dt]);
             }
         }
     }
