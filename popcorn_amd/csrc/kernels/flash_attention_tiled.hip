@@ -35,6 +35,10 @@ using pk::u32x4;
 constexpr int kWaves = 4;
 constexpr int BQ = 32 * kWaves;  // query rows per block
 constexpr int BKV = 32;          // keys per step
+// How far (natural log) a score may pass a row's reference max before the
+// reference moves: softmax weights stay below e^8 ~ 2981 (f16 holds 65504).
+constexpr float kRescaleGap = 8.0f;
+constexpr float kLog2e = 1.4426950408889634f;
 
 __device__ inline bool fa_allowed(const MPPFlashAttentionConstants &p, int posQ, int key) {
     if (key < 0 || key >= (int)p.Sk) return false;
@@ -58,7 +62,8 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
     __shared__ __attribute__((aligned(16))) uint16_t sK[BKV * LDK];
     __shared__ __attribute__((aligned(16))) uint16_t sV[HD * LDV];
 
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, c32 = lane & 31;
+    const uint32_t lane = threadIdx.x & 63, h = lane >> 5, c32 = lane & 31;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t nQT = p.qTilesPerHead;
     const uint32_t qt = nQT - 1 - blockIdx.x % nQT;
     const uint32_t bh = blockIdx.x / nQT;  // b * Nq + hq
@@ -72,6 +77,8 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
     const uint32_t myq = qt * BQ + wave * 32 + c32;
     const int posQ = (int)p.Sk - (int)p.Sq + (int)myq;
     const int posQ0 = (int)p.Sk - (int)p.Sq + (int)(qt * BQ + wave * 32);  // the wave's first row
+    // scores, m and the rescale gap are kept in log2 units: exp(x) = 2^(x log2 e)
+    const float c2 = p.scale * kLog2e;
 
     u32x4 qf[KS];
     {
@@ -135,12 +142,16 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
             const uint32_t pr = threadIdx.x + i * 64 * kWaves;
             if (pr < (uint32_t)kVP) {
                 const uint32_t kq = pr % (BKV / 4), db = pr / (BKV / 4);
+                // word j of each key row holds dims 2j (low half) and 2j + 1
+                // (high half); v_perm_b32 pairs the halves of two keys
+                // (selector bytes 0-3: second operand, 4-7: first)
 #pragma unroll
-                for (int d = 0; d < 8; ++d) {
-                    const int sh = (d & 1) * 16;
-                    const uint32_t w0 = (vr[i][0][d >> 1] >> sh) & 0xffffu, w1 = (vr[i][1][d >> 1] >> sh) & 0xffffu;
-                    const uint32_t w2 = (vr[i][2][d >> 1] >> sh) & 0xffffu, w3 = (vr[i][3][d >> 1] >> sh) & 0xffffu;
-                    *reinterpret_cast<uint2 *>(&sV[(db * 8 + d) * LDV + 4 * kq]) = uint2{w0 | (w1 << 16), w2 | (w3 << 16)};
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t a = vr[i][0][j], b = vr[i][1][j], c = vr[i][2][j], e = vr[i][3][j];
+                    *reinterpret_cast<uint2 *>(&sV[(db * 8 + 2 * j) * LDV + 4 * kq]) =
+                        uint2{__builtin_amdgcn_perm(b, a, 0x05040100u), __builtin_amdgcn_perm(e, c, 0x05040100u)};
+                    *reinterpret_cast<uint2 *>(&sV[(db * 8 + 2 * j + 1) * LDV + 4 * kq]) =
+                        uint2{__builtin_amdgcn_perm(b, a, 0x07060302u), __builtin_amdgcn_perm(e, c, 0x07060302u)};
                 }
             }
         }
@@ -178,25 +189,56 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
                           (p.maskKind != 1u || posQ0 + 31 - (int)k0 < (int)p.slidingWindow);
         float sv[16];
         float mt = -INFINITY;
+        if (full) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int key = (int)k0 + (i >> 2) * 8 + (int)h * 4 + (i & 3);
-            const float v = (st[i] + st2[i]) * p.scale;
-            sv[i] = full || fa_allowed(p, posQ, key) ? v : -INFINITY;
-            mt = fmaxf(mt, sv[i]);
+            for (int i = 0; i < 16; ++i) {
+                sv[i] = (st[i] + st2[i]) * c2;
+                mt = fmaxf(mt, sv[i]);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int key = (int)k0 + (i >> 2) * 8 + (int)h * 4 + (i & 3);
+                sv[i] = fa_allowed(p, posQ, key) ? (st[i] + st2[i]) * c2 : -INFINITY;
+                mt = fmaxf(mt, sv[i]);
+            }
         }
         mt = fmaxf(mt, pk::swap32(mt));
-        const float mn = fmaxf(m, mt);
+        // Lazy rescaling: a row's reference max m moves only when a score
+        // passes it by more than kRescaleGap, so the weights exp(s - m) stay
+        // below e^kRescaleGap (inside f16's range) and the rescale of the
+        // accumulators, a read-modify-write of all of them, is skipped by
+        // every step in which no row of the wave moved.
+        const bool move = mt > m + kRescaleGap * kLog2e;  // also when m is still -inf and a key is visible
         float alpha = 1.0f, ps = 0.0f;
+        if (move) {
+            const float mn = fmaxf(m, mt);
+            alpha = __builtin_amdgcn_exp2f(m - mn);
+            m = mn;
+        }
+        if (__ballot(move)) {
+            // read-multiply-write in place: a plain `acc *= alpha` makes the
+            // compiler carry every accumulator through VGPRs around the loop
+            // (128 copies per step, taken or not); this way they stay in AGPRs
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    float x = acc[dt][i], t;
+                    asm volatile("v_accvgpr_read_b32 %1, %0\n\tv_mul_f32 %1, %1, %2\n\tv_accvgpr_write_b32 %0, %1"
+                                 : "+a"(x), "=&v"(t)
+                                 : "v"(alpha));
+                    acc[dt][i] = x;
+                }
+        }
         uint32_t pb[16], pr[16];
-        if (mn == -INFINITY) {
+        if (m == -INFINITY) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) pb[i] = pr[i] = 0u;
         } else {
-            alpha = pk::fast_exp(m - mn);
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                const float pv = pk::fast_exp(sv[i] - mn);
+                const float pv = __builtin_amdgcn_exp2f(sv[i] - m);
                 pb[i] = pk::bits16<T>(pv);
                 float w = pk::from_bits16<T>(pb[i]);
                 if constexpr (kSplitP) {
@@ -211,7 +253,6 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
         }
         ps += pk::swap32(ps);
         l = l * alpha + ps;
-        m = mn;
         u32x4 pf[2], pfr[2];
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
@@ -220,15 +261,6 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
                 pf[ks][j] = pb[ks * 8 + 2 * j] | (pb[ks * 8 + 2 * j + 1] << 16);
                 pfr[ks][j] = pr[ks * 8 + 2 * j] | (pr[ks * 8 + 2 * j + 1] << 16);
             }
-        // The running max of most rows stops moving after the first steps:
-        // the rescale (a read-modify-write of every accumulator) runs only
-        // when some row of the wave needs it.
-        if (__ballot(alpha != 1.0f)) {
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) acc[dt][i] *= alpha;
-        }
         // Vt fragments of tile dt + 1 are read while tile dt multiplies.
         auto vfrag = [&](int dt, int ks) {
             const uint16_t *vrow = &sV[(dt * 32 + c32) * LDV];
