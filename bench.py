@@ -52,6 +52,18 @@ def kernel_bytes(cfg, name, pos):
         return 2 * KW * (pos + 1) * 2 + 2 * QW * 2  # K and V rows + q
     if name.startswith("flash_decoding_fresh"):  # K and V rows, raw q/k/v, new K/V row, norm weights
         return 2 * KW * pos * 2 + QKV * 2 + 2 * KW * 2 + 2 * cfg.head_dim * 4
+    # 4-bit weights (group 64): 0.5 byte per weight + a bf16 scale and bias per group
+    q4 = lambda n, k: n * k // 2 + n * (k // 64) * 4
+    if name.startswith("q4_gate_up_bf16_l") and name.endswith("_res"):
+        return 2 * q4(F, H) + 3 * H * 2 + 2 * H * 4 + F * 2
+    if name.startswith("q4_decode_matvec_bf16_bf16_l") and name.endswith(("_f2", "_f3")):
+        return q4(QKV, H) + 3 * H * 2 + 2 * H * 4 + QKV * 2
+    if name.startswith("q4_decode_matvec_bf16_bf16_l") and name.endswith("_f0"):
+        return q4(H, QW) + QW * 2 + H * 2
+    if name.startswith("q4_decode_matvec_bf16_f32_l") and name.endswith("_f3"):
+        return q4(V, H) + 3 * H * 2 + 2 * H * 4 + V * 4
+    if name.startswith("aq_qmv_fast_bf16_bf16_bf16_b4_g64_l") and name.endswith("_j8"):  # down (K = F)
+        return q4(H, F) + F * 2 + H * 2
     return None
 
 
@@ -270,6 +282,62 @@ def prefill_config5(pa, lib, stream, enc, reps=8):
     return rows
 
 
+def library_reference():
+    """The config-5 shapes through the vendor libraries PyTorch calls on ROCm
+    (torch.matmul -> hipBLASLt, scaled_dot_product_attention's flash and
+    memory-efficient backends), as reference points for the hand-written
+    MFMA kernels: same f16 shapes, same FLOP counts. PyTorch carries its own
+    HIP runtime, which cannot share a process with this library's, so the
+    timing runs in a child process."""
+    import subprocess
+    r = subprocess.run([sys.executable, os.path.abspath(__file__), "--library-reference-child"],
+                       capture_output=True, text=True, timeout=900)
+    lines = r.stdout.strip().splitlines()
+    if r.returncode != 0 or not lines:
+        return {"error": (r.stderr.strip().splitlines() or ["no output"])[-1][:200]}
+    return json.loads(lines[-1])
+
+
+def library_reference_child(reps=20):
+    import torch
+    import torch.nn.functional as Fn
+
+    def timed(f):
+        for _ in range(3):
+            f()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            f()
+        e1.record()
+        e1.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / reps
+
+    S, H, F = 2048, 3072, 24576
+    out = {"library": f"torch {torch.__version__}"}
+    g = torch.Generator(device="cuda").manual_seed(0)
+    for name, n, k in (("qkv", 3 * H, H), ("gate", F, H), ("down", H, F)):
+        a = torch.randn(S, k, device="cuda", dtype=torch.float16, generator=g)
+        w = torch.randn(n, k, device="cuda", dtype=torch.float16, generator=g) * 0.02
+        us = timed(lambda: torch.matmul(a, w.t()))
+        out[name] = {"us": round(us, 1), "TFLOP_s": round(2.0 * S * n * k / (us * 1e-6) / 1e12, 1)}
+        del a, w
+    Hq, Hd = 16, 256
+    q, k, v = (torch.randn(1, Hq, S, Hd, device="cuda", dtype=torch.float16, generator=g) for _ in range(3))
+    flop = 4.0 * Hq * Hd * S * (S + 1) / 2
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    for name, be in (("attention_flash", SDPBackend.FLASH_ATTENTION),
+                     ("attention_efficient", SDPBackend.EFFICIENT_ATTENTION)):
+        try:
+            with sdpa_kernel(be):
+                us = timed(lambda: Fn.scaled_dot_product_attention(q, k, v, is_causal=True, scale=1 / 16))
+            out[name] = {"us": round(us, 1), "TFLOP_s": round(flop / (us * 1e-6) / 1e12, 1)}
+        except RuntimeError as ex:  # backend not built for this device
+            out[name] = {"error": str(ex)[:120]}
+    return out
+
+
 def time_decode(pa, dec, stream, token, steps, warmup, use_graph):
     """Warmup (captures the graph), then `steps` timed decode steps from the
     same start; seconds, the larger of the wall clock and the HIP events."""
@@ -328,6 +396,9 @@ def main():
     ap.add_argument("--kernel-reps", type=int, default=4)
     ap.add_argument("--no-fd-sweep", action="store_true", help="skip the config-2 FlashDecoding sweep")
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-5 prefill measurement")
+    ap.add_argument("--library-reference", action="store_true",
+                    help="also time the config-5 shapes through PyTorch's hipBLASLt GEMM and SDPA attention")
+    ap.add_argument("--library-reference-child", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--no-q4", action="store_true", help="skip the 4-bit matvec measurement")
     ap.add_argument("--no-attention-block", action="store_true",
                     help="skip the decode with per-head norms and RoPE (a real attention block)")
@@ -339,6 +410,9 @@ def main():
         print("bench.py measures one GPU: this build has no multi-GPU path (every GPU box here has one GPU); "
               "run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if args.library_reference_child:
+        print(json.dumps(library_reference_child()))
+        return
 
     import popcorn_amd as pa
     import popcorn_amd.decoder as D
@@ -389,6 +463,8 @@ def main():
     prefill = None
     if not args.no_prefill:
         prefill = prefill_config5(pa, lib, stream, pa.KernelCommandEncoder(lib, stream))
+        if args.library_reference:
+            prefill["library_reference"] = library_reference()
 
     cpu = None
     if not args.no_cpu_baseline:
