@@ -93,7 +93,10 @@ typedef struct {
 } FlashAttentionConstants;
 
 /* PopcornKernelTypes.h:133-144 (the reference's MPP tile constants; here the
- * MFMA prefill kernel's), plus kvStride as above. */
+ * MFMA prefill kernel's), plus kvStride as above and splitFrom: query tiles
+ * qt >= splitFrom run as two blocks over the two halves of their key steps,
+ * which write partial (O, m, l) for the split-merge kernel
+ * (splitFrom == qTilesPerHead: no split). */
 typedef struct {
     uint32_t B;
     uint32_t Nq;
@@ -106,6 +109,7 @@ typedef struct {
     int32_t slidingWindow;
     float scale;
     uint32_t kvStride;
+    uint32_t splitFrom;
 } MPPFlashAttentionConstants;
 
 /* PopcornKernelTypes.h:146-156, plus kvStride, Sq (query rows; 0 = 1) and

@@ -47,10 +47,62 @@ __device__ inline bool fa_allowed(const MPPFlashAttentionConstants &p, int posQ,
     return ok;
 }
 
+// Key steps of query tile qt: keys any query of the tile may see.
+__device__ inline void fa_key_range(const MPPFlashAttentionConstants &p, uint32_t qt, int &kLo, int &kHi) {
+    const int first = (int)p.Sk - (int)p.Sq + (int)(qt * BQ);
+    const int last = (int)p.Sk - (int)p.Sq + (int)min(qt * BQ + BQ - 1, p.Sq - 1);
+    kLo = 0;
+    kHi = (int)p.Sk;
+    if (p.maskKind != 2u) kHi = min(kHi, last + 1);
+    if (p.maskKind == 1u) kLo = max(0, first - p.slidingWindow + 1);
+}
+
+__device__ inline uint32_t fa_steps(const MPPFlashAttentionConstants &p, uint32_t qt) {
+    int kLo, kHi;
+    fa_key_range(p, qt, kLo, kHi);
+    return kHi > kLo ? (uint32_t)(kHi - kLo + BKV - 1) / BKV : 0u;
+}
+
+// Work item of a block. Per (batch, query head) there are qTilesPerHead
+// tiles, those from splitFrom on as two halves of their key steps; blocks
+// take the items heaviest first (the larger of the next split half and the
+// next whole tile), the (batch, head) index varying fastest, so the longest
+// items start first on every CU.
+struct FaItem {
+    uint32_t bh, qt, part;
+    bool split;
+};
+
+__device__ inline FaItem fa_item(const MPPFlashAttentionConstants &p) {
+    const uint32_t BH = p.B * p.Nq, nQT = p.qTilesPerHead, sf = p.splitFrom;
+    const uint32_t rank = blockIdx.x / BH, nItems = nQT + (nQT - sf);
+    FaItem it{blockIdx.x % BH, 0u, 0u, false};
+    int a = (int)nQT - 1, b = (int)sf - 1;  // next split tile, next whole tile
+    uint32_t halves = 2;
+    for (uint32_t r = 0; r < nItems; ++r) {
+        const bool takeSplit = a >= (int)sf && (b < 0 || (fa_steps(p, a) + 1) / 2 >= fa_steps(p, b));
+        if (r == rank) {
+            it.qt = (uint32_t)(takeSplit ? a : b);
+            it.part = takeSplit ? 2u - halves : 0u;
+            it.split = takeSplit;
+            break;
+        }
+        if (takeSplit) {
+            if (--halves == 0) {
+                --a;
+                halves = 2;
+            }
+        } else {
+            --b;
+        }
+    }
+    return it;
+}
+
 template <typename T, typename O, int HD>
 __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
                          const uint16_t *__restrict__ V, typename O::storage *__restrict__ out,
-                         const MPPFlashAttentionConstants &p) {
+                         float *__restrict__ pO, float *__restrict__ pML, const MPPFlashAttentionConstants &p) {
     constexpr int KS = HD / 16;  // k-steps of S^T = K . Q^T
     constexpr int DT = HD / 32;  // 32-row tiles of O^T
     constexpr int LDK = HD + 8;  // sK row (padded, elements)
@@ -64,9 +116,9 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
 
     const uint32_t lane = threadIdx.x & 63, h = lane >> 5, c32 = lane & 31;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t nQT = p.qTilesPerHead;
-    const uint32_t qt = nQT - 1 - blockIdx.x % nQT;
-    const uint32_t bh = blockIdx.x / nQT;  // b * Nq + hq
+    const FaItem item = fa_item(p);
+    const uint32_t qt = item.qt;
+    const uint32_t bh = item.bh;  // b * Nq + hq
     const uint32_t b = bh / p.Nq, hq = bh % p.Nq;
     const uint32_t hkv = hq / (p.Nq / p.Nkv);
     const uint32_t stride = p.kvStride ? p.kvStride : p.Sk;
@@ -93,13 +145,14 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
         for (int i = 0; i < 16; ++i) acc[dt][i] = 0.0f;
     float m = -INFINITY, l = 0.0f;
 
-    // keys any query of the block may see
-    const int first = (int)p.Sk - (int)p.Sq + (int)(qt * BQ);
-    const int last = (int)p.Sk - (int)p.Sq + (int)min(qt * BQ + BQ - 1, p.Sq - 1);
-    int kLo = 0, kHi = (int)p.Sk;
-    if (p.maskKind != 2u) kHi = min(kHi, last + 1);
-    if (p.maskKind == 1u) kLo = max(0, first - p.slidingWindow + 1);
+    // keys any query of the block may see; a split tile's halves take the
+    // first ceil(n / 2) and the remaining key steps
+    int kLo, kHi;
+    fa_key_range(p, qt, kLo, kHi);
     const uint32_t nSteps = kHi > kLo ? (uint32_t)(kHi - kLo + BKV - 1) / BKV : 0u;
+    const uint32_t half = (nSteps + 1) / 2;
+    const uint32_t itLo = item.split && item.part == 1u ? half : 0u;
+    const uint32_t itHi = item.split && item.part == 0u ? half : nSteps;
 
     // Staging of one step: K as 16-byte chunks (row-major), V as 4 keys x 8
     // dims per thread so its transpose is written as 8-byte runs of 4 keys.
@@ -107,8 +160,13 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
     constexpr int kKC = (kChunks + 64 * kWaves - 1) / (64 * kWaves);
     constexpr int kVP = (BKV / 4) * (HD / 8);  // (key quad, dim block) pairs
     constexpr int kVC = (kVP + 64 * kWaves - 1) / (64 * kWaves);
-    u32x4 kr[kKC], vr[kVC][4];
-    auto gload = [&](uint32_t k0) {
+    // Two register sets take alternate steps, so a step's loads go out two
+    // steps before its LDS copy (one step of compute did not cover their
+    // latency with every CU loading at once).
+    using KRegs = u32x4[kKC];
+    using VRegs = u32x4[kVC][4];
+    u32x4 krA[kKC], vrA[kVC][4], krB[kKC], vrB[kVC][4];
+    auto gload = [&](KRegs &kr, VRegs &vr, uint32_t k0) {
 #pragma unroll
         for (int i = 0; i < kKC; ++i) {
             const uint32_t c = threadIdx.x + i * 64 * kWaves;
@@ -128,7 +186,7 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
             }
         }
     };
-    auto lstore = [&]() {
+    auto lstore = [&](const KRegs &kr, const VRegs &vr) {
 #pragma unroll
         for (int i = 0; i < kKC; ++i) {
             const uint32_t c = threadIdx.x + i * 64 * kWaves;
@@ -157,31 +215,37 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
         }
     };
 
-    if (nSteps > 0) gload((uint32_t)kLo);
-    for (uint32_t it = 0; it < nSteps; ++it) {
-        const uint32_t k0 = (uint32_t)kLo + it * BKV;
-        __syncthreads();  // the previous step's readers are done
-        lstore();
-        __syncthreads();
-        if (it + 1 < nSteps) gload(k0 + BKV);
-
-        // Two accumulators over alternate k-steps, their K fragments read
-        // from LDS four at a time, so neither the MFMA chain nor the LDS
-        // reads wait on each other step by step.
+    auto compute = [&](uint32_t k0) {
+        // All K fragments of the step are read before the first product (the
+        // scheduler otherwise pairs each LDS read with its MFMA and waits on
+        // every one); two accumulators over alternate k-steps halve the
+        // chain of dependent products.
         f32x16 st, st2;
 #pragma unroll
         for (int i = 0; i < 16; ++i) st[i] = st2[i] = 0.0f;
+        u32x4 kf[KS];
 #pragma unroll
-        for (int s0 = 0; s0 < KS; s0 += 4) {
-            u32x4 a[4];
+        for (int s = 0; s < KS; ++s) kf[s] = *reinterpret_cast<const u32x4 *>(&sK[c32 * LDK + s * 16 + h * 8]);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int s = 0; s < 4; ++s) a[s] = *reinterpret_cast<const u32x4 *>(&sK[c32 * LDK + (s0 + s) * 16 + h * 8]);
+        for (int s = 0; s < KS; s += 2) {
+            st = Mma<T>::run(kf[s], qf[s], st);
+            st2 = Mma<T>::run(kf[s + 1], qf[s + 1], st2);
+        }
+        // Vt fragments of the whole step, read now so they land while the
+        // softmax below runs.
+        u32x4 va[DT][2];
 #pragma unroll
-            for (int s = 0; s < 4; s += 2) {
-                st = Mma<T>::run(a[s], qf[s0 + s], st);
-                st2 = Mma<T>::run(a[s + 1], qf[s0 + s + 1], st2);
+        for (int dt = 0; dt < DT; ++dt) {
+            const uint16_t *vrow = &sV[(dt * 32 + c32) * LDV];
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                const uint2 lo = *reinterpret_cast<const uint2 *>(vrow + ks * 16 + h * 4);
+                const uint2 hi = *reinterpret_cast<const uint2 *>(vrow + ks * 16 + 8 + h * 4);
+                va[dt][ks] = u32x4{lo.x, lo.y, hi.x, hi.y};
             }
         }
+        __builtin_amdgcn_sched_barrier(0);
         // The whole step is visible to every row of the wave (keys in
         // range, at or before the wave's first query, inside the window of
         // its last): no per-key test.
@@ -261,31 +325,52 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
                 pf[ks][j] = pb[ks * 8 + 2 * j] | (pb[ks * 8 + 2 * j + 1] << 16);
                 pfr[ks][j] = pr[ks * 8 + 2 * j] | (pr[ks * 8 + 2 * j + 1] << 16);
             }
-        // Vt fragments of tile dt + 1 are read while tile dt multiplies.
-        auto vfrag = [&](int dt, int ks) {
-            const uint16_t *vrow = &sV[(dt * 32 + c32) * LDV];
-            const uint2 lo = *reinterpret_cast<const uint2 *>(vrow + ks * 16 + h * 4);
-            const uint2 hi = *reinterpret_cast<const uint2 *>(vrow + ks * 16 + 8 + h * 4);
-            return u32x4{lo.x, lo.y, hi.x, hi.y};
-        };
-        u32x4 va[2][2];
-        va[0][0] = vfrag(0, 0);
-        va[0][1] = vfrag(0, 1);
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-            if (dt + 1 < DT) {
-                va[(dt + 1) & 1][0] = vfrag(dt + 1, 0);
-                va[(dt + 1) & 1][1] = vfrag(dt + 1, 1);
-            }
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
-                acc[dt] = Mma<T>::run(va[dt & 1][ks], pf[ks], acc[dt]);
-                if constexpr (kSplitP) acc[dt] = Mma<T>::run(va[dt & 1][ks], pfr[ks], acc[dt]);
+                acc[dt] = Mma<T>::run(va[dt][ks], pf[ks], acc[dt]);
+                if constexpr (kSplitP) acc[dt] = Mma<T>::run(va[dt][ks], pfr[ks], acc[dt]);
             }
+        }
+    };
+
+    if (itLo < itHi) gload(krA, vrA, (uint32_t)kLo + itLo * BKV);
+    if (itLo + 1 < itHi) gload(krB, vrB, (uint32_t)kLo + (itLo + 1) * BKV);
+    for (uint32_t it = itLo; it < itHi; it += 2) {
+        const uint32_t k0 = (uint32_t)kLo + it * BKV;
+        __syncthreads();  // the previous step's readers are done
+        lstore(krA, vrA);
+        __syncthreads();
+        if (it + 2 < itHi) gload(krA, vrA, k0 + 2 * BKV);
+        compute(k0);
+        if (it + 1 < itHi) {
+            __syncthreads();
+            lstore(krB, vrB);
+            __syncthreads();
+            if (it + 3 < itHi) gload(krB, vrB, k0 + 3 * BKV);
+            compute(k0 + BKV);
         }
     }
 
     if (myq >= p.Sq) return;
+    if (item.split) {
+        // unnormalised O (f32), and m (log2 units) and l, of this half
+        const uint32_t tile = (bh * (p.qTilesPerHead - p.splitFrom) + (qt - p.splitFrom)) * 2u + item.part;
+        const uint64_t row = (uint64_t)tile * BQ + wave * 32 + c32;
+        float *prow = pO + row * HD;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+            for (int i4 = 0; i4 < 4; ++i4) {
+                const uint32_t d = dt * 32 + i4 * 8 + h * 4;
+                *reinterpret_cast<float4 *>(prow + d) =
+                    float4{acc[dt][4 * i4], acc[dt][4 * i4 + 1], acc[dt][4 * i4 + 2], acc[dt][4 * i4 + 3]};
+            }
+        }
+        if (h == 0) *reinterpret_cast<float2 *>(pML + 2 * row) = float2{m, l};
+        return;
+    }
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
     typename O::storage *orow = out + ((uint64_t)bh * p.Sq + myq) * HD;
 #pragma unroll
@@ -298,18 +383,64 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
     }
 }
 
+// Combine of a split tile's two halves (maxima in log2 units):
+//   M = max(m0, m1), w_i = 2^(m_i - M) (0 for a half with no visible key),
+//   O = (w0 O0 + w1 O1) / (w0 l0 + w1 l1),
+// the log-sum-exp combine of FlashDecoding.metal:202-227 for two partitions.
+// One block per 16 rows of a split tile; a thread takes 4 dims of a row.
+constexpr int kMergeRows = 16;
+
+template <typename O, int HD>
+__device__ void fa_split_merge(const float *__restrict__ pO, const float *__restrict__ pML,
+                               typename O::storage *__restrict__ out, const MPPFlashAttentionConstants &p) {
+    const uint32_t nSplit = p.qTilesPerHead - p.splitFrom;
+    const uint32_t tile = blockIdx.x / (BQ / kMergeRows);  // bh * nSplit + (qt - splitFrom)
+    const uint32_t r0 = blockIdx.x % (BQ / kMergeRows) * kMergeRows;
+    const uint32_t bh = tile / nSplit, qt = p.splitFrom + tile % nSplit;
+    constexpr uint32_t kPerRow = HD / 4;
+    for (uint32_t idx = threadIdx.x; idx < (uint32_t)kMergeRows * kPerRow; idx += blockDim.x) {
+        const uint32_t r = r0 + idx / kPerRow, d = (idx % kPerRow) * 4;
+        const uint32_t q = qt * BQ + r;
+        if (q >= p.Sq) continue;
+        const uint64_t row0 = (uint64_t)tile * 2 * BQ + r, row1 = row0 + BQ;
+        const float2 ml0 = *reinterpret_cast<const float2 *>(pML + 2 * row0);
+        const float2 ml1 = *reinterpret_cast<const float2 *>(pML + 2 * row1);
+        const float M = fmaxf(ml0.x, ml1.x);
+        const float w0 = ml0.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml0.x - M);
+        const float w1 = ml1.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml1.x - M);
+        const float L = w0 * ml0.y + w1 * ml1.y;
+        const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+        const float4 a = *reinterpret_cast<const float4 *>(pO + row0 * HD + d);
+        const float4 c = *reinterpret_cast<const float4 *>(pO + row1 * HD + d);
+        typename O::storage *orow = out + ((uint64_t)bh * p.Sq + q) * HD + d;
+        orow[0] = O::store((w0 * a.x + w1 * c.x) * inv);
+        orow[1] = O::store((w0 * a.y + w1 * c.y) * inv);
+        orow[2] = O::store((w0 * a.z + w1 * c.z) * inv);
+        orow[3] = O::store((w0 * a.w + w1 * c.w) * inv);
+    }
+}
+
 }  // namespace
 
 #define FA_TILED(name, T, O, HD)                                                                       \
     POPCORN_KERNEL void __launch_bounds__(256)                                                         \
-        name(const uint16_t *q, const uint16_t *k, const uint16_t *v, O::storage *out,                 \
-             MPPFlashAttentionConstants p) {                                                           \
-        fa_tiled<T, O, HD>(q, k, v, out, p);                                                           \
+        name(const uint16_t *q, const uint16_t *k, const uint16_t *v, O::storage *out, float *pO,      \
+             float *pML, MPPFlashAttentionConstants p) {                                               \
+        fa_tiled<T, O, HD>(q, k, v, out, pO, pML, p);                                                  \
     }
 #define FA_TILED_D(t, T, o, O)                                   \
     FA_TILED(flash_attention_tiled_##t##_##o##_d64, T, O, 64)    \
     FA_TILED(flash_attention_tiled_##t##_##o##_d128, T, O, 128)  \
     FA_TILED(flash_attention_tiled_##t##_##o##_d256, T, O, 256)
+#define FA_MERGE(name, O, HD)                                                                          \
+    POPCORN_KERNEL void __launch_bounds__(256)                                                         \
+        name(const float *pO, const float *pML, O::storage *out, MPPFlashAttentionConstants p) {       \
+        fa_split_merge<O, HD>(pO, pML, out, p);                                                        \
+    }
+#define FA_MERGE_D(o, O)                                         \
+    FA_MERGE(flash_attention_split_merge_##o##_d64, O, 64)       \
+    FA_MERGE(flash_attention_split_merge_##o##_d128, O, 128)     \
+    FA_MERGE(flash_attention_split_merge_##o##_d256, O, 256)
 
 using pk::BF16;
 using pk::F16;
@@ -319,3 +450,6 @@ FA_TILED_D(f16, F16, f16, F16)
 FA_TILED_D(f16, F16, f32, F32)
 FA_TILED_D(bf16, BF16, bf16, BF16)
 FA_TILED_D(bf16, BF16, f32, F32)
+FA_MERGE_D(f16, F16)
+FA_MERGE_D(bf16, BF16)
+FA_MERGE_D(f32, F32)

@@ -171,9 +171,11 @@ public:
             (hasPos_ || !aligned16(q.data) || !aligned16(k.data) || !aligned16(v.data) ||
              !(out.dataType == q.dataType || out.dataType == DataType::f32)))
             path_ = Kernels::AttentionPath::plain;
-        if (path_ == Kernels::AttentionPath::tiled)
+        if (path_ == Kernels::AttentionPath::tiled) {
             tiledName_ = std::string("flash_attention_tiled_") + tag(q.dataType) + "_" + tag(out.dataType) + "_d" +
                          std::to_string(d.Hd);
+            planTileSplit();
+        }
         planSplit();
     }
 
@@ -184,7 +186,8 @@ public:
     }
 
     std::string describe() const override {
-        return path_ == Kernels::AttentionPath::tiled ? tiledName_ : partialName_ + "," + reduceName_;
+        if (path_ == Kernels::AttentionPath::tiled) return nSplit_ ? tiledName_ + "," + mergeName_ : tiledName_;
+        return partialName_ + "," + reduceName_;
     }
 
     void encode(KernelCommandEncoder &enc) const override {
@@ -203,9 +206,30 @@ public:
             c.slidingWindow = mask_.kind == 1 ? mask_.window : -1;
             c.scale = scale_;
             c.kvStride = (uint32_t)d_.cap;
-            FixedDispatch fa(tiledName_, {{q_, kRead}, {k_, kRead}, {v_, kRead}, {out_, kWrite}}, {bytesOf(c)},
-                             grid1(d_.B * d_.Nq * (int64_t)c.qTilesPerHead, kBlock));
-            enc.dispatch(fa);
+            c.splitFrom = (uint32_t)(c.qTilesPerHead - nSplit_);
+            const int64_t items = d_.B * d_.Nq * ((int64_t)c.qTilesPerHead + nSplit_);
+            if (!nSplit_) {
+                // no split tile: the partial-state arguments are never touched
+                FixedDispatch fa(tiledName_,
+                                 {{q_, kRead}, {k_, kRead}, {v_, kRead}, {out_, kWrite}, {q_, kRead}, {q_, kRead}},
+                                 {bytesOf(c)}, grid1(items, kBlock));
+                enc.dispatch(fa);
+                return;
+            }
+            // the halves of split tiles: unnormalised O, then (m, l) per row
+            const int64_t rows = d_.B * d_.Nq * nSplit_ * 2 * 128;
+            enc.withTemporaryTensor(ScratchSpec{{rows, d_.Hd}, DataType::f32}, [&](Tensor pO) {
+                enc.withTemporaryTensor(ScratchSpec{{rows, 2}, DataType::f32}, [&](Tensor pML) {
+                    FixedDispatch fa(tiledName_,
+                                     {{q_, kRead}, {k_, kRead}, {v_, kRead}, {out_, kWrite}, {pO, kWrite}, {pML, kWrite}},
+                                     {bytesOf(c)}, grid1(items, kBlock));
+                    enc.dispatch(fa);
+                    // one block per 16 rows of a split tile
+                    FixedDispatch merge(mergeName_, {{pO, kRead}, {pML, kRead}, {out_, kWrite}}, {bytesOf(c)},
+                                        grid1(d_.B * d_.Nq * nSplit_ * 8, kBlock));
+                    enc.dispatch(merge);
+                });
+            });
             return;
         }
         // FlashDecoding.swift:54-73: borrow partial O, m, l; partial; combine.
@@ -255,6 +279,27 @@ public:
     }
 
 private:
+    // Causal prefill with few tiles per CU: the last query tiles see up to
+    // twice the mean number of keys and, one tile per CU, set the kernel's
+    // time. Tiles with more than half the largest tile's key steps run as
+    // two blocks over the halves of their keys, merged by a second kernel.
+    void planTileSplit() {
+        nSplit_ = 0;
+        const int64_t nQT = cdiv(d_.Sq, 128);
+        if (mask_.kind != 0 || nQT < 4 || d_.B * d_.Nq * nQT > 2 * (int64_t)deviceCUs()) return;
+        auto steps = [&](int64_t qt) {
+            const int64_t last = d_.Sk - d_.Sq + std::min(qt * 128 + 127, d_.Sq - 1);
+            const int64_t hi = std::min(d_.Sk, last + 1);
+            return hi > 0 ? cdiv(hi, 32) : int64_t(0);
+        };
+        const int64_t most = steps(nQT - 1);
+        int64_t from = nQT;
+        while (from > 0 && steps(from - 1) * 2 > most) --from;
+        if (most < 4 || from == nQT) return;
+        nSplit_ = nQT - from;
+        mergeName_ = std::string("flash_attention_split_merge_") + tag(out_.dataType) + "_d" + std::to_string(d_.Hd);
+    }
+
     void planSplit() {
         const DataType t = q_.dataType;
         const bool alignedOk = aligned16(q_.data) && aligned16(k_.data) && aligned16(v_.data);
@@ -271,7 +316,8 @@ private:
     AttentionMask mask_;
     bool hasPos_;
     Kernels::AttentionPath path_ = Kernels::AttentionPath::plain;
-    std::string partialName_, reduceName_, tiledName_;
+    std::string partialName_, reduceName_, tiledName_, mergeName_;
+    int64_t nSplit_ = 0;
     int64_t ngroups_ = 1, P_ = 1;
 };
 

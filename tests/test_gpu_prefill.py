@@ -118,6 +118,27 @@ def test_tiled_attention_vs_oracle(env, dtype, ot, B, Nq, Nkv, Sq, Sk, Hd, mask)
     assert_out(got, ref, EPS[dtype], ot, f"tiled attention {dtype}->{ot} {mask} Sq={Sq} Sk={Sk} Hd={Hd}")
 
 
+@pytest.mark.parametrize("dtype,ot", [("f16", "f16"), ("bf16", "bf16"), ("bf16", "f32")])
+@pytest.mark.parametrize("B,Nq,Nkv,Sq,Sk,Hd", [
+    (1, 2, 1, 512, 512, 64),
+    (2, 2, 1, 520, 700, 128),   # Sq < Sk, ragged last tile: every tile split
+    (1, 2, 2, 640, 640, 256),
+])
+def test_tiled_attention_split_tiles_vs_oracle(env, dtype, ot, B, Nq, Nkv, Sq, Sk, Hd):
+    # causal prefill with few tiles per CU: the heavy query tiles run as two
+    # blocks over the halves of their keys and a merge kernel combines them
+    pa = env[0]
+    q = rounded(O.normal(Sq + Hd + 7, (B, Nq, Sq, Hd)), dtype)
+    k = rounded(O.normal(Sk + Hd + 8, (B, Nkv, Sk, Hd)), dtype)
+    v = rounded(O.normal(Sk + Hd + 9, (B, Nkv, Sk, Hd)), dtype)
+    scale = 1 / np.sqrt(Hd)
+    got, kern = _attend(env, q, k, v, dtype, ot, scale, pa.AttentionMask(0, -1))
+    assert kern.function_names == [f"flash_attention_tiled_{dtype}_{ot}_d{Hd}", f"flash_attention_split_merge_{ot}_d{Hd}"]
+    ref = O.attention_naive(q, k, v, scale, mask_kind=0)
+    assert not np.isnan(got).any()
+    assert_out(got, ref, EPS[dtype], ot, f"split tiled attention {dtype}->{ot} Sq={Sq} Sk={Sk} Hd={Hd}")
+
+
 def test_tiled_attention_config5_sampled(env):
     # BASELINE config 5 attention: [1, 16, 2048, 256] f16, causal, scale 1/16.
     # A sampled query row r is checked as a single-row query over keys 0..r
@@ -130,7 +151,8 @@ def test_tiled_attention_config5_sampled(env):
     to = pa.Tensor.empty([1, H, S, Hd], "f16")
     kern = pa.Kernels.FlashAttention(tq, tk, tv, out=to, scale=1 / 16, batch=1, query_heads=H, kv_heads=H,
                                      query_len=S, key_len=S, head_dim=Hd)
-    assert kern.function_names == ["flash_attention_tiled_f16_f16_d256"]
+    # 16 tiles per head on 256 CUs: the 8 heaviest run split in two halves of their keys
+    assert kern.function_names == ["flash_attention_tiled_f16_f16_d256", "flash_attention_split_merge_f16_d256"]
     enc.encode(kern)
     stream.synchronize()
     q, k, v = (download(t, stream).reshape(1, H, S, Hd) for t in (tq, tk, tv))
