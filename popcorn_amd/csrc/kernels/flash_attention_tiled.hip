@@ -170,7 +170,7 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
 #pragma unroll
         for (int i = 0; i < kKC; ++i) {
             const uint32_t c = threadIdx.x + i * 64 * kWaves;
-            if (c < (uint32_t)kChunks) {
+            if (kChunks % (64 * kWaves) == 0 || c < (uint32_t)kChunks) {
                 const uint32_t key = c / (HD / 8), dc = (c % (HD / 8)) * 8;
                 kr[i] = *reinterpret_cast<const u32x4 *>(Kh + (uint64_t)min(k0 + key, p.Sk - 1) * HD + dc);
             }
@@ -178,7 +178,7 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
 #pragma unroll
         for (int i = 0; i < kVC; ++i) {
             const uint32_t pr = threadIdx.x + i * 64 * kWaves;
-            if (pr < (uint32_t)kVP) {
+            if (kVP % (64 * kWaves) == 0 || pr < (uint32_t)kVP) {
                 const uint32_t kq = pr % (BKV / 4), db = pr / (BKV / 4);
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
@@ -190,7 +190,7 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
 #pragma unroll
         for (int i = 0; i < kKC; ++i) {
             const uint32_t c = threadIdx.x + i * 64 * kWaves;
-            if (c < (uint32_t)kChunks) {
+            if (kChunks % (64 * kWaves) == 0 || c < (uint32_t)kChunks) {
                 const uint32_t key = c / (HD / 8), dc = (c % (HD / 8)) * 8;
                 *reinterpret_cast<u32x4 *>(&sK[key * LDK + dc]) = kr[i];
             }
@@ -198,7 +198,7 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
 #pragma unroll
         for (int i = 0; i < kVC; ++i) {
             const uint32_t pr = threadIdx.x + i * 64 * kWaves;
-            if (pr < (uint32_t)kVP) {
+            if (kVP % (64 * kWaves) == 0 || pr < (uint32_t)kVP) {
                 const uint32_t kq = pr % (BKV / 4), db = pr / (BKV / 4);
                 // word j of each key row holds dims 2j (low half) and 2j + 1
                 // (high half); v_perm_b32 pairs the halves of two keys
@@ -335,21 +335,24 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
         }
     };
 
-    if (itLo < itHi) gload(krA, vrA, (uint32_t)kLo + itLo * BKV);
-    if (itLo + 1 < itHi) gload(krB, vrB, (uint32_t)kLo + (itLo + 1) * BKV);
-    for (uint32_t it = itLo; it < itHi; it += 2) {
-        const uint32_t k0 = (uint32_t)kLo + it * BKV;
-        __syncthreads();  // the previous step's readers are done
-        lstore(krA, vrA);
-        __syncthreads();
-        if (it + 2 < itHi) gload(krA, vrA, k0 + 2 * BKV);
-        compute(k0);
-        if (it + 1 < itHi) {
+    // Every pass issues both sets' loads (steps past the range re-read the
+    // last one): with loads on every path the compiler's wait for set A
+    // leaves set B in flight, which a conditional load would not.
+    if (itLo < itHi) {
+        auto kstep = [&](uint32_t it) { return (uint32_t)kLo + min(it, itHi - 1) * BKV; };
+        gload(krA, vrA, kstep(itLo));
+        gload(krB, vrB, kstep(itLo + 1));
+        for (uint32_t it = itLo; it < itHi; it += 2) {
+            __syncthreads();  // the previous step's readers are done
+            lstore(krA, vrA);
+            __syncthreads();
+            gload(krA, vrA, kstep(it + 2));
+            compute(kstep(it));
             __syncthreads();
             lstore(krB, vrB);
             __syncthreads();
-            if (it + 3 < itHi) gload(krB, vrB, k0 + 3 * BKV);
-            compute(k0 + BKV);
+            gload(krB, vrB, kstep(it + 3));
+            if (it + 1 < itHi) compute(kstep(it + 1));
         }
     }
 
