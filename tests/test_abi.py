@@ -65,6 +65,23 @@ def test_route():
     assert pa.Kernels.route(2, 256) == "plain"
 
 
+def test_prefill_attention_split_plan():
+    # causal prefill with at most two 128-row tiles per CU (256 CUs when no
+    # GPU answers): tiles with more than half the last tile's key steps run
+    # as two blocks, merged by a second kernel
+    def fa(Nq, S, mask=(0, -1), dtype="f16"):
+        q = T([1, Nq, S, 256], dtype)
+        return pa.Kernels.FlashAttention(q, q, q, out=T([1, Nq, S, 256], dtype), scale=1 / 16,
+                                         mask=pa.AttentionMask(*mask), batch=1, query_heads=Nq, kv_heads=Nq,
+                                         query_len=S, key_len=S, head_dim=256).function_names
+    assert fa(16, 2048) == ["flash_attention_tiled_f16_f16_d256", "flash_attention_split_merge_f16_d256"]
+    assert fa(16, 2048, dtype="bf16") == ["flash_attention_tiled_bf16_bf16_d256", "flash_attention_split_merge_bf16_d256"]
+    assert fa(16, 2048, mask=(2, -1)) == ["flash_attention_tiled_f16_f16_d256"]   # every tile sees every key
+    assert fa(16, 2048, mask=(1, 256)) == ["flash_attention_tiled_f16_f16_d256"]  # window: equal work per tile
+    assert fa(16, 384) == ["flash_attention_tiled_f16_f16_d256"]                  # 3 tiles per head
+    assert fa(64, 2048) == ["flash_attention_tiled_f16_f16_d256"]                 # 1024 tiles: 4 per CU
+
+
 def test_flash_attention_routing_names():
     q, o = T([1, 8, 1, 256]), T([1, 8, 1, 256])
     k = T([1, 4, 4352, 256])
@@ -299,4 +316,4 @@ def test_prefill_routes_to_tiled():
     assert pa.Kernels.route(1, 256, "f16") == "decoding"
     q = T([1, 16, 2048, 256], "f16")
     k = pa.Kernels.FlashAttention(q, q, q, out=T([1, 16, 2048, 256], "f16", ptr=FAKE + 2 ** 32), scale=1 / 16)
-    assert k.function_names == ["flash_attention_tiled_f16_f16_d256"]
+    assert k.function_names == ["flash_attention_tiled_f16_f16_d256", "flash_attention_split_merge_f16_d256"]
