@@ -376,7 +376,7 @@ def decode_variant(pa, lib, stream, D, token, steps, warmup, graph_steps, use_gr
     dec.reset(token, START_POS)
     kernels = {}
     for name in dict.fromkeys(names):
-        if name.startswith(("embedding", "aq_embedding", "argmax", "position", "scalar_mul", "flash_decoding_reduce")):
+        if name.startswith(("embedding", "aq_embedding", "argmax", "decode_next_token", "scalar_mul", "flash_decoding_reduce")):
             continue
         ms, _ = dec.time_kernel(name, reps=reps)
         kernels[name] = round(ms * 1e3, 2)

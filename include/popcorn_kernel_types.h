@@ -285,6 +285,24 @@ typedef struct {
     uint32_t historyLen;
 } PositionAdvanceConstants;
 
+/* No counterpart in the reference: the end of a captured greedy decode step
+ * in one launch. From stage-1 argmax candidates (slices of them, over N
+ * logits) it picks the token (Argmax.metal's tie and NaN rules), records it
+ * in the history ring (historyLen entries, index = position), advances the
+ * position by delta, and writes the next step's input row: the token's
+ * embedding row (H values; 4-bit rows dequantised as q * scale + bias,
+ * rounded to bf16 as the gather stores it) times `scale`, rounded to bf16
+ * (EmbeddingGather then ScalarMul, Gemma4TextInference.swift:184-185). */
+typedef struct {
+    uint32_t N;
+    uint32_t slices;
+    uint32_t H;
+    uint32_t historyLen;
+    int32_t delta;
+    float scale;
+    uint32_t hasBias;
+} DecodeNextTokenConstants;
+
 #ifdef __cplusplus
 }
 #endif

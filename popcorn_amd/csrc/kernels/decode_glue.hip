@@ -2,6 +2,7 @@
 // position update that closes a captured step, and a device-side normal
 // generator for synthetic benchmark inputs.
 #include "common.hpp"
+#include "q4.hpp"
 
 namespace {
 
@@ -121,6 +122,67 @@ POPCORN_KERNEL void __launch_bounds__(256)
         if (bi == 0x7fffffff || __builtin_isnan(x[(uint64_t)row * p.N])) bi = 0;
         indices[row] = bi;
     }
+}
+
+namespace {
+
+// The tail of a greedy decode step (DecodeNextTokenConstants): stage 2 of the
+// argmax over the candidates of argmax_partial, token / history / position
+// as position_advance does, then the next step's input row as the gather and
+// scalar multiply at the head of a step compute it. One block.
+template <bool Q4>
+__device__ void next_token(const float *logits, const float *pv, const int32_t *pi, int32_t *token, int32_t *pos,
+                           int32_t *history, const uint16_t *table, const uint32_t *W, const uint16_t *Sc,
+                           const uint16_t *Bi, uint16_t *x, const DecodeNextTokenConstants &c) {
+    float bv = -INFINITY;
+    int32_t bi = 0x7fffffff;
+    for (uint32_t s = threadIdx.x; s < c.slices; s += blockDim.x) {
+        if (better(pv[s], pi[s], bv, bi)) {
+            bv = pv[s];
+            bi = pi[s];
+        }
+    }
+    block_best(bv, bi);  // every thread holds the winner
+    if (bi == 0x7fffffff || __builtin_isnan(logits[0])) bi = 0;
+    if (threadIdx.x == 0) {
+        token[0] = bi;
+        const int32_t at = pos[0];
+        if (c.historyLen && at >= 0) history[(uint32_t)at % c.historyLen] = bi;
+        pos[0] = at + c.delta;
+    }
+    const uint64_t row = (uint32_t)bi;
+    if constexpr (!Q4) {
+        for (uint32_t h = threadIdx.x; h < c.H; h += blockDim.x)
+            x[h] = BF16::store(BF16::load(table[row * c.H + h]) * c.scale);
+    } else {
+        const uint32_t wordsPerRow = c.H / 8, groups = c.H / 64;
+        for (uint32_t wi = threadIdx.x; wi < wordsPerRow; wi += blockDim.x) {
+            const uint32_t g = wi / pk::kQ4GroupWords;
+            const uint32_t w = W[row * wordsPerRow + wi];
+            const float s = pk::bf16_lo(Sc[row * groups + g]);
+            const float b = c.hasBias ? pk::bf16_lo(Bi[row * groups + g]) : 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint16_t te = BF16::store((float)((w >> (4 * e)) & 15u) * s + b);
+                x[wi * 8 + e] = BF16::store(BF16::load(te) * c.scale);
+            }
+        }
+    }
+}
+
+}  // namespace
+
+POPCORN_KERNEL void __launch_bounds__(256)
+    decode_next_token_bf16(const float *logits, const float *pv, const int32_t *pi, int32_t *token, int32_t *pos,
+                           int32_t *history, const uint16_t *table, uint16_t *x, DecodeNextTokenConstants c) {
+    next_token<false>(logits, pv, pi, token, pos, history, table, nullptr, nullptr, nullptr, x, c);
+}
+
+POPCORN_KERNEL void __launch_bounds__(256)
+    decode_next_token_q4_bf16(const float *logits, const float *pv, const int32_t *pi, int32_t *token, int32_t *pos,
+                              int32_t *history, const uint32_t *W, const uint16_t *Sc, const uint16_t *Bi, uint16_t *x,
+                              DecodeNextTokenConstants c) {
+    next_token<true>(logits, pv, pi, token, pos, history, nullptr, W, Sc, Bi, x, c);
 }
 
 // The last node of a captured decode step: record the step's token, then

@@ -88,8 +88,12 @@ struct popcorn_decoder_s {
     QMat qqkv, qo, qg, qu, qd, qemb;
     Buffer kcache, vcache;
     Buffer x, x2, e, qkv, attn, o, mlp, hidden, logits /*f32*/, token /*i32*/, position /*i32*/, history /*i32*/;
+    Buffer argValues /*f32 [argSlices]*/, argIndices /*i32 [argSlices]*/;
+    int64_t argSlices = 1;
 
-    std::vector<std::unique_ptr<Kernel>> step;
+    // prime: the input row of the token in `token` (embedding gather, then
+    // x sqrt(H)); every later step's tail writes the next one itself
+    std::vector<std::unique_ptr<Kernel>> prime, step;
     std::vector<std::string> names;
     hipGraphExec_t graph = nullptr;
     hipGraph_t graphDef = nullptr;
@@ -170,10 +174,11 @@ struct popcorn_decoder_s {
         Tensor tfin(finalNorm.p, Shape({H}), DataType::f32);
 
         auto add = [&](std::unique_ptr<Kernel> k) { step.push_back(std::move(k)); };
-        // Gemma4TextInference.swift:184-185: gather, then scale by sqrt(H)
-        if (q4) add(Kernels::EmbeddingGather(ttok, qemb.at(0), te));
-        else add(Kernels::EmbeddingGather(ttok, temb, te));
-        add(Kernels::ScalarMul(te, std::sqrt((float)H), tx));
+        // Gemma4TextInference.swift:184-185: gather, then scale by sqrt(H);
+        // run before the first step of each run(), the steps' tails after
+        if (q4) prime.push_back(Kernels::EmbeddingGather(ttok, qemb.at(0), te));
+        else prime.push_back(Kernels::EmbeddingGather(ttok, temb, te));
+        prime.push_back(Kernels::ScalarMul(te, std::sqrt((float)H), tx));
         const AttentionMask causal{0, -1};
         Tensor prevPostFfn;
         for (int64_t l = 0; l < L; ++l) {
@@ -252,11 +257,28 @@ struct popcorn_decoder_s {
         head.out = &tlog;
         head.eps = eps;
         add(Kernels::DecodeMatvec(head));
-        add(Kernels::Argmax(tlog, ttok));
-        PositionAdvanceConstants pc{1, (uint32_t)std::max(cfg.history_len, 0)};
+        // Argmax (Argmax.metal) in two stages: the slices' candidates, then
+        // one block that picks the token, records it, advances the position
+        // and writes the next step's input row (gather, x sqrt(H))
+        Tensor tpv(argValues.p, Shape({argSlices}), DataType::f32);
+        Tensor tpi(argIndices.p, Shape({argSlices}), DataType::i32);
+        ArgmaxConstants ac{1u, (uint32_t)V, (uint32_t)argSlices};
+        add(Kernels::Custom("argmax_partial", {{tlog, kRead}, {tpv, kWrite}, {tpi, kWrite}}, {bytesOf(ac)},
+                            dim3((unsigned)argSlices, 1, 1), dim3(256, 1, 1)));
         Tensor thist(history.p, Shape({std::max<int64_t>(cfg.history_len, 1)}), DataType::i32);
-        add(Kernels::Custom("position_advance", {{ttok, kRead}, {tpos, kReadWrite}, {thist, kWrite}}, {bytesOf(pc)},
-                            dim3(1, 1, 1), dim3(64, 1, 1)));
+        DecodeNextTokenConstants nc{(uint32_t)V, (uint32_t)argSlices, (uint32_t)H,
+                                    (uint32_t)std::max(cfg.history_len, 0), 1, std::sqrt((float)H), 1u};
+        if (q4)
+            add(Kernels::Custom("decode_next_token_q4_bf16",
+                                {{tlog, kRead}, {tpv, kRead}, {tpi, kRead}, {ttok, kWrite}, {tpos, kReadWrite},
+                                 {thist, kWrite}, {qemb.packedAt(0), kRead}, {qemb.scalesAt(0), kRead},
+                                 {qemb.biasesAt(0), kRead}, {tx, kWrite}},
+                                {bytesOf(nc)}, dim3(1, 1, 1), dim3(256, 1, 1)));
+        else
+            add(Kernels::Custom("decode_next_token_bf16",
+                                {{tlog, kRead}, {tpv, kRead}, {tpi, kRead}, {ttok, kWrite}, {tpos, kReadWrite},
+                                 {thist, kWrite}, {temb, kRead}, {tx, kWrite}},
+                                {bytesOf(nc)}, dim3(1, 1, 1), dim3(256, 1, 1)));
         for (const auto &k : step) {
             std::string d = k->describe();
             size_t s = 0;
@@ -299,13 +321,20 @@ struct popcorn_decoder_s {
         checkHip(hipGraphInstantiate(&graph, graphDef, nullptr, nullptr, 0), "hipGraphInstantiate");
     }
 
+    void encodePrime() {
+        for (const auto &k : prime) enc->encode(*k);
+    }
+
     void run(int32_t steps, bool useGraph) {
         if (steps < 0) throw Error::invalidArgument("steps must be >= 0");
+        if (steps == 0) return;
         if (!useGraph) {
+            encodePrime();
             for (int32_t i = 0; i < steps; ++i) encodeStep();
             return;
         }
         capture();
+        encodePrime();
         int32_t i = 0;
         for (; i + graphSteps <= steps; i += graphSteps) checkHip(hipGraphLaunch(graph, stream), "hipGraphLaunch");
         for (; i < steps; ++i) encodeStep();
@@ -408,6 +437,9 @@ popcorn_status_t popcorn_decoder_create(popcorn_library_t library, popcorn_strea
         d->token = Buffer(4);
         d->position = Buffer(4);
         d->history = Buffer((size_t)(std::max(c.history_len, 1) * 4));
+        d->argSlices = std::clamp<int64_t>((d->V + 4095) / 4096, 1, 256);  // as Kernels::Argmax slices a row
+        d->argValues = Buffer((size_t)(d->argSlices * 4));
+        d->argIndices = Buffer((size_t)(d->argSlices * 4));
         checkHip(hipMemsetAsync(d->token.p, 0, 4, d->stream), "memset");
         checkHip(hipMemsetAsync(d->position.p, 0, 4, d->stream), "memset");
         checkHip(hipMemsetAsync(d->history.p, 0xff, d->history.bytes, d->stream), "memset");
