@@ -23,8 +23,9 @@
  * decode configuration (no per-head norms or RoPE).
  *
  * The position and the token live in device memory and the step ends with a
- * kernel that advances the position, so a step (or several) is captured once
- * as a HIP graph and replayed with no host work per token.
+ * kernel that picks the token, advances the position and writes the next
+ * step's input row, so a step (or several) is captured once as a HIP graph
+ * and replayed with no host work per token.
  */
 #ifndef POPCORN_DECODER_H
 #define POPCORN_DECODER_H
@@ -81,7 +82,9 @@ popcorn_status_t popcorn_decoder_tensor(popcorn_decoder_t decoder, const char *n
 popcorn_status_t popcorn_decoder_reset(popcorn_decoder_t decoder, int32_t token, int32_t position);
 
 /* Enqueues `steps` decode steps on the decoder's stream (no host sync):
- * through captured graphs when use_graph != 0, else dispatch by dispatch. */
+ * through captured graphs when use_graph != 0, else dispatch by dispatch.
+ * The first step starts from the token and position in device memory (its
+ * input row is gathered first); "logits" then holds the last step's. */
 popcorn_status_t popcorn_decoder_step(popcorn_decoder_t decoder, int32_t steps, int32_t use_graph);
 
 /* Waits for the stream, then reads the current token and position. */
