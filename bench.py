@@ -213,6 +213,38 @@ def fd_sweep(pa, lib, stream, enc):
     return out_rows
 
 
+def mlp_config3(pa, lib, stream, enc, sets=4, reps=64):
+    """the Gemma-2B-shaped MLP decode at batch 1 in bf16
+    (f32 accumulation): RMSNorm over x [2304] (N(0, 1), eps 1e-6, weight
+    1 + N(0, 0.1)), the fused gate/up matvec ([9216, 2304] each, N(0, 0.02))
+    with GELU-tanh gating, then the down matvec ([2304, 9216]). `sets` weight
+    sets (510 MB, cold in the 256 MB MALL) are cycled. Bytes: the three
+    matrices, x, the norm weight, the hidden vector written and read, y."""
+    H, F = 2304, 9216
+    x = pa.Tensor.empty([H], "bf16")
+    lib.fill_normal(x, 61, stream=stream)
+    nw = pa.Tensor.empty([H], "f32")
+    lib.fill_normal(nw, 62, mean=1.0, std=0.1, stream=stream)
+    wg = pa.Tensor.empty([sets * F * H], "bf16")
+    wu = pa.Tensor.empty([sets * F * H], "bf16")
+    wd = pa.Tensor.empty([sets * H * F], "bf16")
+    for i, w in enumerate((wg, wu, wd)):
+        lib.fill_normal(w, 63 + i, std=0.02, stream=stream)
+    y = pa.Tensor.empty([H], "bf16")
+    hid = pa.Tensor.empty([F], "bf16")
+    kerns = [pa.Kernels.GatedMLP(x, nw, wg.view([F, H], offset_elements=i * F * H),
+                                 wu.view([F, H], offset_elements=i * F * H),
+                                 wd.view([H, F], offset_elements=i * H * F), y, eps=1e-6, hidden=hid)
+             for i in range(sets)]
+    enc.encode(*kerns)
+    stream.synchronize()
+    us = timed_launches(pa, stream, enc, [kerns[r % sets] for r in range(reps)])
+    nbytes = 3 * F * H * 2 + H * 2 + H * 4 + 2 * F * 2 + H * 2
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"kernels": kerns[0].function_names, "us": round(us, 2), "bytes": nbytes, "GB_s": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 3)}
+
+
 MFMA_PEAK_F16_TFLOPS = 2500.0
 
 
@@ -395,6 +427,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=4)
     ap.add_argument("--no-fd-sweep", action="store_true", help="skip the config-2 FlashDecoding sweep")
+    ap.add_argument("--no-mlp", action="store_true", help="skip the config-3 MLP decode measurement")
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-5 prefill measurement")
     ap.add_argument("--library-reference", action="store_true",
                     help="also time the config-5 shapes through PyTorch's hipBLASLt GEMM and SDPA attention")
@@ -460,6 +493,10 @@ def main():
     if not args.no_fd_sweep:
         fd = fd_sweep(pa, lib, stream, pa.KernelCommandEncoder(lib, stream))
 
+    mlp = None
+    if not args.no_mlp:
+        mlp = mlp_config3(pa, lib, stream, pa.KernelCommandEncoder(lib, stream))
+
     prefill = None
     if not args.no_prefill:
         prefill = prefill_config5(pa, lib, stream, pa.KernelCommandEncoder(lib, stream))
@@ -504,6 +541,7 @@ def main():
         "roofline": roofline,
         "kernels": kernels,
         "flash_decoding_config2": fd,
+        "mlp_config3": mlp,
         "prefill_config5": prefill,
         "decode_attention_block": block,
         "q4_matvec": q4,
