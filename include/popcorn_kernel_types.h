@@ -275,18 +275,10 @@ typedef struct {
     float stddev;
 } FillNormalConstants;
 
-/* The update that closes a captured decode step: the step's token is stored
- * in history[position % historyLen] (when historyLen > 0) and the position
- * tensor advances by `delta` (a kernel, so graph replays need no memset or
- * host write). No counterpart in the reference (GemmaCLI writes the position
- * from the CPU, Gemma4TextInference.swift:95-99). */
-typedef struct {
-    int32_t delta;
-    uint32_t historyLen;
-} PositionAdvanceConstants;
-
-/* No counterpart in the reference: the end of a captured greedy decode step
- * in one launch. From stage-1 argmax candidates (slices of them, over N
+/* No counterpart in the reference (GemmaCLI picks the token and writes the
+ * position from the CPU, Gemma4TextInference.swift:95-99): the end of a
+ * captured greedy decode step in one launch, so graph replays need no host
+ * write. From stage-1 argmax candidates (slices of them, over N
  * logits) it picks the token (Argmax.metal's tie and NaN rules), records it
  * in the history ring (historyLen entries, index = position), advances the
  * position by delta, and writes the next step's input row: the token's

@@ -127,9 +127,11 @@ POPCORN_KERNEL void __launch_bounds__(256)
 namespace {
 
 // The tail of a greedy decode step (DecodeNextTokenConstants): stage 2 of the
-// argmax over the candidates of argmax_partial, token / history / position
-// as position_advance does, then the next step's input row as the gather and
-// scalar multiply at the head of a step compute it. One block.
+// argmax over the candidates of argmax_partial; the token is stored in
+// history[position % historyLen] and the position advances by delta (a
+// kernel, so graph replays need no host write); then the next step's input
+// row as the gather and scalar multiply at the head of a step compute it.
+// One block.
 template <bool Q4>
 __device__ void next_token(const float *logits, const float *pv, const int32_t *pi, int32_t *token, int32_t *pos,
                            int32_t *history, const uint16_t *table, const uint32_t *W, const uint16_t *Sc,
@@ -185,15 +187,6 @@ POPCORN_KERNEL void __launch_bounds__(256)
     next_token<true>(logits, pv, pi, token, pos, history, nullptr, W, Sc, Bi, x, c);
 }
 
-// The last node of a captured decode step: record the step's token, then
-// pos[0] += delta.
-POPCORN_KERNEL void position_advance(const int32_t *token, int32_t *pos, int32_t *history, PositionAdvanceConstants p) {
-    if (threadIdx.x == 0 && blockIdx.x == 0) {
-        const int32_t at = pos[0];
-        if (p.historyLen && at >= 0) history[(uint32_t)at % p.historyLen] = token[0];
-        pos[0] = at + p.delta;
-    }
-}
 
 namespace {
 
