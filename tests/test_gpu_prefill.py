@@ -139,6 +139,24 @@ def test_tiled_attention_split_tiles_vs_oracle(env, dtype, ot, B, Nq, Nkv, Sq, S
     assert_out(got, ref, EPS[dtype], ot, f"split tiled attention {dtype}->{ot} Sq={Sq} Sk={Sk} Hd={Hd}")
 
 
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_tiled_attention_wide_score_range(env, dtype):
+    # scores spread over hundreds of natural-log units (scale 1, inputs x 3):
+    # the running max moves often and far, so the lazy rescale (the reference
+    # max moves only when a score passes it by more than 8) is exercised on
+    # most steps, split tiles included
+    pa = env[0]
+    B, Nq, Nkv, S, Hd = 1, 2, 1, 640, 64
+    q = rounded(3.0 * O.normal(901, (B, Nq, S, Hd)), dtype)
+    k = rounded(3.0 * O.normal(902, (B, Nkv, S, Hd)), dtype)
+    v = rounded(O.normal(903, (B, Nkv, S, Hd)), dtype)
+    got, kern = _attend(env, q, k, v, dtype, dtype, 1.0, pa.AttentionMask(0, -1))
+    assert kern.function_names[0] == f"flash_attention_tiled_{dtype}_{dtype}_d{Hd}"
+    ref = O.attention_naive(q, k, v, 1.0, mask_kind=0)
+    assert np.isfinite(got).all()
+    assert_out(got, ref, EPS[dtype], dtype, f"wide-range tiled attention {dtype}")
+
+
 def test_tiled_attention_config5_sampled(env):
     # BASELINE config 5 attention: [1, 16, 2048, 256] f16, causal, scale 1/16.
     # A sampled query row r is checked as a single-row query over keys 0..r
