@@ -548,7 +548,8 @@ GemmTile gemmTile(int64_t m, int64_t n, int64_t k) {
     static const GemmTile tiles[] = {{256, 256, 512, "t256x256"}, {256, 256, 256, "t256x256w4"},
                                      {256, 128, 512, "t256x128"}, {128, 256, 512, "t128x256"},
                                      {128, 128, 256, "t128x128"}, {256, 256, 512, "d256x256"},
-                                     {128, 128, 256, "d128x128"}, {128, 256, 512, "d128x256"}};
+                                     {128, 128, 256, "d128x128"}, {128, 256, 512, "d128x256"},
+                                     {128, 192, 256, "d128x192"}};
     if (const char *e = std::getenv("POPCORN_GEMM_TILE")) {  // tuning override, e.g. "t256x128"
         for (const GemmTile &t : tiles)
             if (std::string(t.suffix) == e && (t.suffix[0] != 'd' || k % 32 == 0)) return t;
@@ -565,9 +566,14 @@ GemmTile gemmTile(int64_t m, int64_t n, int64_t k) {
     const bool big = cdiv(m, 256) * cdiv(n, 256) >= 3 * deviceCUs();
     if (k % 32 == 0) {
         if (big) return tiles[5];
+        // 128 x 192 tiles when their grid is whole rounds of one tile per CU
+        // (config-5 QKV, N 9216: 768 tiles, 155 -> 135 us; down, N 3072:
+        // 256 tiles, 397 -> 352 us)
+        const int64_t t192 = cdiv(m, 128) * cdiv(n, 192);
+        if (n % 192 == 0 && t192 % deviceCUs() == 0) return tiles[8];
         // a 128 x 128 grid between one and two tiles per CU leaves half the
         // CUs with a second tile; one 128 x 256 tile per CU (8 waves) ends
-        // sooner (config-5 down, M 2048 N 3072 K 24576: 379 against 423 us)
+        // sooner (config-5 down: 379 against 423 us before 128 x 192 took it)
         const int64_t t128 = cdiv(m, 128) * cdiv(n, 128);
         if (t128 > deviceCUs() && t128 < 2 * (int64_t)deviceCUs() && n >= 256) return tiles[7];
         return tiles[6];
