@@ -302,6 +302,7 @@ __device__ void gemm_nt_direct(const uint16_t *__restrict__ A, const uint16_t *_
     GEMM_MFMA_D(base##_d128x128, T, O, 128, 128, 2, 2)       \
     GEMM_MFMA_D(base##_d128x256, T, O, 128, 256, 2, 4)       \
     GEMM_MFMA_D(base##_d128x192, T, O, 128, 192, 2, 2)       \
+    GEMM_MFMA_D(base##_d256x384, T, O, 256, 384, 2, 4)       \
     GEMM_MFMA(base##_t128x128, T, O, 128, 128, 2, 2)         \
     GEMM_MFMA(base##_t256x128, T, O, 256, 128, 4, 2)         \
     GEMM_MFMA(base##_t128x256, T, O, 128, 256, 2, 4)         \

@@ -549,7 +549,7 @@ GemmTile gemmTile(int64_t m, int64_t n, int64_t k) {
                                      {256, 128, 512, "t256x128"}, {128, 256, 512, "t128x256"},
                                      {128, 128, 256, "t128x128"}, {256, 256, 512, "d256x256"},
                                      {128, 128, 256, "d128x128"}, {128, 256, 512, "d128x256"},
-                                     {128, 192, 256, "d128x192"}};
+                                     {128, 192, 256, "d128x192"}, {256, 384, 512, "d256x384"}};
     if (const char *e = std::getenv("POPCORN_GEMM_TILE")) {  // tuning override, e.g. "t256x128"
         for (const GemmTile &t : tiles)
             if (std::string(t.suffix) == e && (t.suffix[0] != 'd' || k % 32 == 0)) return t;
@@ -565,6 +565,13 @@ GemmTile gemmTile(int64_t m, int64_t n, int64_t k) {
     //   down N 3072  K 24576  589   430   712   485
     const bool big = cdiv(m, 256) * cdiv(n, 256) >= 3 * deviceCUs();
     if (k % 32 == 0) {
+        // 256 x 384 (8 waves of 128 x 96: 7 fragment reads per 12 MFMAs) when
+        // its grid keeps at least 70% of the CUs busy in every round
+        // (config-5 QKV, 192 tiles: 136 -> 127 us; gate and up, 512 tiles:
+        // 294-303 -> 284-288 us)
+        const int64_t cus = deviceCUs();
+        const int64_t t384 = cdiv(m, 256) * cdiv(n, 384);
+        if (t384 * 10 >= cus * 7 && t384 * 10 >= cdiv(t384, cus) * cus * 7) return tiles[9];
         if (big) return tiles[5];
         // 128 x 192 tiles when their grid is whole rounds of one tile per CU
         // (config-5 QKV, N 9216: 768 tiles, 155 -> 135 us; down, N 3072:
