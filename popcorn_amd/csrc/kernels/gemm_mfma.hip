@@ -178,9 +178,13 @@ __device__ inline void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-template <typename T, typename O, int BM, int BN, int WM_N, int WN_N>
+// SPLITK: gridDim.y blocks share a tile, each over K / gridDim.y of the
+// reduction, and write f32 partial products to P [gridDim.y][M][N] for
+// gemm_splitk_reduce (C is then unused).
+template <typename T, typename O, int BM, int BN, int WM_N, int WN_N, bool SPLITK = false>
 __device__ void gemm_nt_direct(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
-                               typename O::storage *__restrict__ C, const MatmulConstants &p) {
+                               typename O::storage *__restrict__ C, const MatmulConstants &p,
+                               float *__restrict__ P = nullptr) {
     constexpr int NW = WM_N * WN_N;
     constexpr int WM = BM / WM_N, WN = BN / WN_N;
     constexpr int TM = WM / 32, TN = WN / 32;
@@ -201,8 +205,9 @@ __device__ void gemm_nt_direct(const uint16_t *__restrict__ A, const uint16_t *_
 
     // this lane's source rows / chunk for each of its wave's instructions
     const uint32_t lr = lane >> 2, lpos = lane & 3;
+    const uint32_t kBase = SPLITK ? blockIdx.y * (K / gridDim.y) : 0u;
     auto issue = [&](uint32_t kt) {
-        const uint32_t k0 = kt * BKD;
+        const uint32_t k0 = kBase + kt * BKD;
         uint8_t *stage = smem + (kt % kStagesD) * kStageB;
 #pragma unroll
         for (int i = 0; i < kInstA; ++i) {
@@ -248,7 +253,7 @@ __device__ void gemm_nt_direct(const uint16_t *__restrict__ A, const uint16_t *_
         }
     };
 
-    const uint32_t nk = K / BKD;
+    const uint32_t nk = (SPLITK ? K / gridDim.y : K) / BKD;
 #pragma unroll
     for (int s = 0; s < kStagesD - 1; ++s)
         if ((uint32_t)s < nk) issue(s);
@@ -277,9 +282,37 @@ __device__ void gemm_nt_direct(const uint16_t *__restrict__ A, const uint16_t *_
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const uint32_t row = bm + wm + mi * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
-                if (row < M && col < N) C[(uint64_t)row * N + col] = O::store(acc[mi][ni][i]);
+                if (row < M && col < N) {
+                    if constexpr (SPLITK)
+                        P[((uint64_t)blockIdx.y * M + row) * N + col] = acc[mi][ni][i];
+                    else
+                        C[(uint64_t)row * N + col] = O::store(acc[mi][ni][i]);
+                }
             }
         }
+    }
+}
+
+// C = sum over the gridDim.y-way split of P [splits][M][N] (f32), rounded
+// once to C's dtype; 4 elements per thread (M N % 4 == 0).
+template <typename O>
+__device__ void gemm_splitk_reduce(const float *__restrict__ P, typename O::storage *__restrict__ C,
+                                   const MatmulConstants &p, uint32_t splits) {
+    const uint64_t mn = (uint64_t)p.M * p.N;
+    for (uint64_t i = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4; i < mn;
+         i += (uint64_t)gridDim.x * blockDim.x * 4) {
+        float4 a = *reinterpret_cast<const float4 *>(P + i);
+        for (uint32_t s = 1; s < splits; ++s) {
+            const float4 b = *reinterpret_cast<const float4 *>(P + s * mn + i);
+            a.x += b.x;
+            a.y += b.y;
+            a.z += b.z;
+            a.w += b.w;
+        }
+        C[i] = O::store(a.x);
+        C[i + 1] = O::store(a.y);
+        C[i + 2] = O::store(a.z);
+        C[i + 3] = O::store(a.w);
     }
 }
 
@@ -317,3 +350,20 @@ GEMM_MFMA_TILES(matmul_mfma_f16_f16_f16, F16, F16)
 GEMM_MFMA_TILES(matmul_mfma_f16_f16_f32, F16, F32)
 GEMM_MFMA_TILES(matmul_mfma_bf16_bf16_bf16, BF16, BF16)
 GEMM_MFMA_TILES(matmul_mfma_bf16_bf16_f32, BF16, F32)
+
+// Split-K form of the 256 x 384 tile (f32 partials) and the reduction.
+#define GEMM_MFMA_SPLITK(name, T)                                                                 \
+    POPCORN_KERNEL void __launch_bounds__(512)                                                    \
+        name(const uint16_t *a, const uint16_t *b, float *partial, MatmulConstants p) {          \
+        gemm_nt_direct<T, F32, 256, 384, 2, 4, true>(a, b, nullptr, p, partial);                  \
+    }
+#define GEMM_SPLITK_REDUCE(name, O)                                                                    \
+    POPCORN_KERNEL void __launch_bounds__(256)                                                         \
+        name(const float *partial, O::storage *c, MatmulConstants p, uint32_t splits) {                \
+        gemm_splitk_reduce<O>(partial, c, p, splits);                                                  \
+    }
+GEMM_MFMA_SPLITK(matmul_mfma_f16_splitk_d256x384, F16)
+GEMM_MFMA_SPLITK(matmul_mfma_bf16_splitk_d256x384, BF16)
+GEMM_SPLITK_REDUCE(matmul_splitk_reduce_f16, F16)
+GEMM_SPLITK_REDUCE(matmul_splitk_reduce_bf16, BF16)
+GEMM_SPLITK_REDUCE(matmul_splitk_reduce_f32, F32)

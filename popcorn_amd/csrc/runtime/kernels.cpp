@@ -588,6 +588,50 @@ GemmTile gemmTile(int64_t m, int64_t n, int64_t k) {
     return big ? tiles[0] : tiles[4];
 }
 
+// Split-K for a GEMM whose 256 x 384 tiles are too few to fill the CUs:
+// the number of K splits that makes the grid whole rounds of one tile per
+// CU, each split at least 2048 deep, or 0. Config-5 down (M 2048, N 3072,
+// K 24576): 64 tiles x 4 splits of K 6144.
+int64_t gemmSplitK(int64_t m, int64_t n, int64_t k) {
+    if (std::getenv("POPCORN_GEMM_TILE") || k % 32 != 0 || (m * n) % 4 != 0) return 0;
+    const int64_t cus = deviceCUs();
+    const int64_t t384 = cdiv(m, 256) * cdiv(n, 384);
+    if (t384 * 10 >= cus * 7) return 0;
+    for (int64_t s = 2; s <= 8; ++s)
+        if ((t384 * s) % cus == 0 && k % (32 * s) == 0 && k / s >= 2048) return s;
+    return 0;
+}
+
+// The split-K GEMM: f32 partial products per split in scratch, then one
+// pass that sums them and rounds to C's dtype.
+class SplitKMatmulKernel : public Kernel {
+public:
+    SplitKMatmulKernel(const Tensor &a, const Tensor &b, const Tensor &c, int64_t m, int64_t k, int64_t n, int64_t splits)
+        : a_(a), b_(b), c_(c), m_(m), k_(k), n_(n), splits_(splits) {}
+    std::vector<Binding> tensors() const override { return {{a_, kRead}, {b_, kRead}, {c_, kWrite}}; }
+    std::string describe() const override { return mainName() + "," + reduceName(); }
+    void encode(KernelCommandEncoder &enc) const override {
+        MatmulConstants mc{(uint32_t)m_, (uint32_t)k_, (uint32_t)n_, 1u};
+        enc.withTemporaryTensor(ScratchSpec{{splits_ * m_, n_}, DataType::f32}, [&](Tensor part) {
+            DispatchSize ds;
+            ds.grid = dim3((unsigned)(cdiv(m_, 256) * cdiv(n_, 384)), (unsigned)splits_, 1);
+            ds.block = dim3(512, 1, 1);
+            FixedDispatch s1(mainName(), {{a_, kRead}, {b_, kRead}, {part, kWrite}}, {bytesOf(mc)}, ds);
+            enc.dispatch(s1);
+            const uint32_t splits = (uint32_t)splits_;
+            const int64_t blocks = std::clamp<int64_t>(cdiv(m_ * n_ / 4, kBlock), 1, 8 * deviceCUs());
+            FixedDispatch s2(reduceName(), {{part, kRead}, {c_, kWrite}}, {bytesOf(mc), bytesOf(splits)}, grid1(blocks, kBlock));
+            enc.dispatch(s2);
+        });
+    }
+
+private:
+    std::string mainName() const { return std::string("matmul_mfma_") + tag(a_.dataType) + "_splitk_d256x384"; }
+    std::string reduceName() const { return std::string("matmul_splitk_reduce_") + tag(c_.dataType); }
+    Tensor a_, b_, c_;
+    int64_t m_, k_, n_, splits_;
+};
+
 constexpr int64_t kMaxStagedK = 16384;  // x staged as f32 in 64 KB of LDS
 
 std::unique_ptr<Kernel> makeMatmul(const Tensor &a, const Tensor &b, const Tensor &c, int64_t m, int64_t k, int64_t n,
@@ -624,6 +668,8 @@ std::unique_ptr<Kernel> makeMatmul(const Tensor &a, const Tensor &b, const Tenso
         if (transposeB && (t == DataType::f16 || t == DataType::bf16) && b.dataType == t &&
             (c.dataType == t || c.dataType == DataType::f32) && k % 8 == 0 && k > 0 && aligned16(a.data) &&
             aligned16(b.data)) {
+            if (const int64_t splits = gemmSplitK(m, n, k))
+                return std::make_unique<SplitKMatmulKernel>(a, b, c, m, k, n, splits);
             MatmulConstants mc{(uint32_t)m, (uint32_t)k, (uint32_t)n, 1u};
             const GemmTile tile = gemmTile(m, n, k);
             const std::string fn =

@@ -82,6 +82,20 @@ def test_prefill_attention_split_plan():
     assert fa(64, 2048) == ["flash_attention_tiled_f16_f16_d256"]                 # 1024 tiles: 4 per CU
 
 
+def test_prefill_gemm_tile_plan():
+    # MFMA GEMM tiles by CU fill (256 CUs when no GPU answers); a grid of
+    # 256 x 384 tiles too small for the CUs splits K into whole rounds
+    def mm(M, K, N, dtype="f16", out=None):
+        return pa.Kernels.Matmul(T([M, K], dtype), T([N, K], dtype), T([M, N], out or dtype), True).function_names
+    assert mm(2048, 3072, 9216) == ["matmul_mfma_f16_f16_f16_d256x384"]    # QKV: 192 tiles, 75% fill
+    assert mm(2048, 3072, 24576) == ["matmul_mfma_f16_f16_f16_d256x384"]   # gate / up: 512 tiles
+    assert mm(2048, 24576, 3072) == ["matmul_mfma_f16_splitk_d256x384", "matmul_splitk_reduce_f16"]  # down: 64 x 4
+    assert mm(2000, 16384, 1500, "bf16", "f32") == ["matmul_mfma_bf16_splitk_d256x384",
+                                                    "matmul_splitk_reduce_f32"]  # 32 tiles x 8 splits
+    assert mm(2048, 4096, 3072) == ["matmul_mfma_f16_f16_f16_d128x192"]    # splits would be under 2048 deep
+    assert mm(256, 1024, 384) == ["matmul_mfma_f16_f16_f16_d128x128"]
+
+
 def test_flash_attention_routing_names():
     q, o = T([1, 8, 1, 256]), T([1, 8, 1, 256])
     k = T([1, 4, 4352, 256])

@@ -65,13 +65,50 @@ def test_mfma_matmul_config5_shapes_sampled(env, M, K, N):
     k = pa.Kernels.Matmul(ta, tb, c, True)
     enc.encode(k)
     stream.synchronize()
-    assert k.function_names[0].startswith("matmul_mfma_f16_f16_f16_")
+    assert k.function_names[0].startswith(("matmul_mfma_f16_f16_f16_", "matmul_mfma_f16_splitk_"))
     rows = [0, 1, 127, 128, M // 2 + 3, M - 1]
     a = download(ta, stream).reshape(M, K)[rows]
     b = download(tb, stream).reshape(N, K)
     got = download(c, stream).reshape(M, N)[rows]
     ref = O.matmul(a, b, len(rows), K, N, True).reshape(len(rows), N)
     assert_out(got, ref, EPS["f16"], "f16", f"config5 {M}x{K}x{N}")
+
+
+@pytest.mark.parametrize("at", ["f16", "bf16"])
+def test_mfma_matmul_split_k_integer_exact(env, at):
+    # 32 ragged 256 x 384 tiles x 8 K splits of 2048: small integers keep every
+    # partial sum exact, so the f32 result is exact whatever the split
+    pa, lib, stream, enc = env
+    rng = np.random.default_rng(13)
+    M, K, N = 2000, 16384, 1500
+    a = rng.integers(-4, 5, (M, K)).astype(np.float32)
+    b = rng.integers(-4, 5, (N, K)).astype(np.float32)
+    got, k = _gemm(env, a, b, at, "f32")
+    assert k.function_names == [f"matmul_mfma_{at}_splitk_d256x384", "matmul_splitk_reduce_f32"]
+    # |sums| <= 16 K < 2^24: exact in f64 (BLAS) and in f32
+    np.testing.assert_array_equal(got, (a.astype(np.float64) @ b.T.astype(np.float64)).astype(np.float32))
+
+
+@pytest.mark.parametrize("at,ot", [("f16", "f16"), ("bf16", "bf16"), ("bf16", "f32")])
+def test_mfma_matmul_split_k_vs_oracle(env, at, ot):
+    # the split-K reduction rounds once to the output dtype; oracle on sampled rows
+    pa, lib, stream, enc = env
+    M, K, N = 2000, 16384, 1500
+    a = rounded(O.normal(5, (M, K)), at)
+    b = rounded(O.normal(6, (N, K), std=0.02), at)
+    got, k = _gemm(env, a, b, at, ot)
+    assert k.function_names[1] == f"matmul_splitk_reduce_{ot}"
+    rows = [0, 255, 256, 1000, 1791, 1792, M - 1]
+    ref = O.matmul(a[rows], b, len(rows), K, N, True).reshape(len(rows), N)
+    if ot == "f32":
+        # f32 sums of 16384 terms in another order: the bar is 1e-5 of the
+        # sum of the terms' magnitudes (an element that cancels to near zero
+        # keeps the rounding of its large partial sums)
+        mag = np.abs(a[rows]).astype(np.float64) @ np.abs(b).T.astype(np.float64)
+        err = np.abs(got[rows].astype(np.float64) - ref)
+        assert (err <= 1e-5 * mag).all(), f"split-K gemm {at}->f32: max err/mag {np.max(err / mag):.3e}"
+    else:
+        assert_out(got[rows], ref, EPS[at], ot, f"split-K gemm {at}->{ot}")
 
 
 # ---- tiled (MFMA) FlashAttention prefill ---------------------------------------
