@@ -457,11 +457,14 @@ __device__ void fd_partial_generic(const typename T::storage *__restrict__ Q, co
 // LSE combine, FlashDecoding.metal:179-228:
 //   m* = max m_k, l* = sum exp(m_k - m*) l_k, O = sum exp(m_k - m*) O_k / l*.
 // Grid: x = (b * Nq + hq) * Sq + row, y = 64-dim slice of the head. Lane =
-// one dim; the 4 waves take interleaved partitions, each folding its
-// partitions in with a running max (so all of a wave's loads are
-// independent and in flight together), then the 4 wave states are merged
-// in LDS. Empty partitions (m = -inf, l = 0) contribute nothing.
-constexpr int kReduceBatch = 8;
+// one dim; each wave takes a contiguous quarter of the partitions, a batch
+// of kReduceBatch at a time: lane j loads batch entry j's m and l (one
+// vector load each; read back with readlane) and every lane its dim of each
+// entry's O, all in flight together, so a decode-sized combine (P <= 128)
+// is one memory round trip. The batch's max is taken first, so each batch
+// rescales the running state once; the 4 wave states are then merged in
+// LDS. Empty partitions (m = -inf, l = 0) contribute nothing.
+constexpr int kReduceBatch = 32;
 
 template <typename O>
 __device__ void fd_reduce(const float *__restrict__ pO, const float *__restrict__ pM, const float *__restrict__ pL,
@@ -470,33 +473,44 @@ __device__ void fd_reduce(const float *__restrict__ pO, const float *__restrict_
     __shared__ float sm_o[kWaves][64];
     const uint32_t P = p.P, Hd = p.Hd;
     const uint64_t slot = blockIdx.x;
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t d = blockIdx.y * 64 + lane;
     const uint32_t dc = min(d, Hd - 1);  // lanes past Hd read a valid dim and store nothing
     const float *m = pM + slot * P;
     const float *l = pL + slot * P;
     const float *o = pO + slot * P * Hd + dc;
+    const uint32_t per = (P + kWaves - 1) / kWaves;
+    const uint32_t kBeg = wave * per, kEnd = min(P, kBeg + per);
 
     float mr = -INFINITY, lr = 0.0f, acc = 0.0f;
-    for (uint32_t k0 = wave; k0 < P; k0 += kWaves * kReduceBatch) {
-        float mk[kReduceBatch], lk[kReduceBatch], ok[kReduceBatch];
+    for (uint32_t k0 = kBeg; k0 < kEnd; k0 += kReduceBatch) {
+        // entries past the range repeat the last one and are masked below
+        const uint32_t kl = min(k0 + (lane % kReduceBatch), kEnd - 1);
+        const float mv = m[kl], lv = l[kl];
+        float ok[kReduceBatch];
+#pragma unroll
+        for (int i = 0; i < kReduceBatch; ++i) ok[i] = o[(uint64_t)min(k0 + i, kEnd - 1) * Hd];
+        float mk[kReduceBatch];
+        float mx = mr;
 #pragma unroll
         for (int i = 0; i < kReduceBatch; ++i) {
-            const uint32_t k = min(k0 + kWaves * i, P - 1);
-            mk[i] = m[k];
-            lk[i] = l[k];
-            ok[i] = o[(uint64_t)k * Hd];
+            mk[i] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mv), i));
+            if (k0 + i < kEnd) mx = fmaxf(mx, mk[i]);
         }
+        // selects, not branches (a branch here lets the compiler sink the O
+        // loads below it): while every partition so far is empty, mx = -inf
+        // and every weight is 0
+        const float a = mr == -INFINITY ? 0.0f : pk::fast_exp(mr - mx);
+        acc *= a;
+        lr *= a;
 #pragma unroll
         for (int i = 0; i < kReduceBatch; ++i) {
-            if (k0 + kWaves * i >= P || mk[i] == -INFINITY) continue;
-            const float mn = fmaxf(mr, mk[i]);
-            const float a = mr == -INFINITY ? 0.0f : pk::fast_exp(mr - mn);
-            const float b = pk::fast_exp(mk[i] - mn);
-            acc = acc * a + ok[i] * b;
-            lr = lr * a + lk[i] * b;
-            mr = mn;
+            const float e = pk::fast_exp(mk[i] - mx);
+            const float b = (k0 + i < kEnd && mk[i] != -INFINITY) ? e : 0.0f;
+            acc += ok[i] * b;
+            lr += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lv), i)) * b;
         }
+        mr = mx;
     }
     if (lane == 0) {
         sm_m[wave] = mr;
