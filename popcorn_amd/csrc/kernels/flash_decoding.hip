@@ -39,8 +39,8 @@ struct FdGeom {
 };
 
 __device__ inline bool fd_allowed(const FlashDecodingPartialConstants &p, int posQ, int posK) {
-    bool allowed = (p.maskKind == 2u) || (posK <= posQ);
-    if (p.maskKind == 1u) allowed = allowed && ((posQ - posK) < p.slidingWindow);
+    bool allowed = (p.maskKind == 2u) | (posK <= posQ);
+    if (p.maskKind == 1u) allowed = allowed & ((posQ - posK) < p.slidingWindow);
     return allowed;
 }
 
@@ -155,7 +155,7 @@ __device__ void fd_partial_fast(const typename T::storage *__restrict__ Q, const
     __shared__ float sm_ss[kUnits];
 
     const FdGeom geo = fd_geometry(p, position, GMAX, FRESH);
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t kg = lane / LPK, dl = lane % LPK;
     const uint32_t G = p.Nq / p.Nkv;
     const uint32_t stride = p.kvStride ? p.kvStride : p.Sk;
@@ -244,6 +244,7 @@ __device__ void fd_partial_fast(const typename T::storage *__restrict__ Q, const
     }
 
     float q[GMAX][DL], o[GMAX][DL], m[GMAX], l[GMAX];
+    pk::Vec<T> qv[GMAX][CPL];  // the query rows as loaded (converted in the key loop)
 #pragma unroll
     for (int g = 0; g < GMAX; ++g) {
         m[g] = -INFINITY;
@@ -263,13 +264,9 @@ __device__ void fd_partial_fast(const typename T::storage *__restrict__ Q, const
             const typename T::storage *qrow = Q + ((uint64_t)(geo.b * p.Nq + hq) * geo.Sq + geo.qi) * HD;
 #pragma unroll
             for (int c = 0; c < CPL; ++c) {
-                pk::Vec<T> v;
-                v.load(qrow + (c * LPK + dl) * kV);
+                qv[g][c].load(qrow + (c * LPK + dl) * kV);
 #pragma unroll
-                for (int e = 0; e < kV; ++e) {
-                    q[g][c * kV + e] = v.get(e) * p.scale;
-                    o[g][c * kV + e] = 0.0f;
-                }
+                for (int e = 0; e < kV; ++e) o[g][c * kV + e] = 0.0f;
             }
         }
     }
@@ -286,13 +283,30 @@ __device__ void fd_partial_fast(const typename T::storage *__restrict__ Q, const
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const uint32_t j = j0 + u * KPW + kg;
-            valid[u] = j < geo.jHi && fd_allowed(p, (int)geo.posQ, (int)j);
+            valid[u] = (j < geo.jHi) & fd_allowed(p, (int)geo.posQ, (int)j);
             const uint32_t jj = j < geo.jHi ? j : geo.jLo;
 #pragma unroll
             for (int c = 0; c < CPL; ++c) {
                 kv[u][c].load_nt(Kh + (uint64_t)jj * HD + (c * LPK + dl) * kV);
                 vv[u][c].load_nt(Vh + (uint64_t)jj * HD + (c * LPK + dl) * kV);
             }
+        }
+        if constexpr (!FRESH) {
+            __builtin_amdgcn_sched_barrier(0);  // every K/V load above issues first
+            // The query rows are converted here, after this tile's K and V
+            // loads are issued, so their round trip overlaps the keys'
+            // (converted before the loop, they made every K/V load wait for
+            // them). The empty volatile asm keeps the conversion from being
+            // hoisted out of the loop and is a scheduling boundary.
+#pragma unroll
+            for (int g = 0; g < GMAX; ++g)
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) {
+                    pk::Vec<T> t = qv[g][c];
+                    asm volatile("" : "+v"(t.raw));
+#pragma unroll
+                    for (int e = 0; e < kV; ++e) q[g][c * kV + e] = t.get(e) * p.scale;
+                }
         }
         float s[GMAX][U];
 #pragma unroll
