@@ -87,11 +87,24 @@ POPCORN_KERNEL void __launch_bounds__(256)
     const float *xr = x + (uint64_t)row * p.N;
     float bv = -INFINITY;
     int32_t bi = 0x7fffffff;
-    for (uint64_t i = lo + threadIdx.x; i < hi; i += blockDim.x) {
-        float v = xr[i];
-        if (better(v, (int32_t)i, bv, bi)) {
-            bv = v;
-            bi = (int32_t)i;
+    // kArgmaxBatch loads per thread in flight together (a decode-sized slice
+    // of 4096 is one memory round trip); entries past the slice re-read its
+    // last element and are masked. better() is a total order on (value,
+    // index), so the visiting order does not change the result.
+    constexpr int kArgmaxBatch = 16;
+    if (lo < hi) {
+        for (uint64_t i0 = lo + threadIdx.x; i0 < hi; i0 += (uint64_t)blockDim.x * kArgmaxBatch) {
+            float v[kArgmaxBatch];
+#pragma unroll
+            for (int b = 0; b < kArgmaxBatch; ++b) v[b] = xr[min(i0 + (uint64_t)b * blockDim.x, hi - 1)];
+#pragma unroll
+            for (int b = 0; b < kArgmaxBatch; ++b) {
+                const uint64_t i = i0 + (uint64_t)b * blockDim.x;
+                if (i < hi && better(v[b], (int32_t)i, bv, bi)) {
+                    bv = v[b];
+                    bi = (int32_t)i;
+                }
+            }
         }
     }
     block_best(bv, bi);

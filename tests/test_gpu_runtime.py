@@ -114,12 +114,16 @@ def test_embedding_gather_bf16_rows(env):
     assert not got[4].any()
 
 
-@pytest.mark.parametrize("N", [1, 5, 31, 4096, 256000, 300001])
+@pytest.mark.parametrize("N", [1, 5, 31, 4096, 256000, 300001, 2000003])
 def test_argmax_vs_oracle(env, N):
     pa, lib, stream, enc = env
     x = O.normal(N, (3, N))
     if N > 5:
         x[1, N // 2] = x[1, N // 3] = x[1].max() + 1.0  # tie: the first index wins (Argmax.metal:7-9)
+    if N > 4101:
+        # a tie between two loads of one thread (4096 apart: consecutive
+        # batches of its 16 loads when a slice is over 4096 long)
+        x[2, 5] = x[2, 4101] = x[2].max() + 1.0
     idx = pa.Tensor.empty([3], "i32")
     enc.encode(pa.Kernels.Argmax(pa.Tensor.from_numpy(x), idx))
     stream.synchronize()
