@@ -40,7 +40,7 @@ def kernel_bytes(cfg, name, pos):
     QKV = QW + 2 * KW
     if name.startswith("gated_mlp_gate_up"):  # residual + norm, Wg and Wu, h
         return 2 * F * H * 2 + 3 * H * 2 + 2 * H * 4 + F * 2
-    if name == "matvec_nk_simd_bf16_bf16_bf16_r1":  # down projection (K = F)
+    if name == "matvec_nk_stream_bf16_bf16_bf16_r1":  # down projection (K = F)
         return H * F * 2 + F * 2 + H * 2
     if name in ("decode_matvec_bf16_bf16_r1_f2", "decode_matvec_bf16_bf16_r1_f3"):  # QKV (+ residual), norm, KV scatter
         return QKV * H * 2 + 3 * H * 2 + 2 * H * 4 + QKV * 2

@@ -72,7 +72,10 @@ popcorn_status_t popcorn_decoder_randomize(popcorn_decoder_t decoder, uint64_t s
  * "norm_post_ffn", "k_cache", "v_cache" and, with attention_block, "q_norm"
  * and "k_norm" (per `layer`); "inv_freq" (attention_block), "x", "logits",
  * "token", "position", "history", plus the last layer's step buffers
- * "q", "qkv", "attn", "o", "mlp", "hidden". With weight_bits 4 a weight name
+ * "q", "qkv", "attn", "o", "mlp", "hidden" and "x2" (the residual stream
+ * the last layer's MLP and the head read: after a step it holds the stream
+ * after the last attention block, while "x" holds the next step's input
+ * row). With weight_bits 4 a weight name
  * ("embedding", "w_qkv", ...) is its packed u32 values [N, K/8], and
  * "<name>.scales" / "<name>.biases" its bf16 [N, K/64] groups. */
 popcorn_status_t popcorn_decoder_tensor(popcorn_decoder_t decoder, const char *name, int32_t layer,
@@ -84,7 +87,10 @@ popcorn_status_t popcorn_decoder_reset(popcorn_decoder_t decoder, int32_t token,
 /* Enqueues `steps` decode steps on the decoder's stream (no host sync):
  * through captured graphs when use_graph != 0, else dispatch by dispatch.
  * The first step starts from the token and position in device memory (its
- * input row is gathered first); "logits" then holds the last step's. */
+ * input row is gathered first); "logits" then holds the last step's. Steps
+ * that would decode at a position >= max_seq (write past the KV cache) are
+ * refused with -1007 (tensorShapeMismatch) before anything is enqueued; the
+ * position is tracked on the host from reset and read. */
 popcorn_status_t popcorn_decoder_step(popcorn_decoder_t decoder, int32_t steps, int32_t use_graph);
 
 /* Waits for the stream, then reads the current token and position. */
@@ -102,7 +108,8 @@ int64_t popcorn_decoder_step_bytes(popcorn_decoder_t decoder, int32_t position);
  * whose function is `function_name` (one per layer, say) is launched back to
  * back `reps` times between two events on the decoder's stream, all other
  * dispatches skipped. Reports the mean duration per launch and the number of
- * launches timed. State other than those kernels' outputs is unchanged. */
+ * launches timed. State other than those kernels' outputs is unchanged; the
+ * token and position are restored afterwards. */
 popcorn_status_t popcorn_decoder_time_kernel(popcorn_decoder_t decoder, const char *function_name, int32_t reps,
                                              float *mean_ms, int32_t *launches);
 

@@ -190,10 +190,35 @@ popcorn_status_t popcorn_function_attributes(popcorn_function_t function,
 /* Number of functions found so far (the pipeline-state cache size). */
 int32_t popcorn_library_cached_function_count(popcorn_library_t library);
 
+/* A kernel's parameter list as its code object's metadata states it: the
+ * leading device pointers, then the by-value constants blocks (no
+ * counterpart in the reference, where Metal reflects it; the checks below
+ * use it). */
+#define POPCORN_MAX_CONSTANT_BLOCKS 8
+typedef struct {
+    int32_t nbuffers;       /* leading device-pointer parameters */
+    int32_t nconstants;     /* parameters after them */
+    uint32_t constant_sizes[POPCORN_MAX_CONSTANT_BLOCKS]; /* bytes; 8 for a pointer
+                                                      among them (trailing_pointers) */
+    int32_t trailing_pointers; /* pointers after the first constants block (0 here) */
+    uint32_t max_threads_per_block;
+} popcorn_kernel_layout_t;
+
+popcorn_status_t popcorn_function_layout(popcorn_function_t function, popcorn_kernel_layout_t *layout);
+/* The same read from a code-object file without a GPU (-1006 if the file
+ * holds no kernel of that name, -1100 for an unreadable file). */
+popcorn_status_t popcorn_code_object_layout(const char *path, const char *kernel, popcorn_kernel_layout_t *layout);
+
 /* Raw launch (replaces setBuffer/setBytes/dispatchThreads,
  * KernelCommandEncoder.swift:193-208): the kernel's parameters are the
  * `nbuffers` device pointers in order, then each constants block by value.
- * grid and block are in blocks and threads (not threads and threads). */
+ * grid and block are in blocks and threads (not threads and threads).
+ * The launch must bind exactly the kernel's parameter list (pointer count
+ * and each block's size, popcorn_function_layout) and at most its block
+ * size, else -1100 (invalidArgument) and nothing runs. Kernels under the
+ * reference's host names take the reference's parameter list and compute
+ * the reference's result under its launch geometry (threads converted to
+ * blocks). */
 popcorn_status_t popcorn_launch(popcorn_stream_t stream, popcorn_function_t function,
                                 const uint32_t grid[3], const uint32_t block[3],
                                 void *const *buffers, int32_t nbuffers,

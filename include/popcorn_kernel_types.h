@@ -2,12 +2,15 @@
  * popcorn_kernel_types.h — kernel parameter blocks shared by the host runtime
  * and the gfx950 kernels.
  *
- * Each struct keeps the field order of its counterpart in the reference's
- * Sources/PopcornShaderTypes/PopcornKernelTypes.h (cited per struct), so a
- * caller that packs the reference's constants packs these. Fields this build
- * adds sit after the reference's fields and default to the reference's
- * behaviour when zero. Fields are 4 bytes (FillNormalConstants' counters are
- * 8); none of the structs has padding.
+ * A struct named as in the reference's
+ * Sources/PopcornShaderTypes/PopcornKernelTypes.h (cited per struct) has
+ * exactly the reference's fields in the reference's order, and the kernels
+ * exported under the reference's host names take exactly it, so a caller
+ * that packs the reference's constants for a raw launch packs these. Where a
+ * kernel of this build needs more, it takes a struct of its own (suffix Ext,
+ * or a name of its own): the reference's fields first, then the additions.
+ * Fields are 4 bytes (FillNormalConstants' counters are 8); none of the
+ * structs has padding.
  */
 #ifndef POPCORN_KERNEL_TYPES_H
 #define POPCORN_KERNEL_TYPES_H
@@ -18,13 +21,20 @@
 extern "C" {
 #endif
 
-/* PopcornKernelTypes.h:10-13, plus V (table rows; 0 = unchecked): an id
- * outside [0, V) yields a zero row instead of an out-of-bounds read. */
+/* PopcornKernelTypes.h:10-13 */
+typedef struct {
+    uint32_t N;
+    uint32_t H;
+} EmbeddingGatherConstants;
+
+/* EmbeddingGatherConstants plus V (table rows; 0 = unchecked): an id outside
+ * [0, V) yields a zero row instead of an out-of-bounds read
+ * (embedding_gather*_ext). */
 typedef struct {
     uint32_t N;
     uint32_t H;
     uint32_t V;
-} EmbeddingGatherConstants;
+} EmbeddingGatherExtConstants;
 
 /* PopcornKernelTypes.h:15-18 */
 typedef struct {
@@ -70,13 +80,7 @@ typedef struct {
     float eps;
 } RMSNormConstants;
 
-/* PopcornKernelTypes.h:121-131, plus:
- *   kvStride       rows between consecutive KV heads in K/V (0 = Sk), so a
- *                  cache with spare capacity [B, Nkv, Smax, Hd] is read in
- *                  place;
- *   P              key partitions per query row (0 = 1);
- *   keyLenFromPosition  when 1, Sk = position[0] + Sq is read from the bound
- *                  position tensor (decode under graph replay).           */
+/* PopcornKernelTypes.h:121-131 */
 typedef struct {
     uint32_t B;
     uint32_t Nq;
@@ -87,16 +91,30 @@ typedef struct {
     uint32_t maskKind;
     int32_t slidingWindow;
     float scale;
-    uint32_t kvStride;
-    uint32_t P;
-    uint32_t keyLenFromPosition;
 } FlashAttentionConstants;
 
-/* PopcornKernelTypes.h:133-144 (the reference's MPP tile constants; here the
- * MFMA prefill kernel's), plus kvStride as above and splitFrom: query tiles
- * qt >= splitFrom run as two blocks over the two halves of their key steps,
- * which write partial (O, m, l) for the split-merge kernel
- * (splitFrom == qTilesPerHead: no split). */
+/* PopcornKernelTypes.h:133-144 (the reference's MPP kernels have no
+ * counterpart here; kept for callers that pack it). */
+typedef struct {
+    uint32_t B;
+    uint32_t Nq;
+    uint32_t Nkv;
+    uint32_t Sq;
+    uint32_t Sk;
+    uint32_t Hd;
+    uint32_t qTilesPerHead;
+    uint32_t maskKind;
+    int32_t slidingWindow;
+    float scale;
+} MPPFlashAttentionConstants;
+
+/* The MFMA prefill kernel's constants (flash_attention_tiled_*, the kernel
+ * in the MPP route's place): MPPFlashAttentionConstants' fields, plus
+ *   kvStride   rows between consecutive KV heads in K/V (0 = Sk);
+ *   splitFrom  query tiles qt >= splitFrom run as two blocks over the two
+ *              halves of their key steps, which write partial (O, m, l) for
+ *              the split-merge kernel; splitFrom >= qTilesPerHead splits
+ *              nothing. */
 typedef struct {
     uint32_t B;
     uint32_t Nq;
@@ -110,10 +128,29 @@ typedef struct {
     float scale;
     uint32_t kvStride;
     uint32_t splitFrom;
-} MPPFlashAttentionConstants;
+} TiledFlashAttentionConstants;
 
-/* PopcornKernelTypes.h:146-156, plus kvStride, Sq (query rows; 0 = 1) and
- * keyLenFromPosition as in FlashAttentionConstants. */
+/* PopcornKernelTypes.h:146-156 */
+typedef struct {
+    uint32_t B;
+    uint32_t Nq;
+    uint32_t Nkv;
+    uint32_t Sk;
+    uint32_t Hd;
+    uint32_t P;
+    uint32_t maskKind;
+    int32_t slidingWindow;
+    float scale;
+} FlashDecodingPartialConstants;
+
+/* FlashDecodingPartialConstants plus (flash_decoding_partial_*_ext, the fast
+ * flash_decoding_partial_<t>_l*_c*_g* and flash_decoding_fresh_* kernels):
+ *   kvStride       rows between consecutive KV heads in K/V (0 = Sk), so a
+ *                  cache with spare capacity [B, Nkv, Smax, Hd] is read in
+ *                  place;
+ *   Sq             query rows (0 = 1); row r attends as position Sk - Sq + r;
+ *   keyLenFromPosition  when 1, Sk = position[0] + Sq is read from the bound
+ *                  position tensor (decode under graph replay). */
 typedef struct {
     uint32_t B;
     uint32_t Nq;
@@ -127,7 +164,7 @@ typedef struct {
     uint32_t kvStride;
     uint32_t Sq;
     uint32_t keyLenFromPosition;
-} FlashDecodingPartialConstants;
+} FlashDecodingPartialExtConstants;
 
 /* No counterpart in the reference: the attention block of one decode token
  * with the per-head glue folded into the split-KV partial kernel
@@ -149,17 +186,37 @@ typedef struct {
     uint32_t rowStride;
 } DecodeAttentionConstants;
 
-/* PopcornKernelTypes.h:158-163, plus Sq (0 = 1). */
+/* PopcornKernelTypes.h:158-163 */
+typedef struct {
+    uint32_t B;
+    uint32_t Nq;
+    uint32_t Hd;
+    uint32_t P;
+} FlashDecodingReduceConstants;
+
+/* FlashDecodingReduceConstants plus Sq (query rows; 0 = 1)
+ * (flash_decoding_reduce_*_ext). */
 typedef struct {
     uint32_t B;
     uint32_t Nq;
     uint32_t Hd;
     uint32_t P;
     uint32_t Sq;
-} FlashDecodingReduceConstants;
+} FlashDecodingReduceExtConstants;
 
-/* PopcornKernelTypes.h:165-172, plus offsetFromPosition: when 1 the write
- * offset is read from the bound position tensor. */
+/* PopcornKernelTypes.h:165-172 */
+typedef struct {
+    uint32_t B;
+    uint32_t Nkv;
+    uint32_t Snew;
+    uint32_t Smax;
+    uint32_t Hd;
+    uint32_t offset;
+} KVCacheWriteConstants;
+
+/* KVCacheWriteConstants plus offsetFromPosition (kv_cache_write*_ext): when 1
+ * the write offset is read from the bound position tensor, and a range that
+ * would leave the cache writes nothing. */
 typedef struct {
     uint32_t B;
     uint32_t Nkv;
@@ -168,7 +225,7 @@ typedef struct {
     uint32_t Hd;
     uint32_t offset;
     uint32_t offsetFromPosition;
-} KVCacheWriteConstants;
+} KVCacheWriteExtConstants;
 
 /* PopcornKernelTypes.h:174-178: RoPE tables for T positions and Hd2 = Hd/2
  * frequencies, both scaled by `scaling`. */
@@ -206,9 +263,18 @@ typedef struct {
     uint32_t hasBias;
 } AffineQMatmulConstants;
 
-/* PopcornKernelTypes.h:249-255: out[T, H] = dequantize(table[ids[t], :]),
- * plus V (table rows; 0 = unchecked): an id outside [0, V) yields a zero row
- * instead of an out-of-bounds read. */
+/* PopcornKernelTypes.h:249-255: out[T, H] = dequantize(table[ids[t], :]). */
+typedef struct {
+    uint32_t T;
+    uint32_t H;
+    uint32_t kGroups;
+    uint32_t wordsPerRow;
+    uint32_t hasBias;
+} AffineQEmbeddingGatherConstants;
+
+/* AffineQEmbeddingGatherConstants plus V (table rows; 0 = unchecked): an id
+ * outside [0, V) yields a zero row instead of an out-of-bounds read
+ * (aq_embedding_gather_*_ext). */
 typedef struct {
     uint32_t T;
     uint32_t H;
@@ -216,15 +282,21 @@ typedef struct {
     uint32_t wordsPerRow;
     uint32_t hasBias;
     uint32_t V;
-} AffineQEmbeddingGatherConstants;
+} AffineQEmbeddingGatherExtConstants;
 
-/* PopcornKernelTypes.h:197-200, plus slices: the number of row slices the
- * two-stage argmax splits each row into (stage 1 grid width). */
+/* PopcornKernelTypes.h:197-200 */
+typedef struct {
+    uint32_t rows;
+    uint32_t N;
+} ArgmaxConstants;
+
+/* ArgmaxConstants plus slices: the number of row slices this build's
+ * two-stage argmax (argmax_partial, argmax_finish) splits each row into. */
 typedef struct {
     uint32_t rows;
     uint32_t N;
     uint32_t slices;
-} ArgmaxConstants;
+} ArgmaxSliceConstants;
 
 /* No counterpart in the reference: the fused gated-MLP front half
  * (RMSNorm -> gate and up matvecs -> GELU-tanh(gate) * up), which replaces the

@@ -25,6 +25,7 @@ from .runtime import (  # noqa: F401
     device_count,
     device_info,
     lib,
+    code_object_layout,
     scratch_spec_byte_count,
     stride,
     synchronize,

@@ -56,6 +56,11 @@ class FunctionAttrs(C.Structure):
                 ("private_bytes", C.c_int32)]
 
 
+class KernelLayout(C.Structure):
+    _fields_ = [("nbuffers", C.c_int32), ("nconstants", C.c_int32), ("constant_sizes", C.c_uint32 * 8),
+                ("trailing_pointers", C.c_int32), ("max_threads_per_block", C.c_uint32)]
+
+
 class EncoderStats(C.Structure):
     _fields_ = [("dispatches", C.c_int64), ("hazards", C.c_int64), ("scratch_borrows", C.c_int64)]
 
@@ -124,6 +129,8 @@ PROTOTYPES = {
     "popcorn_library_destroy": (_st, [C.c_void_p]),
     "popcorn_library_function": (_st, [C.c_void_p, C.c_char_p, C.POINTER(C.c_void_p)]),
     "popcorn_function_attributes": (_st, [C.c_void_p, C.POINTER(FunctionAttrs)]),
+    "popcorn_function_layout": (_st, [C.c_void_p, C.POINTER(KernelLayout)]),
+    "popcorn_code_object_layout": (_st, [C.c_char_p, C.c_char_p, C.POINTER(KernelLayout)]),
     "popcorn_library_cached_function_count": (C.c_int32, [C.c_void_p]),
     "popcorn_launch": (_st, [C.c_void_p, C.c_void_p, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32),
                              C.POINTER(C.c_void_p), C.c_int32, C.POINTER(C.c_void_p), C.POINTER(C.c_size_t),

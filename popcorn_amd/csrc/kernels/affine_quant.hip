@@ -88,11 +88,11 @@ __device__ void aq_matvec(const uint32_t *__restrict__ W, const uint16_t *__rest
 }
 
 // AffineQuantizedEmbeddingGather.metal:16-26, one thread per packed word (8
-// values of one group) of one token.
+// values of one group) of one token (aq_embedding_gather_*_ext).
 template <typename O>
 __device__ void aq_gather(const int32_t *__restrict__ ids, const uint32_t *__restrict__ W, const uint16_t *__restrict__ Sc,
                           const uint16_t *__restrict__ Bi, typename O::storage *__restrict__ out,
-                          const AffineQEmbeddingGatherConstants &p) {
+                          const AffineQEmbeddingGatherExtConstants &p) {
     const uint64_t words = (uint64_t)p.T * p.wordsPerRow;
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < words; i += (uint64_t)gridDim.x * blockDim.x) {
         const uint32_t t = (uint32_t)(i / p.wordsPerRow), wi = (uint32_t)(i % p.wordsPerRow);
@@ -112,35 +112,103 @@ __device__ void aq_gather(const int32_t *__restrict__ ids, const uint32_t *__res
     }
 }
 
-// Any alignment and any M (Matmul.swift:321-331 geometry, reworked for wave64):
-// one wave per 4 rows of one x row, lanes strided over K, the form of
-// AffineQuantizedMatmul.metal:34-58.
+// The reference's launch of the gather (EmbeddingGather.swift:90, :117-118):
+// the thread at (x, y) writes value y of token x's row; the grid strides in
+// both dimensions.
+template <typename O>
+__device__ void aq_gather_ref(const int32_t *__restrict__ ids, const uint32_t *__restrict__ W,
+                              const uint16_t *__restrict__ Sc, const uint16_t *__restrict__ Bi,
+                              typename O::storage *__restrict__ out, const AffineQEmbeddingGatherConstants &p) {
+    const uint32_t sx = gridDim.x * blockDim.x, sy = gridDim.y * blockDim.y;
+    for (uint32_t n = blockIdx.x * blockDim.x + threadIdx.x; n < p.T; n += sx) {
+        const uint64_t row = (uint32_t)ids[n];
+        for (uint32_t h = blockIdx.y * blockDim.y + threadIdx.y; h < p.H; h += sy) {
+            const uint32_t g = h / kQ4Group;
+            const float s = pk::bf16_lo(Sc[row * p.kGroups + g]);
+            const float b = p.hasBias ? pk::bf16_lo(Bi[row * p.kGroups + g]) : 0.0f;
+            const uint32_t q = (W[row * p.wordsPerRow + h / 8] >> (4 * (h % 8))) & 15u;
+            out[(uint64_t)n * p.H + h] = O::store((float)q * s + b);
+        }
+    }
+}
+
+// Any alignment and any M: the reference's aq_matvec_simd4 launch
+// (Matmul.swift:321-331: threads ceil(N / 4) * 32 by M): the 32-lane
+// half-wave u of grid row m computes rows 4u .. 4u + 3 of x row m, its lanes
+// strided over K (AffineQuantizedMatmul.metal:34-58). The Matmul descriptor
+// takes it for shapes the fast kernels do not; the block size must be a
+// multiple of 32.
 template <typename X, typename O>
 __device__ void aq_matvec_any(const uint32_t *__restrict__ W, const uint16_t *__restrict__ Sc,
                               const uint16_t *__restrict__ Bi, const typename X::storage *__restrict__ x,
                               typename O::storage *__restrict__ y, const AffineQMatmulConstants &p) {
     constexpr uint32_t kR = 4;
-    const uint32_t lane = threadIdx.x & 63;
-    const uint32_t row0 = (blockIdx.x * pk::kStreamWaves + (threadIdx.x >> 6)) * kR;
-    const uint32_t m = blockIdx.y;
-    if (row0 >= p.N) return;
-    const typename X::storage *xr = x + (uint64_t)m * p.K;
-    float acc[kR] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (uint32_t k = lane; k < p.K; k += 64) {
-        const float xv = X::load(xr[k]);
-        const uint32_t g = k / kQ4Group;
+    const uint32_t lane = threadIdx.x & 31;
+    const uint64_t row0 = (((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 5) * kR;
+    if (row0 >= p.N) return;  // uniform over the half-wave
+    for (uint32_t m = blockIdx.y * blockDim.y + threadIdx.y; m < p.M; m += gridDim.y * blockDim.y) {
+        const typename X::storage *xr = x + (uint64_t)m * p.K;
+        float acc[kR] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (uint32_t k = lane; k < p.K; k += 32) {
+            const float xv = X::load(xr[k]);
+            const uint32_t g = k / kQ4Group;
+#pragma unroll
+            for (uint32_t r = 0; r < kR; ++r) {
+                const uint64_t row = min(row0 + r, (uint64_t)p.N - 1);
+                const float s = pk::bf16_lo(Sc[row * p.kGroups + g]);
+                const float b = p.hasBias ? pk::bf16_lo(Bi[row * p.kGroups + g]) : 0.0f;
+                const uint32_t q = (W[row * p.wordsPerRow + k / 8] >> (4 * (k % 8))) & 15u;
+                acc[r] += xv * ((float)q * s + b);
+            }
+        }
 #pragma unroll
         for (uint32_t r = 0; r < kR; ++r) {
-            const uint64_t row = min(row0 + r, p.N - 1);
+            const float sum = pk::half32_sum(acc[r]);
+            if (lane == 0 && row0 + r < p.N) y[(uint64_t)m * p.N + row0 + r] = O::store(sum);
+        }
+    }
+}
+
+// The reference's aq_qmv_fast launch (Matmul.swift:311-320: threadgroups of
+// 64 threads, grid M by ceil(N / 8)): threadgroup (m, t), half-wave h < 2
+// computes rows 8t + 4h .. + 3 of x row m; each lane takes 16 consecutive
+// values of every 512 and sums s * sum(x q) + b * sum(x) per group
+// (AffineQuantizedMatmul.metal:84-160). K is a multiple of 64.
+template <typename X, typename O>
+__device__ void aq_qmv_ref(const uint32_t *__restrict__ W, const uint16_t *__restrict__ Sc, const uint16_t *__restrict__ Bi,
+                           const typename X::storage *__restrict__ x, typename O::storage *__restrict__ y,
+                           const AffineQMatmulConstants &p) {
+    constexpr uint32_t kR = 4, kPerLane = 16;
+    const uint32_t half = threadIdx.x >> 5, lane = threadIdx.x & 31;
+    const uint32_t m = blockIdx.x;
+    const uint64_t row0 = (uint64_t)blockIdx.y * 8 + half * kR;
+    if (half >= 2 || m >= p.M || row0 >= p.N) return;  // uniform over the half-wave
+    float acc[kR] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t k0 = lane * kPerLane; k0 < p.K; k0 += 32 * kPerLane) {
+        float xv[kPerLane], sx = 0.0f;
+#pragma unroll
+        for (uint32_t j = 0; j < kPerLane; ++j) {
+            xv[j] = X::load(x[(uint64_t)m * p.K + k0 + j]);
+            sx += xv[j];
+        }
+        const uint32_t g = k0 / kQ4Group;
+#pragma unroll
+        for (uint32_t r = 0; r < kR; ++r) {
+            const uint64_t row = min(row0 + r, (uint64_t)p.N - 1);
             const float s = pk::bf16_lo(Sc[row * p.kGroups + g]);
             const float b = p.hasBias ? pk::bf16_lo(Bi[row * p.kGroups + g]) : 0.0f;
-            const uint32_t q = (W[row * p.wordsPerRow + k / 8] >> (4 * (k % 8))) & 15u;
-            acc[r] += xv * ((float)q * s + b);
+            float qdot = 0.0f;
+#pragma unroll
+            for (uint32_t j = 0; j < kPerLane; ++j) {
+                const uint32_t w = W[row * p.wordsPerRow + (k0 + j) / 8];
+                qdot += xv[j] * (float)((w >> (4 * ((k0 + j) % 8))) & 15u);
+            }
+            acc[r] += s * qdot + b * sx;
         }
     }
 #pragma unroll
     for (uint32_t r = 0; r < kR; ++r) {
-        const float sum = pk::wave_sum(acc[r]);
+        const float sum = pk::half32_sum(acc[r]);
         if (lane == 0 && row0 + r < p.N) y[(uint64_t)m * p.N + row0 + r] = O::store(sum);
     }
 }
@@ -324,24 +392,35 @@ Q4_ALL(32)
 AQ_MV_ALL(aq_qmv_fast)
 AQ_MV_ALL(aq_matvec_simd4)
 
+// The reference's host names on the reference's launch geometry.
 #define AQ_ANY(xt, ot, X, O)                                                                                  \
-    POPCORN_KERNEL void __launch_bounds__(256) aq_matvec_simd4_##xt##_bf16_##ot##_b4_g64(                          \
+    POPCORN_KERNEL void __launch_bounds__(1024) aq_matvec_simd4_##xt##_bf16_##ot##_b4_g64(                         \
         const uint32_t *W, const uint16_t *S, const uint16_t *B, const X::storage *x, O::storage *y,            \
         AffineQMatmulConstants p) {                                                                            \
         aq_matvec_any<X, O>(W, S, B, x, y, p);                                                                 \
+    }                                                                                                          \
+    POPCORN_KERNEL void __launch_bounds__(1024) aq_qmv_fast_##xt##_bf16_##ot##_b4_g64(                             \
+        const uint32_t *W, const uint16_t *S, const uint16_t *B, const X::storage *x, O::storage *y,            \
+        AffineQMatmulConstants p) {                                                                            \
+        aq_qmv_ref<X, O>(W, S, B, x, y, p);                                                                    \
     }
 AQ_ANY(bf16, bf16, BF16, BF16)
 AQ_ANY(bf16, f32, BF16, F32)
 AQ_ANY(f32, f32, F32, F32)
 
-// EmbeddingGather.swift:80 (AffineQuantizedEmbeddingGather.metal:29-30)
-POPCORN_KERNEL void __launch_bounds__(256)
-    aq_embedding_gather_bf16_bf16_b4_g64(const int32_t *ids, const uint32_t *W, const uint16_t *S, const uint16_t *B,
-                                         uint16_t *out, AffineQEmbeddingGatherConstants p) {
-    aq_gather<BF16>(ids, W, S, B, out, p);
-}
-POPCORN_KERNEL void __launch_bounds__(256)
-    aq_embedding_gather_bf16_f32_b4_g64(const int32_t *ids, const uint32_t *W, const uint16_t *S, const uint16_t *B,
-                                        float *out, AffineQEmbeddingGatherConstants p) {
-    aq_gather<F32>(ids, W, S, B, out, p);
-}
+// EmbeddingGather.swift:80 (AffineQuantizedEmbeddingGather.metal:29-30): the
+// reference's names on its parameter list and launch, and the _ext forms
+// the descriptor runs.
+#define AQ_GATHER(ot, O)                                                                                          \
+    POPCORN_KERNEL void __launch_bounds__(1024) aq_embedding_gather_bf16_##ot##_b4_g64(                          \
+        const int32_t *ids, const uint32_t *W, const uint16_t *S, const uint16_t *B, O::storage *out,           \
+        AffineQEmbeddingGatherConstants p) {                                                                    \
+        aq_gather_ref<O>(ids, W, S, B, out, p);                                                                 \
+    }                                                                                                           \
+    POPCORN_KERNEL void __launch_bounds__(256) aq_embedding_gather_bf16_##ot##_b4_g64_ext(                       \
+        const int32_t *ids, const uint32_t *W, const uint16_t *S, const uint16_t *B, O::storage *out,           \
+        AffineQEmbeddingGatherExtConstants p) {                                                                 \
+        aq_gather<O>(ids, W, S, B, out, p);                                                                     \
+    }
+AQ_GATHER(bf16, BF16)
+AQ_GATHER(f32, F32)

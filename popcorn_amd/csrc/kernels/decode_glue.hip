@@ -6,11 +6,30 @@
 
 namespace {
 
-// EmbeddingGather.metal:6-23: out[n, :] = table[ids[n], :]; one thread per
-// 16-byte run of a row. An id outside [0, V) (when V is given) gives zeros.
+// EmbeddingGather.metal:6-23: out[n, :] = table[ids[n], :].
+// embedding_gather*_ext (the descriptor's): one thread per 16-byte run of a
+// row; an id outside [0, V) (when V is given) gives zeros.
+// embedding_gather* keep the reference's host names, parameter list and
+// launch geometry (EmbeddingGather.swift:26, :117-118): the thread at (x, y)
+// copies elements 4y .. 4y + 3 of token x's row; the grid strides in both
+// dimensions, so any launch shape covers the rows.
+template <typename T, typename O>
+__device__ void gather_ref(const int32_t *__restrict__ ids, const typename T::storage *__restrict__ table,
+                           typename O::storage *__restrict__ out, const EmbeddingGatherConstants &p) {
+    const uint32_t chunks = (p.H + 3) / 4;
+    const uint32_t sx = gridDim.x * blockDim.x, sy = gridDim.y * blockDim.y;
+    for (uint32_t n = blockIdx.x * blockDim.x + threadIdx.x; n < p.N; n += sx) {
+        const uint64_t row = (uint32_t)ids[n];
+        for (uint32_t c = blockIdx.y * blockDim.y + threadIdx.y; c < chunks; c += sy) {
+            for (uint32_t h = 4 * c; h < 4 * c + 4 && h < p.H; ++h)
+                out[(uint64_t)n * p.H + h] = O::store(T::load(table[row * p.H + h]));
+        }
+    }
+}
+
 template <typename T, typename O>
 __device__ void gather(const int32_t *__restrict__ ids, const typename T::storage *__restrict__ table,
-                       typename O::storage *__restrict__ out, const EmbeddingGatherConstants &p) {
+                       typename O::storage *__restrict__ out, const EmbeddingGatherExtConstants &p) {
     constexpr uint32_t kRun = 16 / sizeof(typename T::storage);
     const uint32_t runs = (p.H + kRun - 1) / kRun;
     const uint64_t total = (uint64_t)p.N * runs;
@@ -61,10 +80,14 @@ __device__ void block_best(float &bv, int32_t &bi) {
 
 }  // namespace
 
-#define GATHER(name, T, O)                                                                                \
-    POPCORN_KERNEL void __launch_bounds__(256)                                                            \
-        name(const int32_t *ids, const T::storage *table, O::storage *out, EmbeddingGatherConstants p) {  \
-        gather<T, O>(ids, table, out, p);                                                                 \
+#define GATHER(name, T, O)                                                                                   \
+    POPCORN_KERNEL void __launch_bounds__(1024)                                                              \
+        name(const int32_t *ids, const T::storage *table, O::storage *out, EmbeddingGatherConstants p) {     \
+        gather_ref<T, O>(ids, table, out, p);                                                                \
+    }                                                                                                        \
+    POPCORN_KERNEL void __launch_bounds__(256)                                                               \
+        name##_ext(const int32_t *ids, const T::storage *table, O::storage *out, EmbeddingGatherExtConstants p) { \
+        gather<T, O>(ids, table, out, p);                                                                    \
     }
 
 using pk::BF16;
@@ -80,7 +103,7 @@ GATHER(embedding_gather_bf16_to_f32, BF16, F32)
 // Grid: x = slices, y = rows. A NaN never wins (v > best is false for NaN),
 // as in the reference's sequential loop when the first element is not NaN.
 POPCORN_KERNEL void __launch_bounds__(256)
-    argmax_partial(const float *x, float *pv, int32_t *pi, ArgmaxConstants p) {
+    argmax_partial(const float *x, float *pv, int32_t *pi, ArgmaxSliceConstants p) {
     const uint32_t row = blockIdx.y, slices = gridDim.x;
     const uint64_t per = ((uint64_t)p.N + slices - 1) / slices;
     const uint64_t lo = (uint64_t)blockIdx.x * per, hi = min(lo + per, (uint64_t)p.N);
@@ -118,7 +141,7 @@ POPCORN_KERNEL void __launch_bounds__(256)
 // loop starts from x[0] (Argmax.metal:20-21), so a NaN at x[0] keeps index 0;
 // a row with no candidate (all NaN) also yields 0.
 POPCORN_KERNEL void __launch_bounds__(256)
-    argmax_finish(const float *x, const float *pv, const int32_t *pi, int32_t *indices, ArgmaxConstants p) {
+    argmax_finish(const float *x, const float *pv, const int32_t *pi, int32_t *indices, ArgmaxSliceConstants p) {
     const uint32_t row = blockIdx.x, slices = p.slices;
     float bv = -INFINITY;
     int32_t bi = 0x7fffffff;

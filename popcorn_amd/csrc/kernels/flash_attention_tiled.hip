@@ -40,7 +40,7 @@ constexpr int BKV = 32;          // keys per step
 constexpr float kRescaleGap = 8.0f;
 constexpr float kLog2e = 1.4426950408889634f;
 
-__device__ inline bool fa_allowed(const MPPFlashAttentionConstants &p, int posQ, int key) {
+__device__ inline bool fa_allowed(const TiledFlashAttentionConstants &p, int posQ, int key) {
     if (key < 0 || key >= (int)p.Sk) return false;
     bool ok = (p.maskKind == 2u) || (key <= posQ);
     if (p.maskKind == 1u) ok = ok && (posQ - key < p.slidingWindow);
@@ -48,7 +48,7 @@ __device__ inline bool fa_allowed(const MPPFlashAttentionConstants &p, int posQ,
 }
 
 // Key steps of query tile qt: keys any query of the tile may see.
-__device__ inline void fa_key_range(const MPPFlashAttentionConstants &p, uint32_t qt, int &kLo, int &kHi) {
+__device__ inline void fa_key_range(const TiledFlashAttentionConstants &p, uint32_t qt, int &kLo, int &kHi) {
     const int first = (int)p.Sk - (int)p.Sq + (int)(qt * BQ);
     const int last = (int)p.Sk - (int)p.Sq + (int)min(qt * BQ + BQ - 1, p.Sq - 1);
     kLo = 0;
@@ -57,7 +57,7 @@ __device__ inline void fa_key_range(const MPPFlashAttentionConstants &p, uint32_
     if (p.maskKind == 1u) kLo = max(0, first - p.slidingWindow + 1);
 }
 
-__device__ inline uint32_t fa_steps(const MPPFlashAttentionConstants &p, uint32_t qt) {
+__device__ inline uint32_t fa_steps(const TiledFlashAttentionConstants &p, uint32_t qt) {
     int kLo, kHi;
     fa_key_range(p, qt, kLo, kHi);
     return kHi > kLo ? (uint32_t)(kHi - kLo + BKV - 1) / BKV : 0u;
@@ -73,7 +73,7 @@ struct FaItem {
     bool split;
 };
 
-__device__ inline FaItem fa_item(const MPPFlashAttentionConstants &p) {
+__device__ inline FaItem fa_item(const TiledFlashAttentionConstants &p) {
     const uint32_t BH = p.B * p.Nq, nQT = p.qTilesPerHead, sf = p.splitFrom;
     const uint32_t rank = blockIdx.x / BH, nItems = nQT + (nQT - sf);
     FaItem it{blockIdx.x % BH, 0u, 0u, false};
@@ -102,7 +102,7 @@ __device__ inline FaItem fa_item(const MPPFlashAttentionConstants &p) {
 template <typename T, typename O, int HD>
 __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
                          const uint16_t *__restrict__ V, typename O::storage *__restrict__ out,
-                         float *__restrict__ pO, float *__restrict__ pML, const MPPFlashAttentionConstants &p) {
+                         float *__restrict__ pO, float *__restrict__ pML, const TiledFlashAttentionConstants &p) {
     constexpr int KS = HD / 16;  // k-steps of S^T = K . Q^T
     constexpr int DT = HD / 32;  // 32-row tiles of O^T
     constexpr int LDK = HD + 8;  // sK row (padded, elements)
@@ -395,7 +395,7 @@ constexpr int kMergeRows = 16;
 
 template <typename O, int HD>
 __device__ void fa_split_merge(const float *__restrict__ pO, const float *__restrict__ pML,
-                               typename O::storage *__restrict__ out, const MPPFlashAttentionConstants &p) {
+                               typename O::storage *__restrict__ out, const TiledFlashAttentionConstants &p) {
     const uint32_t nSplit = p.qTilesPerHead - p.splitFrom;
     const uint32_t tile = blockIdx.x / (BQ / kMergeRows);  // bh * nSplit + (qt - splitFrom)
     const uint32_t r0 = blockIdx.x % (BQ / kMergeRows) * kMergeRows;
@@ -428,7 +428,7 @@ __device__ void fa_split_merge(const float *__restrict__ pO, const float *__rest
 #define FA_TILED(name, T, O, HD)                                                                       \
     POPCORN_KERNEL void __launch_bounds__(256)                                                         \
         name(const uint16_t *q, const uint16_t *k, const uint16_t *v, O::storage *out, float *pO,      \
-             float *pML, MPPFlashAttentionConstants p) {                                               \
+             float *pML, TiledFlashAttentionConstants p) {                                               \
         fa_tiled<T, O, HD>(q, k, v, out, pO, pML, p);                                                  \
     }
 #define FA_TILED_D(t, T, o, O)                                   \
@@ -437,7 +437,7 @@ __device__ void fa_split_merge(const float *__restrict__ pO, const float *__rest
     FA_TILED(flash_attention_tiled_##t##_##o##_d256, T, O, 256)
 #define FA_MERGE(name, O, HD)                                                                          \
     POPCORN_KERNEL void __launch_bounds__(256)                                                         \
-        name(const float *pO, const float *pML, O::storage *out, MPPFlashAttentionConstants p) {       \
+        name(const float *pO, const float *pML, O::storage *out, TiledFlashAttentionConstants p) {       \
         fa_split_merge<O, HD>(pO, pML, out, p);                                                        \
     }
 #define FA_MERGE_D(o, O)                                         \

@@ -21,6 +21,13 @@
 //    lane's own dims; l and O stay group-local until the end of the range;
 //  * waves take interleaved tiles of the partition's key range; the 4 wave
 //    states are merged in LDS and written as the partition's (O, m, l).
+// Host names: flash_decoding_partial_<t>, flash_decoding_reduce_<t> and the
+// plain flash_attention* keep the reference's names, parameter lists
+// (FlashDecoding.metal:29-36, :181-187, FlashAttention.metal:31-36) and launch
+// geometry (FlashDecoding.swift:155-160, :225-230, FlashAttention.swift:203),
+// for raw launches built like the reference's; the descriptors use the fast
+// kernels above, flash_decoding_partial_<t>_ext (any head dim, Sq rows,
+// a KV row stride and a device position) and flash_decoding_reduce_<t>_ext.
 // Keys outside the causal / sliding-window range are skipped by clamping
 // the range; the per-key mask is still applied. A range with no allowed key
 // writes m = -inf, l = 0, O = 0 (FlashDecoding.metal:78-87); a tile whose
@@ -38,7 +45,7 @@ struct FdGeom {
     bool owner;  // fresh-key variant: this block's partition holds key posQ
 };
 
-__device__ inline bool fd_allowed(const FlashDecodingPartialConstants &p, int posQ, int posK) {
+__device__ inline bool fd_allowed(const FlashDecodingPartialExtConstants &p, int posQ, int posK) {
     bool allowed = (p.maskKind == 2u) | (posK <= posQ);
     if (p.maskKind == 1u) allowed = allowed & ((posQ - posK) < p.slidingWindow);
     return allowed;
@@ -48,7 +55,7 @@ __device__ inline bool fd_allowed(const FlashDecodingPartialConstants &p, int po
 // With freshLast, key posQ is left out of the block's range (the fresh-key
 // variant attends it from its prologue) and `owner` marks the block whose
 // partition holds it.
-__device__ inline FdGeom fd_geometry(const FlashDecodingPartialConstants &p, const int32_t *position, uint32_t gmax,
+__device__ inline FdGeom fd_geometry(const FlashDecodingPartialExtConstants &p, const int32_t *position, uint32_t gmax,
                                      bool freshLast = false) {
     FdGeom g;
     const uint32_t G = p.Nq / p.Nkv;
@@ -63,9 +70,11 @@ __device__ inline FdGeom fd_geometry(const FlashDecodingPartialConstants &p, con
     g.Sq = p.Sq ? p.Sq : 1u;
     const uint32_t stride = p.kvStride ? p.kvStride : p.Sk;
     uint32_t Sk = p.Sk;
+    bool inCache = true;  // the query rows' own keys lie inside the cache
     if (p.keyLenFromPosition) {
         int32_t pos = position[0];
         Sk = pos < 0 ? 0u : (uint32_t)pos + g.Sq;
+        inCache = pos >= 0 && (uint64_t)pos + g.Sq <= stride;
     }
     if (Sk > stride) Sk = stride;  // never read past the cache
     g.Sk = Sk;
@@ -75,7 +84,8 @@ __device__ inline FdGeom fd_geometry(const FlashDecodingPartialConstants &p, con
     const uint32_t per = (Sk + P - 1) / P;
     int lo = (int)(blockIdx.x * per);
     int hi = min(lo + (int)per, (int)Sk);
-    g.owner = freshLast && posQ >= 0 && (uint32_t)posQ < stride && lo <= posQ && posQ < hi;
+    // a position past the cache writes no key row (and attends the clamped range)
+    g.owner = freshLast && inCache && posQ >= 0 && (uint32_t)posQ < stride && lo <= posQ && posQ < hi;
     if (p.maskKind != 2u) hi = min(hi, posQ + 1);
     if (freshLast) hi = min(hi, posQ);
     if (p.maskKind == 1u) lo = max(lo, posQ - p.slidingWindow + 1);
@@ -87,7 +97,7 @@ __device__ inline FdGeom fd_geometry(const FlashDecodingPartialConstants &p, con
 
 // Writes one partition's state for `gcount` heads: wave states sm_* merged.
 template <int GMAX, int HD, int NSLOTS = kWaves>
-__device__ void fd_merge_store(const FlashDecodingPartialConstants &p, const FdGeom &geo, float (*sm_m)[GMAX],
+__device__ void fd_merge_store(const FlashDecodingPartialExtConstants &p, const FdGeom &geo, float (*sm_m)[GMAX],
                                float (*sm_l)[GMAX], float (*sm_o)[GMAX][HD], float *pO, float *pM, float *pL) {
     const uint32_t P = p.P ? p.P : 1u;
     const uint32_t G = p.Nq / p.Nkv;
@@ -139,7 +149,7 @@ template <typename T, int LPK, int CPL, int GMAX, int U, bool FRESH = false, typ
 __device__ void fd_partial_fast(const typename T::storage *__restrict__ Q, const typename T::storage *__restrict__ K,
                                 const typename T::storage *__restrict__ V, float *__restrict__ pO,
                                 float *__restrict__ pM, float *__restrict__ pL, const int32_t *__restrict__ position,
-                                const FlashDecodingPartialConstants &p, const FA &fa = FA{}) {
+                                const FlashDecodingPartialExtConstants &p, const FA &fa = FA{}) {
     constexpr int kV = pk::Vec<T>::kVec;
     constexpr int DL = CPL * kV;   // dims per lane
     constexpr int HD = LPK * DL;   // head dim
@@ -395,7 +405,7 @@ template <typename T>
 __device__ void fd_partial_generic(const typename T::storage *__restrict__ Q, const typename T::storage *__restrict__ K,
                                    const typename T::storage *__restrict__ V, float *__restrict__ pO,
                                    float *__restrict__ pM, float *__restrict__ pL, const int32_t *__restrict__ position,
-                                   const FlashDecodingPartialConstants &p) {
+                                   const FlashDecodingPartialExtConstants &p) {
     constexpr int kMaxHd = 512, kDL = kMaxHd / 64;
     __shared__ float sm_m[kWaves][1];
     __shared__ float sm_l[kWaves][1];
@@ -482,7 +492,7 @@ constexpr int kReduceBatch = 32;
 
 template <typename O>
 __device__ void fd_reduce(const float *__restrict__ pO, const float *__restrict__ pM, const float *__restrict__ pL,
-                          typename O::storage *__restrict__ out, const FlashDecodingReduceConstants &p) {
+                          typename O::storage *__restrict__ out, const FlashDecodingReduceExtConstants &p) {
     __shared__ float sm_m[kWaves], sm_l[kWaves];
     __shared__ float sm_o[kWaves][64];
     const uint32_t P = p.P, Hd = p.Hd;
@@ -548,12 +558,169 @@ __device__ void fd_reduce(const float *__restrict__ pO, const float *__restrict_
     if (d < Hd) out[slot * Hd + d] = O::store(ls > 0.0f ? os / ls : 0.0f);
 }
 
+// ---- the reference's launch -----------------------------------------------
+// One block per (b, hq, partition) for the partial (grid B x Nq x P) and per
+// (b, hq) for the combine (grid B x Nq), any block size up to 1024 threads
+// (the reference launches 128, FlashDecoding.swift:164, :234), with the
+// reference's constants blocks. The partial walks its keys in tiles of
+// kRefTile: each thread scores its keys of the tile over the whole head dim,
+// the block reduces the tile's max and weight sum in LDS, then each thread
+// updates its own dims of O (kept in LDS). Any head dim up to kRefMaxHd.
+
+constexpr uint32_t kRefTile = 128, kRefMaxHd = 512;
+
+__device__ inline uint32_t block_tid() { return threadIdx.x + blockDim.x * (threadIdx.y + blockDim.y * threadIdx.z); }
+__device__ inline uint32_t block_size() { return blockDim.x * blockDim.y * blockDim.z; }
+
+// Reduction over every thread of the block; every thread calls it and gets
+// the result. buf holds one float per thread.
+template <typename Op>
+__device__ float block_reduce(float v, float *buf, Op op) {
+    const uint32_t tid = block_tid();
+    buf[tid] = v;
+    __syncthreads();
+    for (uint32_t n = block_size(); n > 1;) {
+        const uint32_t half = (n + 1) / 2;
+        if (tid < n - half) buf[tid] = op(buf[tid], buf[tid + half]);
+        __syncthreads();
+        n = half;
+    }
+    const float r = buf[0];
+    __syncthreads();
+    return r;
+}
+
+// The online softmax of one query row over keys [jLo, jHi) of one KV head,
+// on the whole block: O (unnormalised) ends in o_sm[0, Hd), the running max
+// and sum in m and l (every thread holds them). q_sm holds q * scale.
+template <typename TKV>
+__device__ void attend_ref(const float *q_sm, const typename TKV::storage *__restrict__ Kh,
+                           const typename TKV::storage *__restrict__ Vh, uint32_t Hd, uint32_t jLo, uint32_t jHi, int posQ,
+                           uint32_t maskKind, int32_t window, float *o_sm, float *w_sm, float *buf, float &m, float &l) {
+    const uint32_t tid = block_tid(), bs = block_size();
+    m = -INFINITY;
+    l = 0.0f;
+    for (uint32_t j0 = jLo; j0 < jHi; j0 += kRefTile) {
+        const uint32_t n = min(kRefTile, jHi - j0);
+        float tmax = -INFINITY;
+        for (uint32_t i = tid; i < n; i += bs) {
+            const uint32_t j = j0 + i;
+            bool allowed = (maskKind == 2u) | ((int)j <= posQ);
+            if (maskKind == 1u) allowed = allowed & ((posQ - (int)j) < window);
+            float s = -INFINITY;
+            if (allowed) {
+                const typename TKV::storage *kr = Kh + (uint64_t)j * Hd;
+                float acc = 0.0f;
+                for (uint32_t d = 0; d < Hd; ++d) acc += q_sm[d] * TKV::load(kr[d]);
+                s = acc;
+            }
+            w_sm[i] = s;
+            tmax = fmaxf(tmax, s);
+        }
+        tmax = block_reduce(tmax, buf, [](float a, float c) { return fmaxf(a, c); });
+        const float m_new = fmaxf(m, tmax);
+        if (m_new == -INFINITY) continue;  // no allowed key yet
+        const float alpha = pk::fast_exp(m - m_new);
+        float ps = 0.0f;
+        for (uint32_t i = tid; i < n; i += bs) {
+            const float e = w_sm[i] == -INFINITY ? 0.0f : pk::fast_exp(w_sm[i] - m_new);
+            w_sm[i] = e;
+            ps += e;
+        }
+        ps = block_reduce(ps, buf, [](float a, float c) { return a + c; });
+        l = alpha * l + ps;
+        m = m_new;
+        for (uint32_t d = tid; d < Hd; d += bs) {
+            float o = o_sm[d] * alpha;
+            for (uint32_t i = 0; i < n; ++i) o += w_sm[i] * TKV::load(Vh[(uint64_t)(j0 + i) * Hd + d]);
+            o_sm[d] = o;
+        }
+        __syncthreads();
+    }
+}
+
+template <typename T>
+__device__ void fd_partial_ref(const typename T::storage *__restrict__ Q, const typename T::storage *__restrict__ K,
+                               const typename T::storage *__restrict__ V, float *__restrict__ pO, float *__restrict__ pM,
+                               float *__restrict__ pL, const FlashDecodingPartialConstants &p) {
+    __shared__ float q_sm[kRefMaxHd], o_sm[kRefMaxHd], w_sm[kRefTile], buf[1024];
+    const uint32_t b = blockIdx.x, hq = blockIdx.y, part = blockIdx.z;
+    if (b >= p.B || hq >= p.Nq || part >= p.P || p.Hd > kRefMaxHd || p.Nkv == 0 || p.Nq % p.Nkv != 0) return;
+    const uint32_t tid = block_tid(), bs = block_size();
+    const uint32_t Hd = p.Hd, Sk = p.Sk, hkv = hq * p.Nkv / p.Nq;
+    const uint32_t per = (Sk + p.P - 1) / p.P;
+    const uint32_t jLo = min(part * per, Sk), jHi = min(jLo + per, Sk);
+    const uint64_t slot = (uint64_t)(b * p.Nq + hq) * p.P + part;
+    for (uint32_t d = tid; d < Hd; d += bs) {
+        q_sm[d] = T::load(Q[(uint64_t)(b * p.Nq + hq) * Hd + d]) * p.scale;
+        o_sm[d] = 0.0f;
+    }
+    __syncthreads();
+    const uint64_t head = (uint64_t)(b * p.Nkv + hkv) * Sk * Hd;
+    float m, l;
+    // Sq = 1: the query sits at the last key, posQ = Sk - 1
+    attend_ref<T>(q_sm, K + head, V + head, Hd, jLo, jHi, (int)Sk - 1, p.maskKind, p.slidingWindow, o_sm, w_sm, buf, m, l);
+    for (uint32_t d = tid; d < Hd; d += bs) pO[slot * Hd + d] = o_sm[d];
+    if (tid == 0) {
+        pM[slot] = m;
+        pL[slot] = l;
+    }
+}
+
+// FlashAttention.metal:30-161 on the reference's launch (FlashAttention.swift:
+// 203, :220-222): one block per (b, hq, query row), grid B x Nq x Sq, the row
+// attending as position Sk - Sq + q over all Sk keys, O = O / l.
+template <typename TQ, typename TKV, typename TO>
+__device__ void fa_plain_ref(const typename TQ::storage *__restrict__ Q, const typename TKV::storage *__restrict__ K,
+                             const typename TKV::storage *__restrict__ V, typename TO::storage *__restrict__ O,
+                             const FlashAttentionConstants &p) {
+    __shared__ float q_sm[kRefMaxHd], o_sm[kRefMaxHd], w_sm[kRefTile], buf[1024];
+    const uint32_t b = blockIdx.x, hq = blockIdx.y, q = blockIdx.z;
+    if (b >= p.B || hq >= p.Nq || q >= p.Sq || p.Hd > kRefMaxHd || p.Nkv == 0 || p.Nq % p.Nkv != 0) return;
+    const uint32_t tid = block_tid(), bs = block_size();
+    const uint32_t Hd = p.Hd, hkv = hq * p.Nkv / p.Nq;
+    const uint64_t row = ((uint64_t)(b * p.Nq + hq) * p.Sq + q) * Hd;
+    for (uint32_t d = tid; d < Hd; d += bs) {
+        q_sm[d] = TQ::load(Q[row + d]) * p.scale;
+        o_sm[d] = 0.0f;
+    }
+    __syncthreads();
+    const uint64_t head = (uint64_t)(b * p.Nkv + hkv) * p.Sk * Hd;
+    float m, l;
+    attend_ref<TKV>(q_sm, K + head, V + head, Hd, 0, p.Sk, (int)p.Sk - (int)p.Sq + (int)q, p.maskKind, p.slidingWindow,
+                    o_sm, w_sm, buf, m, l);
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    for (uint32_t d = tid; d < Hd; d += bs) O[row + d] = TO::store(o_sm[d] * inv);
+}
+
+// FlashDecoding.metal:202-227 at one block per (b, hq): every thread takes
+// the max and the weighted sum over the P partitions, then its dims.
+template <typename O>
+__device__ void fd_reduce_ref(const float *__restrict__ pO, const float *__restrict__ pM, const float *__restrict__ pL,
+                              typename O::storage *__restrict__ out, const FlashDecodingReduceConstants &p) {
+    const uint32_t b = blockIdx.x, hq = blockIdx.y;
+    if (b >= p.B || hq >= p.Nq) return;
+    const uint32_t tid = block_tid(), bs = block_size();
+    const uint64_t s0 = (uint64_t)(b * p.Nq + hq) * p.P;
+    float mstar = -INFINITY;
+    for (uint32_t k = 0; k < p.P; ++k) mstar = fmaxf(mstar, pM[s0 + k]);
+    float lstar = 0.0f;
+    for (uint32_t k = 0; k < p.P; ++k)
+        if (pM[s0 + k] != -INFINITY) lstar += pk::fast_exp(pM[s0 + k] - mstar) * pL[s0 + k];
+    for (uint32_t d = tid; d < p.Hd; d += bs) {
+        float acc = 0.0f;
+        for (uint32_t k = 0; k < p.P; ++k)
+            if (pM[s0 + k] != -INFINITY) acc += pk::fast_exp(pM[s0 + k] - mstar) * pO[(s0 + k) * p.Hd + d];
+        out[(uint64_t)(b * p.Nq + hq) * p.Hd + d] = O::store(lstar > 0.0f ? acc / lstar : 0.0f);
+    }
+}
+
 }  // namespace
 
 #define FD_FAST(name, T, LPK, CPL, G, U)                                                                   \
     POPCORN_KERNEL void __launch_bounds__(256)                                                             \
         name(const T::storage *q, const T::storage *k, const T::storage *v, float *pO, float *pM, float *pL, \
-             const int32_t *position, FlashDecodingPartialConstants p) {                                    \
+             const int32_t *position, FlashDecodingPartialExtConstants p) {                                    \
         fd_partial_fast<T, LPK, CPL, G, U>(q, k, v, pO, pM, pL, position, p);                               \
     }
 
@@ -561,7 +728,7 @@ __device__ void fd_reduce(const float *__restrict__ pO, const float *__restrict_
     POPCORN_KERNEL void __launch_bounds__(256)                                                             \
         name(const T::storage *qkv, T::storage *k, T::storage *v, float *pO, float *pM, float *pL,          \
              const int32_t *position, const float *wq, const float *wk, const float *invFreq,                \
-             FlashDecodingPartialConstants p, DecodeAttentionConstants c) {                                 \
+             FlashDecodingPartialExtConstants p, DecodeAttentionConstants c) {                                 \
         FreshArgs<T> fa{k, v, wq, wk, invFreq, c};                                                          \
         fd_partial_fast<T, LPK, CPL, G, U, true>(qkv, k, v, pO, pM, pL, position, p, fa);                   \
     }
@@ -569,27 +736,54 @@ __device__ void fd_reduce(const float *__restrict__ pO, const float *__restrict_
 #define FD_GENERIC(name, T)                                                                                 \
     POPCORN_KERNEL void __launch_bounds__(256)                                                             \
         name(const T::storage *q, const T::storage *k, const T::storage *v, float *pO, float *pM, float *pL, \
-             const int32_t *position, FlashDecodingPartialConstants p) {                                    \
+             const int32_t *position, FlashDecodingPartialExtConstants p) {                                    \
         fd_partial_generic<T>(q, k, v, pO, pM, pL, position, p);                                            \
     }
 
 #define FD_REDUCE(name, O)                                                                                  \
     POPCORN_KERNEL void __launch_bounds__(256)                                                             \
-        name(const float *pO, const float *pM, const float *pL, O::storage *out, FlashDecodingReduceConstants p) { \
+        name(const float *pO, const float *pM, const float *pL, O::storage *out, FlashDecodingReduceExtConstants p) { \
         fd_reduce<O>(pO, pM, pL, out, p);                                                                   \
+    }
+
+#define FD_REF(pname, rname, T)                                                                             \
+    POPCORN_KERNEL void __launch_bounds__(1024)                                                             \
+        pname(const T::storage *q, const T::storage *k, const T::storage *v, float *pO, float *pM, float *pL, \
+              FlashDecodingPartialConstants p) {                                                             \
+        fd_partial_ref<T>(q, k, v, pO, pM, pL, p);                                                           \
+    }                                                                                                        \
+    POPCORN_KERNEL void __launch_bounds__(1024)                                                             \
+        rname(const float *pO, const float *pM, const float *pL, T::storage *out, FlashDecodingReduceConstants p) { \
+        fd_reduce_ref<T>(pO, pM, pL, out, p);                                                                \
     }
 
 using pk::BF16;
 using pk::F16;
 using pk::F32;
 
-FD_GENERIC(flash_decoding_partial_f32, F32)
-FD_GENERIC(flash_decoding_partial_bf16, BF16)
-FD_GENERIC(flash_decoding_partial_f16, F16)
+FD_GENERIC(flash_decoding_partial_f32_ext, F32)
+FD_GENERIC(flash_decoding_partial_bf16_ext, BF16)
+FD_GENERIC(flash_decoding_partial_f16_ext, F16)
 
-FD_REDUCE(flash_decoding_reduce_f32, F32)
-FD_REDUCE(flash_decoding_reduce_bf16, BF16)
-FD_REDUCE(flash_decoding_reduce_f16, F16)
+FD_REDUCE(flash_decoding_reduce_f32_ext, F32)
+FD_REDUCE(flash_decoding_reduce_bf16_ext, BF16)
+FD_REDUCE(flash_decoding_reduce_f16_ext, F16)
+
+// FlashAttention.metal:164-167
+#define FA_REF(name, TQ, TKV, TO)                                                                           \
+    POPCORN_KERNEL void __launch_bounds__(1024)                                                             \
+        name(const TQ::storage *q, const TKV::storage *k, const TKV::storage *v, TO::storage *o,           \
+             FlashAttentionConstants p) {                                                                   \
+        fa_plain_ref<TQ, TKV, TO>(q, k, v, o, p);                                                           \
+    }
+FA_REF(flash_attention, F32, F32, F32)
+FA_REF(flash_attention_bf16, BF16, BF16, BF16)
+FA_REF(flash_attention_bf16_to_f32, BF16, BF16, F32)
+FA_REF(flash_attention_f32_bf16_to_bf16, F32, BF16, BF16)
+
+FD_REF(flash_decoding_partial_f32, flash_decoding_reduce_f32, F32)
+FD_REF(flash_decoding_partial_bf16, flash_decoding_reduce_bf16, BF16)
+FD_REF(flash_decoding_partial_f16, flash_decoding_reduce_f16, F16)
 
 // Fast path instantiations: 2-byte types (8 dims per 16B chunk):
 // Hd 64 -> LPK 8, Hd 128 -> 16, Hd 256 -> 32, Hd 512 -> 64 (CPL 1).

@@ -6,16 +6,22 @@
 //
 // Each thread moves one run of up to kRun consecutive elements of one cache
 // row (kRun = 8 for 2-byte sources, 4 for f32: one 16B load). A run never
-// crosses a row, so the destination of a run is contiguous. When the write
-// offset comes from a position tensor (decode replayed from a graph) and the
-// range would leave the cache, the kernel writes nothing.
+// crosses a row, so the destination of a run is contiguous. The grid strides
+// over the runs, so any launch shape covers the whole source (the
+// reference's one thread per 4 elements, KVCacheWrite.swift:33-34, included).
+//
+// kv_cache_write* keep the reference's host names and parameter list
+// (src, cache, KVCacheWriteConstants; KVCacheWrite.metal:6-11);
+// kv_cache_write*_ext take a position tensor and KVCacheWriteExtConstants:
+// when the write offset comes from the position (decode replayed from a
+// graph) and the range would leave the cache, they write nothing.
 #include "common.hpp"
 
 namespace {
 
 template <typename S, typename C>
 __device__ void kv_write(const typename S::storage *__restrict__ src, typename C::storage *__restrict__ cache,
-                         const int32_t *__restrict__ position, const KVCacheWriteConstants &p) {
+                         const int32_t *__restrict__ position, const KVCacheWriteExtConstants &p) {
     constexpr uint32_t kRun = 16 / sizeof(typename S::storage);
     uint32_t offset = p.offset;
     if (p.offsetFromPosition) {
@@ -64,10 +70,14 @@ __device__ void kv_write(const typename S::storage *__restrict__ src, typename C
 
 }  // namespace
 
-#define KV_WRITE(name, S, C)                                                                          \
-    POPCORN_KERNEL void __launch_bounds__(256)                                                           \
-        name(const S::storage *src, C::storage *cache, const int32_t *position, KVCacheWriteConstants p) { \
-        kv_write<S, C>(src, cache, position, p);                                                      \
+#define KV_WRITE(name, S, C)                                                                                  \
+    POPCORN_KERNEL void __launch_bounds__(1024) name(const S::storage *src, C::storage *cache, KVCacheWriteConstants p) { \
+        const KVCacheWriteExtConstants e{p.B, p.Nkv, p.Snew, p.Smax, p.Hd, p.offset, 0u};                   \
+        kv_write<S, C>(src, cache, nullptr, e);                                                               \
+    }                                                                                                         \
+    POPCORN_KERNEL void __launch_bounds__(1024)                                                               \
+        name##_ext(const S::storage *src, C::storage *cache, const int32_t *position, KVCacheWriteExtConstants p) { \
+        kv_write<S, C>(src, cache, position, p);                                                              \
     }
 
 using pk::BF16;

@@ -1,9 +1,12 @@
 // General matmul C[m, n] = sum_k A[m, k] * B(^T)[k, n] with f32 accumulation:
-// the semantics of Sources/Popcorn/Kernels/Matmul.metal:6-26 (host names and
-// dtype triples of Matmul.swift:222-229, plus f16 triples). This is the
-// SIMT fallback for shapes and dtypes the MFMA GEMM does not take: 64x64
-// output tiles per 256-thread block, 4x4 outputs per thread, K staged through
-// LDS in steps of 16.
+// the semantics of Sources/Popcorn/Kernels/Matmul.metal:6-26 (dtype triples
+// of Matmul.swift:222-229, plus f16 triples).
+// matmul_tiled*: the SIMT fallback the Matmul descriptor runs for shapes and
+// dtypes the MFMA GEMM does not take: 64x64 output tiles per 256-thread
+// block, 4x4 outputs per thread, K staged through LDS in steps of 16.
+// matmul*: the reference's host names, parameter list and launch geometry
+// (one thread per output, thread x = row m, y = column n; Matmul.swift:63-64),
+// for raw launches built like the reference's.
 #include "common.hpp"
 
 namespace {
@@ -65,22 +68,45 @@ __device__ void matmul_tiled(const typename A::storage *__restrict__ a, const ty
         }
 }
 
+// The reference's launch: the thread at (x, y) of the grid computes C[x, y];
+// the grid strides in both dimensions, so any launch shape covers C.
+template <typename A, typename B, typename C>
+__device__ void matmul_ref(const typename A::storage *__restrict__ a, const typename B::storage *__restrict__ b,
+                           typename C::storage *__restrict__ c, const MatmulConstants &p) {
+    const uint32_t sx = gridDim.x * blockDim.x, sy = gridDim.y * blockDim.y;
+    for (uint32_t m = blockIdx.x * blockDim.x + threadIdx.x; m < p.M; m += sx) {
+        for (uint32_t n = blockIdx.y * blockDim.y + threadIdx.y; n < p.N; n += sy) {
+            float acc = 0.0f;
+            const uint64_t arow = (uint64_t)m * p.K;
+            for (uint32_t k = 0; k < p.K; ++k) {
+                const uint64_t bi = p.transposeB ? (uint64_t)n * p.K + k : (uint64_t)k * p.N + n;
+                acc += A::load(a[arow + k]) * B::load(b[bi]);
+            }
+            c[(uint64_t)m * p.N + n] = C::store(acc);
+        }
+    }
+}
+
 }  // namespace
 
-#define MATMUL(name, A, B, C)                                                                    \
-    POPCORN_KERNEL void __launch_bounds__(256)                                                   \
-        name(const A::storage *a, const B::storage *b, C::storage *c, MatmulConstants p) {       \
-        matmul_tiled<A, B, C>(a, b, c, p);                                                       \
+#define MATMUL(sfx, A, B, C)                                                                        \
+    POPCORN_KERNEL void __launch_bounds__(256)                                                      \
+        matmul_tiled##sfx(const A::storage *a, const B::storage *b, C::storage *c, MatmulConstants p) { \
+        matmul_tiled<A, B, C>(a, b, c, p);                                                          \
+    }                                                                                               \
+    POPCORN_KERNEL void __launch_bounds__(1024)                                                     \
+        matmul##sfx(const A::storage *a, const B::storage *b, C::storage *c, MatmulConstants p) {   \
+        matmul_ref<A, B, C>(a, b, c, p);                                                            \
     }
 
 using pk::BF16;
 using pk::F16;
 using pk::F32;
 
-MATMUL(matmul, F32, F32, F32)
-MATMUL(matmul_f16, F32, F16, F32)
-MATMUL(matmul_bf16, F32, BF16, F32)
-MATMUL(matmul_bf16_bf16_f32, BF16, BF16, F32)
-MATMUL(matmul_bf16_bf16_bf16, BF16, BF16, BF16)
-MATMUL(matmul_f16_f16_f32, F16, F16, F32)
-MATMUL(matmul_f16_f16_f16, F16, F16, F16)
+MATMUL(, F32, F32, F32)
+MATMUL(_f16, F32, F16, F32)
+MATMUL(_bf16, F32, BF16, F32)
+MATMUL(_bf16_bf16_f32, BF16, BF16, F32)
+MATMUL(_bf16_bf16_bf16, BF16, BF16, BF16)
+MATMUL(_f16_f16_f32, F16, F16, F32)
+MATMUL(_f16_f16_f16, F16, F16, F16)

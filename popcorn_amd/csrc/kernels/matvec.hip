@@ -1,9 +1,14 @@
 // Matrix-vector products of the decode step (the reference's Matmul with
 // m == 1):
-// matvec_nk_*: y[n] = sum_k x[k] * W[n, k] with W row-major [N, K] (the
-// transposeB layout of Sources/Popcorn/Kernels/Matvec.metal:55-126; host names
-// keep the reference's matvec_nk_simd_<x>_<w>_<out> pattern, with an _r1
-// suffix for one row per unit instead of four, and its MatvecConstants).
+// matvec_nk_stream_<x>_<w>_<out>_r<R>: y[n] = sum_k x[k] * W[n, k] with W
+// row-major [N, K] (the transposeB layout of
+// Sources/Popcorn/Kernels/Matvec.metal:55-126, the reference's
+// MatvecConstants), R = 4 or 1 rows per streamed unit; what the Matmul
+// descriptor runs for m == 1.
+// matvec_nk_simd_<x>_<w>_<out>: the reference's host name, parameter list
+// and launch geometry (Matmul.swift:248-251: threads ceil(N / 4) * 32 in
+// blocks of 128): each 32-lane half-wave takes 4 rows, its lanes strided
+// over K, for raw launches built like the reference's.
 // decode_matvec_<t>_<o>_r<R>_f<F>: the same product with the decoder-layer
 // glue folded in (DecodeMatvecConstants): F bit 0 = residual + post-norm in
 // front, bit 1 = pre-norm, compiled in; the KV-cache scatter of the output
@@ -80,6 +85,36 @@ __device__ void matvec_nk(const typename X::storage *__restrict__ x_in, const ty
     rs.run(xs, rows, store);
 }
 
+// The reference's launch: half-wave u = global thread / 32 computes rows
+// 4u .. 4u + 3, lanes strided over K (4 elements per step when K % 4 == 0,
+// Matvec.metal:82-97, else 1), summed over the half-wave. The block size
+// must be a multiple of 32 (the reference's is 128).
+template <typename X, typename W, typename O>
+__device__ void matvec_nk_ref(const typename X::storage *__restrict__ x, const typename W::storage *__restrict__ w,
+                              typename O::storage *__restrict__ out, const MatvecConstants &p) {
+    const uint64_t gid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t lane = threadIdx.x & 31;
+    const uint64_t row0 = (gid >> 5) * 4;
+    if (row0 >= p.N) return;  // uniform over the half-wave
+    const uint32_t K = p.K, step = (K % 4 == 0) ? 4u : 1u;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t k0 = lane * step; k0 < K; k0 += 32 * step) {
+#pragma unroll
+        for (uint32_t e = 0; e < 4; ++e) {
+            if (e >= step) break;
+            const float xv = X::load(x[k0 + e]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                if (row0 + r < p.N) acc[r] += xv * W::load(w[(row0 + r) * K + k0 + e]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float sum = pk::half32_sum(acc[r]);
+        if (lane == 0 && row0 + r < p.N) out[row0 + r] = O::store(sum);
+    }
+}
+
 template <typename X, typename W, typename O>
 __device__ void matvec_kn(const typename X::storage *__restrict__ x, const typename W::storage *__restrict__ w,
                           typename O::storage *__restrict__ out, const MatvecConstants &p) {
@@ -92,7 +127,7 @@ __device__ void matvec_kn(const typename X::storage *__restrict__ x, const typen
 
 }  // namespace
 
-// Reference-named matvec: plain product, x staged in dynamic LDS (K floats).
+// Streaming matvec: plain product, x staged in dynamic LDS (K floats).
 #define MATVEC_NK(name, X, W, O, R)                                                                   \
     POPCORN_KERNEL void __launch_bounds__(256)                                                        \
         name(const X::storage *x, const W::storage *w, O::storage *out, MatvecConstants p) {          \
@@ -101,9 +136,13 @@ __device__ void matvec_kn(const typename X::storage *__restrict__ x, const typen
         matvec_nk<X, W, O, R, false, false, 8>(x, nullptr, nullptr, nullptr, w, out, nullptr, nullptr, \
                                                nullptr, nullptr, d, xs);                              \
     }
-#define MATVEC_NK_ALL(base, X, W, O) \
-    MATVEC_NK(base, X, W, O, 4)      \
-    MATVEC_NK(base##_r1, X, W, O, 1)
+#define MATVEC_NK_ALL(xt, wt, ot, X, W, O)                                                   \
+    MATVEC_NK(matvec_nk_stream_##xt##_##wt##_##ot##_r4, X, W, O, 4)                          \
+    MATVEC_NK(matvec_nk_stream_##xt##_##wt##_##ot##_r1, X, W, O, 1)                          \
+    POPCORN_KERNEL void __launch_bounds__(1024) matvec_nk_simd_##xt##_##wt##_##ot(            \
+        const X::storage *x, const W::storage *w, O::storage *out, MatvecConstants p) {      \
+        matvec_nk_ref<X, W, O>(x, w, out, p);                                                \
+    }
 
 // Decode matvec with the layer glue; the plain form stages up to 8 runs of
 // x per thread in registers, the glued forms 2 (K <= 4096 for 16-bit types).
@@ -135,13 +174,13 @@ using pk::BF16;
 using pk::F16;
 using pk::F32;
 
-MATVEC_NK_ALL(matvec_nk_simd_f32_f32_f32, F32, F32, F32)
-MATVEC_NK_ALL(matvec_nk_simd_f32_bf16_f32, F32, BF16, F32)
-MATVEC_NK_ALL(matvec_nk_simd_bf16_bf16_f32, BF16, BF16, F32)
-MATVEC_NK_ALL(matvec_nk_simd_bf16_bf16_bf16, BF16, BF16, BF16)
-MATVEC_NK_ALL(matvec_nk_simd_f32_f16_f32, F32, F16, F32)
-MATVEC_NK_ALL(matvec_nk_simd_f16_f16_f32, F16, F16, F32)
-MATVEC_NK_ALL(matvec_nk_simd_f16_f16_f16, F16, F16, F16)
+MATVEC_NK_ALL(f32, f32, f32, F32, F32, F32)
+MATVEC_NK_ALL(f32, bf16, f32, F32, BF16, F32)
+MATVEC_NK_ALL(bf16, bf16, f32, BF16, BF16, F32)
+MATVEC_NK_ALL(bf16, bf16, bf16, BF16, BF16, BF16)
+MATVEC_NK_ALL(f32, f16, f32, F32, F16, F32)
+MATVEC_NK_ALL(f16, f16, f32, F16, F16, F32)
+MATVEC_NK_ALL(f16, f16, f16, F16, F16, F16)
 
 DECODE_MATVEC_R(decode_matvec_bf16_bf16, BF16, BF16)
 DECODE_MATVEC_R(decode_matvec_bf16_f32, BF16, F32)

@@ -295,6 +295,41 @@ int32_t popcorn_library_cached_function_count(popcorn_library_t library) {
     return library ? (int32_t)library->lib->cachedCount() : 0;
 }
 
+static void fillLayout(const KernelLayout &L, popcorn_kernel_layout_t *out) {
+    std::memset(out, 0, sizeof(*out));
+    size_t i = 0;
+    while (i < L.args.size() && L.args[i].pointer) ++i;
+    out->nbuffers = (int32_t)i;
+    out->nconstants = (int32_t)(L.args.size() - i);
+    for (size_t j = i; j < L.args.size(); ++j) {
+        if (j - i < POPCORN_MAX_CONSTANT_BLOCKS) out->constant_sizes[j - i] = L.args[j].size;
+        if (L.args[j].pointer) ++out->trailing_pointers;
+    }
+    out->max_threads_per_block = L.maxThreads;
+}
+
+popcorn_status_t popcorn_function_layout(popcorn_function_t function, popcorn_kernel_layout_t *layout) {
+    return guarded([&] {
+        need(function, "function");
+        need(layout, "layout");
+        const Function *f = reinterpret_cast<const Function *>(function);
+        if (!f->layout) throw Error::invalidArgument("no parameter metadata for " + f->name);
+        fillLayout(*f->layout, layout);
+    });
+}
+
+popcorn_status_t popcorn_code_object_layout(const char *path, const char *kernel, popcorn_kernel_layout_t *layout) {
+    return guarded([&] {
+        need(path, "path");
+        need(kernel, "kernel");
+        need(layout, "layout");
+        const auto all = readKernelLayouts(std::string(path));
+        auto it = all.find(kernel);
+        if (it == all.end()) throw Error::kernelFunctionNotFound(kernel);
+        fillLayout(it->second, layout);
+    });
+}
+
 popcorn_status_t popcorn_launch(popcorn_stream_t stream, popcorn_function_t function, const uint32_t grid[3],
                                 const uint32_t block[3], void *const *buffers, int32_t nbuffers,
                                 const void *const *constants, const size_t *constant_sizes, int32_t nconstants,
@@ -310,6 +345,11 @@ popcorn_status_t popcorn_launch(popcorn_stream_t stream, popcorn_function_t func
             need(constant_sizes, "constant_sizes");
         }
         const Function *f = reinterpret_cast<const Function *>(function);
+        if (f->layout) f->layout->check(f->name, (size_t)nbuffers, std::vector<size_t>(constant_sizes, constant_sizes + nconstants));
+        if ((uint64_t)block[0] * block[1] * block[2] > (uint64_t)f->attrs.maxThreadsPerBlock)
+            throw Error::invalidArgument("block of " + std::to_string((uint64_t)block[0] * block[1] * block[2]) +
+                                         " threads exceeds the limit of " + f->name + " (" +
+                                         std::to_string(f->attrs.maxThreadsPerBlock) + ")");
         std::vector<void *> ptrs(buffers, buffers + nbuffers);
         std::vector<void *> params;
         for (int32_t i = 0; i < nbuffers; ++i) params.push_back(&ptrs[(size_t)i]);

@@ -98,6 +98,10 @@ struct popcorn_decoder_s {
     hipGraphExec_t graph = nullptr;
     hipGraph_t graphDef = nullptr;
     int graphSteps = 1;
+    // The position the next enqueued step decodes at, tracked on the host
+    // (reset sets it, every enqueued step adds one, read resynchronises it
+    // with device memory) so that run() refuses steps past the KV cache.
+    int64_t hostPos = 0;
 
     ~popcorn_decoder_s() {
         if (graph) (void)hipGraphExecDestroy(graph);
@@ -262,7 +266,7 @@ struct popcorn_decoder_s {
         // and writes the next step's input row (gather, x sqrt(H))
         Tensor tpv(argValues.p, Shape({argSlices}), DataType::f32);
         Tensor tpi(argIndices.p, Shape({argSlices}), DataType::i32);
-        ArgmaxConstants ac{1u, (uint32_t)V, (uint32_t)argSlices};
+        ArgmaxSliceConstants ac{1u, (uint32_t)V, (uint32_t)argSlices};
         add(Kernels::Custom("argmax_partial", {{tlog, kRead}, {tpv, kWrite}, {tpi, kWrite}}, {bytesOf(ac)},
                             dim3((unsigned)argSlices, 1, 1), dim3(256, 1, 1)));
         Tensor thist(history.p, Shape({std::max<int64_t>(cfg.history_len, 1)}), DataType::i32);
@@ -328,6 +332,12 @@ struct popcorn_decoder_s {
     void run(int32_t steps, bool useGraph) {
         if (steps < 0) throw Error::invalidArgument("steps must be >= 0");
         if (steps == 0) return;
+        // a step at position p writes KV row p and attends rows 0..p
+        if (hostPos < 0 || hostPos + steps > S)
+            throw Error::tensorShapeMismatch("decode steps at positions " + std::to_string(hostPos) + "..<" +
+                                             std::to_string(hostPos + steps) + " exceed the KV cache length " +
+                                             std::to_string(S) + ".");
+        hostPos += steps;
         if (!useGraph) {
             encodePrime();
             for (int32_t i = 0; i < steps; ++i) encodeStep();
@@ -498,6 +508,7 @@ popcorn_status_t popcorn_decoder_tensor(popcorn_decoder_t d, const char *name, i
         } else if (n == "embedding") t = d->bf(d->embedding.p, {d->V, d->H});
         else if (n == "final_norm") t = Tensor(d->finalNorm.p, Shape({d->H}), DataType::f32);
         else if (n == "x") t = d->bf(d->x.p, {d->H});
+        else if (n == "x2") t = d->bf(d->x2.p, {d->H});
         else if (n == "q") t = d->bf(d->qkv.p, {d->QW});
         else if (n == "qkv") t = d->bf(d->qkv.p, {d->QKV});
         else if (n == "inv_freq" && d->invFreq.p) t = Tensor(d->invFreq.p, Shape({d->Hd / 2}), DataType::f32);
@@ -529,6 +540,7 @@ popcorn_status_t popcorn_decoder_reset(popcorn_decoder_t d, int32_t token, int32
         checkHip(hipMemcpyAsync(d->token.p, &token, 4, hipMemcpyHostToDevice, d->stream), "write token");
         checkHip(hipMemcpyAsync(d->position.p, &position, 4, hipMemcpyHostToDevice, d->stream), "write position");
         checkHip(hipStreamSynchronize(d->stream), "sync");
+        d->hostPos = position;
     });
 }
 
@@ -548,6 +560,7 @@ popcorn_status_t popcorn_decoder_read(popcorn_decoder_t d, int32_t *token, int32
         checkHip(hipStreamSynchronize(d->stream), "sync");
         if (token) *token = v[0];
         if (position) *position = v[1];
+        d->hostPos = v[1];
     });
 }
 
@@ -586,6 +599,21 @@ popcorn_status_t popcorn_decoder_time_kernel(popcorn_decoder_t d, const char *fu
                 (void)hipEventDestroy(b);
             }
         } cleanup{d, a, b};
+        // the step's tail kernel advances the position and rewrites the
+        // token; both are restored afterwards
+        int32_t saved[2] = {0, 0};
+        checkHip(hipMemcpyAsync(&saved[0], d->token.p, 4, hipMemcpyDeviceToHost, d->stream), "read token");
+        checkHip(hipMemcpyAsync(&saved[1], d->position.p, 4, hipMemcpyDeviceToHost, d->stream), "read position");
+        checkHip(hipStreamSynchronize(d->stream), "sync");
+        struct Restore {
+            popcorn_decoder_s *d;
+            int32_t *v;
+            ~Restore() {
+                (void)hipStreamSynchronize(d->stream);
+                (void)hipMemcpy(d->token.p, &v[0], 4, hipMemcpyHostToDevice);
+                (void)hipMemcpy(d->position.p, &v[1], 4, hipMemcpyHostToDevice);
+            }
+        } restore{d, saved};
         d->enc->setDispatchFilter(function_name);
         d->encodeStep();  // warm: first launch of each
         checkHip(hipEventRecord(a, d->stream), "hipEventRecord");

@@ -192,9 +192,10 @@ public:
 
     void encode(KernelCommandEncoder &enc) const override {
         if (path_ == Kernels::AttentionPath::tiled) {
-            // MPPFlashAttentionConstants (PopcornKernelTypes.h:133-144): one
-            // block per 128 query rows of each (batch, query head)
-            MPPFlashAttentionConstants c{};
+            // TiledFlashAttentionConstants (the fields of
+            // PopcornKernelTypes.h:133-144 and two more): one block per 128
+            // query rows of each (batch, query head)
+            TiledFlashAttentionConstants c{};
             c.B = (uint32_t)d_.B;
             c.Nq = (uint32_t)d_.Nq;
             c.Nkv = (uint32_t)d_.Nkv;
@@ -237,7 +238,7 @@ public:
         enc.withTemporaryTensor(ScratchSpec{{slots, d_.Hd}, DataType::f32}, [&](Tensor pO) {
             enc.withTemporaryTensor(ScratchSpec{{slots}, DataType::f32}, [&](Tensor pM) {
                 enc.withTemporaryTensor(ScratchSpec{{slots}, DataType::f32}, [&](Tensor pL) {
-                    FlashDecodingPartialConstants pc{};
+                    FlashDecodingPartialExtConstants pc{};
                     pc.B = (uint32_t)d_.B;
                     pc.Nq = (uint32_t)d_.Nq;
                     pc.Nkv = (uint32_t)d_.Nkv;
@@ -260,7 +261,7 @@ public:
                                            {posOrDummy, kRead}},
                                           {bytesOf(pc)}, ds);
                     enc.dispatch(partial);
-                    FlashDecodingReduceConstants rc{};
+                    FlashDecodingReduceExtConstants rc{};
                     rc.B = (uint32_t)d_.B;
                     rc.Nq = (uint32_t)d_.Nq;
                     rc.Hd = (uint32_t)d_.Hd;
@@ -304,8 +305,8 @@ private:
         const DataType t = q_.dataType;
         const bool alignedOk = aligned16(q_.data) && aligned16(k_.data) && aligned16(v_.data);
         const FdPlan f = fdPlan(t, d_, alignedOk, hasPos_ ? d_.cap : d_.Sk);
-        partialName_ = std::string("flash_decoding_partial_") + tag(t) + (f.lpk ? f.suffix() : std::string());
-        reduceName_ = std::string("flash_decoding_reduce_") + tag(out_.dataType);
+        partialName_ = std::string("flash_decoding_partial_") + tag(t) + (f.lpk ? f.suffix() : std::string("_ext"));
+        reduceName_ = std::string("flash_decoding_reduce_") + tag(out_.dataType) + "_ext";
         ngroups_ = f.ngroups;
         P_ = f.P;
     }
@@ -381,7 +382,7 @@ public:
             throw Error::unsupportedDataTypeCombination(
                 "DecodeAttention needs 16-byte aligned f16/bf16 data with head dim 64, 128, 256 or 512 (f32: 128, 256, 512).");
         partialName_ = std::string("flash_decoding_fresh_") + tag(t) + plan_.suffix();
-        reduceName_ = std::string("flash_decoding_reduce_") + tag(out_.dataType);
+        reduceName_ = std::string("flash_decoding_reduce_") + tag(out_.dataType) + "_ext";
     }
 
     std::vector<Binding> tensors() const override {
@@ -396,7 +397,7 @@ public:
         enc.withTemporaryTensor(ScratchSpec{{slots, d_.Hd}, DataType::f32}, [&](Tensor pO) {
             enc.withTemporaryTensor(ScratchSpec{{slots}, DataType::f32}, [&](Tensor pM) {
                 enc.withTemporaryTensor(ScratchSpec{{slots}, DataType::f32}, [&](Tensor pL) {
-                    FlashDecodingPartialConstants pc{};
+                    FlashDecodingPartialExtConstants pc{};
                     pc.B = (uint32_t)d_.B;
                     pc.Nq = (uint32_t)d_.Nq;
                     pc.Nkv = (uint32_t)d_.Nkv;
@@ -417,7 +418,7 @@ public:
                                            {pL, kWrite}, {pos_, kRead}, {wq_, kRead}, {wk_, kRead}, {invf_, kRead}},
                                           {bytesOf(pc), bytesOf(dc_)}, ds);
                     enc.dispatch(partial);
-                    FlashDecodingReduceConstants rc{};
+                    FlashDecodingReduceExtConstants rc{};
                     rc.B = (uint32_t)d_.B;
                     rc.Nq = (uint32_t)d_.Nq;
                     rc.Hd = (uint32_t)d_.Hd;
@@ -448,17 +449,17 @@ private:
 // Matmul (Matmul.swift)
 // ---------------------------------------------------------------------------
 
+// The streaming matvec for a transposeB product with m == 1 (the triples of
+// Matmul.swift:362-374, plus f16 triples): matvec_nk_stream_<x>_<w>_<o>,
+// suffixed _r<R> by the caller.
 std::string matvecNKName(DataType x, DataType w, DataType o) {
     using D = DataType;
-    // Matmul.swift:362-374, plus f16 triples
-    if (x == D::f32 && w == D::f32 && o == D::f32) return "matvec_nk_simd_f32_f32_f32";
-    if (x == D::f32 && w == D::bf16 && o == D::f32) return "matvec_nk_simd_f32_bf16_f32";
-    if (x == D::bf16 && w == D::bf16 && o == D::f32) return "matvec_nk_simd_bf16_bf16_f32";
-    if (x == D::bf16 && w == D::bf16 && o == D::bf16) return "matvec_nk_simd_bf16_bf16_bf16";
-    if (x == D::f32 && w == D::f16 && o == D::f32) return "matvec_nk_simd_f32_f16_f32";
-    if (x == D::f16 && w == D::f16 && o == D::f32) return "matvec_nk_simd_f16_f16_f32";
-    if (x == D::f16 && w == D::f16 && o == D::f16) return "matvec_nk_simd_f16_f16_f16";
-    return "";
+    const bool ok = (x == D::f32 && w == D::f32 && o == D::f32) || (x == D::f32 && w == D::bf16 && o == D::f32) ||
+                    (x == D::bf16 && w == D::bf16 && o == D::f32) || (x == D::bf16 && w == D::bf16 && o == D::bf16) ||
+                    (x == D::f32 && w == D::f16 && o == D::f32) || (x == D::f16 && w == D::f16 && o == D::f32) ||
+                    (x == D::f16 && w == D::f16 && o == D::f16);
+    if (!ok) return "";
+    return std::string("matvec_nk_stream_") + tag(x) + "_" + tag(w) + "_" + tag(o);
 }
 
 std::string plainName(const char *base, DataType x, DataType w, DataType o) {
@@ -651,7 +652,7 @@ std::unique_ptr<Kernel> makeMatmul(const Tensor &a, const Tensor &b, const Tenso
                                                             tag(a.dataType) + ", " + tag(b.dataType) + ", " + tag(c.dataType) + ".");
             if (k > kMaxStagedK) throw Error::tensorShapeMismatch("matvec K above " + std::to_string(kMaxStagedK) + " is not supported.");
             const int R = matvecRows(n);
-            if (R != 4) fn += "_r" + std::to_string(R);
+            fn += "_r" + std::to_string(R);
             return std::make_unique<FixedDispatch>(fn, binds, std::vector<std::vector<uint8_t>>{bytesOf(mc)},
                                                    grid1(streamBlocks(cdiv(n, R)), kBlock, (size_t)std::max<int64_t>(k, 1) * 4));
         }
@@ -678,7 +679,8 @@ std::unique_ptr<Kernel> makeMatmul(const Tensor &a, const Tensor &b, const Tenso
                                                    grid1(cdiv(m, tile.bm) * cdiv(n, tile.bn), tile.threads));
         }
     }
-    std::string fn = plainName("matmul", a.dataType, b.dataType, c.dataType);
+    // the SIMT tiles (matmul.hip) in the place of the reference's matmul_typed
+    std::string fn = plainName("matmul_tiled", a.dataType, b.dataType, c.dataType);
     if (fn.empty())
         throw Error::unsupportedDataTypeCombination(std::string("Unsupported matmul data type combination: ") +
                                                     tag(a.dataType) + ", " + tag(b.dataType) + ", " + tag(c.dataType) + ".");
@@ -935,7 +937,7 @@ public:
     std::string describe() const override { return "argmax_partial,argmax_finish"; }
     void encode(KernelCommandEncoder &enc) const override {
         if (rows_ == 0) return;
-        ArgmaxConstants ac{(uint32_t)rows_, (uint32_t)n_, (uint32_t)slices_};
+        ArgmaxSliceConstants ac{(uint32_t)rows_, (uint32_t)n_, (uint32_t)slices_};
         enc.withTemporaryTensor(ScratchSpec{{rows_ * slices_}, DataType::f32}, [&](Tensor pv) {
             enc.withTemporaryTensor(ScratchSpec{{rows_ * slices_}, DataType::i32}, [&](Tensor pi) {
                 DispatchSize ds;
@@ -1119,13 +1121,21 @@ std::unique_ptr<Kernel> KVCacheWrite(const Tensor &source, const Tensor &cache, 
         if (position->dataType != D::i32) throw Error::unsupportedDataTypeCombination("position tensor must be i32");
         requireElements(*position, 1, "position");
     }
-    KVCacheWriteConstants kc{(uint32_t)batch, (uint32_t)kvHeads, (uint32_t)newLen, (uint32_t)maxLen, (uint32_t)headDim,
-                             (uint32_t)std::max<int64_t>(offset, 0), position ? 1u : 0u};
     const int64_t run = 16 / stride(s);
     const int64_t runs = batch * kvHeads * newLen * cdiv(headDim, run);
     const int64_t blocks = std::clamp<int64_t>(cdiv(runs, kBlock), 1, 4096);
-    const Tensor &pos = position ? *position : source;
-    return std::make_unique<FixedDispatch>(fn, std::vector<Binding>{{source, kRead}, {cache, kWrite}, {pos, kRead}},
+    if (!position) {
+        // the reference's kernel and constants (KVCacheWrite.metal:6-11)
+        KVCacheWriteConstants kc{(uint32_t)batch, (uint32_t)kvHeads, (uint32_t)newLen, (uint32_t)maxLen,
+                                 (uint32_t)headDim, (uint32_t)offset};
+        return std::make_unique<FixedDispatch>(fn, std::vector<Binding>{{source, kRead}, {cache, kWrite}},
+                                               std::vector<std::vector<uint8_t>>{bytesOf(kc)},
+                                               grid1(runs ? blocks : 0, kBlock));
+    }
+    KVCacheWriteExtConstants kc{(uint32_t)batch, (uint32_t)kvHeads, (uint32_t)newLen, (uint32_t)maxLen, (uint32_t)headDim,
+                                (uint32_t)std::max<int64_t>(offset, 0), 1u};
+    return std::make_unique<FixedDispatch>(std::string(fn) + "_ext",
+                                           std::vector<Binding>{{source, kRead}, {cache, kWrite}, {*position, kRead}},
                                            std::vector<std::vector<uint8_t>>{bytesOf(kc)}, grid1(runs ? blocks : 0, kBlock));
 }
 
@@ -1455,9 +1465,10 @@ std::unique_ptr<Kernel> EmbeddingGather(const Tensor &ids, const Tensor &table, 
     else if (table.dataType == D::bf16 && out.dataType == D::f32) fn = "embedding_gather_bf16_to_f32";
     else throw Error::unsupportedDataTypeCombination("Unsupported EmbeddingGather data type combination.");
     requireElements(out, N * H, "EmbeddingGather out");
-    EmbeddingGatherConstants ec{(uint32_t)N, (uint32_t)H, (uint32_t)V};
+    EmbeddingGatherExtConstants ec{(uint32_t)N, (uint32_t)H, (uint32_t)V};
     const int64_t runs = N * cdiv(H, 16 / stride(table.dataType));
-    return std::make_unique<FixedDispatch>(fn, std::vector<Binding>{{ids, kRead}, {table, kRead}, {out, kWrite}},
+    return std::make_unique<FixedDispatch>(std::string(fn) + "_ext",
+                                           std::vector<Binding>{{ids, kRead}, {table, kRead}, {out, kWrite}},
                                            std::vector<std::vector<uint8_t>>{bytesOf(ec)},
                                            grid1(runs ? std::clamp<int64_t>(cdiv(runs, kBlock), 1, 4096) : 0, kBlock));
 }
@@ -1509,8 +1520,9 @@ std::unique_ptr<Kernel> Matmul(const Tensor &a, const AffineQuantizedTensor &b, 
         ds.grid = dim3((unsigned)streamBlocks(units), (unsigned)m, 1);
     } else {
         if (m > 65535) throw Error::tensorShapeMismatch("quantized Matmul supports at most 65535 rows of a.");
-        fn = "aq_matvec_simd4_" + combo3;  // 4 waves x 4 rows per block
-        ds.grid = dim3((unsigned)cdiv(n, 16), (unsigned)m, 1);
+        // the reference's kernel: a 32-lane half-wave per 4 rows, 8 per block
+        fn = "aq_matvec_simd4_" + combo3;
+        ds.grid = dim3((unsigned)cdiv(cdiv(n, 4), kBlock / 32), (unsigned)m, 1);
     }
     if (m == 0 || n == 0) ds.grid = dim3(0, 1, 1);
     return std::make_unique<FixedDispatch>(fn, binds, std::vector<std::vector<uint8_t>>{bytesOf(qc)}, ds);
@@ -1544,10 +1556,10 @@ std::unique_ptr<Kernel> EmbeddingGather(const Tensor &ids, const AffineQuantized
     requireElements(table.scales, V * (H / 64), "EmbeddingGather quantized scales");
     if (table.hasBiases) requireElements(table.biases, V * (H / 64), "EmbeddingGather quantized biases");
     requireElements(out, T * H, "EmbeddingGather out");
-    AffineQEmbeddingGatherConstants gc{(uint32_t)T, (uint32_t)H, (uint32_t)(H / 64), (uint32_t)(H / 8),
-                                       table.hasBiases ? 1u : 0u, (uint32_t)V};
+    AffineQEmbeddingGatherExtConstants gc{(uint32_t)T, (uint32_t)H, (uint32_t)(H / 64), (uint32_t)(H / 8),
+                                          table.hasBiases ? 1u : 0u, (uint32_t)V};
     const Tensor &bias = table.hasBiases ? table.biases : table.scales;
-    const std::string fn = std::string("aq_embedding_gather_bf16_") + tag(out.dataType) + "_b4_g64";
+    const std::string fn = std::string("aq_embedding_gather_bf16_") + tag(out.dataType) + "_b4_g64_ext";
     const int64_t words = T * (H / 8);
     return std::make_unique<FixedDispatch>(
         fn, std::vector<Binding>{{ids, kRead}, {table.packedValues, kRead}, {table.scales, kRead}, {bias, kRead}, {out, kWrite}},

@@ -161,10 +161,35 @@ struct FunctionAttributes {
     int privateBytes = 0;
 };
 
+// A kernel's explicit parameters as its code object's metadata lists them
+// (code_object.cpp): device pointers and by-value constants blocks.
+struct KernelArg {
+    bool pointer = false;
+    uint32_t size = 0;
+    uint32_t offset = 0;
+};
+
+struct KernelLayout {
+    std::vector<KernelArg> args;
+    uint32_t kernargBytes = 0;
+    uint32_t maxThreads = 0;
+    uint32_t staticLds = 0;
+    std::string str() const;
+    // Throws invalidArgument unless the launch binds exactly `nbuffers`
+    // pointers then one block of each of `constantSizes`, as the kernel takes.
+    void check(const std::string &name, size_t nbuffers, const std::vector<size_t> &constantSizes) const;
+};
+
+// Every kernel's layout in a code object (ELF or clang offload bundle);
+// throws invalidArgument for a malformed file.
+std::map<std::string, KernelLayout> readKernelLayouts(const std::vector<uint8_t> &file);
+std::map<std::string, KernelLayout> readKernelLayouts(const std::string &path);
+
 struct Function {
     hipFunction_t fn = nullptr;
     std::string name;
     FunctionAttributes attrs;
+    const KernelLayout *layout = nullptr;  // null when the code object's metadata was not readable
 };
 
 class KernelLibrary {
@@ -184,6 +209,7 @@ public:
 
 private:
     std::vector<hipModule_t> modules_;
+    std::map<std::string, KernelLayout> layouts_;
     std::map<std::string, std::unique_ptr<Function>> cache_;
     mutable std::mutex mu_;
     int device_ = 0;

@@ -185,6 +185,12 @@ KernelLibrary::KernelLibrary(const std::string &pathIn) {
     }
     if (files.empty()) throw Error(POPCORN_ERR_KERNEL_FUNCTION_NOT_FOUND, "no code objects in " + path);
     for (const std::string &f : files) {
+        // parameter layouts for launch checks; a code object whose metadata
+        // cannot be read still loads, its launches go unchecked
+        try {
+            for (auto &kv : readKernelLayouts(f)) layouts_.emplace(kv.first, std::move(kv.second));
+        } catch (const Error &) {
+        }
         hipModule_t m = nullptr;
         hipError_t err = hipModuleLoad(&m, f.c_str());
         if (err != hipSuccess) {
@@ -217,6 +223,7 @@ const Function &KernelLibrary::function(const std::string &fname) {
             if (hipFuncGetAttribute(&v, HIP_FUNC_ATTRIBUTE_LOCAL_SIZE_BYTES, fn) == hipSuccess) f->attrs.privateBytes = v;
             (void)hipGetLastError();
             f->attrs.waveSize = 64;
+            if (auto it = layouts_.find(fname); it != layouts_.end()) f->layout = &it->second;
             const Function &ref = *f;
             cache_[fname] = std::move(f);
             return ref;
@@ -275,6 +282,11 @@ void KernelCommandEncoder::dispatch(const DispatchKernel &kernel) {
         throw Error::invalidArgument("block of " + std::to_string(ds.block.x * ds.block.y * ds.block.z) +
                                      " threads exceeds the limit of " + kernel.functionName());
     const std::vector<std::vector<uint8_t>> consts = kernel.constants();
+    if (fn.layout) {
+        std::vector<size_t> sizes;
+        for (const auto &c : consts) sizes.push_back(c.size());
+        fn.layout->check(kernel.functionName(), bindings.size(), sizes);
+    }
     std::vector<void *> ptrs(bindings.size());
     std::vector<void *> params;
     params.reserve(bindings.size() + consts.size());

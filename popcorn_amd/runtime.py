@@ -331,6 +331,14 @@ class KernelLibrary:
     def cached_function_count(self) -> int:
         return int(lib().popcorn_library_cached_function_count(self.handle))
 
+    def layout(self, name: str) -> dict:
+        """The kernel's parameter list from its code object: leading device
+        pointers, then the byte size of each by-value block."""
+        L = _capi.KernelLayout()
+        check(lib().popcorn_function_layout(self.function(name).handle, C.byref(L)))
+        return {"buffers": L.nbuffers, "constants": list(L.constant_sizes[:L.nconstants]),
+                "max_threads": L.max_threads_per_block}
+
     def launch(self, name: str, grid, block, buffers: Sequence[int], constants: Sequence[bytes] = (),
                dynamic_lds: int = 0, stream: Optional[Stream] = None) -> None:
         """Raw launch: device pointers in order, then constants blocks by value."""
@@ -409,6 +417,14 @@ class KernelScratchAllocator:
 
         self._cb = (_capi.BORROW_FN(_borrow), _capi.RELEASE_FN(_release))
         return _capi.ScratchAllocatorDesc(None, self._cb[0], self._cb[1])
+
+
+def code_object_layout(path: str, kernel: str) -> dict:
+    """A kernel's parameter list read from a code-object file (no GPU needed)."""
+    L = _capi.KernelLayout()
+    check(lib().popcorn_code_object_layout(path.encode(), kernel.encode(), C.byref(L)))
+    return {"buffers": L.nbuffers, "constants": list(L.constant_sizes[:L.nconstants]),
+            "max_threads": L.max_threads_per_block}
 
 
 def scratch_spec_byte_count(shape: Sequence[int], dtype: str) -> int:

@@ -1,6 +1,8 @@
 """CPU tests of the C ABI: the library loads, exports every function that
 include/*.h declares, and the descriptors validate and route without a GPU
 (fake device addresses: nothing is launched)."""
+import glob
+import json
 import os
 import re
 
@@ -101,13 +103,13 @@ def test_flash_attention_routing_names():
     k = T([1, 4, 4352, 256])
     kern = pa.Kernels.FlashAttention(q, k, k, out=o, scale=1 / 16, batch=1, query_heads=8, kv_heads=4,
                                      query_len=1, key_len=4097, head_dim=256, key_capacity=4352)
-    assert kern.function_names == ["flash_decoding_partial_bf16_l32_c1_g2", "flash_decoding_reduce_bf16"]
+    assert kern.function_names == ["flash_decoding_partial_bf16_l32_c1_g2", "flash_decoding_reduce_bf16_ext"]
     f = pa.Kernels.FlashAttention(T([1, 4, 1, 64], "f32"), T([1, 1, 129, 64], "f32"), T([1, 1, 129, 64], "f32"),
                                   T([1, 4, 1, 64], "f32"), scale=0.125)
     assert f.function_names[0] == "flash_decoding_partial_f32_l16_c1_g4"
     g = pa.Kernels.FlashAttention(T([1, 2, 1, 80]), T([1, 1, 9, 80]), T([1, 1, 9, 80]), T([1, 2, 1, 80], "f32"),
                                   scale=0.1)
-    assert g.function_names == ["flash_decoding_partial_bf16", "flash_decoding_reduce_f32"]
+    assert g.function_names == ["flash_decoding_partial_bf16_ext", "flash_decoding_reduce_f32_ext"]
 
 
 def test_flash_attention_validation_codes():
@@ -138,12 +140,12 @@ def test_flash_attention_validation_codes():
 def test_matmul_routing_and_validation():
     x = T([1, 2304])
     # 4 rows per unit for long outputs (the LM head), 1 otherwise
-    assert pa.Kernels.Matmul(x, T([32768, 2304]), T([1, 32768]), True).describe() == "matvec_nk_simd_bf16_bf16_bf16"
-    assert pa.Kernels.Matmul(x, T([9216, 2304]), T([1, 9216]), True).describe() == "matvec_nk_simd_bf16_bf16_bf16_r1"
+    assert pa.Kernels.Matmul(x, T([32768, 2304]), T([1, 32768]), True).describe() == "matvec_nk_stream_bf16_bf16_bf16_r4"
+    assert pa.Kernels.Matmul(x, T([9216, 2304]), T([1, 9216]), True).describe() == "matvec_nk_stream_bf16_bf16_bf16_r1"
     assert pa.Kernels.Matmul(T([1, 9216]), T([2304, 9216]), T([1, 2304]), True).describe() == \
-        "matvec_nk_simd_bf16_bf16_bf16_r1"
+        "matvec_nk_stream_bf16_bf16_bf16_r1"
     assert pa.Kernels.Matmul(x, T([2304, 300]), T([1, 300]), False).describe() == "matvec_bf16_bf16_bf16"
-    assert pa.Kernels.Matmul(T([4, 8], "f32"), T([8, 3], "f32"), T([4, 3], "f32")).describe() == "matmul"
+    assert pa.Kernels.Matmul(T([4, 8], "f32"), T([8, 3], "f32"), T([4, 3], "f32")).describe() == "matmul_tiled"
     with pytest.raises(pa.PopcornError) as e:  # Matmul.swift:85-87
         pa.Kernels.Matmul(x, T([9216, 2300]), T([1, 9216]), True)
     assert e.value.code == pa.PopcornError.TENSOR_SHAPE_MISMATCH
@@ -256,7 +258,7 @@ def test_quantized_validation_and_routing():
     assert e.value.code == E.TENSOR_SHAPE_MISMATCH
     emb = _q4(256000, 2304)
     ids = T([3], "i32")
-    assert pa.Kernels.EmbeddingGather(ids, emb, T([3, 2304])).describe() == "aq_embedding_gather_bf16_bf16_b4_g64"
+    assert pa.Kernels.EmbeddingGather(ids, emb, T([3, 2304])).describe() == "aq_embedding_gather_bf16_bf16_b4_g64_ext"
     with pytest.raises(E) as e:
         pa.Kernels.EmbeddingGather(T([3], "i64"), emb, T([3, 2304]))
     assert e.value.code == E.UNSUPPORTED_DATA_TYPE_COMBINATION
@@ -269,10 +271,10 @@ def test_gated_mlp_validation_and_routing():
     E = pa.PopcornError
     k = pa.Kernels.GatedMLP(T([2304]), T([2304], "f32"), T([9216, 2304]), T([9216, 2304]), T([2304, 9216]),
                             T([2304]), eps=1e-6)
-    assert k.function_names == ["gated_mlp_gate_up_bf16_r1", "matvec_nk_simd_bf16_bf16_bf16_r1"]
+    assert k.function_names == ["gated_mlp_gate_up_bf16_r1", "matvec_nk_stream_bf16_bf16_bf16_r1"]
     r = pa.Kernels.GatedMLPResidual(T([2304]), T([2304]), T([2304], "f32"), T([2304], ptr=FAKE + 4096), T([2304], "f32"),
                                     T([9216, 2304]), T([9216, 2304]), T([2304, 9216]), T([2304]), eps=1e-6)
-    assert r.function_names == ["gated_mlp_gate_up_bf16_r1_res", "matvec_nk_simd_bf16_bf16_bf16_r1"]
+    assert r.function_names == ["gated_mlp_gate_up_bf16_r1_res", "matvec_nk_stream_bf16_bf16_bf16_r1"]
     with pytest.raises(E) as e:
         pa.Kernels.GatedMLP(T([2304]), None, T([9216, 2304]), T([9216, 2300]), T([2304, 9216]), T([2304]), eps=1e-6)
     assert e.value.code == E.TENSOR_SHAPE_MISMATCH
@@ -331,3 +333,55 @@ def test_prefill_routes_to_tiled():
     q = T([1, 16, 2048, 256], "f16")
     k = pa.Kernels.FlashAttention(q, q, q, out=T([1, 16, 2048, 256], "f16", ptr=FAKE + 2 ** 32), scale=1 / 16)
     assert k.function_names == ["flash_attention_tiled_f16_f16_d256", "flash_attention_split_merge_f16_d256"]
+
+
+# Reference kernels outside the decode hot path (the reference's own unfused
+# attention, LayerNorm/GroupNorm, softmax, slicing, broadcast add, soft-cap):
+# not built here.
+OUT_OF_SCOPE = ("attention_output", "attention_scores", "broadcast_add", "groupnorm", "layernorm", "logit_softcap",
+                "row_slice2d", "slice2d", "softmax")
+
+
+def test_reference_named_kernels_take_the_reference_parameter_lists():
+    # tests/golden/reference_kernel_abi.json lists every kernel the reference
+    # instantiates with its parameter list (device pointers, then the byte
+    # size of each constants block), written from the Metal sources by
+    # tests/golden/make_reference_abi.py. Every one on the hot path is
+    # exported under the same name and takes exactly that list, read back
+    # from this build's code objects; a raw launch packed like the
+    # reference's therefore matches the kernel.
+    ref = json.load(open(os.path.join(ROOT, "tests", "golden", "reference_kernel_abi.json")))
+    assert ref["kv_cache_write"] == {"buffers": 2, "constants": [24], "source": "Sources/Popcorn/Kernels/KVCacheWrite.metal:7"}
+    assert ref["flash_decoding_partial_bf16"]["buffers"] == 6 and ref["flash_decoding_partial_bf16"]["constants"] == [36]
+    files = sorted(glob.glob(os.path.join(pa.KERNEL_DIR, "*.hsaco")))
+    assert files
+    required = [n for n in ref if not n.startswith(OUT_OF_SCOPE)]
+    assert len(required) == 58
+    for name in required:
+        got = None
+        for f in files:
+            try:
+                got = pa.code_object_layout(f, name)
+                break
+            except pa.PopcornError as e:
+                assert e.code == -1006, e
+        assert got is not None, f"{name} is not exported"
+        assert (got["buffers"], got["constants"]) == (ref[name]["buffers"], ref[name]["constants"]), (name, got, ref[name])
+
+
+def test_extended_kernels_have_names_of_their_own():
+    # the forms with this build's extra parameters (device position, KV row
+    # stride, bounds on table ids) carry an _ext suffix and their own
+    # constants blocks
+    f = os.path.join(pa.KERNEL_DIR, "kv_cache_write.hsaco")
+    assert pa.code_object_layout(f, "kv_cache_write_bf16_ext")["buffers"] == 3
+    assert pa.code_object_layout(f, "kv_cache_write_bf16_ext")["constants"] == [28]
+    fd = os.path.join(pa.KERNEL_DIR, "flash_decoding.hsaco")
+    assert pa.code_object_layout(fd, "flash_decoding_partial_bf16_ext")["constants"] == [48]
+    assert pa.code_object_layout(fd, "flash_decoding_reduce_bf16_ext")["constants"] == [20]
+    with pytest.raises(pa.PopcornError) as e:
+        pa.code_object_layout(fd, "no_such_kernel")
+    assert e.value.code == -1006
+    with pytest.raises(pa.PopcornError) as e:
+        pa.code_object_layout(os.path.join(ROOT, "README.md"), "kv_cache_write")
+    assert e.value.code == -1100

@@ -5,7 +5,9 @@ import numpy as np
 import pytest
 
 import oracle as O
+import flips
 from conftest import assert_out, half_ulp
+from flips import assert_any
 from gpu_util import download, gpu_env
 
 pytestmark = pytest.mark.gpu
@@ -175,4 +177,131 @@ def test_gemma2_2b_shape_decodes(env, attention_block, weight_bits):
     np.testing.assert_array_equal(dec.history(4096, 8), hist)
     np.testing.assert_array_equal(dec.tensor("logits").numpy(stream), logits)
     assert dec.step_bytes(4096) > (5.0e9 if weight_bits == 16 else 1.4e9)
+    dec.close()
+
+
+LAYER_WEIGHTS = [("in_norm", "norm_in"), ("qkv", "w_qkv"), ("o", "w_o"), ("post_attn_norm", "norm_post_attn"),
+                 ("pre_ffn_norm", "norm_pre_ffn"), ("gate", "w_gate"), ("up", "w_up"), ("down", "w_down"),
+                 ("post_ffn_norm", "norm_post_ffn")]
+
+
+def test_gemma2_2b_step_matches_oracle(env):
+    # BASELINE config 4 at full size, one greedy step at position 4096 on the
+    # decoder's own random weights, against the oracle's composition of the
+    # reference's step (Gemma4TextInference.swift:184-206, :312-436), run
+    # layer by layer with every activation stored in bf16 (and again in f32
+    # for the precision of that dataflow). Checked:
+    #  * end to end, in the form of test_small_decoder_matches_oracle's bar:
+    #    over 26 layers a rounding flip anywhere propagates through the
+    #    residual stream, so the GPU's bf16 dataflow and the oracle's are two
+    #    equally good bf16 approximations of the f32 ideal; logits within
+    #    twice the oracle's bf16-vs-f32 gap of the bf16 composition, and the
+    #    token its argmax up to a near tie;
+    #  * every layer's new K/V row against the composition's, to the same
+    #    form of bar at that layer;
+    #  * tightly, on the GPU's own intermediates of this step: the last
+    #    layer's attention (cache rows 0..4096), its O projection, its gated
+    #    MLP, and the LM head (last post-FFN norm + residual, final norm,
+    #    256000 x 2304 tied head), each to the 2e-3 bar over the rounding
+    #    outcomes of the norm in front of it.
+    pa, lib, stream, enc = env
+    import popcorn_amd.decoder as D
+
+    cfg = D.DecoderConfig(graph_steps=1)
+    dec = D.Decoder(lib, stream, cfg)
+    dec.randomize(seed=0)
+    H, Nq, Nkv, Hd, F, L = cfg.hidden, cfg.query_heads, cfg.kv_heads, cfg.head_dim, cfg.ffn, cfg.layers
+    assert (L, H, Nq, Nkv, Hd, F, cfg.vocab) == (26, 2304, 8, 4, 256, 9216, 256000)
+    token, pos, eps = 123, 4096, cfg.eps
+    dec.reset(token, pos)
+    dec.step(1, use_graph=False)
+    got_tok, got_pos = dec.read()
+    assert got_pos == pos + 1
+    logits = dec.tensor("logits").numpy(stream)
+
+    emb = _weight(dec, "embedding", 0, stream)
+    x16 = O.round_to(O.scalar_mul(emb[token], np.float32(np.sqrt(np.float32(H)))), O.BF16)
+    x32 = x16.copy()
+    last = {}
+    for l in range(L):
+        W = {n: _weight(dec, t, l, stream) for n, t in LAYER_WEIGHTS}
+        kc = download(dec.tensor("k_cache", l), stream)[0]
+        vc = download(dec.tensor("v_cache", l), stream)[0]
+        gpu_k, gpu_v = kc[:, pos].copy(), vc[:, pos].copy()  # the rows this step wrote
+        k16, v16, k32, v32 = kc.copy(), vc.copy(), kc.copy(), vc.copy()
+        kw = dict(H=H, Nq=Nq, Nkv=Nkv, Hd=Hd, F=F, eps=eps, scale=cfg.attn_scale)
+        O.decoder_layer(W, x16, k16, v16, pos, act_tag=O.BF16, **kw)
+        O.decoder_layer(W, x32, k32, v32, pos, act_tag=O.F32, **kw)
+        for got, w16, w32, what in ((gpu_k, k16[:, pos], k32[:, pos], "K"), (gpu_v, v16[:, pos], v32[:, pos], "V")):
+            # two bf16 dataflows (the GPU's and the oracle's) from one f32
+            # ideal: each is off it by about the oracle's bf16-vs-f32 gap
+            noise = float(np.abs(w16 - w32).max())
+            err = float(np.abs(got - w16).max())
+            assert err <= 2 * noise + 2e-3 * float(np.abs(w16).max()), \
+                f"layer {l} new {what} row off by {err:.3e}; the bf16 dataflow's own gap is {noise:.3e}"
+        if l == L - 1:
+            last = dict(W=W, kc=kc, vc=vc)
+    fin = download(dec.tensor("final_norm"), stream)
+    ref16 = O.matmul(O.round_to(O.rmsnorm(x16, fin, eps), O.BF16), emb, 1, H, cfg.vocab, True).ravel()
+    ref32 = O.matmul(O.rmsnorm(x32, fin, eps), emb, 1, H, cfg.vocab, True).ravel()
+    noise = float(np.abs(ref16 - ref32).max())
+    err = float(np.abs(logits - ref16).max())
+    assert err <= max(2 * noise, 2e-3), f"logits off by {err:.3e}; the bf16 dataflow's own gap is {noise:.3e}"
+    best = int(O.argmax(ref16[None])[0])
+    if got_tok != best:
+        assert abs(ref16[got_tok] - ref16[best]) <= 4 * max(noise, 2e-3), (got_tok, best)
+    assert int(np.argmax(logits)) == got_tok or logits[got_tok] == logits.max()
+
+    # the last layer and the head on the GPU's own intermediates
+    W = last["W"]
+    q = download(dec.tensor("q"), stream).reshape(1, Nq, 1, Hd)
+    attn = download(dec.tensor("attn"), stream)
+    ref_attn = O.attention_naive(q, last["kc"][None], last["vc"][None], cfg.attn_scale, key_len=pos + 1)
+    assert_out(attn, ref_attn.ravel(), 2e-3, "bf16", "last layer attention")
+    o = download(dec.tensor("o"), stream)
+    assert_out(o, O.matmul(attn[None], W["o"], 1, Nq * Hd, H, True).ravel(), 2e-3, "bf16", "last O projection")
+    x2 = download(dec.tensor("x2"), stream)
+    mlp = download(dec.tensor("mlp"), stream)
+    refs = [flips.mlp_from_normed(n, W["gate"], W["up"], W["down"], O.BF16)[1]
+            for n in flips.norm_candidates(x2, W["pre_ffn_norm"], eps, O.BF16)]
+    assert_any(mlp, refs, 2e-3, "bf16", "last gated MLP")
+    heads = [O.matmul(n, emb, 1, H, cfg.vocab, True).ravel()
+             for x in flips.residual_candidates(x2, mlp, W["post_ffn_norm"], eps, O.BF16)
+             for n in flips.norm_candidates(x, fin, eps, O.BF16)]
+    assert_any(logits, heads, 2e-3, "f32", "LM head (post-FFN residual + final norm)")
+    dec.close()
+
+
+def test_steps_past_the_cache_are_refused(env):
+    # a step at position p writes KV row p: with max_seq 64, positions 62 and
+    # 63 decode, position 64 is refused with tensorShapeMismatch before
+    # anything is enqueued, and the caches are left as they were
+    pa, lib, stream, enc = env
+    import popcorn_amd.decoder as D
+
+    cfg = _small(D, graph_steps=2)
+    dec = D.Decoder(lib, stream, cfg)
+    dec.randomize(seed=3)
+    dec.reset(5, 62)
+    dec.step(2, use_graph=False)
+    assert dec.read()[1] == 64
+    snap = [dec.tensor(n, l).numpy(stream).copy() for l in range(cfg.layers) for n in ("k_cache", "v_cache")]
+    for steps, graph in ((1, False), (1, True), (3, True)):
+        with pytest.raises(pa.PopcornError) as e:
+            dec.step(steps, use_graph=graph)
+        assert e.value.code == pa.PopcornError.TENSOR_SHAPE_MISMATCH
+    dec.reset(5, 60)
+    with pytest.raises(pa.PopcornError):
+        dec.step(5, use_graph=True)  # 60..64: the last one leaves the cache
+    assert dec.read() == (5, 60)
+    now = [dec.tensor(n, l).numpy(stream) for l in range(cfg.layers) for n in ("k_cache", "v_cache")]
+    for a, b in zip(snap, now):
+        np.testing.assert_array_equal(a, b)
+    dec.step(4, use_graph=True)  # 60..63 fit
+    assert dec.read()[1] == 64
+    # timing the step's tail kernel (which advances the position) restores it
+    dec.reset(7, 10)
+    ms, n = dec.time_kernel("decode_next_token_bf16", reps=3)
+    assert n == 3 and ms > 0
+    assert dec.read() == (7, 10)
     dec.close()

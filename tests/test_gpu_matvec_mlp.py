@@ -38,7 +38,7 @@ def test_matmul_reference_kats(env):
     assert c1.numpy(stream).ravel().tolist() == [58, 64, 139, 154]
     assert c2.numpy(stream).ravel().tolist() == [58, 64, 139, 154]
     assert y.numpy(stream).ravel().tolist() == [58, 64]
-    assert pa.Kernels.Matmul(x, bt, y, True).function_names == ["matvec_nk_simd_f32_f32_f32_r1"]
+    assert pa.Kernels.Matmul(x, bt, y, True).function_names == ["matvec_nk_stream_f32_f32_f32_r1"]
 
 
 TRIPLES = [("f32", "f32", "f32"), ("f32", "bf16", "f32"), ("bf16", "bf16", "f32"), ("bf16", "bf16", "bf16"),

@@ -108,7 +108,7 @@ def test_quantized_embedding_gather(env, ot):
     ids = np.array([0, 999, 17, 17, 1000, -1], np.int32)  # the last two are outside the table
     out = pa.Tensor.empty([ids.size, H], ot)
     k = pa.Kernels.EmbeddingGather(pa.Tensor.from_numpy(ids, "i32"), _qtensor(pa, packed, s, b, V, H), out)
-    assert k.function_names == [f"aq_embedding_gather_bf16_{ot}_b4_g64"]
+    assert k.function_names == [f"aq_embedding_gather_bf16_{ot}_b4_g64_ext"]
     enc.encode(k)
     stream.synchronize()
     got = download(out, stream).reshape(ids.size, H)
