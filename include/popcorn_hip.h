@@ -307,6 +307,28 @@ popcorn_status_t popcorn_kernel_flash_attention_dims(
     popcorn_attention_mask_t mask, int64_t key_capacity, const popcorn_tensor_t *position,
     popcorn_kernel_t *kernel);
 
+/* No counterpart in the reference: popcorn_kernel_flash_attention_dims'
+ * split-KV attention (the partial kernel and the log-sum-exp combine) in one
+ * call that allocates nothing, for callers that cannot call hipMalloc (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation). The partials live in a static device array of
+ * POPCORN_NO_ALLOC_SCRATCH_BYTES per GPU, part of this library and held
+ * until the process ends, instead of a borrowed scratch buffer; a call needing
+ * more (B * Nq * Sq * P * (Hd + 2) * 4 bytes, P the partitions chosen for the
+ * shape) fails with -1012 (workspaceExhausted) and launches nothing. Same
+ * arguments, validation, kernels and results as the split-KV route of the
+ * descriptor (whatever route the descriptor would take for the shape);
+ * enqueued on `stream`. Calls that overlap on one GPU share the array and
+ * race: order them on one stream. */
+#define POPCORN_NO_ALLOC_SCRATCH_BYTES ((size_t)4 << 20)
+popcorn_status_t popcorn_flash_decoding_no_alloc(popcorn_library_t library, popcorn_stream_t stream,
+                                                 const popcorn_tensor_t *q, const popcorn_tensor_t *k,
+                                                 const popcorn_tensor_t *v, const popcorn_tensor_t *out, int64_t batch,
+                                                 int64_t query_heads, int64_t kv_heads, int64_t query_len,
+                                                 int64_t key_len, int64_t head_dim, float scale,
+                                                 popcorn_attention_mask_t mask, int64_t key_capacity,
+                                                 const popcorn_tensor_t *position);
+
 /* Kernels.Matmul(_:_:into:transposeB:) (Matmul.swift:68-93); m == 1 routes to
  * the matvec (Matmul.swift:22-32). */
 popcorn_status_t popcorn_kernel_matmul(const popcorn_tensor_t *a, const popcorn_tensor_t *b,

@@ -151,6 +151,9 @@ PROTOTYPES = {
     "popcorn_kernel_flash_attention_dims": (_st, [_T, _T, _T, _T, C.c_int64, C.c_int64, C.c_int64, C.c_int64,
                                                   C.c_int64, C.c_int64, C.c_float, AttentionMaskDesc, C.c_int64,
                                                   _T, _K]),
+    "popcorn_flash_decoding_no_alloc": (_st, [C.c_void_p, C.c_void_p, _T, _T, _T, _T, C.c_int64, C.c_int64,
+                                              C.c_int64, C.c_int64, C.c_int64, C.c_int64, C.c_float,
+                                              AttentionMaskDesc, C.c_int64, _T]),
     "popcorn_kernel_matmul": (_st, [_T, _T, _T, C.c_int32, _K]),
     "popcorn_kernel_matmul_dims": (_st, [_T, _T, _T, C.c_int64, C.c_int64, C.c_int64, C.c_int32, _K]),
     "popcorn_kernel_rmsnorm": (_st, [_T, _T, _T, C.c_int32, C.c_float, C.c_int32, _K]),

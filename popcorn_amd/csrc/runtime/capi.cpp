@@ -498,6 +498,23 @@ popcorn_status_t popcorn_kernel_flash_attention_dims(const popcorn_tensor_t *q, 
     });
 }
 
+popcorn_status_t popcorn_flash_decoding_no_alloc(popcorn_library_t library, popcorn_stream_t stream,
+                                                 const popcorn_tensor_t *q, const popcorn_tensor_t *k,
+                                                 const popcorn_tensor_t *v, const popcorn_tensor_t *out, int64_t batch,
+                                                 int64_t query_heads, int64_t kv_heads, int64_t query_len,
+                                                 int64_t key_len, int64_t head_dim, float scale,
+                                                 popcorn_attention_mask_t mask, int64_t key_capacity,
+                                                 const popcorn_tensor_t *position) {
+    return guarded([&] {
+        need(library, "library");
+        Tensor pos;
+        if (position) pos = Tensor::fromC(*position);
+        Kernels::FlashDecodingNoAlloc(*library->lib, S(stream), T(q, "q"), T(k, "k"), T(v, "v"), T(out, "out"), batch,
+                                      query_heads, kv_heads, query_len, key_len, head_dim, scale, M(mask), key_capacity,
+                                      position ? &pos : nullptr);
+    });
+}
+
 popcorn_status_t popcorn_kernel_matmul(const popcorn_tensor_t *a, const popcorn_tensor_t *b, const popcorn_tensor_t *c,
                                        int32_t transpose_b, popcorn_kernel_t *kernel) {
     return guarded([&] { emit(kernel, Kernels::Matmul(T(a, "a"), T(b, "b"), T(c, "c"), transpose_b != 0)); });

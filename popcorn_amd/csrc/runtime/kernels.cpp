@@ -238,45 +238,72 @@ public:
         enc.withTemporaryTensor(ScratchSpec{{slots, d_.Hd}, DataType::f32}, [&](Tensor pO) {
             enc.withTemporaryTensor(ScratchSpec{{slots}, DataType::f32}, [&](Tensor pM) {
                 enc.withTemporaryTensor(ScratchSpec{{slots}, DataType::f32}, [&](Tensor pL) {
-                    FlashDecodingPartialExtConstants pc{};
-                    pc.B = (uint32_t)d_.B;
-                    pc.Nq = (uint32_t)d_.Nq;
-                    pc.Nkv = (uint32_t)d_.Nkv;
-                    pc.Sk = (uint32_t)d_.Sk;
-                    pc.Hd = (uint32_t)d_.Hd;
-                    pc.P = (uint32_t)P_;
-                    pc.maskKind = mask_.kind;
-                    pc.slidingWindow = mask_.kind == 1 ? mask_.window : -1;
-                    pc.scale = scale_;
-                    pc.kvStride = (uint32_t)d_.cap;
-                    pc.Sq = (uint32_t)d_.Sq;
-                    pc.keyLenFromPosition = hasPos_ ? 1u : 0u;
-                    DispatchSize ds;
-                    ds.grid = dim3((unsigned)P_, (unsigned)(d_.B * d_.Nkv * ngroups_), (unsigned)d_.Sq);
-                    ds.block = dim3(kBlock, 1, 1);
-                    // the position binding is read only when keyLenFromPosition
-                    Tensor posOrDummy = hasPos_ ? pos_ : q_;
-                    FixedDispatch partial(partialName_,
-                                          {{q_, kRead}, {k_, kRead}, {v_, kRead}, {pO, kWrite}, {pM, kWrite}, {pL, kWrite},
-                                           {posOrDummy, kRead}},
-                                          {bytesOf(pc)}, ds);
-                    enc.dispatch(partial);
-                    FlashDecodingReduceExtConstants rc{};
-                    rc.B = (uint32_t)d_.B;
-                    rc.Nq = (uint32_t)d_.Nq;
-                    rc.Hd = (uint32_t)d_.Hd;
-                    rc.P = (uint32_t)P_;
-                    rc.Sq = (uint32_t)d_.Sq;
-                    // one block per (query row, 64-dim slice of the head)
-                    DispatchSize rs;
-                    rs.grid = dim3((unsigned)(d_.B * d_.Nq * d_.Sq), (unsigned)cdiv(d_.Hd, 64), 1);
-                    rs.block = dim3(kBlock, 1, 1);
-                    FixedDispatch reduce(reduceName_, {{pO, kRead}, {pM, kRead}, {pL, kRead}, {out_, kWrite}},
-                                         {bytesOf(rc)}, rs);
-                    enc.dispatch(reduce);
+                    encodeSplit(enc, pO, pM, pL);
                 });
             });
         });
+    }
+
+    // The split-KV path's partial (O, m, l) in f32: slots x (Hd + 2) floats.
+    size_t splitScratchBytes() const { return (size_t)(d_.B * d_.Nq * d_.Sq * P_) * (size_t)(d_.Hd + 2) * 4; }
+
+    // The split-KV path on caller-given partial buffers (no scratch borrowed):
+    // O [slots, Hd], then m and l [slots] each, inside `bytes` at `scratch`.
+    void encodeSplitInto(KernelCommandEncoder &enc, void *scratch, size_t bytes) const {
+        const int64_t slots = d_.B * d_.Nq * d_.Sq * P_;
+        if (splitScratchBytes() > bytes)
+            throw Error(POPCORN_ERR_WORKSPACE_EXHAUSTED,
+                        "split-KV attention needs " + std::to_string(splitScratchBytes()) +
+                            " bytes of partials; the static scratch holds " + std::to_string(bytes) + ".");
+        float *base = static_cast<float *>(scratch);
+        Tensor pO(base, Shape({slots, d_.Hd}), DataType::f32);
+        Tensor pM(base + slots * d_.Hd, Shape({slots}), DataType::f32);
+        Tensor pL(base + slots * (d_.Hd + 1), Shape({slots}), DataType::f32);
+        encodeSplit(enc, pO, pM, pL);
+    }
+
+    bool tiled() const { return path_ == Kernels::AttentionPath::tiled; }
+
+    // Forces the split-KV kernels (the plain/decoding routes) whatever route
+    // the shape would take.
+    void useSplitPath() { path_ = Kernels::AttentionPath::decoding; }
+
+    void encodeSplit(KernelCommandEncoder &enc, const Tensor &pO, const Tensor &pM, const Tensor &pL) const {
+        FlashDecodingPartialExtConstants pc{};
+        pc.B = (uint32_t)d_.B;
+        pc.Nq = (uint32_t)d_.Nq;
+        pc.Nkv = (uint32_t)d_.Nkv;
+        pc.Sk = (uint32_t)d_.Sk;
+        pc.Hd = (uint32_t)d_.Hd;
+        pc.P = (uint32_t)P_;
+        pc.maskKind = mask_.kind;
+        pc.slidingWindow = mask_.kind == 1 ? mask_.window : -1;
+        pc.scale = scale_;
+        pc.kvStride = (uint32_t)d_.cap;
+        pc.Sq = (uint32_t)d_.Sq;
+        pc.keyLenFromPosition = hasPos_ ? 1u : 0u;
+        DispatchSize ds;
+        ds.grid = dim3((unsigned)P_, (unsigned)(d_.B * d_.Nkv * ngroups_), (unsigned)d_.Sq);
+        ds.block = dim3(kBlock, 1, 1);
+        // the position binding is read only when keyLenFromPosition
+        Tensor posOrDummy = hasPos_ ? pos_ : q_;
+        FixedDispatch partial(partialName_,
+                              {{q_, kRead}, {k_, kRead}, {v_, kRead}, {pO, kWrite}, {pM, kWrite}, {pL, kWrite},
+                               {posOrDummy, kRead}},
+                              {bytesOf(pc)}, ds);
+        enc.dispatch(partial);
+        FlashDecodingReduceExtConstants rc{};
+        rc.B = (uint32_t)d_.B;
+        rc.Nq = (uint32_t)d_.Nq;
+        rc.Hd = (uint32_t)d_.Hd;
+        rc.P = (uint32_t)P_;
+        rc.Sq = (uint32_t)d_.Sq;
+        // one block per (query row, 64-dim slice of the head)
+        DispatchSize rs;
+        rs.grid = dim3((unsigned)(d_.B * d_.Nq * d_.Sq), (unsigned)cdiv(d_.Hd, 64), 1);
+        rs.block = dim3(kBlock, 1, 1);
+        FixedDispatch reduce(reduceName_, {{pO, kRead}, {pM, kRead}, {pL, kRead}, {out_, kWrite}}, {bytesOf(rc)}, rs);
+        enc.dispatch(reduce);
     }
 
 private:
@@ -1034,6 +1061,28 @@ std::unique_ptr<Kernel> FlashAttention(const Tensor &q, const Tensor &k, const T
     const int64_t cap = keyCapacity > 0 ? keyCapacity : keyLen;
     return std::make_unique<FlashAttentionKernel>(q, k, v, out, AttnDims{batch, queryHeads, kvHeads, queryLen, keyLen, headDim, cap},
                                                   scale, mask, position);
+}
+
+// The split-KV attention with its partials in the static scratch
+// (static_scratch.hip) instead of a borrowed buffer: validation and kernels
+// as for FlashAttention with the same dims; no device memory is allocated.
+void FlashDecodingNoAlloc(KernelLibrary &library, hipStream_t stream, const Tensor &q, const Tensor &k, const Tensor &v,
+                          const Tensor &out, int64_t batch, int64_t queryHeads, int64_t kvHeads, int64_t queryLen,
+                          int64_t keyLen, int64_t headDim, float scale, AttentionMask mask, int64_t keyCapacity,
+                          const Tensor *position) {
+    struct NoScratch : KernelScratchAllocator {
+        KernelTemporaryBuffer borrowTemporaryBuffer(size_t) override {
+            throw Error(POPCORN_ERR_WORKSPACE_EXHAUSTED, "the allocation-free attention borrows no scratch");
+        }
+    } none;
+    const int64_t cap = keyCapacity > 0 ? keyCapacity : keyLen;
+    FlashAttentionKernel fa(q, k, v, out, AttnDims{batch, queryHeads, kvHeads, queryLen, keyLen, headDim, cap}, scale,
+                            mask, position);
+    fa.useSplitPath();
+    size_t bytes = 0;
+    void *scratch = staticScratch(&bytes);
+    KernelCommandEncoder enc(library, stream, none);
+    fa.encodeSplitInto(enc, scratch, bytes);
 }
 
 // Matmul.swift:68-93

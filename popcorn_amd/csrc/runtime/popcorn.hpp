@@ -430,7 +430,18 @@ std::unique_ptr<Kernel> Custom(const std::string &functionName, std::vector<Bind
 std::unique_ptr<Kernel> FillNormal(void *data, DataType dtype, uint64_t count, uint64_t seed, float mean,
                                    float stddev);
 
+// FlashAttention's split-KV kernels with the partials in the static scratch:
+// enqueues on `stream`, allocates no device memory (popcorn_flash_decoding_no_alloc).
+void FlashDecodingNoAlloc(KernelLibrary &library, hipStream_t stream, const Tensor &q, const Tensor &k, const Tensor &v,
+                          const Tensor &out, int64_t batch, int64_t queryHeads, int64_t kvHeads, int64_t queryLen,
+                          int64_t keyLen, int64_t headDim, float scale, AttentionMask mask, int64_t keyCapacity,
+                          const Tensor *position);
+
 }  // namespace Kernels
+
+// The current device's copy of the static scratch array (static_scratch.hip)
+// and its size in bytes; looked up once per device.
+void *staticScratch(size_t *bytes);
 
 // Thread-local message of the last failure reported through the C ABI.
 void setLastError(const std::string &message);
