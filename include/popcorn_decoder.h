@@ -107,11 +107,21 @@ int64_t popcorn_decoder_step_bytes(popcorn_decoder_t decoder, int32_t position);
 /* Times one kernel of the step in isolation: every dispatch of the step
  * whose function is `function_name` (one per layer, say) is launched back to
  * back `reps` times between two events on the decoder's stream, all other
- * dispatches skipped. Reports the mean duration per launch and the number of
+ * dispatches skipped (captured once as a graph and replayed, so no host work
+ * sits between the launches). Reports the mean duration per launch and the number of
  * launches timed. State other than those kernels' outputs is unchanged; the
  * token and position are restored afterwards. */
 popcorn_status_t popcorn_decoder_time_kernel(popcorn_decoder_t decoder, const char *function_name, int32_t reps,
                                              float *mean_ms, int32_t *launches);
+
+/* Times one kernel inside the step: runs `steps` eager decode steps from the
+ * current position (advancing it, like popcorn_decoder_step without a graph)
+ * with start and stop events attached to the dispatch packet of every launch
+ * of `function_name` (hipExtModuleLaunchKernel: the packet's own begin and
+ * end, as a profiler's kernel trace reads them), and reports their mean: the
+ * kernel as the step runs it, after its neighbours, with their cache state. */
+popcorn_status_t popcorn_decoder_time_kernel_in_step(popcorn_decoder_t decoder, const char *function_name,
+                                                     int32_t steps, float *mean_ms, int32_t *launches);
 
 #ifdef __cplusplus
 }

@@ -211,6 +211,8 @@ PROTOTYPES = {
     "popcorn_decoder_step_bytes": (C.c_int64, [C.c_void_p, C.c_int32]),
     "popcorn_decoder_time_kernel": (_st, [C.c_void_p, C.c_char_p, C.c_int32, C.POINTER(C.c_float),
                                           C.POINTER(C.c_int32)]),
+    "popcorn_decoder_time_kernel_in_step": (_st, [C.c_void_p, C.c_char_p, C.c_int32, C.POINTER(C.c_float),
+                                          C.POINTER(C.c_int32)]),
 }
 
 _lib = None

@@ -616,14 +616,81 @@ popcorn_status_t popcorn_decoder_time_kernel(popcorn_decoder_t d, const char *fu
         } restore{d, saved};
         d->enc->setDispatchFilter(function_name);
         d->encodeStep();  // warm: first launch of each
+        // the filtered launches of `reps` steps captured as one graph and
+        // replayed, so the timing holds GPU time only (no host walk of the
+        // other dispatches between lone launches)
+        hipGraph_t g = nullptr;
+        hipGraphExec_t ge = nullptr;
+        checkHip(hipStreamBeginCapture(d->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+        try {
+            for (int32_t r = 0; r < reps; ++r) d->encodeStep();
+        } catch (...) {
+            (void)hipStreamEndCapture(d->stream, &g);
+            if (g) (void)hipGraphDestroy(g);
+            throw;
+        }
+        checkHip(hipStreamEndCapture(d->stream, &g), "hipStreamEndCapture");
+        struct GraphGuard {
+            hipGraph_t &g;
+            hipGraphExec_t &e;
+            ~GraphGuard() {
+                if (e) (void)hipGraphExecDestroy(e);
+                if (g) (void)hipGraphDestroy(g);
+            }
+        } graphGuard{g, ge};
+        checkHip(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0), "hipGraphInstantiate");
+        checkHip(hipGraphLaunch(ge, d->stream), "hipGraphLaunch");  // warm
         checkHip(hipEventRecord(a, d->stream), "hipEventRecord");
-        for (int32_t r = 0; r < reps; ++r) d->encodeStep();
+        checkHip(hipGraphLaunch(ge, d->stream), "hipGraphLaunch");
         checkHip(hipEventRecord(b, d->stream), "hipEventRecord");
         checkHip(hipEventSynchronize(b), "hipEventSynchronize");
         float ms = 0;
         checkHip(hipEventElapsedTime(&ms, a, b), "hipEventElapsedTime");
         *mean_ms = ms / (float)(per * reps);
         if (launches) *launches = per * reps;
+    });
+}
+
+popcorn_status_t popcorn_decoder_time_kernel_in_step(popcorn_decoder_t d, const char *function_name, int32_t steps,
+                                                     float *mean_ms, int32_t *launches) {
+    return guardedDec([&] {
+        if (!d || !function_name || !mean_ms) throw Error::invalidArgument("decoder, name and mean_ms must not be NULL");
+        if (steps <= 0) throw Error::invalidArgument("steps must be positive");
+        int32_t per = 0;
+        for (const std::string &n : d->names) per += (n == function_name) ? 1 : 0;
+        if (per == 0) throw Error::kernelFunctionNotFound(std::string(function_name) + " (not dispatched by a decode step)");
+        if (d->hostPos < 0 || d->hostPos + steps > d->S)
+            throw Error::tensorShapeMismatch("timed steps would leave the KV cache");
+        const int32_t n = per * steps;
+        std::vector<hipEvent_t> ev((size_t)2 * n, nullptr);
+        struct Events {
+            std::vector<hipEvent_t> &ev;
+            popcorn_decoder_s *d;
+            ~Events() {
+                d->enc->setDispatchHook(nullptr);
+                for (hipEvent_t e : ev)
+                    if (e) (void)hipEventDestroy(e);
+            }
+        } guard{ev, d};
+        for (hipEvent_t &e : ev) checkHip(hipEventCreate(&e), "hipEventCreate");
+        int32_t next = 0;
+        KernelCommandEncoder::TimingHook hook = [&](const std::string &name) -> std::pair<hipEvent_t, hipEvent_t> {
+            if (name != function_name || next >= 2 * n) return {nullptr, nullptr};
+            next += 2;
+            return {ev[(size_t)next - 2], ev[(size_t)next - 1]};
+        };
+        d->enc->setDispatchHook(&hook);
+        d->run(steps, false);
+        d->enc->setDispatchHook(nullptr);
+        checkHip(hipStreamSynchronize(d->stream), "sync");
+        double total = 0;
+        for (int32_t i = 0; i + 1 < next; i += 2) {
+            float ms = 0;
+            checkHip(hipEventElapsedTime(&ms, ev[(size_t)i], ev[(size_t)i + 1]), "hipEventElapsedTime");
+            total += ms;
+        }
+        *mean_ms = next >= 2 ? (float)(total / (next / 2)) : 0.0f;
+        if (launches) *launches = next / 2;
     });
 }
 

@@ -284,6 +284,11 @@ public:
     // When set, dispatch() launches only kernels with this function name and
     // skips the rest (used to time one kernel of a composite sequence).
     void setDispatchFilter(const std::string &functionName) { filter_ = functionName; }
+    // When set, called with each launch's function name; a pair of events it
+    // returns is attached to that launch's dispatch packet (its start and end,
+    // as a profiler times it), a pair of nulls launches it plainly.
+    using TimingHook = std::function<std::pair<hipEvent_t, hipEvent_t>(const std::string &)>;
+    void setDispatchHook(const TimingHook *hook) { hook_ = hook; }
 
 
 private:
@@ -296,6 +301,7 @@ private:
     std::map<const void *, uint8_t> accessByBuffer_;
     int64_t dispatches_ = 0, hazards_ = 0, scratchBorrows_ = 0;
     std::string filter_;
+    const TimingHook *hook_ = nullptr;
 };
 
 // ---- Kernels.* descriptors --------------------------------------------------

@@ -9,6 +9,15 @@
 
 #include "popcorn.hpp"
 
+// hip/hip_ext.h's C entry point (its header's C++ part needs the HIP
+// compiler): a module launch whose dispatch packet carries start and stop
+// events.
+extern "C" hipError_t hipExtModuleLaunchKernel(hipFunction_t f, uint32_t globalWorkSizeX, uint32_t globalWorkSizeY,
+                                               uint32_t globalWorkSizeZ, uint32_t localWorkSizeX,
+                                               uint32_t localWorkSizeY, uint32_t localWorkSizeZ, size_t sharedMemBytes,
+                                               hipStream_t hStream, void **kernelParams, void **extra,
+                                               hipEvent_t startEvent, hipEvent_t stopEvent, uint32_t flags);
+
 namespace popcorn {
 
 // ---- errors ------------------------------------------------------------------
@@ -295,8 +304,17 @@ void KernelCommandEncoder::dispatch(const DispatchKernel &kernel) {
         params.push_back(&ptrs[i]);
     }
     for (const auto &c : consts) params.push_back(const_cast<uint8_t *>(c.data()));
-    hipError_t err = hipModuleLaunchKernel(fn.fn, ds.grid.x, ds.grid.y, ds.grid.z, ds.block.x, ds.block.y,
-                                           ds.block.z, (unsigned)ds.dynamicLds, stream_, params.data(), nullptr);
+    std::pair<hipEvent_t, hipEvent_t> timing{nullptr, nullptr};
+    if (hook_) timing = (*hook_)(kernel.functionName());
+    hipError_t err;
+    if (timing.first) {
+        err = hipExtModuleLaunchKernel(fn.fn, ds.grid.x * ds.block.x, ds.grid.y * ds.block.y, ds.grid.z * ds.block.z,
+                                       ds.block.x, ds.block.y, ds.block.z, ds.dynamicLds, stream_, params.data(),
+                                       nullptr, timing.first, timing.second, 0);
+    } else {
+        err = hipModuleLaunchKernel(fn.fn, ds.grid.x, ds.grid.y, ds.grid.z, ds.block.x, ds.block.y, ds.block.z,
+                                    (unsigned)ds.dynamicLds, stream_, params.data(), nullptr);
+    }
     if (err != hipSuccess) throw Error::fromHip(err, "launch " + kernel.functionName());
     ++dispatches_;
     recordAccesses(bindings);

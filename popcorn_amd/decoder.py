@@ -80,6 +80,13 @@ class Decoder:
     def step_bytes(self, position: int) -> int:
         return int(lib().popcorn_decoder_step_bytes(self.handle, position))
 
+    def time_kernel_in_step(self, function_name: str, steps: int = 4):
+        """(mean ms per launch, launches) of one kernel inside `steps` eager decode steps (advances the position)."""
+        ms, n = C.c_float(), C.c_int32()
+        check(lib().popcorn_decoder_time_kernel_in_step(self.handle, function_name.encode(), steps, C.byref(ms),
+                                                        C.byref(n)))
+        return ms.value, n.value
+
     def time_kernel(self, function_name: str, reps: int = 5):
         """(mean ms per launch, launches) of one kernel of the step, launched alone."""
         ms, n = C.c_float(), C.c_int32()
