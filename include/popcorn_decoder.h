@@ -116,10 +116,14 @@ popcorn_status_t popcorn_decoder_time_kernel(popcorn_decoder_t decoder, const ch
 
 /* Times one kernel inside the step: runs `steps` eager decode steps from the
  * current position (advancing it, like popcorn_decoder_step without a graph)
- * with start and stop events attached to the dispatch packet of every launch
- * of `function_name` (hipExtModuleLaunchKernel: the packet's own begin and
- * end, as a profiler's kernel trace reads them), and reports their mean: the
- * kernel as the step runs it, after its neighbours, with their cache state. */
+ * with a stop event attached to every launch of `function_name` and to the
+ * launch just before each (hipExtModuleLaunchKernel; events without the
+ * system-scope fence), and reports the mean of end(kernel) - end(previous
+ * launch): the kernel's dispatch and run as the step pays for them, after its
+ * neighbours and with their cache state. These times add up to the step.
+ * A bounded wait kernel (hold_stream) runs first, so that every step is
+ * enqueued before the GPU reaches it and no host gap falls between launches.
+ * steps: 1..16. */
 popcorn_status_t popcorn_decoder_time_kernel_in_step(popcorn_decoder_t decoder, const char *function_name,
                                                      int32_t steps, float *mean_ms, int32_t *launches);
 

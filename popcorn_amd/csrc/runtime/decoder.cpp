@@ -3,6 +3,7 @@
 // graph capture/replay of whole steps.
 #include <cmath>
 #include <cstring>
+#include <set>
 
 #include "handles.hpp"
 #include "popcorn_decoder.h"
@@ -655,14 +656,27 @@ popcorn_status_t popcorn_decoder_time_kernel_in_step(popcorn_decoder_t d, const 
                                                      float *mean_ms, int32_t *launches) {
     return guardedDec([&] {
         if (!d || !function_name || !mean_ms) throw Error::invalidArgument("decoder, name and mean_ms must not be NULL");
-        if (steps <= 0) throw Error::invalidArgument("steps must be positive");
+        if (steps <= 0 || steps > 16) throw Error::invalidArgument("steps must be in 1..16");
         int32_t per = 0;
         for (const std::string &n : d->names) per += (n == function_name) ? 1 : 0;
         if (per == 0) throw Error::kernelFunctionNotFound(std::string(function_name) + " (not dispatched by a decode step)");
         if (d->hostPos < 0 || d->hostPos + steps > d->S)
             throw Error::tensorShapeMismatch("timed steps would leave the KV cache");
-        const int32_t n = per * steps;
-        std::vector<hipEvent_t> ev((size_t)2 * n, nullptr);
+        // A stop event on every launch of the kernel and on every launch of
+        // the kernels that come just before it in the step: each event takes
+        // its launch's end of execution, so the kernel's time in the step is
+        // end(kernel) - end(the launch before it) (its dispatch and its run,
+        // as a kernel trace adds up to the step).
+        std::set<std::string> before;
+        const size_t perStep = d->names.size();
+        for (size_t i = 0; i < perStep; ++i)
+            if (d->names[(i + 1) % perStep] == function_name) before.insert(d->names[i]);
+        size_t marked = 0;  // launches per step that carry an event
+        for (const std::string &n : d->names) marked += (n == function_name || before.count(n)) ? 1 : 0;
+        const size_t maxEvents = marked * (size_t)steps + 2;
+        std::vector<hipEvent_t> ev(maxEvents, nullptr);
+        std::vector<size_t> at(maxEvents, 0);
+        std::vector<char> self(maxEvents, 0);
         struct Events {
             std::vector<hipEvent_t> &ev;
             popcorn_decoder_s *d;
@@ -672,25 +686,40 @@ popcorn_status_t popcorn_decoder_time_kernel_in_step(popcorn_decoder_t d, const 
                     if (e) (void)hipEventDestroy(e);
             }
         } guard{ev, d};
-        for (hipEvent_t &e : ev) checkHip(hipEventCreate(&e), "hipEventCreate");
-        int32_t next = 0;
+        for (hipEvent_t &e : ev) checkHip(hipEventCreateWithFlags(&e, hipEventDisableSystemFence), "hipEventCreate");
+        size_t next = 0, dispatch = 0;
         KernelCommandEncoder::TimingHook hook = [&](const std::string &name) -> std::pair<hipEvent_t, hipEvent_t> {
-            if (name != function_name || next >= 2 * n) return {nullptr, nullptr};
-            next += 2;
-            return {ev[(size_t)next - 2], ev[(size_t)next - 1]};
+            const size_t i = dispatch++;
+            const bool isSelf = name == function_name;
+            if ((!isSelf && !before.count(name)) || next >= maxEvents) return {nullptr, nullptr};
+            at[next] = i;
+            self[next] = isSelf;
+            return {nullptr, ev[next++]};
         };
+        // the stream waits (about 4 ms per step) while the host enqueues the
+        // steps, so they then run back to back with no host gaps between
+        // launches
+        {
+            const Function &hold = d->lib->function("hold_stream");
+            uint64_t ticks = (uint64_t)steps * 400000u;
+            void *args[] = {&ticks};
+            checkHip(hipModuleLaunchKernel(hold.fn, 1, 1, 1, 64, 1, 1, 0, d->stream, args, nullptr), "launch hold_stream");
+        }
         d->enc->setDispatchHook(&hook);
         d->run(steps, false);
         d->enc->setDispatchHook(nullptr);
         checkHip(hipStreamSynchronize(d->stream), "sync");
         double total = 0;
-        for (int32_t i = 0; i + 1 < next; i += 2) {
+        int32_t timed = 0;
+        for (size_t j = 1; j < next; ++j) {
+            if (!self[j] || at[j] != at[j - 1] + 1) continue;
             float ms = 0;
-            checkHip(hipEventElapsedTime(&ms, ev[(size_t)i], ev[(size_t)i + 1]), "hipEventElapsedTime");
+            checkHip(hipEventElapsedTime(&ms, ev[j - 1], ev[j]), "hipEventElapsedTime");
             total += ms;
+            ++timed;
         }
-        *mean_ms = next >= 2 ? (float)(total / (next / 2)) : 0.0f;
-        if (launches) *launches = next / 2;
+        *mean_ms = timed ? (float)(total / timed) : 0.0f;
+        if (launches) *launches = timed;
     });
 }
 

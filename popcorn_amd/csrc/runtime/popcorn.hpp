@@ -284,9 +284,9 @@ public:
     // When set, dispatch() launches only kernels with this function name and
     // skips the rest (used to time one kernel of a composite sequence).
     void setDispatchFilter(const std::string &functionName) { filter_ = functionName; }
-    // When set, called with each launch's function name; a pair of events it
-    // returns is attached to that launch's dispatch packet (its start and end,
-    // as a profiler times it), a pair of nulls launches it plainly.
+    // When set, called with each launch's function name; the events it
+    // returns (start, stop; either may be null) are attached to that launch
+    // (hipExtModuleLaunchKernel), a pair of nulls launches it plainly.
     using TimingHook = std::function<std::pair<hipEvent_t, hipEvent_t>(const std::string &)>;
     void setDispatchHook(const TimingHook *hook) { hook_ = hook; }
 

@@ -307,7 +307,7 @@ void KernelCommandEncoder::dispatch(const DispatchKernel &kernel) {
     std::pair<hipEvent_t, hipEvent_t> timing{nullptr, nullptr};
     if (hook_) timing = (*hook_)(kernel.functionName());
     hipError_t err;
-    if (timing.first) {
+    if (timing.first || timing.second) {
         err = hipExtModuleLaunchKernel(fn.fn, ds.grid.x * ds.block.x, ds.grid.y * ds.block.y, ds.grid.z * ds.block.z,
                                        ds.block.x, ds.block.y, ds.block.z, ds.dynamicLds, stream_, params.data(),
                                        nullptr, timing.first, timing.second, 0);
