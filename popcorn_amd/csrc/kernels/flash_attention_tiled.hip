@@ -166,13 +166,23 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
     using KRegs = u32x4[kKC];
     using VRegs = u32x4[kVC][4];
     u32x4 krA[kKC], vrA[kVC][4], krB[kKC], vrB[kVC][4];
+    // K and V are read through buffer resources over the head's Sk rows
+    // (the host keeps Sk * HD * 2 below 2^31): a row past Sk reads as zeros
+    // (its key is masked), the thread's offset within a step is fixed and
+    // the step's offset k0 * HD * 2 goes in the scalar offset, so a step's
+    // loads need no address arithmetic.
+    const __amdgpu_buffer_rsrc_t rsK = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(Kh), 0,
+                                                                          (int)(p.Sk * HD * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsV = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(Vh), 0,
+                                                                          (int)(p.Sk * HD * 2), 0x00020000);
     auto gload = [&](KRegs &kr, VRegs &vr, uint32_t k0) {
+        const int so = (int)(k0 * HD * 2);
 #pragma unroll
         for (int i = 0; i < kKC; ++i) {
             const uint32_t c = threadIdx.x + i * 64 * kWaves;
             if (kChunks % (64 * kWaves) == 0 || c < (uint32_t)kChunks) {
                 const uint32_t key = c / (HD / 8), dc = (c % (HD / 8)) * 8;
-                kr[i] = *reinterpret_cast<const u32x4 *>(Kh + (uint64_t)min(k0 + key, p.Sk - 1) * HD + dc);
+                kr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsK, (int)((key * HD + dc) * 2), so, 0));
             }
         }
 #pragma unroll
@@ -182,7 +192,8 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
                 const uint32_t kq = pr % (BKV / 4), db = pr / (BKV / 4);
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
-                    vr[i][j] = *reinterpret_cast<const u32x4 *>(Vh + (uint64_t)min(k0 + 4 * kq + j, p.Sk - 1) * HD + db * 8);
+                    vr[i][j] = __builtin_bit_cast(
+                        u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsV, (int)(((4 * kq + j) * HD + db * 8) * 2), so, 0));
             }
         }
     };
@@ -251,23 +262,25 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
         // its last): no per-key test.
         const bool full = (int)k0 + BKV <= (int)p.Sk && (p.maskKind == 2u || (int)k0 + BKV - 1 <= posQ0) &&
                           (p.maskKind != 1u || posQ0 + 31 - (int)k0 < (int)p.slidingWindow);
+        // raw scores K.q: the scale (c2 > 0, in log2 units) is applied to the
+        // row max and inside the exponent, exp2(s c2 - m)
         float sv[16];
         float mt = -INFINITY;
         if (full) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                sv[i] = (st[i] + st2[i]) * c2;
+                sv[i] = st[i] + st2[i];
                 mt = fmaxf(mt, sv[i]);
             }
         } else {
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const int key = (int)k0 + (i >> 2) * 8 + (int)h * 4 + (i & 3);
-                sv[i] = fa_allowed(p, posQ, key) ? (st[i] + st2[i]) * c2 : -INFINITY;
+                sv[i] = fa_allowed(p, posQ, key) ? st[i] + st2[i] : -INFINITY;
                 mt = fmaxf(mt, sv[i]);
             }
         }
-        mt = fmaxf(mt, pk::swap32(mt));
+        mt = fmaxf(mt, pk::swap32(mt)) * c2;
         // Lazy rescaling: a row's reference max m moves only when a score
         // passes it by more than kRescaleGap, so the weights exp(s - m) stay
         // below e^kRescaleGap (inside f16's range) and the rescale of the
@@ -295,36 +308,34 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
                     acc[dt][i] = x;
                 }
         }
-        uint32_t pb[16], pr[16];
+        // P^T as the B operand: word j of pf[ks] holds the weights of slots
+        // ks * 8 + 2j (low half) and + 1; the row sum takes the unrounded
+        // weights (the rounding to 16 bits is below the output's precision)
+        u32x4 pf[2], pfr[2];
         if (m == -INFINITY) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) pb[i] = pr[i] = 0u;
+            for (int ks = 0; ks < 2; ++ks) pf[ks] = pfr[ks] = u32x4{0u, 0u, 0u, 0u};
         } else {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const float pv = __builtin_amdgcn_exp2f(sv[i] - m);
-                pb[i] = pk::bits16<T>(pv);
-                float w = pk::from_bits16<T>(pb[i]);
-                if constexpr (kSplitP) {
-                    // bf16 keeps 8 bits: the remainder goes in a second product
-                    pr[i] = pk::bits16<T>(pv - w);
-                    w += pk::from_bits16<T>(pr[i]);
-                } else {
-                    pr[i] = 0u;
+            for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int i = ks * 8 + 2 * j;
+                    const float p0 = __builtin_amdgcn_exp2f(fmaf(sv[i], c2, -m));
+                    const float p1 = __builtin_amdgcn_exp2f(fmaf(sv[i + 1], c2, -m));
+                    ps += p0 + p1;
+                    const uint32_t w = pk::pack2<T>(p0, p1);
+                    pf[ks][j] = w;
+                    if constexpr (kSplitP) {
+                        // bf16 keeps 8 bits: the remainder goes in a second product
+                        pfr[ks][j] = pk::pack2<T>(p0 - __uint_as_float(w << 16), p1 - __uint_as_float(w & 0xffff0000u));
+                    } else {
+                        pfr[ks][j] = 0u;
+                    }
                 }
-                ps += w;  // the weight the MFMAs apply
-            }
         }
         ps += pk::swap32(ps);
         l = l * alpha + ps;
-        u32x4 pf[2], pfr[2];
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                pf[ks][j] = pb[ks * 8 + 2 * j] | (pb[ks * 8 + 2 * j + 1] << 16);
-                pfr[ks][j] = pr[ks * 8 + 2 * j] | (pr[ks * 8 + 2 * j + 1] << 16);
-            }
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll

@@ -43,6 +43,24 @@ __device__ inline uint32_t bits16<BF16>(float x) {
     return (uint32_t)BF16::store(x);
 }
 
+// Two f32 values rounded to nearest-even in T and packed (a in the low half):
+// one v_cvt_pk_f16_f32 / v_cvt_pk_bf16_f32 on gfx950. For finite values the
+// bf16 result equals BF16::store's.
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+template <typename T>
+__device__ inline uint32_t pack2(float a, float b);
+template <>
+__device__ inline uint32_t pack2<F16>(float a, float b) {
+    const f16x2 v = {(_Float16)a, (_Float16)b};
+    return __builtin_bit_cast(uint32_t, v);
+}
+template <>
+__device__ inline uint32_t pack2<BF16>(float a, float b) {
+    const bf16x2 v = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
 // f32 value of 16-bit storage bits in T.
 template <typename T>
 __device__ inline float from_bits16(uint32_t b);
