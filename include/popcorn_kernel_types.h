@@ -111,10 +111,16 @@ typedef struct {
 /* The MFMA prefill kernel's constants (flash_attention_tiled_*, the kernel
  * in the MPP route's place): MPPFlashAttentionConstants' fields, plus
  *   kvStride   rows between consecutive KV heads in K/V (0 = Sk);
- *   splitFrom  query tiles qt >= splitFrom run as two blocks over the two
- *              halves of their key steps, which write partial (O, m, l) for
- *              the split-merge kernel; splitFrom >= qTilesPerHead splits
- *              nothing. */
+ *   splitFrom  splitFrom >= qTilesPerHead: one block per query tile.
+ *              Otherwise tiles qt >= splitFrom are split in two parts, each
+ *              written as partial (O, m, l) for the split-merge kernel:
+ *   pairTiles  0: the split tiles run as two blocks over the halves of their
+ *              key steps (qTilesPerHead + split tiles blocks per head);
+ *              1 (causal, splitFrom = qTilesPerHead - qTilesPerHead / 2):
+ *              tile i is paired with tile qTilesPerHead - 1 - i and each
+ *              pair runs as two blocks of equal work, tile i and the first
+ *              steps of its partner, then the partner's remaining steps
+ *              (qTilesPerHead blocks per head). */
 typedef struct {
     uint32_t B;
     uint32_t Nq;
@@ -128,6 +134,7 @@ typedef struct {
     float scale;
     uint32_t kvStride;
     uint32_t splitFrom;
+    uint32_t pairTiles;
 } TiledFlashAttentionConstants;
 
 /* PopcornKernelTypes.h:146-156 */

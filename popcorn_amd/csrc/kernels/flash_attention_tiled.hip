@@ -63,40 +63,91 @@ __device__ inline uint32_t fa_steps(const TiledFlashAttentionConstants &p, uint3
     return kHi > kLo ? (uint32_t)(kHi - kLo + BKV - 1) / BKV : 0u;
 }
 
-// Work item of a block. Per (batch, query head) there are qTilesPerHead
-// tiles, those from splitFrom on as two halves of their key steps; blocks
-// take the items heaviest first (the larger of the next split half and the
-// next whole tile), the (batch, head) index varying fastest, so the longest
-// items start first on every CU.
-struct FaItem {
-    uint32_t bh, qt, part;
-    bool split;
+// Work of a block: one or two items, each a query tile qt over its key
+// steps [lo, hi) (counted from the tile's first step), written whole or, for
+// a split tile, as part `part` of two (partial O, m, l for the merge kernel).
+//
+// Without splits (splitFrom >= qTilesPerHead) a block takes one whole tile,
+// the heaviest tiles first. With splits and pairTiles (at most one tile per
+// CU), a causal head's tiles are paired, light tile a = i with heavy tile
+// b = qTilesPerHead - 1 - i, and each pair runs as two blocks of equal work:
+// the first takes tile a and the first x steps of tile b, the second the
+// rest of tile b, where x makes the two halves of the pair's steps equal
+// (the host uses this only where x >= 1 for every pair, so the b tiles,
+// qt >= splitFrom, are exactly the split ones); an odd tile count leaves the
+// middle tile whole, one block. Every block then holds about the mean work,
+// so the CUs finish together. With splits and no pairTiles (up to two tiles
+// per CU), the tiles from splitFrom on run as two blocks over the halves of
+// their key steps and blocks take the items heaviest first (the larger of
+// the next split half and the next whole tile), the (batch, head) index
+// varying fastest, so the longest items start first on every CU.
+struct FaWork {
+    uint32_t bh, n;
+    uint32_t qt[2], lo[2], hi[2], part[2];
+    bool split[2];
 };
 
-__device__ inline FaItem fa_item(const TiledFlashAttentionConstants &p) {
-    const uint32_t BH = p.B * p.Nq, nQT = p.qTilesPerHead, sf = p.splitFrom;
-    const uint32_t rank = blockIdx.x / BH, nItems = nQT + (nQT - sf);
-    FaItem it{blockIdx.x % BH, 0u, 0u, false};
-    int a = (int)nQT - 1, b = (int)sf - 1;  // next split tile, next whole tile
-    uint32_t halves = 2;
-    for (uint32_t r = 0; r < nItems; ++r) {
-        const bool takeSplit = a >= (int)sf && (b < 0 || (fa_steps(p, a) + 1) / 2 >= fa_steps(p, b));
-        if (r == rank) {
-            it.qt = (uint32_t)(takeSplit ? a : b);
-            it.part = takeSplit ? 2u - halves : 0u;
-            it.split = takeSplit;
-            break;
-        }
-        if (takeSplit) {
-            if (--halves == 0) {
-                --a;
-                halves = 2;
-            }
-        } else {
-            --b;
-        }
+__device__ inline FaWork fa_work(const TiledFlashAttentionConstants &p) {
+    const uint32_t BH = p.B * p.Nq, nQT = p.qTilesPerHead;
+    const uint32_t rank = blockIdx.x / BH;
+    FaWork w{};
+    w.bh = blockIdx.x % BH;
+    w.n = 1;
+    if (p.splitFrom >= nQT) {
+        w.qt[0] = nQT - 1 - rank;
+        w.hi[0] = fa_steps(p, w.qt[0]);
+        return w;
     }
-    return it;
+    if (!p.pairTiles) {
+        const uint32_t sf = p.splitFrom, nItems = nQT + (nQT - sf);
+        int a = (int)nQT - 1, b = (int)sf - 1;  // next split tile, next whole tile
+        uint32_t halves = 2;
+        for (uint32_t r = 0; r < nItems; ++r) {
+            const bool takeSplit = a >= (int)sf && (b < 0 || (fa_steps(p, a) + 1) / 2 >= fa_steps(p, b));
+            if (r == rank) {
+                const uint32_t qt = (uint32_t)(takeSplit ? a : b), n = fa_steps(p, qt), half = (n + 1) / 2;
+                w.qt[0] = qt;
+                w.split[0] = takeSplit;
+                w.part[0] = takeSplit ? 2u - halves : 0u;
+                w.lo[0] = takeSplit && w.part[0] == 1u ? half : 0u;
+                w.hi[0] = takeSplit && w.part[0] == 0u ? half : n;
+                break;
+            }
+            if (takeSplit) {
+                if (--halves == 0) {
+                    --a;
+                    halves = 2;
+                }
+            } else {
+                --b;
+            }
+        }
+        return w;
+    }
+    const uint32_t pairs = nQT / 2;
+    if (rank >= 2 * pairs) {  // the middle tile of an odd count
+        w.qt[0] = pairs;
+        w.hi[0] = fa_steps(p, pairs);
+        return w;
+    }
+    const uint32_t i = rank >> 1, a = i, bt = nQT - 1 - i;
+    const uint32_t sa = fa_steps(p, a), sb = fa_steps(p, bt);
+    const uint32_t x = (sa + sb + 1) / 2 - sa;
+    if ((rank & 1u) == 0u) {
+        w.n = 2;
+        w.qt[0] = a;
+        w.hi[0] = sa;
+        w.qt[1] = bt;
+        w.hi[1] = x;
+        w.split[1] = true;
+    } else {
+        w.qt[0] = bt;
+        w.lo[0] = x;
+        w.hi[0] = sb;
+        w.split[0] = true;
+        w.part[0] = 1;
+    }
+    return w;
 }
 
 template <typename T, typename O, int HD>
@@ -116,9 +167,8 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
 
     const uint32_t lane = threadIdx.x & 63, h = lane >> 5, c32 = lane & 31;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const FaItem item = fa_item(p);
-    const uint32_t qt = item.qt;
-    const uint32_t bh = item.bh;  // b * Nq + hq
+    const FaWork work = fa_work(p);
+    const uint32_t bh = work.bh;  // b * Nq + hq
     const uint32_t b = bh / p.Nq, hq = bh % p.Nq;
     const uint32_t hkv = hq / (p.Nq / p.Nkv);
     const uint32_t stride = p.kvStride ? p.kvStride : p.Sk;
@@ -126,33 +176,14 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
     const uint64_t kvoff = (uint64_t)(b * p.Nkv + hkv) * stride * HD;
     const uint16_t *Kh = K + kvoff;
     const uint16_t *Vh = V + kvoff;
-    const uint32_t myq = qt * BQ + wave * 32 + c32;
-    const int posQ = (int)p.Sk - (int)p.Sq + (int)myq;
-    const int posQ0 = (int)p.Sk - (int)p.Sq + (int)(qt * BQ + wave * 32);  // the wave's first row
+    // the current item's tile, this lane's query row and the wave's first
+    uint32_t qt = 0, myq = 0;
+    int posQ = 0, posQ0 = 0;
     // scores, m and the rescale gap are kept in log2 units: exp(x) = 2^(x log2 e)
     const float c2 = p.scale * kLog2e;
-
     u32x4 qf[KS];
-    {
-        const uint16_t *qrow = Qh + (uint64_t)min(myq, p.Sq - 1) * HD + h * 8;
-#pragma unroll
-        for (int s = 0; s < KS; ++s) qf[s] = *reinterpret_cast<const u32x4 *>(qrow + s * 16);
-    }
     f32x16 acc[DT];
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) acc[dt][i] = 0.0f;
     float m = -INFINITY, l = 0.0f;
-
-    // keys any query of the block may see; a split tile's halves take the
-    // first ceil(n / 2) and the remaining key steps
-    int kLo, kHi;
-    fa_key_range(p, qt, kLo, kHi);
-    const uint32_t nSteps = kHi > kLo ? (uint32_t)(kHi - kLo + BKV - 1) / BKV : 0u;
-    const uint32_t half = (nSteps + 1) / 2;
-    const uint32_t itLo = item.split && item.part == 1u ? half : 0u;
-    const uint32_t itHi = item.split && item.part == 0u ? half : nSteps;
 
     // Staging of one step: K as 16-byte chunks (row-major), V as 4 keys x 8
     // dims per thread so its transpose is written as 8-byte runs of 4 keys.
@@ -346,55 +377,82 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
         }
     };
 
-    // Every pass issues both sets' loads (steps past the range re-read the
-    // last one): with loads on every path the compiler's wait for set A
-    // leaves set B in flight, which a conditional load would not.
-    if (itLo < itHi) {
-        auto kstep = [&](uint32_t it) { return (uint32_t)kLo + min(it, itHi - 1) * BKV; };
-        gload(krA, vrA, kstep(itLo));
-        gload(krB, vrB, kstep(itLo + 1));
-        for (uint32_t it = itLo; it < itHi; it += 2) {
-            __syncthreads();  // the previous step's readers are done
-            lstore(krA, vrA);
-            __syncthreads();
-            gload(krA, vrA, kstep(it + 2));
-            compute(kstep(it));
-            __syncthreads();
-            lstore(krB, vrB);
-            __syncthreads();
-            gload(krB, vrB, kstep(it + 3));
-            if (it + 1 < itHi) compute(kstep(it + 1));
+    auto item = [&](uint32_t w) {
+        qt = work.qt[w];
+        myq = qt * BQ + wave * 32 + c32;
+        posQ = (int)p.Sk - (int)p.Sq + (int)myq;
+        posQ0 = (int)p.Sk - (int)p.Sq + (int)(qt * BQ + wave * 32);
+        {
+            const uint16_t *qrow = Qh + (uint64_t)min(myq, p.Sq - 1) * HD + h * 8;
+#pragma unroll
+            for (int s = 0; s < KS; ++s) qf[s] = *reinterpret_cast<const u32x4 *>(qrow + s * 16);
         }
-    }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[dt][i] = 0.0f;
+        m = -INFINITY;
+        l = 0.0f;
 
-    if (myq >= p.Sq) return;
-    if (item.split) {
-        // unnormalised O (f32), and m (log2 units) and l, of this half
-        const uint32_t tile = (bh * (p.qTilesPerHead - p.splitFrom) + (qt - p.splitFrom)) * 2u + item.part;
-        const uint64_t row = (uint64_t)tile * BQ + wave * 32 + c32;
-        float *prow = pO + row * HD;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-#pragma unroll
-            for (int i4 = 0; i4 < 4; ++i4) {
-                const uint32_t d = dt * 32 + i4 * 8 + h * 4;
-                *reinterpret_cast<float4 *>(prow + d) =
-                    float4{acc[dt][4 * i4], acc[dt][4 * i4 + 1], acc[dt][4 * i4 + 2], acc[dt][4 * i4 + 3]};
+        // keys any query of the tile may see, and the item's steps of them
+        int kLo, kHi;
+        fa_key_range(p, qt, kLo, kHi);
+        const uint32_t nSteps = kHi > kLo ? (uint32_t)(kHi - kLo + BKV - 1) / BKV : 0u;
+        const uint32_t itLo = work.lo[w], itHi = min(work.hi[w], nSteps);
+
+        // Every pass issues both sets' loads (steps past the range re-read the
+        // last one): with loads on every path the compiler's wait for set A
+        // leaves set B in flight, which a conditional load would not.
+        if (itLo < itHi) {
+            auto kstep = [&](uint32_t it) { return (uint32_t)kLo + min(it, itHi - 1) * BKV; };
+            gload(krA, vrA, kstep(itLo));
+            gload(krB, vrB, kstep(itLo + 1));
+            for (uint32_t it = itLo; it < itHi; it += 2) {
+                __syncthreads();  // the previous step's readers are done
+                lstore(krA, vrA);
+                __syncthreads();
+                gload(krA, vrA, kstep(it + 2));
+                compute(kstep(it));
+                __syncthreads();
+                lstore(krB, vrB);
+                __syncthreads();
+                gload(krB, vrB, kstep(it + 3));
+                if (it + 1 < itHi) compute(kstep(it + 1));
             }
         }
-        if (h == 0) *reinterpret_cast<float2 *>(pML + 2 * row) = float2{m, l};
-        return;
-    }
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-    typename O::storage *orow = out + ((uint64_t)bh * p.Sq + myq) * HD;
+
+        if (myq >= p.Sq) {
+            // a row past Sq (ragged last tile) writes nothing
+        } else if (work.split[w]) {
+            // unnormalised O (f32), and m (log2 units) and l, of this half
+            const uint32_t tile = (bh * (p.qTilesPerHead - p.splitFrom) + (qt - p.splitFrom)) * 2u + work.part[w];
+            const uint64_t row = (uint64_t)tile * BQ + wave * 32 + c32;
+            float *prow = pO + row * HD;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
+            for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const uint32_t d = dt * 32 + (i >> 2) * 8 + h * 4 + (i & 3);
-            orow[d] = O::store(acc[dt][i] * inv);
+                for (int i4 = 0; i4 < 4; ++i4) {
+                    const uint32_t d = dt * 32 + i4 * 8 + h * 4;
+                    *reinterpret_cast<float4 *>(prow + d) =
+                        float4{acc[dt][4 * i4], acc[dt][4 * i4 + 1], acc[dt][4 * i4 + 2], acc[dt][4 * i4 + 3]};
+                }
+            }
+            if (h == 0) *reinterpret_cast<float2 *>(pML + 2 * row) = float2{m, l};
+        } else {
+            const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+            typename O::storage *orow = out + ((uint64_t)bh * p.Sq + myq) * HD;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const uint32_t d = dt * 32 + (i >> 2) * 8 + h * 4 + (i & 3);
+                    orow[d] = O::store(acc[dt][i] * inv);
+                }
+            }
         }
-    }
+    };
+    item(0);
+    if (work.n > 1) item(1);
 }
 
 // Combine of a split tile's two halves (maxima in log2 units):

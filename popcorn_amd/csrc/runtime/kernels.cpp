@@ -211,7 +211,10 @@ public:
             c.scale = scale_;
             c.kvStride = (uint32_t)d_.cap;
             c.splitFrom = (uint32_t)(c.qTilesPerHead - nSplit_);
-            const int64_t items = d_.B * d_.Nq * ((int64_t)c.qTilesPerHead + nSplit_);
+            c.pairTiles = pairTiles_ ? 1u : 0u;
+            // one block per tile; a split tile's two halves take two, a pair
+            // of tiles two in all
+            const int64_t items = d_.B * d_.Nq * ((int64_t)c.qTilesPerHead + (pairTiles_ ? 0 : nSplit_));
             if (!nSplit_) {
                 // no split tile: the partial-state arguments are never touched
                 FixedDispatch fa(tiledName_,
@@ -220,7 +223,7 @@ public:
                 enc.dispatch(fa);
                 return;
             }
-            // the halves of split tiles: unnormalised O, then (m, l) per row
+            // the two parts of each split tile: unnormalised O, then (m, l) per row
             const int64_t rows = d_.B * d_.Nq * nSplit_ * 2 * 128;
             enc.withTemporaryTensor(ScratchSpec{{rows, d_.Hd}, DataType::f32}, [&](Tensor pO) {
                 enc.withTemporaryTensor(ScratchSpec{{rows, 2}, DataType::f32}, [&](Tensor pML) {
@@ -314,21 +317,40 @@ private:
     // twice the mean number of keys and, one tile per CU, set the kernel's
     // time. Tiles with more than half the largest tile's key steps run as
     // two blocks over the halves of their keys, merged by a second kernel.
+    // Causal prefill with at most two tiles per CU splits tiles in two
+    // (flash_attention_tiled.hip, fa_work). With at most one tile per CU a
+    // head's query tiles are paired light with heavy (tile i with nQT - 1 - i)
+    // and each pair runs as two blocks of equal work, when every pair splits
+    // its heavy tile (x >= 1 steps in the first block); otherwise the tiles
+    // with more than half the heaviest tile's steps run as two halves.
     void planTileSplit() {
         nSplit_ = 0;
+        pairTiles_ = false;
         const int64_t nQT = cdiv(d_.Sq, 128);
-        if (mask_.kind != 0 || nQT < 4 || d_.B * d_.Nq * nQT > 2 * (int64_t)deviceCUs()) return;
+        const int64_t tiles = d_.B * d_.Nq * nQT;
+        if (mask_.kind != 0 || nQT < 4 || tiles > 2 * (int64_t)deviceCUs()) return;
         auto steps = [&](int64_t qt) {
             const int64_t last = d_.Sk - d_.Sq + std::min(qt * 128 + 127, d_.Sq - 1);
             const int64_t hi = std::min(d_.Sk, last + 1);
             return hi > 0 ? cdiv(hi, 32) : int64_t(0);
         };
+        mergeName_ = std::string("flash_attention_split_merge_") + tag(out_.dataType) + "_d" + std::to_string(d_.Hd);
+        bool pairs = tiles <= (int64_t)deviceCUs();
+        for (int64_t i = 0; pairs && i < nQT / 2; ++i) {
+            const int64_t sa = steps(i), sb = steps(nQT - 1 - i);
+            const int64_t x = (sa + sb + 1) / 2 - sa;
+            pairs = x >= 1 && x < sb;
+        }
+        if (pairs) {
+            pairTiles_ = true;
+            nSplit_ = nQT / 2;
+            return;
+        }
         const int64_t most = steps(nQT - 1);
         int64_t from = nQT;
         while (from > 0 && steps(from - 1) * 2 > most) --from;
         if (most < 4 || from == nQT) return;
         nSplit_ = nQT - from;
-        mergeName_ = std::string("flash_attention_split_merge_") + tag(out_.dataType) + "_d" + std::to_string(d_.Hd);
     }
 
     void planSplit() {
@@ -349,6 +371,7 @@ private:
     Kernels::AttentionPath path_ = Kernels::AttentionPath::plain;
     std::string partialName_, reduceName_, tiledName_, mergeName_;
     int64_t nSplit_ = 0;
+    bool pairTiles_ = false;
     int64_t ngroups_ = 1, P_ = 1;
 };
 
