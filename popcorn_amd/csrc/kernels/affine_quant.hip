@@ -261,7 +261,7 @@ __device__ void q4_decode_matvec(const uint16_t *__restrict__ x_in, const uint16
         return Q4Row{W + (uint64_t)r * q.wordsPerRow, Sc + (uint64_t)r * q.kGroups, B + (uint64_t)r * q.kGroups};
     };
     const bool scatter = (p.flags & pk::kKVScatter) != 0;
-    const int32_t pos = scatter ? position[0] : 0;
+    const int32_t posLoaded = pk::load_position(position, scatter);
     auto store = [&](uint32_t unit, const float *sums) {
         const uint32_t row = unit * kRows + lane / LPR;
         if (lane % LPR != 0 || row >= N) return;
@@ -269,6 +269,7 @@ __device__ void q4_decode_matvec(const uint16_t *__restrict__ x_in, const uint16
             uint32_t j = row - p.qRows;
             const bool isV = j >= p.kvRows;
             if (isV) j -= p.kvRows;
+            const int32_t pos = pk::position_value(posLoaded);
             if (pos >= 0 && (uint32_t)pos < p.kvStride) {
                 const uint64_t at = ((uint64_t)(j / p.headDim) * p.kvStride + (uint32_t)pos) * p.headDim + j % p.headDim;
                 (isV ? vcache : kcache)[at] = O::store(sums[0]);

@@ -47,7 +47,7 @@ __device__ void matvec_nk(const typename X::storage *__restrict__ x_in, const ty
     const uint32_t first = blockIdx.x * kStreamWaves + wave, stride = gridDim.x * kStreamWaves;
     const bool vec = (K % kV) == 0 && (reinterpret_cast<uintptr_t>(w) % 16) == 0;
     const bool scatter = (p.flags & pk::kKVScatter) != 0;
-    const int32_t pos = scatter ? position[0] : 0;
+    const int32_t posLoaded = pk::load_position(position, scatter);
     auto rows = [&](uint32_t unit, int s) { return w + (uint64_t)min(unit * R + s, N - 1) * K; };
 
     using Stage = pk::Stage<X, RES, PRE, J>;
@@ -62,6 +62,7 @@ __device__ void matvec_nk(const typename X::storage *__restrict__ x_in, const ty
                 uint32_t j = row - p.qRows;
                 const bool isV = j >= p.kvRows;
                 if (isV) j -= p.kvRows;
+                const int32_t pos = pk::position_value(posLoaded);
                 if (pos >= 0 && (uint32_t)pos < p.kvStride) {
                     const uint64_t at = ((uint64_t)(j / p.headDim) * p.kvStride + (uint32_t)pos) * p.headDim + j % p.headDim;
                     (isV ? vcache : kcache)[at] = O::store(sums[r]);

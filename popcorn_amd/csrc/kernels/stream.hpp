@@ -30,6 +30,24 @@ constexpr uint32_t kKVScatter = 4u;  // DecodeMatvecConstants.flags bit 2 (runti
 
 __device__ inline uint32_t uniform(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
 
+// The device position read by a vector (buffer) load, issued where it is
+// called: a plain read of a uniform address becomes a scalar load, and
+// scalar loads are waited for all together, so the kernel's first use of an
+// argument would wait for this memory round trip before a weight load could
+// go out. With `valid` false the load reads nothing (an empty buffer) and
+// returns 0, so every path issues the same loads. Read the value through
+// position_value() where it is used: the compiler would otherwise move the
+// value to a scalar register, and wait for the load, right after issuing it.
+__device__ inline int32_t load_position(const int32_t *position, bool valid) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int32_t *>(valid ? position : nullptr), 0, valid ? 4 : 0, 0x00020000);
+    return (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r, 0, 0, 0);
+}
+__device__ inline int32_t position_value(int32_t loaded) {
+    asm volatile("" : "+v"(loaded));
+    return loaded;
+}
+
 // Sum over the block (every thread gets it); `red` holds one float per wave.
 __device__ inline float block_sum(float v, float *red) {
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
