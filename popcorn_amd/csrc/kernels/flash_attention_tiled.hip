@@ -441,12 +441,23 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
         } else {
             const float inv = l > 0.0f ? 1.0f / l : 0.0f;
             typename O::storage *orow = out + ((uint64_t)bh * p.Sq + myq) * HD;
+            // the lane's 4 consecutive dims d .. d + 3 of each (dt, i4) go out
+            // as one store (16 bytes in f32, 8 in 16-bit types): a lane's
+            // row is 64 lanes away from its neighbour's, so every element
+            // store would be a separate memory transaction
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const uint32_t d = dt * 32 + (i >> 2) * 8 + h * 4 + (i & 3);
-                    orow[d] = O::store(acc[dt][i] * inv);
+                for (int i4 = 0; i4 < 4; ++i4) {
+                    const uint32_t d = dt * 32 + i4 * 8 + h * 4;
+                    const float v0 = acc[dt][4 * i4] * inv, v1 = acc[dt][4 * i4 + 1] * inv;
+                    const float v2 = acc[dt][4 * i4 + 2] * inv, v3 = acc[dt][4 * i4 + 3] * inv;
+                    if constexpr (std::is_same<O, pk::F32>::value) {
+                        *reinterpret_cast<float4 *>(orow + d) = float4{v0, v1, v2, v3};
+                    } else {
+                        auto b16 = [](float x) { return (uint32_t)__builtin_bit_cast(uint16_t, O::store(x)); };
+                        *reinterpret_cast<uint2 *>(orow + d) = uint2{b16(v0) | (b16(v1) << 16), b16(v2) | (b16(v3) << 16)};
+                    }
                 }
             }
         }

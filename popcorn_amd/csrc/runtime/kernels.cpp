@@ -165,12 +165,12 @@ public:
             requireElements(pos_, 1, "position");
         }
         path_ = Kernels::route(d.Sq, d.Hd, q.dataType);
-        // the tiled kernel reads Q/K/V as 16-byte runs, takes a fixed key
-        // length (no device-side position), addresses a head's keys with
-        // 32-bit buffer offsets and tracks row maxima on unscaled scores
-        // (scale > 0)
+        // the tiled kernel reads Q/K/V and writes O as 8- and 16-byte runs,
+        // takes a fixed key length (no device-side position), addresses a
+        // head's keys with 32-bit buffer offsets and tracks row maxima on
+        // unscaled scores (scale > 0)
         if (path_ == Kernels::AttentionPath::tiled &&
-            (hasPos_ || !aligned16(q.data) || !aligned16(k.data) || !aligned16(v.data) ||
+            (hasPos_ || !aligned16(q.data) || !aligned16(k.data) || !aligned16(v.data) || !aligned16(out.data) ||
              !(out.dataType == q.dataType || out.dataType == DataType::f32) || !(scale > 0.0f) ||
              d.Sk * d.Hd * 2 >= (int64_t{1} << 31)))
             path_ = Kernels::AttentionPath::plain;
