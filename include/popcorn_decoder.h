@@ -55,6 +55,15 @@ typedef struct {
     int32_t weight_bits;  /* 16 (or 0): bf16 weights; 4: block-affine 4-bit, group
                              64, bf16 scales and biases (the MLX format of
                              AffineQuantizedTensor.swift), embedding included  */
+    int32_t fused_layers; /* 1: the layers of a step run as one persistent kernel
+                             (decode_layers_bf16_h<Hd>_g<G>, one block per CU,
+                             grid-wide waits between its phases) followed by
+                             the head's three kernels, where the shape allows
+                             it (bf16 weights, no attention_block, a compiled
+                             head dim and group size, LDS and occupancy for
+                             one block per CU); otherwise, and with 0, six
+                             kernels per layer. popcorn_decoder_describe
+                             lists what a step dispatches.                     */
 } popcorn_decoder_config_t;
 
 typedef struct popcorn_decoder_s *popcorn_decoder_t;
@@ -71,7 +80,10 @@ popcorn_status_t popcorn_decoder_randomize(popcorn_decoder_t decoder, uint64_t s
  * "w_gate", "w_up", "w_down", "norm_in", "norm_post_attn", "norm_pre_ffn",
  * "norm_post_ffn", "k_cache", "v_cache" and, with attention_block, "q_norm"
  * and "k_norm" (per `layer`); "inv_freq" (attention_block), "x", "logits",
- * "token", "position", "history", plus the last layer's step buffers
+ * "token", "position", "history", "layer_stamps" (after
+ * popcorn_decoder_phase_times: the persistent kernel's last stamped step,
+ * u64 [blocks][2048], per block and wait the 100 MHz clock at arrival and at
+ * release), plus the last layer's step buffers
  * "q", "qkv", "attn", "o", "mlp", "hidden" and "x2" (the residual stream
  * the last layer's MLP and the head read: after a step it holds the stream
  * after the last attention block, while "x" holds the next step's input
@@ -126,6 +138,17 @@ popcorn_status_t popcorn_decoder_time_kernel(popcorn_decoder_t decoder, const ch
  * steps: 1..16. */
 popcorn_status_t popcorn_decoder_time_kernel_in_step(popcorn_decoder_t decoder, const char *function_name,
                                                      int32_t steps, float *mean_ms, int32_t *launches);
+
+/* Phase times of the persistent layer kernel (fused_layers): runs `steps`
+ * eager decode steps from the current position (advancing it) with the
+ * kernel's per-block stamps on (the 100 MHz clock read by each block when it
+ * arrives at a grid-wide wait and when the wait releases), and reports for
+ * each of the six phases of a layer (0 QKV, 1 attention partials, 2 combine,
+ * 3 O projection, 4 gate/up, 5 down) the mean over layers and steps of
+ * (last release of the phase's wait) - (last release of the previous wait),
+ * in microseconds, in phase_us[0..5]. -1001 when the decoder does not run
+ * the fused kernel. steps: 1..16. */
+popcorn_status_t popcorn_decoder_phase_times(popcorn_decoder_t decoder, int32_t steps, float *phase_us);
 
 #ifdef __cplusplus
 }

@@ -374,6 +374,33 @@ typedef struct {
     uint32_t hasBias;
 } DecodeNextTokenConstants;
 
+/* No counterpart in the reference: the decoder layers of one batch-1 decode
+ * step (Gemma4TextInference.swift:312-436, `layers` times, in the headline
+ * decode configuration: no per-head norms or RoPE) as one persistent kernel,
+ * one block per CU. Each layer runs as six phases separated by grid-wide
+ * waits on arrival counters (QKV matvec with the residual glue and the
+ * KV-cache writes; split-KV attention over `partitions` partitions per KV
+ * head; the log-sum-exp combine; the O projection; the gate/up matvec with
+ * the residual glue; the down matvec). Before each wait every wave issues the
+ * first weight loads of its next phase (and of the next layer's KV rows), so
+ * memory streams through the synchronisation. spinTicks bounds each wait
+ * (100 MHz ticks, 0: 0.5 s); a wait that runs out sets the abort word and
+ * the kernel finishes without waiting again. */
+typedef struct {
+    uint32_t layers;
+    uint32_t H;
+    uint32_t Nq;
+    uint32_t Nkv;
+    uint32_t Hd;
+    uint32_t F;
+    uint32_t kvStride;   /* KV-cache rows per head (capacity)                 */
+    uint32_t partitions; /* split-KV partitions per KV head, 1..64            */
+    float eps;
+    float scale;         /* attention scale                                  */
+    uint32_t spinTicks;
+    uint32_t reserved;
+} DecodeLayersConstants;
+
 #ifdef __cplusplus
 }
 #endif

@@ -78,7 +78,7 @@ class DecoderConfig(C.Structure):
                 ("kv_heads", C.c_int32), ("head_dim", C.c_int32), ("ffn", C.c_int32), ("vocab", C.c_int32),
                 ("max_seq", C.c_int32), ("eps", C.c_float), ("attn_scale", C.c_float),
                 ("history_len", C.c_int32), ("graph_steps", C.c_int32), ("attention_block", C.c_int32),
-                ("rope_theta", C.c_float), ("weight_bits", C.c_int32)]
+                ("rope_theta", C.c_float), ("weight_bits", C.c_int32), ("fused_layers", C.c_int32)]
 
 
 _T = C.POINTER(TensorDesc)
@@ -211,6 +211,7 @@ PROTOTYPES = {
     "popcorn_decoder_step_bytes": (C.c_int64, [C.c_void_p, C.c_int32]),
     "popcorn_decoder_time_kernel": (_st, [C.c_void_p, C.c_char_p, C.c_int32, C.POINTER(C.c_float),
                                           C.POINTER(C.c_int32)]),
+    "popcorn_decoder_phase_times": (_st, [C.c_void_p, C.c_int32, C.POINTER(C.c_float)]),
     "popcorn_decoder_time_kernel_in_step": (_st, [C.c_void_p, C.c_char_p, C.c_int32, C.POINTER(C.c_float),
                                           C.POINTER(C.c_int32)]),
 }

@@ -1655,9 +1655,15 @@ std::unique_ptr<Kernel> Argmax(const Tensor &x, const Tensor &indices) {
 
 std::unique_ptr<Kernel> Custom(const std::string &functionName, std::vector<Binding> tensors,
                                std::vector<std::vector<uint8_t>> constants, dim3 grid, dim3 block) {
+    return Custom(functionName, std::move(tensors), std::move(constants), grid, block, 0);
+}
+
+std::unique_ptr<Kernel> Custom(const std::string &functionName, std::vector<Binding> tensors,
+                               std::vector<std::vector<uint8_t>> constants, dim3 grid, dim3 block, size_t dynamicLds) {
     DispatchSize ds;
     ds.grid = grid;
     ds.block = block;
+    ds.dynamicLds = dynamicLds;
     return std::make_unique<FixedDispatch>(functionName, std::move(tensors), std::move(constants), ds);
 }
 

@@ -432,6 +432,9 @@ std::unique_ptr<Kernel> Argmax(const Tensor &x, const Tensor &indices);
 
 std::unique_ptr<Kernel> Custom(const std::string &functionName, std::vector<Binding> tensors,
                                std::vector<std::vector<uint8_t>> constants, dim3 grid, dim3 block);
+// The same with `dynamicLds` bytes of dynamic LDS per block.
+std::unique_ptr<Kernel> Custom(const std::string &functionName, std::vector<Binding> tensors,
+                               std::vector<std::vector<uint8_t>> constants, dim3 grid, dim3 block, size_t dynamicLds);
 
 std::unique_ptr<Kernel> FillNormal(void *data, DataType dtype, uint64_t count, uint64_t seed, float mean,
                                    float stddev);
