@@ -80,10 +80,12 @@ popcorn_status_t popcorn_decoder_randomize(popcorn_decoder_t decoder, uint64_t s
  * "w_gate", "w_up", "w_down", "norm_in", "norm_post_attn", "norm_pre_ffn",
  * "norm_post_ffn", "k_cache", "v_cache" and, with attention_block, "q_norm"
  * and "k_norm" (per `layer`); "inv_freq" (attention_block), "x", "logits",
- * "token", "position", "history", "layer_stamps" (after
+ * "token", "position", "history", "layer_sync" (fused_layers: the persistent
+ * kernel's sync words, u32: arrival counters, done counter, abort word and
+ * launch epoch), "layer_stamps" (after
  * popcorn_decoder_phase_times: the persistent kernel's last stamped step,
- * u64 [blocks][2048], per block and wait the 100 MHz clock at arrival and at
- * release), plus the last layer's step buffers
+ * u64 [blocks][2048], per block the 100 MHz clock at the release of each
+ * block-wide barrier, six per layer), plus the last layer's step buffers
  * "q", "qkv", "attn", "o", "mlp", "hidden" and "x2" (the residual stream
  * the last layer's MLP and the head read: after a step it holds the stream
  * after the last attention block, while "x" holds the next step's input
@@ -141,13 +143,14 @@ popcorn_status_t popcorn_decoder_time_kernel_in_step(popcorn_decoder_t decoder, 
 
 /* Phase times of the persistent layer kernel (fused_layers): runs `steps`
  * eager decode steps from the current position (advancing it) with the
- * kernel's per-block stamps on (the 100 MHz clock read by each block when it
- * arrives at a grid-wide wait and when the wait releases), and reports for
- * each of the six phases of a layer (0 QKV, 1 attention partials, 2 combine,
- * 3 O projection, 4 gate/up, 5 down) the mean over layers and steps of
- * (last release of the phase's wait) - (last release of the previous wait),
- * in microseconds, in phase_us[0..5]. -1001 when the decoder does not run
- * the fused kernel. steps: 1..16. */
+ * kernel's per-block stamps on (the 100 MHz clock read by each block when
+ * its block-wide barrier at a phase boundary releases), and reports for each
+ * of the six intervals between a layer's barriers (0 QKV, 1 attention
+ * partials and combine, 2 O projection, 3 gate/up, 4 fetching hidden, 5 down)
+ * the mean over layers and steps of (last block's release of the next
+ * barrier) - (last block's release of this one), in microseconds, in
+ * phase_us[0..5]. -1001 when the decoder does not run the fused kernel.
+ * steps: 1..16. */
 popcorn_status_t popcorn_decoder_phase_times(popcorn_decoder_t decoder, int32_t steps, float *phase_us);
 
 #ifdef __cplusplus

@@ -377,15 +377,16 @@ typedef struct {
 /* No counterpart in the reference: the decoder layers of one batch-1 decode
  * step (Gemma4TextInference.swift:312-436, `layers` times, in the headline
  * decode configuration: no per-head norms or RoPE) as one persistent kernel,
- * one block per CU. Each layer runs as six phases separated by grid-wide
- * waits on arrival counters (QKV matvec with the residual glue and the
+ * one block per CU. Per layer: QKV matvec with the residual glue and the
  * KV-cache writes; split-KV attention over `partitions` partitions per KV
  * head; the log-sum-exp combine; the O projection; the gate/up matvec with
- * the residual glue; the down matvec). Before each wait every wave issues the
- * first weight loads of its next phase (and of the next layer's KV rows), so
- * memory streams through the synchronisation. spinTicks bounds each wait
- * (100 MHz ticks, 0: 0.5 s); a wait that runs out sets the abort word and
- * the kernel finishes without waiting again. */
+ * the residual glue; the down matvec. Blocks exchange activations through a
+ * workspace of tagged words (each value stored with a tag naming the launch,
+ * layer and phase), so a consumer waits for exactly the values it reads and
+ * no step waits for the whole grid; each block's staging wave prepares the
+ * next phase's input while its streaming waves run the current one.
+ * spinTicks bounds each wait (100 MHz ticks, 0: 0.5 s); a wait that runs out
+ * sets the abort word and the block stops waiting. */
 typedef struct {
     uint32_t layers;
     uint32_t H;

@@ -3,6 +3,8 @@
 // graph capture/replay of whole steps.
 #include <cmath>
 #include <cstring>
+#include <map>
+#include <mutex>
 #include <set>
 
 #include "decode_layers_geometry.hpp"
@@ -37,6 +39,61 @@ struct Buffer {
     }
     template <typename T = uint8_t>
     T *at(size_t byteOffset) const { return reinterpret_cast<T *>(static_cast<uint8_t *>(p) + byteOffset); }
+};
+
+// Uncached device memory (hipDeviceMallocUncached: every access goes to
+// memory, past the per-XCD L2 caches) for the words the persistent layer
+// kernel's blocks exchange within a launch. Such memory is never freed once a
+// kernel has read it: a block a decoder gives back goes to a process-wide
+// pool, keyed by device and size, and the next decoder of that shape reuses
+// it.
+class UncachedBlock {
+public:
+    UncachedBlock() = default;
+    explicit UncachedBlock(size_t bytes) : bytes_(bytes) {
+        checkHip(hipGetDevice(&dev_), "hipGetDevice");
+        std::lock_guard<std::mutex> g(mu());
+        auto &pool = free_()[{dev_, bytes}];
+        if (!pool.empty()) {
+            p = pool.back();
+            pool.pop_back();
+            return;
+        }
+        if (hipExtMallocWithFlags(&p, bytes ? bytes : 1, hipDeviceMallocUncached) != hipSuccess) {
+            (void)hipGetLastError();
+            p = nullptr;
+            throw Error::tensorAllocationFailed(bytes);
+        }
+    }
+    UncachedBlock(const UncachedBlock &) = delete;
+    UncachedBlock &operator=(const UncachedBlock &) = delete;
+    UncachedBlock &operator=(UncachedBlock &&o) noexcept {
+        std::swap(p, o.p);
+        std::swap(bytes_, o.bytes_);
+        std::swap(dev_, o.dev_);
+        return *this;
+    }
+    ~UncachedBlock() {
+        if (!p) return;
+        std::lock_guard<std::mutex> g(mu());
+        free_()[{dev_, bytes_}].push_back(p);
+    }
+    size_t bytes() const { return bytes_; }
+    template <typename T = uint8_t>
+    T *at(size_t byteOffset) const { return reinterpret_cast<T *>(static_cast<uint8_t *>(p) + byteOffset); }
+    void *p = nullptr;
+
+private:
+    size_t bytes_ = 0;
+    int dev_ = 0;
+    static std::mutex &mu() {
+        static std::mutex m;
+        return m;
+    }
+    static std::map<std::pair<int, size_t>, std::vector<void *>> &free_() {
+        static auto *pool = new std::map<std::pair<int, size_t>, std::vector<void *>>();  // lives to process exit
+        return *pool;
+    }
 };
 
 // `count` stacked [N, K] block-affine 4-bit matrices (group 64, bf16 scales
@@ -99,13 +156,14 @@ struct popcorn_decoder_s {
     std::vector<std::string> names;
 
     // fused_layers: the persistent layer kernel (decode_layers.hip), its
-    // sync words, attention partials and (for phase_times) per-block stamps
+    // sync words, tagged activation workspace and (for phase_times) per-block stamps
     bool fused = false;
     std::string layersFn;
     unsigned layersGrid = 0;
     size_t layersLds = 0;
     int64_t fdParts = 0;
-    Buffer syncWords, partials, stamps;
+    UncachedBlock syncWords, tagged;
+    Buffer stamps;
     std::unique_ptr<Kernel> layersTimed;  // the same launch with stamps on
     hipGraphExec_t graph = nullptr;
     hipGraph_t graphDef = nullptr;
@@ -173,13 +231,14 @@ struct popcorn_decoder_s {
         if (!cfg.fused_layers || q4 || cfg.attention_block || Nq % Nkv != 0) return;
         const int64_t G = Nq / Nkv;
         if (!LY::compiled((int)Hd, (int)G) || H % 8 != 0 || F % 8 != 0) return;
+        if (H > LY::kMaxStaged || QW > LY::kMaxStaged) return;  // the staging wave's vectors
+        if (H % 256 != 0) return;                                 // norm weights copied in 1 KB pieces
         int dev = 0, cus = 0, maxLds = 0;
         checkHip(hipGetDevice(&dev), "hipGetDevice");
         checkHip(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "hipDeviceGetAttribute");
         checkHip(hipDeviceGetAttribute(&maxLds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev), "hipDeviceGetAttribute");
         if (cus < 1 || Nkv > cus) return;
-        const uint32_t maxK = (uint32_t)std::max({H, QW, F});
-        const size_t lds = LY::ldsBytes((uint32_t)H, maxK);
+        const size_t lds = LY::ldsLayout((uint32_t)H, (uint32_t)QW, (uint32_t)F, (uint32_t)G, (uint32_t)Hd).bytes;
         const std::string fn = "decode_layers_bf16_h" + std::to_string(Hd) + "_g" + std::to_string(G);
         const Function &f = lib->function(fn);
         if (lds + (size_t)f.attrs.staticLds > (size_t)maxLds) return;
@@ -191,9 +250,15 @@ struct popcorn_decoder_s {
         // every block must be resident at once: the kernel's waits need all of them
         if (perCU < 1) return;
         fdParts = std::min<int64_t>(LY::kMaxPartitions, cus / Nkv);
-        syncWords = Buffer(LY::kSyncBytes);
-        checkHip(hipMemsetAsync(syncWords.p, 0, syncWords.bytes, stream), "memset");
-        partials = Buffer((size_t)(Nq * fdParts * (Hd + 2) * 4));
+        // sync words: done 0, abort 0, epoch 1; tagged words start with tag
+        // 0xffff, which the first launches never expect
+        syncWords = UncachedBlock(LY::kSyncBytes);
+        std::vector<uint32_t> words(LY::kSyncBytes / 4, 0u);
+        words[LY::kEpochWord] = 1u;
+        checkHip(hipMemcpy(syncWords.p, words.data(), LY::kSyncBytes, hipMemcpyHostToDevice), "init sync words");
+        tagged = UncachedBlock((size_t)LY::taggedLayout((uint32_t)H, (uint32_t)Nq, (uint32_t)Nkv, (uint32_t)Hd,
+                                                        (uint32_t)F, (uint32_t)fdParts).bytes);
+        checkHip(hipMemset(tagged.p, 0xff, tagged.bytes()), "memset");
         layersFn = fn;
         layersGrid = (unsigned)cus;
         layersLds = lds;
@@ -207,8 +272,8 @@ struct popcorn_decoder_s {
         Tensor tpos(position.p, Shape({1}), DataType::i32);
         Tensor tnorms(norms.p, Shape({L, 4, H}), DataType::f32);
         Tensor tkc = bf(kcache.p, {L, Nkv, S, Hd}), tvc = bf(vcache.p, {L, Nkv, S, Hd});
-        Tensor tpart(partials.p, Shape({(int64_t)(partials.bytes / 4)}), DataType::f32);
-        Tensor tsync(syncWords.p, Shape({(int64_t)(syncWords.bytes / 4)}), DataType::u32);
+        Tensor ttag(tagged.p, Shape({(int64_t)tagged.bytes()}), DataType::u8);
+        Tensor tsync(syncWords.p, Shape({(int64_t)(syncWords.bytes() / 4)}), DataType::u32);
         Tensor tstamps(stampBuffer, Shape({stampBuffer ? (int64_t)(stamps.bytes / 8) : 0}), DataType::u64);
         DecodeLayersConstants c{(uint32_t)L, (uint32_t)H, (uint32_t)Nq, (uint32_t)Nkv, (uint32_t)Hd, (uint32_t)F,
                                 (uint32_t)S, (uint32_t)fdParts, cfg.eps, cfg.attn_scale, 0u, 0u};
@@ -217,7 +282,7 @@ struct popcorn_decoder_s {
                                 {bf(wg.p, {L, F, H}), kRead}, {bf(wu.p, {L, F, H}), kRead},
                                 {bf(wd.p, {L, H, F}), kRead}, {tnorms, kRead}, {tkc, kReadWrite},
                                 {tvc, kReadWrite}, {tpos, kRead}, {tq, kWrite}, {tattn, kWrite}, {to, kWrite},
-                                {th, kWrite}, {tmlp, kWrite}, {tx2, kWrite}, {tpart, kReadWrite},
+                                {th, kWrite}, {tmlp, kWrite}, {tx2, kWrite}, {ttag, kReadWrite},
                                 {tsync, kReadWrite}, {tstamps, kReadWrite}},
                                {bytesOf(c)}, dim3(layersGrid, 1, 1), dim3(pk::layers::kThreads, 1, 1), layersLds);
     }
@@ -431,7 +496,9 @@ struct popcorn_decoder_s {
         checkHip(hipMemcpy(&abortWord, syncWords.at<uint32_t>(pk::layers::kAbortWord * 4), 4, hipMemcpyDeviceToHost),
                  "read abort word");
         if (abortWord != 0) {
-            checkHip(hipMemset(syncWords.p, 0, syncWords.bytes), "memset");
+            const uint32_t zero = 0;
+            checkHip(hipMemcpy(syncWords.at<uint32_t>(pk::layers::kAbortWord * 4), &zero, 4, hipMemcpyHostToDevice),
+                     "clear abort word");
             throw Error(POPCORN_ERR_GPU_INTERNAL,
                         "decode layers: a grid-wide wait timed out (not every block was resident); the step's results are invalid");
         }
@@ -608,6 +675,8 @@ popcorn_status_t popcorn_decoder_tensor(popcorn_decoder_t d, const char *name, i
         else if (n == "token") t = Tensor(d->token.p, Shape({1}), DataType::i32);
         else if (n == "position") t = Tensor(d->position.p, Shape({1}), DataType::i32);
         else if (n == "history") t = Tensor(d->history.p, Shape({std::max(d->cfg.history_len, 1)}), DataType::i32);
+        else if (n == "layer_sync" && d->syncWords.p)
+            t = Tensor(d->syncWords.p, Shape({(int64_t)(d->syncWords.bytes() / 4)}), DataType::u32);
         else if (n == "layer_stamps" && d->stamps.p)
             t = Tensor(d->stamps.p, Shape({(int64_t)d->layersGrid, (int64_t)pk::layers::kStampsPerBlock}), DataType::u64);
         else {
@@ -758,7 +827,7 @@ popcorn_status_t popcorn_decoder_phase_times(popcorn_decoder_t d, int32_t steps,
             popcorn_decoder_s *d;
             ~Swap() { std::swap(d->step[0], d->layersTimed); }
         } swapBack{d};
-        const size_t waits = (size_t)(6 * d->L - 1);
+        const size_t bars = (size_t)(LY::kBarriersPerLayer * d->L);
         std::vector<uint64_t> host(blocks * per);
         double sum[6] = {0, 0, 0, 0, 0, 0};
         int count[6] = {0, 0, 0, 0, 0, 0};
@@ -769,15 +838,15 @@ popcorn_status_t popcorn_decoder_phase_times(popcorn_decoder_t d, int32_t steps,
                      "read stamps");
             checkHip(hipStreamSynchronize(d->stream), "sync");
             d->checkAbort();
-            // wait k ends phase k % 6 of layer k / 6; a phase lasts from the
-            // previous wait's last release to its own wait's last release
+            // barrier k of a layer opens interval k % 6, which lasts until the
+            // next barrier's last release
             uint64_t prev = 0;
-            for (size_t k = 0; k < waits && 2 * k + 1 < per; ++k) {
+            for (size_t k = 0; k < bars && k < per; ++k) {
                 uint64_t rel = 0;
-                for (size_t b = 0; b < blocks; ++b) rel = std::max(rel, host[b * per + 2 * k + 1]);
+                for (size_t b = 0; b < blocks; ++b) rel = std::max(rel, host[b * per + k]);
                 if (k > 0 && rel > prev) {
-                    sum[k % 6] += (double)(rel - prev) * 0.01;  // 100 MHz ticks -> us
-                    count[k % 6] += 1;
+                    sum[(k - 1) % 6] += (double)(rel - prev) * 0.01;  // 100 MHz ticks -> us
+                    count[(k - 1) % 6] += 1;
                 }
                 prev = rel;
             }

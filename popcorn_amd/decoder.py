@@ -89,9 +89,9 @@ class Decoder:
         return ms.value, n.value
 
     def phase_times(self, steps: int = 4):
-        """Mean microseconds of the persistent layer kernel's six phases per layer
-        (QKV, attention partials, combine, O, gate/up, down) over `steps` eager
-        steps (advances the position)."""
+        """Mean microseconds of the persistent layer kernel's six intervals per layer
+        (QKV, attention partials + combine, O, gate/up, fetching hidden, down) over
+        `steps` eager steps (advances the position)."""
         out = (C.c_float * 6)()
         check(lib().popcorn_decoder_phase_times(self.handle, steps, out))
         return [float(v) for v in out]

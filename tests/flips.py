@@ -22,18 +22,19 @@ SCALE_NOISE = 2.0 ** -19
 MAX_AMBIGUOUS = 32
 
 
-def scaled_candidates(tf, tag, noise=SCALE_NOISE):
-    """The distinct round(tf * s) for s in [1 - noise, 1 + noise]."""
+def scaled_candidates(tf, tag, noise=SCALE_NOISE, s_lo=1.0, s_hi=1.0):
+    """The distinct round(tf * s) for s in [s_lo (1 - noise), s_hi (1 + noise)]."""
     tf = np.asarray(tf, np.float64)
     if tag == O.F32:  # no 16-bit store: the f32 bar covers the scale noise
         return [tf.astype(np.float32)]
-    lo = O.round_to((tf * (1 - noise)).astype(np.float32), tag).astype(np.float64)
-    hi = O.round_to((tf * (1 + noise)).astype(np.float32), tag).astype(np.float64)
+    a, b = s_lo * (1 - noise), s_hi * (1 + noise)
+    lo = O.round_to((tf * a).astype(np.float32), tag).astype(np.float64)
+    hi = O.round_to((tf * b).astype(np.float32), tag).astype(np.float64)
     amb = np.flatnonzero(lo != hi)
     assert amb.size <= MAX_AMBIGUOUS, f"{amb.size} elements near a midpoint"
     # element i flips where tf_i * s crosses the midpoint of its two roundings
     thresholds = np.sort((lo[amb] + hi[amb]) / 2 / tf[amb])
-    edges = np.concatenate([[1 - noise], thresholds, [1 + noise]])
+    edges = np.concatenate([[a], thresholds, [b]])
     points = (edges[:-1] + edges[1:]) / 2
     out, seen = [], set()
     for s in points:
@@ -46,8 +47,21 @@ def scaled_candidates(tf, tag, noise=SCALE_NOISE):
 
 
 def norm_candidates(x, w, eps, tag, add_one=False):
-    """16-bit RMSNorm(x) * w outcomes (RMSNorm.metal:32-40) over the scale noise."""
-    return scaled_candidates(O.rmsnorm(x, w, eps, add_one), tag)
+    """16-bit RMSNorm(x) * w outcomes (RMSNorm.metal:32-40) over the scale noise.
+
+    The window spans the reference loop's scale (a sequential f32 sum of
+    squares, the oracle's) and the exact one (the sum in float64): over a few
+    thousand terms the sequential f32 sum can itself sit a few 2^-20 from the
+    exact sum, and a kernel summing in a shallower order lands near the exact
+    scale."""
+    x = np.asarray(x, np.float32)
+    acc = np.float32(0)
+    for v in x.ravel():
+        acc = np.float32(acc + np.float32(v * v))
+    s32 = 1.0 / np.sqrt(np.float32(acc / np.float32(x.size) + np.float32(eps)))
+    s64 = 1.0 / np.sqrt(np.sum(x.astype(np.float64) ** 2) / x.size + eps)
+    r = float(s64) / float(s32)
+    return scaled_candidates(O.rmsnorm(x, w, eps, add_one), tag, s_lo=min(1.0, r), s_hi=max(1.0, r))
 
 
 def residual_candidates(x_in, delta, w_post, eps, tag):
