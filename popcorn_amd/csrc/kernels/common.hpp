@@ -158,6 +158,19 @@ __device__ inline float half32_max(float v) {
 // xor-32 exchange (the other half of the wave).
 __device__ inline float swap32(float v) { return __shfl_xor(v, 32, 64); }
 
+// max and sum of v over lanes l and l ^ 32 in registers: v_permlane32_swap
+// trades lanes 0-31 of its first operand with lanes 32-63 of its second, so
+// with v in both, lane l holds v[l | 32] in the first result and
+// v[l & 31] in the second (both halves add in the same order)
+__device__ inline float pair32_max(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float pair32_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Sum over the wave, result in every lane.
 __device__ inline float wave_sum(float v) {
     v = half32_sum(v);

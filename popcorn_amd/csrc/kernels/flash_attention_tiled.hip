@@ -17,9 +17,10 @@
 //    two products) is already the B operand of
 //    O^T += Vt . P^T for k-step ks if the 16 key slots of the step are read
 //    in the order the C layout holds them: slot (l / 32) * 8 + j is key
-//    16 ks + (j / 4) * 8 + (l / 32) * 4 + j % 4; the A operand (Vt) is read
-//    in that same order, two runs of 4 keys. O^T accumulates per lane for
-//    one query, so the softmax rescale is lane-local too.
+//    16 ks + (j / 4) * 8 + (l / 32) * 4 + j % 4; Vt rows keep the keys in
+//    that order (vt_pos), so the A operand is one 16-byte read. O^T
+//    accumulates per lane for one query, so the softmax rescale is
+//    lane-local too.
 // Causal / sliding-window keys outside the block's range are not visited;
 // the rest are masked per query. Heavy (late) query tiles start first.
 #include <type_traits>
@@ -39,12 +40,20 @@ constexpr int BKV = 32;          // keys per step
 // reference moves: softmax weights stay below e^8 ~ 2981 (f16 holds 65504).
 constexpr float kRescaleGap = 8.0f;
 constexpr float kLog2e = 1.4426950408889634f;
+// Vt rows hold a step's keys in the order of P^T's key slots (key index
+// with bits 2 and 3 swapped): slots 8 h .. 8 h + 7 of k-step ks, which lane
+// half h feeds to the product, are keys 16 ks + 4 h + 0..3 and
+// 16 ks + 8 + 4 h + 0..3, so a lane's fragment is one 16-byte read. Rows of
+// 40 elements (80 bytes) keep those reads 16-byte aligned and spread the
+// 16 rows a quarter-wave reads over all 64 banks.
+constexpr int LDV = BKV + 8;
+__device__ inline uint32_t vt_pos(uint32_t key) { return (key & ~12u) | ((key & 4u) << 1) | ((key & 8u) >> 1); }
 
+// Bitwise, not short-circuit, so a masked step's 16 keys become selects
+// rather than 16 branches.
 __device__ inline bool fa_allowed(const TiledFlashAttentionConstants &p, int posQ, int key) {
-    if (key < 0 || key >= (int)p.Sk) return false;
-    bool ok = (p.maskKind == 2u) || (key <= posQ);
-    if (p.maskKind == 1u) ok = ok && (posQ - key < p.slidingWindow);
-    return ok;
+    return (key >= 0) & (key < (int)p.Sk) & ((p.maskKind == 2u) | (key <= posQ)) &
+           ((p.maskKind != 1u) | (posQ - key < p.slidingWindow));
 }
 
 // Key steps of query tile qt: keys any query of the tile may see.
@@ -157,7 +166,6 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
     constexpr int KS = HD / 16;  // k-steps of S^T = K . Q^T
     constexpr int DT = HD / 32;  // 32-row tiles of O^T
     constexpr int LDK = HD + 8;  // sK row (padded, elements)
-    constexpr int LDV = BKV + 4; // sVt row (padded, elements; 72 bytes spread 8-byte reads over the banks)
     constexpr int kChunks = BKV * HD / 8;
     // softmax weights enter P.V in the input dtype; bf16 (8-bit significand)
     // carries them as a bf16 pair, f16 (11 bits) as one value
@@ -248,9 +256,9 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const uint32_t a = vr[i][0][j], b = vr[i][1][j], c = vr[i][2][j], e = vr[i][3][j];
-                    *reinterpret_cast<uint2 *>(&sV[(db * 8 + 2 * j) * LDV + 4 * kq]) =
+                    *reinterpret_cast<uint2 *>(&sV[(db * 8 + 2 * j) * LDV + vt_pos(4 * kq)]) =
                         uint2{__builtin_amdgcn_perm(b, a, 0x05040100u), __builtin_amdgcn_perm(e, c, 0x05040100u)};
-                    *reinterpret_cast<uint2 *>(&sV[(db * 8 + 2 * j + 1) * LDV + 4 * kq]) =
+                    *reinterpret_cast<uint2 *>(&sV[(db * 8 + 2 * j + 1) * LDV + vt_pos(4 * kq)]) =
                         uint2{__builtin_amdgcn_perm(b, a, 0x07060302u), __builtin_amdgcn_perm(e, c, 0x07060302u)};
                 }
             }
@@ -260,11 +268,10 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
     auto compute = [&](uint32_t k0) {
         // All K fragments of the step are read before the first product (the
         // scheduler otherwise pairs each LDS read with its MFMA and waits on
-        // every one); two accumulators over alternate k-steps halve the
-        // chain of dependent products.
-        f32x16 st, st2;
+        // every one); one accumulator chain.
+        f32x16 st;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) st[i] = st2[i] = 0.0f;
+        for (int i = 0; i < 16; ++i) st[i] = 0.0f;
         u32x4 kf[KS];
 #pragma unroll
         for (int s = 0; s < KS; ++s) kf[s] = *reinterpret_cast<const u32x4 *>(&sK[c32 * LDK + s * 16 + h * 8]);
@@ -272,7 +279,7 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
 #pragma unroll
         for (int s = 0; s < KS; s += 2) {
             st = Mma<T>::run(kf[s], qf[s], st);
-            st2 = Mma<T>::run(kf[s + 1], qf[s + 1], st2);
+            st = Mma<T>::run(kf[s + 1], qf[s + 1], st);
         }
         // Vt fragments of the whole step, read now so they land while the
         // softmax below runs.
@@ -281,11 +288,7 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
         for (int dt = 0; dt < DT; ++dt) {
             const uint16_t *vrow = &sV[(dt * 32 + c32) * LDV];
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                const uint2 lo = *reinterpret_cast<const uint2 *>(vrow + ks * 16 + h * 4);
-                const uint2 hi = *reinterpret_cast<const uint2 *>(vrow + ks * 16 + 8 + h * 4);
-                va[dt][ks] = u32x4{lo.x, lo.y, hi.x, hi.y};
-            }
+            for (int ks = 0; ks < 2; ++ks) va[dt][ks] = *reinterpret_cast<const u32x4 *>(vrow + ks * 16 + h * 8);
         }
         __builtin_amdgcn_sched_barrier(0);
         // The whole step is visible to every row of the wave (keys in
@@ -300,18 +303,18 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
         if (full) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                sv[i] = st[i] + st2[i];
+                sv[i] = st[i];
                 mt = fmaxf(mt, sv[i]);
             }
         } else {
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const int key = (int)k0 + (i >> 2) * 8 + (int)h * 4 + (i & 3);
-                sv[i] = fa_allowed(p, posQ, key) ? st[i] + st2[i] : -INFINITY;
+                sv[i] = fa_allowed(p, posQ, key) ? st[i] : -INFINITY;
                 mt = fmaxf(mt, sv[i]);
             }
         }
-        mt = fmaxf(mt, pk::swap32(mt)) * c2;
+        mt = pk::pair32_max(mt) * c2;
         // Lazy rescaling: a row's reference max m moves only when a score
         // passes it by more than kRescaleGap, so the weights exp(s - m) stay
         // below e^kRescaleGap (inside f16's range) and the rescale of the
@@ -365,7 +368,7 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
                     }
                 }
         }
-        ps += pk::swap32(ps);
+        ps = pk::pair32_sum(ps);
         l = l * alpha + ps;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {

@@ -136,6 +136,8 @@ MASKS = {"causal": (0, -1), "bidirectional": (2, -1), "window40": (1, 40)}
     (1, 2, 2, 96, 96, 256, "bidirectional"),
     (1, 2, 1, 128, 160, 64, "window40"),
     (1, 1, 1, 32, 32, 256, "causal"),
+    (2, 4, 2, 130, 200, 256, "causal"),        # GQA, Sq < Sk, ragged tiles at Hd 256
+    (1, 2, 1, 128, 160, 256, "window40"),
 ])
 def test_tiled_attention_vs_oracle(env, dtype, ot, B, Nq, Nkv, Sq, Sk, Hd, mask):
     pa = env[0]
@@ -176,14 +178,15 @@ def test_tiled_attention_split_tiles_vs_oracle(env, dtype, ot, B, Nq, Nkv, Sq, S
     assert_out(got, ref, EPS[dtype], ot, f"split tiled attention {dtype}->{ot} Sq={Sq} Sk={Sk} Hd={Hd}")
 
 
+@pytest.mark.parametrize("Hd", [64, 256])
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
-def test_tiled_attention_wide_score_range(env, dtype):
+def test_tiled_attention_wide_score_range(env, dtype, Hd):
     # scores spread over hundreds of natural-log units (scale 1, inputs x 3):
     # the running max moves often and far, so the lazy rescale (the reference
     # max moves only when a score passes it by more than 8) is exercised on
     # most steps, split tiles included
     pa = env[0]
-    B, Nq, Nkv, S, Hd = 1, 2, 1, 640, 64
+    B, Nq, Nkv, S = 1, 2, 1, 640
     q = rounded(3.0 * O.normal(901, (B, Nq, S, Hd)), dtype)
     k = rounded(3.0 * O.normal(902, (B, Nkv, S, Hd)), dtype)
     v = rounded(O.normal(903, (B, Nkv, S, Hd)), dtype)
