@@ -170,8 +170,10 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
     // softmax weights enter P.V in the input dtype; bf16 (8-bit significand)
     // carries them as a bf16 pair, f16 (11 bits) as one value
     constexpr bool kSplitP = std::is_same<T, pk::BF16>::value;
-    __shared__ __attribute__((aligned(16))) uint16_t sK[BKV * LDK];
-    __shared__ __attribute__((aligned(16))) uint16_t sV[HD * LDV];
+    // two LDS buffers: step s is multiplied from buffer s & 1 while the next
+    // step is written into the other
+    __shared__ __attribute__((aligned(16))) uint16_t sK[2][BKV * LDK];
+    __shared__ __attribute__((aligned(16))) uint16_t sV[2][HD * LDV];
 
     const uint32_t lane = threadIdx.x & 63, h = lane >> 5, c32 = lane & 31;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -236,13 +238,13 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
             }
         }
     };
-    auto lstore = [&](const KRegs &kr, const VRegs &vr) {
+    auto lstore = [&](const KRegs &kr, const VRegs &vr, int buf) {
 #pragma unroll
         for (int i = 0; i < kKC; ++i) {
             const uint32_t c = threadIdx.x + i * 64 * kWaves;
             if (kChunks % (64 * kWaves) == 0 || c < (uint32_t)kChunks) {
                 const uint32_t key = c / (HD / 8), dc = (c % (HD / 8)) * 8;
-                *reinterpret_cast<u32x4 *>(&sK[key * LDK + dc]) = kr[i];
+                *reinterpret_cast<u32x4 *>(&sK[buf][key * LDK + dc]) = kr[i];
             }
         }
 #pragma unroll
@@ -256,16 +258,16 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const uint32_t a = vr[i][0][j], b = vr[i][1][j], c = vr[i][2][j], e = vr[i][3][j];
-                    *reinterpret_cast<uint2 *>(&sV[(db * 8 + 2 * j) * LDV + vt_pos(4 * kq)]) =
+                    *reinterpret_cast<uint2 *>(&sV[buf][(db * 8 + 2 * j) * LDV + vt_pos(4 * kq)]) =
                         uint2{__builtin_amdgcn_perm(b, a, 0x05040100u), __builtin_amdgcn_perm(e, c, 0x05040100u)};
-                    *reinterpret_cast<uint2 *>(&sV[(db * 8 + 2 * j + 1) * LDV + vt_pos(4 * kq)]) =
+                    *reinterpret_cast<uint2 *>(&sV[buf][(db * 8 + 2 * j + 1) * LDV + vt_pos(4 * kq)]) =
                         uint2{__builtin_amdgcn_perm(b, a, 0x07060302u), __builtin_amdgcn_perm(e, c, 0x07060302u)};
                 }
             }
         }
     };
 
-    auto compute = [&](uint32_t k0) {
+    auto compute = [&](uint32_t k0, int buf) {
         // All K fragments of the step are read before the first product (the
         // scheduler otherwise pairs each LDS read with its MFMA and waits on
         // every one); one accumulator chain.
@@ -274,7 +276,7 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
         for (int i = 0; i < 16; ++i) st[i] = 0.0f;
         u32x4 kf[KS];
 #pragma unroll
-        for (int s = 0; s < KS; ++s) kf[s] = *reinterpret_cast<const u32x4 *>(&sK[c32 * LDK + s * 16 + h * 8]);
+        for (int s = 0; s < KS; ++s) kf[s] = *reinterpret_cast<const u32x4 *>(&sK[buf][c32 * LDK + s * 16 + h * 8]);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int s = 0; s < KS; s += 2) {
@@ -286,7 +288,7 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
         u32x4 va[DT][2];
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-            const uint16_t *vrow = &sV[(dt * 32 + c32) * LDV];
+            const uint16_t *vrow = &sV[buf][(dt * 32 + c32) * LDV];
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) va[dt][ks] = *reinterpret_cast<const u32x4 *>(vrow + ks * 16 + h * 8);
         }
@@ -403,24 +405,32 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
         const uint32_t nSteps = kHi > kLo ? (uint32_t)(kHi - kLo + BKV - 1) / BKV : 0u;
         const uint32_t itLo = work.lo[w], itHi = min(work.hi[w], nSteps);
 
-        // Every pass issues both sets' loads (steps past the range re-read the
-        // last one): with loads on every path the compiler's wait for set A
-        // leaves set B in flight, which a conditional load would not.
+        // Step s (counted from itLo) is multiplied from LDS buffer s & 1 and
+        // staged through register set A (even s) or B (odd s). Each step: one
+        // barrier (it publishes step s, written during step s - 1, and
+        // retires the readers of the other buffer), then step s + 1 goes from
+        // its registers into the other buffer, those registers take step
+        // s + 3, and step s is multiplied: a step's loads go out two steps
+        // before its LDS copy. Steps past the range re-read the last one, so
+        // every pass issues the same loads.
         if (itLo < itHi) {
             auto kstep = [&](uint32_t it) { return (uint32_t)kLo + min(it, itHi - 1) * BKV; };
+            __syncthreads();  // the previous item's readers of both buffers are done
             gload(krA, vrA, kstep(itLo));
             gload(krB, vrB, kstep(itLo + 1));
+            lstore(krA, vrA, 0);
+            gload(krA, vrA, kstep(itLo + 2));
             for (uint32_t it = itLo; it < itHi; it += 2) {
-                __syncthreads();  // the previous step's readers are done
-                lstore(krA, vrA);
                 __syncthreads();
-                gload(krA, vrA, kstep(it + 2));
-                compute(kstep(it));
-                __syncthreads();
-                lstore(krB, vrB);
-                __syncthreads();
+                lstore(krB, vrB, 1);
                 gload(krB, vrB, kstep(it + 3));
-                if (it + 1 < itHi) compute(kstep(it + 1));
+                compute(kstep(it), 0);
+                if (it + 1 < itHi) {
+                    __syncthreads();
+                    lstore(krA, vrA, 0);
+                    gload(krA, vrA, kstep(it + 4));
+                    compute(kstep(it + 1), 1);
+                }
             }
         }
 
