@@ -479,6 +479,260 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
     if (work.n > 1) item(1);
 }
 
+// ---- 16 query rows per wave -------------------------------------------------------
+// The same tiles (128 rows), items, masks, lazy rescale and outputs as
+// fa_tiled on 8 waves of 16 rows, with v_mfma_f32_16x16x32 (mfma.hpp). A
+// wave's output is HD x 16 (HD / 4 accumulators per lane), which keeps a
+// wave within 256 registers at Hd 256, so two waves share each SIMD; every
+// wave runs the whole step for its own rows. Per step of 32 keys:
+//  * S^T = K . Q^T as two 16-key tiles; lane l holds the scores of query
+//    l % 16 for keys 4 g + i and 16 + 4 g + i (g = l / 16, i < 4), so the
+//    row max and sum run over 8 values and the lanes l, l ^ 16, l ^ 32
+//    (v_permlane16_swap, v_permlane32_swap);
+//  * those 8 weights, in that order, are the lane's P^T slots 8 g .. 8 g + 7
+//    for O^T += Vt . P^T; Vt rows hold the keys in the same slot order
+//    (vt16_pos), so a lane's Vt fragment is one 16-byte read;
+//  * K rows in LDS keep 16-byte chunk c of row r in slot c ^ (r % chunks),
+//    so the 16 rows a quarter-wave reads fall in 16 distinct bank groups.
+constexpr int kWaves16 = 8;
+
+__device__ inline uint32_t vt16_pos(uint32_t key) {
+    return key < 16u ? (key >> 2) * 8u + (key & 3u) : ((key - 16u) >> 2) * 8u + 4u + (key & 3u);
+}
+__device__ inline float quad16_max(float v) { return pk::pair32_max(pk::pair16_max(v)); }
+__device__ inline float quad16_sum(float v) { return pk::pair32_sum(pk::pair16_sum(v)); }
+
+template <typename T, typename O, int HD>
+__device__ void fa_tiled16(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
+                           const uint16_t *__restrict__ V, typename O::storage *__restrict__ out,
+                           float *__restrict__ pO, float *__restrict__ pML, const TiledFlashAttentionConstants &p) {
+    constexpr int KS = HD / 32;   // k-steps of each S^T tile
+    constexpr int DT = HD / 16;   // 16-row tiles of O^T
+    constexpr int CH = HD / 8;    // 16-byte chunks per K row
+    constexpr int kThreads = 64 * kWaves16;
+    constexpr bool kSplitP = std::is_same<T, pk::BF16>::value;
+    static_assert(CH >= 16, "the K swizzle needs 16 chunks per row");
+    __shared__ __attribute__((aligned(16))) uint16_t sK[2][BKV * HD];
+    __shared__ __attribute__((aligned(16))) uint16_t sV[2][HD * LDV];
+
+    const uint32_t lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const FaWork work = fa_work(p);
+    const uint32_t bh = work.bh;
+    const uint32_t b = bh / p.Nq, hq = bh % p.Nq;
+    const uint32_t hkv = hq / (p.Nq / p.Nkv);
+    const uint32_t stride = p.kvStride ? p.kvStride : p.Sk;
+    const uint16_t *Qh = Q + (uint64_t)bh * p.Sq * HD;
+    const uint64_t kvoff = (uint64_t)(b * p.Nkv + hkv) * stride * HD;
+    uint32_t qt = 0, myq = 0;
+    int posQ = 0, posQ0 = 0;
+    const float c2 = p.scale * kLog2e;
+    u32x4 qf[KS];
+    pk::f32x4 acc[DT];
+    float m = -INFINITY, l = 0.0f;
+
+    // Staging: K as 16-byte chunks (thread t takes chunks t + i kThreads),
+    // V as two consecutive keys x 8 dims per (key pair, dim block), written
+    // transposed as 32-bit words of two keys. Rows past Sk read as zeros.
+    constexpr int kKC = (BKV * CH + kThreads - 1) / kThreads;
+    constexpr int kVP = (BKV / 2) * (HD / 8);
+    constexpr int kVC = (kVP + kThreads - 1) / kThreads;
+    using KRegs = u32x4[kKC];
+    using VRegs = u32x4[kVC][2];
+    u32x4 krA[kKC], vrA[kVC][2], krB[kKC], vrB[kVC][2];
+    const __amdgpu_buffer_rsrc_t rsK = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(K + kvoff), 0,
+                                                                          (int)(p.Sk * HD * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsV = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(V + kvoff), 0,
+                                                                          (int)(p.Sk * HD * 2), 0x00020000);
+    auto gload = [&](KRegs &kr, VRegs &vr, uint32_t k0) {
+        const int so = (int)(k0 * HD * 2);
+#pragma unroll
+        for (int i = 0; i < kKC; ++i) {
+            const uint32_t c = threadIdx.x + i * kThreads;
+            if ((BKV * CH) % kThreads == 0 || c < (uint32_t)(BKV * CH)) {
+                const uint32_t key = c / CH, ch = c % CH;
+                kr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsK, (int)((key * HD + ch * 8) * 2), so, 0));
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kVC; ++i) {
+            const uint32_t pr = threadIdx.x + i * kThreads;
+            if (kVP % kThreads == 0 || pr < (uint32_t)kVP) {
+                const uint32_t kp = pr % (BKV / 2), db = pr / (BKV / 2);
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    vr[i][j] = __builtin_bit_cast(
+                        u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsV, (int)(((2 * kp + j) * HD + db * 8) * 2), so, 0));
+            }
+        }
+    };
+    auto lstore = [&](const KRegs &kr, const VRegs &vr, int buf) {
+#pragma unroll
+        for (int i = 0; i < kKC; ++i) {
+            const uint32_t c = threadIdx.x + i * kThreads;
+            if ((BKV * CH) % kThreads == 0 || c < (uint32_t)(BKV * CH)) {
+                const uint32_t key = c / CH, ch = c % CH;
+                *reinterpret_cast<u32x4 *>(&sK[buf][key * HD + ((ch ^ (key % CH)) * 8)]) = kr[i];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kVC; ++i) {
+            const uint32_t pr = threadIdx.x + i * kThreads;
+            if (kVP % kThreads == 0 || pr < (uint32_t)kVP) {
+                const uint32_t kp = pr % (BKV / 2), db = pr / (BKV / 2);
+                const uint32_t at = vt16_pos(2 * kp);
+                // word j of a key row holds dims 2j (low half) and 2j + 1
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t a = vr[i][0][j], e = vr[i][1][j];
+                    *reinterpret_cast<uint32_t *>(&sV[buf][(db * 8 + 2 * j) * LDV + at]) = __builtin_amdgcn_perm(e, a, 0x05040100u);
+                    *reinterpret_cast<uint32_t *>(&sV[buf][(db * 8 + 2 * j + 1) * LDV + at]) = __builtin_amdgcn_perm(e, a, 0x07060302u);
+                }
+            }
+        }
+    };
+
+    auto compute = [&](uint32_t k0, int buf) {
+        pk::f32x4 st[2];
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+            st[mt] = pk::f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            const uint32_t row = mt * 16 + c16;
+            // K fragments four at a time (registers: two waves share a SIMD)
+#pragma unroll
+            for (int s0 = 0; s0 < KS; s0 += 4) {
+                u32x4 kf[4];
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+                    kf[s] = *reinterpret_cast<const u32x4 *>(&sK[buf][row * HD + ((((s0 + s) * 4 + g) ^ (row % CH)) * 8)]);
+#pragma unroll
+                for (int s = 0; s < 4; ++s) st[mt] = pk::Mma16<T>::run(kf[s], qf[s0 + s], st[mt]);
+            }
+        }
+        const bool full = (int)k0 + BKV <= (int)p.Sk && (p.maskKind == 2u || (int)k0 + BKV - 1 <= posQ0) &&
+                          (p.maskKind != 1u || posQ0 + 15 - (int)k0 < (int)p.slidingWindow);
+        float sv[8];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int key = (int)k0 + mt * 16 + (int)g * 4 + i;
+                sv[mt * 4 + i] = (full || fa_allowed(p, posQ, key)) ? st[mt][i] : -INFINITY;
+                mx = fmaxf(mx, sv[mt * 4 + i]);
+            }
+        mx = quad16_max(mx) * c2;
+        const bool move = mx > m + kRescaleGap * kLog2e;
+        float alpha = 1.0f, ps = 0.0f;
+        if (move) {
+            const float mn = fmaxf(m, mx);
+            alpha = __builtin_amdgcn_exp2f(m - mn);
+            m = mn;
+        }
+        if (__ballot(move)) {
+            // the accumulators stay in VGPRs here (a wave's 256 registers
+            // hold all of its state), so a plain multiply
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
+        }
+        u32x4 pf, pfr;
+        if (m == -INFINITY) {
+            pf = pfr = u32x4{0u, 0u, 0u, 0u};
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float p0 = __builtin_amdgcn_exp2f(fmaf(sv[2 * j], c2, -m));
+                const float p1 = __builtin_amdgcn_exp2f(fmaf(sv[2 * j + 1], c2, -m));
+                ps += p0 + p1;
+                const uint32_t w = pk::pack2<T>(p0, p1);
+                pf[j] = w;
+                if constexpr (kSplitP) {
+                    pfr[j] = pk::pack2<T>(p0 - __uint_as_float(w << 16), p1 - __uint_as_float(w & 0xffff0000u));
+                } else {
+                    pfr[j] = 0u;
+                }
+            }
+        }
+        l = l * alpha + quad16_sum(ps);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            const u32x4 va = *reinterpret_cast<const u32x4 *>(&sV[buf][(dt * 16 + c16) * LDV + g * 8]);
+            acc[dt] = pk::Mma16<T>::run(va, pf, acc[dt]);
+            if constexpr (kSplitP) acc[dt] = pk::Mma16<T>::run(va, pfr, acc[dt]);
+        }
+    };
+
+    auto item = [&](uint32_t w) {
+        qt = work.qt[w];
+        myq = qt * BQ + wave * 16 + c16;
+        posQ = (int)p.Sk - (int)p.Sq + (int)myq;
+        posQ0 = (int)p.Sk - (int)p.Sq + (int)(qt * BQ + wave * 16);
+        {
+            const uint16_t *qrow = Qh + (uint64_t)min(myq, p.Sq - 1) * HD + g * 8;
+#pragma unroll
+            for (int s = 0; s < KS; ++s) qf[s] = *reinterpret_cast<const u32x4 *>(qrow + s * 32);
+        }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) acc[dt] = pk::f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        m = -INFINITY;
+        l = 0.0f;
+        int kLo, kHi;
+        fa_key_range(p, qt, kLo, kHi);
+        const uint32_t nSteps = kHi > kLo ? (uint32_t)(kHi - kLo + BKV - 1) / BKV : 0u;
+        const uint32_t itLo = work.lo[w], itHi = min(work.hi[w], nSteps);
+        // the double-buffered loop of fa_tiled: one barrier per step, a
+        // step's loads two steps ahead of its LDS copy
+        if (itLo < itHi) {
+            auto kstep = [&](uint32_t it) { return (uint32_t)kLo + min(it, itHi - 1) * BKV; };
+            __syncthreads();
+            gload(krA, vrA, kstep(itLo));
+            gload(krB, vrB, kstep(itLo + 1));
+            lstore(krA, vrA, 0);
+            gload(krA, vrA, kstep(itLo + 2));
+            for (uint32_t it = itLo; it < itHi; it += 2) {
+                __syncthreads();
+                lstore(krB, vrB, 1);
+                gload(krB, vrB, kstep(it + 3));
+                compute(kstep(it), 0);
+                if (it + 1 < itHi) {
+                    __syncthreads();
+                    lstore(krA, vrA, 0);
+                    gload(krA, vrA, kstep(it + 4));
+                    compute(kstep(it + 1), 1);
+                }
+            }
+        }
+
+        if (myq >= p.Sq) {
+            // a row past Sq (ragged last tile) writes nothing
+        } else if (work.split[w]) {
+            const uint32_t tile = (bh * (p.qTilesPerHead - p.splitFrom) + (qt - p.splitFrom)) * 2u + work.part[w];
+            const uint64_t row = (uint64_t)tile * BQ + wave * 16 + c16;
+            float *prow = pO + row * HD;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+                *reinterpret_cast<float4 *>(prow + dt * 16 + g * 4) = float4{acc[dt][0], acc[dt][1], acc[dt][2], acc[dt][3]};
+            if (g == 0) *reinterpret_cast<float2 *>(pML + 2 * row) = float2{m, l};
+        } else {
+            const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+            typename O::storage *orow = out + ((uint64_t)bh * p.Sq + myq) * HD;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                const uint32_t d = dt * 16 + g * 4;
+                const float v0 = acc[dt][0] * inv, v1 = acc[dt][1] * inv, v2 = acc[dt][2] * inv, v3 = acc[dt][3] * inv;
+                if constexpr (std::is_same<O, pk::F32>::value) {
+                    *reinterpret_cast<float4 *>(orow + d) = float4{v0, v1, v2, v3};
+                } else {
+                    auto b16 = [](float x) { return (uint32_t)__builtin_bit_cast(uint16_t, O::store(x)); };
+                    *reinterpret_cast<uint2 *>(orow + d) = uint2{b16(v0) | (b16(v1) << 16), b16(v2) | (b16(v3) << 16)};
+                }
+            }
+        }
+    };
+    item(0);
+    if (work.n > 1) item(1);
+}
+
 // Combine of a split tile's two halves (maxima in log2 units):
 //   M = max(m0, m1), w_i = 2^(m_i - M) (0 for a half with no visible key),
 //   O = (w0 O0 + w1 O1) / (w0 l0 + w1 l1),
@@ -528,6 +782,13 @@ __device__ void fa_split_merge(const float *__restrict__ pO, const float *__rest
     FA_TILED(flash_attention_tiled_##t##_##o##_d64, T, O, 64)    \
     FA_TILED(flash_attention_tiled_##t##_##o##_d128, T, O, 128)  \
     FA_TILED(flash_attention_tiled_##t##_##o##_d256, T, O, 256)
+#define FA_TILED16(name, T, O, HD)                                                                     \
+    POPCORN_KERNEL void __launch_bounds__(64 * kWaves16)                                               \
+        name(const uint16_t *q, const uint16_t *k, const uint16_t *v, O::storage *out, float *pO,      \
+             float *pML, TiledFlashAttentionConstants p) {                                               \
+        fa_tiled16<T, O, HD>(q, k, v, out, pO, pML, p);                                                \
+    }
+#define FA_TILED16_D(t, T, o, O) FA_TILED16(flash_attention_tiled16_##t##_##o##_d256, T, O, 256)
 #define FA_MERGE(name, O, HD)                                                                          \
     POPCORN_KERNEL void __launch_bounds__(256)                                                         \
         name(const float *pO, const float *pML, O::storage *out, TiledFlashAttentionConstants p) {       \
@@ -546,6 +807,10 @@ FA_TILED_D(f16, F16, f16, F16)
 FA_TILED_D(f16, F16, f32, F32)
 FA_TILED_D(bf16, BF16, bf16, BF16)
 FA_TILED_D(bf16, BF16, f32, F32)
+FA_TILED16_D(f16, F16, f16, F16)
+FA_TILED16_D(f16, F16, f32, F32)
+FA_TILED16_D(bf16, BF16, bf16, BF16)
+FA_TILED16_D(bf16, BF16, f32, F32)
 FA_MERGE_D(f16, F16)
 FA_MERGE_D(bf16, BF16)
 FA_MERGE_D(f32, F32)

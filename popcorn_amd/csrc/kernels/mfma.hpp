@@ -31,6 +31,28 @@ struct Mma<BF16> {
     }
 };
 
+// v_mfma_f32_16x16x32_{f16,bf16}, for C[16 x 16] += A[16 x 32] . B[32 x 16]:
+//   A fragment: lane l holds A[l % 16][(l / 16) * 8 + i], i < 8
+//   B fragment: lane l holds B[(l / 16) * 8 + i][l % 16]
+//   C (4 floats): lane l, element i is C[(l / 16) * 4 + i][l % 16]
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+template <typename T>
+struct Mma16;
+template <>
+struct Mma16<F16> {
+    __device__ static inline f32x4 run(u32x4 a, u32x4 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0,
+                                                      0, 0);
+    }
+};
+template <>
+struct Mma16<BF16> {
+    __device__ static inline f32x4 run(u32x4 a, u32x4 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf168, a), __builtin_bit_cast(bf168, b), c,
+                                                       0, 0, 0);
+    }
+};
+
 // 16-bit storage bits of x in T (f16 IEEE RNE; bf16 the reference's formula).
 template <typename T>
 __device__ inline uint32_t bits16(float x);

@@ -175,8 +175,13 @@ public:
              d.Sk * d.Hd * 2 >= (int64_t{1} << 31)))
             path_ = Kernels::AttentionPath::plain;
         if (path_ == Kernels::AttentionPath::tiled) {
-            tiledName_ = std::string("flash_attention_tiled_") + tag(q.dataType) + "_" + tag(out.dataType) + "_d" +
-                         std::to_string(d.Hd);
+            // Hd 256 runs 16 query rows per wave (two waves per SIMD);
+            // POPCORN_FA_ROWS=32 selects the 32-row kernel there (a tuning
+            // override)
+            const char *e = std::getenv("POPCORN_FA_ROWS");
+            rows16_ = d.Hd == 256 && !(e && std::string(e) == "32");
+            tiledName_ = std::string(rows16_ ? "flash_attention_tiled16_" : "flash_attention_tiled_") + tag(q.dataType) +
+                         "_" + tag(out.dataType) + "_d" + std::to_string(d.Hd);
             planTileSplit();
         }
         planSplit();
@@ -219,7 +224,7 @@ public:
                 // no split tile: the partial-state arguments are never touched
                 FixedDispatch fa(tiledName_,
                                  {{q_, kRead}, {k_, kRead}, {v_, kRead}, {out_, kWrite}, {q_, kRead}, {q_, kRead}},
-                                 {bytesOf(c)}, grid1(items, kBlock));
+                                 {bytesOf(c)}, grid1(items, tiledBlock()));
                 enc.dispatch(fa);
                 return;
             }
@@ -229,7 +234,7 @@ public:
                 enc.withTemporaryTensor(ScratchSpec{{rows, 2}, DataType::f32}, [&](Tensor pML) {
                     FixedDispatch fa(tiledName_,
                                      {{q_, kRead}, {k_, kRead}, {v_, kRead}, {out_, kWrite}, {pO, kWrite}, {pML, kWrite}},
-                                     {bytesOf(c)}, grid1(items, kBlock));
+                                     {bytesOf(c)}, grid1(items, tiledBlock()));
                     enc.dispatch(fa);
                     // one block per 16 rows of a split tile
                     FixedDispatch merge(mergeName_, {{pO, kRead}, {pML, kRead}, {out_, kWrite}}, {bytesOf(c)},
@@ -372,6 +377,8 @@ private:
     std::string partialName_, reduceName_, tiledName_, mergeName_;
     int64_t nSplit_ = 0;
     bool pairTiles_ = false;
+    bool rows16_ = false;  // the 16-rows-per-wave kernel: 8 waves per 128-row tile
+    int64_t tiledBlock() const { return rows16_ ? 512 : kBlock; }
     int64_t ngroups_ = 1, P_ = 1;
 };
 

@@ -76,12 +76,12 @@ def test_prefill_attention_split_plan():
         return pa.Kernels.FlashAttention(q, q, q, out=T([1, Nq, S, 256], dtype), scale=1 / 16,
                                          mask=pa.AttentionMask(*mask), batch=1, query_heads=Nq, kv_heads=Nq,
                                          query_len=S, key_len=S, head_dim=256).function_names
-    assert fa(16, 2048) == ["flash_attention_tiled_f16_f16_d256", "flash_attention_split_merge_f16_d256"]
-    assert fa(16, 2048, dtype="bf16") == ["flash_attention_tiled_bf16_bf16_d256", "flash_attention_split_merge_bf16_d256"]
-    assert fa(16, 2048, mask=(2, -1)) == ["flash_attention_tiled_f16_f16_d256"]   # every tile sees every key
-    assert fa(16, 2048, mask=(1, 256)) == ["flash_attention_tiled_f16_f16_d256"]  # window: equal work per tile
-    assert fa(16, 384) == ["flash_attention_tiled_f16_f16_d256"]                  # 3 tiles per head
-    assert fa(64, 2048) == ["flash_attention_tiled_f16_f16_d256"]                 # 1024 tiles: 4 per CU
+    assert fa(16, 2048) == ["flash_attention_tiled16_f16_f16_d256", "flash_attention_split_merge_f16_d256"]
+    assert fa(16, 2048, dtype="bf16") == ["flash_attention_tiled16_bf16_bf16_d256", "flash_attention_split_merge_bf16_d256"]
+    assert fa(16, 2048, mask=(2, -1)) == ["flash_attention_tiled16_f16_f16_d256"]   # every tile sees every key
+    assert fa(16, 2048, mask=(1, 256)) == ["flash_attention_tiled16_f16_f16_d256"]  # window: equal work per tile
+    assert fa(16, 384) == ["flash_attention_tiled16_f16_f16_d256"]                  # 3 tiles per head
+    assert fa(64, 2048) == ["flash_attention_tiled16_f16_f16_d256"]                 # 1024 tiles: 4 per CU
 
 
 def test_prefill_gemm_tile_plan():
@@ -332,7 +332,7 @@ def test_prefill_routes_to_tiled():
     assert pa.Kernels.route(1, 256, "f16") == "decoding"
     q = T([1, 16, 2048, 256], "f16")
     k = pa.Kernels.FlashAttention(q, q, q, out=T([1, 16, 2048, 256], "f16", ptr=FAKE + 2 ** 32), scale=1 / 16)
-    assert k.function_names == ["flash_attention_tiled_f16_f16_d256", "flash_attention_split_merge_f16_d256"]
+    assert k.function_names == ["flash_attention_tiled16_f16_f16_d256", "flash_attention_split_merge_f16_d256"]
 
 
 # Reference kernels outside the decode hot path (the reference's own unfused

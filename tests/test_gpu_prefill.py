@@ -129,6 +129,22 @@ def _attend(env, q, k, v, dtype, out_dtype, scale, mask):
 MASKS = {"causal": (0, -1), "bidirectional": (2, -1), "window40": (1, 40)}
 
 
+@pytest.fixture(params=["rows16", "rows32"])
+def rows(request, monkeypatch):
+    # Hd 256 runs the 16-rows-per-wave kernel unless POPCORN_FA_ROWS=32
+    # selects the 32-row one: both are checked
+    if request.param == "rows32":
+        monkeypatch.setenv("POPCORN_FA_ROWS", "32")
+    else:
+        monkeypatch.delenv("POPCORN_FA_ROWS", raising=False)
+    return request.param
+
+
+def _tiled(dtype, ot, Hd, rows):
+    kind = "tiled16" if Hd == 256 and rows == "rows16" else "tiled"
+    return f"flash_attention_{kind}_{dtype}_{ot}_d{Hd}"
+
+
 @pytest.mark.parametrize("dtype,ot", [("f16", "f16"), ("f16", "f32"), ("bf16", "bf16"), ("bf16", "f32")])
 @pytest.mark.parametrize("B,Nq,Nkv,Sq,Sk,Hd,mask", [
     (1, 2, 1, 64, 64, 64, "causal"),
@@ -139,7 +155,7 @@ MASKS = {"causal": (0, -1), "bidirectional": (2, -1), "window40": (1, 40)}
     (2, 4, 2, 130, 200, 256, "causal"),        # GQA, Sq < Sk, ragged tiles at Hd 256
     (1, 2, 1, 128, 160, 256, "window40"),
 ])
-def test_tiled_attention_vs_oracle(env, dtype, ot, B, Nq, Nkv, Sq, Sk, Hd, mask):
+def test_tiled_attention_vs_oracle(env, rows, dtype, ot, B, Nq, Nkv, Sq, Sk, Hd, mask):
     pa = env[0]
     kind, window = MASKS[mask]
     q = rounded(O.normal(Sq + Hd, (B, Nq, Sq, Hd)), dtype)
@@ -148,7 +164,7 @@ def test_tiled_attention_vs_oracle(env, dtype, ot, B, Nq, Nkv, Sq, Sk, Hd, mask)
     pm = pa.AttentionMask(kind, window)
     scale = 1 / np.sqrt(Hd)
     got, kern = _attend(env, q, k, v, dtype, ot, scale, pm)
-    assert kern.function_names == [f"flash_attention_tiled_{dtype}_{ot}_d{Hd}"]
+    assert kern.function_names == [_tiled(dtype, ot, Hd, rows)]
     ref = O.attention_naive(q, k, v, scale, mask_kind=kind, window=window)
     assert not np.isnan(got).any()
     # softmax weights enter the P.V product in the input dtype (the matrix
@@ -163,7 +179,7 @@ def test_tiled_attention_vs_oracle(env, dtype, ot, B, Nq, Nkv, Sq, Sk, Hd, mask)
     (2, 2, 1, 520, 700, 128),   # Sq < Sk, ragged last tile: every tile split
     (1, 2, 2, 640, 640, 256),
 ])
-def test_tiled_attention_split_tiles_vs_oracle(env, dtype, ot, B, Nq, Nkv, Sq, Sk, Hd):
+def test_tiled_attention_split_tiles_vs_oracle(env, rows, dtype, ot, B, Nq, Nkv, Sq, Sk, Hd):
     # causal prefill with few tiles per CU: the heavy query tiles run as two
     # blocks over the halves of their keys and a merge kernel combines them
     pa = env[0]
@@ -172,7 +188,7 @@ def test_tiled_attention_split_tiles_vs_oracle(env, dtype, ot, B, Nq, Nkv, Sq, S
     v = rounded(O.normal(Sk + Hd + 9, (B, Nkv, Sk, Hd)), dtype)
     scale = 1 / np.sqrt(Hd)
     got, kern = _attend(env, q, k, v, dtype, ot, scale, pa.AttentionMask(0, -1))
-    assert kern.function_names == [f"flash_attention_tiled_{dtype}_{ot}_d{Hd}", f"flash_attention_split_merge_{ot}_d{Hd}"]
+    assert kern.function_names == [_tiled(dtype, ot, Hd, rows), f"flash_attention_split_merge_{ot}_d{Hd}"]
     ref = O.attention_naive(q, k, v, scale, mask_kind=0)
     assert not np.isnan(got).any()
     assert_out(got, ref, EPS[dtype], ot, f"split tiled attention {dtype}->{ot} Sq={Sq} Sk={Sk} Hd={Hd}")
@@ -180,7 +196,7 @@ def test_tiled_attention_split_tiles_vs_oracle(env, dtype, ot, B, Nq, Nkv, Sq, S
 
 @pytest.mark.parametrize("Hd", [64, 256])
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
-def test_tiled_attention_wide_score_range(env, dtype, Hd):
+def test_tiled_attention_wide_score_range(env, rows, dtype, Hd):
     # scores spread over hundreds of natural-log units (scale 1, inputs x 3):
     # the running max moves often and far, so the lazy rescale (the reference
     # max moves only when a score passes it by more than 8) is exercised on
@@ -191,30 +207,33 @@ def test_tiled_attention_wide_score_range(env, dtype, Hd):
     k = rounded(3.0 * O.normal(902, (B, Nkv, S, Hd)), dtype)
     v = rounded(O.normal(903, (B, Nkv, S, Hd)), dtype)
     got, kern = _attend(env, q, k, v, dtype, dtype, 1.0, pa.AttentionMask(0, -1))
-    assert kern.function_names[0] == f"flash_attention_tiled_{dtype}_{dtype}_d{Hd}"
+    assert kern.function_names[0] == _tiled(dtype, dtype, Hd, rows)
     ref = O.attention_naive(q, k, v, 1.0, mask_kind=0)
     assert np.isfinite(got).all()
     assert_out(got, ref, EPS[dtype], dtype, f"wide-range tiled attention {dtype}")
 
 
-def test_tiled_attention_config5_sampled(env):
-    # BASELINE config 5 attention: [1, 16, 2048, 256] f16, causal, scale 1/16.
-    # A sampled query row r is checked as a single-row query over keys 0..r
-    # (the same posQ = r), against the oracle.
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_tiled_attention_config5_sampled(env, rows, dtype):
+    # BASELINE config 5 attention: [1, 16, 2048, 256] f16 (and bf16), causal,
+    # scale 1/16. A sampled query row r is checked as a single-row query over
+    # keys 0..r (the same posQ = r), against the oracle; the output starts as
+    # NaN, so a row either kernel skips fails.
     pa, lib, stream, enc = env
     H, S, Hd = 16, 2048, 256
-    tq, tk, tv = (pa.Tensor.empty([1, H, S, Hd], "f16") for _ in range(3))
+    tq, tk, tv = (pa.Tensor.empty([1, H, S, Hd], dtype) for _ in range(3))
     for i, t in enumerate((tq, tk, tv)):
         lib.fill_normal(t, 40 + i, stream=stream)
-    to = pa.Tensor.empty([1, H, S, Hd], "f16")
+    to = upload(pa, np.full((1, H, S, Hd), np.nan, np.float32), dtype)
     kern = pa.Kernels.FlashAttention(tq, tk, tv, out=to, scale=1 / 16, batch=1, query_heads=H, kv_heads=H,
                                      query_len=S, key_len=S, head_dim=Hd)
-    # 16 tiles per head on 256 CUs: the 8 heaviest run split in two halves of their keys
-    assert kern.function_names == ["flash_attention_tiled_f16_f16_d256", "flash_attention_split_merge_f16_d256"]
+    # 16 tiles per head on 256 CUs: light and heavy tiles paired, the heavy ones split
+    assert kern.function_names == [_tiled(dtype, dtype, Hd, rows), f"flash_attention_split_merge_{dtype}_d256"]
     enc.encode(kern)
     stream.synchronize()
     q, k, v = (download(t, stream).reshape(1, H, S, Hd) for t in (tq, tk, tv))
     got = download(to, stream).reshape(1, H, S, Hd)
-    for r in (0, 1, 127, 128, 1000, 2047):
+    assert not np.isnan(got).any()
+    for r in (0, 1, 127, 128, 1000, 1151, 1152, 2047):
         ref = O.attention_naive(q[:, :, r:r + 1], k[:, :, :r + 1].copy(), v[:, :, :r + 1].copy(), 1 / 16)
-        assert_out(got[:, :, r:r + 1], ref, EPS["f16"], "f16", f"config5 row {r}")
+        assert_out(got[:, :, r:r + 1], ref, EPS[dtype], dtype, f"config5 {dtype} row {r}")
