@@ -611,16 +611,28 @@ __device__ void fa_tiled16(const uint16_t *__restrict__ Q, const uint16_t *__res
         }
         const bool full = (int)k0 + BKV <= (int)p.Sk && (p.maskKind == 2u || (int)k0 + BKV - 1 <= posQ0) &&
                           (p.maskKind != 1u || posQ0 + 15 - (int)k0 < (int)p.slidingWindow);
+        // one uniform branch per step: a step every row of the wave sees
+        // takes the scores as they are, the others mask each key
         float sv[8];
         float mx = -INFINITY;
+        if (full) {
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
+            for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int key = (int)k0 + mt * 16 + (int)g * 4 + i;
-                sv[mt * 4 + i] = (full || fa_allowed(p, posQ, key)) ? st[mt][i] : -INFINITY;
-                mx = fmaxf(mx, sv[mt * 4 + i]);
-            }
+                for (int i = 0; i < 4; ++i) {
+                    sv[mt * 4 + i] = st[mt][i];
+                    mx = fmaxf(mx, sv[mt * 4 + i]);
+                }
+        } else {
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int key = (int)k0 + mt * 16 + (int)g * 4 + i;
+                    sv[mt * 4 + i] = fa_allowed(p, posQ, key) ? st[mt][i] : -INFINITY;
+                    mx = fmaxf(mx, sv[mt * 4 + i]);
+                }
+        }
         mx = quad16_max(mx) * c2;
         const bool move = mx > m + kRescaleGap * kLog2e;
         float alpha = 1.0f, ps = 0.0f;
