@@ -800,7 +800,9 @@ __device__ void fa_split_merge(const float *__restrict__ pO, const float *__rest
              float *pML, TiledFlashAttentionConstants p) {                                               \
         fa_tiled16<T, O, HD>(q, k, v, out, pO, pML, p);                                                \
     }
-#define FA_TILED16_D(t, T, o, O) FA_TILED16(flash_attention_tiled16_##t##_##o##_d256, T, O, 256)
+#define FA_TILED16_D(t, T, o, O)                                      \
+    FA_TILED16(flash_attention_tiled16_##t##_##o##_d128, T, O, 128)   \
+    FA_TILED16(flash_attention_tiled16_##t##_##o##_d256, T, O, 256)
 #define FA_MERGE(name, O, HD)                                                                          \
     POPCORN_KERNEL void __launch_bounds__(256)                                                         \
         name(const float *pO, const float *pML, O::storage *out, TiledFlashAttentionConstants p) {       \

@@ -175,11 +175,11 @@ public:
              d.Sk * d.Hd * 2 >= (int64_t{1} << 31)))
             path_ = Kernels::AttentionPath::plain;
         if (path_ == Kernels::AttentionPath::tiled) {
-            // Hd 256 runs 16 query rows per wave (two waves per SIMD);
+            // Hd 128 and 256 run 16 query rows per wave (two waves per SIMD);
             // POPCORN_FA_ROWS=32 selects the 32-row kernel there (a tuning
             // override)
             const char *e = std::getenv("POPCORN_FA_ROWS");
-            rows16_ = d.Hd == 256 && !(e && std::string(e) == "32");
+            rows16_ = (d.Hd == 128 || d.Hd == 256) && !(e && std::string(e) == "32");
             tiledName_ = std::string(rows16_ ? "flash_attention_tiled16_" : "flash_attention_tiled_") + tag(q.dataType) +
                          "_" + tag(out.dataType) + "_d" + std::to_string(d.Hd);
             planTileSplit();

@@ -131,8 +131,8 @@ MASKS = {"causal": (0, -1), "bidirectional": (2, -1), "window40": (1, 40)}
 
 @pytest.fixture(params=["rows16", "rows32"])
 def rows(request, monkeypatch):
-    # Hd 256 runs the 16-rows-per-wave kernel unless POPCORN_FA_ROWS=32
-    # selects the 32-row one: both are checked
+    # Hd 128 and 256 run the 16-rows-per-wave kernel unless
+    # POPCORN_FA_ROWS=32 selects the 32-row one: both are checked
     if request.param == "rows32":
         monkeypatch.setenv("POPCORN_FA_ROWS", "32")
     else:
@@ -141,7 +141,7 @@ def rows(request, monkeypatch):
 
 
 def _tiled(dtype, ot, Hd, rows):
-    kind = "tiled16" if Hd == 256 and rows == "rows16" else "tiled"
+    kind = "tiled16" if Hd in (128, 256) and rows == "rows16" else "tiled"
     return f"flash_attention_{kind}_{dtype}_{ot}_d{Hd}"
 
 
