@@ -120,7 +120,16 @@ typedef struct {
  *              tile i is paired with tile qTilesPerHead - 1 - i and each
  *              pair runs as two blocks of equal work, tile i and the first
  *              steps of its partner, then the partner's remaining steps
- *              (qTilesPerHead blocks per head). */
+ *              (qTilesPerHead blocks per head);
+ *              2 (the 16-row kernels only): pairs as for 1, but the first
+ *              block of a pair runs its steps of the partner first and
+ *              publishes them (partial O for part 0 only, (m, l), then a
+ *              64-bit ready flag per split tile after the (m, l) rows), and
+ *              the second block merges them into the output itself: no
+ *              split-merge kernel;
+ *   ticketLo, ticketHi  pairTiles 2: the 64-bit value (never 0) the ready
+ *              flags are set to, distinct per launch; the merging block
+ *              resets its flag to 0. */
 typedef struct {
     uint32_t B;
     uint32_t Nq;
@@ -135,6 +144,8 @@ typedef struct {
     uint32_t kvStride;
     uint32_t splitFrom;
     uint32_t pairTiles;
+    uint32_t ticketLo;
+    uint32_t ticketHi;
 } TiledFlashAttentionConstants;
 
 /* PopcornKernelTypes.h:146-156 */

@@ -40,6 +40,24 @@ constexpr int BKV = 32;          // keys per step
 // reference moves: softmax weights stay below e^8 ~ 2981 (f16 holds 65504).
 constexpr float kRescaleGap = 8.0f;
 constexpr float kLog2e = 1.4426950408889634f;
+
+// Partial state handed between the two blocks of a merged pair (pairTiles
+// 2) goes through agent-coherent accesses: 16-byte buffer stores and loads
+// with cache policy sc1, which write through and read past the XCD's L2
+// (the two blocks may run on different XCDs, whose L2s are not coherent),
+// and single-copy atomic 64-bit words for (m, l) and the ready flag.
+constexpr int kSc1 = 16;
+// polls of the ready flag before the merging block gives up (about 0.3 s;
+// the publishing block has the lower index, so it was dispatched first and
+// waits for nothing)
+constexpr uint32_t kFlagPolls = 1u << 22;
+__device__ inline uint64_t ld64c(const void *p) {
+    return __hip_atomic_load(reinterpret_cast<uint64_t *>(const_cast<void *>(p)), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline void st64c(void *p, uint64_t v) {
+    __hip_atomic_store(reinterpret_cast<uint64_t *>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 // Vt rows hold a step's keys in the order of P^T's key slots (key index
 // with bits 2 and 3 swapped): slots 8 h .. 8 h + 7 of k-step ks, which lane
 // half h feeds to the product, are keys 16 ks + 4 h + 0..3 and
@@ -82,6 +100,8 @@ __device__ inline uint32_t fa_steps(const TiledFlashAttentionConstants &p, uint3
 // b = qTilesPerHead - 1 - i, and each pair runs as two blocks of equal work:
 // the first takes tile a and the first x steps of tile b, the second the
 // rest of tile b, where x makes the two halves of the pair's steps equal
+// (pairTiles 2: the first block runs its steps of tile b first and
+// publishes their partial state, which the second block merges itself)
 // (the host uses this only where x >= 1 for every pair, so the b tiles,
 // qt >= splitFrom, are exactly the split ones); an odd tile count leaves the
 // middle tile whole, one block. Every block then holds about the mean work,
@@ -142,7 +162,17 @@ __device__ inline FaWork fa_work(const TiledFlashAttentionConstants &p) {
     const uint32_t i = rank >> 1, a = i, bt = nQT - 1 - i;
     const uint32_t sa = fa_steps(p, a), sb = fa_steps(p, bt);
     const uint32_t x = (sa + sb + 1) / 2 - sa;
-    if ((rank & 1u) == 0u) {
+    if ((rank & 1u) == 0u && p.pairTiles == 2u) {
+        // merged in the kernel: the partner's first steps come first, so
+        // their partial state is published long before the second block
+        // of the pair needs it
+        w.n = 2;
+        w.qt[0] = bt;
+        w.hi[0] = x;
+        w.split[0] = true;
+        w.qt[1] = a;
+        w.hi[1] = sa;
+    } else if ((rank & 1u) == 0u) {
         w.n = 2;
         w.qt[0] = a;
         w.hi[0] = sa;
@@ -420,17 +450,24 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
             gload(krB, vrB, kstep(itLo + 1));
             lstore(krA, vrA, 0);
             gload(krA, vrA, kstep(itLo + 2));
-            for (uint32_t it = itLo; it < itHi; it += 2) {
+            // two steps per pass and the odd last step outside the loop, so
+            // the loop's back edge always follows the second register set's
+            // loads and the wait before each LDS copy leaves the other set's
+            // loads in flight
+            uint32_t it = itLo;
+            for (; it + 1 < itHi; it += 2) {
                 __syncthreads();
                 lstore(krB, vrB, 1);
                 gload(krB, vrB, kstep(it + 3));
                 compute(kstep(it), 0);
-                if (it + 1 < itHi) {
-                    __syncthreads();
-                    lstore(krA, vrA, 0);
-                    gload(krA, vrA, kstep(it + 4));
-                    compute(kstep(it + 1), 1);
-                }
+                __syncthreads();
+                lstore(krA, vrA, 0);
+                gload(krA, vrA, kstep(it + 4));
+                compute(kstep(it + 1), 1);
+            }
+            if (it < itHi) {
+                __syncthreads();
+                compute(kstep(it), 0);
             }
         }
 
@@ -514,6 +551,7 @@ __device__ void fa_tiled16(const uint16_t *__restrict__ Q, const uint16_t *__res
     static_assert(CH >= 16, "the K swizzle needs 16 chunks per row");
     __shared__ __attribute__((aligned(16))) uint16_t sK[2][BKV * HD];
     __shared__ __attribute__((aligned(16))) uint16_t sV[2][HD * LDV];
+    __shared__ uint32_t sReady;  // a merged pair's partner state was seen
 
     const uint32_t lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -701,21 +739,102 @@ __device__ void fa_tiled16(const uint16_t *__restrict__ Q, const uint16_t *__res
             gload(krB, vrB, kstep(itLo + 1));
             lstore(krA, vrA, 0);
             gload(krA, vrA, kstep(itLo + 2));
-            for (uint32_t it = itLo; it < itHi; it += 2) {
+            // two steps per pass and the odd last step outside the loop, so
+            // the loop's back edge always follows the second register set's
+            // loads and the wait before each LDS copy leaves the other set's
+            // loads in flight
+            uint32_t it = itLo;
+            for (; it + 1 < itHi; it += 2) {
                 __syncthreads();
                 lstore(krB, vrB, 1);
                 gload(krB, vrB, kstep(it + 3));
                 compute(kstep(it), 0);
-                if (it + 1 < itHi) {
-                    __syncthreads();
-                    lstore(krA, vrA, 0);
-                    gload(krA, vrA, kstep(it + 4));
-                    compute(kstep(it + 1), 1);
-                }
+                __syncthreads();
+                lstore(krA, vrA, 0);
+                gload(krA, vrA, kstep(it + 4));
+                compute(kstep(it + 1), 1);
+            }
+            if (it < itHi) {
+                __syncthreads();
+                compute(kstep(it), 0);
             }
         }
 
-        if (myq >= p.Sq) {
+        // this lane's 4 consecutive dims of each 16-dim slice of its row,
+        // value(dt, i) for dim dt * 16 + 4 g + i
+        auto store_out = [&](auto &&value) {
+            typename O::storage *orow = out + ((uint64_t)bh * p.Sq + myq) * HD;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                const uint32_t d = dt * 16 + g * 4;
+                const float v0 = value(dt, 0), v1 = value(dt, 1), v2 = value(dt, 2), v3 = value(dt, 3);
+                if constexpr (std::is_same<O, pk::F32>::value) {
+                    *reinterpret_cast<float4 *>(orow + d) = float4{v0, v1, v2, v3};
+                } else {
+                    auto b16 = [](float x) { return (uint32_t)__builtin_bit_cast(uint16_t, O::store(x)); };
+                    *reinterpret_cast<uint2 *>(orow + d) = uint2{b16(v0) | (b16(v1) << 16), b16(v2) | (b16(v3) << 16)};
+                }
+            }
+        };
+        if (work.split[w] && p.pairTiles == 2u) {
+            // A merged pair: the first block publishes its part of the split
+            // tile (unnormalised O, then (m, l) per row, then the tile's
+            // ready flag, set to this launch's ticket once every wave's
+            // stores have completed); the second waits for the flag, resets
+            // it for the next launch and combines the published part with
+            // its own, as fa_split_merge does.
+            const uint32_t nSplit = p.qTilesPerHead - p.splitFrom;
+            const uint32_t tile = bh * nSplit + (qt - p.splitFrom);
+            const uint32_t rowsTotal = p.B * p.Nq * nSplit * BQ;
+            const uint64_t row = (uint64_t)tile * BQ + wave * 16 + c16;
+            void *flag = pML + 2 * (uint64_t)rowsTotal + 2 * (uint64_t)tile;
+            const uint64_t ticket = ((uint64_t)p.ticketHi << 32) | p.ticketLo;
+            const __amdgpu_buffer_rsrc_t rsO =
+                __builtin_amdgcn_make_buffer_rsrc(pO, 0, (int)(rowsTotal * HD * 4u), 0x00020000);
+            const int obase = (int)((row * HD + g * 4) * 4);
+            if (work.part[w] == 0u) {
+                if (myq < p.Sq) {
+#pragma unroll
+                    for (int dt = 0; dt < DT; ++dt)
+                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[dt]), rsO, obase + dt * 64, 0, kSc1);
+                    if (g == 0) st64c(pML + 2 * row, (uint64_t)__float_as_uint(m) | ((uint64_t)__float_as_uint(l) << 32));
+                }
+                __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's stores have completed
+                __syncthreads();
+                if (threadIdx.x == 0) st64c(flag, ticket);
+            } else {
+                if (threadIdx.x == 0) {
+                    uint32_t ok = 0u;
+                    for (uint32_t i = 0; i < kFlagPolls; ++i) {
+                        if (ld64c(flag) == ticket) {
+                            ok = 1u;
+                            break;
+                        }
+                        __builtin_amdgcn_s_sleep(2);
+                    }
+                    sReady = ok;
+                }
+                __syncthreads();
+                asm volatile("" ::: "memory");  // the partner's state is read after the flag
+                const bool ok = sReady != 0u;
+                if (threadIdx.x == 0) st64c(flag, 0u);
+                if (myq < p.Sq) {
+                    u32x4 oa[DT];
+#pragma unroll
+                    for (int dt = 0; dt < DT; ++dt)
+                        oa[dt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsO, obase + dt * 64, 0, kSc1));
+                    const uint64_t ml = ld64c(pML + 2 * row);
+                    const float m0 = __uint_as_float((uint32_t)ml), l0 = __uint_as_float((uint32_t)(ml >> 32));
+                    const float M = fmaxf(m0, m);
+                    const float w0 = m0 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m0 - M);
+                    const float w1 = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M);
+                    const float L = w0 * l0 + w1 * l;
+                    // a flag never seen (the partner never ran) gives NaN rows, not stale data
+                    const float inv = !ok ? __builtin_nanf("") : (L > 0.0f ? 1.0f / L : 0.0f);
+                    store_out([&](int dt, int i) { return (w0 * __uint_as_float(oa[dt][i]) + w1 * acc[dt][i]) * inv; });
+                }
+            }
+        } else if (myq >= p.Sq) {
             // a row past Sq (ragged last tile) writes nothing
         } else if (work.split[w]) {
             const uint32_t tile = (bh * (p.qTilesPerHead - p.splitFrom) + (qt - p.splitFrom)) * 2u + work.part[w];
@@ -727,18 +846,7 @@ __device__ void fa_tiled16(const uint16_t *__restrict__ Q, const uint16_t *__res
             if (g == 0) *reinterpret_cast<float2 *>(pML + 2 * row) = float2{m, l};
         } else {
             const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-            typename O::storage *orow = out + ((uint64_t)bh * p.Sq + myq) * HD;
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-                const uint32_t d = dt * 16 + g * 4;
-                const float v0 = acc[dt][0] * inv, v1 = acc[dt][1] * inv, v2 = acc[dt][2] * inv, v3 = acc[dt][3] * inv;
-                if constexpr (std::is_same<O, pk::F32>::value) {
-                    *reinterpret_cast<float4 *>(orow + d) = float4{v0, v1, v2, v3};
-                } else {
-                    auto b16 = [](float x) { return (uint32_t)__builtin_bit_cast(uint16_t, O::store(x)); };
-                    *reinterpret_cast<uint2 *>(orow + d) = uint2{b16(v0) | (b16(v1) << 16), b16(v2) | (b16(v3) << 16)};
-                }
-            }
+            store_out([&](int dt, int i) { return acc[dt][i] * inv; });
         }
     };
     item(0);

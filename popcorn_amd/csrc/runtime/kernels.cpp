@@ -2,6 +2,8 @@
 // Swift descriptors (Sources/Popcorn/Kernels/*.swift, cited per descriptor),
 // with dispatch geometry chosen for wave64 and the device's CU count.
 #include <algorithm>
+#include <atomic>
+#include <chrono>
 #include <cstdlib>
 #include <cstring>
 
@@ -180,6 +182,10 @@ public:
             // override)
             const char *e = std::getenv("POPCORN_FA_ROWS");
             rows16_ = (d.Hd == 128 || d.Hd == 256) && !(e && std::string(e) == "32");
+            // POPCORN_FA_PAIR_MERGE=0: paired tiles merged by the merge
+            // kernel in the 16-row kernels too (a tuning override)
+            const char *pm = std::getenv("POPCORN_FA_PAIR_MERGE");
+            pairMergeInKernel_ = !(pm && std::string(pm) == "0");
             tiledName_ = std::string(rows16_ ? "flash_attention_tiled16_" : "flash_attention_tiled_") + tag(q.dataType) +
                          "_" + tag(out.dataType) + "_d" + std::to_string(d.Hd);
             planTileSplit();
@@ -194,7 +200,7 @@ public:
     }
 
     std::string describe() const override {
-        if (path_ == Kernels::AttentionPath::tiled) return nSplit_ ? tiledName_ + "," + mergeName_ : tiledName_;
+        if (path_ == Kernels::AttentionPath::tiled) return nSplit_ && !mergedPairs() ? tiledName_ + "," + mergeName_ : tiledName_;
         return partialName_ + "," + reduceName_;
     }
 
@@ -216,7 +222,7 @@ public:
             c.scale = scale_;
             c.kvStride = (uint32_t)d_.cap;
             c.splitFrom = (uint32_t)(c.qTilesPerHead - nSplit_);
-            c.pairTiles = pairTiles_ ? 1u : 0u;
+            c.pairTiles = pairTiles_ ? (mergedPairs() ? 2u : 1u) : 0u;
             // one block per tile; a split tile's two halves take two, a pair
             // of tiles two in all
             const int64_t items = d_.B * d_.Nq * ((int64_t)c.qTilesPerHead + (pairTiles_ ? 0 : nSplit_));
@@ -226,6 +232,25 @@ public:
                                  {{q_, kRead}, {k_, kRead}, {v_, kRead}, {out_, kWrite}, {q_, kRead}, {q_, kRead}},
                                  {bytesOf(c)}, grid1(items, tiledBlock()));
                 enc.dispatch(fa);
+                return;
+            }
+            if (mergedPairs()) {
+                // the published part of each split tile: unnormalised O, then
+                // (m, l) per row and a 64-bit ready flag per tile; the second
+                // block of each pair merges, so no merge kernel
+                const int64_t tiles = d_.B * d_.Nq * nSplit_;
+                const uint64_t ticket = nextTicket();
+                c.ticketLo = (uint32_t)ticket;
+                c.ticketHi = (uint32_t)(ticket >> 32);
+                enc.withTemporaryTensor(ScratchSpec{{tiles * 128, d_.Hd}, DataType::f32}, [&](Tensor pO) {
+                    enc.withTemporaryTensor(ScratchSpec{{tiles * 128 * 2 + tiles * 2}, DataType::f32}, [&](Tensor pML) {
+                        FixedDispatch fa(tiledName_,
+                                         {{q_, kRead}, {k_, kRead}, {v_, kRead}, {out_, kWrite}, {pO, kReadWrite},
+                                          {pML, kReadWrite}},
+                                         {bytesOf(c)}, grid1(items, tiledBlock()));
+                        enc.dispatch(fa);
+                    });
+                });
                 return;
             }
             // the two parts of each split tile: unnormalised O, then (m, l) per row
@@ -379,6 +404,22 @@ private:
     bool pairTiles_ = false;
     bool rows16_ = false;  // the 16-rows-per-wave kernel: 8 waves per 128-row tile
     int64_t tiledBlock() const { return rows16_ ? 512 : kBlock; }
+    // Paired tiles are merged inside the 16-row kernels (pairTiles 2).
+    bool pairMergeInKernel_ = true;
+    bool mergedPairs() const { return pairTiles_ && rows16_ && pairMergeInKernel_; }
+    // A 64-bit value, never 0 and distinct per launch, for the ready flags
+    // of merged pairs: a counter, started from the clock so that processes
+    // differ, through the splitmix64 finaliser.
+    static uint64_t nextTicket() {
+        static std::atomic<uint64_t> counter{(uint64_t)std::chrono::steady_clock::now().time_since_epoch().count()};
+        for (;;) {
+            uint64_t z = (counter.fetch_add(1, std::memory_order_relaxed) + 1) * 0x9E3779B97F4A7C15ull;
+            z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+            z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+            z ^= z >> 31;
+            if (z != 0) return z;
+        }
+    }
     int64_t ngroups_ = 1, P_ = 1;
 };
 

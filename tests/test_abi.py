@@ -69,15 +69,19 @@ def test_route():
 
 def test_prefill_attention_split_plan():
     # causal prefill with at most two 128-row tiles per CU (256 CUs when no
-    # GPU answers): tiles with more than half the last tile's key steps run
-    # as two blocks, merged by a second kernel
+    # GPU answers). At most one tile per CU: light and heavy tiles paired,
+    # the second block of a pair merging the split tile itself in the
+    # 16-row kernel (the 32-row kernel leaves it to a merge kernel). Up to
+    # two per CU: tiles with more than half the last tile's key steps run as
+    # two blocks, merged by a second kernel.
     def fa(Nq, S, mask=(0, -1), dtype="f16"):
         q = T([1, Nq, S, 256], dtype)
         return pa.Kernels.FlashAttention(q, q, q, out=T([1, Nq, S, 256], dtype), scale=1 / 16,
                                          mask=pa.AttentionMask(*mask), batch=1, query_heads=Nq, kv_heads=Nq,
                                          query_len=S, key_len=S, head_dim=256).function_names
-    assert fa(16, 2048) == ["flash_attention_tiled16_f16_f16_d256", "flash_attention_split_merge_f16_d256"]
-    assert fa(16, 2048, dtype="bf16") == ["flash_attention_tiled16_bf16_bf16_d256", "flash_attention_split_merge_bf16_d256"]
+    assert fa(16, 2048) == ["flash_attention_tiled16_f16_f16_d256"]
+    assert fa(16, 2048, dtype="bf16") == ["flash_attention_tiled16_bf16_bf16_d256"]
+    assert fa(24, 2048) == ["flash_attention_tiled16_f16_f16_d256", "flash_attention_split_merge_f16_d256"]
     assert fa(16, 2048, mask=(2, -1)) == ["flash_attention_tiled16_f16_f16_d256"]   # every tile sees every key
     assert fa(16, 2048, mask=(1, 256)) == ["flash_attention_tiled16_f16_f16_d256"]  # window: equal work per tile
     assert fa(16, 384) == ["flash_attention_tiled16_f16_f16_d256"]                  # 3 tiles per head
@@ -332,7 +336,7 @@ def test_prefill_routes_to_tiled():
     assert pa.Kernels.route(1, 256, "f16") == "decoding"
     q = T([1, 16, 2048, 256], "f16")
     k = pa.Kernels.FlashAttention(q, q, q, out=T([1, 16, 2048, 256], "f16", ptr=FAKE + 2 ** 32), scale=1 / 16)
-    assert k.function_names == ["flash_attention_tiled16_f16_f16_d256", "flash_attention_split_merge_f16_d256"]
+    assert k.function_names == ["flash_attention_tiled16_f16_f16_d256"]
 
 
 # Reference kernels outside the decode hot path (the reference's own unfused

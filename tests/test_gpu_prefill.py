@@ -6,7 +6,7 @@ import pytest
 
 import oracle as O
 from conftest import assert_out
-from gpu_util import EPS, download, gpu_env, rounded, upload
+from gpu_util import EPS, TAG, download, gpu_env, rounded, upload
 
 pytestmark = pytest.mark.gpu
 
@@ -145,6 +145,15 @@ def _tiled(dtype, ot, Hd, rows):
     return f"flash_attention_{kind}_{dtype}_{ot}_d{Hd}"
 
 
+def _paired(dtype, ot, Hd, rows):
+    # paired causal tiles (at most one tile per CU): the 16-row kernel
+    # merges the split tiles itself, the 32-row kernel through a merge kernel
+    names = [_tiled(dtype, ot, Hd, rows)]
+    if not names[0].startswith("flash_attention_tiled16_"):
+        names.append(f"flash_attention_split_merge_{ot}_d{Hd}")
+    return names
+
+
 @pytest.mark.parametrize("dtype,ot", [("f16", "f16"), ("f16", "f32"), ("bf16", "bf16"), ("bf16", "f32")])
 @pytest.mark.parametrize("B,Nq,Nkv,Sq,Sk,Hd,mask", [
     (1, 2, 1, 64, 64, 64, "causal"),
@@ -180,15 +189,17 @@ def test_tiled_attention_vs_oracle(env, rows, dtype, ot, B, Nq, Nkv, Sq, Sk, Hd,
     (1, 2, 2, 640, 640, 256),
 ])
 def test_tiled_attention_split_tiles_vs_oracle(env, rows, dtype, ot, B, Nq, Nkv, Sq, Sk, Hd):
-    # causal prefill with few tiles per CU: the heavy query tiles run as two
-    # blocks over the halves of their keys and a merge kernel combines them
+    # causal prefill with few tiles per CU: light and heavy query tiles
+    # paired into blocks of equal work, the heavy tile of a pair split over
+    # the two blocks and its parts merged (in the 16-row kernel by the
+    # second block of the pair, else by a merge kernel)
     pa = env[0]
     q = rounded(O.normal(Sq + Hd + 7, (B, Nq, Sq, Hd)), dtype)
     k = rounded(O.normal(Sk + Hd + 8, (B, Nkv, Sk, Hd)), dtype)
     v = rounded(O.normal(Sk + Hd + 9, (B, Nkv, Sk, Hd)), dtype)
     scale = 1 / np.sqrt(Hd)
     got, kern = _attend(env, q, k, v, dtype, ot, scale, pa.AttentionMask(0, -1))
-    assert kern.function_names == [_tiled(dtype, ot, Hd, rows), f"flash_attention_split_merge_{ot}_d{Hd}"]
+    assert kern.function_names == _paired(dtype, ot, Hd, rows)
     ref = O.attention_naive(q, k, v, scale, mask_kind=0)
     assert not np.isnan(got).any()
     assert_out(got, ref, EPS[dtype], ot, f"split tiled attention {dtype}->{ot} Sq={Sq} Sk={Sk} Hd={Hd}")
@@ -228,12 +239,41 @@ def test_tiled_attention_config5_sampled(env, rows, dtype):
     kern = pa.Kernels.FlashAttention(tq, tk, tv, out=to, scale=1 / 16, batch=1, query_heads=H, kv_heads=H,
                                      query_len=S, key_len=S, head_dim=Hd)
     # 16 tiles per head on 256 CUs: light and heavy tiles paired, the heavy ones split
-    assert kern.function_names == [_tiled(dtype, dtype, Hd, rows), f"flash_attention_split_merge_{dtype}_d256"]
+    assert kern.function_names == _paired(dtype, dtype, Hd, rows)
+    # twice: the second launch finds the ready flags the first one reset
+    for rep in range(2):
+        if rep:
+            lib.fill_normal(tq, 60, stream=stream)
+            to.copy_from(O.to_bits(np.full((1, H, S, Hd), np.nan, np.float32), TAG[dtype]), stream)
+        enc.encode(kern)
+        stream.synchronize()
+        q, k, v = (download(t, stream).reshape(1, H, S, Hd) for t in (tq, tk, tv))
+        got = download(to, stream).reshape(1, H, S, Hd)
+        assert not np.isnan(got).any()
+        for r in (0, 1, 127, 128, 1000, 1151, 1152, 2047):
+            ref = O.attention_naive(q[:, :, r:r + 1], k[:, :, :r + 1].copy(), v[:, :, :r + 1].copy(), 1 / 16)
+            assert_out(got[:, :, r:r + 1], ref, EPS[dtype], dtype, f"config5 {dtype} launch {rep} row {r}")
+
+
+def test_tiled_attention_two_tiles_per_cu_sampled(env, rows):
+    # 24 heads x 16 tiles on 256 CUs (up to two tiles per CU): the tiles
+    # with more than half the last tile's key steps run as two blocks over
+    # the halves of their keys, merged by the merge kernel (f16, Hd 256,
+    # causal). Sampled rows as in the config-5 test, from a NaN-filled output.
+    pa, lib, stream, enc = env
+    H, S, Hd = 24, 2048, 256
+    tq, tk, tv = (pa.Tensor.empty([1, H, S, Hd], "f16") for _ in range(3))
+    for i, t in enumerate((tq, tk, tv)):
+        lib.fill_normal(t, 70 + i, stream=stream)
+    to = upload(pa, np.full((1, H, S, Hd), np.nan, np.float32), "f16")
+    kern = pa.Kernels.FlashAttention(tq, tk, tv, out=to, scale=1 / 16, batch=1, query_heads=H, kv_heads=H,
+                                     query_len=S, key_len=S, head_dim=Hd)
+    assert kern.function_names == [_tiled("f16", "f16", Hd, rows), "flash_attention_split_merge_f16_d256"]
     enc.encode(kern)
     stream.synchronize()
     q, k, v = (download(t, stream).reshape(1, H, S, Hd) for t in (tq, tk, tv))
     got = download(to, stream).reshape(1, H, S, Hd)
     assert not np.isnan(got).any()
-    for r in (0, 1, 127, 128, 1000, 1151, 1152, 2047):
+    for r in (0, 127, 1023, 1024, 1100, 1535, 2047):
         ref = O.attention_naive(q[:, :, r:r + 1], k[:, :, :r + 1].copy(), v[:, :, :r + 1].copy(), 1 / 16)
-        assert_out(got[:, :, r:r + 1], ref, EPS[dtype], dtype, f"config5 {dtype} row {r}")
+        assert_out(got[:, :, r:r + 1], ref, EPS["f16"], "f16", f"two tiles per CU row {r}")
