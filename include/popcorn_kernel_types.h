@@ -121,7 +121,7 @@ typedef struct {
  *              pair runs as two blocks of equal work, tile i and the first
  *              steps of its partner, then the partner's remaining steps
  *              (qTilesPerHead blocks per head);
- *              2 (the 16-row kernels only): pairs as for 1, but the first
+ *              2: pairs as for 1, but the first
  *              block of a pair runs its steps of the partner first and
  *              publishes them (partial O for part 0 only, (m, l), then a
  *              64-bit ready flag per split tile after the (m, l) rows), and

@@ -204,6 +204,7 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
     // step is written into the other
     __shared__ __attribute__((aligned(16))) uint16_t sK[2][BKV * LDK];
     __shared__ __attribute__((aligned(16))) uint16_t sV[2][HD * LDV];
+    __shared__ uint32_t sReady;  // a merged pair's partner state was seen
 
     const uint32_t lane = threadIdx.x & 63, h = lane >> 5, c32 = lane & 31;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -471,7 +472,92 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
             }
         }
 
-        if (myq >= p.Sq) {
+        // the lane's 4 consecutive dims d .. d + 3 of each (dt, i4) go out
+        // as one store (16 bytes in f32, 8 in 16-bit types): a lane's row is
+        // 64 lanes away from its neighbour's, so every element store would
+        // be a separate memory transaction; value(dt, e) for accumulator
+        // element e of acc[dt]
+        auto store_dt = [&](int dt, auto &&value) {
+            typename O::storage *orow = out + ((uint64_t)bh * p.Sq + myq) * HD;
+#pragma unroll
+            for (int i4 = 0; i4 < 4; ++i4) {
+                const uint32_t d = dt * 32 + i4 * 8 + h * 4;
+                const float v0 = value(dt, 4 * i4), v1 = value(dt, 4 * i4 + 1);
+                const float v2 = value(dt, 4 * i4 + 2), v3 = value(dt, 4 * i4 + 3);
+                if constexpr (std::is_same<O, pk::F32>::value) {
+                    *reinterpret_cast<float4 *>(orow + d) = float4{v0, v1, v2, v3};
+                } else {
+                    auto b16 = [](float x) { return (uint32_t)__builtin_bit_cast(uint16_t, O::store(x)); };
+                    *reinterpret_cast<uint2 *>(orow + d) = uint2{b16(v0) | (b16(v1) << 16), b16(v2) | (b16(v3) << 16)};
+                }
+            }
+        };
+        if (work.split[w] && p.pairTiles == 2u) {
+            // a merged pair, as in fa_tiled16: the first block publishes its
+            // part of the split tile and a ready flag, the second merges
+            const uint32_t nSplit = p.qTilesPerHead - p.splitFrom;
+            const uint32_t tile = bh * nSplit + (qt - p.splitFrom);
+            const uint32_t rowsTotal = p.B * p.Nq * nSplit * BQ;
+            const uint64_t row = (uint64_t)tile * BQ + wave * 32 + c32;
+            void *flag = pML + 2 * (uint64_t)rowsTotal + 2 * (uint64_t)tile;
+            const uint64_t ticket = ((uint64_t)p.ticketHi << 32) | p.ticketLo;
+            const __amdgpu_buffer_rsrc_t rsO =
+                __builtin_amdgcn_make_buffer_rsrc(pO, 0, (int)(rowsTotal * HD * 4u), 0x00020000);
+            const int obase = (int)((row * HD + h * 4) * 4);
+            if (work.part[w] == 0u) {
+                if (myq < p.Sq) {
+#pragma unroll
+                    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                        for (int i4 = 0; i4 < 4; ++i4) {
+                            const pk::f32x4 v = {acc[dt][4 * i4], acc[dt][4 * i4 + 1], acc[dt][4 * i4 + 2], acc[dt][4 * i4 + 3]};
+                            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rsO,
+                                                                   obase + (dt * 32 + i4 * 8) * 4, 0, kSc1);
+                        }
+                    if (h == 0) st64c(pML + 2 * row, (uint64_t)__float_as_uint(m) | ((uint64_t)__float_as_uint(l) << 32));
+                }
+                __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's stores have completed
+                __syncthreads();
+                if (threadIdx.x == 0) st64c(flag, ticket);
+            } else {
+                if (threadIdx.x == 0) {
+                    uint32_t ok = 0u;
+                    for (uint32_t i = 0; i < kFlagPolls; ++i) {
+                        if (ld64c(flag) == ticket) {
+                            ok = 1u;
+                            break;
+                        }
+                        __builtin_amdgcn_s_sleep(2);
+                    }
+                    sReady = ok;
+                }
+                __syncthreads();
+                asm volatile("" ::: "memory");  // the partner's state is read after the flag
+                const bool ok = sReady != 0u;
+                if (threadIdx.x == 0) st64c(flag, 0u);
+                if (myq < p.Sq) {
+                    const uint64_t ml = ld64c(pML + 2 * row);
+                    const float m0 = __uint_as_float((uint32_t)ml), l0 = __uint_as_float((uint32_t)(ml >> 32));
+                    const float M = fmaxf(m0, m);
+                    const float w0 = m0 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m0 - M);
+                    const float w1 = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M);
+                    const float L = w0 * l0 + w1 * l;
+                    // a flag never seen (the partner never ran) gives NaN rows, not stale data
+                    const float inv = !ok ? __builtin_nanf("") : (L > 0.0f ? 1.0f / L : 0.0f);
+                    // one 32-dim slice at a time (registers: the wave's
+                    // accumulators already fill its AGPRs)
+#pragma unroll
+                    for (int dt = 0; dt < DT; ++dt) {
+                        u32x4 oa[4];
+#pragma unroll
+                        for (int i4 = 0; i4 < 4; ++i4)
+                            oa[i4] = __builtin_bit_cast(
+                                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsO, obase + (dt * 32 + i4 * 8) * 4, 0, kSc1));
+                        store_dt(dt, [&](int, int e) { return (w0 * __uint_as_float(oa[e / 4][e % 4]) + w1 * acc[dt][e]) * inv; });
+                    }
+                }
+            }
+        } else if (myq >= p.Sq) {
             // a row past Sq (ragged last tile) writes nothing
         } else if (work.split[w]) {
             // unnormalised O (f32), and m (log2 units) and l, of this half
@@ -490,26 +576,8 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
             if (h == 0) *reinterpret_cast<float2 *>(pML + 2 * row) = float2{m, l};
         } else {
             const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-            typename O::storage *orow = out + ((uint64_t)bh * p.Sq + myq) * HD;
-            // the lane's 4 consecutive dims d .. d + 3 of each (dt, i4) go out
-            // as one store (16 bytes in f32, 8 in 16-bit types): a lane's
-            // row is 64 lanes away from its neighbour's, so every element
-            // store would be a separate memory transaction
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-#pragma unroll
-                for (int i4 = 0; i4 < 4; ++i4) {
-                    const uint32_t d = dt * 32 + i4 * 8 + h * 4;
-                    const float v0 = acc[dt][4 * i4] * inv, v1 = acc[dt][4 * i4 + 1] * inv;
-                    const float v2 = acc[dt][4 * i4 + 2] * inv, v3 = acc[dt][4 * i4 + 3] * inv;
-                    if constexpr (std::is_same<O, pk::F32>::value) {
-                        *reinterpret_cast<float4 *>(orow + d) = float4{v0, v1, v2, v3};
-                    } else {
-                        auto b16 = [](float x) { return (uint32_t)__builtin_bit_cast(uint16_t, O::store(x)); };
-                        *reinterpret_cast<uint2 *>(orow + d) = uint2{b16(v0) | (b16(v1) << 16), b16(v2) | (b16(v3) << 16)};
-                    }
-                }
-            }
+            for (int dt = 0; dt < DT; ++dt) store_dt(dt, [&](int, int e) { return acc[dt][e] * inv; });
         }
     };
     item(0);

@@ -183,7 +183,7 @@ public:
             const char *e = std::getenv("POPCORN_FA_ROWS");
             rows16_ = (d.Hd == 128 || d.Hd == 256) && !(e && std::string(e) == "32");
             // POPCORN_FA_PAIR_MERGE=0: paired tiles merged by the merge
-            // kernel in the 16-row kernels too (a tuning override)
+            // kernel instead of the pair's second block (a tuning override)
             const char *pm = std::getenv("POPCORN_FA_PAIR_MERGE");
             pairMergeInKernel_ = !(pm && std::string(pm) == "0");
             tiledName_ = std::string(rows16_ ? "flash_attention_tiled16_" : "flash_attention_tiled_") + tag(q.dataType) +
@@ -404,9 +404,9 @@ private:
     bool pairTiles_ = false;
     bool rows16_ = false;  // the 16-rows-per-wave kernel: 8 waves per 128-row tile
     int64_t tiledBlock() const { return rows16_ ? 512 : kBlock; }
-    // Paired tiles are merged inside the 16-row kernels (pairTiles 2).
+    // Paired tiles are merged inside the tiled kernels (pairTiles 2).
     bool pairMergeInKernel_ = true;
-    bool mergedPairs() const { return pairTiles_ && rows16_ && pairMergeInKernel_; }
+    bool mergedPairs() const { return pairTiles_ && pairMergeInKernel_; }
     // A 64-bit value, never 0 and distinct per launch, for the ready flags
     // of merged pairs: a counter, started from the clock so that processes
     // differ, through the splitmix64 finaliser.

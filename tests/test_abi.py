@@ -70,10 +70,9 @@ def test_route():
 def test_prefill_attention_split_plan():
     # causal prefill with at most two 128-row tiles per CU (256 CUs when no
     # GPU answers). At most one tile per CU: light and heavy tiles paired,
-    # the second block of a pair merging the split tile itself in the
-    # 16-row kernel (the 32-row kernel leaves it to a merge kernel). Up to
-    # two per CU: tiles with more than half the last tile's key steps run as
-    # two blocks, merged by a second kernel.
+    # the second block of a pair merging the split tile itself. Up to two
+    # per CU: tiles with more than half the last tile's key steps run as two
+    # blocks, merged by a second kernel.
     def fa(Nq, S, mask=(0, -1), dtype="f16"):
         q = T([1, Nq, S, 256], dtype)
         return pa.Kernels.FlashAttention(q, q, q, out=T([1, Nq, S, 256], dtype), scale=1 / 16,

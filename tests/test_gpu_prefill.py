@@ -146,12 +146,9 @@ def _tiled(dtype, ot, Hd, rows):
 
 
 def _paired(dtype, ot, Hd, rows):
-    # paired causal tiles (at most one tile per CU): the 16-row kernel
-    # merges the split tiles itself, the 32-row kernel through a merge kernel
-    names = [_tiled(dtype, ot, Hd, rows)]
-    if not names[0].startswith("flash_attention_tiled16_"):
-        names.append(f"flash_attention_split_merge_{ot}_d{Hd}")
-    return names
+    # paired causal tiles (at most one tile per CU): the second block of a
+    # pair merges the split tile itself, no merge kernel
+    return [_tiled(dtype, ot, Hd, rows)]
 
 
 @pytest.mark.parametrize("dtype,ot", [("f16", "f16"), ("f16", "f32"), ("bf16", "bf16"), ("bf16", "f32")])
@@ -191,8 +188,7 @@ def test_tiled_attention_vs_oracle(env, rows, dtype, ot, B, Nq, Nkv, Sq, Sk, Hd,
 def test_tiled_attention_split_tiles_vs_oracle(env, rows, dtype, ot, B, Nq, Nkv, Sq, Sk, Hd):
     # causal prefill with few tiles per CU: light and heavy query tiles
     # paired into blocks of equal work, the heavy tile of a pair split over
-    # the two blocks and its parts merged (in the 16-row kernel by the
-    # second block of the pair, else by a merge kernel)
+    # the two blocks and its parts merged by the pair's second block
     pa = env[0]
     q = rounded(O.normal(Sq + Hd + 7, (B, Nq, Sq, Hd)), dtype)
     k = rounded(O.normal(Sk + Hd + 8, (B, Nkv, Sk, Hd)), dtype)
