@@ -236,42 +236,94 @@ __device__ void gemm_nt_direct(const uint16_t *__restrict__ A, const uint16_t *_
     auto frag = [&](const uint8_t *base, uint32_t row, uint32_t kc) {
         return *reinterpret_cast<const u32x4 *>(base + row * kRowB + ((kc ^ ((row >> 2) & 3)) << 4));
     };
-    auto compute = [&](uint32_t kt) {
-        const uint8_t *stage = smem + (kt % kStagesD) * kStageB;
-#pragma unroll
-        for (int kk = 0; kk < BKD / 16; ++kk) {
-            const uint32_t kc = kk * 2 + (lane >> 5);
-            u32x4 fa[TM], fb[TN];
-#pragma unroll
-            for (int mi = 0; mi < TM; ++mi) fa[mi] = frag(stage, wm + mi * 32 + (lane & 31), kc);
-#pragma unroll
-            for (int ni = 0; ni < TN; ++ni) fb[ni] = frag(stage + BM * kRowB, wn + ni * 32 + (lane & 31), kc);
-#pragma unroll
-            for (int mi = 0; mi < TM; ++mi)
-#pragma unroll
-                for (int ni = 0; ni < TN; ++ni) acc[mi][ni] = Mma<T>::run(fa[mi], fb[ni], acc[mi][ni]);
-        }
+    // fragment mi of A / ni of B for K-16 half kk of stage kt
+    auto fragA = [&](uint32_t kt, int kk, int mi) {
+        return frag(smem + (kt % kStagesD) * kStageB, wm + mi * 32 + (lane & 31), kk * 2 + (lane >> 5));
     };
-
-    const uint32_t nk = (SPLITK ? K / gridDim.y : K) / BKD;
-#pragma unroll
-    for (int s = 0; s < kStagesD - 1; ++s)
-        if ((uint32_t)s < nk) issue(s);
-    for (uint32_t kt = 0; kt < nk; ++kt) {
-        // stage kt has landed once at most (stages issued after it) x kLPS of
-        // this wave's loads are outstanding; the barrier publishes every
-        // wave's copies and retires the readers of the buffer refilled below
-        const uint32_t after = min((uint32_t)(kStagesD - 2), nk - 1 - kt);
+    auto fragB = [&](uint32_t kt, int kk, int ni) {
+        return frag(smem + (kt % kStagesD) * kStageB + BM * kRowB, wn + ni * 32 + (lane & 31), kk * 2 + (lane >> 5));
+    };
+    // wait until at most `after` stages' copies issued after the awaited
+    // one are outstanding (this wave's own copies of it have landed)
+    auto wait_stage = [&](uint32_t after) {
         if (after >= 2) wait_vmcnt<2 * kLPS>();
         else if (after == 1) wait_vmcnt<kLPS>();
         else wait_vmcnt<0>();
-        // a bare barrier: this wave's copies of stage kt have landed (the
-        // wait above) and its reads of the buffer refilled next were consumed
-        // by last step's MFMAs; __syncthreads() would also drain the copies
-        // still in flight
+    };
+
+    // Each stage is two K-16 halves. The B fragments of the second half are
+    // read at the start of the first (two B sets), and each A fragment is
+    // re-read for the next half as soon as its MFMAs are issued, so a half's
+    // fragments arrive while the previous half's products run. The stage
+    // barrier sits between the halves: before it this wave has read all of
+    // stage kt (lgkmcnt(0)) and its copies of stage kt + 1 have landed;
+    // after it stage kt + 1 is visible, the buffer of stage kt is free for
+    // the copies of stage kt + 4, and the first reads of stage kt + 1 overlap
+    // the second half's products.
+    const uint32_t nk = (SPLITK ? K / gridDim.y : K) / BKD;
+    static_assert(kStagesD == 4, "the waits below count two stages in flight behind the awaited one");
+#pragma unroll
+    for (int s = 0; s < kStagesD - 1; ++s)
+        if ((uint32_t)s < nk) issue(s);
+    wait_stage(min((uint32_t)(kStagesD - 2), nk - 1));
+    __builtin_amdgcn_s_barrier();
+    if ((uint32_t)(kStagesD - 1) < nk) issue(kStagesD - 1);
+    u32x4 fa[TM], fb[TN], fb2[TN];
+    // Scalar loads (kernel arguments) also count in lgkmcnt and complete out
+    // of order: with one still outstanding on entry, the wait before the
+    // loop's first MFMA would have to be lgkmcnt(0) on every pass.
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    // in the order of the passes below (B, then A in order), held by
+    // scheduling barriers: the wait before the first pass's first MFMA is
+    // then the same on entry as around the loop, lgkmcnt(TM - 1)
+#pragma unroll
+    for (int ni = 0; ni < TN; ++ni) {
+        fb[ni] = fragB(0, 0, ni);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int mi = 0; mi < TM; ++mi) {
+        fa[mi] = fragA(0, 0, mi);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // The compiler would sink each fragment read to just before its first
+    // use; the scheduling groups keep this order: per A fragment its MFMAs,
+    // then its re-read (after the first group also the B reads).
+    auto pin_order = [&] {
+        __builtin_amdgcn_sched_group_barrier(0x008, TN, 0);      // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, TN + 1, 0);  // DS reads
+#pragma unroll
+        for (int mi = 1; mi < TM; ++mi) {
+            __builtin_amdgcn_sched_group_barrier(0x008, TN, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
+        }
+    };
+    for (uint32_t kt = 0; kt < nk; ++kt) {
+#pragma unroll
+        for (int ni = 0; ni < TN; ++ni) fb2[ni] = fragB(kt, 1, ni);
+#pragma unroll
+        for (int mi = 0; mi < TM; ++mi) {
+#pragma unroll
+            for (int ni = 0; ni < TN; ++ni) acc[mi][ni] = Mma<T>::run(fa[mi], fb[ni], acc[mi][ni]);
+            fa[mi] = fragA(kt, 1, mi);
+        }
+        pin_order();
+        // stages issued so far: up to min(kt + 3, nk - 1). In the last pass
+        // nothing is outstanding, and the reads of "stage kt + 1" fetch a
+        // buffer no copy is writing, unused (no branches inside the pass).
+        wait_stage(kt + 2 < nk ? min((uint32_t)(kStagesD - 2), nk - 2 - kt) : 0u);
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of stage kt are done
         __builtin_amdgcn_s_barrier();
-        if (kt + kStagesD - 1 < nk) issue(kt + kStagesD - 1);
-        compute(kt);
+        if (kt + kStagesD < nk) issue(kt + kStagesD);
+#pragma unroll
+        for (int ni = 0; ni < TN; ++ni) fb[ni] = fragB(kt + 1, 0, ni);
+#pragma unroll
+        for (int mi = 0; mi < TM; ++mi) {
+#pragma unroll
+            for (int ni = 0; ni < TN; ++ni) acc[mi][ni] = Mma<T>::run(fa[mi], fb2[ni], acc[mi][ni]);
+            fa[mi] = fragA(kt + 1, 0, mi);
+        }
+        pin_order();
     }
 
 #pragma unroll
