@@ -202,6 +202,23 @@ def test_tiled_attention_split_tiles_vs_oracle(env, rows, dtype, ot, B, Nq, Nkv,
 
 
 @pytest.mark.parametrize("Hd", [64, 256])
+def test_tiled_attention_pairs_with_merge_kernel(env, monkeypatch, Hd):
+    # POPCORN_FA_PAIR_MERGE=0: paired tiles merged by the split-merge kernel
+    # (pairTiles 1) instead of the pair's second block
+    monkeypatch.setenv("POPCORN_FA_PAIR_MERGE", "0")
+    pa = env[0]
+    B, Nq, Nkv, S, dtype = 1, 2, 1, 640, "f16"
+    q = rounded(O.normal(S + Hd + 1, (B, Nq, S, Hd)), dtype)
+    k = rounded(O.normal(S + Hd + 2, (B, Nkv, S, Hd)), dtype)
+    v = rounded(O.normal(S + Hd + 3, (B, Nkv, S, Hd)), dtype)
+    scale = 1 / np.sqrt(Hd)
+    got, kern = _attend(env, q, k, v, dtype, dtype, scale, pa.AttentionMask(0, -1))
+    assert kern.function_names[1] == f"flash_attention_split_merge_{dtype}_d{Hd}"
+    ref = O.attention_naive(q, k, v, scale, mask_kind=0)
+    assert_out(got, ref, EPS[dtype], dtype, f"paired tiles, merge kernel, Hd={Hd}")
+
+
+@pytest.mark.parametrize("Hd", [64, 256])
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
 def test_tiled_attention_wide_score_range(env, rows, dtype, Hd):
     # scores spread over hundreds of natural-log units (scale 1, inputs x 3):
