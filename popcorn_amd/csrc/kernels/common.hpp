@@ -113,8 +113,10 @@ __device__ inline float Vec<F16>::get(int i) const {
 }
 
 // ---- wave64 reductions --------------------------------------------------
-// DPP moves within 16-lane rows, ds_swizzle across the two rows of a 32-lane
-// half, readlane across halves.
+// DPP moves within 16-lane rows, then the gfx950 lane swaps across rows
+// (v_permlane16_swap) and across the wave's halves (v_permlane32_swap), all
+// in registers. Each swap step adds (or maxes) a lane's value and its
+// partner's; addition is commutative, so every lane ends with the same bits.
 
 template <int kCtrl>
 __device__ inline float dpp(float v) {
@@ -137,26 +139,6 @@ __device__ inline float row16_max(float v) {
     v = fmaxf(v, dpp<0x140>(v));
     return v;
 }
-
-// xor-16 lane exchange inside each 32-lane half (ds_swizzle bitmask mode:
-// and 0x1f, or 0, xor 0x10).
-__device__ inline float swap16(float v) {
-    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401f));
-}
-
-// Sum over each 32-lane half, result in every lane of the half.
-__device__ inline float half32_sum(float v) {
-    v = row16_sum(v);
-    return v + swap16(v);
-}
-
-__device__ inline float half32_max(float v) {
-    v = row16_max(v);
-    return fmaxf(v, swap16(v));
-}
-
-// xor-32 exchange (the other half of the wave).
-__device__ inline float swap32(float v) { return __shfl_xor(v, 32, 64); }
 
 // max and sum of v over lanes l and l ^ 32 in registers: v_permlane32_swap
 // trades lanes 0-31 of its first operand with lanes 32-63 of its second, so
@@ -181,16 +163,13 @@ __device__ inline float pair32_sum(float v) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// Sum over the wave, result in every lane.
-__device__ inline float wave_sum(float v) {
-    v = half32_sum(v);
-    return v + swap32(v);
-}
+// Sum over each 32-lane half, result in every lane of the half.
+__device__ inline float half32_sum(float v) { return pair16_sum(row16_sum(v)); }
+__device__ inline float half32_max(float v) { return pair16_max(row16_max(v)); }
 
-__device__ inline float wave_max(float v) {
-    v = half32_max(v);
-    return fmaxf(v, swap32(v));
-}
+// Sum over the wave, result in every lane.
+__device__ inline float wave_sum(float v) { return pair32_sum(half32_sum(v)); }
+__device__ inline float wave_max(float v) { return pair32_max(half32_max(v)); }
 
 // Sum over groups of `kLanes` consecutive lanes (power of two, 1..64),
 // result in every lane of the group.
@@ -200,8 +179,8 @@ __device__ inline float group_sum(float v) {
     if constexpr (kLanes >= 4) v += dpp<0x4E>(v);
     if constexpr (kLanes >= 8) v += dpp<0x141>(v);
     if constexpr (kLanes >= 16) v += dpp<0x140>(v);
-    if constexpr (kLanes >= 32) v += swap16(v);
-    if constexpr (kLanes >= 64) v += swap32(v);
+    if constexpr (kLanes >= 32) v = pair16_sum(v);
+    if constexpr (kLanes >= 64) v = pair32_sum(v);
     return v;
 }
 
@@ -211,8 +190,8 @@ __device__ inline float group_max(float v) {
     if constexpr (kLanes >= 4) v = fmaxf(v, dpp<0x4E>(v));
     if constexpr (kLanes >= 8) v = fmaxf(v, dpp<0x141>(v));
     if constexpr (kLanes >= 16) v = fmaxf(v, dpp<0x140>(v));
-    if constexpr (kLanes >= 32) v = fmaxf(v, swap16(v));
-    if constexpr (kLanes >= 64) v = fmaxf(v, swap32(v));
+    if constexpr (kLanes >= 32) v = pair16_max(v);
+    if constexpr (kLanes >= 64) v = pair32_max(v);
     return v;
 }
 

@@ -372,13 +372,24 @@ __device__ void fd_partial_fast(const typename T::storage *__restrict__ Q, const
         }
     }
 
-    // Merge the key groups of this wave (lanes dl, dl + LPK, ...).
+    // Merge the key groups of this wave (lanes dl, dl + LPK, ...): the xor-16
+    // and xor-32 steps as register lane swaps
 #pragma unroll
     for (int g = 0; g < GMAX; ++g) {
-        for (int sft = LPK; sft < 64; sft <<= 1) {
-            l[g] += __shfl_xor(l[g], sft, 64);
+        if constexpr (LPK <= 8) {
+            l[g] += __shfl_xor(l[g], 8, 64);
 #pragma unroll
-            for (int e = 0; e < DL; ++e) o[g][e] += __shfl_xor(o[g][e], sft, 64);
+            for (int e = 0; e < DL; ++e) o[g][e] += __shfl_xor(o[g][e], 8, 64);
+        }
+        if constexpr (LPK <= 16) {
+            l[g] = pk::pair16_sum(l[g]);
+#pragma unroll
+            for (int e = 0; e < DL; ++e) o[g][e] = pk::pair16_sum(o[g][e]);
+        }
+        if constexpr (LPK <= 32) {
+            l[g] = pk::pair32_sum(l[g]);
+#pragma unroll
+            for (int e = 0; e < DL; ++e) o[g][e] = pk::pair32_sum(o[g][e]);
         }
     }
     if (kg == 0) {
