@@ -16,6 +16,8 @@
 // are dealt round-robin to the 8 XCDs, so block b runs on XCD b % 8) and,
 // within an XCD's range, in groups of 8 tile rows, so the A and B panels a
 // group shares stay in that XCD's L2.
+#include <type_traits>
+
 #include "mfma.hpp"
 
 namespace {
@@ -361,10 +363,13 @@ __device__ void gemm_splitk_reduce(const float *__restrict__ P, typename O::stor
             a.z += b.z;
             a.w += b.w;
         }
-        C[i] = O::store(a.x);
-        C[i + 1] = O::store(a.y);
-        C[i + 2] = O::store(a.z);
-        C[i + 3] = O::store(a.w);
+        if constexpr (std::is_same<O, pk::F32>::value) {
+            *reinterpret_cast<float4 *>(C + i) = a;
+        } else {
+            // the four 16-bit results as one 8-byte store
+            auto b16 = [](float x) { return (uint32_t)__builtin_bit_cast(uint16_t, O::store(x)); };
+            *reinterpret_cast<uint2 *>(C + i) = uint2{b16(a.x) | (b16(a.y) << 16), b16(a.z) | (b16(a.w) << 16)};
+        }
     }
 }
 

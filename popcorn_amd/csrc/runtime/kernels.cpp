@@ -770,7 +770,8 @@ std::unique_ptr<Kernel> makeMatmul(const Tensor &a, const Tensor &b, const Tenso
         if (transposeB && (t == DataType::f16 || t == DataType::bf16) && b.dataType == t &&
             (c.dataType == t || c.dataType == DataType::f32) && k % 8 == 0 && k > 0 && aligned16(a.data) &&
             aligned16(b.data)) {
-            if (const int64_t splits = gemmSplitK(m, n, k))
+            // the split-K reduction stores 4 results of C at a time
+            if (const int64_t splits = aligned16(c.data) ? gemmSplitK(m, n, k) : 0)
                 return std::make_unique<SplitKMatmulKernel>(a, b, c, m, k, n, splits);
             MatmulConstants mc{(uint32_t)m, (uint32_t)k, (uint32_t)n, 1u};
             const GemmTile tile = gemmTile(m, n, k);
