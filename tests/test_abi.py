@@ -98,6 +98,10 @@ def test_prefill_gemm_tile_plan():
     assert mm(2000, 16384, 1500, "bf16", "f32") == ["matmul_mfma_bf16_splitk_d256x384",
                                                     "matmul_splitk_reduce_f32"]  # 32 tiles x 8 splits
     assert mm(2048, 4096, 3072) == ["matmul_mfma_f16_f16_f16_d128x192"]    # splits would be under 2048 deep
+    # the split-K reduction stores 4 results at a time: a C not 16-byte aligned keeps one pass
+    c_off = pa.Kernels.Matmul(T([2048, 24576], "f16"), T([3072, 24576], "f16"), T([2048, 3072], "f16", FAKE + 8),
+                              True).function_names
+    assert c_off == ["matmul_mfma_f16_f16_f16_d128x192"]
     assert mm(256, 1024, 384) == ["matmul_mfma_f16_f16_f16_d128x128"]
 
 
