@@ -290,3 +290,40 @@ def test_tiled_attention_two_tiles_per_cu_sampled(env, rows):
     for r in (0, 127, 1023, 1024, 1100, 1535, 2047):
         ref = O.attention_naive(q[:, :, r:r + 1], k[:, :, :r + 1].copy(), v[:, :, :r + 1].copy(), 1 / 16)
         assert_out(got[:, :, r:r + 1], ref, EPS["f16"], "f16", f"two tiles per CU row {r}")
+
+
+def test_merged_pairs_reset_ready_flags(env):
+    # A raw launch of the 16-row kernel with pairTiles 2 (causal, 2 heads x 5
+    # tiles: two pairs and a middle tile per head) twice with the same
+    # ticket, as a replayed graph would: after each launch every ready flag
+    # is back to 0 (the merging block resets it), and the second launch,
+    # over new queries, matches the oracle too.
+    import struct
+    pa, lib, stream, enc = env
+    B, Nq, S, Hd, dtype = 1, 2, 640, 128, "f16"
+    nQT = (S + 127) // 128
+    nSplit = nQT // 2
+    tiles = B * Nq * nSplit
+    ticket = 0x5EED1234ABCD0001
+    # TiledFlashAttentionConstants: B, Nq, Nkv, Sq, Sk, Hd, qTilesPerHead,
+    # maskKind (0: causal), slidingWindow (-1), scale, kvStride, splitFrom,
+    # pairTiles, ticketLo, ticketHi
+    consts = struct.pack("<8Iif5I", B, Nq, Nq, S, S, Hd, nQT, 0, -1, 1 / np.sqrt(Hd), 0,
+                         nQT - nSplit, 2, ticket & 0xFFFFFFFF, ticket >> 32)
+    k = rounded(O.normal(11, (B, Nq, S, Hd)), dtype)
+    v = rounded(O.normal(12, (B, Nq, S, Hd)), dtype)
+    tk, tv = upload(pa, k, dtype), upload(pa, v, dtype)
+    pO = pa.Tensor.empty([tiles * 128, Hd], "f32")
+    pML = upload(pa, np.zeros(tiles * 128 * 2 + tiles * 2, np.float32), "f32")
+    for rep in range(2):
+        q = rounded(O.normal(20 + rep, (B, Nq, S, Hd)), dtype)
+        tq = upload(pa, q, dtype)
+        out = upload(pa, np.full((B, Nq, S, Hd), np.nan, np.float32), dtype)
+        lib.launch(f"flash_attention_tiled16_{dtype}_{dtype}_d{Hd}", (B * Nq * nQT, 1, 1), (512, 1, 1),
+                   [tq.ptr, tk.ptr, tv.ptr, out.ptr, pO.ptr, pML.ptr], [consts], stream=stream)
+        stream.synchronize()
+        flags = download(pML, stream)[tiles * 128 * 2:].view(np.uint64)
+        assert (flags == 0).all(), f"launch {rep}: ready flags not reset: {flags}"
+        got = download(out, stream).reshape(B, Nq, S, Hd)
+        ref = O.attention_naive(q, k, v, 1 / np.sqrt(Hd), mask_kind=0)
+        assert_out(got, ref, EPS[dtype], dtype, f"merged pairs, launch {rep}")
