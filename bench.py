@@ -425,9 +425,7 @@ def decode_variant(pa, lib, stream, D, token, steps, warmup, graph_steps, use_gr
     rate of the whole step, and the mean time of each of the step's kernels.
     attention_block=1: a real attention block (per-head q/k RMSNorm, v RMSNorm,
     RoPE at theta 10000, Gemma4TextInference.swift:352-371) folded into the
-    attention partial kernel; weight_bits=4: block-affine 4-bit weights;
-    fused_layers=1: all layers in one persistent launch, with the mean time of
-    each of its phases per layer (stamped steps)."""
+    attention partial kernel; weight_bits=4: block-affine 4-bit weights."""
     cfg = D.DecoderConfig(graph_steps=graph_steps, **variant)
     dec = D.Decoder(lib, stream, cfg)
     dec.randomize(seed=0)
@@ -443,10 +441,6 @@ def decode_variant(pa, lib, stream, D, token, steps, warmup, graph_steps, use_gr
         kernels[name] = round(ms * 1e3, 2)
     out = {"tok_s": round(tok_s, 2), "ms_per_step": round(elapsed * 1e3 / steps, 4), "dispatches_per_step": nd,
            "hbm_step_GB_s": round(step_bytes * tok_s / 1e9, 1), "kernel_in_step_us": kernels}
-    if dec.fused:
-        dec.reset(token, START_POS)
-        phases = ["qkv", "attention_combine", "o", "gate_up", "hidden_fetch", "down"]
-        out["phase_us_per_layer"] = dict(zip(phases, (round(p, 2) for p in dec.phase_times(2))))
     dec.close()
     return out
 
@@ -469,8 +463,6 @@ def main():
     ap.add_argument("--no-q4", action="store_true", help="skip the 4-bit matvec measurement")
     ap.add_argument("--no-attention-block", action="store_true",
                     help="skip the decode with per-head norms and RoPE (a real attention block)")
-    ap.add_argument("--no-fused-layers", action="store_true",
-                    help="skip the decode through the persistent decode-layers kernel")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 3 device-to-device copies of 1 GiB (the known-size kernel that scales the "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -563,10 +555,7 @@ def main():
     if not args.no_q4:
         q4 = q4_sweep(pa, lib, stream, pa.KernelCommandEncoder(lib, stream))
 
-    block = q4dec = fused = None
-    if not args.no_fused_layers:
-        fused = decode_variant(pa, lib, stream, D, token, args.steps, args.warmup, args.graph_steps, use_graph,
-                               args.kernel_reps, fused_layers=1)
+    block = q4dec = None
     if not args.no_attention_block:
         block = decode_variant(pa, lib, stream, D, token, args.steps, args.warmup, args.graph_steps, use_graph,
                                args.kernel_reps, attention_block=1)
@@ -600,7 +589,6 @@ def main():
         "mlp_config3": mlp,
         "prefill_config5": prefill,
         "decode_attention_block": block,
-        "decode_fused_layers": fused,
         "q4_matvec": q4,
         "decode_q4": q4dec,
         "cpu_baseline": cpu,

@@ -55,15 +55,6 @@ typedef struct {
     int32_t weight_bits;  /* 16 (or 0): bf16 weights; 4: block-affine 4-bit, group
                              64, bf16 scales and biases (the MLX format of
                              AffineQuantizedTensor.swift), embedding included  */
-    int32_t fused_layers; /* 1: the layers of a step run as one persistent kernel
-                             (decode_layers_bf16_h<Hd>_g<G>, one block per CU,
-                             grid-wide waits between its phases) followed by
-                             the head's three kernels, where the shape allows
-                             it (bf16 weights, no attention_block, a compiled
-                             head dim and group size, LDS and occupancy for
-                             one block per CU); otherwise, and with 0, six
-                             kernels per layer. popcorn_decoder_describe
-                             lists what a step dispatches.                     */
 } popcorn_decoder_config_t;
 
 typedef struct popcorn_decoder_s *popcorn_decoder_t;
@@ -80,12 +71,7 @@ popcorn_status_t popcorn_decoder_randomize(popcorn_decoder_t decoder, uint64_t s
  * "w_gate", "w_up", "w_down", "norm_in", "norm_post_attn", "norm_pre_ffn",
  * "norm_post_ffn", "k_cache", "v_cache" and, with attention_block, "q_norm"
  * and "k_norm" (per `layer`); "inv_freq" (attention_block), "x", "logits",
- * "token", "position", "history", "layer_sync" (fused_layers: the persistent
- * kernel's sync words, u32: arrival counters, done counter, abort word and
- * launch epoch), "layer_stamps" (after
- * popcorn_decoder_phase_times: the persistent kernel's last stamped step,
- * u64 [blocks][2048], per block the 100 MHz clock at the release of each
- * block-wide barrier, six per layer), plus the last layer's step buffers
+ * "token", "position", "history", plus the last layer's step buffers
  * "q", "qkv", "attn", "o", "mlp", "hidden" and "x2" (the residual stream
  * the last layer's MLP and the head read: after a step it holds the stream
  * after the last attention block, while "x" holds the next step's input
@@ -140,18 +126,6 @@ popcorn_status_t popcorn_decoder_time_kernel(popcorn_decoder_t decoder, const ch
  * steps: 1..16. */
 popcorn_status_t popcorn_decoder_time_kernel_in_step(popcorn_decoder_t decoder, const char *function_name,
                                                      int32_t steps, float *mean_ms, int32_t *launches);
-
-/* Phase times of the persistent layer kernel (fused_layers): runs `steps`
- * eager decode steps from the current position (advancing it) with the
- * kernel's per-block stamps on (the 100 MHz clock read by each block when
- * its block-wide barrier at a phase boundary releases), and reports for each
- * of the six intervals between a layer's barriers (0 QKV, 1 attention
- * partials and combine, 2 O projection, 3 gate/up, 4 fetching hidden, 5 down)
- * the mean over layers and steps of (last block's release of the next
- * barrier) - (last block's release of this one), in microseconds, in
- * phase_us[0..5]. -1001 when the decoder does not run the fused kernel.
- * steps: 1..16. */
-popcorn_status_t popcorn_decoder_phase_times(popcorn_decoder_t decoder, int32_t steps, float *phase_us);
 
 #ifdef __cplusplus
 }

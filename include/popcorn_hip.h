@@ -131,11 +131,25 @@ typedef struct {
 popcorn_status_t popcorn_device_count(int32_t *count);
 popcorn_status_t popcorn_set_device(int32_t device);
 popcorn_status_t popcorn_device_info(int32_t device, popcorn_device_info_t *info);
+/* Waits for the device; then, like popcorn_stream_synchronize, reports a
+ * merged-pair wait of the tiled prefill attention that gave up on any stream
+ * of the device (-1019). */
 popcorn_status_t popcorn_device_synchronize(void);
 
 /* makeTensor's allocation; -1003 (tensorAllocationFailed) on failure. */
 popcorn_status_t popcorn_malloc(size_t bytes, void **ptr);
 popcorn_status_t popcorn_free(void *ptr);
+
+/* No counterpart in the reference (Metal buffers have no per-XCD caches):
+ * uncached device memory (hipDeviceMallocUncached), for buffers that blocks
+ * on different XCDs of one launch exchange data through, such as the
+ * pO/pML/pairFlags buffers of a raw launch of flash_attention_tiled*_ with
+ * pairTiles 2. popcorn_free_uncached returns the block to a process-wide
+ * pool for reuse by a later request of the same size on the same device;
+ * such memory is never given back to the driver (memory of this kind, once
+ * read by a kernel, is not freed before the process ends). */
+popcorn_status_t popcorn_malloc_uncached(size_t bytes, void **ptr);
+popcorn_status_t popcorn_free_uncached(void *ptr);
 
 typedef struct popcorn_stream_s *popcorn_stream_t; /* NULL = default stream */
 
@@ -153,7 +167,19 @@ typedef struct popcorn_event_s *popcorn_event_t;
 
 popcorn_status_t popcorn_stream_create(popcorn_stream_t *stream);
 popcorn_status_t popcorn_stream_destroy(popcorn_stream_t stream);
+/* Waits for the stream; then reports -1019 (gpuInternal) when a merged pair
+ * of the tiled prefill attention (pairTiles 2) gave up waiting for its
+ * partner block on this stream since the last check (its rows were written
+ * as NaN; the stream's ready flags are cleared before returning), the way
+ * the reference reports a command buffer's GPU error on completion
+ * (PopcornError.swift:240-266). */
 popcorn_status_t popcorn_stream_synchronize(popcorn_stream_t stream);
+
+/* No counterpart in the reference: the ready flags of the tiled prefill
+ * attention's merged pairs on `stream` (created on first use): u64
+ * [count], index 0 the abort word, 1 + t the flag of split tile t, in
+ * uncached device memory. For inspection and tests. */
+popcorn_status_t popcorn_attention_pair_flags(popcorn_stream_t stream, void **flags, int32_t *count);
 
 popcorn_status_t popcorn_event_create(popcorn_event_t *event);
 popcorn_status_t popcorn_event_destroy(popcorn_event_t event);

@@ -123,13 +123,20 @@ typedef struct {
  *              (qTilesPerHead blocks per head);
  *              2: pairs as for 1, but the first
  *              block of a pair runs its steps of the partner first and
- *              publishes them (partial O for part 0 only, (m, l), then a
- *              64-bit ready flag per split tile after the (m, l) rows), and
- *              the second block merges them into the output itself: no
- *              split-merge kernel;
- *   ticketLo, ticketHi  pairTiles 2: the 64-bit value (never 0) the ready
- *              flags are set to, distinct per launch; the merging block
- *              resets its flag to 0. */
+ *              publishes them (partial O and (m, l) of part 0 in the pO and
+ *              pML buffers, then the split tile's 64-bit ready flag in
+ *              pairFlags), and the second block merges them into the output
+ *              itself: no split-merge kernel. pO, pML and pairFlags must be
+ *              uncached device memory (popcorn_malloc_uncached): the two
+ *              blocks may sit on XCDs whose L2 caches are not coherent.
+ *              pairFlags (u64) holds the abort word at index 0 and the flag
+ *              of split tile t at index 1 + t; all start at 0;
+ *   ticketLo, ticketHi  pairTiles 2: the 64-bit value (neither 0 nor
+ *              ~0) the first block sets its flag to, by compare-and-swap
+ *              from 0, distinct per launch; the merging block resets the
+ *              flag to 0. A merging block that gives up (0.2 s, or a flag
+ *              holding a value other than 0 and the ticket) sets the flag
+ *              to ~0, the abort word to 1 and its rows to NaN. */
 typedef struct {
     uint32_t B;
     uint32_t Nq;
@@ -384,34 +391,6 @@ typedef struct {
     float scale;
     uint32_t hasBias;
 } DecodeNextTokenConstants;
-
-/* No counterpart in the reference: the decoder layers of one batch-1 decode
- * step (Gemma4TextInference.swift:312-436, `layers` times, in the headline
- * decode configuration: no per-head norms or RoPE) as one persistent kernel,
- * one block per CU. Per layer: QKV matvec with the residual glue and the
- * KV-cache writes; split-KV attention over `partitions` partitions per KV
- * head; the log-sum-exp combine; the O projection; the gate/up matvec with
- * the residual glue; the down matvec. Blocks exchange activations through a
- * workspace of tagged words (each value stored with a tag naming the launch,
- * layer and phase), so a consumer waits for exactly the values it reads and
- * no step waits for the whole grid; each block's staging wave prepares the
- * next phase's input while its streaming waves run the current one.
- * spinTicks bounds each wait (100 MHz ticks, 0: 0.5 s); a wait that runs out
- * sets the abort word and the block stops waiting. */
-typedef struct {
-    uint32_t layers;
-    uint32_t H;
-    uint32_t Nq;
-    uint32_t Nkv;
-    uint32_t Hd;
-    uint32_t F;
-    uint32_t kvStride;   /* KV-cache rows per head (capacity)                 */
-    uint32_t partitions; /* split-KV partitions per KV head, 1..64            */
-    float eps;
-    float scale;         /* attention scale                                  */
-    uint32_t spinTicks;
-    uint32_t reserved;
-} DecodeLayersConstants;
 
 #ifdef __cplusplus
 }

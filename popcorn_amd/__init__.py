@@ -8,6 +8,8 @@ Swift API over that ABI.
 from ._capi import LIB_PATH, KERNEL_DIR  # noqa: F401
 from .runtime import (  # noqa: F401
     AffineQuantizedTensor,
+    UncachedBuffer,
+    attention_pair_flags,
     AttentionMask,
     DeviceBuffer,
     Event,

@@ -78,7 +78,7 @@ class DecoderConfig(C.Structure):
                 ("kv_heads", C.c_int32), ("head_dim", C.c_int32), ("ffn", C.c_int32), ("vocab", C.c_int32),
                 ("max_seq", C.c_int32), ("eps", C.c_float), ("attn_scale", C.c_float),
                 ("history_len", C.c_int32), ("graph_steps", C.c_int32), ("attention_block", C.c_int32),
-                ("rope_theta", C.c_float), ("weight_bits", C.c_int32), ("fused_layers", C.c_int32)]
+                ("rope_theta", C.c_float), ("weight_bits", C.c_int32)]
 
 
 _T = C.POINTER(TensorDesc)
@@ -112,6 +112,8 @@ PROTOTYPES = {
     "popcorn_device_synchronize": (_st, []),
     "popcorn_malloc": (_st, [C.c_size_t, C.POINTER(C.c_void_p)]),
     "popcorn_free": (_st, [C.c_void_p]),
+    "popcorn_malloc_uncached": (_st, [C.c_size_t, C.POINTER(C.c_void_p)]),
+    "popcorn_free_uncached": (_st, [C.c_void_p]),
     "popcorn_memcpy_h2d": (_st, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
     "popcorn_memcpy_d2h": (_st, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
     "popcorn_memcpy_d2d": (_st, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
@@ -119,6 +121,7 @@ PROTOTYPES = {
     "popcorn_stream_create": (_st, [C.POINTER(C.c_void_p)]),
     "popcorn_stream_destroy": (_st, [C.c_void_p]),
     "popcorn_stream_synchronize": (_st, [C.c_void_p]),
+    "popcorn_attention_pair_flags": (_st, [C.c_void_p, C.POINTER(C.c_void_p), C.POINTER(C.c_int32)]),
     "popcorn_event_create": (_st, [C.POINTER(C.c_void_p)]),
     "popcorn_event_destroy": (_st, [C.c_void_p]),
     "popcorn_event_record": (_st, [C.c_void_p, C.c_void_p]),
@@ -211,7 +214,6 @@ PROTOTYPES = {
     "popcorn_decoder_step_bytes": (C.c_int64, [C.c_void_p, C.c_int32]),
     "popcorn_decoder_time_kernel": (_st, [C.c_void_p, C.c_char_p, C.c_int32, C.POINTER(C.c_float),
                                           C.POINTER(C.c_int32)]),
-    "popcorn_decoder_phase_times": (_st, [C.c_void_p, C.c_int32, C.POINTER(C.c_float)]),
     "popcorn_decoder_time_kernel_in_step": (_st, [C.c_void_p, C.c_char_p, C.c_int32, C.POINTER(C.c_float),
                                           C.POINTER(C.c_int32)]),
 }

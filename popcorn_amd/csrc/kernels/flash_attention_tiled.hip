@@ -42,21 +42,70 @@ constexpr float kRescaleGap = 8.0f;
 constexpr float kLog2e = 1.4426950408889634f;
 
 // Partial state handed between the two blocks of a merged pair (pairTiles
-// 2) goes through agent-coherent accesses: 16-byte buffer stores and loads
-// with cache policy sc1, which write through and read past the XCD's L2
-// (the two blocks may run on different XCDs, whose L2s are not coherent),
-// and single-copy atomic 64-bit words for (m, l) and the ready flag.
+// 2). The two blocks may run on different XCDs, whose L2 caches are not
+// coherent with each other, so the exchange lives in uncached device memory
+// (hipDeviceMallocUncached: every access goes to memory, whatever the
+// instruction's cache policy), which the host allocates for it and never
+// frees: 16-byte buffer stores and loads for O (with the agent-scope cache
+// policy sc1 as well), single-copy atomic 64-bit words for (m, l).
+//
+// Ready flags: pairFlags[0] is the abort word, pairFlags[1 + tile] the flag
+// of split tile `tile`: 0 while idle, the launch's ticket once the first
+// block's part is published, kPoison once a merging block gave up on it.
+// The first block publishes with a compare-and-swap from 0, so it never
+// writes into a poisoned flag; the merging block takes the ticket and resets
+// the flag to 0. A merging block whose wait ends without the ticket (0.2 s
+// of the 100 MHz clock, or a flag holding anything but 0 or the ticket)
+// poisons the flag with a compare-and-swap from 0, writes NaN rows and sets
+// the abort word: a producer that publishes late then finds the flag
+// poisoned and leaves it, so no later launch with the same ticket (a replayed
+// graph) can take a stale part, and every later launch on that flag fails
+// the same way until the host, reporting the abort, clears the flags. The
+// wait cannot deadlock: the publishing block has the lower index, so it was
+// dispatched first, and it waits for nothing.
 constexpr int kSc1 = 16;
-// polls of the ready flag before the merging block gives up (about 0.3 s;
-// the publishing block has the lower index, so it was dispatched first and
-// waits for nothing)
-constexpr uint32_t kFlagPolls = 1u << 22;
+constexpr uint64_t kPoison = ~0ull;
+constexpr uint64_t kWaitTicks = 20000000ull;  // 0.2 s of s_memrealtime (100 MHz)
+constexpr uint32_t kFlagPolls = 1u << 22;     // a second bound on the polls
 __device__ inline uint64_t ld64c(const void *p) {
     return __hip_atomic_load(reinterpret_cast<uint64_t *>(const_cast<void *>(p)), __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ inline void st64c(void *p, uint64_t v) {
     __hip_atomic_store(reinterpret_cast<uint64_t *>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline bool cas64c(uint64_t *p, uint64_t &expected, uint64_t v) {
+    return __hip_atomic_compare_exchange_strong(p, &expected, v, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+}
+// The first block of a pair, once every wave's stores of its part have
+// completed: the flag goes from 0 to the ticket, or stays as it is.
+__device__ inline void pair_publish(uint64_t *pairFlags, uint32_t tile, uint64_t ticket) {
+    uint64_t expected = 0;
+    (void)cas64c(pairFlags + 1 + tile, expected, ticket);
+}
+// The merging block (one thread): 1 when the partner's part of this launch
+// is there (the flag is then reset to 0), 0 when the wait gave up (the flag
+// is then poisoned and the abort word set).
+__device__ inline uint32_t pair_take(uint64_t *pairFlags, uint32_t tile, uint64_t ticket) {
+    uint64_t *flag = pairFlags + 1 + tile;
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    for (uint32_t i = 0; i < kFlagPolls; ++i) {
+        const uint64_t v = ld64c(flag);
+        if (v == ticket) {
+            st64c(flag, 0u);
+            return 1u;
+        }
+        if (v != 0u || __builtin_amdgcn_s_memrealtime() - t0 > kWaitTicks) break;
+        __builtin_amdgcn_s_sleep(2);
+    }
+    uint64_t expected = 0;
+    if (!cas64c(flag, expected, kPoison) && expected == ticket) {  // published meanwhile
+        st64c(flag, 0u);
+        return 1u;
+    }
+    st64c(pairFlags, 1u);
+    return 0u;
 }
 // Vt rows hold a step's keys in the order of P^T's key slots (key index
 // with bits 2 and 3 swapped): slots 8 h .. 8 h + 7 of k-step ks, which lane
@@ -192,7 +241,8 @@ __device__ inline FaWork fa_work(const TiledFlashAttentionConstants &p) {
 template <typename T, typename O, int HD>
 __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
                          const uint16_t *__restrict__ V, typename O::storage *__restrict__ out,
-                         float *__restrict__ pO, float *__restrict__ pML, const TiledFlashAttentionConstants &p) {
+                         float *__restrict__ pO, float *__restrict__ pML, uint64_t *__restrict__ pairFlags,
+                         const TiledFlashAttentionConstants &p) {
     constexpr int KS = HD / 16;  // k-steps of S^T = K . Q^T
     constexpr int DT = HD / 32;  // 32-row tiles of O^T
     constexpr int LDK = HD + 8;  // sK row (padded, elements)
@@ -499,7 +549,6 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
             const uint32_t tile = bh * nSplit + (qt - p.splitFrom);
             const uint32_t rowsTotal = p.B * p.Nq * nSplit * BQ;
             const uint64_t row = (uint64_t)tile * BQ + wave * 32 + c32;
-            void *flag = pML + 2 * (uint64_t)rowsTotal + 2 * (uint64_t)tile;
             const uint64_t ticket = ((uint64_t)p.ticketHi << 32) | p.ticketLo;
             const __amdgpu_buffer_rsrc_t rsO =
                 __builtin_amdgcn_make_buffer_rsrc(pO, 0, (int)(rowsTotal * HD * 4u), 0x00020000);
@@ -518,23 +567,12 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
                 }
                 __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's stores have completed
                 __syncthreads();
-                if (threadIdx.x == 0) st64c(flag, ticket);
+                if (threadIdx.x == 0) pair_publish(pairFlags, tile, ticket);
             } else {
-                if (threadIdx.x == 0) {
-                    uint32_t ok = 0u;
-                    for (uint32_t i = 0; i < kFlagPolls; ++i) {
-                        if (ld64c(flag) == ticket) {
-                            ok = 1u;
-                            break;
-                        }
-                        __builtin_amdgcn_s_sleep(2);
-                    }
-                    sReady = ok;
-                }
+                if (threadIdx.x == 0) sReady = pair_take(pairFlags, tile, ticket);
                 __syncthreads();
                 asm volatile("" ::: "memory");  // the partner's state is read after the flag
                 const bool ok = sReady != 0u;
-                if (threadIdx.x == 0) st64c(flag, 0u);
                 if (myq < p.Sq) {
                     const uint64_t ml = ld64c(pML + 2 * row);
                     const float m0 = __uint_as_float((uint32_t)ml), l0 = __uint_as_float((uint32_t)(ml >> 32));
@@ -542,7 +580,7 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
                     const float w0 = m0 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m0 - M);
                     const float w1 = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M);
                     const float L = w0 * l0 + w1 * l;
-                    // a flag never seen (the partner never ran) gives NaN rows, not stale data
+                    // a wait that gave up gives NaN rows, not stale data
                     const float inv = !ok ? __builtin_nanf("") : (L > 0.0f ? 1.0f / L : 0.0f);
                     // one 32-dim slice at a time (registers: the wave's
                     // accumulators already fill its AGPRs)
@@ -610,7 +648,8 @@ __device__ inline float quad16_sum(float v) { return pk::pair32_sum(pk::pair16_s
 template <typename T, typename O, int HD>
 __device__ void fa_tiled16(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
                            const uint16_t *__restrict__ V, typename O::storage *__restrict__ out,
-                           float *__restrict__ pO, float *__restrict__ pML, const TiledFlashAttentionConstants &p) {
+                           float *__restrict__ pO, float *__restrict__ pML, uint64_t *__restrict__ pairFlags,
+                           const TiledFlashAttentionConstants &p) {
     constexpr int KS = HD / 32;   // k-steps of each S^T tile
     constexpr int DT = HD / 16;   // 16-row tiles of O^T
     constexpr int CH = HD / 8;    // 16-byte chunks per K row
@@ -855,7 +894,6 @@ __device__ void fa_tiled16(const uint16_t *__restrict__ Q, const uint16_t *__res
             const uint32_t tile = bh * nSplit + (qt - p.splitFrom);
             const uint32_t rowsTotal = p.B * p.Nq * nSplit * BQ;
             const uint64_t row = (uint64_t)tile * BQ + wave * 16 + c16;
-            void *flag = pML + 2 * (uint64_t)rowsTotal + 2 * (uint64_t)tile;
             const uint64_t ticket = ((uint64_t)p.ticketHi << 32) | p.ticketLo;
             const __amdgpu_buffer_rsrc_t rsO =
                 __builtin_amdgcn_make_buffer_rsrc(pO, 0, (int)(rowsTotal * HD * 4u), 0x00020000);
@@ -869,23 +907,12 @@ __device__ void fa_tiled16(const uint16_t *__restrict__ Q, const uint16_t *__res
                 }
                 __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's stores have completed
                 __syncthreads();
-                if (threadIdx.x == 0) st64c(flag, ticket);
+                if (threadIdx.x == 0) pair_publish(pairFlags, tile, ticket);
             } else {
-                if (threadIdx.x == 0) {
-                    uint32_t ok = 0u;
-                    for (uint32_t i = 0; i < kFlagPolls; ++i) {
-                        if (ld64c(flag) == ticket) {
-                            ok = 1u;
-                            break;
-                        }
-                        __builtin_amdgcn_s_sleep(2);
-                    }
-                    sReady = ok;
-                }
+                if (threadIdx.x == 0) sReady = pair_take(pairFlags, tile, ticket);
                 __syncthreads();
                 asm volatile("" ::: "memory");  // the partner's state is read after the flag
                 const bool ok = sReady != 0u;
-                if (threadIdx.x == 0) st64c(flag, 0u);
                 if (myq < p.Sq) {
                     u32x4 oa[DT];
 #pragma unroll
@@ -897,7 +924,7 @@ __device__ void fa_tiled16(const uint16_t *__restrict__ Q, const uint16_t *__res
                     const float w0 = m0 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m0 - M);
                     const float w1 = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M);
                     const float L = w0 * l0 + w1 * l;
-                    // a flag never seen (the partner never ran) gives NaN rows, not stale data
+                    // a wait that gave up gives NaN rows, not stale data
                     const float inv = !ok ? __builtin_nanf("") : (L > 0.0f ? 1.0f / L : 0.0f);
                     store_out([&](int dt, int i) { return (w0 * __uint_as_float(oa[dt][i]) + w1 * acc[dt][i]) * inv; });
                 }
@@ -963,8 +990,8 @@ __device__ void fa_split_merge(const float *__restrict__ pO, const float *__rest
 #define FA_TILED(name, T, O, HD)                                                                       \
     POPCORN_KERNEL void __launch_bounds__(256)                                                         \
         name(const uint16_t *q, const uint16_t *k, const uint16_t *v, O::storage *out, float *pO,      \
-             float *pML, TiledFlashAttentionConstants p) {                                               \
-        fa_tiled<T, O, HD>(q, k, v, out, pO, pML, p);                                                  \
+             float *pML, uint64_t *pairFlags, TiledFlashAttentionConstants p) {                        \
+        fa_tiled<T, O, HD>(q, k, v, out, pO, pML, pairFlags, p);                                       \
     }
 #define FA_TILED_D(t, T, o, O)                                   \
     FA_TILED(flash_attention_tiled_##t##_##o##_d64, T, O, 64)    \
@@ -973,8 +1000,8 @@ __device__ void fa_split_merge(const float *__restrict__ pO, const float *__rest
 #define FA_TILED16(name, T, O, HD)                                                                     \
     POPCORN_KERNEL void __launch_bounds__(64 * kWaves16)                                               \
         name(const uint16_t *q, const uint16_t *k, const uint16_t *v, O::storage *out, float *pO,      \
-             float *pML, TiledFlashAttentionConstants p) {                                               \
-        fa_tiled16<T, O, HD>(q, k, v, out, pO, pML, p);                                                \
+             float *pML, uint64_t *pairFlags, TiledFlashAttentionConstants p) {                        \
+        fa_tiled16<T, O, HD>(q, k, v, out, pO, pML, pairFlags, p);                                     \
     }
 #define FA_TILED16_D(t, T, o, O)                                      \
     FA_TILED16(flash_attention_tiled16_##t##_##o##_d128, T, O, 128)   \

@@ -5,6 +5,7 @@
 #include <new>
 
 #include "handles.hpp"
+#include "uncached.hpp"
 
 using namespace popcorn;
 
@@ -141,7 +142,10 @@ popcorn_status_t popcorn_device_info(int32_t device, popcorn_device_info_t *info
 }
 
 popcorn_status_t popcorn_device_synchronize(void) {
-    return guarded([&] { checkHip(hipDeviceSynchronize(), "hipDeviceSynchronize"); });
+    return guarded([&] {
+        checkHip(hipDeviceSynchronize(), "hipDeviceSynchronize");
+        checkPairExchange(nullptr, true);
+    });
 }
 
 popcorn_status_t popcorn_malloc(size_t bytes, void **ptr) {
@@ -159,6 +163,21 @@ popcorn_status_t popcorn_malloc(size_t bytes, void **ptr) {
 popcorn_status_t popcorn_free(void *ptr) {
     return guarded([&] {
         if (ptr) checkHip(hipFree(ptr), "hipFree");
+    });
+}
+
+popcorn_status_t popcorn_malloc_uncached(size_t bytes, void **ptr) {
+    return guarded([&] {
+        need(ptr, "ptr");
+        *ptr = nullptr;
+        *ptr = UncachedPool::take(bytes ? bytes : 1);
+    });
+}
+
+popcorn_status_t popcorn_free_uncached(void *ptr) {
+    return guarded([&] {
+        if (ptr && !UncachedPool::give(ptr))
+            throw Error::invalidArgument("popcorn_free_uncached: the pointer was not returned by popcorn_malloc_uncached");
     });
 }
 
@@ -207,7 +226,20 @@ popcorn_status_t popcorn_stream_destroy(popcorn_stream_t stream) {
     });
 }
 popcorn_status_t popcorn_stream_synchronize(popcorn_stream_t stream) {
-    return guarded([&] { checkHip(hipStreamSynchronize(S(stream)), "hipStreamSynchronize"); });
+    return guarded([&] {
+        checkHip(hipStreamSynchronize(S(stream)), "hipStreamSynchronize");
+        checkPairExchange(S(stream));
+    });
+}
+
+popcorn_status_t popcorn_attention_pair_flags(popcorn_stream_t stream, void **flags, int32_t *count) {
+    return guarded([&] {
+        need(flags, "flags");
+        need(count, "count");
+        const PairExchange &x = pairExchange(S(stream), 0);
+        *flags = x.flags;
+        *count = (int32_t)PairExchange::kFlags;
+    });
 }
 
 popcorn_status_t popcorn_event_create(popcorn_event_t *event) {

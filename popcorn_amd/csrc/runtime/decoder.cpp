@@ -7,7 +7,6 @@
 #include <mutex>
 #include <set>
 
-#include "decode_layers_geometry.hpp"
 #include "handles.hpp"
 #include "popcorn_decoder.h"
 
@@ -39,61 +38,6 @@ struct Buffer {
     }
     template <typename T = uint8_t>
     T *at(size_t byteOffset) const { return reinterpret_cast<T *>(static_cast<uint8_t *>(p) + byteOffset); }
-};
-
-// Uncached device memory (hipDeviceMallocUncached: every access goes to
-// memory, past the per-XCD L2 caches) for the words the persistent layer
-// kernel's blocks exchange within a launch. Such memory is never freed once a
-// kernel has read it: a block a decoder gives back goes to a process-wide
-// pool, keyed by device and size, and the next decoder of that shape reuses
-// it.
-class UncachedBlock {
-public:
-    UncachedBlock() = default;
-    explicit UncachedBlock(size_t bytes) : bytes_(bytes) {
-        checkHip(hipGetDevice(&dev_), "hipGetDevice");
-        std::lock_guard<std::mutex> g(mu());
-        auto &pool = free_()[{dev_, bytes}];
-        if (!pool.empty()) {
-            p = pool.back();
-            pool.pop_back();
-            return;
-        }
-        if (hipExtMallocWithFlags(&p, bytes ? bytes : 1, hipDeviceMallocUncached) != hipSuccess) {
-            (void)hipGetLastError();
-            p = nullptr;
-            throw Error::tensorAllocationFailed(bytes);
-        }
-    }
-    UncachedBlock(const UncachedBlock &) = delete;
-    UncachedBlock &operator=(const UncachedBlock &) = delete;
-    UncachedBlock &operator=(UncachedBlock &&o) noexcept {
-        std::swap(p, o.p);
-        std::swap(bytes_, o.bytes_);
-        std::swap(dev_, o.dev_);
-        return *this;
-    }
-    ~UncachedBlock() {
-        if (!p) return;
-        std::lock_guard<std::mutex> g(mu());
-        free_()[{dev_, bytes_}].push_back(p);
-    }
-    size_t bytes() const { return bytes_; }
-    template <typename T = uint8_t>
-    T *at(size_t byteOffset) const { return reinterpret_cast<T *>(static_cast<uint8_t *>(p) + byteOffset); }
-    void *p = nullptr;
-
-private:
-    size_t bytes_ = 0;
-    int dev_ = 0;
-    static std::mutex &mu() {
-        static std::mutex m;
-        return m;
-    }
-    static std::map<std::pair<int, size_t>, std::vector<void *>> &free_() {
-        static auto *pool = new std::map<std::pair<int, size_t>, std::vector<void *>>();  // lives to process exit
-        return *pool;
-    }
 };
 
 // `count` stacked [N, K] block-affine 4-bit matrices (group 64, bf16 scales
@@ -155,16 +99,6 @@ struct popcorn_decoder_s {
     std::vector<std::unique_ptr<Kernel>> prime, step;
     std::vector<std::string> names;
 
-    // fused_layers: the persistent layer kernel (decode_layers.hip), its
-    // sync words, tagged activation workspace and (for phase_times) per-block stamps
-    bool fused = false;
-    std::string layersFn;
-    unsigned layersGrid = 0;
-    size_t layersLds = 0;
-    int64_t fdParts = 0;
-    UncachedBlock syncWords, tagged;
-    Buffer stamps;
-    std::unique_ptr<Kernel> layersTimed;  // the same launch with stamps on
     hipGraphExec_t graph = nullptr;
     hipGraph_t graphDef = nullptr;
     int graphSteps = 1;
@@ -224,69 +158,6 @@ struct popcorn_decoder_s {
         throw Error::invalidArgument(std::string("unknown decoder tensor ") + which);
     }
 
-    // Chooses the persistent layer kernel when the configuration asks for it
-    // and the shape has a compiled kernel that fits one block per CU.
-    void setupFused() {
-        namespace LY = pk::layers;
-        if (!cfg.fused_layers || q4 || cfg.attention_block || Nq % Nkv != 0) return;
-        const int64_t G = Nq / Nkv;
-        if (!LY::compiled((int)Hd, (int)G) || H % 8 != 0 || F % 8 != 0) return;
-        if (H > LY::kMaxStaged || QW > LY::kMaxStaged) return;  // the staging wave's vectors
-        if (H % 256 != 0) return;                                 // norm weights copied in 1 KB pieces
-        int dev = 0, cus = 0, maxLds = 0;
-        checkHip(hipGetDevice(&dev), "hipGetDevice");
-        checkHip(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "hipDeviceGetAttribute");
-        checkHip(hipDeviceGetAttribute(&maxLds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev), "hipDeviceGetAttribute");
-        if (cus < 1 || Nkv > cus) return;
-        const size_t lds = LY::ldsLayout((uint32_t)H, (uint32_t)QW, (uint32_t)F, (uint32_t)G, (uint32_t)Hd).bytes;
-        const std::string fn = "decode_layers_bf16_h" + std::to_string(Hd) + "_g" + std::to_string(G);
-        const Function &f = lib->function(fn);
-        if (lds + (size_t)f.attrs.staticLds > (size_t)maxLds) return;
-        int perCU = 0;
-        if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&perCU, f.fn, LY::kThreads, lds) != hipSuccess) {
-            (void)hipGetLastError();
-            return;
-        }
-        // every block must be resident at once: the kernel's waits need all of them
-        if (perCU < 1) return;
-        fdParts = std::min<int64_t>(LY::kMaxPartitions, cus / Nkv);
-        // sync words: done 0, abort 0, epoch 1; tagged words start with tag
-        // 0xffff, which the first launches never expect
-        syncWords = UncachedBlock(LY::kSyncBytes);
-        std::vector<uint32_t> words(LY::kSyncBytes / 4, 0u);
-        words[LY::kEpochWord] = 1u;
-        checkHip(hipMemcpy(syncWords.p, words.data(), LY::kSyncBytes, hipMemcpyHostToDevice), "init sync words");
-        tagged = UncachedBlock((size_t)LY::taggedLayout((uint32_t)H, (uint32_t)Nq, (uint32_t)Nkv, (uint32_t)Hd,
-                                                        (uint32_t)F, (uint32_t)fdParts).bytes);
-        checkHip(hipMemset(tagged.p, 0xff, tagged.bytes()), "memset");
-        layersFn = fn;
-        layersGrid = (unsigned)cus;
-        layersLds = lds;
-        fused = true;
-    }
-
-    std::unique_ptr<Kernel> layersKernel(void *stampBuffer) {
-        Tensor tx = bf(x.p, {H}), tx2 = bf(x2.p, {H});
-        Tensor tq = bf(qkv.p, {QKV}), tattn = bf(attn.p, {QW}), to = bf(o.p, {H}), th = bf(hidden.p, {F});
-        Tensor tmlp = bf(mlp.p, {H});
-        Tensor tpos(position.p, Shape({1}), DataType::i32);
-        Tensor tnorms(norms.p, Shape({L, 4, H}), DataType::f32);
-        Tensor tkc = bf(kcache.p, {L, Nkv, S, Hd}), tvc = bf(vcache.p, {L, Nkv, S, Hd});
-        Tensor ttag(tagged.p, Shape({(int64_t)tagged.bytes()}), DataType::u8);
-        Tensor tsync(syncWords.p, Shape({(int64_t)(syncWords.bytes() / 4)}), DataType::u32);
-        Tensor tstamps(stampBuffer, Shape({stampBuffer ? (int64_t)(stamps.bytes / 8) : 0}), DataType::u64);
-        DecodeLayersConstants c{(uint32_t)L, (uint32_t)H, (uint32_t)Nq, (uint32_t)Nkv, (uint32_t)Hd, (uint32_t)F,
-                                (uint32_t)S, (uint32_t)fdParts, cfg.eps, cfg.attn_scale, 0u, 0u};
-        return Kernels::Custom(layersFn,
-                               {{tx, kRead}, {bf(wqkv.p, {L, QKV, H}), kRead}, {bf(wo.p, {L, H, QW}), kRead},
-                                {bf(wg.p, {L, F, H}), kRead}, {bf(wu.p, {L, F, H}), kRead},
-                                {bf(wd.p, {L, H, F}), kRead}, {tnorms, kRead}, {tkc, kReadWrite},
-                                {tvc, kReadWrite}, {tpos, kRead}, {tq, kWrite}, {tattn, kWrite}, {to, kWrite},
-                                {th, kWrite}, {tmlp, kWrite}, {tx2, kWrite}, {ttag, kReadWrite},
-                                {tsync, kReadWrite}, {tstamps, kReadWrite}},
-                               {bytesOf(c)}, dim3(layersGrid, 1, 1), dim3(pk::layers::kThreads, 1, 1), layersLds);
-    }
-
     // Six dispatches per layer: the QKV matvec (previous layer's post-FFN
     // norm + residual, this layer's input norm, K/V scattered into the caches),
     // split-KV attention with its combine, the O projection, the gate/up
@@ -318,11 +189,7 @@ struct popcorn_decoder_s {
         prime.push_back(Kernels::ScalarMul(te, std::sqrt((float)H), tx));
         const AttentionMask causal{0, -1};
         Tensor prevPostFfn;
-        if (fused) {
-            add(layersKernel(nullptr));
-            prevPostFfn = weight("norm_post_ffn", L - 1);
-        }
-        for (int64_t l = 0; l < (fused ? 0 : L); ++l) {
+        for (int64_t l = 0; l < L; ++l) {
             Tensor nin = weight("norm_in", l), npa = weight("norm_post_attn", l);
             Tensor npf = weight("norm_pre_ffn", l), npo = weight("norm_post_ffn", l);
             Tensor kc = weight("k_cache", l), vc = weight("v_cache", l);
@@ -487,23 +354,6 @@ struct popcorn_decoder_s {
         for (; i < steps; ++i) encodeStep();
     }
 
-    // A grid-wide wait of the persistent kernel that ran out of time leaves
-    // the abort word set (the launch then finished without waiting): report
-    // it once and clear the sync words for the next launch.
-    void checkAbort() {
-        if (!fused) return;
-        uint32_t abortWord = 0;
-        checkHip(hipMemcpy(&abortWord, syncWords.at<uint32_t>(pk::layers::kAbortWord * 4), 4, hipMemcpyDeviceToHost),
-                 "read abort word");
-        if (abortWord != 0) {
-            const uint32_t zero = 0;
-            checkHip(hipMemcpy(syncWords.at<uint32_t>(pk::layers::kAbortWord * 4), &zero, 4, hipMemcpyHostToDevice),
-                     "clear abort word");
-            throw Error(POPCORN_ERR_GPU_INTERNAL,
-                        "decode layers: a grid-wide wait timed out (not every block was resident); the step's results are invalid");
-        }
-    }
-
     int64_t stepBytes(int32_t pos) const {
         // bytes per weight: 2 (bf16), or 1/2 + 2 x 2 / 64 (4-bit values, bf16 scale and bias per 64)
         auto wbytes = [&](int64_t elems) { return q4 ? elems / 2 + elems / 16 : elems * 2; };
@@ -608,7 +458,6 @@ popcorn_status_t popcorn_decoder_create(popcorn_library_t library, popcorn_strea
         checkHip(hipMemsetAsync(d->position.p, 0, 4, d->stream), "memset");
         checkHip(hipMemsetAsync(d->history.p, 0xff, d->history.bytes, d->stream), "memset");
         d->enc = std::make_unique<KernelCommandEncoder>(*d->lib, d->stream, d->pool);
-        d->setupFused();
         d->build();
         *decoder = d.release();
     });
@@ -675,10 +524,6 @@ popcorn_status_t popcorn_decoder_tensor(popcorn_decoder_t d, const char *name, i
         else if (n == "token") t = Tensor(d->token.p, Shape({1}), DataType::i32);
         else if (n == "position") t = Tensor(d->position.p, Shape({1}), DataType::i32);
         else if (n == "history") t = Tensor(d->history.p, Shape({std::max(d->cfg.history_len, 1)}), DataType::i32);
-        else if (n == "layer_sync" && d->syncWords.p)
-            t = Tensor(d->syncWords.p, Shape({(int64_t)(d->syncWords.bytes() / 4)}), DataType::u32);
-        else if (n == "layer_stamps" && d->stamps.p)
-            t = Tensor(d->stamps.p, Shape({(int64_t)d->layersGrid, (int64_t)pk::layers::kStampsPerBlock}), DataType::u64);
         else {
             if (layer < 0 || layer >= d->L) throw Error::invalidArgument("layer out of range");
             t = d->weight(name, layer);
@@ -720,7 +565,6 @@ popcorn_status_t popcorn_decoder_read(popcorn_decoder_t d, int32_t *token, int32
         if (token) *token = v[0];
         if (position) *position = v[1];
         d->hostPos = v[1];
-        d->checkAbort();
     });
 }
 
@@ -808,50 +652,6 @@ popcorn_status_t popcorn_decoder_time_kernel(popcorn_decoder_t d, const char *fu
         checkHip(hipEventElapsedTime(&ms, a, b), "hipEventElapsedTime");
         *mean_ms = ms / (float)(per * reps);
         if (launches) *launches = per * reps;
-    });
-}
-
-popcorn_status_t popcorn_decoder_phase_times(popcorn_decoder_t d, int32_t steps, float *phase_us) {
-    return guardedDec([&] {
-        namespace LY = pk::layers;
-        if (!d || !phase_us) throw Error::invalidArgument("decoder and phase_us must not be NULL");
-        if (!d->fused) throw Error::invalidArgument("the decoder does not run the persistent layer kernel");
-        if (steps <= 0 || steps > 16) throw Error::invalidArgument("steps must be in 1..16");
-        if (d->hostPos < 0 || d->hostPos + steps > d->S)
-            throw Error::tensorShapeMismatch("timed steps would leave the KV cache");
-        const size_t per = (size_t)LY::kStampsPerBlock, blocks = d->layersGrid;
-        if (!d->stamps.p) d->stamps = Buffer(blocks * per * 8);
-        if (!d->layersTimed) d->layersTimed = d->layersKernel(d->stamps.p);
-        std::swap(d->step[0], d->layersTimed);  // the stamped launch in the step's place
-        struct Swap {
-            popcorn_decoder_s *d;
-            ~Swap() { std::swap(d->step[0], d->layersTimed); }
-        } swapBack{d};
-        const size_t bars = (size_t)(LY::kBarriersPerLayer * d->L);
-        std::vector<uint64_t> host(blocks * per);
-        double sum[6] = {0, 0, 0, 0, 0, 0};
-        int count[6] = {0, 0, 0, 0, 0, 0};
-        for (int32_t i = 0; i < steps; ++i) {
-            checkHip(hipMemsetAsync(d->stamps.p, 0, d->stamps.bytes, d->stream), "memset");
-            d->run(1, false);
-            checkHip(hipMemcpyAsync(host.data(), d->stamps.p, host.size() * 8, hipMemcpyDeviceToHost, d->stream),
-                     "read stamps");
-            checkHip(hipStreamSynchronize(d->stream), "sync");
-            d->checkAbort();
-            // barrier k of a layer opens interval k % 6, which lasts until the
-            // next barrier's last release
-            uint64_t prev = 0;
-            for (size_t k = 0; k < bars && k < per; ++k) {
-                uint64_t rel = 0;
-                for (size_t b = 0; b < blocks; ++b) rel = std::max(rel, host[b * per + k]);
-                if (k > 0 && rel > prev) {
-                    sum[(k - 1) % 6] += (double)(rel - prev) * 0.01;  // 100 MHz ticks -> us
-                    count[(k - 1) % 6] += 1;
-                }
-                prev = rel;
-            }
-        }
-        for (int p = 0; p < 6; ++p) phase_us[p] = count[p] ? (float)(sum[p] / count[p]) : 0.0f;
     });
 }
 

@@ -6,8 +6,11 @@
 #include <chrono>
 #include <cstdlib>
 #include <cstring>
+#include <map>
+#include <mutex>
 
 #include "popcorn.hpp"
+#include "uncached.hpp"
 
 namespace popcorn {
 namespace {
@@ -229,28 +232,31 @@ public:
             if (!nSplit_) {
                 // no split tile: the partial-state arguments are never touched
                 FixedDispatch fa(tiledName_,
-                                 {{q_, kRead}, {k_, kRead}, {v_, kRead}, {out_, kWrite}, {q_, kRead}, {q_, kRead}},
+                                 {{q_, kRead}, {k_, kRead}, {v_, kRead}, {out_, kWrite}, {q_, kRead}, {q_, kRead},
+                                  {q_, kRead}},
                                  {bytesOf(c)}, grid1(items, tiledBlock()));
                 enc.dispatch(fa);
                 return;
             }
             if (mergedPairs()) {
-                // the published part of each split tile: unnormalised O, then
-                // (m, l) per row and a 64-bit ready flag per tile; the second
-                // block of each pair merges, so no merge kernel
+                // the published part of each split tile (unnormalised O, then
+                // (m, l) per row) and its ready flag, in the stream's
+                // uncached pair exchange; the second block of each pair
+                // merges, so no merge kernel
                 const int64_t tiles = d_.B * d_.Nq * nSplit_;
+                const size_t oBytes = (size_t)(tiles * 128 * d_.Hd) * 4;
+                const PairExchange &x = pairExchange(enc.stream(), oBytes + (size_t)(tiles * 128 * 2) * 4);
                 const uint64_t ticket = nextTicket();
                 c.ticketLo = (uint32_t)ticket;
                 c.ticketHi = (uint32_t)(ticket >> 32);
-                enc.withTemporaryTensor(ScratchSpec{{tiles * 128, d_.Hd}, DataType::f32}, [&](Tensor pO) {
-                    enc.withTemporaryTensor(ScratchSpec{{tiles * 128 * 2 + tiles * 2}, DataType::f32}, [&](Tensor pML) {
-                        FixedDispatch fa(tiledName_,
-                                         {{q_, kRead}, {k_, kRead}, {v_, kRead}, {out_, kWrite}, {pO, kReadWrite},
-                                          {pML, kReadWrite}},
-                                         {bytesOf(c)}, grid1(items, tiledBlock()));
-                        enc.dispatch(fa);
-                    });
-                });
+                Tensor pO(x.data, Shape({tiles * 128, d_.Hd}), DataType::f32);
+                Tensor pML(static_cast<uint8_t *>(x.data) + oBytes, Shape({tiles * 128 * 2}), DataType::f32);
+                Tensor flags(x.flags, Shape({(int64_t)PairExchange::kFlags}), DataType::u64);
+                FixedDispatch fa(tiledName_,
+                                 {{q_, kRead}, {k_, kRead}, {v_, kRead}, {out_, kWrite}, {pO, kReadWrite},
+                                  {pML, kReadWrite}, {flags, kReadWrite}},
+                                 {bytesOf(c)}, grid1(items, tiledBlock()));
+                enc.dispatch(fa);
                 return;
             }
             // the two parts of each split tile: unnormalised O, then (m, l) per row
@@ -258,7 +264,8 @@ public:
             enc.withTemporaryTensor(ScratchSpec{{rows, d_.Hd}, DataType::f32}, [&](Tensor pO) {
                 enc.withTemporaryTensor(ScratchSpec{{rows, 2}, DataType::f32}, [&](Tensor pML) {
                     FixedDispatch fa(tiledName_,
-                                     {{q_, kRead}, {k_, kRead}, {v_, kRead}, {out_, kWrite}, {pO, kWrite}, {pML, kWrite}},
+                                     {{q_, kRead}, {k_, kRead}, {v_, kRead}, {out_, kWrite}, {pO, kWrite}, {pML, kWrite},
+                                      {q_, kRead}},
                                      {bytesOf(c)}, grid1(items, tiledBlock()));
                     enc.dispatch(fa);
                     // one block per 16 rows of a split tile
@@ -371,6 +378,8 @@ private:
             const int64_t x = (sa + sb + 1) / 2 - sa;
             pairs = x >= 1 && x < sb;
         }
+        // one ready flag per split tile in the stream's pair exchange
+        pairs = pairs && d_.B * d_.Nq * (nQT / 2) < (int64_t)PairExchange::kFlags;
         if (pairs) {
             pairTiles_ = true;
             nSplit_ = nQT / 2;
@@ -407,7 +416,7 @@ private:
     // Paired tiles are merged inside the tiled kernels (pairTiles 2).
     bool pairMergeInKernel_ = true;
     bool mergedPairs() const { return pairTiles_ && pairMergeInKernel_; }
-    // A 64-bit value, never 0 and distinct per launch, for the ready flags
+    // A 64-bit value, never 0 or ~0 and distinct per launch, for the ready flags
     // of merged pairs: a counter, started from the clock so that processes
     // differ, through the splitmix64 finaliser.
     static uint64_t nextTicket() {
@@ -417,7 +426,7 @@ private:
             z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
             z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
             z ^= z >> 31;
-            if (z != 0) return z;
+            if (z != 0 && z != ~0ull) return z;
         }
     }
     int64_t ngroups_ = 1, P_ = 1;
@@ -1727,4 +1736,74 @@ std::unique_ptr<Kernel> FillNormal(void *data, DataType dtype, uint64_t count, u
 }
 
 }  // namespace Kernels
+}  // namespace popcorn
+
+// ---------------------------------------------------------------------------
+// The merged-pair exchange of the tiled prefill attention, per stream
+// ---------------------------------------------------------------------------
+
+namespace popcorn {
+namespace {
+
+struct PairExchangeRegistry {
+    std::mutex mu;
+    std::map<std::pair<int, hipStream_t>, PairExchange> byStream;
+};
+PairExchangeRegistry &pairRegistry() {
+    static auto *r = new PairExchangeRegistry();  // lives to process exit, as the memory does
+    return *r;
+}
+
+size_t roundUpPow2(size_t n) {
+    size_t p = 1 << 20;
+    while (p < n) p <<= 1;
+    return p;
+}
+
+// Reads the abort word; when set, clears every flag and throws -1019.
+void checkOne(const PairExchange &x) {
+    uint64_t abortWord = 0;
+    checkHip(hipMemcpy(&abortWord, x.flags, 8, hipMemcpyDeviceToHost), "read the pair exchange's abort word");
+    if (abortWord == 0) return;
+    checkHip(hipMemset(x.flags, 0, PairExchange::kFlags * 8), "clear the pair exchange's flags");
+    throw Error(POPCORN_ERR_GPU_INTERNAL,
+                "FlashAttention: a merged causal tile pair's ready-flag wait gave up (0.2 s, or a flag left by a "
+                "launch that gave up before); the affected output rows hold NaN. The flags have been cleared.");
+}
+
+}  // namespace
+
+PairExchange &pairExchange(hipStream_t stream, size_t dataBytes) {
+    int dev = 0;
+    checkHip(hipGetDevice(&dev), "hipGetDevice");
+    auto &r = pairRegistry();
+    std::lock_guard<std::mutex> g(r.mu);
+    PairExchange &x = r.byStream[{dev, stream}];
+    if (!x.flags) {
+        x.flags = static_cast<uint64_t *>(UncachedPool::take(PairExchange::kFlags * 8));
+        x.dev = dev;
+        checkHip(hipMemset(x.flags, 0, PairExchange::kFlags * 8), "zero the pair exchange's flags");
+    }
+    if (x.dataBytes < dataBytes) {
+        // the old block stays reserved: a graph captured with it still uses it
+        const size_t n = roundUpPow2(dataBytes);
+        x.data = UncachedPool::take(n);
+        x.dataBytes = n;
+    }
+    return x;
+}
+
+void checkPairExchange(hipStream_t stream, bool allStreams) {
+    int dev = 0;
+    checkHip(hipGetDevice(&dev), "hipGetDevice");
+    auto &r = pairRegistry();
+    std::vector<PairExchange> todo;
+    {
+        std::lock_guard<std::mutex> g(r.mu);
+        for (auto &kv : r.byStream)
+            if (kv.first.first == dev && (allStreams || kv.first.second == stream)) todo.push_back(kv.second);
+    }
+    for (const PairExchange &x : todo) checkOne(x);
+}
+
 }  // namespace popcorn

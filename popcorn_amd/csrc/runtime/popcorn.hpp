@@ -452,6 +452,27 @@ void FlashDecodingNoAlloc(KernelLibrary &library, hipStream_t stream, const Tens
 // and its size in bytes; looked up once per device.
 void *staticScratch(size_t *bytes);
 
+// The exchange of the tiled prefill attention's merged pairs on one stream
+// (flash_attention_tiled.hip, pairTiles 2), in uncached device memory that
+// is never freed: `data` holds the published partial O and (m, l) rows
+// (grown on demand; a grown-out block stays reserved for graphs captured
+// with it), `flags` the abort word and one ready flag per split tile, zeroed
+// once at creation.
+struct PairExchange {
+    static constexpr size_t kFlags = 4097;  // abort word + 4096 tiles
+    void *data = nullptr;
+    size_t dataBytes = 0;
+    uint64_t *flags = nullptr;
+    int dev = 0;
+};
+// The exchange of `stream` on the current device with at least `dataBytes`
+// of data.
+PairExchange &pairExchange(hipStream_t stream, size_t dataBytes);
+// After `stream` has drained (or, with stream == nullptr and allStreams,
+// every stream of the current device): throws -1019 when a merged pair's
+// wait gave up since the last check, clearing that exchange's flags first.
+void checkPairExchange(hipStream_t stream, bool allStreams = false);
+
 // Thread-local message of the last failure reported through the C ABI.
 void setLastError(const std::string &message);
 const char *lastError();

@@ -29,7 +29,6 @@ class DecoderConfig:
     attention_block: int = 0      # 1: per-head q/k/v RMSNorm and RoPE (a real attention block)
     rope_theta: float = 10000.0
     weight_bits: int = 16         # 4: block-affine 4-bit weights (group 64, bf16 scales and biases)
-    fused_layers: int = 0         # 1: the layers as one persistent kernel per step where the shape allows
 
     def c(self) -> _capi.DecoderConfig:
         return _capi.DecoderConfig(*[getattr(self, f.name) for f in fields(self)])
@@ -87,18 +86,6 @@ class Decoder:
         check(lib().popcorn_decoder_time_kernel_in_step(self.handle, function_name.encode(), steps, C.byref(ms),
                                                         C.byref(n)))
         return ms.value, n.value
-
-    def phase_times(self, steps: int = 4):
-        """Mean microseconds of the persistent layer kernel's six intervals per layer
-        (QKV, attention partials + combine, O, gate/up, fetching hidden, down) over
-        `steps` eager steps (advances the position)."""
-        out = (C.c_float * 6)()
-        check(lib().popcorn_decoder_phase_times(self.handle, steps, out))
-        return [float(v) for v in out]
-
-    @property
-    def fused(self) -> bool:
-        return self.describe()[0][0].startswith("decode_layers_")
 
     def time_kernel(self, function_name: str, reps: int = 5):
         """(mean ms per launch, launches) of one kernel of the step, launched alone."""

@@ -145,6 +145,33 @@ class DeviceBuffer:
             pass
 
 
+class UncachedBuffer:
+    """Uncached device memory (popcorn_malloc_uncached): every access goes to
+    memory, past the per-XCD L2 caches. Given back to the library's pool,
+    never to the driver."""
+
+    def __init__(self, nbytes: int):
+        p = C.c_void_p()
+        check(lib().popcorn_malloc_uncached(max(int(nbytes), 1), C.byref(p)))
+        self.ptr = p.value
+        self.nbytes = int(nbytes)
+
+    def __del__(self):
+        try:
+            if self.ptr:
+                lib().popcorn_free_uncached(self.ptr)
+        except Exception:
+            pass
+
+
+def attention_pair_flags(stream: Optional["Stream"] = None) -> "Tensor":
+    """The ready flags of the tiled prefill attention's merged pairs on
+    `stream` (u64: the abort word, then one flag per split tile)."""
+    p, n = C.c_void_p(), C.c_int32()
+    check(lib().popcorn_attention_pair_flags(_stream_handle(stream), C.byref(p), C.byref(n)))
+    return Tensor(p.value, [n.value], "u64")
+
+
 # ---- tensors (Tensor.swift) ----------------------------------------------------
 
 _NP = {"f32": np.float32, "f16": np.float16, "bf16": np.uint16, "i32": np.int32, "u8": np.uint8,
@@ -185,6 +212,12 @@ class Tensor:
     def empty(cls, shape: Sequence[int], dtype: str = "f32") -> "Tensor":
         n = int(np.prod(shape)) if len(shape) else 1
         buf = DeviceBuffer(n * stride(dtype))
+        return cls(buf.ptr, shape, dtype, owner=buf)
+
+    @classmethod
+    def empty_uncached(cls, shape: Sequence[int], dtype: str = "f32") -> "Tensor":
+        n = int(np.prod(shape)) if len(shape) else 1
+        buf = UncachedBuffer(n * stride(dtype))
         return cls(buf.ptr, shape, dtype, owner=buf)
 
     @classmethod

@@ -18,19 +18,10 @@ def env():
     return gpu_env()
 
 
-def _small(pa_dec, graph_steps=1, attention_block=0, weight_bits=16, fused=0, heads=(4, 2), head_dim=64):
+def _small(pa_dec, graph_steps=1, attention_block=0, weight_bits=16, heads=(4, 2), head_dim=64):
     return pa_dec.DecoderConfig(layers=2, hidden=256, query_heads=heads[0], kv_heads=heads[1], head_dim=head_dim,
                                 ffn=512, vocab=1000, max_seq=64, eps=1e-6, attn_scale=0.125, history_len=64,
-                                graph_steps=graph_steps, attention_block=attention_block, weight_bits=weight_bits,
-                                fused_layers=fused)
-
-
-def _check_fused(dec, fused):
-    """The decoder runs the persistent layer kernel exactly when asked to."""
-    names, n = dec.describe()
-    assert names[0].startswith("decode_layers_bf16_") == bool(fused), names[:3]
-    if fused:  # the layers, then the head's matvec, argmax and next-token kernels
-        assert n == 4 and names[1].startswith("decode_matvec_bf16_f32_") and names[2] == "argmax_partial", names
+                                graph_steps=graph_steps, attention_block=attention_block, weight_bits=weight_bits)
 
 
 def _weight(dec, name, layer, stream):
@@ -69,11 +60,10 @@ def _oracle_step(dec, cfg, caches, token, pos, stream, act=O.BF16):
     return O.matmul(n, emb, 1, cfg.hidden, cfg.vocab, True).ravel()
 
 
-@pytest.mark.parametrize("attention_block,weight_bits,fused,heads,head_dim",
-                         [(0, 16, 0, (4, 2), 64), (1, 16, 0, (4, 2), 64), (0, 4, 0, (4, 2), 64), (1, 4, 0, (4, 2), 64),
-                          (0, 16, 1, (4, 2), 64), (0, 16, 1, (8, 2), 64), (0, 16, 1, (4, 2), 128),
-                          (0, 16, 1, (2, 2), 256), (0, 16, 1, (4, 2), 256)])
-def test_small_decoder_matches_oracle(env, attention_block, weight_bits, fused, heads, head_dim):
+@pytest.mark.parametrize("attention_block,weight_bits,heads,head_dim",
+                         [(0, 16, (4, 2), 64), (1, 16, (4, 2), 64), (0, 4, (4, 2), 64), (1, 4, (4, 2), 64),
+                          (0, 16, (8, 2), 64), (0, 16, (4, 2), 128), (0, 16, (2, 2), 256), (0, 16, (4, 2), 256)])
+def test_small_decoder_matches_oracle(env, attention_block, weight_bits, heads, head_dim):
     # The decode step is a composition of ~10 bf16-stored stages per layer;
     # each stage is pinned to 2e-3 by the kernel tests. Composed, a GPU sum
     # that lands on the other side of a bf16 rounding midpoint than the
@@ -85,10 +75,8 @@ def test_small_decoder_matches_oracle(env, attention_block, weight_bits, fused, 
     pa, lib, stream, enc = env
     import popcorn_amd.decoder as D
 
-    cfg = _small(D, attention_block=attention_block, weight_bits=weight_bits, fused=fused, heads=heads,
-                 head_dim=head_dim)
+    cfg = _small(D, attention_block=attention_block, weight_bits=weight_bits, heads=heads, head_dim=head_dim)
     dec = D.Decoder(lib, stream, cfg)
-    _check_fused(dec, fused)
     dec.randomize(seed=1)
     if attention_block:  # inv_freq of theta 10000 (Gemma4Workspace.swift:195-197)
         inv = np.array([1 / 10000.0 ** (2 * i / cfg.head_dim) for i in range(cfg.head_dim // 2)], np.float32)
@@ -126,16 +114,14 @@ def test_small_decoder_matches_oracle(env, attention_block, weight_bits, fused, 
     dec.close()
 
 
-@pytest.mark.parametrize("graph_steps,steps,attention_block,weight_bits,fused",
-                         [(1, 5, 0, 16, 0), (3, 7, 0, 16, 0), (3, 7, 1, 16, 0), (3, 7, 1, 4, 0), (1, 5, 0, 16, 1),
-                          (3, 7, 0, 16, 1)])
-def test_graph_replay_equals_eager(env, graph_steps, steps, attention_block, weight_bits, fused):
+@pytest.mark.parametrize("graph_steps,steps,attention_block,weight_bits",
+                         [(1, 5, 0, 16), (3, 7, 0, 16), (3, 7, 1, 16), (3, 7, 1, 4)])
+def test_graph_replay_equals_eager(env, graph_steps, steps, attention_block, weight_bits):
     pa, lib, stream, enc = env
     import popcorn_amd.decoder as D
 
-    cfg = _small(D, graph_steps, attention_block, weight_bits, fused)
+    cfg = _small(D, graph_steps, attention_block, weight_bits)
     dec = D.Decoder(lib, stream, cfg)
-    _check_fused(dec, fused)
     dec.randomize(seed=2)
     k0 = [dec.tensor("k_cache", l).numpy(stream) for l in range(cfg.layers)]
     v0 = [dec.tensor("v_cache", l).numpy(stream) for l in range(cfg.layers)]
@@ -162,8 +148,8 @@ def test_graph_replay_equals_eager(env, graph_steps, steps, attention_block, wei
     dec.close()
 
 
-@pytest.mark.parametrize("attention_block,weight_bits,fused", [(0, 16, 0), (1, 16, 0), (0, 4, 0), (0, 16, 1)])
-def test_gemma2_2b_shape_decodes(env, attention_block, weight_bits, fused):
+@pytest.mark.parametrize("attention_block,weight_bits", [(0, 16), (1, 16), (0, 4)])
+def test_gemma2_2b_shape_decodes(env, attention_block, weight_bits):
     # BASELINE config 4 shape at full size: 26 layers, H 2304, 8/4 heads of
     # 256, FFN 9216, vocab 256000, context 4096 -> 4352; random weights;
     # attention_block adds the per-head norms and RoPE of a real block,
@@ -171,15 +157,13 @@ def test_gemma2_2b_shape_decodes(env, attention_block, weight_bits, fused):
     pa, lib, stream, enc = env
     import popcorn_amd.decoder as D
 
-    cfg = D.DecoderConfig(graph_steps=4, attention_block=attention_block, weight_bits=weight_bits,
-                          fused_layers=fused)
+    cfg = D.DecoderConfig(graph_steps=4, attention_block=attention_block, weight_bits=weight_bits)
     dec = D.Decoder(lib, stream, cfg)
-    _check_fused(dec, fused)
     dec.randomize(seed=0)
     names, n = dec.describe()
     assert n == len(names)
     assert any(m.startswith("q4_gate_up_bf16_l") and m.endswith("_res") for m in names) if weight_bits == 4 \
-        else ("decode_layers_bf16_h256_g2" in names) if fused else "gated_mlp_gate_up_bf16_r1_res" in names
+        else "gated_mlp_gate_up_bf16_r1_res" in names
     assert any(m.startswith("flash_decoding_fresh_") for m in names) == bool(attention_block)
     dec.reset(123, 4096)
     dec.step(8, use_graph=True)
@@ -195,10 +179,6 @@ def test_gemma2_2b_shape_decodes(env, attention_block, weight_bits, fused):
     np.testing.assert_array_equal(dec.history(4096, 8), hist)
     np.testing.assert_array_equal(dec.tensor("logits").numpy(stream), logits)
     assert dec.step_bytes(4096) > (5.0e9 if weight_bits == 16 else 1.4e9)
-    if fused:  # the persistent kernel's phase times (QKV, attention, combine, O, gate/up, down)
-        ph = dec.phase_times(2)
-        assert len(ph) == 6 and all(0 < p < 1000 for p in ph), ph
-        assert dec.read()[1] == 4104 + 2
     dec.close()
 
 
@@ -207,8 +187,7 @@ LAYER_WEIGHTS = [("in_norm", "norm_in"), ("qkv", "w_qkv"), ("o", "w_o"), ("post_
                  ("post_ffn_norm", "norm_post_ffn")]
 
 
-@pytest.mark.parametrize("fused", [0, 1])
-def test_gemma2_2b_step_matches_oracle(env, fused):
+def test_gemma2_2b_step_matches_oracle(env):
     # BASELINE config 4 at full size, one greedy step at position 4096 on the
     # decoder's own random weights, against the oracle's composition of the
     # reference's step (Gemma4TextInference.swift:184-206, :312-436), run
@@ -230,9 +209,8 @@ def test_gemma2_2b_step_matches_oracle(env, fused):
     pa, lib, stream, enc = env
     import popcorn_amd.decoder as D
 
-    cfg = D.DecoderConfig(graph_steps=1, fused_layers=fused)
+    cfg = D.DecoderConfig(graph_steps=1)
     dec = D.Decoder(lib, stream, cfg)
-    _check_fused(dec, fused)
     dec.randomize(seed=0)
     H, Nq, Nkv, Hd, F, L = cfg.hidden, cfg.query_heads, cfg.kv_heads, cfg.head_dim, cfg.ffn, cfg.layers
     assert (L, H, Nq, Nkv, Hd, F, cfg.vocab) == (26, 2304, 8, 4, 256, 9216, 256000)
@@ -296,17 +274,15 @@ def test_gemma2_2b_step_matches_oracle(env, fused):
     dec.close()
 
 
-@pytest.mark.parametrize("fused", [0, 1])
-def test_steps_past_the_cache_are_refused(env, fused):
+def test_steps_past_the_cache_are_refused(env):
     # a step at position p writes KV row p: with max_seq 64, positions 62 and
     # 63 decode, position 64 is refused with tensorShapeMismatch before
     # anything is enqueued, and the caches are left as they were
     pa, lib, stream, enc = env
     import popcorn_amd.decoder as D
 
-    cfg = _small(D, graph_steps=2, fused=fused)
+    cfg = _small(D, graph_steps=2)
     dec = D.Decoder(lib, stream, cfg)
-    _check_fused(dec, fused)
     dec.randomize(seed=3)
     dec.reset(5, 62)
     dec.step(2, use_graph=False)

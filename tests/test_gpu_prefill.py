@@ -292,38 +292,164 @@ def test_tiled_attention_two_tiles_per_cu_sampled(env, rows):
         assert_out(got[:, :, r:r + 1], ref, EPS["f16"], "f16", f"two tiles per CU row {r}")
 
 
-def test_merged_pairs_reset_ready_flags(env):
-    # A raw launch of the 16-row kernel with pairTiles 2 (causal, 2 heads x 5
-    # tiles: two pairs and a middle tile per head) twice with the same
-    # ticket, as a replayed graph would: after each launch every ready flag
-    # is back to 0 (the merging block resets it), and the second launch,
-    # over new queries, matches the oracle too.
+def _merged_pair_launch(pa, lib, stream, tq, tk, tv, out, pO, pML, flags, B, Nq, S, Hd, dtype, ticket):
+    """A raw launch of the 16-row kernel with pairTiles 2 (causal)."""
     import struct
-    pa, lib, stream, enc = env
-    B, Nq, S, Hd, dtype = 1, 2, 640, 128, "f16"
     nQT = (S + 127) // 128
     nSplit = nQT // 2
-    tiles = B * Nq * nSplit
-    ticket = 0x5EED1234ABCD0001
     # TiledFlashAttentionConstants: B, Nq, Nkv, Sq, Sk, Hd, qTilesPerHead,
     # maskKind (0: causal), slidingWindow (-1), scale, kvStride, splitFrom,
     # pairTiles, ticketLo, ticketHi
     consts = struct.pack("<8Iif5I", B, Nq, Nq, S, S, Hd, nQT, 0, -1, 1 / np.sqrt(Hd), 0,
                          nQT - nSplit, 2, ticket & 0xFFFFFFFF, ticket >> 32)
+    lib.launch(f"flash_attention_tiled16_{dtype}_{dtype}_d{Hd}", (B * Nq * nQT, 1, 1), (512, 1, 1),
+               [tq.ptr, tk.ptr, tv.ptr, out.ptr, pO.ptr, pML.ptr, flags.ptr], [consts], stream=stream)
+
+
+def _pair_buffers(pa, tiles, Hd, stream):
+    """The exchange of a raw merged-pair launch, in uncached memory as the
+    kernel requires: pO, pML and the flags (abort word + one per tile), zeroed."""
+    pO = pa.Tensor.empty_uncached([tiles * 128, Hd], "f32")
+    pML = pa.Tensor.empty_uncached([tiles * 128 * 2], "f32")
+    flags = pa.Tensor.empty_uncached([1 + tiles], "u64")
+    flags.copy_from(np.zeros(1 + tiles, np.uint64), stream)
+    return pO, pML, flags
+
+
+def test_merged_pairs_reset_ready_flags(env):
+    # A raw launch of the 16-row kernel with pairTiles 2 (causal, 2 heads x 5
+    # tiles: two pairs and a middle tile per head) twice with the same
+    # ticket, as a replayed graph would: after each launch every ready flag
+    # and the abort word are 0 (the merging block resets its flag), and the
+    # second launch, over new queries, matches the oracle too.
+    pa, lib, stream, enc = env
+    B, Nq, S, Hd, dtype = 1, 2, 640, 128, "f16"
+    tiles = B * Nq * (((S + 127) // 128) // 2)
+    ticket = 0x5EED1234ABCD0001
     k = rounded(O.normal(11, (B, Nq, S, Hd)), dtype)
     v = rounded(O.normal(12, (B, Nq, S, Hd)), dtype)
     tk, tv = upload(pa, k, dtype), upload(pa, v, dtype)
-    pO = pa.Tensor.empty([tiles * 128, Hd], "f32")
-    pML = upload(pa, np.zeros(tiles * 128 * 2 + tiles * 2, np.float32), "f32")
+    pO, pML, flags = _pair_buffers(pa, tiles, Hd, stream)
     for rep in range(2):
         q = rounded(O.normal(20 + rep, (B, Nq, S, Hd)), dtype)
         tq = upload(pa, q, dtype)
         out = upload(pa, np.full((B, Nq, S, Hd), np.nan, np.float32), dtype)
-        lib.launch(f"flash_attention_tiled16_{dtype}_{dtype}_d{Hd}", (B * Nq * nQT, 1, 1), (512, 1, 1),
-                   [tq.ptr, tk.ptr, tv.ptr, out.ptr, pO.ptr, pML.ptr], [consts], stream=stream)
+        _merged_pair_launch(pa, lib, stream, tq, tk, tv, out, pO, pML, flags, B, Nq, S, Hd, dtype, ticket)
         stream.synchronize()
-        flags = download(pML, stream)[tiles * 128 * 2:].view(np.uint64)
-        assert (flags == 0).all(), f"launch {rep}: ready flags not reset: {flags}"
+        f = flags.numpy(stream)
+        assert (f == 0).all(), f"launch {rep}: ready flags or abort word not reset: {f}"
         got = download(out, stream).reshape(B, Nq, S, Hd)
         ref = O.attention_naive(q, k, v, 1 / np.sqrt(Hd), mask_kind=0)
         assert_out(got, ref, EPS[dtype], dtype, f"merged pairs, launch {rep}")
+
+
+def test_merged_pairs_give_up_is_replay_safe(env):
+    # The give-up path, forced from the host: split tile 1 (head 0, query
+    # tile 4: rows 512..639) starts with its flag poisoned, as a merging
+    # block that gave up leaves it. Its merging block must not wait or merge:
+    # it writes NaN rows and sets the abort word, and its publishing block's
+    # compare-and-swap from 0 leaves the poison in place. A second launch
+    # with the same ticket (a replayed graph) fails the same way instead of
+    # taking a stale part. Every other tile matches the oracle. Once the
+    # flags are cleared, a third launch is whole.
+    pa, lib, stream, enc = env
+    B, Nq, S, Hd, dtype = 1, 2, 640, 128, "f16"
+    tiles = B * Nq * (((S + 127) // 128) // 2)
+    ticket = 0x0123456789ABCDEF
+    poison = np.uint64(0xFFFFFFFFFFFFFFFF)
+    q = rounded(O.normal(31, (B, Nq, S, Hd)), dtype)
+    k = rounded(O.normal(32, (B, Nq, S, Hd)), dtype)
+    v = rounded(O.normal(33, (B, Nq, S, Hd)), dtype)
+    tq, tk, tv = upload(pa, q, dtype), upload(pa, k, dtype), upload(pa, v, dtype)
+    ref = O.attention_naive(q, k, v, 1 / np.sqrt(Hd), mask_kind=0)
+    pO, pML, flags = _pair_buffers(pa, tiles, Hd, stream)
+    init = np.zeros(1 + tiles, np.uint64)
+    init[1 + 1] = poison
+    flags.copy_from(init, stream)
+    bad = np.zeros((B, Nq, S), bool)
+    bad[0, 0, 512:640] = True
+    for rep in range(3):
+        if rep == 2:
+            flags.copy_from(np.zeros(1 + tiles, np.uint64), stream)
+        out = upload(pa, np.full((B, Nq, S, Hd), 7.0, np.float32), dtype)
+        _merged_pair_launch(pa, lib, stream, tq, tk, tv, out, pO, pML, flags, B, Nq, S, Hd, dtype, ticket)
+        stream.synchronize()
+        f = flags.numpy(stream)
+        got = download(out, stream).reshape(B, Nq, S, Hd)
+        if rep < 2:
+            assert f[0] == 1, f"launch {rep}: abort word not set"
+            assert f[2] == poison, f"launch {rep}: the poisoned flag was overwritten: {f[2]:#x}"
+            assert (np.delete(f, [0, 2]) == 0).all(), f
+            assert np.isnan(got[bad]).all(), f"launch {rep}: the given-up tile's rows are not NaN"
+            assert not np.isnan(got[~bad]).any()
+            assert_out(got[~bad], ref[~bad], EPS[dtype], dtype, f"merged pairs around a given-up tile, launch {rep}")
+        else:
+            assert (f == 0).all(), f
+            assert_out(got, ref, EPS[dtype], dtype, "merged pairs after the flags were cleared")
+
+
+def test_merged_pairs_abort_reported_at_stream_sync(env):
+    # The stream's own exchange (the descriptor path): a poisoned flag makes
+    # the launch write NaN rows for that tile, and popcorn_stream_synchronize
+    # reports -1019 and clears the flags; the next launch is whole.
+    pa, lib, stream, enc = env
+    B, Nq, S, Hd, dtype = 1, 2, 640, 128, "f16"
+    q = rounded(O.normal(41, (B, Nq, S, Hd)), dtype)
+    k = rounded(O.normal(42, (B, Nq, S, Hd)), dtype)
+    v = rounded(O.normal(43, (B, Nq, S, Hd)), dtype)
+    ref = O.attention_naive(q, k, v, 1 / np.sqrt(Hd), mask_kind=0)
+    tq, tk, tv = upload(pa, q, dtype), upload(pa, k, dtype), upload(pa, v, dtype)
+    to = pa.Tensor.empty([B, Nq, S, Hd], dtype)
+    kern = pa.Kernels.FlashAttention(tq, tk, tv, out=to, scale=1 / np.sqrt(Hd), batch=B, query_heads=Nq,
+                                     kv_heads=Nq, query_len=S, key_len=S, head_dim=Hd)
+    assert kern.function_names == [f"flash_attention_tiled16_{dtype}_{dtype}_d{Hd}"]
+    stream.synchronize()
+    flags = pa.attention_pair_flags(stream)
+    init = np.zeros(flags.shape[0], np.uint64)
+    init[1 + 3] = np.uint64(0xFFFFFFFFFFFFFFFF)  # split tile 3: head 1, query tile 4
+    flags.copy_from(init, stream)
+    enc.encode(kern)
+    with pytest.raises(pa.PopcornError) as e:
+        stream.synchronize()
+    assert e.value.code == pa.PopcornError.GPU_INTERNAL
+    got = download(to, stream).reshape(B, Nq, S, Hd)
+    assert np.isnan(got[0, 1, 512:640]).all() and not np.isnan(got[0, 0]).any()
+    assert (flags.numpy(stream) == 0).all()
+    enc.encode(kern)
+    stream.synchronize()
+    assert_out(download(to, stream).reshape(B, Nq, S, Hd), ref, EPS[dtype], dtype, "merged pairs after the abort")
+
+
+def test_merged_pairs_bitwise_stable_over_launches(env):
+    # Config-5 attention (f16, 16 heads x 2048, Hd 256, causal: merged pairs)
+    # launched 200 times, with a split-K GEMM borrowing and writing pooled
+    # scratch between launches; every output must equal the first bit for
+    # bit (the merge is deterministic), stopping at the first difference.
+    pa, lib, stream, enc = env
+    H, S, Hd = 16, 2048, 256
+    tq, tk, tv = (pa.Tensor.empty([1, H, S, Hd], "f16") for _ in range(3))
+    for i, t in enumerate((tq, tk, tv)):
+        lib.fill_normal(t, 80 + i, stream=stream)
+    to = pa.Tensor.empty([1, H, S, Hd], "f16")
+    kern = pa.Kernels.FlashAttention(tq, tk, tv, out=to, scale=1 / 16, batch=1, query_heads=H, kv_heads=H,
+                                     query_len=S, key_len=S, head_dim=Hd)
+    assert kern.function_names == [_tiled("f16", "f16", Hd, "rows16")]
+    # a down-projection-shaped split-K GEMM: its f32 partials in pooled scratch
+    ga, gb = pa.Tensor.empty([1024, 24576], "f16"), pa.Tensor.empty([3072, 24576], "f16")
+    lib.fill_normal(ga, 90, stream=stream)
+    lib.fill_normal(gb, 91, std=0.02, stream=stream)
+    gc = pa.Tensor.empty([1024, 3072], "f16")
+    gemm = pa.Kernels.Matmul(ga, gb, gc, True)
+    assert gemm.function_names[1] == "matmul_splitk_reduce_f16"
+    first = None
+    for i in range(200):
+        enc.encode(kern)
+        enc.encode(gemm)
+        stream.synchronize()
+        got = to.numpy(stream)
+        if first is None:
+            first = got
+            assert not np.isnan(first.view(np.float16)).any()
+        elif not np.array_equal(got, first):
+            diff = int(np.count_nonzero(got != first))
+            raise AssertionError(f"launch {i}: {diff} output elements differ from the first launch")
