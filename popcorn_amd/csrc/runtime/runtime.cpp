@@ -308,6 +308,13 @@ void KernelCommandEncoder::dispatch(const DispatchKernel &kernel) {
     if (hook_) timing = (*hook_)(kernel.functionName());
     hipError_t err;
     if (timing.first || timing.second) {
+        // hipExtModuleLaunchKernel takes the global size in threads as
+        // 32-bit values: a grid whose thread count does not fit is refused
+        const uint64_t gx = (uint64_t)ds.grid.x * ds.block.x, gy = (uint64_t)ds.grid.y * ds.block.y,
+                       gz = (uint64_t)ds.grid.z * ds.block.z;
+        if (gx > UINT32_MAX || gy > UINT32_MAX || gz > UINT32_MAX)
+            throw Error::invalidArgument("timed launch of " + kernel.functionName() +
+                                         ": the grid holds more than 2^32 - 1 threads in one dimension");
         err = hipExtModuleLaunchKernel(fn.fn, ds.grid.x * ds.block.x, ds.grid.y * ds.block.y, ds.grid.z * ds.block.z,
                                        ds.block.x, ds.block.y, ds.block.z, ds.dynamicLds, stream_, params.data(),
                                        nullptr, timing.first, timing.second, 0);
