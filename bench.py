@@ -199,6 +199,36 @@ def q4_sweep(pa, lib, stream, enc):
     return rows
 
 
+def skinny_gemm(pa, lib, stream, enc):
+    """The skinny 16-bit Matmul (2 <= M <= 64; the reference's small-M MPP
+    tiles, Matmul.swift:175-196): C[M, N] = A[M, K] . B[N, K]^T in bf16 with
+    f32 accumulation at M = 8 on the Gemma-2-2B gate shape (N 9216, K 2304:
+    an 8-token prompt or an 8-wide decode batch) and at M = 16, 32, 64; every
+    launch reads a B it has not read for >= 512 MB of others (cold in the
+    MALL). Bytes: B + A + C."""
+    rows = []
+    N, K = 9216, 2304
+    wbytes = N * K * 2
+    sets = max(1, -(-(512 << 20) // wbytes))
+    w = pa.Tensor.empty([sets * N, K], "bf16")
+    lib.fill_normal(w, 5, std=0.02, stream=stream)
+    for M in (8, 16, 32, 64):
+        a = pa.Tensor.empty([M, K], "bf16")
+        lib.fill_normal(a, 6, stream=stream)
+        c = pa.Tensor.empty([M, N], "bf16")
+        kerns = [pa.Kernels.Matmul(a, w.view([N, K], offset_elements=i * N * K), c, True) for i in range(sets)]
+        enc.encode(*kerns)
+        stream.synchronize()
+        nbytes = wbytes + M * K * 2 + M * N * 2
+        us = timed_launches(pa, stream, enc, [kerns[r % sets] for r in range(8 * sets)])
+        gbs = nbytes / (us * 1e-6) / 1e9
+        rows.append({"M": M, "N": N, "K": K, "kernel": kerns[0].function_names[0], "us": round(us, 2),
+                     "bytes": nbytes, "GB_s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 3),
+                     "TFLOP_s": round(2 * M * N * K / (us * 1e-6) / 1e12, 2)})
+    del w
+    return rows
+
+
 def fd_sweep(pa, lib, stream, enc):
     """split-KV FlashDecoding (partial + LSE combine) in f16,
     Q [B, 8, 1, 256], K/V [B, 4, ctx, 256] N(0, 1), scale 1/16, no mask, over
@@ -461,6 +491,7 @@ def main():
                     help="also time the config-5 shapes through PyTorch's hipBLASLt GEMM and SDPA attention")
     ap.add_argument("--library-reference-child", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--no-q4", action="store_true", help="skip the 4-bit matvec measurement")
+    ap.add_argument("--no-skinny", action="store_true", help="skip the skinny (2 <= M <= 64) GEMM measurement")
     ap.add_argument("--no-attention-block", action="store_true",
                     help="skip the decode with per-head norms and RoPE (a real attention block)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -551,6 +582,10 @@ def main():
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(dec, cfg, stream, token)
 
+    skinny = None
+    if not args.no_skinny:
+        skinny = skinny_gemm(pa, lib, stream, pa.KernelCommandEncoder(lib, stream))
+
     q4 = None
     if not args.no_q4:
         q4 = q4_sweep(pa, lib, stream, pa.KernelCommandEncoder(lib, stream))
@@ -589,6 +624,7 @@ def main():
         "mlp_config3": mlp,
         "prefill_config5": prefill,
         "decode_attention_block": block,
+        "skinny_gemm": skinny,
         "q4_matvec": q4,
         "decode_q4": q4dec,
         "cpu_baseline": cpu,

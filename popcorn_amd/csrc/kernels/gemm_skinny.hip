@@ -1,0 +1,157 @@
+// Skinny Matmul on the matrix cores, 2 <= M <= 64: C[M, N] = A[M, K] . B[N, K]^T
+// with 16-bit A and B (the reference's transposeB layout), f32 accumulation,
+// C in f32 or the input dtype (popcorn_store rounding). This is the role of
+// the reference's small-M MPP tiles (TileM 8/16/32, Matmul.swift:175-196,
+// MPPMatmul.metal:19-91): an 8-token prompt or an 8-wide decode batch, where
+// B (the weights) is read once and the time is the stream of its bytes.
+//
+// The product is computed transposed, C^T = B . A^T, on
+// v_mfma_f32_16x16x32_{f16,bf16} (lane layout in mfma.hpp): 16 rows of B
+// are the A operand, 16 rows of A (M padded to 16, 32, 48 or 64 in MT
+// tiles) the B operand, so both are 16-byte runs along K of one row and a
+// lane's fragment is one 16-byte load: lane l reads row l % 16 at
+// k0 + (l / 16) * 8. A block takes 32 rows of B (two 16-row tiles, so each
+// A fragment serves two products); its W waves split K, each wave a
+// contiguous run of k-steps of 32 with U steps in flight, and sum their
+// partial C^T tiles in LDS at the end. A (M x K, a few tens of KB) is read
+// from L2 beside B. Rows past N or M read a valid row and are not stored;
+// K % 8 == 0, so a chunk lies wholly inside or outside K and the chunks past
+// it are zeros in both operands.
+#include <type_traits>
+
+#include "mfma.hpp"
+
+namespace {
+
+using pk::f32x4;
+using pk::Mma16;
+using pk::u32x4;
+
+constexpr int NT = 2;                 // 16-row tiles of B per block
+constexpr int U = 4;                  // k-steps in flight per wave
+constexpr int kMaxWaves = 8;          // waves per block (K split)
+constexpr int kRedFloats = 16384;     // LDS for the partial tiles: W x NT x MT x 256 floats
+
+template <typename T, typename O, int MT>
+__device__ void gemm_skinny(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
+                            typename O::storage *__restrict__ C, const MatmulConstants &p) {
+    static_assert(kMaxWaves * NT * MT * 256 <= kRedFloats, "LDS for the partial tiles");
+    __shared__ __attribute__((aligned(16))) float red[kRedFloats];
+
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, W = blockDim.x >> 6;
+    const uint32_t M = p.M, K = p.K, N = p.N;
+    const uint32_t r = lane & 15, g = lane >> 4;
+    const uint32_t n0 = blockIdx.x * (16 * NT);
+    // Buffer loads (the host keeps A and B under 4 GB): byte offsets of this
+    // lane's rows. As intrinsic calls they also stay where they are issued
+    // (plain loads of a loop-carried ring are folded into one load at the
+    // point of use, which would drain the queue every step).
+    const __amdgpu_buffer_rsrc_t rsB =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(B), 0, (int)(N * K * 2u), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsA =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(A), 0, (int)(M * K * 2u), 0x00020000);
+    uint32_t boff[NT], aoff[MT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) boff[t] = min(n0 + 16 * t + r, N - 1) * K * 2u;
+#pragma unroll
+    for (int u = 0; u < MT; ++u) aoff[u] = min(16u * u + r, M - 1) * K * 2u;
+
+    f32x4 acc[NT][MT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int u = 0; u < MT; ++u) acc[t][u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // this wave's k-steps: a contiguous run of KS / W (rounded up)
+    const uint32_t KS = (K + 31) / 32;
+    const uint32_t SPW = (KS + W - 1) / W;
+    const uint32_t first = wave * SPW;
+    const uint32_t nsteps = first < KS ? min(SPW, KS - first) : 0u;
+    // Every load reads a valid address (a step past the wave's last reads
+    // its last, a chunk past K the row's last chunk), so every path issues
+    // the same loads and the wait counts stay exact; what lies outside is
+    // replaced by zeros in both operands. The scheduling barriers hold the
+    // loads in this order in the prologue and in the loop alike, so the
+    // compiler's wait before each step counts the same loads in flight on
+    // entry and around the loop (otherwise the loop header merges two orders
+    // and waits for everything).
+    u32x4 bf[U][NT], af[U][MT];
+    auto issue = [&](int slot, uint32_t q) {
+        const uint32_t s = first + min(q, nsteps ? nsteps - 1 : 0u);
+        const uint32_t k2 = min(s * 32 + g * 8, K - 8) * 2u;
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+            bf[slot][t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsB, boff[t] + k2, 0, 0));
+#pragma unroll
+        for (int u = 0; u < MT; ++u)
+            af[slot][u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsA, aoff[u] + k2, 0, 0));
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    const u32x4 zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int j = 0; j < U; ++j) issue(j, j);
+    // Step q of slot j: data out of range replaced by zeros; the selects
+    // also place real instructions on the slot's registers before the refill
+    // reuses them, so each step waits only for its own loads.
+    for (uint32_t q0 = 0; q0 < nsteps; q0 += U) {
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+            const uint32_t q = q0 + j;
+            const bool in = q < nsteps && (first + q) * 32 + g * 8 < K;
+            u32x4 b[NT], a[MT];
+#pragma unroll
+            for (int t = 0; t < NT; ++t) b[t] = in ? bf[j][t] : zero;
+#pragma unroll
+            for (int u = 0; u < MT; ++u) a[u] = in ? af[j][u] : zero;
+            issue(j, q + U);
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int u = 0; u < MT; ++u) acc[t][u] = Mma16<T>::run(b[t], a[u], acc[t][u]);
+        }
+    }
+
+    // partial tiles to LDS: [wave][t][u][element i][lane], then every
+    // thread sums the waves' values of some (t, u, lane, i) and stores them:
+    // C^T element i of lane l in tile (t, u) is row n0 + 16 t + (l / 16) * 4 + i
+    // of B, row 16 u + l % 16 of A
+    constexpr int kTile = NT * MT * 256;
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int u = 0; u < MT; ++u)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) red[wave * kTile + ((t * MT + u) * 4 + i) * 64 + lane] = acc[t][u][i];
+    __syncthreads();
+    for (uint32_t e = threadIdx.x; e < (uint32_t)kTile; e += blockDim.x) {
+        float v = 0.0f;
+        for (uint32_t w = 0; w < W; ++w) v += red[w * kTile + e];
+        const uint32_t l = e & 63, i = (e >> 6) & 3, tu = e >> 8;
+        const uint32_t t = tu / MT, u = tu % MT;
+        const uint32_t n = n0 + 16 * t + (l >> 4) * 4 + i, m = 16 * u + (l & 15);
+        if (n < N && m < M) C[(uint64_t)m * N + n] = O::store(v);
+    }
+}
+
+}  // namespace
+
+#define GEMM_SKINNY(name, T, O, MT)                                                                       \
+    POPCORN_KERNEL void __launch_bounds__(64 * kMaxWaves)                                                 \
+        name(const uint16_t *a, const uint16_t *b, O::storage *c, MatmulConstants p) {                    \
+        gemm_skinny<T, O, MT>(a, b, c, p);                                                                \
+    }
+#define GEMM_SKINNY_M(t, T, o, O)                                \
+    GEMM_SKINNY(matmul_skinny_##t##_##t##_##o##_m16, T, O, 1)    \
+    GEMM_SKINNY(matmul_skinny_##t##_##t##_##o##_m32, T, O, 2)    \
+    GEMM_SKINNY(matmul_skinny_##t##_##t##_##o##_m48, T, O, 3)    \
+    GEMM_SKINNY(matmul_skinny_##t##_##t##_##o##_m64, T, O, 4)
+
+using pk::BF16;
+using pk::F16;
+using pk::F32;
+
+GEMM_SKINNY_M(f16, F16, f16, F16)
+GEMM_SKINNY_M(f16, F16, f32, F32)
+GEMM_SKINNY_M(bf16, BF16, bf16, BF16)
+GEMM_SKINNY_M(bf16, BF16, f32, F32)

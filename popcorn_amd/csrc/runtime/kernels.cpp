@@ -779,6 +779,22 @@ std::unique_ptr<Kernel> makeMatmul(const Tensor &a, const Tensor &b, const Tenso
         if (transposeB && (t == DataType::f16 || t == DataType::bf16) && b.dataType == t &&
             (c.dataType == t || c.dataType == DataType::f32) && k % 8 == 0 && k > 0 && aligned16(a.data) &&
             aligned16(b.data)) {
+            // 2 <= M <= 64: the skinny kernel (gemm_skinny.hip), which
+            // streams B once with its K split over a block's waves: about
+            // 3 waves per CU in all, at most 4 per block (measured best on
+            // MI355X for N 2304..24576 x K 2304..9216)
+            if (m <= 64 && !std::getenv("POPCORN_GEMM_TILE") && n * k * 2 <= INT32_MAX && m * k * 2 <= INT32_MAX) {
+                const int mt = (int)cdiv(m, 16);
+                const int64_t blocks = cdiv(n, 32);
+                const int64_t want = 3 * (int64_t)deviceCUs() / blocks;
+                int64_t w = 1;
+                while (2 * w <= want && w < 4 && 2 * w <= cdiv(k, 32)) w *= 2;
+                MatmulConstants mc{(uint32_t)m, (uint32_t)k, (uint32_t)n, 1u};
+                const std::string fn = std::string("matmul_skinny_") + tag(t) + "_" + tag(t) + "_" + tag(c.dataType) +
+                                       "_m" + std::to_string(16 * mt);
+                return std::make_unique<FixedDispatch>(fn, binds, std::vector<std::vector<uint8_t>>{bytesOf(mc)},
+                                                       grid1(blocks, (int)(64 * w)));
+            }
             // the split-K reduction stores 4 results of C at a time
             if (const int64_t splits = aligned16(c.data) ? gemmSplitK(m, n, k) : 0)
                 return std::make_unique<SplitKMatmulKernel>(a, b, c, m, k, n, splits);

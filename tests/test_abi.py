@@ -103,6 +103,14 @@ def test_prefill_gemm_tile_plan():
                               True).function_names
     assert c_off == ["matmul_mfma_f16_f16_f16_d128x192"]
     assert mm(256, 1024, 384) == ["matmul_mfma_f16_f16_f16_d128x128"]
+    # 2 <= M <= 64: the skinny kernel, M padded to 16 per MFMA tile
+    assert mm(2, 64, 67) == ["matmul_skinny_f16_f16_f16_m16"]
+    assert mm(8, 2304, 9216, "bf16") == ["matmul_skinny_bf16_bf16_bf16_m16"]
+    assert mm(17, 2304, 9216, "bf16", "f32") == ["matmul_skinny_bf16_bf16_f32_m32"]
+    assert mm(48, 2304, 9216) == ["matmul_skinny_f16_f16_f16_m48"]
+    assert mm(64, 3072, 24576) == ["matmul_skinny_f16_f16_f16_m64"]
+    assert mm(65, 2048, 2048) == ["matmul_mfma_f16_f16_f16_d128x128"]
+    assert mm(8, 2300, 9216)[0].startswith("matmul_tiled")  # K % 8 != 0: the SIMT tiles
 
 
 def test_flash_attention_routing_names():
