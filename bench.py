@@ -372,6 +372,39 @@ def prefill_config5(pa, lib, stream, enc, reps=8):
     return rows
 
 
+def prefill_attention_hd512(pa, lib, stream, enc, reps=8):
+    """Causal FlashAttention at the reference's other matrix-unit bucket,
+    head dim 512 (MPPFlashAttention's hd512, FlashAttention.swift:305-311;
+    Gemma-4's global layers): [1, 16, 2048, 512] bf16, GQA 2:1, scale
+    1/sqrt(512), on the matrix cores; the per-query-row split-KV kernels (the
+    route this head dim took before) on the same inputs beside it, reached
+    through an output that is not 16-byte aligned."""
+    S, Hq, Hkv, Hd = 2048, 16, 8, 512
+    q = pa.Tensor.empty([1, Hq, S, Hd], "bf16")
+    k, v = (pa.Tensor.empty([1, Hkv, S, Hd], "bf16") for _ in range(2))
+    for i, t in enumerate((q, k, v)):
+        lib.fill_normal(t, 60 + i, stream=stream)
+    o = pa.Tensor.empty([1, Hq, S, Hd + 8], "bf16")
+    flop = 4.0 * Hq * Hd * S * (S + 1) / 2
+    out = {}
+    for name, view in (("tiled", o.view([1, Hq, S, Hd])), ("per_row", o.view([1, Hq, S, Hd], offset_elements=1))):
+        fa = pa.Kernels.FlashAttention(q, k, v, out=view, scale=1 / Hd ** 0.5, batch=1, query_heads=Hq,
+                                       kv_heads=Hkv, query_len=S, key_len=S, head_dim=Hd)
+        enc.encode(fa)
+        stream.synchronize()
+        e0, e1 = pa.Event(), pa.Event()
+        e0.record(stream)
+        for _ in range(reps):
+            enc.encode(fa)
+        e1.record(stream)
+        e1.synchronize()
+        us = e0.elapsed_ms(e1) * 1e3 / reps
+        out[name] = {"kernel": fa.function_names[0], "us": round(us, 1),
+                     "TFLOP_s": round(flop / (us * 1e-6) / 1e12, 1),
+                     "frac": round(flop / (us * 1e-6) / 1e12 / MFMA_PEAK_F16_TFLOPS, 3)}
+    return out
+
+
 def library_reference():
     """The config-5 shapes through the vendor libraries PyTorch calls on ROCm
     (torch.matmul -> hipBLASLt, scaled_dot_product_attention's flash and
@@ -575,6 +608,7 @@ def main():
     prefill = None
     if not args.no_prefill:
         prefill = prefill_config5(pa, lib, stream, pa.KernelCommandEncoder(lib, stream))
+        prefill["attention_hd512"] = prefill_attention_hd512(pa, lib, stream, pa.KernelCommandEncoder(lib, stream))
         if args.library_reference:
             prefill["library_reference"] = library_reference()
 

@@ -110,6 +110,9 @@ typedef struct {
 
 /* The MFMA prefill kernel's constants (flash_attention_tiled_*, the kernel
  * in the MPP route's place): MPPFlashAttentionConstants' fields, plus
+ *   Hd         the head dim, at most the kernel's (_d64/_d128/_d256/_d512)
+ *              and a multiple of 8: rows of Q, K, V and O are Hd apart, and
+ *              the kernel's dims past Hd are zeros;
  *   kvStride   rows between consecutive KV heads in K/V (0 = Sk);
  *   splitFrom  splitFrom >= qTilesPerHead: one block per query tile.
  *              Otherwise tiles qt >= splitFrom are split in two parts, each
@@ -131,6 +134,8 @@ typedef struct {
  *              blocks may sit on XCDs whose L2 caches are not coherent.
  *              pairFlags (u64) holds the abort word at index 0 and the flag
  *              of split tile t at index 1 + t; all start at 0;
+ *              The _d512 kernels (64 query rows per block, 256 threads)
+ *              run every tile whole whatever splitFrom and pairTiles say;
  *   ticketLo, ticketHi  pairTiles 2: the 64-bit value (neither 0 nor
  *              ~0) the first block sets its flag to, by compare-and-swap
  *              from 0, distinct per launch; the merging block resets the

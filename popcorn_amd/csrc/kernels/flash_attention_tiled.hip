@@ -40,6 +40,11 @@ constexpr int BKV = 32;          // keys per step
 // reference moves: softmax weights stay below e^8 ~ 2981 (f16 holds 65504).
 constexpr float kRescaleGap = 8.0f;
 constexpr float kLog2e = 1.4426950408889634f;
+// A buffer offset past every head's range (the host keeps Sk * Hd * 2 below
+// 2^31, and a step's scalar offset below that too): the load returns zeros.
+// Chunks of a row past the runtime head dim Hd read it, so a kernel compiled
+// for HD > Hd multiplies zeros there.
+constexpr int kOutOfRange = (int)0x80000000u;
 
 // Partial state handed between the two blocks of a merged pair (pairTiles
 // 2). The two blocks may run on different XCDs, whose L2 caches are not
@@ -124,18 +129,19 @@ __device__ inline bool fa_allowed(const TiledFlashAttentionConstants &p, int pos
 }
 
 // Key steps of query tile qt: keys any query of the tile may see.
-__device__ inline void fa_key_range(const TiledFlashAttentionConstants &p, uint32_t qt, int &kLo, int &kHi) {
-    const int first = (int)p.Sk - (int)p.Sq + (int)(qt * BQ);
-    const int last = (int)p.Sk - (int)p.Sq + (int)min(qt * BQ + BQ - 1, p.Sq - 1);
+__device__ inline void fa_key_range(const TiledFlashAttentionConstants &p, uint32_t qt, int &kLo, int &kHi,
+                                    uint32_t bq = BQ) {
+    const int first = (int)p.Sk - (int)p.Sq + (int)(qt * bq);
+    const int last = (int)p.Sk - (int)p.Sq + (int)min(qt * bq + bq - 1, p.Sq - 1);
     kLo = 0;
     kHi = (int)p.Sk;
     if (p.maskKind != 2u) kHi = min(kHi, last + 1);
     if (p.maskKind == 1u) kLo = max(0, first - p.slidingWindow + 1);
 }
 
-__device__ inline uint32_t fa_steps(const TiledFlashAttentionConstants &p, uint32_t qt) {
+__device__ inline uint32_t fa_steps(const TiledFlashAttentionConstants &p, uint32_t qt, uint32_t bq = BQ) {
     int kLo, kHi;
-    fa_key_range(p, qt, kLo, kHi);
+    fa_key_range(p, qt, kLo, kHi, bq);
     return kHi > kLo ? (uint32_t)(kHi - kLo + BKV - 1) / BKV : 0u;
 }
 
@@ -165,15 +171,15 @@ struct FaWork {
     bool split[2];
 };
 
-__device__ inline FaWork fa_work(const TiledFlashAttentionConstants &p) {
+__device__ inline FaWork fa_work(const TiledFlashAttentionConstants &p, uint32_t bq = BQ, bool whole = false) {
     const uint32_t BH = p.B * p.Nq, nQT = p.qTilesPerHead;
     const uint32_t rank = blockIdx.x / BH;
     FaWork w{};
     w.bh = blockIdx.x % BH;
     w.n = 1;
-    if (p.splitFrom >= nQT) {
+    if (whole || p.splitFrom >= nQT) {
         w.qt[0] = nQT - 1 - rank;
-        w.hi[0] = fa_steps(p, w.qt[0]);
+        w.hi[0] = fa_steps(p, w.qt[0], bq);
         return w;
     }
     if (!p.pairTiles) {
@@ -181,9 +187,9 @@ __device__ inline FaWork fa_work(const TiledFlashAttentionConstants &p) {
         int a = (int)nQT - 1, b = (int)sf - 1;  // next split tile, next whole tile
         uint32_t halves = 2;
         for (uint32_t r = 0; r < nItems; ++r) {
-            const bool takeSplit = a >= (int)sf && (b < 0 || (fa_steps(p, a) + 1) / 2 >= fa_steps(p, b));
+            const bool takeSplit = a >= (int)sf && (b < 0 || (fa_steps(p, a, bq) + 1) / 2 >= fa_steps(p, b, bq));
             if (r == rank) {
-                const uint32_t qt = (uint32_t)(takeSplit ? a : b), n = fa_steps(p, qt), half = (n + 1) / 2;
+                const uint32_t qt = (uint32_t)(takeSplit ? a : b), n = fa_steps(p, qt, bq), half = (n + 1) / 2;
                 w.qt[0] = qt;
                 w.split[0] = takeSplit;
                 w.part[0] = takeSplit ? 2u - halves : 0u;
@@ -205,11 +211,11 @@ __device__ inline FaWork fa_work(const TiledFlashAttentionConstants &p) {
     const uint32_t pairs = nQT / 2;
     if (rank >= 2 * pairs) {  // the middle tile of an odd count
         w.qt[0] = pairs;
-        w.hi[0] = fa_steps(p, pairs);
+        w.hi[0] = fa_steps(p, pairs, bq);
         return w;
     }
     const uint32_t i = rank >> 1, a = i, bt = nQT - 1 - i;
-    const uint32_t sa = fa_steps(p, a), sb = fa_steps(p, bt);
+    const uint32_t sa = fa_steps(p, a, bq), sb = fa_steps(p, bt, bq);
     const uint32_t x = (sa + sb + 1) / 2 - sa;
     if ((rank & 1u) == 0u && p.pairTiles == 2u) {
         // merged in the kernel: the partner's first steps come first, so
@@ -263,8 +269,9 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
     const uint32_t b = bh / p.Nq, hq = bh % p.Nq;
     const uint32_t hkv = hq / (p.Nq / p.Nkv);
     const uint32_t stride = p.kvStride ? p.kvStride : p.Sk;
-    const uint16_t *Qh = Q + (uint64_t)bh * p.Sq * HD;
-    const uint64_t kvoff = (uint64_t)(b * p.Nkv + hkv) * stride * HD;
+    const uint32_t D = p.Hd;  // runtime head dim (<= HD, a multiple of 8): rows are D apart
+    const uint16_t *Qh = Q + (uint64_t)bh * p.Sq * D;
+    const uint64_t kvoff = (uint64_t)(b * p.Nkv + hkv) * stride * D;
     const uint16_t *Kh = K + kvoff;
     const uint16_t *Vh = V + kvoff;
     // the current item's tile, this lane's query row and the wave's first
@@ -289,22 +296,23 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
     using VRegs = u32x4[kVC][4];
     u32x4 krA[kKC], vrA[kVC][4], krB[kKC], vrB[kVC][4];
     // K and V are read through buffer resources over the head's Sk rows
-    // (the host keeps Sk * HD * 2 below 2^31): a row past Sk reads as zeros
+    // (the host keeps Sk * Hd * 2 below 2^31): a row past Sk reads as zeros
     // (its key is masked), the thread's offset within a step is fixed and
-    // the step's offset k0 * HD * 2 goes in the scalar offset, so a step's
+    // the step's offset k0 * Hd * 2 goes in the scalar offset, so a step's
     // loads need no address arithmetic.
     const __amdgpu_buffer_rsrc_t rsK = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(Kh), 0,
-                                                                          (int)(p.Sk * HD * 2), 0x00020000);
+                                                                          (int)(p.Sk * D * 2), 0x00020000);
     const __amdgpu_buffer_rsrc_t rsV = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(Vh), 0,
-                                                                          (int)(p.Sk * HD * 2), 0x00020000);
+                                                                          (int)(p.Sk * D * 2), 0x00020000);
     auto gload = [&](KRegs &kr, VRegs &vr, uint32_t k0) {
-        const int so = (int)(k0 * HD * 2);
+        const int so = (int)(k0 * D * 2);
 #pragma unroll
         for (int i = 0; i < kKC; ++i) {
             const uint32_t c = threadIdx.x + i * 64 * kWaves;
             if (kChunks % (64 * kWaves) == 0 || c < (uint32_t)kChunks) {
                 const uint32_t key = c / (HD / 8), dc = (c % (HD / 8)) * 8;
-                kr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsK, (int)((key * HD + dc) * 2), so, 0));
+                const int off = dc < D ? (int)((key * D + dc) * 2) : kOutOfRange;
+                kr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsK, off, so, 0));
             }
         }
 #pragma unroll
@@ -313,9 +321,10 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
             if (kVP % (64 * kWaves) == 0 || pr < (uint32_t)kVP) {
                 const uint32_t kq = pr % (BKV / 4), db = pr / (BKV / 4);
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    vr[i][j] = __builtin_bit_cast(
-                        u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsV, (int)(((4 * kq + j) * HD + db * 8) * 2), so, 0));
+                for (int j = 0; j < 4; ++j) {
+                    const int off = db * 8 < D ? (int)(((4 * kq + j) * D + db * 8) * 2) : kOutOfRange;
+                    vr[i][j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsV, off, so, 0));
+                }
             }
         }
     };
@@ -469,9 +478,10 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
         posQ = (int)p.Sk - (int)p.Sq + (int)myq;
         posQ0 = (int)p.Sk - (int)p.Sq + (int)(qt * BQ + wave * 32);
         {
-            const uint16_t *qrow = Qh + (uint64_t)min(myq, p.Sq - 1) * HD + h * 8;
+            const uint16_t *qrow = Qh + (uint64_t)min(myq, p.Sq - 1) * D + h * 8;
 #pragma unroll
-            for (int s = 0; s < KS; ++s) qf[s] = *reinterpret_cast<const u32x4 *>(qrow + s * 16);
+            for (int s = 0; s < KS; ++s)
+                qf[s] = s * 16 + h * 8 < D ? *reinterpret_cast<const u32x4 *>(qrow + s * 16) : u32x4{0u, 0u, 0u, 0u};
         }
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
@@ -528,10 +538,11 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
         // be a separate memory transaction; value(dt, e) for accumulator
         // element e of acc[dt]
         auto store_dt = [&](int dt, auto &&value) {
-            typename O::storage *orow = out + ((uint64_t)bh * p.Sq + myq) * HD;
+            typename O::storage *orow = out + ((uint64_t)bh * p.Sq + myq) * D;
 #pragma unroll
             for (int i4 = 0; i4 < 4; ++i4) {
                 const uint32_t d = dt * 32 + i4 * 8 + h * 4;
+                if (d >= D) continue;  // padding dims of a kernel compiled for HD > Hd
                 const float v0 = value(dt, 4 * i4), v1 = value(dt, 4 * i4 + 1);
                 const float v2 = value(dt, 4 * i4 + 2), v3 = value(dt, 4 * i4 + 3);
                 if constexpr (std::is_same<O, pk::F32>::value) {
@@ -637,7 +648,6 @@ __device__ void fa_tiled(const uint16_t *__restrict__ Q, const uint16_t *__restr
 //    (vt16_pos), so a lane's Vt fragment is one 16-byte read;
 //  * K rows in LDS keep 16-byte chunk c of row r in slot c ^ (r % chunks),
 //    so the 16 rows a quarter-wave reads fall in 16 distinct bank groups.
-constexpr int kWaves16 = 8;
 
 __device__ inline uint32_t vt16_pos(uint32_t key) {
     return key < 16u ? (key >> 2) * 8u + (key & 3u) : ((key - 16u) >> 2) * 8u + 4u + (key & 3u);
@@ -645,7 +655,7 @@ __device__ inline uint32_t vt16_pos(uint32_t key) {
 __device__ inline float quad16_max(float v) { return pk::pair32_max(pk::pair16_max(v)); }
 __device__ inline float quad16_sum(float v) { return pk::pair32_sum(pk::pair16_sum(v)); }
 
-template <typename T, typename O, int HD>
+template <typename T, typename O, int HD, int NW>
 __device__ void fa_tiled16(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
                            const uint16_t *__restrict__ V, typename O::storage *__restrict__ out,
                            float *__restrict__ pO, float *__restrict__ pML, uint64_t *__restrict__ pairFlags,
@@ -653,7 +663,8 @@ __device__ void fa_tiled16(const uint16_t *__restrict__ Q, const uint16_t *__res
     constexpr int KS = HD / 32;   // k-steps of each S^T tile
     constexpr int DT = HD / 16;   // 16-row tiles of O^T
     constexpr int CH = HD / 8;    // 16-byte chunks per K row
-    constexpr int kThreads = 64 * kWaves16;
+    constexpr int kThreads = 64 * NW;
+    constexpr uint32_t BQ16 = 16 * NW;  // query rows per block
     constexpr bool kSplitP = std::is_same<T, pk::BF16>::value;
     static_assert(CH >= 16, "the K swizzle needs 16 chunks per row");
     __shared__ __attribute__((aligned(16))) uint16_t sK[2][BKV * HD];
@@ -662,13 +673,17 @@ __device__ void fa_tiled16(const uint16_t *__restrict__ Q, const uint16_t *__res
 
     const uint32_t lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const FaWork work = fa_work(p);
+    // Hd 512 runs every tile whole, one block each (no split or paired tiles:
+    // the merge paths' extra registers would spill)
+    constexpr bool kSplits = HD < 512;
+    const FaWork work = fa_work(p, BQ16, !kSplits);
     const uint32_t bh = work.bh;
     const uint32_t b = bh / p.Nq, hq = bh % p.Nq;
     const uint32_t hkv = hq / (p.Nq / p.Nkv);
     const uint32_t stride = p.kvStride ? p.kvStride : p.Sk;
-    const uint16_t *Qh = Q + (uint64_t)bh * p.Sq * HD;
-    const uint64_t kvoff = (uint64_t)(b * p.Nkv + hkv) * stride * HD;
+    const uint32_t D = p.Hd;  // runtime head dim (<= HD, a multiple of 8): rows are D apart
+    const uint16_t *Qh = Q + (uint64_t)bh * p.Sq * D;
+    const uint64_t kvoff = (uint64_t)(b * p.Nkv + hkv) * stride * D;
     uint32_t qt = 0, myq = 0;
     int posQ = 0, posQ0 = 0;
     const float c2 = p.scale * kLog2e;
@@ -684,19 +699,21 @@ __device__ void fa_tiled16(const uint16_t *__restrict__ Q, const uint16_t *__res
     constexpr int kVC = (kVP + kThreads - 1) / kThreads;
     using KRegs = u32x4[kKC];
     using VRegs = u32x4[kVC][2];
-    u32x4 krA[kKC], vrA[kVC][2], krB[kKC], vrB[kVC][2];
+    constexpr bool kOneSet = HD >= 512;
+    u32x4 krA[kKC], vrA[kVC][2], krB[kOneSet ? 1 : kKC], vrB[kOneSet ? 1 : kVC][2];
     const __amdgpu_buffer_rsrc_t rsK = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(K + kvoff), 0,
-                                                                          (int)(p.Sk * HD * 2), 0x00020000);
+                                                                          (int)(p.Sk * D * 2), 0x00020000);
     const __amdgpu_buffer_rsrc_t rsV = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(V + kvoff), 0,
-                                                                          (int)(p.Sk * HD * 2), 0x00020000);
+                                                                          (int)(p.Sk * D * 2), 0x00020000);
     auto gload = [&](KRegs &kr, VRegs &vr, uint32_t k0) {
-        const int so = (int)(k0 * HD * 2);
+        const int so = (int)(k0 * D * 2);
 #pragma unroll
         for (int i = 0; i < kKC; ++i) {
             const uint32_t c = threadIdx.x + i * kThreads;
             if ((BKV * CH) % kThreads == 0 || c < (uint32_t)(BKV * CH)) {
                 const uint32_t key = c / CH, ch = c % CH;
-                kr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsK, (int)((key * HD + ch * 8) * 2), so, 0));
+                const int off = ch * 8 < D ? (int)((key * D + ch * 8) * 2) : kOutOfRange;
+                kr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsK, off, so, 0));
             }
         }
 #pragma unroll
@@ -705,9 +722,10 @@ __device__ void fa_tiled16(const uint16_t *__restrict__ Q, const uint16_t *__res
             if (kVP % kThreads == 0 || pr < (uint32_t)kVP) {
                 const uint32_t kp = pr % (BKV / 2), db = pr / (BKV / 2);
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    vr[i][j] = __builtin_bit_cast(
-                        u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsV, (int)(((2 * kp + j) * HD + db * 8) * 2), so, 0));
+                for (int j = 0; j < 2; ++j) {
+                    const int off = db * 8 < D ? (int)(((2 * kp + j) * D + db * 8) * 2) : kOutOfRange;
+                    vr[i][j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsV, off, so, 0));
+                }
             }
         }
     };
@@ -821,25 +839,52 @@ __device__ void fa_tiled16(const uint16_t *__restrict__ Q, const uint16_t *__res
 
     auto item = [&](uint32_t w) {
         qt = work.qt[w];
-        myq = qt * BQ + wave * 16 + c16;
+        myq = qt * BQ16 + wave * 16 + c16;
         posQ = (int)p.Sk - (int)p.Sq + (int)myq;
-        posQ0 = (int)p.Sk - (int)p.Sq + (int)(qt * BQ + wave * 16);
+        posQ0 = (int)p.Sk - (int)p.Sq + (int)(qt * BQ16 + wave * 16);
         {
-            const uint16_t *qrow = Qh + (uint64_t)min(myq, p.Sq - 1) * HD + g * 8;
+            const uint16_t *qrow = Qh + (uint64_t)min(myq, p.Sq - 1) * D + g * 8;
 #pragma unroll
-            for (int s = 0; s < KS; ++s) qf[s] = *reinterpret_cast<const u32x4 *>(qrow + s * 32);
+            for (int s = 0; s < KS; ++s)
+                qf[s] = s * 32 + g * 8 < D ? *reinterpret_cast<const u32x4 *>(qrow + s * 32) : u32x4{0u, 0u, 0u, 0u};
         }
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) acc[dt] = pk::f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         m = -INFINITY;
         l = 0.0f;
         int kLo, kHi;
-        fa_key_range(p, qt, kLo, kHi);
+        fa_key_range(p, qt, kLo, kHi, BQ16);
         const uint32_t nSteps = kHi > kLo ? (uint32_t)(kHi - kLo + BKV - 1) / BKV : 0u;
         const uint32_t itLo = work.lo[w], itHi = min(work.hi[w], nSteps);
         // the double-buffered loop of fa_tiled: one barrier per step, a
         // step's loads two steps ahead of its LDS copy
-        if (itLo < itHi) {
+        if constexpr (kOneSet) {
+          if (itLo < itHi) {
+            // one register set (Hd 512: a step's products take twice as
+            // long, and the second set would not fit the registers): a
+            // step's loads go out one step before its LDS copy
+            auto kstep = [&](uint32_t it) { return (uint32_t)kLo + min(it, itHi - 1) * BKV; };
+            __syncthreads();
+            gload(krA, vrA, kstep(itLo));
+            lstore(krA, vrA, 0);
+            gload(krA, vrA, kstep(itLo + 1));
+            uint32_t it = itLo;
+            for (; it + 1 < itHi; it += 2) {
+                __syncthreads();
+                lstore(krA, vrA, 1);
+                gload(krA, vrA, kstep(it + 2));
+                compute(kstep(it), 0);
+                __syncthreads();
+                lstore(krA, vrA, 0);
+                gload(krA, vrA, kstep(it + 3));
+                compute(kstep(it + 1), 1);
+            }
+            if (it < itHi) {
+                __syncthreads();
+                compute(kstep(it), 0);
+            }
+          }
+        } else if (itLo < itHi) {
             auto kstep = [&](uint32_t it) { return (uint32_t)kLo + min(it, itHi - 1) * BKV; };
             __syncthreads();
             gload(krA, vrA, kstep(itLo));
@@ -870,10 +915,11 @@ __device__ void fa_tiled16(const uint16_t *__restrict__ Q, const uint16_t *__res
         // this lane's 4 consecutive dims of each 16-dim slice of its row,
         // value(dt, i) for dim dt * 16 + 4 g + i
         auto store_out = [&](auto &&value) {
-            typename O::storage *orow = out + ((uint64_t)bh * p.Sq + myq) * HD;
+            typename O::storage *orow = out + ((uint64_t)bh * p.Sq + myq) * D;
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
                 const uint32_t d = dt * 16 + g * 4;
+                if (d >= D) continue;  // padding dims of a kernel compiled for HD > Hd
                 const float v0 = value(dt, 0), v1 = value(dt, 1), v2 = value(dt, 2), v3 = value(dt, 3);
                 if constexpr (std::is_same<O, pk::F32>::value) {
                     *reinterpret_cast<float4 *>(orow + d) = float4{v0, v1, v2, v3};
@@ -883,7 +929,7 @@ __device__ void fa_tiled16(const uint16_t *__restrict__ Q, const uint16_t *__res
                 }
             }
         };
-        if (work.split[w] && p.pairTiles == 2u) {
+        if (kSplits && work.split[w] && p.pairTiles == 2u) {
             // A merged pair: the first block publishes its part of the split
             // tile (unnormalised O, then (m, l) per row, then the tile's
             // ready flag, set to this launch's ticket once every wave's
@@ -892,8 +938,8 @@ __device__ void fa_tiled16(const uint16_t *__restrict__ Q, const uint16_t *__res
             // its own, as fa_split_merge does.
             const uint32_t nSplit = p.qTilesPerHead - p.splitFrom;
             const uint32_t tile = bh * nSplit + (qt - p.splitFrom);
-            const uint32_t rowsTotal = p.B * p.Nq * nSplit * BQ;
-            const uint64_t row = (uint64_t)tile * BQ + wave * 16 + c16;
+            const uint32_t rowsTotal = p.B * p.Nq * nSplit * BQ16;
+            const uint64_t row = (uint64_t)tile * BQ16 + wave * 16 + c16;
             const uint64_t ticket = ((uint64_t)p.ticketHi << 32) | p.ticketLo;
             const __amdgpu_buffer_rsrc_t rsO =
                 __builtin_amdgcn_make_buffer_rsrc(pO, 0, (int)(rowsTotal * HD * 4u), 0x00020000);
@@ -931,9 +977,9 @@ __device__ void fa_tiled16(const uint16_t *__restrict__ Q, const uint16_t *__res
             }
         } else if (myq >= p.Sq) {
             // a row past Sq (ragged last tile) writes nothing
-        } else if (work.split[w]) {
+        } else if (kSplits && work.split[w]) {
             const uint32_t tile = (bh * (p.qTilesPerHead - p.splitFrom) + (qt - p.splitFrom)) * 2u + work.part[w];
-            const uint64_t row = (uint64_t)tile * BQ + wave * 16 + c16;
+            const uint64_t row = (uint64_t)tile * BQ16 + wave * 16 + c16;
             float *prow = pO + row * HD;
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt)
@@ -977,7 +1023,8 @@ __device__ void fa_split_merge(const float *__restrict__ pO, const float *__rest
         const float inv = L > 0.0f ? 1.0f / L : 0.0f;
         const float4 a = *reinterpret_cast<const float4 *>(pO + row0 * HD + d);
         const float4 c = *reinterpret_cast<const float4 *>(pO + row1 * HD + d);
-        typename O::storage *orow = out + ((uint64_t)bh * p.Sq + q) * HD + d;
+        if (d >= p.Hd) continue;  // padding dims of a kernel compiled for HD > Hd
+        typename O::storage *orow = out + ((uint64_t)bh * p.Sq + q) * p.Hd + d;
         orow[0] = O::store((w0 * a.x + w1 * c.x) * inv);
         orow[1] = O::store((w0 * a.y + w1 * c.y) * inv);
         orow[2] = O::store((w0 * a.z + w1 * c.z) * inv);
@@ -997,15 +1044,18 @@ __device__ void fa_split_merge(const float *__restrict__ pO, const float *__rest
     FA_TILED(flash_attention_tiled_##t##_##o##_d64, T, O, 64)    \
     FA_TILED(flash_attention_tiled_##t##_##o##_d128, T, O, 128)  \
     FA_TILED(flash_attention_tiled_##t##_##o##_d256, T, O, 256)
-#define FA_TILED16(name, T, O, HD)                                                                     \
-    POPCORN_KERNEL void __launch_bounds__(64 * kWaves16)                                               \
+#define FA_TILED16(name, T, O, HD, NW)                                                                 \
+    POPCORN_KERNEL void __launch_bounds__(64 * NW)                                                     \
         name(const uint16_t *q, const uint16_t *k, const uint16_t *v, O::storage *out, float *pO,      \
              float *pML, uint64_t *pairFlags, TiledFlashAttentionConstants p) {                        \
-        fa_tiled16<T, O, HD>(q, k, v, out, pO, pML, pairFlags, p);                                     \
+        fa_tiled16<T, O, HD, NW>(q, k, v, out, pO, pML, pairFlags, p);                                     \
     }
-#define FA_TILED16_D(t, T, o, O)                                      \
-    FA_TILED16(flash_attention_tiled16_##t##_##o##_d128, T, O, 128)   \
-    FA_TILED16(flash_attention_tiled16_##t##_##o##_d256, T, O, 256)
+// Hd 512 on 4 waves (64 query rows per block): a wave's output and query
+// fragments need up to 512 registers, one wave per SIMD
+#define FA_TILED16_D(t, T, o, O)                                         \
+    FA_TILED16(flash_attention_tiled16_##t##_##o##_d128, T, O, 128, 8)   \
+    FA_TILED16(flash_attention_tiled16_##t##_##o##_d256, T, O, 256, 8)   \
+    FA_TILED16(flash_attention_tiled16_##t##_##o##_d512, T, O, 512, 4)
 #define FA_MERGE(name, O, HD)                                                                          \
     POPCORN_KERNEL void __launch_bounds__(256)                                                         \
         name(const float *pO, const float *pML, O::storage *out, TiledFlashAttentionConstants p) {       \

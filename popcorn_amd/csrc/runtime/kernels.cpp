@@ -184,13 +184,14 @@ public:
             // POPCORN_FA_ROWS=32 selects the 32-row kernel there (a tuning
             // override)
             const char *e = std::getenv("POPCORN_FA_ROWS");
-            rows16_ = (d.Hd == 128 || d.Hd == 256) && !(e && std::string(e) == "32");
+            hdp_ = d.Hd <= 64 ? 64 : d.Hd <= 128 ? 128 : d.Hd <= 256 ? 256 : 512;
+            rows16_ = hdp_ == 512 || ((hdp_ == 128 || hdp_ == 256) && !(e && std::string(e) == "32"));
             // POPCORN_FA_PAIR_MERGE=0: paired tiles merged by the merge
             // kernel instead of the pair's second block (a tuning override)
             const char *pm = std::getenv("POPCORN_FA_PAIR_MERGE");
             pairMergeInKernel_ = !(pm && std::string(pm) == "0");
             tiledName_ = std::string(rows16_ ? "flash_attention_tiled16_" : "flash_attention_tiled_") + tag(q.dataType) +
-                         "_" + tag(out.dataType) + "_d" + std::to_string(d.Hd);
+                         "_" + tag(out.dataType) + "_d" + std::to_string(hdp_);
             planTileSplit();
         }
         planSplit();
@@ -219,7 +220,7 @@ public:
             c.Sq = (uint32_t)d_.Sq;
             c.Sk = (uint32_t)d_.Sk;
             c.Hd = (uint32_t)d_.Hd;
-            c.qTilesPerHead = (uint32_t)cdiv(d_.Sq, 128);
+            c.qTilesPerHead = (uint32_t)cdiv(d_.Sq, tileRows());
             c.maskKind = mask_.kind;
             c.slidingWindow = mask_.kind == 1 ? mask_.window : -1;
             c.scale = scale_;
@@ -244,12 +245,12 @@ public:
                 // uncached pair exchange; the second block of each pair
                 // merges, so no merge kernel
                 const int64_t tiles = d_.B * d_.Nq * nSplit_;
-                const size_t oBytes = (size_t)(tiles * 128 * d_.Hd) * 4;
+                const size_t oBytes = (size_t)(tiles * 128 * hdp_) * 4;
                 const PairExchange &x = pairExchange(enc.stream(), oBytes + (size_t)(tiles * 128 * 2) * 4);
                 const uint64_t ticket = nextTicket();
                 c.ticketLo = (uint32_t)ticket;
                 c.ticketHi = (uint32_t)(ticket >> 32);
-                Tensor pO(x.data, Shape({tiles * 128, d_.Hd}), DataType::f32);
+                Tensor pO(x.data, Shape({tiles * 128, hdp_}), DataType::f32);
                 Tensor pML(static_cast<uint8_t *>(x.data) + oBytes, Shape({tiles * 128 * 2}), DataType::f32);
                 Tensor flags(x.flags, Shape({(int64_t)PairExchange::kFlags}), DataType::u64);
                 FixedDispatch fa(tiledName_,
@@ -261,7 +262,7 @@ public:
             }
             // the two parts of each split tile: unnormalised O, then (m, l) per row
             const int64_t rows = d_.B * d_.Nq * nSplit_ * 2 * 128;
-            enc.withTemporaryTensor(ScratchSpec{{rows, d_.Hd}, DataType::f32}, [&](Tensor pO) {
+            enc.withTemporaryTensor(ScratchSpec{{rows, hdp_}, DataType::f32}, [&](Tensor pO) {
                 enc.withTemporaryTensor(ScratchSpec{{rows, 2}, DataType::f32}, [&](Tensor pML) {
                     FixedDispatch fa(tiledName_,
                                      {{q_, kRead}, {k_, kRead}, {v_, kRead}, {out_, kWrite}, {pO, kWrite}, {pML, kWrite},
@@ -365,13 +366,14 @@ private:
         pairTiles_ = false;
         const int64_t nQT = cdiv(d_.Sq, 128);
         const int64_t tiles = d_.B * d_.Nq * nQT;
-        if (mask_.kind != 0 || nQT < 4 || tiles > 2 * (int64_t)deviceCUs()) return;
+        // the Hd 512 kernel runs every tile whole
+        if (hdp_ == 512 || mask_.kind != 0 || nQT < 4 || tiles > 2 * (int64_t)deviceCUs()) return;
         auto steps = [&](int64_t qt) {
             const int64_t last = d_.Sk - d_.Sq + std::min(qt * 128 + 127, d_.Sq - 1);
             const int64_t hi = std::min(d_.Sk, last + 1);
             return hi > 0 ? cdiv(hi, 32) : int64_t(0);
         };
-        mergeName_ = std::string("flash_attention_split_merge_") + tag(out_.dataType) + "_d" + std::to_string(d_.Hd);
+        mergeName_ = std::string("flash_attention_split_merge_") + tag(out_.dataType) + "_d" + std::to_string(hdp_);
         bool pairs = tiles <= (int64_t)deviceCUs();
         for (int64_t i = 0; pairs && i < nQT / 2; ++i) {
             const int64_t sa = steps(i), sb = steps(nQT - 1 - i);
@@ -411,8 +413,10 @@ private:
     std::string partialName_, reduceName_, tiledName_, mergeName_;
     int64_t nSplit_ = 0;
     bool pairTiles_ = false;
-    bool rows16_ = false;  // the 16-rows-per-wave kernel: 8 waves per 128-row tile
-    int64_t tiledBlock() const { return rows16_ ? 512 : kBlock; }
+    bool rows16_ = false;  // the 16-rows-per-wave kernel: 8 waves per 128-row tile (4 per 64 at Hd 512)
+    int64_t hdp_ = 0;      // the tiled kernel's head dim: Hd padded to 64, 128, 256 or 512
+    int64_t tiledBlock() const { return hdp_ == 512 ? 256 : rows16_ ? 512 : kBlock; }
+    int64_t tileRows() const { return hdp_ == 512 ? 64 : 128; }
     // Paired tiles are merged inside the tiled kernels (pairTiles 2).
     bool pairMergeInKernel_ = true;
     bool mergedPairs() const { return pairTiles_ && pairMergeInKernel_; }
@@ -1133,7 +1137,10 @@ namespace Kernels {
 AttentionPath route(int64_t queryLen, int64_t headDim, DataType qType) {
     if (queryLen == 1) return AttentionPath::decoding;
     const bool sixteen = qType == DataType::f16 || qType == DataType::bf16;
-    if (queryLen >= 32 && sixteen && (headDim == 64 || headDim == 128 || headDim == 256)) return AttentionPath::tiled;
+    // the matrix-core kernels take any head dim up to 512 in 16-byte rows,
+    // padded to 64, 128, 256 or 512 inside (MPPFlashAttention's hd256 and
+    // hd512 buckets, FlashAttention.swift:305-311)
+    if (queryLen >= 32 && sixteen && headDim <= 512 && headDim % 8 == 0) return AttentionPath::tiled;
     return AttentionPath::plain;
 }
 

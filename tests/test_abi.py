@@ -67,6 +67,26 @@ def test_route():
     assert pa.Kernels.route(2, 256) == "plain"
 
 
+def test_prefill_attention_head_dims():
+    # Sq >= 32 and any 16-bit head dim up to 512 in 16-byte rows take the
+    # matrix cores (the reference's MPP route, FlashAttention.swift:109-113,
+    # hd256/hd512 buckets :305-311), padded to the kernel's 64/128/256/512
+    def fa(Hd, S=640, dtype="bf16", out=None):
+        q = T([1, 2, S, Hd], dtype)
+        return pa.Kernels.FlashAttention(q, q, q, out=T([1, 2, S, Hd], out or dtype), scale=0.1,
+                                         batch=1, query_heads=2, kv_heads=2, query_len=S, key_len=S,
+                                         head_dim=Hd).function_names
+    assert fa(512) == ["flash_attention_tiled16_bf16_bf16_d512"]          # whole tiles, no merge
+    assert fa(512, S=4096) == ["flash_attention_tiled16_bf16_bf16_d512"]
+    assert fa(512, out="f32") == ["flash_attention_tiled16_bf16_f32_d512"]
+    assert fa(320, dtype="f16") == ["flash_attention_tiled16_f16_f16_d512"]
+    assert fa(192) == ["flash_attention_tiled16_bf16_bf16_d256"]
+    assert fa(80) == ["flash_attention_tiled16_bf16_bf16_d128"]
+    assert fa(40) == ["flash_attention_tiled_bf16_bf16_d64"]
+    assert fa(8) == ["flash_attention_tiled_bf16_bf16_d64"]
+    assert fa(36)[0].startswith("flash_decoding_partial_")   # not 16-byte rows: the per-row kernel
+
+
 def test_prefill_attention_split_plan():
     # causal prefill with at most two 128-row tiles per CU (256 CUs when no
     # GPU answers). At most one tile per CU: light and heavy tiles paired,
@@ -342,7 +362,10 @@ def test_prefill_routes_to_tiled():
     assert pa.Kernels.route(2048, 256, "f16") == "tiled"
     assert pa.Kernels.route(32, 64, "bf16") == "tiled"
     assert pa.Kernels.route(31, 64, "bf16") == "plain"
-    assert pa.Kernels.route(2048, 80, "f16") == "plain"
+    assert pa.Kernels.route(2048, 80, "f16") == "tiled"
+    assert pa.Kernels.route(2048, 512, "bf16") == "tiled"
+    assert pa.Kernels.route(2048, 36, "f16") == "plain"     # rows not in 16-byte chunks
+    assert pa.Kernels.route(2048, 520, "f16") == "plain"
     assert pa.Kernels.route(2048, 256, "f32") == "plain"
     assert pa.Kernels.route(1, 256, "f16") == "decoding"
     q = T([1, 16, 2048, 256], "f16")

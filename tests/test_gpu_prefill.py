@@ -179,6 +179,80 @@ def test_tiled_attention_vs_oracle(env, rows, dtype, ot, B, Nq, Nkv, Sq, Sk, Hd,
     assert_out(got, ref, EPS[dtype], ot, f"tiled attention {dtype}->{ot} {mask} Sq={Sq} Sk={Sk} Hd={Hd}")
 
 
+def _tiled_any(dtype, ot, Hd, rows):
+    # the kernel of a head dim padded to 64, 128, 256 or 512
+    hdp = 64 if Hd <= 64 else 128 if Hd <= 128 else 256 if Hd <= 256 else 512
+    kind = "tiled16" if hdp == 512 or (hdp in (128, 256) and rows == "rows16") else "tiled"
+    return f"flash_attention_{kind}_{dtype}_{ot}_d{hdp}"
+
+
+@pytest.mark.parametrize("dtype,ot", [("f16", "f16"), ("f16", "f32"), ("bf16", "bf16"), ("bf16", "f32")])
+@pytest.mark.parametrize("B,Nq,Nkv,Sq,Sk,Hd,mask", [
+    (1, 2, 1, 130, 200, 512, "causal"),        # Gemma-4 global head dim: GQA, Sq < Sk, ragged tiles
+    (1, 2, 2, 96, 96, 512, "bidirectional"),
+    (1, 2, 1, 128, 160, 512, "window40"),
+    (1, 4, 2, 300, 300, 320, "causal"),        # padded to 512
+    (2, 4, 2, 70, 90, 80, "causal"),           # padded to 128
+    (1, 2, 1, 64, 100, 192, "window40"),       # padded to 256
+    (1, 2, 2, 40, 40, 40, "bidirectional"),    # padded to 64
+    (1, 2, 1, 33, 33, 8, "causal"),
+])
+def test_tiled_attention_any_head_dim_vs_oracle(env, rows, dtype, ot, B, Nq, Nkv, Sq, Sk, Hd, mask):
+    # the matrix-core route for every 16-bit head dim up to 512 in 16-byte
+    # rows (the reference's MPP route takes any Hd <= 512 with Sq >= 32,
+    # FlashAttention.swift:109-113, in hd256/hd512 buckets :305-311): the
+    # kernel's dims past Hd are zeros and its stores stop at Hd. The output
+    # starts as NaN with guard rows after it, so a skipped or stray store fails.
+    pa, lib, stream, enc = env
+    kind, window = MASKS[mask]
+    q = rounded(O.normal(Sq + Hd + 5, (B, Nq, Sq, Hd)), dtype)
+    k = rounded(O.normal(Sk + Hd + 6, (B, Nkv, Sk, Hd)), dtype)
+    v = rounded(O.normal(Sk + Hd + 7, (B, Nkv, Sk, Hd)), dtype)
+    scale = 1 / np.sqrt(Hd)
+    n = B * Nq * Sq * Hd
+    buf = upload(pa, np.full(n + 64, np.nan, np.float32), ot)
+    to = buf.view([B, Nq, Sq, Hd])
+    kern = pa.Kernels.FlashAttention(upload(pa, q, dtype), upload(pa, k, dtype), upload(pa, v, dtype), out=to,
+                                     scale=scale, mask=pa.AttentionMask(kind, window), batch=B, query_heads=Nq,
+                                     kv_heads=Nkv, query_len=Sq, key_len=Sk, head_dim=Hd)
+    assert kern.function_names == [_tiled_any(dtype, ot, Hd, rows)]
+    enc.encode(kern)
+    stream.synchronize()
+    out = download(buf, stream)
+    assert np.isnan(out[n:]).all(), "stores past the output"
+    got = out[:n].reshape(B, Nq, Sq, Hd)
+    assert not np.isnan(got).any()
+    ref = O.attention_naive(q, k, v, scale, mask_kind=kind, window=window)
+    assert_out(got, ref, EPS[dtype], ot, f"tiled attention {dtype}->{ot} {mask} Sq={Sq} Sk={Sk} Hd={Hd}")
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_tiled_attention_hd512_sampled(env, dtype):
+    # a Gemma-4-shaped global-attention prefill: [1, 8, 2048, 512], GQA 2:1,
+    # causal, scale 1/sqrt(512): 32 tiles of 64 rows per head. Sampled query
+    # rows against the oracle over keys 0..r, from a NaN-filled output.
+    pa, lib, stream, enc = env
+    Nq, Nkv, S, Hd = 8, 4, 2048, 512
+    tq = pa.Tensor.empty([1, Nq, S, Hd], dtype)
+    tk, tv = (pa.Tensor.empty([1, Nkv, S, Hd], dtype) for _ in range(2))
+    for i, t in enumerate((tq, tk, tv)):
+        lib.fill_normal(t, 50 + i, stream=stream)
+    to = upload(pa, np.full((1, Nq, S, Hd), np.nan, np.float32), dtype)
+    scale = 1 / np.sqrt(Hd)
+    kern = pa.Kernels.FlashAttention(tq, tk, tv, out=to, scale=scale, batch=1, query_heads=Nq, kv_heads=Nkv,
+                                     query_len=S, key_len=S, head_dim=Hd)
+    assert kern.function_names == [f"flash_attention_tiled16_{dtype}_{dtype}_d512"]
+    enc.encode(kern)
+    stream.synchronize()
+    q = download(tq, stream).reshape(1, Nq, S, Hd)
+    k, v = (download(t, stream).reshape(1, Nkv, S, Hd) for t in (tk, tv))
+    got = download(to, stream).reshape(1, Nq, S, Hd)
+    assert not np.isnan(got).any()
+    for r in (0, 63, 64, 1000, 2047):
+        ref = O.attention_naive(q[:, :, r:r + 1], k[:, :, :r + 1].copy(), v[:, :, :r + 1].copy(), scale)
+        assert_out(got[:, :, r:r + 1], ref, EPS[dtype], dtype, f"Hd 512 {dtype} row {r}")
+
+
 @pytest.mark.parametrize("dtype,ot", [("f16", "f16"), ("bf16", "bf16"), ("bf16", "f32")])
 @pytest.mark.parametrize("B,Nq,Nkv,Sq,Sk,Hd", [
     (1, 2, 1, 512, 512, 64),
