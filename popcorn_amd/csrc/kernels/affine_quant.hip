@@ -14,7 +14,6 @@ namespace {
 using pk::BF16;
 using pk::F32;
 using pk::kQ4Group;
-using pk::Q4Row;
 using pk::Q4Staging;
 using pk::Q4Stream;
 using pk::u32x4;
@@ -26,7 +25,7 @@ constexpr uint32_t maxK() { return 2048u * J; }
 
 // The J octets (8 values) of x this thread stages, loaded into registers
 // before the weight stream starts (loads retire in issue order); octets past
-// the row re-read its last octet and are not used.
+// the row load nothing and are not used.
 template <typename X, int J>
 struct XOctets {
     static constexpr int kPieces = sizeof(typename X::storage) * 8 / 16;  // 16-byte loads per octet
@@ -35,7 +34,8 @@ struct XOctets {
         const uint32_t octets = K / 8;
 #pragma unroll
         for (int j = 0; j < J; ++j) {
-            const uint32_t o = min(threadIdx.x + pk::kStreamThreads * (uint32_t)j, octets - 1);
+            const uint32_t o = threadIdx.x + pk::kStreamThreads * (uint32_t)j;
+            if (o >= octets) continue;
 #pragma unroll
             for (int h = 0; h < kPieces; ++h) v[j][h] = *reinterpret_cast<const u32x4 *>(x + (uint64_t)o * 8 + h * (8 / kPieces));
         }
@@ -70,21 +70,20 @@ __device__ void aq_matvec(const uint32_t *__restrict__ W, const uint16_t *__rest
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t units = (p.N + kRows - 1) / kRows;
     const uint16_t *B = p.hasBias ? Bi : Sc;
-    auto rows = [&](uint32_t unit, int) {
-        const uint32_t r = min(unit * kRows + lane / LPR, p.N - 1);
-        return Q4Row{W + (uint64_t)r * p.wordsPerRow, Sc + (uint64_t)r * p.kGroups, B + (uint64_t)r * p.kGroups};
-    };
+    auto rowOf = [&](uint32_t unit) { return min(unit * kRows + lane / LPR, p.N - 1); };
+    const pk::Q4Mat mats[1] = {{W, Sc, B}};
     XOctets<X, J> xo;
     xo.issue(x + (uint64_t)m * p.K, p.K);
     Q4Stream<LPR, 1, pk::kStreamSteps, XF32> st;
-    st.init(rows, p.K, units, blockIdx.x * pk::kStreamWaves + wave, gridDim.x * pk::kStreamWaves, p.hasBias != 0);
-    st.start(rows);
+    st.init(rowOf, mats, p.N, p.K, units, blockIdx.x * pk::kStreamWaves + wave, gridDim.x * pk::kStreamWaves,
+            p.hasBias != 0);
+    st.start(rowOf);
     Q4Staging<XF32>::build(p.K, xw, xf, gsum, [&](uint32_t j, uint32_t, float *v) { xo.get(min(j, (uint32_t)J - 1), v); });
     auto store = [&](uint32_t unit, const float *sums) {
         const uint32_t r = unit * kRows + lane / LPR;
-        if (lane % LPR == 0 && r < p.N) y[(uint64_t)m * p.N + r] = O::store(sums[0]);
+        if (lane % LPR == 0 && lane / LPR < kRows && r < p.N) y[(uint64_t)m * p.N + r] = O::store(sums[0]);
     };
-    st.run(xw, xf, gsum, rows, store);
+    st.run(xw, xf, gsum, rowOf, store);
 }
 
 // AffineQuantizedEmbeddingGather.metal:16-26, one thread per packed word (8
@@ -256,15 +255,13 @@ __device__ void q4_decode_matvec(const uint16_t *__restrict__ x_in, const uint16
     const uint32_t units = (N + kRows - 1) / kRows;
     const uint32_t first = blockIdx.x * pk::kStreamWaves + wave, stride = gridDim.x * pk::kStreamWaves;
     const uint16_t *B = q.hasBias ? Bi : Sc;
-    auto rows = [&](uint32_t unit, int) {
-        const uint32_t r = min(unit * kRows + lane / LPR, N - 1);
-        return Q4Row{W + (uint64_t)r * q.wordsPerRow, Sc + (uint64_t)r * q.kGroups, B + (uint64_t)r * q.kGroups};
-    };
+    auto rowOf = [&](uint32_t unit) { return min(unit * kRows + lane / LPR, N - 1); };
+    const pk::Q4Mat mats[1] = {{W, Sc, B}};
     const bool scatter = (p.flags & pk::kKVScatter) != 0;
     const int32_t posLoaded = pk::load_position(position, scatter);
     auto store = [&](uint32_t unit, const float *sums) {
         const uint32_t row = unit * kRows + lane / LPR;
-        if (lane % LPR != 0 || row >= N) return;
+        if (lane % LPR != 0 || lane / LPR >= kRows || row >= N) return;
         if (scatter && row >= p.qRows) {
             uint32_t j = row - p.qRows;
             const bool isV = j >= p.kvRows;
@@ -283,22 +280,27 @@ __device__ void q4_decode_matvec(const uint16_t *__restrict__ x_in, const uint16
     if (!Stage::fast_ok(x_in, delta, w_post, w_pre, x_out, K, 1u)) {
         Stage::finish_scalar(L.xs, red, x_in, delta, w_post, w_pre, x_out, K, 1u, p.eps, p.interDataType);
         L.stage_from_xs(K);
-        st.init(rows, K, units, first, stride, q.hasBias != 0);
-        st.start(rows);
-        st.run(L.xw, nullptr, L.gsum, rows, store);
+        st.init(rowOf, mats, N, K, units, first, stride, q.hasBias != 0);
+        st.start(rowOf);
+        st.run(L.xw, nullptr, L.gsum, rowOf, store);
         return;
     }
     Stage stage;
     stage.issue(x_in, delta, w_post, w_pre, K);
-    st.init(rows, K, units, first, stride, q.hasBias != 0);
-    st.start(rows);
+    st.init(rowOf, mats, N, K, units, first, stride, q.hasBias != 0);
+    st.start(rowOf);
     stage.finish(L.xs, red, x_out, K, 1u, p.eps, p.interDataType);
     L.stage_from_xs(K);
-    st.run(L.xw, nullptr, L.gsum, rows, store);
+    st.run(L.xw, nullptr, L.gsum, rowOf, store);
 }
 
 // The gated-MLP front half (GatedMLPConstants; gated_mlp.hip's semantics)
 // with Wg and Wu block-affine 4-bit: each lane streams the same row of both.
+// Each wave issues one step of its weight loads before the vector is built
+// and the rest after: the block's barriers wait for every wave's issued
+// loads, and under a full memory pipeline a wave's issue stalls (with all
+// steps issued first, the vector was ready only once nearly all of the
+// block's stream had arrived, and the dot products could not start before).
 template <int LPR, bool RES>
 __device__ void q4_gate_up(const uint16_t *__restrict__ x, const float *__restrict__ norm_w,
                            const uint32_t *__restrict__ Wg, const uint16_t *__restrict__ Sg, const uint16_t *__restrict__ Bg,
@@ -316,14 +318,11 @@ __device__ void q4_gate_up(const uint16_t *__restrict__ x, const float *__restri
     const uint32_t preMode = p.hasWeight ? (p.addOneToWeight ? 2u : 1u) : 0u;
     const uint32_t inter = p.interDataType;
     const uint16_t *BgB = q.hasBias ? Bg : Sg, *BuB = q.hasBias ? Bu : Su;
-    auto rows = [&](uint32_t unit, int s) {
-        const uint64_t r = min(unit * kRows + lane / LPR, F - 1);
-        return s == 0 ? Q4Row{Wg + r * q.wordsPerRow, Sg + r * q.kGroups, BgB + r * q.kGroups}
-                      : Q4Row{Wu + r * q.wordsPerRow, Su + r * q.kGroups, BuB + r * q.kGroups};
-    };
+    auto rowOf = [&](uint32_t unit) { return min(unit * kRows + lane / LPR, F - 1); };
+    const pk::Q4Mat mats[2] = {{Wg, Sg, BgB}, {Wu, Su, BuB}};
     auto store = [&](uint32_t unit, const float *sums) {
         const uint32_t row = unit * kRows + lane / LPR;
-        if (lane % LPR != 0 || row >= F) return;
+        if (lane % LPR != 0 || lane / LPR >= kRows || row >= F) return;
         const float g = pk::round_through(inter, sums[0]);
         const float u = pk::round_through(inter, sums[1]);
         const float a = pk::round_through(inter, pk::gelu_tanh(g));
@@ -334,18 +333,19 @@ __device__ void q4_gate_up(const uint16_t *__restrict__ x, const float *__restri
     if (!Stage::fast_ok(x, delta, w_post, norm_w, x_out, H, preMode)) {
         Stage::finish_scalar(L.xs, red, x, delta, w_post, norm_w, x_out, H, preMode, p.eps, inter);
         L.stage_from_xs(H);
-        st.init(rows, H, units, first, stride, q.hasBias != 0);
-        st.start(rows);
-        st.run(L.xw, nullptr, L.gsum, rows, store);
+        st.init(rowOf, mats, F, H, units, first, stride, q.hasBias != 0);
+        st.start(rowOf);
+        st.run(L.xw, nullptr, L.gsum, rowOf, store);
         return;
     }
     Stage stage;
     stage.issue(x, delta, w_post, norm_w, H);
-    st.init(rows, H, units, first, stride, q.hasBias != 0);
-    st.start(rows);
+    st.init(rowOf, mats, F, H, units, first, stride, q.hasBias != 0);
+    st.template start<0, 1>(rowOf);
     stage.finish(L.xs, red, x_out, H, preMode, p.eps, inter);
     L.stage_from_xs(H);
-    st.run(L.xw, nullptr, L.gsum, rows, store);
+    st.template start<1>(rowOf);
+    st.run(L.xw, nullptr, L.gsum, rowOf, store);
 }
 
 }  // namespace
@@ -370,6 +370,7 @@ __device__ void q4_gate_up(const uint16_t *__restrict__ x, const float *__restri
     }
 #define Q4_ALL(LPR) Q4_DMV_F(bf16, BF16, LPR) Q4_DMV_F(f32, F32, LPR) Q4_GU(LPR, , false) Q4_GU(LPR, _res, true)
 Q4_ALL(8)
+Q4_ALL(12)
 Q4_ALL(16)
 Q4_ALL(32)
 
@@ -381,8 +382,9 @@ Q4_ALL(32)
     }
 // bf16 x: J 2 (K <= 4096) and 8 (K <= 16384); f32 x: J 2 (K <= 4096, 16 KB
 // of LDS; larger K takes the any-shape kernel)
-#define AQ_MV_L(prefix, xt, ot, X, O, J) \
-    AQ_MV(prefix, xt, ot, X, O, 8, J) AQ_MV(prefix, xt, ot, X, O, 16, J) AQ_MV(prefix, xt, ot, X, O, 32, J)
+#define AQ_MV_L(prefix, xt, ot, X, O, J)                                                                 \
+    AQ_MV(prefix, xt, ot, X, O, 8, J) AQ_MV(prefix, xt, ot, X, O, 12, J) AQ_MV(prefix, xt, ot, X, O, 16, J) \
+        AQ_MV(prefix, xt, ot, X, O, 32, J)
 #define AQ_MV_ALL(prefix)                                                                  \
     AQ_MV_L(prefix, bf16, bf16, BF16, BF16, 2) AQ_MV_L(prefix, bf16, bf16, BF16, BF16, 8) \
     AQ_MV_L(prefix, bf16, f32, BF16, F32, 2) AQ_MV_L(prefix, bf16, f32, BF16, F32, 8)     \

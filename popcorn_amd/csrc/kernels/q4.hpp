@@ -87,24 +87,54 @@ struct Q4Staging {
     }
 };
 
-// The rows of a unit as seen by one lane: its row's packed words, scales and
-// biases (biases == scales when the tensor has none; hasBias says so). The
-// scale and bias rows start 4-byte aligned (an even number of groups per row).
-struct Q4Row {
+// One 4-bit matrix of N rows: its packed words, scales and biases (biases ==
+// scales when the tensor has none; hasBias says so). Read through buffer
+// resources with 32-bit byte offsets, so each array stays under 2 GB (the
+// host checks); the scale and bias rows start 4-byte aligned (an even number
+// of groups per row).
+struct Q4Mat {
     const uint32_t *w;
     const uint16_t *s;
     const uint16_t *b;
 };
 
+// A buffer load at this byte offset is out of range: it returns zeros and
+// reads no memory.
+constexpr uint32_t kQ4OutOfRange = 0x80000000u;
+
 // Streams units of kRows = 64 / LPR rows through a wave: lane l serves row
 // l / LPR of the unit and groups g = l % LPR + LPR i of that row, one group
 // (two 16-byte loads of words, one scale, one bias) per step; NS rows (of NS
-// weight matrices, same row index) per lane. U steps stay in flight and each
-// slot is refilled as soon as it is consumed (in issue order, as in
-// RowStream). A unit's per-row results are summed over its LPR lanes.
+// weight matrices of one shape, same row index) per lane. U steps stay in
+// flight and each slot is refilled as soon as it is consumed (in issue
+// order, as in RowStream). A unit's per-row results are summed over its LPR
+// lanes.
+// The sum over the LPR lanes of a row, in the row's first lane (LPR a power
+// of two: in every lane of the row). LPR that is not a power of two is a
+// multiple of 4, so rows start on quad boundaries: quads sum over DPP, and
+// the row's first lane adds its row's other quads through ds_bpermute.
+template <int LPR>
+__device__ inline float row_sum(float v) {
+    if constexpr ((LPR & (LPR - 1)) == 0) {
+        return group_sum<LPR>(v);
+    } else {
+        static_assert(LPR % 4 == 0, "a row of lanes starts on a quad");
+        const float q = group_sum<4>(v);
+        const int lane = (int)(threadIdx.x & 63);
+        float t = q;
+#pragma unroll
+        for (int k = 1; k < LPR / 4; ++k)
+            t += __int_as_float(__builtin_amdgcn_ds_bpermute(((lane + 4 * k) & 63) * 4, __float_as_int(q)));
+        return t;
+    }
+}
+
+// Streams units of kRows = 64 / LPR rows through a wave (lanes past kRows x
+// LPR idle: they read a valid row, and their sums are not stored).
 template <int LPR, int NS, int U, bool XF32>
 struct Q4Stream {
-    static_assert(LPR >= 4 && LPR <= 64 && (LPR & (LPR - 1)) == 0, "LPR is a power of two in [4, 64]");
+    static_assert(LPR >= 4 && LPR <= 64 && ((LPR & (LPR - 1)) == 0 || LPR % 4 == 0),
+                  "LPR is a power of two or a multiple of 4 in [4, 64]");
     static constexpr int kRows = 64 / LPR;
     u32x4 wv[U][NS][2];
     // Scale and bias of the step's group, as the aligned 32-bit word that
@@ -114,15 +144,18 @@ struct Q4Stream {
     // extension included) makes the compiler wait for the load right there,
     // and as loads retire in order the whole queue would drain.
     uint32_t sv[U][NS], bv[U][NS];
-    Q4Row ip[NS];
+    __amdgpu_buffer_rsrc_t rw[NS], rs[NS], rb[NS];
     uint32_t G, cpl, steps, first, stride, is, ii, iu, gl;
+    uint32_t orow, srow;  // byte offsets of this lane's row of the unit being issued (words, scales)
     bool hasBias;
     // The nibble-pair mask and the bf16 (128, 128) base, held in registers so
     // that each pair is one v_and_or_b32 (which cannot take two literals).
     uint32_t pairMask, pairBase;
 
-    template <class Rows>
-    __device__ void init(const Rows &rows, uint32_t K, uint32_t units, uint32_t first_, uint32_t stride_, bool hasBias_) {
+    // rowOf(unit): this lane's row of the unit (clamped to N - 1 by the caller).
+    template <class RowOf>
+    __device__ void init(const RowOf &rowOf, const Q4Mat (&m)[NS], uint32_t N, uint32_t K, uint32_t units,
+                         uint32_t first_, uint32_t stride_, bool hasBias_) {
         asm volatile("v_mov_b32 %0, 0x000f000f" : "=v"(pairMask));
         asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(pairBase));
         G = K / kQ4Group;
@@ -136,40 +169,57 @@ struct Q4Stream {
         is = 0;
         ii = 0;
         iu = first;
-#pragma unroll
-        for (int s = 0; s < NS; ++s) ip[s] = rows(iu, s);
-    }
-
-    // Once every step is issued the last one is loaded again, so every path
-    // has the same loads in flight (exact wait counts, as in RowStream).
-    template <class Rows>
-    __device__ inline void issue(int slot, const Rows &rows) {
-        const uint32_t g = min(gl + LPR * ii, G - 1);
+        const int wordBytes = (int)(N * (K / 8) * 4u), scaleBytes = (int)(N * G * 2u);
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
-            const uint32_t *p = ip[s].w + (uint64_t)g * kQ4GroupWords;
-            wv[slot][s][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
-            wv[slot][s][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p + 4));
-            sv[slot][s] = reinterpret_cast<const uint32_t *>(ip[s].s)[g >> 1];
-            bv[slot][s] = reinterpret_cast<const uint32_t *>(ip[s].b)[g >> 1];
+            rw[s] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t *>(m[s].w), 0, wordBytes, 0x00020000);
+            rs[s] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(m[s].s), 0, scaleBytes, 0x00020000);
+            rb[s] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(m[s].b), 0, scaleBytes, 0x00020000);
         }
-        if (is + 1 < steps) {
+        set_row(rowOf(iu));
+    }
+
+    __device__ inline void set_row(uint32_t row) {
+        orow = row * (G * kQ4GroupWords * 4u);
+        srow = row * (G * 2u);
+    }
+
+    // Loads step `is` into `slot`. Once every step is issued, a slot is
+    // filled from out-of-range offsets instead (zeros, no memory read), so
+    // every path through the kernel issues the same loads and the compiler's
+    // wait counts stay exact.
+    template <class RowOf>
+    __device__ inline void issue(int slot, const RowOf &rowOf) {
+        const bool real = is < steps;
+        const uint32_t g = min(gl + LPR * ii, G - 1);
+        const uint32_t ow = real ? orow + g * (kQ4GroupWords * 4u) : kQ4OutOfRange;
+        const uint32_t os = real ? srow + (g >> 1) * 4u : kQ4OutOfRange;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            wv[slot][s][0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw[s], ow, 0, 2));
+            wv[slot][s][1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw[s], ow + 16u, 0, 2));
+            sv[slot][s] = __builtin_amdgcn_raw_buffer_load_b32(rs[s], os, 0, 0);
+            bv[slot][s] = __builtin_amdgcn_raw_buffer_load_b32(rb[s], os, 0, 0);
+        }
+        if (real) {
             ++is;
             if (++ii == cpl) {
                 ii = 0;
                 iu += stride;
-#pragma unroll
-                for (int s = 0; s < NS; ++s) ip[s] = rows(iu, s);
+                if (is < steps) set_row(rowOf(iu));
             }
-        } else {
-            is = steps;
         }
     }
 
-    template <class Rows>
-    __device__ void start(const Rows &rows) {
+    // Issues slots FROM .. TO - 1 (all of them by default). A kernel that
+    // builds its vector with block barriers in between issues a first slot
+    // before and the rest after: a wave whose loads back up in the memory
+    // pipeline stalls at the issue, and the barrier would wait for the
+    // slowest wave's last load, i.e. for nearly all of the block's stream.
+    template <int FROM = 0, int TO = U, class RowOf>
+    __device__ void start(const RowOf &rowOf) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) issue(u, rows);
+        for (int u = FROM; u < TO; ++u) issue(u, rowOf);
     }
 
     __device__ static inline uint32_t word(const u32x4 (&w)[2], int j) {
@@ -226,7 +276,7 @@ struct Q4Stream {
             float sums[NS];
 #pragma unroll
             for (int s = 0; s < NS; ++s) {
-                sums[s] = group_sum<LPR>(acc[s]);
+                sums[s] = row_sum<LPR>(acc[s]);
                 acc[s] = 0.0f;
             }
             store(cu, sums);
@@ -235,8 +285,8 @@ struct Q4Stream {
         }
     }
 
-    template <class Rows, class Store>
-    __device__ void run(const uint32_t *xw, const float *xf, const float *gsum, const Rows &rows, Store &store) {
+    template <class RowOf, class Store>
+    __device__ void run(const uint32_t *xw, const float *xf, const float *gsum, const RowOf &rowOf, Store &store) {
         float acc[NS];
 #pragma unroll
         for (int s = 0; s < NS; ++s) acc[s] = 0.0f;
@@ -245,7 +295,7 @@ struct Q4Stream {
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 consume(u, xw, xf, gsum, acc, ci, cu, store);
-                issue(u, rows);
+                issue(u, rowOf);
             }
             cs += U;
         }
@@ -253,7 +303,7 @@ struct Q4Stream {
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 if (cs + u < steps) consume(u, xw, xf, gsum, acc, ci, cu, store);
-                issue(u, rows);
+                issue(u, rowOf);
             }
             cs += U;
         }

@@ -122,13 +122,17 @@ struct Stage {
         return (K % E) == 0 && K / E <= (uint32_t)(kStreamThreads * J) && (al % 16) == 0 && (!PRE || preMode != 0u);
     }
 
-    // Every thread issues all J runs' loads; runs past K / E re-read the
-    // last run (same addresses as a valid thread) and are not used.
+    // Each thread loads its runs q < K / E; a run past the end loads nothing
+    // (its registers are not read): a re-read of a valid run instead would
+    // cost the memory pipeline as much as a real load (at K 2304, 288 runs
+    // over 2 x 256 threads, 44% of the loads would be such re-reads).
     __device__ void issue(const S *x_in, const S *delta, const float *w_post, const float *w_pre, uint32_t K) {
         const uint32_t runs = K / E, tid = threadIdx.x;
 #pragma unroll
         for (int j = 0; j < J; ++j) {
-            const uint64_t at = (uint64_t)min(tid + (uint32_t)(kStreamThreads * j), runs - 1) * E;
+            const uint32_t q = tid + (uint32_t)(kStreamThreads * j);
+            if (q >= runs) continue;
+            const uint64_t at = (uint64_t)q * E;
             xv[j].load(x_in + at);
             if constexpr (RES) {
                 dv[j].load(delta + at);

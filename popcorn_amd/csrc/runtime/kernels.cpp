@@ -618,12 +618,15 @@ int64_t streamBlocks(int64_t units) {
     return cdiv(cdiv(units, per), kBlock / 64);
 }
 
-// The 4-bit fast kernels' launch shape: lanes per row LPR (8, 16 or 32; a
-// unit is 64 / LPR rows and a row's K / 64 groups are dealt to its LPR
-// lanes, one group per lane and step) and x octets per thread J (2 or 8).
-// LPR minimises the steps of the busiest wave, units per wave x steps per
-// unit, at the grid's waves per CU: short matrices want many small units,
-// long ones full lanes. Ties go to the higher lane occupancy.
+// The 4-bit fast kernels' launch shape: lanes per row LPR (8, 12, 16 or 32;
+// a unit is floor(64 / LPR) rows and a row's K / 64 groups are dealt to its
+// LPR lanes, one group per lane and step) and x octets per thread J (2 or
+// 8). LPR minimises the steps of the busiest SIMD, waves per SIMD x units
+// per wave x steps per unit, at the grid's waves per CU (the 4-bit inner
+// loop is bound by its vector ALU work): short matrices want many small
+// units, long ones full lanes (12 lanes fit rows of 36 groups, K 2304, in 3
+// whole steps, where 16 lanes take 3 steps with a quarter of them idle).
+// Ties go to the higher lane occupancy.
 struct Q4Shape {
     int lpr = 0, j = 0;
 };
@@ -632,16 +635,19 @@ Q4Shape q4Shape(int64_t N, int64_t K, bool xF32) {
     Q4Shape q;
     const int64_t G = K / 64;
     const int64_t kMax = xF32 ? 4096 : 16384;
-    // the fast kernels read a row's scales and biases as 32-bit words
-    if (N <= 0 || G <= 0 || G % 2 != 0 || K > kMax) return q;
+    // the fast kernels read a row's scales and biases as 32-bit words, and
+    // the packed words through 32-bit byte offsets
+    if (N <= 0 || G <= 0 || G % 2 != 0 || K > kMax || N * (K / 2) >= (int64_t{1} << 31)) return q;
     q.j = K <= 4096 ? 2 : 8;
     const int64_t waves = (int64_t)deviceCUs() * streamWavesPerCU();
     int64_t bestSteps = INT64_MAX;
     double bestEff = 0.0;
-    for (int lpr : {32, 16, 8}) {
-        const int64_t cpl = cdiv(G, lpr);
-        const int64_t steps = cdiv(cdiv(N, 64 / lpr), waves) * cpl;
-        const double eff = (double)G / (double)(lpr * cpl);
+    const int64_t simds = (int64_t)deviceCUs() * 4;
+    for (int lpr : {32, 16, 12, 8}) {
+        const int64_t cpl = cdiv(G, lpr), rows = 64 / lpr, units = cdiv(N, rows);
+        const int64_t used = std::min(units, waves);
+        const int64_t steps = cdiv(used, simds) * cdiv(units, used) * cpl;
+        const double eff = (double)G / (double)(lpr * cpl) * (double)(rows * lpr) / 64.0;
         if (steps < bestSteps || (steps == bestSteps && eff > bestEff)) {
             bestSteps = steps;
             bestEff = eff;

@@ -271,10 +271,10 @@ def test_quantized_validation_and_routing():
         assert e.value.code == code
     w = _q4(9216, 2304)
     out = T([1, 9216], "bf16", FAKE + 2 ** 20)
-    assert pa.Kernels.Matmul(T([1, 2304]), w, out).describe() == "aq_qmv_fast_bf16_bf16_bf16_b4_g64_l16_j2"
-    assert pa.Kernels.Matmul(T([4, 2304]), w, T([4, 9216], "f32")).describe() == "aq_matvec_simd4_bf16_bf16_f32_b4_g64_l16_j2"
+    assert pa.Kernels.Matmul(T([1, 2304]), w, out).describe() == "aq_qmv_fast_bf16_bf16_bf16_b4_g64_l12_j2"
+    assert pa.Kernels.Matmul(T([4, 2304]), w, T([4, 9216], "f32")).describe() == "aq_matvec_simd4_bf16_bf16_f32_b4_g64_l12_j2"
     down = _q4(2304, 9216)
-    assert pa.Kernels.Matmul(T([1, 9216]), down, T([1, 2304])).describe() == "aq_qmv_fast_bf16_bf16_bf16_b4_g64_l32_j8"
+    assert pa.Kernels.Matmul(T([1, 9216]), down, T([1, 2304])).describe() == "aq_qmv_fast_bf16_bf16_bf16_b4_g64_l16_j8"
     # unaligned activations or f32 x past 4096 take the any-shape kernel
     assert pa.Kernels.Matmul(T([1, 2304], ptr=FAKE + 2), w, out).describe() == "aq_matvec_simd4_bf16_bf16_bf16_b4_g64"
     assert pa.Kernels.Matmul(T([1, 9216], "f32"), down, T([1, 2304], "f32")).describe() == \
