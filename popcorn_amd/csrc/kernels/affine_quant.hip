@@ -77,8 +77,9 @@ __device__ void aq_matvec(const uint32_t *__restrict__ W, const uint16_t *__rest
     Q4Stream<LPR, 1, pk::kStreamSteps, XF32> st;
     st.init(rowOf, mats, p.N, p.K, units, blockIdx.x * pk::kStreamWaves + wave, gridDim.x * pk::kStreamWaves,
             p.hasBias != 0);
-    st.start(rowOf);
+    st.template start<0, 1>(rowOf);  // one step before the staging barrier (see q4_gate_up)
     Q4Staging<XF32>::build(p.K, xw, xf, gsum, [&](uint32_t j, uint32_t, float *v) { xo.get(min(j, (uint32_t)J - 1), v); });
+    st.template start<1>(rowOf);
     auto store = [&](uint32_t unit, const float *sums) {
         const uint32_t r = unit * kRows + lane / LPR;
         if (lane % LPR == 0 && lane / LPR < kRows && r < p.N) y[(uint64_t)m * p.N + r] = O::store(sums[0]);
