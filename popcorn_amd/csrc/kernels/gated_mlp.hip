@@ -37,7 +37,9 @@ __device__ void gate_up(const typename T::storage *__restrict__ x, const float *
     const uint32_t units = (F + R - 1) / R;
     const uint32_t wave = pk::uniform(threadIdx.x >> 6);
     const uint32_t first = blockIdx.x * kStreamWaves + wave, stride = gridDim.x * kStreamWaves;
-    const bool vec = (H % kV) == 0 && ((reinterpret_cast<uintptr_t>(wg) | reinterpret_cast<uintptr_t>(wu)) % 16) == 0;
+    const uint64_t wbytes = (uint64_t)F * H * sizeof(typename T::storage);
+    const bool vec = (H % kV) == 0 && ((reinterpret_cast<uintptr_t>(wg) | reinterpret_cast<uintptr_t>(wu)) % 16) == 0 &&
+                     wbytes < (1ull << 31);
     const uint32_t preMode = p.hasWeight ? (p.addOneToWeight ? 2u : 1u) : 0u;
     const uint32_t inter = p.interDataType;
     auto rows = [&](uint32_t unit, int s) {
@@ -65,7 +67,11 @@ __device__ void gate_up(const typename T::storage *__restrict__ x, const float *
     Stage stage;
     stage.issue(x, delta, w_post, norm_w, H);
     pk::RowStream<T, S, U> rs;
-    rs.init(rows, H, units, first, stride);
+    typename pk::RowStream<T, S, U>::Ptr base[S];
+    uint64_t bytes[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) base[s] = s < R ? wg : wu, bytes[s] = wbytes;
+    rs.init(rows, base, bytes, H, units, first, stride);
     rs.start(rows);
     stage.finish(xs, red, x_out, H, preMode, p.eps, inter);
     rs.run(xs, rows, store);

@@ -45,7 +45,8 @@ __device__ void matvec_nk(const typename X::storage *__restrict__ x_in, const ty
     const uint32_t units = (N + R - 1) / R;
     const uint32_t wave = pk::uniform(threadIdx.x >> 6);
     const uint32_t first = blockIdx.x * kStreamWaves + wave, stride = gridDim.x * kStreamWaves;
-    const bool vec = (K % kV) == 0 && (reinterpret_cast<uintptr_t>(w) % 16) == 0;
+    const uint64_t wbytes = (uint64_t)N * K * sizeof(typename W::storage);
+    const bool vec = (K % kV) == 0 && (reinterpret_cast<uintptr_t>(w) % 16) == 0 && wbytes < (1ull << 31);
     const bool scatter = (p.flags & pk::kKVScatter) != 0;
     const int32_t posLoaded = pk::load_position(position, scatter);
     auto rows = [&](uint32_t unit, int s) { return w + (uint64_t)min(unit * R + s, N - 1) * K; };
@@ -80,7 +81,11 @@ __device__ void matvec_nk(const typename X::storage *__restrict__ x_in, const ty
     Stage stage;
     stage.issue(x_in, delta, w_post, w_pre, K);
     pk::RowStream<W, R, U> rs;
-    rs.init(rows, K, units, first, stride);
+    typename pk::RowStream<W, R, U>::Ptr base[R];
+    uint64_t bytes[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) base[r] = w, bytes[r] = wbytes;
+    rs.init(rows, base, bytes, K, units, first, stride);
     rs.start(rows);
     stage.finish(xs, red, x_out, K, 1u, p.eps, p.interDataType);
     rs.run(xs, rows, store);

@@ -271,17 +271,25 @@ struct Stage {
 };
 
 // ---- RowStream -----------------------------------------------------------------
+// Rows are read through buffer resources, one per row stream s over the
+// matrix that holds its rows (`base[s]`, `bytes[s]` long, under 2 GB: the
+// kernels check), with 32-bit byte offsets.
+constexpr uint32_t kOutOfRange = 0x80000000u;  // a buffer load there returns zeros and reads no memory
+
 template <typename W, int S, int U>
 struct RowStream {
     static constexpr int kV = Vec<W>::kVec;
     using Ptr = const typename W::storage *;
     Vec<W> buf[U][S];
-    Ptr iptr[S];
+    __amdgpu_buffer_rsrc_t rsrc[S];
+    Ptr bases[S];
+    uint32_t ioff[S];  // byte offsets of the rows of the unit being issued
     uint32_t nchunks, cpl, steps, first, stride;
     uint32_t is, ii, iu;  // issue cursor: steps issued, step within unit, unit
 
     template <class Rows>
-    __device__ void init(const Rows &rows, uint32_t K, uint32_t units, uint32_t first_, uint32_t stride_) {
+    __device__ void init(const Rows &rows, const Ptr (&base)[S], const uint64_t (&bytes)[S], uint32_t K, uint32_t units,
+                         uint32_t first_, uint32_t stride_) {
         nchunks = K / kV;
         cpl = (nchunks + 63) / 64;
         first = first_;
@@ -292,28 +300,40 @@ struct RowStream {
         ii = 0;
         iu = first;
 #pragma unroll
-        for (int s = 0; s < S; ++s) iptr[s] = rows(iu, s);
+        for (int s = 0; s < S; ++s) {
+            bases[s] = base[s];
+            rsrc[s] = __builtin_amdgcn_make_buffer_rsrc(const_cast<typename W::storage *>(base[s]), 0, (int)bytes[s],
+                                                        0x00020000);
+        }
+        set_unit(rows, iu);
     }
 
-    // Loads step `is` into `slot`. Once every step is issued it loads the
-    // last step again (lines just fetched), so that every path through the
-    // kernel has the same number of loads in flight and the compiler's wait
-    // counts stay exact.
+    template <class Rows>
+    __device__ inline void set_unit(const Rows &rows, uint32_t unit) {
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+            ioff[s] = (uint32_t)(reinterpret_cast<const char *>(rows(unit, s)) - reinterpret_cast<const char *>(bases[s]));
+    }
+
+    // Loads step `is` into `slot`. Once every step is issued, a slot is
+    // filled from out-of-range offsets instead (zeros, no memory read), so
+    // that every path through the kernel issues the same loads and the
+    // compiler's wait counts stay exact.
     template <class Rows>
     __device__ inline void issue(int slot, const Rows &rows) {
-        const uint32_t c = min((threadIdx.x & 63) + 64 * ii, nchunks - 1);
+        const bool real = is < steps;
+        const uint32_t c = min((threadIdx.x & 63) + 64 * ii, nchunks - 1) * 16u;
 #pragma unroll
-        for (int s = 0; s < S; ++s) buf[slot][s].load_nt(iptr[s] + (uint64_t)c * kV);
-        if (is + 1 < steps) {
+        for (int s = 0; s < S; ++s)
+            buf[slot][s].raw = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc[s], real ? ioff[s] + c : kOutOfRange, 0, 2));
+        if (real) {
             ++is;
             if (++ii == cpl) {
                 ii = 0;
                 iu += stride;
-#pragma unroll
-                for (int s = 0; s < S; ++s) iptr[s] = rows(iu, s);
+                if (is < steps) set_unit(rows, iu);
             }
-        } else {
-            is = steps;
         }
     }
 
