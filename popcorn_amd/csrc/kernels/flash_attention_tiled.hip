@@ -994,6 +994,204 @@ __device__ void fa_tiled16(const uint16_t *__restrict__ Q, const uint16_t *__res
     if (work.n > 1) item(1);
 }
 
+// ---- f32 Q, K, V --------------------------------------------------------------------
+// The reference's mpp_flash_attention_f32 (FlashAttention.swift:368-376,
+// MPPFlashAttention.metal:251-256) on v_mfma_f32_16x16x4_f32, whose
+// operands are single floats (lane l: A[l % 16][l / 16], B[l / 16][l % 16];
+// C rows 4 (l / 16) + i, column l % 16). The tiles, masks, item order and
+// lazy rescale are the 16-bit kernel's, every tile whole; a wave owns 16
+// query rows and a step takes 16 keys. Per step:
+//  * S^T = K . Q^T (16 keys x 16 queries) in HD / 4 products; product
+//    4 j + s takes dim 16 j + 4 (l / 16) + s from every lane, so a lane
+//    feeds four consecutive products from one 16-byte K read (LDS) and one
+//    16-byte chunk of its Q row (registers);
+//  * lane l then holds the scores of query l % 16 for keys 4 (l / 16) + i;
+//    ordering the keys of product s of P.V as 4 (l / 16) + s makes score s
+//    the lane's own B operand, and the A operand V^T[dim][4 (l / 16) + s]
+//    one 16-byte read of a Vt row for the four products.
+// LDS rows are padded (K by 4 floats, Vt to 20) so the 16 rows a
+// quarter-wave reads fall in distinct banks. Dims past the runtime Hd (a
+// multiple of 4) and keys past Sk read as zeros (buffer loads out of range).
+template <int HD, int NW>
+__device__ void fa_tiled_f32(const float *__restrict__ Q, const float *__restrict__ K, const float *__restrict__ V,
+                             float *__restrict__ out, const TiledFlashAttentionConstants &p) {
+    constexpr int BK = 16;          // keys per step
+    constexpr int DC = HD / 16;     // 16-byte chunks of a lane's Q row, and 16-dim tiles of O^T
+    constexpr int LDK = HD + 4;     // sK row stride (floats)
+    constexpr int LDT = BK + 4;     // sV (transposed: a row per dim) row stride
+    constexpr int kThreads = 64 * NW;
+    constexpr uint32_t BQ16 = 16 * NW;  // query rows per block
+    constexpr int kChunks = BK * HD / 4;  // 16-byte chunks of K (and of V) per step
+    constexpr int kC = (kChunks + kThreads - 1) / kThreads;
+    constexpr bool kOneSet = HD >= 512;
+    __shared__ __attribute__((aligned(16))) float sK[2][BK * LDK];
+    __shared__ __attribute__((aligned(16))) float sV[2][HD * LDT];
+
+    const uint32_t lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const FaWork work = fa_work(p, BQ16, true);
+    const uint32_t bh = work.bh;
+    const uint32_t b = bh / p.Nq, hq = bh % p.Nq;
+    const uint32_t hkv = hq / (p.Nq / p.Nkv);
+    const uint32_t stride = p.kvStride ? p.kvStride : p.Sk;
+    const uint32_t D = p.Hd;
+    const uint64_t kvoff = (uint64_t)(b * p.Nkv + hkv) * stride * D;
+    const uint32_t qt = work.qt[0];
+    const uint32_t myq = qt * BQ16 + wave * 16 + c16;
+    const int posQ = (int)p.Sk - (int)p.Sq + (int)myq;
+    const int posQ0 = (int)p.Sk - (int)p.Sq + (int)(qt * BQ16 + wave * 16);
+    const float c2 = p.scale * kLog2e;
+
+    using Regs = u32x4[kC];
+    Regs krA, vrA, krB, vrB;
+    const __amdgpu_buffer_rsrc_t rsK = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(K + kvoff), 0,
+                                                                          (int)(p.Sk * D * 4), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsV = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(V + kvoff), 0,
+                                                                          (int)(p.Sk * D * 4), 0x00020000);
+    // K chunk c: key c / (HD / 4), dims 4 (c % (HD / 4)) ..; V chunk c: key
+    // c % 16, dims 4 (c / 16) .. (a wave's transposed stores then cover 64
+    // distinct banks)
+    // (the step's first key enters the vector offset, which the range check
+    // covers, so keys past Sk read as zeros whatever the cache holds there)
+    auto gload = [&](Regs &kr, Regs &vr, uint32_t k0) {
+#pragma unroll
+        for (int i = 0; i < kC; ++i) {
+            const uint32_t c = threadIdx.x + i * kThreads;
+            if (kChunks % kThreads == 0 || c < (uint32_t)kChunks) {
+                const uint32_t kk = c / (HD / 4), kd = (c % (HD / 4)) * 4;
+                const uint32_t vk = c % BK, vd = (c / BK) * 4;
+                const int ko = kd < D ? (int)(((k0 + kk) * D + kd) * 4) : kOutOfRange;
+                const int vo = vd < D ? (int)(((k0 + vk) * D + vd) * 4) : kOutOfRange;
+                kr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsK, ko, 0, 0));
+                vr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsV, vo, 0, 0));
+            }
+        }
+    };
+    auto lstore = [&](const Regs &kr, const Regs &vr, int buf) {
+#pragma unroll
+        for (int i = 0; i < kC; ++i) {
+            const uint32_t c = threadIdx.x + i * kThreads;
+            if (kChunks % kThreads == 0 || c < (uint32_t)kChunks) {
+                const uint32_t kk = c / (HD / 4), kd = (c % (HD / 4)) * 4;
+                const uint32_t vk = c % BK, vd = (c / BK) * 4;
+                *reinterpret_cast<u32x4 *>(&sK[buf][kk * LDK + kd]) = kr[i];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) sV[buf][(vd + e) * LDT + vk] = __uint_as_float(vr[i][e]);
+            }
+        }
+    };
+
+    pk::f32x4 qf[DC], acc[DC];
+    {
+        const float *qrow = Q + ((uint64_t)bh * p.Sq + min(myq, p.Sq - 1)) * D + g * 4;
+#pragma unroll
+        for (int j = 0; j < DC; ++j)
+            qf[j] = j * 16 + g * 4 < D ? *reinterpret_cast<const pk::f32x4 *>(qrow + j * 16) : pk::f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+#pragma unroll
+    for (int dt = 0; dt < DC; ++dt) acc[dt] = pk::f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m = -INFINITY, l = 0.0f;
+
+    auto compute = [&](uint32_t k0, int buf) {
+        pk::f32x4 st = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < DC; ++j) {
+            const pk::f32x4 kf = *reinterpret_cast<const pk::f32x4 *>(&sK[buf][c16 * LDK + j * 16 + g * 4]);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) st = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[s], qf[j][s], st, 0, 0, 0);
+            if (kOneSet && j % 4 == 3) __builtin_amdgcn_sched_barrier(0);
+        }
+        const bool full = (int)k0 + BK <= (int)p.Sk && (p.maskKind == 2u || (int)k0 + BK - 1 <= posQ0) &&
+                          (p.maskKind != 1u || posQ0 + 15 - (int)k0 < (int)p.slidingWindow);
+        float sv[4];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            sv[i] = full || fa_allowed(p, posQ, (int)k0 + (int)g * 4 + i) ? st[i] : -INFINITY;
+            mx = fmaxf(mx, sv[i]);
+        }
+        mx = quad16_max(mx) * c2;
+        const bool move = mx > m + kRescaleGap * kLog2e;
+        float alpha = 1.0f;
+        if (move) {
+            const float mn = fmaxf(m, mx);
+            alpha = __builtin_amdgcn_exp2f(m - mn);
+            m = mn;
+        }
+        if (__ballot(move)) {
+#pragma unroll
+            for (int dt = 0; dt < DC; ++dt) acc[dt] *= alpha;
+        }
+        float pv[4], ps = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            pv[i] = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(fmaf(sv[i], c2, -m));
+            ps += pv[i];
+        }
+        l = l * alpha + quad16_sum(ps);
+#pragma unroll
+        for (int dt = 0; dt < DC; ++dt) {
+            const pk::f32x4 va = *reinterpret_cast<const pk::f32x4 *>(&sV[buf][(dt * 16 + c16) * LDT + g * 4]);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) acc[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(va[s], pv[s], acc[dt], 0, 0, 0);
+            if (kOneSet && dt % 4 == 3) __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    int kLo, kHi;
+    fa_key_range(p, qt, kLo, kHi, BQ16);
+    const uint32_t nSteps = kHi > kLo ? (uint32_t)(kHi - kLo + BK - 1) / BK : 0u;
+    // the double-buffered loop of the 16-bit kernels: one barrier per step;
+    // a step's loads go out two steps (one at Hd 512, one register set)
+    // before its LDS copy
+    if (nSteps > 0) {
+        auto kstep = [&](uint32_t it) { return (uint32_t)kLo + min(it, nSteps - 1) * BK; };
+        uint32_t it = 0;
+        if constexpr (kOneSet) {
+            gload(krA, vrA, kstep(0));
+            lstore(krA, vrA, 0);
+            gload(krA, vrA, kstep(1));
+            for (; it + 1 < nSteps; it += 2) {
+                __syncthreads();
+                lstore(krA, vrA, 1);
+                gload(krA, vrA, kstep(it + 2));
+                compute(kstep(it), 0);
+                __syncthreads();
+                lstore(krA, vrA, 0);
+                gload(krA, vrA, kstep(it + 3));
+                compute(kstep(it + 1), 1);
+            }
+        } else {
+            gload(krA, vrA, kstep(0));
+            gload(krB, vrB, kstep(1));
+            lstore(krA, vrA, 0);
+            gload(krA, vrA, kstep(2));
+            for (; it + 1 < nSteps; it += 2) {
+                __syncthreads();
+                lstore(krB, vrB, 1);
+                gload(krB, vrB, kstep(it + 3));
+                compute(kstep(it), 0);
+                __syncthreads();
+                lstore(krA, vrA, 0);
+                gload(krA, vrA, kstep(it + 4));
+                compute(kstep(it + 1), 1);
+            }
+        }
+        if (it < nSteps) {
+            __syncthreads();
+            compute(kstep(it), 0);
+        }
+    }
+    if (myq >= p.Sq) return;  // a row past Sq (ragged last tile) writes nothing
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    float *orow = out + ((uint64_t)bh * p.Sq + myq) * D;
+#pragma unroll
+    for (int dt = 0; dt < DC; ++dt) {
+        const uint32_t d = dt * 16 + g * 4;
+        if (d < D) *reinterpret_cast<float4 *>(orow + d) = float4{acc[dt][0] * inv, acc[dt][1] * inv, acc[dt][2] * inv, acc[dt][3] * inv};
+    }
+}
+
 // Combine of a split tile's two halves (maxima in log2 units):
 //   M = max(m0, m1), w_i = 2^(m_i - M) (0 for a half with no visible key),
 //   O = (w0 O0 + w1 O1) / (w0 l0 + w1 l1),
@@ -1056,7 +1254,16 @@ __device__ void fa_split_merge(const float *__restrict__ pO, const float *__rest
     FA_TILED16(flash_attention_tiled16_##t##_##o##_d128, T, O, 128, 8)   \
     FA_TILED16(flash_attention_tiled16_##t##_##o##_d256, T, O, 256, 8)   \
     FA_TILED16(flash_attention_tiled16_##t##_##o##_d512, T, O, 512, 4)
-#define FA_MERGE(name, O, HD)                                                                          \
+// f32: 8 waves (128 query rows) per block, 4 (64 rows) at Hd 512, where a
+// wave's Q chunks and accumulators take 256 registers; the partial-state
+// arguments are never read (every tile whole)
+#define FA_TILED_F32(name, HD, NW)                                                                     \
+    POPCORN_KERNEL void __launch_bounds__(64 * NW)                                                     \
+        name(const float *q, const float *k, const float *v, float *out, float *, float *, uint64_t *, \
+             TiledFlashAttentionConstants p) {                                                         \
+        fa_tiled_f32<HD, NW>(q, k, v, out, p);                                                         \
+    }
+#define FA_MERGE(name, O, HD)                                                                       \
     POPCORN_KERNEL void __launch_bounds__(256)                                                         \
         name(const float *pO, const float *pML, O::storage *out, TiledFlashAttentionConstants p) {       \
         fa_split_merge<O, HD>(pO, pML, out, p);                                                        \
@@ -1081,3 +1288,7 @@ FA_TILED16_D(bf16, BF16, f32, F32)
 FA_MERGE_D(f16, F16)
 FA_MERGE_D(bf16, BF16)
 FA_MERGE_D(f32, F32)
+FA_TILED_F32(flash_attention_tiled16_f32_f32_d64, 64, 8)
+FA_TILED_F32(flash_attention_tiled16_f32_f32_d128, 128, 8)
+FA_TILED_F32(flash_attention_tiled16_f32_f32_d256, 256, 8)
+FA_TILED_F32(flash_attention_tiled16_f32_f32_d512, 512, 4)

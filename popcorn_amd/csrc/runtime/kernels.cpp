@@ -177,7 +177,7 @@ public:
         if (path_ == Kernels::AttentionPath::tiled &&
             (hasPos_ || !aligned16(q.data) || !aligned16(k.data) || !aligned16(v.data) || !aligned16(out.data) ||
              !(out.dataType == q.dataType || out.dataType == DataType::f32) || !(scale > 0.0f) ||
-             d.Sk * d.Hd * 2 >= (int64_t{1} << 31)))
+             d.Sk * d.Hd * (int64_t)stride(q.dataType) >= (int64_t{1} << 31)))
             path_ = Kernels::AttentionPath::plain;
         if (path_ == Kernels::AttentionPath::tiled) {
             // Hd 128 and 256 run 16 query rows per wave (two waves per SIMD);
@@ -185,7 +185,9 @@ public:
             // override)
             const char *e = std::getenv("POPCORN_FA_ROWS");
             hdp_ = d.Hd <= 64 ? 64 : d.Hd <= 128 ? 128 : d.Hd <= 256 ? 256 : 512;
-            rows16_ = hdp_ == 512 || ((hdp_ == 128 || hdp_ == 256) && !(e && std::string(e) == "32"));
+            // f32 has only the 16-row kernel (v_mfma_f32_16x16x4_f32)
+            rows16_ = q.dataType == DataType::f32 || hdp_ == 512 ||
+                      ((hdp_ == 128 || hdp_ == 256) && !(e && std::string(e) == "32"));
             // POPCORN_FA_PAIR_MERGE=0: paired tiles merged by the merge
             // kernel instead of the pair's second block (a tuning override)
             const char *pm = std::getenv("POPCORN_FA_PAIR_MERGE");
@@ -366,8 +368,8 @@ private:
         pairTiles_ = false;
         const int64_t nQT = cdiv(d_.Sq, 128);
         const int64_t tiles = d_.B * d_.Nq * nQT;
-        // the Hd 512 kernel runs every tile whole
-        if (hdp_ == 512 || mask_.kind != 0 || nQT < 4 || tiles > 2 * (int64_t)deviceCUs()) return;
+        // the Hd 512 and f32 kernels run every tile whole
+        if (hdp_ == 512 || q_.dataType == DataType::f32 || mask_.kind != 0 || nQT < 4 || tiles > 2 * (int64_t)deviceCUs()) return;
         auto steps = [&](int64_t qt) {
             const int64_t last = d_.Sk - d_.Sq + std::min(qt * 128 + 127, d_.Sq - 1);
             const int64_t hi = std::min(d_.Sk, last + 1);
@@ -1137,16 +1139,17 @@ void AffineQuantizedTensor::validate() const {
 namespace Kernels {
 
 // FlashAttention.swift:109-113: one query row -> split-KV decoding; 32 rows
-// or more of 16-bit data with a head dim the MFMA kernel has (64, 128, 256)
-// -> the tiled kernel (where the reference takes MPP); otherwise the plain
-// per-row kernel.
+// or more with a head dim up to 512 -> the tiled kernel on the matrix cores
+// (where the reference takes MPP); otherwise the plain per-row kernel.
 AttentionPath route(int64_t queryLen, int64_t headDim, DataType qType) {
     if (queryLen == 1) return AttentionPath::decoding;
     const bool sixteen = qType == DataType::f16 || qType == DataType::bf16;
     // the matrix-core kernels take any head dim up to 512 in 16-byte rows,
     // padded to 64, 128, 256 or 512 inside (MPPFlashAttention's hd256 and
-    // hd512 buckets, FlashAttention.swift:305-311)
-    if (queryLen >= 32 && sixteen && headDim <= 512 && headDim % 8 == 0) return AttentionPath::tiled;
+    // hd512 buckets, FlashAttention.swift:305-311), in f16, bf16 and f32
+    const int64_t perChunk = sixteen ? 8 : 4;
+    if (queryLen >= 32 && (sixteen || qType == DataType::f32) && headDim <= 512 && headDim % perChunk == 0)
+        return AttentionPath::tiled;
     return AttentionPath::plain;
 }
 

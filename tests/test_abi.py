@@ -366,11 +366,18 @@ def test_prefill_routes_to_tiled():
     assert pa.Kernels.route(2048, 512, "bf16") == "tiled"
     assert pa.Kernels.route(2048, 36, "f16") == "plain"     # rows not in 16-byte chunks
     assert pa.Kernels.route(2048, 520, "f16") == "plain"
-    assert pa.Kernels.route(2048, 256, "f32") == "plain"
+    assert pa.Kernels.route(2048, 256, "f32") == "tiled"     # v_mfma_f32_16x16x4_f32
+    assert pa.Kernels.route(2048, 36, "f32") == "tiled"      # f32 rows in 16-byte chunks
+    assert pa.Kernels.route(2048, 34, "f32") == "plain"
+    assert pa.Kernels.route(31, 256, "f32") == "plain"
     assert pa.Kernels.route(1, 256, "f16") == "decoding"
     q = T([1, 16, 2048, 256], "f16")
     k = pa.Kernels.FlashAttention(q, q, q, out=T([1, 16, 2048, 256], "f16", ptr=FAKE + 2 ** 32), scale=1 / 16)
     assert k.function_names == ["flash_attention_tiled16_f16_f16_d256"]
+    for hd, hdp in ((64, 64), (80, 128), (256, 256), (320, 512)):
+        qf = T([1, 4, 256, hd], "f32")
+        kf = pa.Kernels.FlashAttention(qf, qf, qf, out=T([1, 4, 256, hd], "f32", ptr=FAKE + 2 ** 32), scale=0.1)
+        assert kf.function_names == [f"flash_attention_tiled16_f32_f32_d{hdp}"]
 
 
 # Reference kernels outside the decode hot path (the reference's own unfused

@@ -226,6 +226,104 @@ def test_tiled_attention_any_head_dim_vs_oracle(env, rows, dtype, ot, B, Nq, Nkv
     assert_out(got, ref, EPS[dtype], ot, f"tiled attention {dtype}->{ot} {mask} Sq={Sq} Sk={Sk} Hd={Hd}")
 
 
+@pytest.mark.parametrize("B,Nq,Nkv,Sq,Sk,cap,Hd,mask", [
+    (1, 2, 1, 64, 64, 64, 64, "causal"),
+    (2, 4, 2, 130, 200, 207, 128, "causal"),     # GQA, Sq < Sk, ragged tiles, key capacity > Sk
+    (1, 2, 2, 96, 96, 96, 256, "bidirectional"),
+    (1, 2, 1, 128, 160, 160, 64, "window40"),
+    (1, 2, 1, 130, 200, 200, 512, "causal"),
+    (1, 2, 2, 96, 96, 96, 512, "bidirectional"),
+    (1, 2, 1, 128, 160, 160, 512, "window40"),
+    (1, 4, 2, 300, 300, 300, 320, "causal"),     # padded to 512
+    (2, 4, 2, 70, 90, 90, 80, "causal"),         # padded to 128
+    (1, 2, 1, 64, 100, 100, 192, "window40"),    # padded to 256
+    (1, 2, 2, 40, 40, 40, 36, "bidirectional"),  # padded to 64
+    (1, 2, 1, 33, 33, 33, 4, "causal"),
+])
+def test_tiled_attention_f32_vs_oracle(env, B, Nq, Nkv, Sq, Sk, cap, Hd, mask):
+    # f32 Q, K, V on v_mfma_f32_16x16x4_f32, the role of the reference's
+    # mpp_flash_attention_f32 (FlashAttention.swift:368-376) for any Hd <= 512
+    # in 16-byte rows: f32 products and sums in another order than the
+    # oracle's, so the f32 bar. The output starts as NaN with guard elements
+    # after it, so a skipped or stray store fails.
+    pa, lib, stream, enc = env
+    kind, window = MASKS[mask]
+    q = O.normal(Sq + Hd + 15, (B, Nq, Sq, Hd))
+    k = O.normal(Sk + Hd + 16, (B, Nkv, cap, Hd))
+    v = O.normal(Sk + Hd + 17, (B, Nkv, cap, Hd))
+    scale = 1 / np.sqrt(Hd)
+    n = B * Nq * Sq * Hd
+    buf = upload(pa, np.full(n + 64, np.nan, np.float32), "f32")
+    kern = pa.Kernels.FlashAttention(upload(pa, q, "f32"), upload(pa, k, "f32"), upload(pa, v, "f32"),
+                                     out=buf.view([B, Nq, Sq, Hd]), scale=scale, mask=pa.AttentionMask(kind, window),
+                                     batch=B, query_heads=Nq, kv_heads=Nkv, query_len=Sq, key_len=Sk, head_dim=Hd,
+                                     key_capacity=cap)
+    hdp = 64 if Hd <= 64 else 128 if Hd <= 128 else 256 if Hd <= 256 else 512
+    assert kern.function_names == [f"flash_attention_tiled16_f32_f32_d{hdp}"]
+    enc.encode(kern)
+    stream.synchronize()
+    out = download(buf, stream)
+    assert np.isnan(out[n:]).all(), "stores past the output"
+    got = out[:n].reshape(B, Nq, Sq, Hd)
+    assert not np.isnan(got).any()
+    ref = O.attention_naive(q, k, v, scale, mask_kind=kind, window=window, key_len=Sk)
+    assert_out(got, ref, EPS["f32"], "f32", f"tiled attention f32 {mask} Sq={Sq} Sk={Sk} Hd={Hd}")
+
+
+@pytest.mark.parametrize("Hd,Nq,Nkv", [(128, 8, 8), (512, 4, 2)])
+def test_tiled_attention_f32_sampled(env, Hd, Nq, Nkv):
+    # f32 prefill at 2048 tokens, causal, with scores of standard deviation
+    # 4.5 natural-log units (inputs x 1.5, scale 1/sqrt(Hd) x 2), so the
+    # running max moves past the lazy-rescale gap; sampled query rows against
+    # the oracle over keys 0..r. (Wider scores would carry the f32 rounding
+    # of the dot products, about 1e-6 of a score here, past the f32 bar.)
+    pa, lib, stream, enc = env
+    S = 2048
+    q = 1.5 * O.normal(91 + Hd, (1, Nq, S, Hd))
+    k = 1.5 * O.normal(92 + Hd, (1, Nkv, S, Hd))
+    v = O.normal(93 + Hd, (1, Nkv, S, Hd))
+    scale = 2 / np.sqrt(Hd)
+    to = upload(pa, np.full((1, Nq, S, Hd), np.nan, np.float32), "f32")
+    kern = pa.Kernels.FlashAttention(upload(pa, q, "f32"), upload(pa, k, "f32"), upload(pa, v, "f32"), out=to,
+                                     scale=scale, batch=1, query_heads=Nq, kv_heads=Nkv, query_len=S, key_len=S,
+                                     head_dim=Hd)
+    assert kern.function_names == [f"flash_attention_tiled16_f32_f32_d{Hd}"]
+    enc.encode(kern)
+    stream.synchronize()
+    got = download(to, stream).reshape(1, Nq, S, Hd)
+    assert not np.isnan(got).any()
+    for r in (0, 15, 16, 127, 1000, 2047):
+        ref = O.attention_naive(q[:, :, r:r + 1], k[:, :, :r + 1].copy(), v[:, :, :r + 1].copy(), scale)
+        assert_out(got[:, :, r:r + 1], ref, EPS["f32"], "f32", f"f32 Hd {Hd} row {r}")
+
+
+@pytest.mark.parametrize("dtype,Hd", [("f16", 64), ("bf16", 128), ("f16", 256), ("bf16", 512), ("f32", 128),
+                                      ("f32", 512)])
+def test_tiled_attention_ignores_cache_past_key_len(env, rows, dtype, Hd):
+    # K/V rows past key_len in a larger cache are not keys: here they hold
+    # NaN (a cache is filled only up to the current length), and the last
+    # key step, ragged (Sk = 100), reaches into them
+    pa, lib, stream, enc = env
+    B, Nq, Nkv, Sq, Sk, cap = 1, 2, 1, 70, 100, 160
+    q = rounded(O.normal(31 + Hd, (B, Nq, Sq, Hd)), dtype)
+    k = rounded(O.normal(32 + Hd, (B, Nkv, cap, Hd)), dtype)
+    v = rounded(O.normal(33 + Hd, (B, Nkv, cap, Hd)), dtype)
+    k[:, :, Sk:] = np.nan
+    v[:, :, Sk:] = np.nan
+    scale = 1 / np.sqrt(Hd)
+    to = pa.Tensor.empty([B, Nq, Sq, Hd], dtype)
+    kern = pa.Kernels.FlashAttention(upload(pa, q, dtype), upload(pa, k, dtype), upload(pa, v, dtype), out=to,
+                                     scale=scale, batch=B, query_heads=Nq, kv_heads=Nkv, query_len=Sq, key_len=Sk,
+                                     head_dim=Hd, key_capacity=cap)
+    assert kern.function_names[0].startswith("flash_attention_tiled")
+    enc.encode(kern)
+    stream.synchronize()
+    got = download(to, stream).reshape(B, Nq, Sq, Hd)
+    assert not np.isnan(got).any(), "a key past key_len entered the output"
+    ref = O.attention_naive(q, k, v, scale, key_len=Sk)
+    assert_out(got, ref, EPS[dtype], dtype, f"cache past key_len {dtype} Hd {Hd}")
+
+
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
 def test_tiled_attention_hd512_sampled(env, dtype):
     # a Gemma-4-shaped global-attention prefill: [1, 8, 2048, 512], GQA 2:1,
