@@ -296,6 +296,7 @@ def mlp_config3(pa, lib, stream, enc, sets=4, reps=64):
 
 
 MFMA_PEAK_F16_TFLOPS = 2500.0
+MFMA_PEAK_F32_TFLOPS = 157.3   # dense f32 on the matrix cores
 
 
 def prefill_config5(pa, lib, stream, enc, reps=8):
@@ -402,6 +403,37 @@ def prefill_attention_hd512(pa, lib, stream, enc, reps=8):
         out[name] = {"kernel": fa.function_names[0], "us": round(us, 1),
                      "TFLOP_s": round(flop / (us * 1e-6) / 1e12, 1),
                      "frac": round(flop / (us * 1e-6) / 1e12 / MFMA_PEAK_F16_TFLOPS, 3)}
+    return out
+
+
+def prefill_attention_f32(pa, lib, stream, enc, reps=4):
+    """Causal FlashAttention in f32 (the reference's mpp_flash_attention_f32,
+    FlashAttention.swift:368-376) at the config-5 attention shape,
+    [1, 16, 2048, 256], scale 1/16, on v_mfma_f32_16x16x4_f32; the per-row
+    split-KV kernels on the same inputs beside it (through an output that is
+    not 16-byte aligned). frac is of the f32 matrix-core peak."""
+    S, H, Hd = 2048, 16, 256
+    q, k, v = (pa.Tensor.empty([1, H, S, Hd], "f32") for _ in range(3))
+    for i, t in enumerate((q, k, v)):
+        lib.fill_normal(t, 70 + i, stream=stream)
+    o = pa.Tensor.empty([1, H, S, Hd + 4], "f32")
+    flop = 4.0 * H * Hd * S * (S + 1) / 2
+    out = {}
+    for name, view in (("tiled", o.view([1, H, S, Hd])), ("per_row", o.view([1, H, S, Hd], offset_elements=1))):
+        fa = pa.Kernels.FlashAttention(q, k, v, out=view, scale=1 / 16, batch=1, query_heads=H, kv_heads=H,
+                                       query_len=S, key_len=S, head_dim=Hd)
+        enc.encode(fa)
+        stream.synchronize()
+        e0, e1 = pa.Event(), pa.Event()
+        e0.record(stream)
+        for _ in range(reps):
+            enc.encode(fa)
+        e1.record(stream)
+        e1.synchronize()
+        us = e0.elapsed_ms(e1) * 1e3 / reps
+        out[name] = {"kernel": fa.function_names[0], "us": round(us, 1),
+                     "TFLOP_s": round(flop / (us * 1e-6) / 1e12, 2),
+                     "frac": round(flop / (us * 1e-6) / 1e12 / MFMA_PEAK_F32_TFLOPS, 3)}
     return out
 
 
@@ -609,6 +641,7 @@ def main():
     if not args.no_prefill:
         prefill = prefill_config5(pa, lib, stream, pa.KernelCommandEncoder(lib, stream))
         prefill["attention_hd512"] = prefill_attention_hd512(pa, lib, stream, pa.KernelCommandEncoder(lib, stream))
+        prefill["attention_f32"] = prefill_attention_f32(pa, lib, stream, pa.KernelCommandEncoder(lib, stream))
         if args.library_reference:
             prefill["library_reference"] = library_reference()
 

@@ -998,9 +998,9 @@ __device__ void fa_tiled16(const uint16_t *__restrict__ Q, const uint16_t *__res
 // The reference's mpp_flash_attention_f32 (FlashAttention.swift:368-376,
 // MPPFlashAttention.metal:251-256) on v_mfma_f32_16x16x4_f32, whose
 // operands are single floats (lane l: A[l % 16][l / 16], B[l / 16][l % 16];
-// C rows 4 (l / 16) + i, column l % 16). The tiles, masks, item order and
-// lazy rescale are the 16-bit kernel's, every tile whole; a wave owns 16
-// query rows and a step takes 16 keys. Per step:
+// C rows 4 (l / 16) + i, column l % 16). The masks and lazy rescale are the
+// 16-bit kernels'; a block of 4 waves takes a whole tile of 64 query rows,
+// a wave 16 of them, and a step 16 keys. Per step:
 //  * S^T = K . Q^T (16 keys x 16 queries) in HD / 4 products; product
 //    4 j + s takes dim 16 j + 4 (l / 16) + s from every lane, so a lane
 //    feeds four consecutive products from one 16-byte K read (LDS) and one
@@ -1012,7 +1012,7 @@ __device__ void fa_tiled16(const uint16_t *__restrict__ Q, const uint16_t *__res
 // LDS rows are padded (K by 4 floats, Vt to 20) so the 16 rows a
 // quarter-wave reads fall in distinct banks. Dims past the runtime Hd (a
 // multiple of 4) and keys past Sk read as zeros (buffer loads out of range).
-template <int HD, int NW>
+template <int HD, int NW, bool ZIGZAG>
 __device__ void fa_tiled_f32(const float *__restrict__ Q, const float *__restrict__ K, const float *__restrict__ V,
                              float *__restrict__ out, const TiledFlashAttentionConstants &p) {
     constexpr int BK = 16;          // keys per step
@@ -1029,14 +1029,22 @@ __device__ void fa_tiled_f32(const float *__restrict__ Q, const float *__restric
 
     const uint32_t lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const FaWork work = fa_work(p, BQ16, true);
-    const uint32_t bh = work.bh;
+    // Tile of the block: the (batch, head) index varies fastest; by rank,
+    // heaviest first, or (ZIGZAG) the heavy half heaviest first and then the
+    // light half lightest first, so ranks r and r + half see a constant
+    // number of keys together. With two blocks per CU (Hd <= 256) this
+    // measured 30-38% faster at 16 heads x 2048 tokens (Hd 64-256) than one
+    // 128-row tile per CU heaviest first, whose heaviest tiles, twice the
+    // mean keys, set the time.
+    const uint32_t BH = p.B * p.Nq, nQT = p.qTilesPerHead;
+    const uint32_t bh = blockIdx.x % BH, rank = blockIdx.x / BH;
+    const uint32_t half = (nQT + 1) / 2;
+    const uint32_t qt = !ZIGZAG || rank < half ? nQT - 1 - rank : rank - half;
     const uint32_t b = bh / p.Nq, hq = bh % p.Nq;
     const uint32_t hkv = hq / (p.Nq / p.Nkv);
     const uint32_t stride = p.kvStride ? p.kvStride : p.Sk;
     const uint32_t D = p.Hd;
     const uint64_t kvoff = (uint64_t)(b * p.Nkv + hkv) * stride * D;
-    const uint32_t qt = work.qt[0];
     const uint32_t myq = qt * BQ16 + wave * 16 + c16;
     const int posQ = (int)p.Sk - (int)p.Sq + (int)myq;
     const int posQ0 = (int)p.Sk - (int)p.Sq + (int)(qt * BQ16 + wave * 16);
@@ -1050,9 +1058,8 @@ __device__ void fa_tiled_f32(const float *__restrict__ Q, const float *__restric
                                                                           (int)(p.Sk * D * 4), 0x00020000);
     // K chunk c: key c / (HD / 4), dims 4 (c % (HD / 4)) ..; V chunk c: key
     // c % 16, dims 4 (c / 16) .. (a wave's transposed stores then cover 64
-    // distinct banks)
-    // (the step's first key enters the vector offset, which the range check
-    // covers, so keys past Sk read as zeros whatever the cache holds there)
+    // distinct banks). The step's first key is part of the vector offset,
+    // which the range check covers: keys past Sk read as zeros.
     auto gload = [&](Regs &kr, Regs &vr, uint32_t k0) {
 #pragma unroll
         for (int i = 0; i < kC; ++i) {
@@ -1091,7 +1098,6 @@ __device__ void fa_tiled_f32(const float *__restrict__ Q, const float *__restric
 #pragma unroll
     for (int dt = 0; dt < DC; ++dt) acc[dt] = pk::f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     float m = -INFINITY, l = 0.0f;
-
     auto compute = [&](uint32_t k0, int buf) {
         pk::f32x4 st = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -1099,7 +1105,6 @@ __device__ void fa_tiled_f32(const float *__restrict__ Q, const float *__restric
             const pk::f32x4 kf = *reinterpret_cast<const pk::f32x4 *>(&sK[buf][c16 * LDK + j * 16 + g * 4]);
 #pragma unroll
             for (int s = 0; s < 4; ++s) st = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[s], qf[j][s], st, 0, 0, 0);
-            if (kOneSet && j % 4 == 3) __builtin_amdgcn_sched_barrier(0);
         }
         const bool full = (int)k0 + BK <= (int)p.Sk && (p.maskKind == 2u || (int)k0 + BK - 1 <= posQ0) &&
                           (p.maskKind != 1u || posQ0 + 15 - (int)k0 < (int)p.slidingWindow);
@@ -1134,7 +1139,6 @@ __device__ void fa_tiled_f32(const float *__restrict__ Q, const float *__restric
             const pk::f32x4 va = *reinterpret_cast<const pk::f32x4 *>(&sV[buf][(dt * 16 + c16) * LDT + g * 4]);
 #pragma unroll
             for (int s = 0; s < 4; ++s) acc[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(va[s], pv[s], acc[dt], 0, 0, 0);
-            if (kOneSet && dt % 4 == 3) __builtin_amdgcn_sched_barrier(0);
         }
     };
 
@@ -1254,14 +1258,14 @@ __device__ void fa_split_merge(const float *__restrict__ pO, const float *__rest
     FA_TILED16(flash_attention_tiled16_##t##_##o##_d128, T, O, 128, 8)   \
     FA_TILED16(flash_attention_tiled16_##t##_##o##_d256, T, O, 256, 8)   \
     FA_TILED16(flash_attention_tiled16_##t##_##o##_d512, T, O, 512, 4)
-// f32: 8 waves (128 query rows) per block, 4 (64 rows) at Hd 512, where a
-// wave's Q chunks and accumulators take 256 registers; the partial-state
-// arguments are never read (every tile whole)
-#define FA_TILED_F32(name, HD, NW)                                                                     \
-    POPCORN_KERNEL void __launch_bounds__(64 * NW)                                                     \
+// f32: 4 waves (64 query rows) per block, two blocks per CU below Hd 512
+// (at Hd 512 a wave's Q chunks and accumulators alone take 256 registers);
+// the partial-state arguments are never read (every tile whole)
+#define FA_TILED_F32(name, HD, ZIGZAG)                                                                 \
+    POPCORN_KERNEL void __launch_bounds__(256, HD < 512 ? 2 : 1)                                       \
         name(const float *q, const float *k, const float *v, float *out, float *, float *, uint64_t *, \
              TiledFlashAttentionConstants p) {                                                         \
-        fa_tiled_f32<HD, NW>(q, k, v, out, p);                                                         \
+        fa_tiled_f32<HD, 4, ZIGZAG>(q, k, v, out, p);                                                  \
     }
 #define FA_MERGE(name, O, HD)                                                                       \
     POPCORN_KERNEL void __launch_bounds__(256)                                                         \
@@ -1288,7 +1292,7 @@ FA_TILED16_D(bf16, BF16, f32, F32)
 FA_MERGE_D(f16, F16)
 FA_MERGE_D(bf16, BF16)
 FA_MERGE_D(f32, F32)
-FA_TILED_F32(flash_attention_tiled16_f32_f32_d64, 64, 8)
-FA_TILED_F32(flash_attention_tiled16_f32_f32_d128, 128, 8)
-FA_TILED_F32(flash_attention_tiled16_f32_f32_d256, 256, 8)
-FA_TILED_F32(flash_attention_tiled16_f32_f32_d512, 512, 4)
+FA_TILED_F32(flash_attention_tiled16_f32_f32_d64, 64, true)
+FA_TILED_F32(flash_attention_tiled16_f32_f32_d128, 128, true)
+FA_TILED_F32(flash_attention_tiled16_f32_f32_d256, 256, true)
+FA_TILED_F32(flash_attention_tiled16_f32_f32_d512, 512, false)

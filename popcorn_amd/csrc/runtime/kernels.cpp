@@ -415,10 +415,11 @@ private:
     std::string partialName_, reduceName_, tiledName_, mergeName_;
     int64_t nSplit_ = 0;
     bool pairTiles_ = false;
-    bool rows16_ = false;  // the 16-rows-per-wave kernel: 8 waves per 128-row tile (4 per 64 at Hd 512)
+    bool rows16_ = false;  // the 16-rows-per-wave kernel: 8 waves per 128-row tile (4 per 64 at Hd 512 and in f32)
     int64_t hdp_ = 0;      // the tiled kernel's head dim: Hd padded to 64, 128, 256 or 512
-    int64_t tiledBlock() const { return hdp_ == 512 ? 256 : rows16_ ? 512 : kBlock; }
-    int64_t tileRows() const { return hdp_ == 512 ? 64 : 128; }
+    bool tiles64() const { return hdp_ == 512 || q_.dataType == DataType::f32; }
+    int64_t tiledBlock() const { return tiles64() ? 256 : rows16_ ? 512 : kBlock; }
+    int64_t tileRows() const { return tiles64() ? 64 : 128; }
     // Paired tiles are merged inside the tiled kernels (pairTiles 2).
     bool pairMergeInKernel_ = true;
     bool mergedPairs() const { return pairTiles_ && pairMergeInKernel_; }
