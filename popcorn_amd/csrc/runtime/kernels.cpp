@@ -1640,6 +1640,51 @@ std::unique_ptr<Kernel> EmbeddingGather(const Tensor &ids, const Tensor &table, 
 }
 
 
+// The 4-bit Matmul on the matrix cores for bf16 rows (aq_gemm.hip): x's
+// group sums and a pair-ordered copy of x in scratch, then 128 x 128 tiles
+// of C. A block walks its K groups one at a time, ~1.45 us each when few
+// tiles hide no latency, while the streaming matvec per row costs about
+// N K / 2 bytes / 4.5 TB/s per row; the GEMM wins once
+// m N K / 2 / 4.5 TB/s > K / 64 x 1.45 us, i.e. m N > ~2^18 (measured
+// crossovers: m ~ 20 at N 9216, m ~ 100 at N 2304).
+constexpr int64_t kQ4GemmMinRows = 16;
+constexpr int64_t kQ4GemmMinWork = int64_t{1} << 18;  // m * N
+
+class AffineQGemmKernel : public Kernel {
+public:
+    AffineQGemmKernel(const Tensor &a, const AffineQuantizedTensor &b, const Tensor &c, const AffineQMatmulConstants &qc)
+        : a_(a), b_(b), c_(c), qc_(qc) {}
+    std::vector<Binding> tensors() const override {
+        std::vector<Binding> t = {{b_.packedValues, kRead}, {b_.scales, kRead}, {a_, kRead}, {c_, kWrite}};
+        if (b_.hasBiases) t.push_back({b_.biases, kRead});
+        return t;
+    }
+    std::string describe() const override { return std::string("aq_gemm_prep_bf16,") + mainName(); }
+    void encode(KernelCommandEncoder &enc) const override {
+        const int64_t m = qc_.M, k = qc_.K, g = qc_.kGroups, n = qc_.N;
+        enc.withTemporaryTensor(ScratchSpec{{m, k}, DataType::bf16}, [&](Tensor xp) {
+            enc.withTemporaryTensor(ScratchSpec{{m, g}, DataType::f32}, [&](Tensor xs) {
+                FixedDispatch prep("aq_gemm_prep_bf16", {{a_, kRead}, {xp, kWrite}, {xs, kWrite}}, {bytesOf(qc_)},
+                                   grid1(cdiv(m * g, kBlock), kBlock));
+                enc.dispatch(prep);
+                const Tensor &bias = b_.hasBiases ? b_.biases : b_.scales;
+                FixedDispatch gemm(mainName(),
+                                   {{b_.packedValues, kRead}, {b_.scales, kRead}, {bias, kRead}, {xp, kRead}, {xs, kRead},
+                                    {c_, kWrite}},
+                                   {bytesOf(qc_)}, grid1(cdiv(m, 128) * cdiv(n, 128), kBlock));
+                enc.dispatch(gemm);
+            });
+        });
+    }
+
+private:
+    std::string mainName() const { return std::string("aq_gemm_mfma_bf16_bf16_") + tag(c_.dataType) + "_b4_g64"; }
+    Tensor a_;
+    AffineQuantizedTensor b_;
+    Tensor c_;
+    AffineQMatmulConstants qc_;
+};
+
 // Matmul.swift:99-130 and :279-332
 std::unique_ptr<Kernel> Matmul(const Tensor &a, const AffineQuantizedTensor &b, const Tensor &c) {
     using D = DataType;
@@ -1676,6 +1721,11 @@ std::unique_ptr<Kernel> Matmul(const Tensor &a, const AffineQuantizedTensor &b, 
     const Q4Shape q = q4Shape(n, k, x == D::f32);
     const bool aligned = aligned16(b.packedValues.data) && aligned16(a.data) &&
                          (reinterpret_cast<uintptr_t>(b.scales.data) & 3) == 0 && (reinterpret_cast<uintptr_t>(bias.data) & 3) == 0;
+    // a prompt's rows of bf16 activations: the matrix-core GEMM (one pass
+    // over the weights for all rows instead of one matvec per row)
+    if (x == D::bf16 && m >= kQ4GemmMinRows && m * n >= kQ4GemmMinWork && aligned &&
+        m * (k / 64) <= (int64_t)UINT32_MAX && cdiv(m, 128) * cdiv(n, 128) <= (int64_t)UINT32_MAX)
+        return std::make_unique<AffineQGemmKernel>(a, b, c, qc);
     DispatchSize ds;
     ds.block = dim3(kBlock, 1, 1);
     std::string fn;

@@ -86,6 +86,60 @@ def test_quantized_matmul_integer_exact(env, xt):
     np.testing.assert_array_equal(got, (x.astype(np.int64) @ w.T).astype(np.float32))
 
 
+def _gemm_names(ot):
+    return ["aq_gemm_prep_bf16", f"aq_gemm_mfma_bf16_bf16_{ot}_b4_g64"]
+
+
+@pytest.mark.parametrize("ot", ["bf16", "f32"])
+@pytest.mark.parametrize("M,N,K,bias", [(16, 16448, 128, True), (100, 2700, 256, True), (130, 2100, 576, False),
+                                        (256, 1100, 2304, True), (300, 900, 9216, False)])
+def test_quantized_gemm_vs_oracle(env, ot, M, N, K, bias):
+    # bf16 activations with m >= 16 and m * N >= 2^18 take the matrix-core
+    # 4-bit GEMM (one pass over the weights for all rows; the reference runs
+    # one matvec per row, Matmul.swift:279-332): group products on the matrix
+    # cores, then s * D + (b - 128 s) * sum(x) per group in f32. Ragged M and
+    # N (tiles of 128) included.
+    pa = env[0]
+    rng = np.random.default_rng(M * 7 + N + K)
+    packed, s, b, q = quantize_q4(0.05 * rng.standard_normal((N, K)).astype(np.float32), bias=bias)
+    x = rounded(rng.standard_normal((M, K)).astype(np.float32), "bf16")
+    got, k = _matmul(env, x, _qtensor(pa, packed, s, b, N, K), "bf16", ot, N)
+    assert k.function_names == _gemm_names(ot)
+    assert_out(got, O.aq_matmul(x, packed, s, b, N, K), EPS["bf16"], ot, f"aq gemm ->{ot} {M}x{N}x{K} bias={bias}")
+
+
+def test_quantized_gemm_integer_exact(env):
+    # small integer x, scale 2, integer biases: every product and partial sum
+    # is an exact f32 integer in any order, so the GEMM's result is exact; pins
+    # the nibble order, the pair order of x and both affine terms
+    pa = env[0]
+    rng = np.random.default_rng(19)
+    M, N, K = 40, 6600, 2304
+    q = rng.integers(0, 16, (N, K)).astype(np.uint32)
+    s = np.full((N, K // 64), 2.0, np.float32)
+    b = rng.integers(-8, 8, (N, K // 64)).astype(np.float32)
+    x = rng.integers(-3, 4, (M, K)).astype(np.float32)
+    got, k = _matmul(env, x, _qtensor(pa, pack_q4(q), s, b, N, K), "bf16", "f32", N)
+    assert k.function_names == _gemm_names("f32")
+    w = q.astype(np.int64) * 2 + np.repeat(b, 64, 1).astype(np.int64)
+    np.testing.assert_array_equal(got, (x.astype(np.int64) @ w.T).astype(np.float32))
+
+
+def test_quantized_gemm_threshold(env):
+    # fewer than 16 rows, or m * N below 2^18, keep the streaming matvec per
+    # row; f32 activations (held to 1e-5) never take the bf16 matrix cores
+    pa = env[0]
+    rng = np.random.default_rng(23)
+    N, K = 18000, 128
+    packed, s, b, q = quantize_q4(0.05 * rng.standard_normal((N, K)).astype(np.float32))
+    qt = _qtensor(pa, packed, s, b, N, K)
+    for M, xt, gemm in ((15, "bf16", False), (16, "bf16", True), (17, "f32", False)):
+        x = rounded(rng.standard_normal((M, K)).astype(np.float32), xt)
+        got, k = _matmul(env, x, qt, xt, "f32", N)
+        assert (k.function_names == _gemm_names("f32")) == gemm, (M, xt, k.function_names)
+        assert_out(got, O.aq_matmul(x, packed, s, b, N, K), EPS[xt] if xt == "bf16" else 2e-5, "f32", f"M={M} {xt}")
+
+
 def test_quantized_matmul_unaligned_any_kernel(env):
     # activations 2 bytes off 16-byte alignment take aq_matvec_simd4 (any shape)
     pa, lib, stream, enc = env
