@@ -23,7 +23,10 @@
 // the unpacked weights (128 x 64 bf16), the columns' (s, b - 128 s) and the
 // rows' X_g in LDS, double-buffered with the next group's loads in
 // registers. Rows past M and columns past N read row M - 1 / N - 1 and are
-// not stored.
+// not stored. A block walks its groups one after another, so with few tiles
+// the groups are split over gridDim.y blocks per tile (SPLIT): each writes
+// its f32 partial tile to P [gridDim.y][M][N] and matmul_splitk_reduce_*
+// sums them and rounds once.
 #include "mfma.hpp"
 
 namespace {
@@ -62,10 +65,10 @@ __device__ void aq_gemm_prep(const uint16_t *__restrict__ X, uint16_t *__restric
     Xs[t] = sum;
 }
 
-template <typename O>
+template <typename O, bool SPLIT>
 __device__ void aq_gemm(const uint32_t *__restrict__ Wp, const uint16_t *__restrict__ S, const uint16_t *__restrict__ Bi,
                         const uint16_t *__restrict__ Xp, const float *__restrict__ Xs, typename O::storage *__restrict__ C,
-                        const AffineQMatmulConstants &p) {
+                        float *__restrict__ P, const AffineQMatmulConstants &p) {
     __shared__ __attribute__((aligned(16))) uint16_t sX[2][BM * LDT];
     __shared__ __attribute__((aligned(16))) uint16_t sW[2][BN * LDT];
     __shared__ __attribute__((aligned(16))) float2 sSC[2][BN];  // (s, b - 128 s) per column
@@ -176,14 +179,19 @@ __device__ void aq_gemm(const uint32_t *__restrict__ Wp, const uint16_t *__restr
         }
     };
 
-    gload(0);
-    lstore(0);
-    __syncthreads();
-    for (uint32_t g = 0; g < G; ++g) {
-        const int st = (int)(g & 1);
-        if (g + 1 < G) gload(g + 1);
+    // this block's groups: all, or split y of gridDim.y
+    const uint32_t g0 = SPLIT ? (uint32_t)((uint64_t)G * blockIdx.y / gridDim.y) : 0u;
+    const uint32_t g1 = SPLIT ? (uint32_t)((uint64_t)G * (blockIdx.y + 1) / gridDim.y) : G;
+    if (g0 < g1) {
+        gload(g0);
+        lstore(0);
+        __syncthreads();
+    }
+    for (uint32_t g = g0; g < g1; ++g) {
+        const int st = (int)((g - g0) & 1);
+        if (g + 1 < g1) gload(g + 1);
         compute(st);
-        if (g + 1 < G) lstore(st ^ 1);
+        if (g + 1 < g1) lstore(st ^ 1);
         __syncthreads();
     }
 
@@ -198,7 +206,12 @@ __device__ void aq_gemm(const uint32_t *__restrict__ Wp, const uint16_t *__restr
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const uint32_t m = bm + wm + mi * 32 + (i / 4) * 8 + h * 4 + (i % 4);
-                if (m < M) C[(uint64_t)m * N + n] = O::store(acc[mi][ni][i]);
+                if (m >= M) continue;
+                if constexpr (SPLIT) {
+                    P[((uint64_t)blockIdx.y * M + m) * N + n] = acc[mi][ni][i];
+                } else {
+                    C[(uint64_t)m * N + n] = O::store(acc[mi][ni][i]);
+                }
             }
         }
 }
@@ -214,8 +227,15 @@ POPCORN_KERNEL void __launch_bounds__(256)
     POPCORN_KERNEL void __launch_bounds__(256)                                                            \
         name(const uint32_t *w, const uint16_t *s, const uint16_t *b, const uint16_t *xp, const float *xs, \
              O::storage *c, AffineQMatmulConstants p) {                                                   \
-        aq_gemm<O>(w, s, b, xp, xs, c, p);                                                                \
+        aq_gemm<O, false>(w, s, b, xp, xs, c, nullptr, p);                                                \
     }
+
+// f32 partial tiles of a K split (gridDim.y splits), for matmul_splitk_reduce_*
+POPCORN_KERNEL void __launch_bounds__(256)
+    aq_gemm_mfma_bf16_bf16_splitk_b4_g64(const uint32_t *w, const uint16_t *s, const uint16_t *b, const uint16_t *xp,
+                                         const float *xs, float *partial, AffineQMatmulConstants p) {
+    aq_gemm<pk::F32, true>(w, s, b, xp, xs, nullptr, partial, p);
+}
 
 using pk::BF16;
 using pk::F32;

@@ -1642,13 +1642,14 @@ std::unique_ptr<Kernel> EmbeddingGather(const Tensor &ids, const Tensor &table, 
 
 // The 4-bit Matmul on the matrix cores for bf16 rows (aq_gemm.hip): x's
 // group sums and a pair-ordered copy of x in scratch, then 128 x 128 tiles
-// of C. A block walks its K groups one at a time, ~1.45 us each when few
-// tiles hide no latency, while the streaming matvec per row costs about
-// N K / 2 bytes / 4.5 TB/s per row; the GEMM wins once
-// m N K / 2 / 4.5 TB/s > K / 64 x 1.45 us, i.e. m N > ~2^18 (measured
-// crossovers: m ~ 20 at N 9216, m ~ 100 at N 2304).
+// of C, with the K groups split over blocks (and a reduction) when the tiles
+// leave CUs idle. Its three launches take ~25-35 us at small m, while the
+// streaming matvec per row costs about N K / 2 bytes / 4.5 TB/s per row, so
+// the GEMM wins once the rows' weight reads pass ~2^27 bytes (measured at
+// N K = 9216 x 2304 both ways: 26 against 43 us at m 16-29, 35 against
+// 210 us at m 128).
 constexpr int64_t kQ4GemmMinRows = 16;
-constexpr int64_t kQ4GemmMinWork = int64_t{1} << 18;  // m * N
+constexpr int64_t kQ4GemmMinBytes = int64_t{1} << 27;  // m * N * K / 2
 
 class AffineQGemmKernel : public Kernel {
 public:
@@ -1659,26 +1660,60 @@ public:
         if (b_.hasBiases) t.push_back({b_.biases, kRead});
         return t;
     }
-    std::string describe() const override { return std::string("aq_gemm_prep_bf16,") + mainName(); }
+    std::string describe() const override {
+        return splits() > 1 ? std::string("aq_gemm_prep_bf16,aq_gemm_mfma_bf16_bf16_splitk_b4_g64,") + reduceName()
+                            : std::string("aq_gemm_prep_bf16,") + mainName();
+    }
     void encode(KernelCommandEncoder &enc) const override {
-        const int64_t m = qc_.M, k = qc_.K, g = qc_.kGroups, n = qc_.N;
+        const int64_t m = qc_.M, k = qc_.K, g = qc_.kGroups, n = qc_.N, tiles = cdiv(m, 128) * cdiv(n, 128);
+        const int64_t s = splits();
         enc.withTemporaryTensor(ScratchSpec{{m, k}, DataType::bf16}, [&](Tensor xp) {
             enc.withTemporaryTensor(ScratchSpec{{m, g}, DataType::f32}, [&](Tensor xs) {
                 FixedDispatch prep("aq_gemm_prep_bf16", {{a_, kRead}, {xp, kWrite}, {xs, kWrite}}, {bytesOf(qc_)},
                                    grid1(cdiv(m * g, kBlock), kBlock));
                 enc.dispatch(prep);
                 const Tensor &bias = b_.hasBiases ? b_.biases : b_.scales;
-                FixedDispatch gemm(mainName(),
-                                   {{b_.packedValues, kRead}, {b_.scales, kRead}, {bias, kRead}, {xp, kRead}, {xs, kRead},
-                                    {c_, kWrite}},
-                                   {bytesOf(qc_)}, grid1(cdiv(m, 128) * cdiv(n, 128), kBlock));
-                enc.dispatch(gemm);
+                if (s <= 1) {
+                    FixedDispatch gemm(mainName(),
+                                       {{b_.packedValues, kRead}, {b_.scales, kRead}, {bias, kRead}, {xp, kRead},
+                                        {xs, kRead}, {c_, kWrite}},
+                                       {bytesOf(qc_)}, grid1(tiles, kBlock));
+                    enc.dispatch(gemm);
+                    return;
+                }
+                enc.withTemporaryTensor(ScratchSpec{{s * m, n}, DataType::f32}, [&](Tensor part) {
+                    DispatchSize ds;
+                    ds.grid = dim3((unsigned)tiles, (unsigned)s, 1);
+                    ds.block = dim3(kBlock, 1, 1);
+                    FixedDispatch gemm("aq_gemm_mfma_bf16_bf16_splitk_b4_g64",
+                                       {{b_.packedValues, kRead}, {b_.scales, kRead}, {bias, kRead}, {xp, kRead},
+                                        {xs, kRead}, {part, kWrite}},
+                                       {bytesOf(qc_)}, ds);
+                    enc.dispatch(gemm);
+                    MatmulConstants mc{(uint32_t)m, (uint32_t)k, (uint32_t)n, 1u};
+                    const uint32_t splits = (uint32_t)s;
+                    const int64_t blocks = std::clamp<int64_t>(cdiv(m * n / 4, kBlock), 1, 8 * deviceCUs());
+                    FixedDispatch reduce(reduceName(), {{part, kRead}, {c_, kWrite}}, {bytesOf(mc), bytesOf(splits)},
+                                         grid1(blocks, kBlock));
+                    enc.dispatch(reduce);
+                });
             });
         });
     }
 
 private:
+    // K splits (groups per block) when the tiles leave CUs idle: about two
+    // blocks per CU, at least 4 groups each; the reduction takes M N % 4 == 0
+    // and 16-byte-aligned C
+    int64_t splits() const {
+        const int64_t tiles = cdiv((int64_t)qc_.M, 128) * cdiv((int64_t)qc_.N, 128);
+        const int64_t want = 2 * (int64_t)deviceCUs() / std::max<int64_t>(tiles, 1);
+        const int64_t s = std::min<int64_t>(want, (int64_t)qc_.kGroups / 4);
+        const bool reducible = ((int64_t)qc_.M * qc_.N) % 4 == 0 && aligned16(c_.data);
+        return reducible && s >= 2 ? s : 1;
+    }
     std::string mainName() const { return std::string("aq_gemm_mfma_bf16_bf16_") + tag(c_.dataType) + "_b4_g64"; }
+    std::string reduceName() const { return std::string("matmul_splitk_reduce_") + tag(c_.dataType); }
     Tensor a_;
     AffineQuantizedTensor b_;
     Tensor c_;
@@ -1723,7 +1758,7 @@ std::unique_ptr<Kernel> Matmul(const Tensor &a, const AffineQuantizedTensor &b, 
                          (reinterpret_cast<uintptr_t>(b.scales.data) & 3) == 0 && (reinterpret_cast<uintptr_t>(bias.data) & 3) == 0;
     // a prompt's rows of bf16 activations: the matrix-core GEMM (one pass
     // over the weights for all rows instead of one matvec per row)
-    if (x == D::bf16 && m >= kQ4GemmMinRows && m * n >= kQ4GemmMinWork && aligned &&
+    if (x == D::bf16 && m >= kQ4GemmMinRows && m * n * (k / 2) >= kQ4GemmMinBytes && aligned &&
         m * (k / 64) <= (int64_t)UINT32_MAX && cdiv(m, 128) * cdiv(n, 128) <= (int64_t)UINT32_MAX)
         return std::make_unique<AffineQGemmKernel>(a, b, c, qc);
     DispatchSize ds;

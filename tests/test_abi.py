@@ -273,18 +273,19 @@ def test_quantized_validation_and_routing():
     out = T([1, 9216], "bf16", FAKE + 2 ** 20)
     assert pa.Kernels.Matmul(T([1, 2304]), w, out).describe() == "aq_qmv_fast_bf16_bf16_bf16_b4_g64_l12_j2"
     assert pa.Kernels.Matmul(T([4, 2304]), w, T([4, 9216], "f32")).describe() == "aq_matvec_simd4_bf16_bf16_f32_b4_g64_l12_j2"
-    # bf16 rows with m * N >= 2^18 (and m >= 16): the matrix-core GEMM
-    # (group sums and pair-ordered x first)
-    assert pa.Kernels.Matmul(T([28, 2304]), w, T([28, 9216], "f32")).describe() == "aq_matvec_simd4_bf16_bf16_f32_b4_g64_l12_j2"
-    assert pa.Kernels.Matmul(T([29, 2304]), w, T([29, 9216], "f32")).describe() == \
-        "aq_gemm_prep_bf16,aq_gemm_mfma_bf16_bf16_f32_b4_g64"
+    # bf16 rows reading >= 2^27 weight bytes in all (and m >= 16): the
+    # matrix-core GEMM, group sums and pair-ordered x first; few tiles split
+    # the K groups over blocks, summed by the split-K reduction
+    assert pa.Kernels.Matmul(T([15, 2304]), w, T([15, 9216], "f32")).describe() == "aq_matvec_simd4_bf16_bf16_f32_b4_g64_l12_j2"
+    assert pa.Kernels.Matmul(T([16, 2304]), w, T([16, 9216], "f32")).describe() == \
+        "aq_gemm_prep_bf16,aq_gemm_mfma_bf16_bf16_splitk_b4_g64,matmul_splitk_reduce_f32"
+    assert pa.Kernels.Matmul(T([16, 1024]), _q4(16000, 1024), T([16, 16000], "f32")).describe().startswith("aq_matvec")
     assert pa.Kernels.Matmul(T([2048, 2304]), w, T([2048, 9216])).describe() == \
         "aq_gemm_prep_bf16,aq_gemm_mfma_bf16_bf16_bf16_b4_g64"
     assert pa.Kernels.Matmul(T([64, 2304], "f32"), w, T([64, 9216], "f32")).describe().startswith("aq_matvec_simd4_f32")
     down = _q4(2304, 9216)
-    assert pa.Kernels.Matmul(T([113, 9216]), down, T([113, 2304], "f32")).describe().startswith("aq_matvec_simd4")
-    assert pa.Kernels.Matmul(T([114, 9216]), down, T([114, 2304], "f32")).describe() == \
-        "aq_gemm_prep_bf16,aq_gemm_mfma_bf16_bf16_f32_b4_g64"
+    assert pa.Kernels.Matmul(T([16, 9216]), down, T([16, 2304], "f32")).describe() == \
+        "aq_gemm_prep_bf16,aq_gemm_mfma_bf16_bf16_splitk_b4_g64,matmul_splitk_reduce_f32"
     assert pa.Kernels.Matmul(T([1, 9216]), down, T([1, 2304])).describe() == "aq_qmv_fast_bf16_bf16_bf16_b4_g64_l16_j8"
     # unaligned activations or f32 x past 4096 take the any-shape kernel
     assert pa.Kernels.Matmul(T([1, 2304], ptr=FAKE + 2), w, out).describe() == "aq_matvec_simd4_bf16_bf16_bf16_b4_g64"

@@ -86,16 +86,21 @@ def test_quantized_matmul_integer_exact(env, xt):
     np.testing.assert_array_equal(got, (x.astype(np.int64) @ w.T).astype(np.float32))
 
 
-def _gemm_names(ot):
+def _gemm_names(ot, split=False):
+    if split:
+        # few tiles: the groups split over blocks, f32 partials summed once
+        return ["aq_gemm_prep_bf16", "aq_gemm_mfma_bf16_bf16_splitk_b4_g64", f"matmul_splitk_reduce_{ot}"]
     return ["aq_gemm_prep_bf16", f"aq_gemm_mfma_bf16_bf16_{ot}_b4_g64"]
 
 
 @pytest.mark.parametrize("ot", ["bf16", "f32"])
-@pytest.mark.parametrize("M,N,K,bias", [(16, 16448, 128, True), (100, 2700, 256, True), (130, 2100, 576, False),
-                                        (256, 1100, 2304, True), (300, 900, 9216, False)])
-def test_quantized_gemm_vs_oracle(env, ot, M, N, K, bias):
-    # bf16 activations with m >= 16 and m * N >= 2^18 take the matrix-core
-    # 4-bit GEMM (one pass over the weights for all rows; the reference runs
+@pytest.mark.parametrize("M,N,K,bias,split", [(16, 16448, 1024, True, True), (100, 2700, 1024, True, True),
+                                              (130, 2100, 1152, False, True), (131, 2003, 1152, True, False),
+                                              (256, 1100, 2304, True, True), (300, 900, 9216, False, True),
+                                              (2048, 2048, 256, True, False), (2048, 1024, 256, False, False)])
+def test_quantized_gemm_vs_oracle(env, ot, M, N, K, bias, split):
+    # bf16 activations with m >= 16 rows reading >= 2^27 weight bytes in all
+    # take the matrix-core 4-bit GEMM (one pass over the weights for all rows; the reference runs
     # one matvec per row, Matmul.swift:279-332): group products on the matrix
     # cores, then s * D + (b - 128 s) * sum(x) per group in f32. Ragged M and
     # N (tiles of 128) included.
@@ -104,7 +109,10 @@ def test_quantized_gemm_vs_oracle(env, ot, M, N, K, bias):
     packed, s, b, q = quantize_q4(0.05 * rng.standard_normal((N, K)).astype(np.float32), bias=bias)
     x = rounded(rng.standard_normal((M, K)).astype(np.float32), "bf16")
     got, k = _matmul(env, x, _qtensor(pa, packed, s, b, N, K), "bf16", ot, N)
-    assert k.function_names == _gemm_names(ot)
+    # split: the tiles leave CUs idle (about two blocks per CU, at least 4
+    # groups per block; 131 x 2003 is not a multiple of 4, and K 256 has too
+    # few groups, so no split there)
+    assert k.function_names == _gemm_names(ot, split)
     assert_out(got, O.aq_matmul(x, packed, s, b, N, K), EPS["bf16"], ot, f"aq gemm ->{ot} {M}x{N}x{K} bias={bias}")
 
 
@@ -120,23 +128,24 @@ def test_quantized_gemm_integer_exact(env):
     b = rng.integers(-8, 8, (N, K // 64)).astype(np.float32)
     x = rng.integers(-3, 4, (M, K)).astype(np.float32)
     got, k = _matmul(env, x, _qtensor(pa, pack_q4(q), s, b, N, K), "bf16", "f32", N)
-    assert k.function_names == _gemm_names("f32")
+    assert k.function_names == _gemm_names("f32", split=True)
     w = q.astype(np.int64) * 2 + np.repeat(b, 64, 1).astype(np.int64)
     np.testing.assert_array_equal(got, (x.astype(np.int64) @ w.T).astype(np.float32))
 
 
 def test_quantized_gemm_threshold(env):
-    # fewer than 16 rows, or m * N below 2^18, keep the streaming matvec per
-    # row; f32 activations (held to 1e-5) never take the bf16 matrix cores
+    # fewer than 16 rows, or under 2^27 weight bytes read in all, keep the
+    # streaming matvec per row; f32 activations (held to 1e-5) never take the
+    # bf16 matrix cores
     pa = env[0]
     rng = np.random.default_rng(23)
-    N, K = 18000, 128
+    N, K = 18000, 1024
     packed, s, b, q = quantize_q4(0.05 * rng.standard_normal((N, K)).astype(np.float32))
     qt = _qtensor(pa, packed, s, b, N, K)
     for M, xt, gemm in ((15, "bf16", False), (16, "bf16", True), (17, "f32", False)):
         x = rounded(rng.standard_normal((M, K)).astype(np.float32), xt)
         got, k = _matmul(env, x, qt, xt, "f32", N)
-        assert (k.function_names == _gemm_names("f32")) == gemm, (M, xt, k.function_names)
+        assert (k.function_names[0] == "aq_gemm_prep_bf16") == gemm, (M, xt, k.function_names)
         assert_out(got, O.aq_matmul(x, packed, s, b, N, K), EPS[xt] if xt == "bf16" else 2e-5, "f32", f"M={M} {xt}")
 
 
