@@ -199,6 +199,39 @@ def q4_sweep(pa, lib, stream, enc):
     return rows
 
 
+def q4_prompt_gemm(pa, lib, stream, enc, reps=10):
+    """The 4-bit Matmul for a prompt (bf16 x, bf16 scales and biases, group
+    64) at the Gemma-2-2B gate and down shapes: m = 2048 and 128 rows on the
+    matrix-core GEMM (aq_gemm.hip; prep, GEMM or split GEMM + reduction,
+    all timed), beside the streaming matvec per row the reference's route
+    runs (Matmul.swift:279-332), timed at m = 15 (its largest m here) and
+    reported per row. TFLOP/s count 2 m N K; frac is of the dense bf16 peak."""
+    rows = []
+    for name, N, K in (("gate", 9216, 2304), ("down", 2304, 9216)):
+        packed = pa.Tensor.empty([N, K // 8], "u32")
+        scales, biases = pa.Tensor.empty([N, K // 64], "bf16"), pa.Tensor.empty([N, K // 64], "bf16")
+        lib.fill_normal(packed.view([N * K // 8], "f32"), 6, stream=stream)
+        lib.fill_normal(scales, 7, std=0.01, stream=stream)
+        lib.fill_normal(biases, 8, std=0.01, stream=stream)
+        qt = pa.AffineQuantizedTensor(packed, scales, biases, [N, K])
+        out = {}
+        for m in (15, 128, 2048):
+            x = pa.Tensor.empty([m, K], "bf16")
+            lib.fill_normal(x, 9, stream=stream)
+            y = pa.Tensor.empty([m, N], "bf16")
+            k = pa.Kernels.Matmul(x, qt, y)
+            enc.encode(k)
+            stream.synchronize()
+            us = timed_launches(pa, stream, enc, [k] * reps)
+            tf = 2.0 * m * N * K / (us * 1e-6) / 1e12
+            out[f"m{m}"] = {"kernels": k.function_names, "us": round(us, 1), "TFLOP_s": round(tf, 1),
+                            "frac": round(tf / MFMA_PEAK_F16_TFLOPS, 3)}
+        out["per_row_us_per_row"] = round(out["m15"]["us"] / 15, 2)
+        out["m2048_speedup_vs_per_row"] = round(out["per_row_us_per_row"] * 2048 / out["m2048"]["us"], 1)
+        rows.append({"matmul": name, "N": N, "K": K, **out})
+    return rows
+
+
 def skinny_gemm(pa, lib, stream, enc):
     """The skinny 16-bit Matmul (2 <= M <= 64; the reference's small-M MPP
     tiles, Matmul.swift:175-196): C[M, N] = A[M, K] . B[N, K]^T in bf16 with
@@ -653,9 +686,10 @@ def main():
     if not args.no_skinny:
         skinny = skinny_gemm(pa, lib, stream, pa.KernelCommandEncoder(lib, stream))
 
-    q4 = None
+    q4 = q4p = None
     if not args.no_q4:
         q4 = q4_sweep(pa, lib, stream, pa.KernelCommandEncoder(lib, stream))
+        q4p = q4_prompt_gemm(pa, lib, stream, pa.KernelCommandEncoder(lib, stream))
 
     block = q4dec = None
     if not args.no_attention_block:
@@ -693,6 +727,7 @@ def main():
         "decode_attention_block": block,
         "skinny_gemm": skinny,
         "q4_matvec": q4,
+        "q4_prompt_gemm": q4p,
         "decode_q4": q4dec,
         "cpu_baseline": cpu,
     }
