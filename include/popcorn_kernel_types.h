@@ -397,6 +397,15 @@ typedef struct {
     uint32_t hasBias;
 } DecodeNextTokenConstants;
 
+/* No counterpart in the reference: out[cols, rows] = in[rows, cols]^T for
+ * 16-bit elements, so a Matmul with a non-transposed 16-bit B (the
+ * reference's mpp_matmul without _tb, Matmul.swift:203-214) can run the
+ * transposed-B matrix-core kernels. */
+typedef struct {
+    uint32_t rows;
+    uint32_t cols;
+} Transpose2DConstants;
+
 #ifdef __cplusplus
 }
 #endif

@@ -409,6 +409,61 @@ GEMM_MFMA_TILES(matmul_mfma_bf16_bf16_bf16, BF16, BF16)
 GEMM_MFMA_TILES(matmul_mfma_bf16_bf16_f32, BF16, F32)
 
 // Split-K form of the 256 x 384 tile (f32 partials) and the reduction.
+// B^T for a Matmul whose 16-bit B is [K, N] (not transposed): a block moves
+// a 64 x 64 tile through LDS (66-element rows: a column read touches 32
+// distinct banks). Whole tiles of 8-aligned shapes move as 16-byte runs (a
+// thread takes two runs in and gathers two runs out); other tiles element
+// by element.
+__device__ void transpose2d_run(const uint16_t *__restrict__ in, uint16_t *__restrict__ out, const Transpose2DConstants &p) {
+    __shared__ uint16_t tile[64][66];
+    const uint32_t tr = blockIdx.y * 64, tc = blockIdx.x * 64;  // tile origin in `in`
+    const bool vec = p.rows % 8 == 0 && p.cols % 8 == 0 && tr + 64 <= p.rows && tc + 64 <= p.cols &&
+                     ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(out)) & 15) == 0;
+    if (vec) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t c = threadIdx.x + 256 * j, row = c >> 3, run = c & 7;
+            const u32x4 v = *reinterpret_cast<const u32x4 *>(in + (uint64_t)(tr + row) * p.cols + tc + run * 8);
+            uint32_t *dst = reinterpret_cast<uint32_t *>(&tile[row][run * 8]);
+            dst[0] = v.x;
+            dst[1] = v.y;
+            dst[2] = v.z;
+            dst[3] = v.w;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t c = threadIdx.x + 256 * j, orow = c >> 3, run = c & 7;  // out row tc + orow
+            uint32_t w[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                w[e] = (uint32_t)tile[run * 8 + 2 * e][orow] | ((uint32_t)tile[run * 8 + 2 * e + 1][orow] << 16);
+            *reinterpret_cast<u32x4 *>(out + (uint64_t)(tc + orow) * p.rows + tr + run * 8) = u32x4{w[0], w[1], w[2], w[3]};
+        }
+        return;
+    }
+    const uint32_t tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 2 elements per thread per row pass
+    for (uint32_t r = ty; r < 64; r += 8) {
+        const uint32_t row = tr + r, col = tc + 2 * tx;
+        if (row < p.rows) {
+            if (col < p.cols) tile[r][2 * tx] = in[(uint64_t)row * p.cols + col];
+            if (col + 1 < p.cols) tile[r][2 * tx + 1] = in[(uint64_t)row * p.cols + col + 1];
+        }
+    }
+    __syncthreads();
+    for (uint32_t c = ty; c < 64; c += 8) {
+        const uint32_t orow = tc + c, ocol = tr + 2 * tx;  // out[orow][ocol] = in[ocol][orow]
+        if (orow < p.cols) {
+            if (ocol < p.rows) out[(uint64_t)orow * p.rows + ocol] = tile[2 * tx][c];
+            if (ocol + 1 < p.rows) out[(uint64_t)orow * p.rows + ocol + 1] = tile[2 * tx + 1][c];
+        }
+    }
+}
+
+POPCORN_KERNEL void __launch_bounds__(256) transpose2d_b16(const uint16_t *in, uint16_t *out, Transpose2DConstants p) {
+    transpose2d_run(in, out, p);
+}
+
 #define GEMM_MFMA_SPLITK(name, T)                                                                 \
     POPCORN_KERNEL void __launch_bounds__(512)                                                    \
         name(const uint16_t *a, const uint16_t *b, float *partial, MatmulConstants p) {          \

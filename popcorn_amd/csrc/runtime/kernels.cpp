@@ -757,6 +757,38 @@ private:
 };
 
 constexpr int64_t kMaxStagedK = 16384;  // x staged as f32 in 64 KB of LDS
+// A Matmul with a non-transposed 16-bit B [K, N] and m > 1: B^T into
+// scratch (transpose2d_b16), then the transposed-B route (the MFMA or
+// skinny kernels) on it.
+std::unique_ptr<Kernel> makeMatmul(const Tensor &a, const Tensor &b, const Tensor &c, int64_t m, int64_t k, int64_t n,
+                                   bool transposeB);
+class TransposeBMatmulKernel : public Kernel {
+public:
+    TransposeBMatmulKernel(const Tensor &a, const Tensor &b, const Tensor &c, int64_t m, int64_t k, int64_t n)
+        : a_(a), b_(b), c_(c), m_(m), k_(k), n_(n) {}
+    std::vector<Binding> tensors() const override { return {{a_, kRead}, {b_, kRead}, {c_, kWrite}}; }
+    std::string describe() const override {
+        // the inner route's kernels, for B^T in (256-byte aligned) scratch
+        Tensor bt(reinterpret_cast<void *>(uintptr_t{1} << 20), Shape({n_, k_}), b_.dataType);
+        return "transpose2d_b16," + makeMatmul(a_, bt, c_, m_, k_, n_, true)->describe();
+    }
+    void encode(KernelCommandEncoder &enc) const override {
+        enc.withTemporaryTensor(ScratchSpec{{n_, k_}, b_.dataType}, [&](Tensor bt) {
+            Transpose2DConstants tc{(uint32_t)k_, (uint32_t)n_};
+            DispatchSize ds;
+            ds.grid = dim3((unsigned)cdiv(n_, 64), (unsigned)cdiv(k_, 64), 1);
+            ds.block = dim3(kBlock, 1, 1);
+            FixedDispatch t("transpose2d_b16", {{b_, kRead}, {bt, kWrite}}, {bytesOf(tc)}, ds);
+            enc.dispatch(t);
+            makeMatmul(a_, bt, c_, m_, k_, n_, true)->encode(enc);
+        });
+    }
+
+private:
+    Tensor a_, b_, c_;
+    int64_t m_, k_, n_;
+};
+
 
 std::unique_ptr<Kernel> makeMatmul(const Tensor &a, const Tensor &b, const Tensor &c, int64_t m, int64_t k, int64_t n,
                                    bool transposeB) {
@@ -789,6 +821,12 @@ std::unique_ptr<Kernel> makeMatmul(const Tensor &a, const Tensor &b, const Tenso
     // GEMM path, Matmul.swift:175-196); 16-byte rows needed (K % 8 == 0).
     {
         const DataType t = a.dataType;
+        // a [K, N] B (the reference's mpp_matmul without _tb): transposed
+        // into scratch first, then this route (the scratch is 256-byte aligned)
+        if (!transposeB && (t == DataType::f16 || t == DataType::bf16) && b.dataType == t &&
+            (c.dataType == t || c.dataType == DataType::f32) && k % 8 == 0 && k > 0 && aligned16(a.data) &&
+            k < 65536 * 64 && n < 65536 * 64)
+            return std::make_unique<TransposeBMatmulKernel>(a, b, c, m, k, n);
         if (transposeB && (t == DataType::f16 || t == DataType::bf16) && b.dataType == t &&
             (c.dataType == t || c.dataType == DataType::f32) && k % 8 == 0 && k > 0 && aligned16(a.data) &&
             aligned16(b.data)) {

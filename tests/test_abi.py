@@ -181,6 +181,12 @@ def test_matmul_routing_and_validation():
         "matvec_nk_stream_bf16_bf16_bf16_r1"
     assert pa.Kernels.Matmul(x, T([2304, 300]), T([1, 300]), False).describe() == "matvec_bf16_bf16_bf16"
     assert pa.Kernels.Matmul(T([4, 8], "f32"), T([8, 3], "f32"), T([4, 3], "f32")).describe() == "matmul_tiled"
+    # a 16-bit [K, N] B: transposed into scratch, then the matrix-core route
+    assert pa.Kernels.Matmul(T([2048, 3072]), T([3072, 3072]), T([2048, 3072]), False).describe().startswith(
+        "transpose2d_b16,matmul_mfma_bf16_bf16_bf16_")
+    assert pa.Kernels.Matmul(T([8, 2304]), T([2304, 9216]), T([8, 9216], "f32"), False).describe() == \
+        "transpose2d_b16,matmul_skinny_bf16_bf16_f32_m16"
+    assert pa.Kernels.Matmul(T([8, 2300]), T([2300, 64]), T([8, 64]), False).describe() == "matmul_tiled_bf16_bf16_bf16"
     with pytest.raises(pa.PopcornError) as e:  # Matmul.swift:85-87
         pa.Kernels.Matmul(x, T([9216, 2300]), T([1, 9216]), True)
     assert e.value.code == pa.PopcornError.TENSOR_SHAPE_MISMATCH

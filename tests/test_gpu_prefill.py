@@ -41,6 +41,27 @@ def test_mfma_matmul_vs_oracle(env, at, ot, M, K, N):
     assert_out(got, ref, 1e-5 if ot == "f32" else EPS[at], ot, f"mfma gemm {at}->{ot} {M}x{K}x{N}")
 
 
+@pytest.mark.parametrize("at,ot", [("f16", "f16"), ("bf16", "bf16"), ("bf16", "f32")])
+@pytest.mark.parametrize("M,K,N", [(128, 64, 128), (130, 200, 90), (256, 1024, 384), (8, 2304, 1000), (300, 8, 129),
+                                   (64, 72, 4097)])
+def test_mfma_matmul_b_not_transposed_vs_oracle(env, at, ot, M, K, N):
+    # a [K, N] B (the reference's mpp_matmul without _tb, Matmul.swift:203-214):
+    # B^T into scratch by transpose2d_b16 (ragged 64 x 64 tiles included),
+    # then the transposed-B matrix-core route (MFMA tiles, or skinny at M <= 64)
+    pa, lib, stream, enc = env
+    a = rounded(O.normal(M + K + 1, (M, K)), at)
+    b = rounded(O.normal(N + K + 2, (K, N), std=0.02), at)
+    c = pa.Tensor.empty([M, N], ot)
+    k = pa.Kernels.Matmul(upload(pa, a, at), upload(pa, b, at), c, False)
+    assert k.function_names[0] == "transpose2d_b16"
+    assert k.function_names[1].startswith(("matmul_mfma_", "matmul_skinny_"))
+    enc.encode(k)
+    stream.synchronize()
+    got = download(c, stream).reshape(M, N)
+    ref = O.matmul(a, b, M, K, N, False).reshape(M, N)
+    assert_out(got, ref, 1e-5 if ot == "f32" else EPS[at], ot, f"gemm B [K, N] {at}->{ot} {M}x{K}x{N}")
+
+
 @pytest.mark.parametrize("at", ["f16", "bf16"])
 def test_mfma_matmul_integer_exact(env, at):
     # small integers: every product and partial sum is exact in f32, so the
