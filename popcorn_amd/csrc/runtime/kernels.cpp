@@ -857,6 +857,20 @@ std::unique_ptr<Kernel> makeMatmul(const Tensor &a, const Tensor &b, const Tenso
                                                    grid1(cdiv(m, tile.bm) * cdiv(n, tile.bn), tile.threads));
         }
     }
+    // m > 1 with f32 output and an f32 operand (the reference's MPP f32
+    // combinations f32 x f32, f32 x bf16, bf16 x f32, Matmul.swift:203-214):
+    // the f32 matrix-core tiles (gemm_f32.hip), B either way round; rows of
+    // 4 values in 16-byte-aligned buffers
+    {
+        const DataType ta = a.dataType, tb = b.dataType, f32 = DataType::f32, bf16 = DataType::bf16;
+        const bool combo = c.dataType == f32 && ((ta == f32 && (tb == f32 || tb == bf16)) || (ta == bf16 && tb == f32));
+        if (combo && m > 1 && k % 4 == 0 && (transposeB || n % 4 == 0) && aligned16(a.data) && aligned16(b.data)) {
+            MatmulConstants mc{(uint32_t)m, (uint32_t)k, (uint32_t)n, transposeB ? 1u : 0u};
+            const std::string fn = std::string("matmul_mfma_") + tag(ta) + "_" + tag(tb) + "_f32" + (transposeB ? "_tb" : "");
+            return std::make_unique<FixedDispatch>(fn, binds, std::vector<std::vector<uint8_t>>{bytesOf(mc)},
+                                                   grid1(cdiv(m, 128) * cdiv(n, 128), kBlock));
+        }
+    }
     // the SIMT tiles (matmul.hip) in the place of the reference's matmul_typed
     std::string fn = plainName("matmul_tiled", a.dataType, b.dataType, c.dataType);
     if (fn.empty())

@@ -180,7 +180,12 @@ def test_matmul_routing_and_validation():
     assert pa.Kernels.Matmul(T([1, 9216]), T([2304, 9216]), T([1, 2304]), True).describe() == \
         "matvec_nk_stream_bf16_bf16_bf16_r1"
     assert pa.Kernels.Matmul(x, T([2304, 300]), T([1, 300]), False).describe() == "matvec_bf16_bf16_bf16"
-    assert pa.Kernels.Matmul(T([4, 8], "f32"), T([8, 3], "f32"), T([4, 3], "f32")).describe() == "matmul_tiled"
+    assert pa.Kernels.Matmul(T([4, 8], "f32"), T([8, 4], "f32"), T([4, 4], "f32")).describe() == "matmul_mfma_f32_f32_f32"
+    assert pa.Kernels.Matmul(T([4, 8], "f32"), T([8, 3], "f32"), T([4, 3], "f32")).describe() == "matmul_tiled"  # N % 4
+    assert pa.Kernels.Matmul(T([64, 256], "f32"), T([300, 256]), T([64, 300], "f32"), True).describe() == \
+        "matmul_mfma_f32_bf16_f32_tb"
+    assert pa.Kernels.Matmul(T([64, 256]), T([256, 300], "f32"), T([64, 300], "f32"), False).describe() == \
+        "matmul_mfma_bf16_f32_f32"
     # a 16-bit [K, N] B: transposed into scratch, then the matrix-core route
     assert pa.Kernels.Matmul(T([2048, 3072]), T([3072, 3072]), T([2048, 3072]), False).describe().startswith(
         "transpose2d_b16,matmul_mfma_bf16_bf16_bf16_")

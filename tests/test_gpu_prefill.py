@@ -62,6 +62,44 @@ def test_mfma_matmul_b_not_transposed_vs_oracle(env, at, ot, M, K, N):
     assert_out(got, ref, 1e-5 if ot == "f32" else EPS[at], ot, f"gemm B [K, N] {at}->{ot} {M}x{K}x{N}")
 
 
+@pytest.mark.parametrize("at,bt", [("f32", "f32"), ("f32", "bf16"), ("bf16", "f32")])
+@pytest.mark.parametrize("tb", [True, False])
+@pytest.mark.parametrize("M,K,N", [(2, 4, 4), (130, 200, 92), (256, 1028, 384), (300, 36, 132), (1024, 3072, 1024)])
+def test_mfma_f32_matmul_vs_oracle(env, at, bt, tb, M, K, N):
+    # f32 output with an f32 operand (the reference's MPP f32 combinations,
+    # Matmul.swift:203-214) on v_mfma_f32_16x16x4_f32: bf16 operands widen
+    # exactly, products and sums in f32 in another order than the oracle's,
+    # so the f32 bar; ragged tiles, K not a multiple of the 16-value step
+    pa, lib, stream, enc = env
+    a = rounded(O.normal(M + K + 3, (M, K)), at)
+    b = rounded(O.normal(N + K + 4, (N, K) if tb else (K, N), std=0.05), bt)
+    c = pa.Tensor.empty([M, N], "f32")
+    k = pa.Kernels.Matmul(upload(pa, a, at), upload(pa, b, bt), c, tb)
+    assert k.function_names == [f"matmul_mfma_{at}_{bt}_f32" + ("_tb" if tb else "")]
+    enc.encode(k)
+    stream.synchronize()
+    got = download(c, stream).reshape(M, N)
+    ref = O.matmul(a, b, M, K, N, tb).reshape(M, N)
+    assert_out(got, ref, 1e-5, "f32", f"f32 mfma gemm {at}x{bt} tb={tb} {M}x{K}x{N}")
+
+
+def test_mfma_f32_matmul_integer_exact(env):
+    # small integers: every product and partial sum is exact in f32, so the
+    # result is exact whatever the order; pins the k order of the 16-value
+    # step and the transposed B staging
+    pa, lib, stream, enc = env
+    rng = np.random.default_rng(31)
+    M, K, N = 200, 516, 260
+    a = rng.integers(-8, 9, (M, K)).astype(np.float32)
+    b = rng.integers(-8, 9, (K, N)).astype(np.float32)
+    c = pa.Tensor.empty([M, N], "f32")
+    k = pa.Kernels.Matmul(upload(pa, a, "f32"), upload(pa, b, "f32"), c, False)
+    assert k.function_names == ["matmul_mfma_f32_f32_f32"]
+    enc.encode(k)
+    stream.synchronize()
+    np.testing.assert_array_equal(download(c, stream).reshape(M, N), (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32))
+
+
 @pytest.mark.parametrize("at", ["f16", "bf16"])
 def test_mfma_matmul_integer_exact(env, at):
     # small integers: every product and partial sum is exact in f32, so the
