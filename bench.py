@@ -470,6 +470,31 @@ def prefill_attention_f32(pa, lib, stream, enc, reps=4):
     return out
 
 
+def matmul_forms(pa, lib, stream, enc, reps=5):
+    """The reference's other MPP Matmul forms (Matmul.swift:203-214) at
+    2048 x 3072 x 3072: a [K, N] bf16 B (transposed into scratch, then the
+    MFMA tiles) and f32 output with f32 or mixed f32/bf16 operands (the f32
+    matrix-core tiles); frac is of the dense bf16 or f32 matrix-core peak."""
+    M, K, N = 2048, 3072, 3072
+    out = {}
+    for at, bt, ot, tb in (("bf16", "bf16", "bf16", False), ("f32", "f32", "f32", True), ("f32", "f32", "f32", False),
+                           ("f32", "bf16", "f32", True), ("bf16", "f32", "f32", False)):
+        a = pa.Tensor.empty([M, K], at)
+        b = pa.Tensor.empty([N, K] if tb else [K, N], bt)
+        c = pa.Tensor.empty([M, N], ot)
+        lib.fill_normal(a, 11, stream=stream)
+        lib.fill_normal(b, 12, std=0.02, stream=stream)
+        k = pa.Kernels.Matmul(a, b, c, tb)
+        enc.encode(k)
+        stream.synchronize()
+        us = timed_launches(pa, stream, enc, [k] * reps)
+        tf = 2.0 * M * N * K / (us * 1e-6) / 1e12
+        peak = MFMA_PEAK_F16_TFLOPS if (at, bt) == ("bf16", "bf16") else MFMA_PEAK_F32_TFLOPS
+        out[f"{at}x{bt}->{ot}" + ("_tb" if tb else "")] = {"kernels": k.function_names, "us": round(us, 1),
+                                                            "TFLOP_s": round(tf, 1), "frac": round(tf / peak, 3)}
+    return out
+
+
 def library_reference():
     """The config-5 shapes through the vendor libraries PyTorch calls on ROCm
     (torch.matmul -> hipBLASLt, scaled_dot_product_attention's flash and
@@ -675,6 +700,7 @@ def main():
         prefill = prefill_config5(pa, lib, stream, pa.KernelCommandEncoder(lib, stream))
         prefill["attention_hd512"] = prefill_attention_hd512(pa, lib, stream, pa.KernelCommandEncoder(lib, stream))
         prefill["attention_f32"] = prefill_attention_f32(pa, lib, stream, pa.KernelCommandEncoder(lib, stream))
+        prefill["matmul_forms"] = matmul_forms(pa, lib, stream, pa.KernelCommandEncoder(lib, stream))
         if args.library_reference:
             prefill["library_reference"] = library_reference()
 
