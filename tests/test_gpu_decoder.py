@@ -274,7 +274,8 @@ def test_gemma2_2b_step_matches_oracle(env):
     dec.close()
 
 
-def test_gemma2_2b_every_layer_tight(env):
+@pytest.mark.parametrize("weight_bits", [16, 4])
+def test_gemma2_2b_every_layer_tight(env, weight_bits):
     # BASELINE config 4 at full size, every one of the 26 layers held to the
     # 2e-3 bar on the GPU's own inputs of each stage (not only the last
     # layer): randomize() fills each weight and cache buffer with one
@@ -285,23 +286,26 @@ def test_gemma2_2b_every_layer_tight(env):
     # entering the layer; the attention (cache rows 0..4096) from the GPU's q;
     # the O projection from its attention; the post-attention residual; the
     # gated MLP from that residual; and the residual leaving the layer, which
-    # the next layer's checks start from (every outcome is carried on).
+    # the next layer's checks start from (every outcome is carried on). With
+    # 4-bit weights the oracle takes them dequantized (q * scale + bias in f32).
     pa, lib, stream, enc = env
     import popcorn_amd.decoder as D
 
-    full = D.DecoderConfig(graph_steps=1)
+    full = D.DecoderConfig(graph_steps=1, weight_bits=weight_bits)
     H, Nq, Nkv, Hd, L, eps = full.hidden, full.query_heads, full.kv_heads, full.head_dim, full.layers, full.eps
     QW, KW = Nq * Hd, Nkv * Hd
     token, pos = 321, 4096
     xs = None  # the outcomes of the residual entering layer l
     for l in range(L):
-        dec = D.Decoder(lib, stream, D.DecoderConfig(graph_steps=1, layers=l + 1))
+        dec = D.Decoder(lib, stream, D.DecoderConfig(graph_steps=1, layers=l + 1, weight_bits=weight_bits))
         dec.randomize(seed=0)
         dec.reset(token, pos)
         dec.step(1, use_graph=False)
         if xs is None:
             emb = _weight(dec, "embedding", 0, stream)
-            xs = [O.round_to(O.scalar_mul(emb[token], np.float32(np.sqrt(np.float32(H)))), O.BF16)]
+            # the gathered row is stored in bf16 (a 4-bit row dequantized), then scaled
+            row = O.round_to(emb[token], O.BF16)
+            xs = [O.round_to(O.scalar_mul(row, np.float32(np.sqrt(np.float32(H)))), O.BF16)]
         W = {n: _weight(dec, t, l, stream) for n, t in LAYER_WEIGHTS}
         kc = download(dec.tensor("k_cache", l), stream)[0]
         vc = download(dec.tensor("v_cache", l), stream)[0]
