@@ -347,6 +347,160 @@ __device__ void gemm_nt_direct(const uint16_t *__restrict__ A, const uint16_t *_
     }
 }
 
+// ---- whole-line pipeline ("e" tiles, K % 64 == 0) ---------------------------
+// The same tile product with K = 64 per stage: 128-byte LDS rows, so each
+// copy instruction (8 lanes per row, buffer_load ... lds) requests whole
+// 128-byte lines. The 64-byte rows of the pipeline above fetch each line
+// twice, a stage apart, and the L2 -> LDS copy rate bounds those tiles
+// (config-5 gate 283 -> 261 us, down 322 -> 290 us, bit for bit the same
+// products). Two stage buffers; the copies of stage kt + 2 are issued at
+// the barrier before the last K-16 quarter of stage kt. Chunk c of row r
+// sits in slot c ^ ((r >> 1) & 7): the 16 rows a quarter-wave of a
+// fragment read touches cover all 64 banks.
+constexpr int BK64 = 64;
+template <typename T, typename O, int BM, int BN, int WM_N, int WN_N, bool SPLITK = false>
+__device__ void gemm_nt_lines(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
+                                 typename O::storage *__restrict__ C, const MatmulConstants &p,
+                                 float *__restrict__ P = nullptr) {
+    constexpr int NW = WM_N * WN_N;
+    constexpr int WM = BM / WM_N, WN = BN / WN_N;
+    constexpr int TM = WM / 32, TN = WN / 32;
+    constexpr int kRowB = BK64 * 2;               // 128 bytes per LDS row
+    constexpr int kStageB = (BM + BN) * kRowB;    // bytes per stage
+    constexpr int kInstA = BM / (8 * NW), kInstB = BN / (8 * NW);  // wave instructions per stage
+    static_assert(kInstA * 8 * NW == BM && kInstB * 8 * NW == BN, "tile rows / waves");
+    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * kStageB];
+
+    const uint32_t M = p.M, N = p.N, K = p.K;
+    const uint32_t nM = (M + BM - 1) / BM, nN = (N + BN - 1) / BN;
+    uint32_t pm, pn;
+    tile_of(blockIdx.x, nM, nN, pm, pn);
+    const uint32_t bm = pm * BM, bn = pn * BN;
+    const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t wm = (wave / WN_N) * WM, wn = (wave % WN_N) * WN;
+
+    // Copies through buffer resources over the tile's rows: rows past M or
+    // N fall outside the resource and read as zeros. A lane's byte offset is
+    // the same for every instruction and both operands; instruction i adds
+    // i NW 8 rows and the stage its K offset, both in the scalar offset.
+    static_assert(NW % 2 == 0, "one chunk swizzle per lane for every instruction");
+    const uint32_t lr = lane >> 3, lpos = lane & 7;
+    const uint32_t kBase = SPLITK ? blockIdx.y * (K / gridDim.y) : 0u;
+    const uint64_t rowB = (uint64_t)K * 2u;
+    const uint32_t bytesA = (uint32_t)min((uint64_t)(M - bm) * rowB, (uint64_t)0xffffffffu);
+    const uint32_t bytesB = (uint32_t)min((uint64_t)(N - bn) * rowB, (uint64_t)0xffffffffu);
+    const __amdgpu_buffer_rsrc_t rsA = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(A + (uint64_t)bm * K), 0, (int)bytesA, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsB = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(B + (uint64_t)bn * K), 0, (int)bytesB, 0x00020000);
+    const uint32_t voff = (wave * 8 + lr) * (uint32_t)rowB + ((lpos ^ (((wave & 1) * 4 + (lr >> 1)) & 7)) << 4);
+    const uint32_t instB = NW * 8 * (uint32_t)rowB;  // bytes between a wave's instructions
+    auto issue = [&](uint32_t kt) {
+        const uint32_t kb = (kBase + kt * BK64) * 2u;
+        uint8_t *stage = smem + (kt & 1) * kStageB;
+#pragma unroll
+        for (int i = 0; i < kInstA; ++i) {
+            const uint32_t r0 = (i * NW + wave) * 8;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsA, (lds_void *)(stage + r0 * kRowB), 16, voff, kb + i * instB, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < kInstB; ++i) {
+            const uint32_t r0 = (i * NW + wave) * 8;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsB, (lds_void *)(stage + (BM + r0) * kRowB), 16, voff, kb + i * instB, 0, 0);
+        }
+    };
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int mi = 0; mi < TM; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < TN; ++ni)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[mi][ni][i] = 0.0f;
+
+    auto frag = [&](const uint8_t *base, uint32_t row, uint32_t kc) {
+        return *reinterpret_cast<const u32x4 *>(base + row * kRowB + ((kc ^ ((row >> 1) & 7)) << 4));
+    };
+    // fragment mi of A / ni of B for K-16 quarter kk of stage kt
+    auto fragA = [&](uint32_t kt, int kk, int mi) {
+        return frag(smem + (kt & 1) * kStageB, wm + mi * 32 + (lane & 31), kk * 2 + (lane >> 5));
+    };
+    auto fragB = [&](uint32_t kt, int kk, int ni) {
+        return frag(smem + (kt & 1) * kStageB + BM * kRowB, wn + ni * 32 + (lane & 31), kk * 2 + (lane >> 5));
+    };
+
+    const uint32_t nk = (SPLITK ? K / gridDim.y : K) / BK64;
+    issue(0);
+    if (nk > 1) issue(1);
+    if (nk > 1) wait_vmcnt<kInstA + kInstB>();
+    else wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();
+    u32x4 fa[TM], fb[TN], fb2[TN];
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+#pragma unroll
+    for (int ni = 0; ni < TN; ++ni) {
+        fb[ni] = fragB(0, 0, ni);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int mi = 0; mi < TM; ++mi) {
+        fa[mi] = fragA(0, 0, mi);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    auto pin_order = [&] {
+        __builtin_amdgcn_sched_group_barrier(0x008, TN, 0);      // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, TN + 1, 0);  // DS reads
+#pragma unroll
+        for (int mi = 1; mi < TM; ++mi) {
+            __builtin_amdgcn_sched_group_barrier(0x008, TN, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
+        }
+    };
+    // one K-16 quarter: products with (fa, fcur), while the next quarter's
+    // B fragments go to fnext and each A fragment is re-read for it
+    auto quarter = [&](u32x4 *fcur, u32x4 *fnext, uint32_t nkt, int nkk) {
+#pragma unroll
+        for (int ni = 0; ni < TN; ++ni) fnext[ni] = fragB(nkt, nkk, ni);
+#pragma unroll
+        for (int mi = 0; mi < TM; ++mi) {
+#pragma unroll
+            for (int ni = 0; ni < TN; ++ni) acc[mi][ni] = Mma<T>::run(fa[mi], fcur[ni], acc[mi][ni]);
+            fa[mi] = fragA(nkt, nkk, mi);
+        }
+        pin_order();
+    };
+    for (uint32_t kt = 0; kt < nk; ++kt) {
+        quarter(fb, fb2, kt, 1);
+        quarter(fb2, fb, kt, 2);
+        quarter(fb, fb2, kt, 3);
+        // this wave's reads of stage kt are issued; wait for them and for
+        // its copies of stage kt + 1 (the only ones outstanding), then the
+        // buffer of stage kt takes the copies of stage kt + 2. In the last
+        // pass the reads of "stage kt + 1" fetch a buffer no copy writes.
+        wait_vmcnt<0>();
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_s_barrier();
+        if (kt + 2 < nk) issue(kt + 2);
+        quarter(fb2, fb, kt + 1, 0);
+    }
+
+#pragma unroll
+    for (int mi = 0; mi < TM; ++mi) {
+#pragma unroll
+        for (int ni = 0; ni < TN; ++ni) {
+            const uint32_t col = bn + wn + ni * 32 + (lane & 31);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const uint32_t row = bm + wm + mi * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+                if (row < M && col < N) {
+                    if constexpr (SPLITK)
+                        P[((uint64_t)blockIdx.y * M + row) * N + col] = acc[mi][ni][i];
+                    else
+                        C[(uint64_t)row * N + col] = O::store(acc[mi][ni][i]);
+                }
+            }
+        }
+    }
+}
+
 // C = sum over the gridDim.y-way split of P [splits][M][N] (f32), rounded
 // once to C's dtype; 4 elements per thread (M N % 4 == 0).
 template <typename O>
@@ -387,7 +541,17 @@ __device__ void gemm_splitk_reduce(const float *__restrict__ P, typename O::stor
         name(const uint16_t *a, const uint16_t *b, O::storage *c, MatmulConstants p) {            \
         gemm_nt_direct<T, O, BM, BN, WMN, WNN>(a, b, c, p);                                       \
     }
+#define GEMM_MFMA_E(name, T, O, BM, BN, WMN, WNN)                                                 \
+    POPCORN_KERNEL void __launch_bounds__(64 * WMN * WNN)                                         \
+        name(const uint16_t *a, const uint16_t *b, O::storage *c, MatmulConstants p) {            \
+        gemm_nt_lines<T, O, BM, BN, WMN, WNN>(a, b, c, p);                                        \
+    }
 #define GEMM_MFMA_TILES(base, T, O)                          \
+    GEMM_MFMA_E(base##_e256x384, T, O, 256, 384, 2, 4)       \
+    GEMM_MFMA_E(base##_e256x256, T, O, 256, 256, 2, 4)       \
+    GEMM_MFMA_E(base##_e128x128, T, O, 128, 128, 2, 2)       \
+    GEMM_MFMA_E(base##_e128x256, T, O, 128, 256, 2, 4)       \
+    GEMM_MFMA_E(base##_e128x192, T, O, 128, 192, 2, 2)       \
     GEMM_MFMA_D(base##_d256x256, T, O, 256, 256, 2, 4)       \
     GEMM_MFMA_D(base##_d128x128, T, O, 128, 128, 2, 2)       \
     GEMM_MFMA_D(base##_d128x256, T, O, 128, 256, 2, 4)       \
@@ -408,7 +572,7 @@ GEMM_MFMA_TILES(matmul_mfma_f16_f16_f32, F16, F32)
 GEMM_MFMA_TILES(matmul_mfma_bf16_bf16_bf16, BF16, BF16)
 GEMM_MFMA_TILES(matmul_mfma_bf16_bf16_f32, BF16, F32)
 
-// Split-K form of the 256 x 384 tile (f32 partials) and the reduction.
+// Split-K forms of the 256 x 384 tile (f32 partials) and the reduction.
 // B^T for a Matmul whose 16-bit B is [K, N] (not transposed): a block moves
 // a 64 x 64 tile through LDS (66-element rows: a column read touches 32
 // distinct banks). Whole tiles of 8-aligned shapes move as 16-byte runs (a
@@ -474,8 +638,15 @@ POPCORN_KERNEL void __launch_bounds__(256) transpose2d_b16(const uint16_t *in, u
         name(const float *partial, O::storage *c, MatmulConstants p, uint32_t splits) {                \
         gemm_splitk_reduce<O>(partial, c, p, splits);                                                  \
     }
+#define GEMM_MFMA_SPLITK_E(name, T)                                                               \
+    POPCORN_KERNEL void __launch_bounds__(512)                                                    \
+        name(const uint16_t *a, const uint16_t *b, float *partial, MatmulConstants p) {          \
+        gemm_nt_lines<T, F32, 256, 384, 2, 4, true>(a, b, nullptr, p, partial);                   \
+    }
 GEMM_MFMA_SPLITK(matmul_mfma_f16_splitk_d256x384, F16)
 GEMM_MFMA_SPLITK(matmul_mfma_bf16_splitk_d256x384, BF16)
+GEMM_MFMA_SPLITK_E(matmul_mfma_f16_splitk_e256x384, F16)
+GEMM_MFMA_SPLITK_E(matmul_mfma_bf16_splitk_e256x384, BF16)
 GEMM_SPLITK_REDUCE(matmul_splitk_reduce_f16, F16)
 GEMM_SPLITK_REDUCE(matmul_splitk_reduce_bf16, BF16)
 GEMM_SPLITK_REDUCE(matmul_splitk_reduce_f32, F32)

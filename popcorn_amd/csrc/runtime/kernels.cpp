@@ -667,16 +667,35 @@ struct GemmTile {
 };
 
 // "d" tiles copy operands global -> LDS directly (4 stages of K 32); they
-// need K % 32 == 0.
+// need K % 32 == 0. Their "e" forms copy whole 128-byte lines (2 stages of
+// K 64, buffer loads whose byte offsets stay below 2^31 over a tile's rows);
+// they need K % 64 == 0 and take every such shape.
+bool gemmLinesFit(int64_t k, int bn) { return k % 64 == 0 && (int64_t)(bn + 16) * k * 2 < (int64_t{1} << 31); }
+
+GemmTile gemmTileForm(int64_t m, int64_t n, int64_t k);
 GemmTile gemmTile(int64_t m, int64_t n, int64_t k) {
+    static const GemmTile lines[] = {{256, 256, 512, "e256x256"}, {128, 128, 256, "e128x128"}, {128, 256, 512, "e128x256"},
+                                     {128, 192, 256, "e128x192"}, {256, 384, 512, "e256x384"}};
+    const GemmTile t = gemmTileForm(m, n, k);
+    if (t.suffix[0] == 'd' && !std::getenv("POPCORN_GEMM_TILE") && gemmLinesFit(k, t.bn))
+        for (const GemmTile &e : lines)
+            if (std::string(e.suffix + 1) == std::string(t.suffix + 1)) return e;
+    return t;
+}
+
+GemmTile gemmTileForm(int64_t m, int64_t n, int64_t k) {
     static const GemmTile tiles[] = {{256, 256, 512, "t256x256"}, {256, 256, 256, "t256x256w4"},
                                      {256, 128, 512, "t256x128"}, {128, 256, 512, "t128x256"},
                                      {128, 128, 256, "t128x128"}, {256, 256, 512, "d256x256"},
                                      {128, 128, 256, "d128x128"}, {128, 256, 512, "d128x256"},
-                                     {128, 192, 256, "d128x192"}, {256, 384, 512, "d256x384"}};
+                                     {128, 192, 256, "d128x192"}, {256, 384, 512, "d256x384"},
+                                     {256, 256, 512, "e256x256"}, {128, 128, 256, "e128x128"},
+                                     {128, 256, 512, "e128x256"}, {128, 192, 256, "e128x192"},
+                                     {256, 384, 512, "e256x384"}};
     if (const char *e = std::getenv("POPCORN_GEMM_TILE")) {  // tuning override, e.g. "t256x128"
         for (const GemmTile &t : tiles)
-            if (std::string(t.suffix) == e && (t.suffix[0] != 'd' || k % 32 == 0)) return t;
+            if (std::string(t.suffix) == e && (t.suffix[0] != 'd' || k % 32 == 0) && (t.suffix[0] != 'e' || gemmLinesFit(k, t.bn)))
+                return t;
     }
     // 256 x 256 on 8 waves reuses each LDS stage for twice the MFMA work of
     // 128 x 128 but runs one block per CU, so it only pays when the tiles
@@ -750,7 +769,11 @@ public:
     }
 
 private:
-    std::string mainName() const { return std::string("matmul_mfma_") + tag(a_.dataType) + "_splitk_d256x384"; }
+    std::string mainName() const {
+        // each split's K a whole number of 64-deep stages; offsets span the full rows
+        const bool lines = gemmLinesFit(k_, 384) && k_ % (64 * splits_) == 0;
+        return std::string("matmul_mfma_") + tag(a_.dataType) + (lines ? "_splitk_e256x384" : "_splitk_d256x384");
+    }
     std::string reduceName() const { return std::string("matmul_splitk_reduce_") + tag(c_.dataType); }
     Tensor a_, b_, c_;
     int64_t m_, k_, n_, splits_;

@@ -112,6 +112,44 @@ def test_mfma_matmul_integer_exact(env, at):
     np.testing.assert_array_equal(got, (a.astype(np.int64) @ b.T.astype(np.int64)).astype(np.float32))
 
 
+TILES = [f"{f}{t}" for f in "ed" for t in ("256x384", "256x256", "128x128", "128x256", "128x192")]
+
+
+@pytest.mark.parametrize("tile", TILES)
+def test_mfma_matmul_every_tile_integer_exact(env, monkeypatch, tile):
+    # every direct-copy tile (POPCORN_GEMM_TILE) on ragged M and N, with 1, 2
+    # and 5 K stages (64 deep for the whole-line "e" tiles, 32 for "d"):
+    # small integers make the f32 result exact in any order, so every copy
+    # offset, LDS slot and fragment index is pinned; rows and columns past
+    # M and N read zeros or clamped rows and are not stored
+    monkeypatch.setenv("POPCORN_GEMM_TILE", tile)
+    rng = np.random.default_rng(21)
+    stage = 64 if tile[0] == "e" else 32
+    for at in ("f16", "bf16"):
+        for M, N, stages in [(300, 400, 1), (517, 131, 2), (264, 392, 5)]:
+            K = stage * stages
+            a = rng.integers(-4, 5, (M, K)).astype(np.float32)
+            b = rng.integers(-4, 5, (N, K)).astype(np.float32)
+            got, k = _gemm(env, a, b, at, "f32")
+            assert k.function_names == [f"matmul_mfma_{at}_{at}_f32_{tile}"]
+            np.testing.assert_array_equal(got, (a.astype(np.int64) @ b.T.astype(np.int64)).astype(np.float32),
+                                          err_msg=f"{tile} {at} {M}x{K}x{N}")
+
+
+@pytest.mark.parametrize("tile", TILES)
+@pytest.mark.parametrize("at,ot", [("f16", "f16"), ("bf16", "bf16")])
+def test_mfma_matmul_every_tile_vs_oracle(env, monkeypatch, tile, at, ot):
+    monkeypatch.setenv("POPCORN_GEMM_TILE", tile)
+    M, N = 390, 270
+    K = 448 if tile[0] == "e" else 416
+    a = rounded(O.normal(M + K + 1, (M, K)), at)
+    b = rounded(O.normal(N + K + 1, (N, K), std=0.02), at)
+    got, k = _gemm(env, a, b, at, ot)
+    assert k.function_names == [f"matmul_mfma_{at}_{at}_{ot}_{tile}"]
+    ref = O.matmul(a, b, M, K, N, True).reshape(M, N)
+    assert_out(got, ref, EPS[at], ot, f"mfma gemm {tile} {at}->{ot} {M}x{K}x{N}")
+
+
 @pytest.mark.parametrize("M,K,N", [(2048, 3072, 9216), (2048, 3072, 24576), (2048, 24576, 3072)])
 def test_mfma_matmul_config5_shapes_sampled(env, M, K, N):
     # BASELINE config 5 (Gemma-7B prefill, f16): QKV, gate/up, down. The
@@ -134,16 +172,18 @@ def test_mfma_matmul_config5_shapes_sampled(env, M, K, N):
 
 
 @pytest.mark.parametrize("at", ["f16", "bf16"])
-def test_mfma_matmul_split_k_integer_exact(env, at):
-    # 32 ragged 256 x 384 tiles x 8 K splits of 2048: small integers keep every
+@pytest.mark.parametrize("K,form", [(16384, "e"), (16640, "d")])
+def test_mfma_matmul_split_k_integer_exact(env, at, K, form):
+    # 32 ragged 256 x 384 tiles x 8 K splits (of 2048: whole-line stages of
+    # 64; of 2080: 64-byte-row stages of 32): small integers keep every
     # partial sum exact, so the f32 result is exact whatever the split
     pa, lib, stream, enc = env
     rng = np.random.default_rng(13)
-    M, K, N = 2000, 16384, 1500
+    M, N = 2000, 1500
     a = rng.integers(-4, 5, (M, K)).astype(np.float32)
     b = rng.integers(-4, 5, (N, K)).astype(np.float32)
     got, k = _gemm(env, a, b, at, "f32")
-    assert k.function_names == [f"matmul_mfma_{at}_splitk_d256x384", "matmul_splitk_reduce_f32"]
+    assert k.function_names == [f"matmul_mfma_{at}_splitk_{form}256x384", "matmul_splitk_reduce_f32"]
     # |sums| <= 16 K < 2^24: exact in f64 (BLAS) and in f32
     np.testing.assert_array_equal(got, (a.astype(np.float64) @ b.T.astype(np.float64)).astype(np.float32))
 
