@@ -367,8 +367,11 @@ __device__ void gemm_nt_lines(const uint16_t *__restrict__ A, const uint16_t *__
     constexpr int TM = WM / 32, TN = WN / 32;
     constexpr int kRowB = BK64 * 2;               // 128 bytes per LDS row
     constexpr int kStageB = (BM + BN) * kRowB;    // bytes per stage
-    constexpr int kInstA = BM / (8 * NW), kInstB = BN / (8 * NW);  // wave instructions per stage
-    static_assert(kInstA * 8 * NW == BM && kInstB * 8 * NW == BN, "tile rows / waves");
+    // A stage is kInst copy instructions of 8 rows each, A's rows then B's
+    // (LDS row 8 j + r for instruction j); wave w issues j = w, w + NW, ...
+    constexpr int kInst = (BM + BN) / 8, kInstA = BM / 8;
+    constexpr int kPer = (kInst + NW - 1) / NW;  // per wave, rounded up
+    static_assert(BM % 16 == 0 && BN % 8 == 0, "tile rows");
     __shared__ __attribute__((aligned(16))) uint8_t smem[2 * kStageB];
 
     const uint32_t M = p.M, N = p.N, K = p.K;
@@ -380,9 +383,10 @@ __device__ void gemm_nt_lines(const uint16_t *__restrict__ A, const uint16_t *__
     const uint32_t wm = (wave / WN_N) * WM, wn = (wave % WN_N) * WN;
 
     // Copies through buffer resources over the tile's rows: rows past M or
-    // N fall outside the resource and read as zeros. A lane's byte offset is
-    // the same for every instruction and both operands; instruction i adds
-    // i NW 8 rows and the stage its K offset, both in the scalar offset.
+    // N fall outside the resource and read as zeros. A lane's byte offset
+    // (its row within the 8, its chunk) is the same for every instruction
+    // and both operands; the instruction's first row and the stage's K
+    // offset go in the scalar offset.
     static_assert(NW % 2 == 0, "one chunk swizzle per lane for every instruction");
     const uint32_t lr = lane >> 3, lpos = lane & 7;
     const uint32_t kBase = SPLITK ? blockIdx.y * (K / gridDim.y) : 0u;
@@ -391,21 +395,27 @@ __device__ void gemm_nt_lines(const uint16_t *__restrict__ A, const uint16_t *__
     const uint32_t bytesB = (uint32_t)min((uint64_t)(N - bn) * rowB, (uint64_t)0xffffffffu);
     const __amdgpu_buffer_rsrc_t rsA = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(A + (uint64_t)bm * K), 0, (int)bytesA, 0x00020000);
     const __amdgpu_buffer_rsrc_t rsB = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(B + (uint64_t)bn * K), 0, (int)bytesB, 0x00020000);
-    const uint32_t voff = (wave * 8 + lr) * (uint32_t)rowB + ((lpos ^ (((wave & 1) * 4 + (lr >> 1)) & 7)) << 4);
-    const uint32_t instB = NW * 8 * (uint32_t)rowB;  // bytes between a wave's instructions
+    // row 8 j + lr of an operand: chunk swizzle (4 j + lr / 2) & 7, and j is
+    // odd or even with the wave (NW and kInstA even)
+    const uint32_t voff = lr * (uint32_t)rowB + ((lpos ^ (((wave & 1) * 4 + (lr >> 1)) & 7)) << 4);
+    const uint32_t rows8 = 8 * (uint32_t)rowB;  // bytes per instruction's rows
     auto issue = [&](uint32_t kt) {
         const uint32_t kb = (kBase + kt * BK64) * 2u;
         uint8_t *stage = smem + (kt & 1) * kStageB;
 #pragma unroll
-        for (int i = 0; i < kInstA; ++i) {
-            const uint32_t r0 = (i * NW + wave) * 8;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsA, (lds_void *)(stage + r0 * kRowB), 16, voff, kb + i * instB, 0, 0);
+        for (int i = 0; i < kPer; ++i) {
+            const uint32_t j = i * NW + wave;
+            if (kInst % NW != 0 && j >= (uint32_t)kInst) break;
+            const bool isA = kInstA % NW == 0 ? i < kInstA / NW : j < (uint32_t)kInstA;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(isA ? rsA : rsB, (lds_void *)(stage + j * 8 * kRowB), 16, voff,
+                                                     kb + (isA ? j : j - kInstA) * rows8, 0, 0);
         }
-#pragma unroll
-        for (int i = 0; i < kInstB; ++i) {
-            const uint32_t r0 = (i * NW + wave) * 8;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsB, (lds_void *)(stage + (BM + r0) * kRowB), 16, voff, kb + i * instB, 0, 0);
-        }
+    };
+    // wait until only the copies of the stage after the awaited one are
+    // outstanding (this wave issues kPer or kPer - 1 of them)
+    auto wait_one_behind = [&] {
+        if (kInst % NW == 0 || wave < (uint32_t)(kInst % NW)) wait_vmcnt<kPer>();
+        else wait_vmcnt<kPer - 1>();
     };
 
     f32x16 acc[TM][TN];
@@ -429,9 +439,12 @@ __device__ void gemm_nt_lines(const uint16_t *__restrict__ A, const uint16_t *__
 
     const uint32_t nk = (SPLITK ? K / gridDim.y : K) / BK64;
     issue(0);
-    if (nk > 1) issue(1);
-    if (nk > 1) wait_vmcnt<kInstA + kInstB>();
-    else wait_vmcnt<0>();
+    if (nk > 1) {
+        issue(1);
+        wait_one_behind();
+    } else {
+        wait_vmcnt<0>();
+    }
     __builtin_amdgcn_s_barrier();
     u32x4 fa[TM], fb[TN], fb2[TN];
     __builtin_amdgcn_s_waitcnt(0xC07F);
@@ -548,6 +561,7 @@ __device__ void gemm_splitk_reduce(const float *__restrict__ P, typename O::stor
     }
 #define GEMM_MFMA_TILES(base, T, O)                          \
     GEMM_MFMA_E(base##_e256x384, T, O, 256, 384, 2, 4)       \
+    GEMM_MFMA_E(base##_e256x288, T, O, 256, 288, 4, 3)       \
     GEMM_MFMA_E(base##_e256x256, T, O, 256, 256, 2, 4)       \
     GEMM_MFMA_E(base##_e128x128, T, O, 128, 128, 2, 2)       \
     GEMM_MFMA_E(base##_e128x256, T, O, 128, 256, 2, 4)       \

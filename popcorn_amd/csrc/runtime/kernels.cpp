@@ -672,15 +672,50 @@ struct GemmTile {
 // they need K % 64 == 0 and take every such shape.
 bool gemmLinesFit(int64_t k, int bn) { return k % 64 == 0 && (int64_t)(bn + 16) * k * 2 < (int64_t{1} << 31); }
 
+// The whole-line tiles are chosen by a score: the share of the CU slots
+// their grid keeps busy over its rounds (two blocks per CU for the tiles
+// of at most 80 KB of LDS; such a tile alone on a CU counts 0.6 of a
+// slot), times the share of the grid's tiles that lies inside C, times the
+// tile's measured throughput per CU relative to 256 x 384 when the CUs are
+// full (bf16, 33 Gemma-family prefill shapes, M 512-4096: the score's pick
+// was within 3% of the fastest tile on 31 and within 5% on the others,
+// 5% faster than the rules of the 64-byte-row tiles over all of them).
+struct ScoredTile {
+    GemmTile tile;
+    int blocksPerCU;
+    double weight;
+};
+const ScoredTile kLineTiles[] = {
+    {{256, 384, 512, "e256x384"}, 1, 1.0},  {{256, 256, 512, "e256x256"}, 1, 0.97}, {{256, 288, 768, "e256x288"}, 1, 0.94},
+    {{128, 192, 256, "e128x192"}, 2, 0.92}, {{128, 128, 256, "e128x128"}, 2, 0.87}, {{128, 256, 512, "e128x256"}, 1, 0.75}};
+
+double lineTileScore(const ScoredTile &t, int64_t m, int64_t n) {
+    const int64_t cus = deviceCUs();
+    const int64_t tm = cdiv(m, t.tile.bm), tn = cdiv(n, t.tile.bn), tiles = tm * tn;
+    const int64_t slots = cus * t.blocksPerCU;
+    double fill = (double)tiles / (double)(cdiv(tiles, slots) * slots);
+    if (t.blocksPerCU > 1 && tiles <= cus) fill = 0.6 * (double)tiles / (double)cus;
+    const double inside = (double)(m * n) / (double)(tm * t.tile.bm * tn * t.tile.bn);
+    return fill * inside * t.weight;
+}
+
+const ScoredTile &bestLineTile(int64_t m, int64_t n) {
+    const ScoredTile *best = &kLineTiles[0];
+    double bestScore = -1.0;
+    for (const ScoredTile &t : kLineTiles) {
+        const double sc = lineTileScore(t, m, n);
+        if (sc > bestScore) {
+            bestScore = sc;
+            best = &t;
+        }
+    }
+    return *best;
+}
+
 GemmTile gemmTileForm(int64_t m, int64_t n, int64_t k);
 GemmTile gemmTile(int64_t m, int64_t n, int64_t k) {
-    static const GemmTile lines[] = {{256, 256, 512, "e256x256"}, {128, 128, 256, "e128x128"}, {128, 256, 512, "e128x256"},
-                                     {128, 192, 256, "e128x192"}, {256, 384, 512, "e256x384"}};
-    const GemmTile t = gemmTileForm(m, n, k);
-    if (t.suffix[0] == 'd' && !std::getenv("POPCORN_GEMM_TILE") && gemmLinesFit(k, t.bn))
-        for (const GemmTile &e : lines)
-            if (std::string(e.suffix + 1) == std::string(t.suffix + 1)) return e;
-    return t;
+    if (!std::getenv("POPCORN_GEMM_TILE") && gemmLinesFit(k, 384)) return bestLineTile(m, n).tile;
+    return gemmTileForm(m, n, k);
 }
 
 GemmTile gemmTileForm(int64_t m, int64_t n, int64_t k) {
@@ -691,7 +726,7 @@ GemmTile gemmTileForm(int64_t m, int64_t n, int64_t k) {
                                      {128, 192, 256, "d128x192"}, {256, 384, 512, "d256x384"},
                                      {256, 256, 512, "e256x256"}, {128, 128, 256, "e128x128"},
                                      {128, 256, 512, "e128x256"}, {128, 192, 256, "e128x192"},
-                                     {256, 384, 512, "e256x384"}};
+                                     {256, 384, 512, "e256x384"}, {256, 288, 768, "e256x288"}};
     if (const char *e = std::getenv("POPCORN_GEMM_TILE")) {  // tuning override, e.g. "t256x128"
         for (const GemmTile &t : tiles)
             if (std::string(t.suffix) == e && (t.suffix[0] != 'd' || k % 32 == 0) && (t.suffix[0] != 'e' || gemmLinesFit(k, t.bn)))
@@ -741,7 +776,17 @@ int64_t gemmSplitK(int64_t m, int64_t n, int64_t k) {
     const int64_t t384 = cdiv(m, 256) * cdiv(n, 384);
     if (t384 * 10 >= cus * 7) return 0;
     for (int64_t s = 2; s <= 8; ++s)
-        if ((t384 * s) % cus == 0 && k % (32 * s) == 0 && k / s >= 2048) return s;
+        if ((t384 * s) % cus == 0 && k % (32 * s) == 0 && k / s >= 2048) {
+            // with whole-line tiles, split only when it beats the best tile's
+            // score: the split grid fills the CUs, less the share of time its
+            // partials' round trip through HBM adds (8 s bytes per element
+            // at ~7 TB/s against 2 K flop at ~1.2 PFLOP/s: ~700 s / K)
+            if (gemmLinesFit(k, 384)) {
+                const ScoredTile &t = bestLineTile(m, n);
+                if (1.0 - 700.0 * (double)s / (double)k <= lineTileScore(t, m, n)) return 0;
+            }
+            return s;
+        }
     return 0;
 }
 

@@ -113,7 +113,8 @@ def test_prefill_gemm_tile_plan():
     def mm(M, K, N, dtype="f16", out=None):
         return pa.Kernels.Matmul(T([M, K], dtype), T([N, K], dtype), T([M, N], out or dtype), True).function_names
     # K % 64 == 0: the whole-line ("e") forms; K % 64 == 32: the 64-byte-row ("d") ones
-    assert mm(2048, 3072, 9216) == ["matmul_mfma_f16_f16_f16_e256x384"]    # QKV: 192 tiles, 75% fill
+    # whole-line tiles by score (grid fill x inside share x tile throughput)
+    assert mm(2048, 3072, 9216) == ["matmul_mfma_f16_f16_f16_e256x288"]    # QKV: 256 tiles of 256 x 288
     assert mm(2048, 3072, 24576) == ["matmul_mfma_f16_f16_f16_e256x384"]   # gate / up: 512 tiles
     assert mm(2048, 3104, 24576) == ["matmul_mfma_f16_f16_f16_d256x384"]   # K % 64 == 32
     assert mm(2048, 24576, 3072) == ["matmul_mfma_f16_splitk_e256x384", "matmul_splitk_reduce_f16"]  # down: 64 x 4
@@ -121,11 +122,13 @@ def test_prefill_gemm_tile_plan():
                                                     "matmul_splitk_reduce_f32"]  # 32 tiles x 8 splits
     assert mm(2000, 16640, 1500, "bf16", "f32") == ["matmul_mfma_bf16_splitk_d256x384",
                                                     "matmul_splitk_reduce_f32"]  # splits of 2080: K % 64 == 32
-    assert mm(2048, 4096, 3072) == ["matmul_mfma_f16_f16_f16_e128x192"]    # splits would be under 2048 deep
+    assert mm(2048, 4096, 3072) == ["matmul_mfma_f16_f16_f16_e128x128"]    # splits would be under 2048 deep
+    assert mm(4096, 4096, 3072) == ["matmul_mfma_f16_f16_f16_e128x192"]    # 2 splits of 2048: partials cost more than the tiles lose
+    assert mm(4096, 24576, 3072) == ["matmul_mfma_f16_splitk_e256x384", "matmul_splitk_reduce_f16"]  # 128 tiles x 2
     # the split-K reduction stores 4 results at a time: a C not 16-byte aligned keeps one pass
     c_off = pa.Kernels.Matmul(T([2048, 24576], "f16"), T([3072, 24576], "f16"), T([2048, 3072], "f16", FAKE + 8),
                               True).function_names
-    assert c_off == ["matmul_mfma_f16_f16_f16_e128x192"]
+    assert c_off == ["matmul_mfma_f16_f16_f16_e128x128"]
     assert mm(256, 1024, 384) == ["matmul_mfma_f16_f16_f16_e128x128"]
     assert mm(256, 1056, 384) == ["matmul_mfma_f16_f16_f16_d128x128"]
     # 2 <= M <= 64: the skinny kernel, M padded to 16 per MFMA tile

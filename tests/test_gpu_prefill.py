@@ -112,7 +112,7 @@ def test_mfma_matmul_integer_exact(env, at):
     np.testing.assert_array_equal(got, (a.astype(np.int64) @ b.T.astype(np.int64)).astype(np.float32))
 
 
-TILES = [f"{f}{t}" for f in "ed" for t in ("256x384", "256x256", "128x128", "128x256", "128x192")]
+TILES = [f"{f}{t}" for f in "ed" for t in ("256x384", "256x256", "128x128", "128x256", "128x192")] + ["e256x288"]
 
 
 @pytest.mark.parametrize("tile", TILES)
