@@ -31,11 +31,28 @@ constexpr int LDK = BK + 8;  // padded LDS row, in elements
 constexpr int kXcds = 8;
 constexpr int kGroupM = 8;
 
+__device__ inline void group_tile(uint32_t pid, uint32_t nM, uint32_t nN, uint32_t &pm, uint32_t &pn);
 // Tile (pm, pn) of block b: XCD-contiguous ranges, grouped rows within.
 __device__ inline void tile_of(uint32_t b, uint32_t nM, uint32_t nN, uint32_t &pm, uint32_t &pn) {
     const uint32_t total = nM * nN;
     uint32_t pid = b;
     if (total % kXcds == 0) pid = (b % kXcds) * (total / kXcds) + b / kXcds;
+    group_tile(pid, nM, nN, pm, pn);
+}
+// Split-K grids (tiles x splits): the XCD-contiguous ranges run over the
+// (split, tile) units, so an XCD's blocks share one split's K range and a
+// band of tiles, whose A and B panels stay in that XCD's L2 (config-5
+// down: 327 -> 314 us against ranges over the tiles alone, where every
+// XCD read all of A).
+__device__ inline void split_tile_of(uint32_t nM, uint32_t nN, uint32_t &pm, uint32_t &pn, uint32_t &split) {
+    const uint32_t tiles = nM * nN, units = tiles * gridDim.y;
+    const uint32_t b = blockIdx.x + blockIdx.y * gridDim.x;
+    const uint32_t u = units % kXcds == 0 ? (b % kXcds) * (units / kXcds) + b / kXcds : b;
+    split = u / tiles;
+    group_tile(u % tiles, nM, nN, pm, pn);
+}
+// Tile pid of an XCD's range: groups of kGroupM tile rows, rows fastest.
+__device__ inline void group_tile(uint32_t pid, uint32_t nM, uint32_t nN, uint32_t &pm, uint32_t &pn) {
     const uint32_t inGroup = kGroupM * nN;
     const uint32_t group = pid / inGroup;
     const uint32_t firstM = group * kGroupM;
@@ -181,7 +198,8 @@ __device__ inline void wait_vmcnt() {
 }
 
 // SPLITK: gridDim.y blocks share a tile, each over K / gridDim.y of the
-// reduction, and write f32 partial products to P [gridDim.y][M][N] for
+// reduction (which split a block takes comes from split_tile_of), and
+// write f32 partial products to P [gridDim.y][M][N] for
 // gemm_splitk_reduce (C is then unused).
 template <typename T, typename O, int BM, int BN, int WM_N, int WN_N, bool SPLITK = false>
 __device__ void gemm_nt_direct(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
@@ -199,15 +217,16 @@ __device__ void gemm_nt_direct(const uint16_t *__restrict__ A, const uint16_t *_
 
     const uint32_t M = p.M, N = p.N, K = p.K;
     const uint32_t nM = (M + BM - 1) / BM, nN = (N + BN - 1) / BN;
-    uint32_t pm, pn;
-    tile_of(blockIdx.x, nM, nN, pm, pn);
+    uint32_t pm, pn, split = 0;
+    if constexpr (SPLITK) split_tile_of(nM, nN, pm, pn, split);
+    else tile_of(blockIdx.x, nM, nN, pm, pn);
     const uint32_t bm = pm * BM, bn = pn * BN;
     const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t wm = (wave / WN_N) * WM, wn = (wave % WN_N) * WN;
 
     // this lane's source rows / chunk for each of its wave's instructions
     const uint32_t lr = lane >> 2, lpos = lane & 3;
-    const uint32_t kBase = SPLITK ? blockIdx.y * (K / gridDim.y) : 0u;
+    const uint32_t kBase = SPLITK ? split * (K / gridDim.y) : 0u;
     auto issue = [&](uint32_t kt) {
         const uint32_t k0 = kBase + kt * BKD;
         uint8_t *stage = smem + (kt % kStagesD) * kStageB;
@@ -338,7 +357,7 @@ __device__ void gemm_nt_direct(const uint16_t *__restrict__ A, const uint16_t *_
                 const uint32_t row = bm + wm + mi * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
                 if (row < M && col < N) {
                     if constexpr (SPLITK)
-                        P[((uint64_t)blockIdx.y * M + row) * N + col] = acc[mi][ni][i];
+                        P[((uint64_t)split * M + row) * N + col] = acc[mi][ni][i];
                     else
                         C[(uint64_t)row * N + col] = O::store(acc[mi][ni][i]);
                 }
@@ -376,8 +395,9 @@ __device__ void gemm_nt_lines(const uint16_t *__restrict__ A, const uint16_t *__
 
     const uint32_t M = p.M, N = p.N, K = p.K;
     const uint32_t nM = (M + BM - 1) / BM, nN = (N + BN - 1) / BN;
-    uint32_t pm, pn;
-    tile_of(blockIdx.x, nM, nN, pm, pn);
+    uint32_t pm, pn, split = 0;
+    if constexpr (SPLITK) split_tile_of(nM, nN, pm, pn, split);
+    else tile_of(blockIdx.x, nM, nN, pm, pn);
     const uint32_t bm = pm * BM, bn = pn * BN;
     const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t wm = (wave / WN_N) * WM, wn = (wave % WN_N) * WN;
@@ -389,7 +409,7 @@ __device__ void gemm_nt_lines(const uint16_t *__restrict__ A, const uint16_t *__
     // offset go in the scalar offset.
     static_assert(NW % 2 == 0, "one chunk swizzle per lane for every instruction");
     const uint32_t lr = lane >> 3, lpos = lane & 7;
-    const uint32_t kBase = SPLITK ? blockIdx.y * (K / gridDim.y) : 0u;
+    const uint32_t kBase = SPLITK ? split * (K / gridDim.y) : 0u;
     const uint64_t rowB = (uint64_t)K * 2u;
     const uint32_t bytesA = (uint32_t)min((uint64_t)(M - bm) * rowB, (uint64_t)0xffffffffu);
     const uint32_t bytesB = (uint32_t)min((uint64_t)(N - bn) * rowB, (uint64_t)0xffffffffu);
@@ -505,7 +525,7 @@ __device__ void gemm_nt_lines(const uint16_t *__restrict__ A, const uint16_t *__
                 const uint32_t row = bm + wm + mi * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
                 if (row < M && col < N) {
                     if constexpr (SPLITK)
-                        P[((uint64_t)blockIdx.y * M + row) * N + col] = acc[mi][ni][i];
+                        P[((uint64_t)split * M + row) * N + col] = acc[mi][ni][i];
                     else
                         C[(uint64_t)row * N + col] = O::store(acc[mi][ni][i]);
                 }
