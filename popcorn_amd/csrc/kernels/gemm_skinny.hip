@@ -11,7 +11,10 @@
 // tiles) the B operand, so both are 16-byte runs along K of one row and a
 // lane's fragment is one 16-byte load: lane l reads row l % 16 at
 // k0 + (l / 16) * 8. A block takes 32 rows of B (two 16-row tiles, so each
-// A fragment serves two products); its W waves split K, each wave a
+// A fragment serves two products), or 16 rows in the _r16 kernels, which
+// the host picks when 32-row blocks would be fewer than the CUs (N < 8192:
+// M 8, K 9216, N 2304 23.7 -> 15.8 us; M 32, K 2304, N 4096 12.5 -> 9.1
+// us); its W waves split K, each wave a
 // contiguous run of k-steps of 32 with U steps in flight, and sum their
 // partial C^T tiles in LDS at the end. A (M x K, a few tens of KB) is read
 // from L2 beside B. Rows past N or M read a valid row and are not stored;
@@ -27,12 +30,11 @@ using pk::f32x4;
 using pk::Mma16;
 using pk::u32x4;
 
-constexpr int NT = 2;                 // 16-row tiles of B per block
 constexpr int U = 4;                  // k-steps in flight per wave
 constexpr int kMaxWaves = 8;          // waves per block (K split)
 constexpr int kRedFloats = 16384;     // LDS for the partial tiles: W x NT x MT x 256 floats
 
-template <typename T, typename O, int MT>
+template <typename T, typename O, int MT, int NT>  // NT: 16-row tiles of B per block
 __device__ void gemm_skinny(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
                             typename O::storage *__restrict__ C, const MatmulConstants &p) {
     static_assert(kMaxWaves * NT * MT * 256 <= kRedFloats, "LDS for the partial tiles");
@@ -136,16 +138,20 @@ __device__ void gemm_skinny(const uint16_t *__restrict__ A, const uint16_t *__re
 
 }  // namespace
 
-#define GEMM_SKINNY(name, T, O, MT)                                                                       \
+#define GEMM_SKINNY(name, T, O, MT, NT)                                                                   \
     POPCORN_KERNEL void __launch_bounds__(64 * kMaxWaves)                                                 \
         name(const uint16_t *a, const uint16_t *b, O::storage *c, MatmulConstants p) {                    \
-        gemm_skinny<T, O, MT>(a, b, c, p);                                                                \
+        gemm_skinny<T, O, MT, NT>(a, b, c, p);                                                            \
     }
-#define GEMM_SKINNY_M(t, T, o, O)                                \
-    GEMM_SKINNY(matmul_skinny_##t##_##t##_##o##_m16, T, O, 1)    \
-    GEMM_SKINNY(matmul_skinny_##t##_##t##_##o##_m32, T, O, 2)    \
-    GEMM_SKINNY(matmul_skinny_##t##_##t##_##o##_m48, T, O, 3)    \
-    GEMM_SKINNY(matmul_skinny_##t##_##t##_##o##_m64, T, O, 4)
+#define GEMM_SKINNY_M(t, T, o, O)                                        \
+    GEMM_SKINNY(matmul_skinny_##t##_##t##_##o##_m16, T, O, 1, 2)         \
+    GEMM_SKINNY(matmul_skinny_##t##_##t##_##o##_m32, T, O, 2, 2)         \
+    GEMM_SKINNY(matmul_skinny_##t##_##t##_##o##_m48, T, O, 3, 2)         \
+    GEMM_SKINNY(matmul_skinny_##t##_##t##_##o##_m64, T, O, 4, 2)         \
+    GEMM_SKINNY(matmul_skinny_##t##_##t##_##o##_m16_r16, T, O, 1, 1)     \
+    GEMM_SKINNY(matmul_skinny_##t##_##t##_##o##_m32_r16, T, O, 2, 1)     \
+    GEMM_SKINNY(matmul_skinny_##t##_##t##_##o##_m48_r16, T, O, 3, 1)     \
+    GEMM_SKINNY(matmul_skinny_##t##_##t##_##o##_m64_r16, T, O, 4, 1)
 
 using pk::BF16;
 using pk::F16;

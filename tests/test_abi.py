@@ -132,7 +132,10 @@ def test_prefill_gemm_tile_plan():
     assert mm(256, 1024, 384) == ["matmul_mfma_f16_f16_f16_e128x128"]
     assert mm(256, 1056, 384) == ["matmul_mfma_f16_f16_f16_d128x128"]
     # 2 <= M <= 64: the skinny kernel, M padded to 16 per MFMA tile
-    assert mm(2, 64, 67) == ["matmul_skinny_f16_f16_f16_m16"]
+    assert mm(2, 64, 67) == ["matmul_skinny_f16_f16_f16_m16_r16"]           # 16-row blocks below 256 x 32 rows
+    assert mm(8, 9216, 2304, "bf16") == ["matmul_skinny_bf16_bf16_bf16_m16_r16"]
+    assert mm(32, 2304, 8160) == ["matmul_skinny_f16_f16_f16_m32_r16"]
+    assert mm(32, 2304, 8192) == ["matmul_skinny_f16_f16_f16_m32"]
     assert mm(8, 2304, 9216, "bf16") == ["matmul_skinny_bf16_bf16_bf16_m16"]
     assert mm(17, 2304, 9216, "bf16", "f32") == ["matmul_skinny_bf16_bf16_f32_m32"]
     assert mm(48, 2304, 9216) == ["matmul_skinny_f16_f16_f16_m48"]
