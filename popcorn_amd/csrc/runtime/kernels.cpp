@@ -904,13 +904,22 @@ std::unique_ptr<Kernel> makeMatmul(const Tensor &a, const Tensor &b, const Tenso
             // MI355X for N 2304..24576 x K 2304..9216)
             if (m <= 64 && !std::getenv("POPCORN_GEMM_TILE") && n * k * 2 <= INT32_MAX && m * k * 2 <= INT32_MAX) {
                 const int mt = (int)cdiv(m, 16);
+                MatmulConstants mc{(uint32_t)m, (uint32_t)k, (uint32_t)n, 1u};
+                // at least 512 tiles of 16 rows of B: A staged in LDS, one
+                // tile per wave (one wave per block at M <= 16, else four)
+                if (cdiv(n, 16) >= 2 * (int64_t)deviceCUs()) {
+                    const int w = mt == 1 ? 1 : 4;
+                    const std::string fn = std::string("matmul_skinny_") + tag(t) + "_" + tag(t) + "_" + tag(c.dataType) +
+                                           "_m" + std::to_string(16 * mt) + "_lds";
+                    return std::make_unique<FixedDispatch>(fn, binds, std::vector<std::vector<uint8_t>>{bytesOf(mc)},
+                                                           grid1(cdiv(cdiv(n, 16), w), 64 * w));
+                }
                 // 16-row blocks (_r16) when 32-row ones would be fewer than the CUs
                 const int rows = cdiv(n, 32) < deviceCUs() ? 16 : 32;
                 const int64_t blocks = cdiv(n, rows);
                 const int64_t want = 3 * (int64_t)deviceCUs() / blocks;
                 int64_t w = 1;
                 while (2 * w <= want && w < 4 && 2 * w <= cdiv(k, 32)) w *= 2;
-                MatmulConstants mc{(uint32_t)m, (uint32_t)k, (uint32_t)n, 1u};
                 const std::string fn = std::string("matmul_skinny_") + tag(t) + "_" + tag(t) + "_" + tag(c.dataType) +
                                        "_m" + std::to_string(16 * mt) + (rows == 16 ? "_r16" : "");
                 return std::make_unique<FixedDispatch>(fn, binds, std::vector<std::vector<uint8_t>>{bytesOf(mc)},

@@ -134,12 +134,14 @@ def test_prefill_gemm_tile_plan():
     # 2 <= M <= 64: the skinny kernel, M padded to 16 per MFMA tile
     assert mm(2, 64, 67) == ["matmul_skinny_f16_f16_f16_m16_r16"]           # 16-row blocks below 256 x 32 rows
     assert mm(8, 9216, 2304, "bf16") == ["matmul_skinny_bf16_bf16_bf16_m16_r16"]
-    assert mm(32, 2304, 8160) == ["matmul_skinny_f16_f16_f16_m32_r16"]
-    assert mm(32, 2304, 8192) == ["matmul_skinny_f16_f16_f16_m32"]
-    assert mm(8, 2304, 9216, "bf16") == ["matmul_skinny_bf16_bf16_bf16_m16"]
-    assert mm(17, 2304, 9216, "bf16", "f32") == ["matmul_skinny_bf16_bf16_f32_m32"]
-    assert mm(48, 2304, 9216) == ["matmul_skinny_f16_f16_f16_m48"]
-    assert mm(64, 3072, 24576) == ["matmul_skinny_f16_f16_f16_m64"]
+    assert mm(32, 2304, 8160) == ["matmul_skinny_f16_f16_f16_m32_r16"]     # 255 blocks of 32 rows
+    assert mm(32, 2304, 8176) == ["matmul_skinny_f16_f16_f16_m32"]         # 256 of 32, 511 tiles of 16
+    assert mm(32, 2304, 8192) == ["matmul_skinny_f16_f16_f16_m32_lds"]     # 512 tiles of 16
+    # at least 512 tiles of 16 rows of B: A staged in LDS
+    assert mm(8, 2304, 9216, "bf16") == ["matmul_skinny_bf16_bf16_bf16_m16_lds"]
+    assert mm(17, 2304, 9216, "bf16", "f32") == ["matmul_skinny_bf16_bf16_f32_m32_lds"]
+    assert mm(48, 2304, 9216) == ["matmul_skinny_f16_f16_f16_m48_lds"]
+    assert mm(64, 3072, 24576) == ["matmul_skinny_f16_f16_f16_m64_lds"]
     assert mm(65, 2048, 2048) == ["matmul_mfma_f16_f16_f16_e128x128"]
     assert mm(8, 2300, 9216)[0].startswith("matmul_tiled")  # K % 8 != 0: the SIMT tiles
 
@@ -201,7 +203,7 @@ def test_matmul_routing_and_validation():
     assert pa.Kernels.Matmul(T([2048, 3072]), T([3072, 3072]), T([2048, 3072]), False).describe().startswith(
         "transpose2d_b16,matmul_mfma_bf16_bf16_bf16_")
     assert pa.Kernels.Matmul(T([8, 2304]), T([2304, 9216]), T([8, 9216], "f32"), False).describe() == \
-        "transpose2d_b16,matmul_skinny_bf16_bf16_f32_m16"
+        "transpose2d_b16,matmul_skinny_bf16_bf16_f32_m16_lds"
     assert pa.Kernels.Matmul(T([8, 2300]), T([2300, 64]), T([8, 64]), False).describe() == "matmul_tiled_bf16_bf16_bf16"
     with pytest.raises(pa.PopcornError) as e:  # Matmul.swift:85-87
         pa.Kernels.Matmul(x, T([9216, 2300]), T([1, 9216]), True)

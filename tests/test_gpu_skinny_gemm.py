@@ -35,15 +35,17 @@ def _gemm(env, a, b, at, ot, guard=0):
 
 
 def _name(at, ot, M, N):
-    # 16-row blocks (_r16) when 32-row blocks would be fewer than the CUs
-    # (MI355X: 256)
-    return f"matmul_skinny_{at}_{at}_{ot}_m{16 * (-(-M // 16))}" + ("_r16" if -(-N // 32) < 256 else "")
+    # A staged in LDS at >= 512 tiles of 16 rows of B; else 16-row blocks
+    # (_r16) when 32-row blocks would be fewer than the CUs (MI355X: 256)
+    suffix = "_lds" if -(-N // 16) >= 512 else ("_r16" if -(-N // 32) < 256 else "")
+    return f"matmul_skinny_{at}_{at}_{ot}_m{16 * (-(-M // 16))}" + suffix
 
 
 @pytest.mark.parametrize("at,ot", [("f16", "f16"), ("f16", "f32"), ("bf16", "bf16"), ("bf16", "f32")])
 @pytest.mark.parametrize("M,K,N", [(2, 64, 67), (8, 2304, 9216), (8, 2304, 2304), (16, 136, 300), (17, 520, 129),
                                    (33, 256, 1000), (48, 2048, 64), (64, 3072, 512), (5, 8, 33), (63, 40, 31),
-                                   (8, 9216, 2304), (32, 2304, 4096), (40, 1032, 8200)])
+                                   (8, 9216, 2304), (32, 2304, 4096), (40, 1032, 8200), (2, 8, 8200),
+                                   (48, 1000, 8195), (64, 520, 9000), (16, 4104, 8192), (8, 2304, 8176)])
 def test_skinny_matmul_vs_oracle(env, at, ot, M, K, N):
     a = rounded(O.normal(M * 7 + K, (M, K)), at)
     b = rounded(O.normal(N * 3 + K, (N, K), std=0.02), at)
@@ -64,7 +66,7 @@ def test_skinny_matmul_vs_oracle(env, at, ot, M, K, N):
 
 @pytest.mark.parametrize("at", ["f16", "bf16"])
 @pytest.mark.parametrize("M,K,N", [(3, 320, 160), (16, 1000, 64), (40, 96, 250), (64, 4104, 96), (16, 520, 9000),
-                                   (61, 264, 8230)])
+                                   (61, 264, 8230), (33, 1000, 8195), (2, 264, 16384), (64, 2056, 8192), (8, 8, 8200)])
 def test_skinny_matmul_integer_exact(env, at, M, K, N):
     # small integers: every product and partial sum is exact in f32, so the
     # result is exact whatever the order (K-split over waves, LDS sum): pins
