@@ -8,8 +8,11 @@
 // AffineQuantizedMatmul.metal:75-82). The nibbles enter the products as the
 // bf16 values 128 + q (0x4300 | q, exact), so a group's product D on
 // v_mfma_f32_32x32x16_bf16 (exact bf16 products, f32 sums) is
-// sum x (128 + q) and the element gains s * D + (b - 128 s) * X_g: two FMAs
-// per element and group, with no rounding of the weights to bf16.
+// sum x (128 + q) and the element gains s * D + (b - 128 s) * X_g, with no
+// rounding of the weights to bf16: s * D is one FMA per element and group;
+// the (b - 128 s) * X_g terms, an outer product per group, go on
+// v_mfma_f32_32x32x2_f32 two groups at a time (the per-element FMAs for
+// them made the kernel bound by its vector ALU work).
 //
 // aq_gemm_prep writes, per row of X and group, X_g (f32) and a copy of the
 // row with each run of 8 values in the order (0, 4, 1, 5, 2, 6, 3, 7): a
@@ -135,8 +138,12 @@ __device__ void aq_gemm(const uint32_t *__restrict__ Wp, const uint16_t *__restr
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[mi][ni][i] = 0.0f;
 
-    auto compute = [&](int st) {
-        // group product per tile, then the affine terms of the group
+    // j: the group's index in this block's range; the bias terms of groups
+    // j - 1 and j go in one product at odd j, a last even j's alone
+    float px[2] = {0.0f, 0.0f}, pb[2] = {0.0f, 0.0f};  // group j - 1's X_g and b - 128 s
+    auto compute = [&](int st, uint32_t j, bool last) {
+        // group product per tile, then its scale; the bias terms on the
+        // matrix cores
         const uint32_t r = lane & 31, h = lane >> 5;
         f32x16 d[2][2];
 #pragma unroll
@@ -161,21 +168,43 @@ __device__ void aq_gemm(const uint32_t *__restrict__ Wp, const uint16_t *__restr
         }
 #pragma unroll
         for (int ni = 0; ni < 2; ++ni) {
-            const float2 sc = sSC[st][wn + ni * 32 + r];
+            const float sc = sSC[st][wn + ni * 32 + r].x;
 #pragma unroll
-            for (int mi = 0; mi < 2; ++mi) {
+            for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    // C rows q * 8 + h * 4 + 0..3 of the tile
-                    const float4 xs = *reinterpret_cast<const float4 *>(&sXs[st][wm + mi * 32 + q * 8 + h * 4]);
-                    const float xv[4] = {xs.x, xs.y, xs.z, xs.w};
+                for (int i = 0; i < 16; ++i) acc[mi][ni][i] = fmaf(sc, d[mi][ni][i], acc[mi][ni][i]);
+        }
+        // acc += X_g (rows) x (b - 128 s)_g (columns) for two groups at a
+        // time on v_mfma_f32_32x32x2_f32 (A lane l: row l % 32, k l / 32; B
+        // lane l: k l / 32, column l % 32; C in the layout of acc): k 0 is
+        // group j - 1, whose terms this lane kept in registers at even j
+        // (the other LDS buffer may already hold group j + 1), k 1 group j;
+        // an unpaired last group takes k 0 with k 1 zero
+        float cx[2], cb[2];
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int i = q * 4 + e;
-                        acc[mi][ni][i] = fmaf(sc.x, d[mi][ni][i], fmaf(sc.y, xv[e], acc[mi][ni][i]));
-                    }
-                }
+        for (int mi = 0; mi < 2; ++mi) cx[mi] = sXs[st][wm + mi * 32 + r];
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni) cb[ni] = sSC[st][wn + ni * 32 + r].y;
+        if (!(j & 1)) {
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                px[e] = cx[e];
+                pb[e] = cb[e];
             }
+        }
+        if ((j & 1) || last) {
+            const bool pair = (j & 1) != 0;
+            float xa[2], bb[2];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                xa[e] = pair ? (h ? cx[e] : px[e]) : (h ? 0.0f : cx[e]);
+                bb[e] = pair ? (h ? cb[e] : pb[e]) : (h ? 0.0f : cb[e]);
+            }
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < 2; ++ni)
+                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[mi], bb[ni], acc[mi][ni], 0, 0, 0);
         }
     };
 
@@ -190,7 +219,7 @@ __device__ void aq_gemm(const uint32_t *__restrict__ Wp, const uint16_t *__restr
     for (uint32_t g = g0; g < g1; ++g) {
         const int st = (int)((g - g0) & 1);
         if (g + 1 < g1) gload(g + 1);
-        compute(st);
+        compute(st, g - g0, g + 1 == g1);
         if (g + 1 < g1) lstore(st ^ 1);
         __syncthreads();
     }
