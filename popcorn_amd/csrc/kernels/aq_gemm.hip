@@ -22,14 +22,13 @@
 // free).
 //
 // aq_gemm: a block of 4 waves takes a 128 x 128 tile of C, each wave 64 x 64
-// (2 x 2 MFMA tiles); per group the block stages the X' tile (128 x 64 bf16),
-// the unpacked weights (128 x 64 bf16), the columns' (s, b - 128 s) and the
-// rows' X_g in LDS, double-buffered with the next group's loads in
-// registers. Rows past M and columns past N read row M - 1 / N - 1 and are
-// not stored. A block walks its groups one after another, so with few tiles
-// the groups are split over gridDim.y blocks per tile (SPLIT): each writes
-// its f32 partial tile to P [gridDim.y][M][N] and matmul_splitk_reduce_*
-// sums them and rounds once.
+// (2 x 2 MFMA tiles); per group the block copies the X' tile (128 x 64
+// bf16), the packed words, the columns' scale and bias words and the rows'
+// X_g into LDS, three groups in flight (below). Rows past M and columns
+// past N read zeros and are not stored. A block walks its groups one after
+// another, so with few tiles the groups are split over gridDim.y blocks per
+// tile (SPLIT): each writes its f32 partial tile to P [gridDim.y][M][N] and
+// matmul_splitk_reduce_* sums them and rounds once.
 #include "mfma.hpp"
 
 namespace {
@@ -39,8 +38,10 @@ using pk::u32x4;
 
 constexpr int BM = 128, BN = 128;
 constexpr int kGroup = 64;
-constexpr int LDT = kGroup + 8;  // LDS row pitch (bf16): 144 bytes, so 16 rows fall in 16 distinct 4-bank groups
 constexpr uint32_t kPairBase = 0x43004300u;
+
+// The bf16 of group g in the 32-bit word that holds groups g & ~1 and g | 1.
+__device__ inline float bf16_half(uint32_t v, uint32_t g) { return __uint_as_float((g & 1u) ? (v & 0xffff0000u) : (v << 16)); }
 
 // One thread per (row, group): X_g, and the row's 64 values in pair order.
 __device__ void aq_gemm_prep(const uint16_t *__restrict__ X, uint16_t *__restrict__ Xp, float *__restrict__ Xs,
@@ -68,66 +69,83 @@ __device__ void aq_gemm_prep(const uint16_t *__restrict__ X, uint16_t *__restric
     Xs[t] = sum;
 }
 
+// One stage per group, NS stages in flight, every tile copied buffer -> LDS
+// directly (no staging registers), one barrier per group:
+//  * x': 128 rows x 128 bytes, chunk c of row r in slot c ^ ((r >> 1) & 7)
+//    (whole 128-byte lines per copy; a fragment read's 16 rows per
+//    quarter-wave cover all banks);
+//  * the packed words: 128 columns x 32 bytes, 16-byte half h of column n
+//    in slot h ^ ((n >> 3) & 1), unpacked to bf16 pairs as the fragments
+//    are read;
+//  * the 32-bit words of the scales and biases that hold the group (and
+//    its even/odd neighbour), and the rows' X_g.
+// Wave w's copies per stage: x' instructions w, w + 4, w + 8, w + 12, the
+// words' instruction w, one of the scale/bias words, and one of X_g (waves
+// 2 and 3 copy the X_g of waves 0 and 1 again, identical bytes), so every
+// wave issues kCopies per stage and the waits count them exactly. In a
+// group's products lane half h takes chunk 4 h + kk of the group in step
+// kk, in x' and in the words alike.
+constexpr int NS = 3;                       // stages in flight
+constexpr int kXB = BM * 128;               // x' bytes per stage
+constexpr int kWB = BN * 32;                // packed-word bytes per stage
+constexpr int kStageB = kXB + kWB + 3 * 512;  // + scale words, bias words, X_g
+constexpr int kCopies = 7;
+constexpr uint32_t kOOR = 0x80000000u;      // a buffer offset past every operand: zeros, no memory read
+typedef __attribute__((address_space(3))) void lds_void;
+
+template <int N>
+__device__ inline void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 template <typename O, bool SPLIT>
 __device__ void aq_gemm(const uint32_t *__restrict__ Wp, const uint16_t *__restrict__ S, const uint16_t *__restrict__ Bi,
                         const uint16_t *__restrict__ Xp, const float *__restrict__ Xs, typename O::storage *__restrict__ C,
                         float *__restrict__ P, const AffineQMatmulConstants &p) {
-    __shared__ __attribute__((aligned(16))) uint16_t sX[2][BM * LDT];
-    __shared__ __attribute__((aligned(16))) uint16_t sW[2][BN * LDT];
-    __shared__ __attribute__((aligned(16))) float2 sSC[2][BN];  // (s, b - 128 s) per column
-    __shared__ __attribute__((aligned(16))) float sXs[2][BM];   // X_g per row
+    __shared__ __attribute__((aligned(16))) uint8_t smem[NS * kStageB];
 
     const uint32_t M = p.M, N = p.N, K = p.K, G = p.kGroups, WPR = p.wordsPerRow;
     const uint32_t nM = (M + BM - 1) / BM;
     const uint32_t pm = blockIdx.x % nM, pn = blockIdx.x / nM;  // blocks sharing weights run together
     const uint32_t bm = pm * BM, bn = pn * BN;
-    const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const uint32_t r = lane & 31, h = lane >> 5;
 
-    // this thread's staging: 4 16-byte runs of X' (row c / 8, run c % 8 for
-    // c = t + 256 j), 4 packed words (row t / 2, words 4 (t % 2) ..), and
-    // for t < 128 the column's scale and bias and the row's X_g
-    const uint32_t wrow = t >> 1, wh = t & 1;
-    const uint64_t wbase = (uint64_t)min(bn + wrow, N - 1) * WPR + 4 * wh;
-    const uint32_t srow = min(bn + (t & 127), N - 1), xrow = min(bm + (t & 127), M - 1);
-    u32x4 xr[4], wr;
-    uint32_t sr = 0, br = 0;
-    float xsr = 0.0f;
-    auto gload = [&](uint32_t g) {
+    // buffer resources over whole operands (the host keeps each under 2^31 bytes)
+    const __amdgpu_buffer_rsrc_t rsX = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(Xp), 0, (int)(M * K * 2u), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsW = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t *>(Wp), 0, (int)(N * WPR * 4u), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsS = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(S), 0, (int)(N * G * 2u), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsB = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(Bi), 0, (int)(N * G * 2u), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsG = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(Xs), 0, (int)(M * G * 4u), 0x00020000);
+
+    auto stageOf = [&](uint32_t j) { return smem + (j % NS) * kStageB; };
+    auto issue = [&](uint32_t g, uint8_t *stage) {
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t c = t + 256 * j, row = c >> 3, run = c & 7;
-            xr[j] = *reinterpret_cast<const u32x4 *>(Xp + (uint64_t)min(bm + row, M - 1) * K + g * kGroup + run * 8);
+        for (int t = 0; t < 4; ++t) {  // x': rows 8 i .. 8 i + 7
+            const uint32_t i = 4 * t + wave, row = 8 * i + (lane >> 3), c = (lane & 7) ^ ((row >> 1) & 7);
+            const uint32_t off = bm + row < M ? ((bm + row) * K + g * kGroup + 8 * c) * 2u : kOOR;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsX, (lds_void *)(stage + i * 1024), 16, off, 0, 0, 0);
         }
-        wr = *reinterpret_cast<const u32x4 *>(Wp + wbase + g * 8);
-        if (t < 128) {
-            sr = S[(uint64_t)srow * G + g];
-            br = p.hasBias ? Bi[(uint64_t)srow * G + g] : 0u;
-            xsr = Xs[(uint64_t)xrow * G + g];
+        {  // words: columns 32 w .. 32 w + 31
+            const uint32_t col = 32 * wave + (lane >> 1), hh = (lane & 1) ^ ((col >> 3) & 1);
+            const uint32_t off = bn + col < N ? ((bn + col) * WPR + g * 8 + 4 * hh) * 4u : kOOR;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsW, (lds_void *)(stage + kXB + wave * 1024), 16, off, 0, 0, 0);
         }
-    };
-    auto lstore = [&](int st) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t c = t + 256 * j, row = c >> 3, run = c & 7;
-            *reinterpret_cast<u32x4 *>(&sX[st][row * LDT + run * 8]) = xr[j];
+        {  // scale words (waves 0, 1) or bias words (waves 2, 3) of columns 64 (w & 1) + l
+            const uint32_t col = 64 * (wave & 1) + lane;
+            const uint32_t off = bn + col < N ? ((bn + col) * G + (g & ~1u)) * 2u : kOOR;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(wave < 2 ? rsS : rsB, (lds_void *)(stage + kXB + kWB + (wave >> 1) * 512 + (wave & 1) * 256),
+                                                     4, off, 0, 0, 0);
         }
-        // word i holds values 8 i .. 8 i + 7 of this half-group; in pair order
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t w = wr[i];
-            u32x4 q;
-            q.x = (w & 0x000F000Fu) | kPairBase;
-            q.y = ((w >> 4) & 0x000F000Fu) | kPairBase;
-            q.z = ((w >> 8) & 0x000F000Fu) | kPairBase;
-            q.w = ((w >> 12) & 0x000F000Fu) | kPairBase;
-            *reinterpret_cast<u32x4 *>(&sW[st][wrow * LDT + wh * 32 + i * 8]) = q;
+        {  // X_g of rows 64 (w & 1) + l
+            const uint32_t row = 64 * (wave & 1) + lane;
+            const uint32_t off = bm + row < M ? ((bm + row) * G + g) * 4u : kOOR;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsG, (lds_void *)(stage + kXB + kWB + 1024 + (wave & 1) * 256), 4, off, 0, 0, 0);
         }
-        if (t < 128) {
-            const float s = __uint_as_float(sr << 16), b = __uint_as_float(br << 16);
-            sSC[st][t] = float2{s, b - 128.0f * s};
-            sXs[st][t] = xsr;
-        }
+        __builtin_amdgcn_sched_barrier(0);
     };
 
     f32x16 acc[2][2];
@@ -141,10 +159,18 @@ __device__ void aq_gemm(const uint32_t *__restrict__ Wp, const uint16_t *__restr
     // j: the group's index in this block's range; the bias terms of groups
     // j - 1 and j go in one product at odd j, a last even j's alone
     float px[2] = {0.0f, 0.0f}, pb[2] = {0.0f, 0.0f};  // group j - 1's X_g and b - 128 s
-    auto compute = [&](int st, uint32_t j, bool last) {
-        // group product per tile, then its scale; the bias terms on the
-        // matrix cores
-        const uint32_t r = lane & 31, h = lane >> 5;
+    auto compute = [&](const uint8_t *stage, uint32_t g, uint32_t j, bool last) {
+        const uint8_t *sX = stage, *sW = stage + kXB;
+        const uint32_t *sS = reinterpret_cast<const uint32_t *>(stage + kXB + kWB);
+        const uint32_t *sB = sS + 128;
+        const float *sG = reinterpret_cast<const float *>(stage + kXB + kWB + 1024);
+        // this lane's 4 packed words of each of its two columns: chunks 4 h .. 4 h + 3
+        u32x4 wr[2];
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni) {
+            const uint32_t col = wn + ni * 32 + r;
+            wr[ni] = *reinterpret_cast<const u32x4 *>(sW + col * 32 + ((h ^ ((col >> 3) & 1)) << 4));
+        }
         f32x16 d[2][2];
 #pragma unroll
         for (int mi = 0; mi < 2; ++mi)
@@ -156,35 +182,46 @@ __device__ void aq_gemm(const uint32_t *__restrict__ Wp, const uint16_t *__restr
         for (int kk = 0; kk < kGroup / 16; ++kk) {
             u32x4 a[2], b[2];
 #pragma unroll
-            for (int mi = 0; mi < 2; ++mi)
-                a[mi] = *reinterpret_cast<const u32x4 *>(&sX[st][(wm + mi * 32 + r) * LDT + kk * 16 + h * 8]);
+            for (int mi = 0; mi < 2; ++mi) {
+                const uint32_t row = wm + mi * 32 + r, c = 4 * h + kk;
+                a[mi] = *reinterpret_cast<const u32x4 *>(sX + row * 128 + ((c ^ ((row >> 1) & 7)) << 4));
+            }
 #pragma unroll
-            for (int ni = 0; ni < 2; ++ni)
-                b[ni] = *reinterpret_cast<const u32x4 *>(&sW[st][(wn + ni * 32 + r) * LDT + kk * 16 + h * 8]);
+            for (int ni = 0; ni < 2; ++ni) {
+                // a packed word gives its values in pair order as 4 bf16 pairs
+                const uint32_t w = wr[ni][kk];
+                b[ni].x = (w & 0x000F000Fu) | kPairBase;
+                b[ni].y = ((w >> 4) & 0x000F000Fu) | kPairBase;
+                b[ni].z = ((w >> 8) & 0x000F000Fu) | kPairBase;
+                b[ni].w = ((w >> 12) & 0x000F000Fu) | kPairBase;
+            }
 #pragma unroll
             for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
                 for (int ni = 0; ni < 2; ++ni) d[mi][ni] = pk::Mma<pk::BF16>::run(a[mi], b[ni], d[mi][ni]);
         }
+        float cs[2], cb[2], cx[2];
 #pragma unroll
         for (int ni = 0; ni < 2; ++ni) {
-            const float sc = sSC[st][wn + ni * 32 + r].x;
+            const uint32_t col = wn + ni * 32 + r;
+            cs[ni] = bf16_half(sS[col], g);
+            const float bias = p.hasBias ? bf16_half(sB[col], g) : 0.0f;
+            cb[ni] = bias - 128.0f * cs[ni];
+        }
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi) cx[mi] = sG[wm + mi * 32 + r];
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
 #pragma unroll
             for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-                for (int i = 0; i < 16; ++i) acc[mi][ni][i] = fmaf(sc, d[mi][ni][i], acc[mi][ni][i]);
-        }
+                for (int i = 0; i < 16; ++i) acc[mi][ni][i] = fmaf(cs[ni], d[mi][ni][i], acc[mi][ni][i]);
         // acc += X_g (rows) x (b - 128 s)_g (columns) for two groups at a
         // time on v_mfma_f32_32x32x2_f32 (A lane l: row l % 32, k l / 32; B
         // lane l: k l / 32, column l % 32; C in the layout of acc): k 0 is
         // group j - 1, whose terms this lane kept in registers at even j
-        // (the other LDS buffer may already hold group j + 1), k 1 group j;
-        // an unpaired last group takes k 0 with k 1 zero
-        float cx[2], cb[2];
-#pragma unroll
-        for (int mi = 0; mi < 2; ++mi) cx[mi] = sXs[st][wm + mi * 32 + r];
-#pragma unroll
-        for (int ni = 0; ni < 2; ++ni) cb[ni] = sSC[st][wn + ni * 32 + r].y;
+        // (its stage may already be refilled), k 1 group j; an unpaired
+        // last group takes k 0 with k 1 zero
         if (!(j & 1)) {
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
@@ -211,35 +248,37 @@ __device__ void aq_gemm(const uint32_t *__restrict__ Wp, const uint16_t *__restr
     // this block's groups: all, or split y of gridDim.y
     const uint32_t g0 = SPLIT ? (uint32_t)((uint64_t)G * blockIdx.y / gridDim.y) : 0u;
     const uint32_t g1 = SPLIT ? (uint32_t)((uint64_t)G * (blockIdx.y + 1) / gridDim.y) : G;
-    if (g0 < g1) {
-        gload(g0);
-        lstore(0);
-        __syncthreads();
-    }
-    for (uint32_t g = g0; g < g1; ++g) {
-        const int st = (int)((g - g0) & 1);
-        if (g + 1 < g1) gload(g + 1);
-        compute(st, g - g0, g + 1 == g1);
-        if (g + 1 < g1) lstore(st ^ 1);
-        __syncthreads();
+    const uint32_t n = g1 > g0 ? g1 - g0 : 0u;
+    // Group j: wait for this wave's copies of stage j (those of stage j + 1,
+    // if issued, may stay in flight), barrier (every wave's copies of stage j
+    // have landed, and every wave is done with stage j - 1), refill stage
+    // j - 1's buffer with group j + NS - 1, then the products.
+    static_assert(NS == 3, "the waits below count one stage in flight behind the awaited one");
+    if (n > 0) issue(g0, stageOf(0));
+    if (n > 1) issue(g0 + 1, stageOf(1));
+    for (uint32_t j = 0; j < n; ++j) {
+        if (j + 1 < n) wait_vm<kCopies>();
+        else wait_vm<0>();
+        __builtin_amdgcn_s_barrier();
+        if (j + NS - 1 < n) issue(g0 + j + NS - 1, stageOf(j + NS - 1));
+        compute(stageOf(j), g0 + j, j, j + 1 == n);
     }
 
     // C element i of lane l in tile (mi, ni): row (i / 4) * 8 + (l / 32) * 4 + i % 4, column l % 32
-    const uint32_t r = lane & 31, h = lane >> 5;
 #pragma unroll
     for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
         for (int ni = 0; ni < 2; ++ni) {
-            const uint32_t n = bn + wn + ni * 32 + r;
-            if (n >= N) continue;
+            const uint32_t col = bn + wn + ni * 32 + r;
+            if (col >= N) continue;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const uint32_t m = bm + wm + mi * 32 + (i / 4) * 8 + h * 4 + (i % 4);
                 if (m >= M) continue;
                 if constexpr (SPLIT) {
-                    P[((uint64_t)blockIdx.y * M + m) * N + n] = acc[mi][ni][i];
+                    P[((uint64_t)blockIdx.y * M + m) * N + col] = acc[mi][ni][i];
                 } else {
-                    C[(uint64_t)m * N + n] = O::store(acc[mi][ni][i]);
+                    C[(uint64_t)m * N + col] = O::store(acc[mi][ni][i]);
                 }
             }
         }

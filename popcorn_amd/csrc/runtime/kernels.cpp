@@ -1889,8 +1889,12 @@ std::unique_ptr<Kernel> Matmul(const Tensor &a, const AffineQuantizedTensor &b, 
                          (reinterpret_cast<uintptr_t>(b.scales.data) & 3) == 0 && (reinterpret_cast<uintptr_t>(bias.data) & 3) == 0;
     // a prompt's rows of bf16 activations: the matrix-core GEMM (one pass
     // over the weights for all rows instead of one matvec per row)
-    if (x == D::bf16 && m >= kQ4GemmMinRows && m * n * (k / 2) >= kQ4GemmMinBytes && aligned &&
-        m * (k / 64) <= (int64_t)UINT32_MAX && cdiv(m, 128) * cdiv(n, 128) <= (int64_t)UINT32_MAX)
+    // (buffer copies: every operand under 2^31 bytes; an even number of
+    // groups per row, so a group's scale and bias share a 32-bit word with
+    // a neighbour of the same row)
+    const int64_t lim = int64_t{1} << 31;
+    if (x == D::bf16 && m >= kQ4GemmMinRows && m * n * (k / 2) >= kQ4GemmMinBytes && aligned && k % 128 == 0 &&
+        m * k * 2 < lim && n * (k / 2) < lim && m * (k / 64) * 4 < lim && cdiv(m, 128) * cdiv(n, 128) <= (int64_t)UINT32_MAX)
         return std::make_unique<AffineQGemmKernel>(a, b, c, qc);
     DispatchSize ds;
     ds.block = dim3(kBlock, 1, 1);
