@@ -43,30 +43,33 @@ constexpr uint32_t kPairBase = 0x43004300u;
 // The bf16 of group g in the 32-bit word that holds groups g & ~1 and g | 1.
 __device__ inline float bf16_half(uint32_t v, uint32_t g) { return __uint_as_float((g & 1u) ? (v & 0xffff0000u) : (v << 16)); }
 
-// One thread per (row, group): X_g, and the row's 64 values in pair order.
+// One thread per run of 8 values (16 bytes): consecutive threads take
+// consecutive runs of a row, so a wave's loads and stores are 1 KB
+// contiguous; a group's 8 runs are 8 consecutive lanes (K % 64 == 0), whose
+// sums meet by lane swaps and whose first lane writes X_g. Runs are written
+// in pair order.
 __device__ void aq_gemm_prep(const uint16_t *__restrict__ X, uint16_t *__restrict__ Xp, float *__restrict__ Xs,
                              const AffineQMatmulConstants &p) {
-    const uint32_t G = p.kGroups;
+    const uint64_t runs = (uint64_t)p.M * (p.K / 8);
     const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= (uint64_t)p.M * G) return;
-    const uint64_t m = t / G, g = t % G;
-    const u32x4 *src = reinterpret_cast<const u32x4 *>(X + m * p.K + g * kGroup);
-    u32x4 *dst = reinterpret_cast<u32x4 *>(Xp + m * p.K + g * kGroup);
-    float sum = 0.0f;
-#pragma unroll
-    for (int c = 0; c < kGroup / 8; ++c) {
-        const u32x4 v = src[c];  // (x0, x1), (x2, x3), (x4, x5), (x6, x7)
-        sum += __uint_as_float(v.x << 16) + __uint_as_float(v.x & 0xffff0000u) + __uint_as_float(v.y << 16) +
-               __uint_as_float(v.y & 0xffff0000u) + __uint_as_float(v.z << 16) + __uint_as_float(v.z & 0xffff0000u) +
-               __uint_as_float(v.w << 16) + __uint_as_float(v.w & 0xffff0000u);
-        u32x4 o;  // (x0, x4), (x1, x5), (x2, x6), (x3, x7)
-        o.x = __builtin_amdgcn_perm(v.z, v.x, 0x05040100u);
-        o.y = __builtin_amdgcn_perm(v.z, v.x, 0x07060302u);
-        o.z = __builtin_amdgcn_perm(v.w, v.y, 0x05040100u);
-        o.w = __builtin_amdgcn_perm(v.w, v.y, 0x07060302u);
-        dst[c] = o;
-    }
-    Xs[t] = sum;
+    const bool live = t < runs;  // every lane takes part in the swaps
+    u32x4 v = {0u, 0u, 0u, 0u};  // (x0, x1), (x2, x3), (x4, x5), (x6, x7)
+    if (live) v = reinterpret_cast<const u32x4 *>(X)[t];
+    float sum = __uint_as_float(v.x << 16) + __uint_as_float(v.x & 0xffff0000u) + __uint_as_float(v.y << 16) +
+                __uint_as_float(v.y & 0xffff0000u) + __uint_as_float(v.z << 16) + __uint_as_float(v.z & 0xffff0000u) +
+                __uint_as_float(v.w << 16) + __uint_as_float(v.w & 0xffff0000u);
+    u32x4 o;  // (x0, x4), (x1, x5), (x2, x6), (x3, x7)
+    o.x = __builtin_amdgcn_perm(v.z, v.x, 0x05040100u);
+    o.y = __builtin_amdgcn_perm(v.z, v.x, 0x07060302u);
+    o.z = __builtin_amdgcn_perm(v.w, v.y, 0x05040100u);
+    o.w = __builtin_amdgcn_perm(v.w, v.y, 0x07060302u);
+    if (live) reinterpret_cast<u32x4 *>(Xp)[t] = o;
+    // the group's 8 lanes (a group starts at a multiple of 8 runs, and
+    // blocks hold whole groups)
+    sum += __shfl_xor(sum, 1);
+    sum += __shfl_xor(sum, 2);
+    sum += __shfl_xor(sum, 4);
+    if (live && (t & 7) == 0) Xs[t / 8] = sum;
 }
 
 // One stage per group, NS stages in flight, every tile copied buffer -> LDS

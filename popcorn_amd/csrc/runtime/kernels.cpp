@@ -1801,7 +1801,7 @@ public:
         enc.withTemporaryTensor(ScratchSpec{{m, k}, DataType::bf16}, [&](Tensor xp) {
             enc.withTemporaryTensor(ScratchSpec{{m, g}, DataType::f32}, [&](Tensor xs) {
                 FixedDispatch prep("aq_gemm_prep_bf16", {{a_, kRead}, {xp, kWrite}, {xs, kWrite}}, {bytesOf(qc_)},
-                                   grid1(cdiv(m * g, kBlock), kBlock));
+                                   grid1(cdiv(m * (k / 8), kBlock), kBlock));
                 enc.dispatch(prep);
                 const Tensor &bias = b_.hasBiases ? b_.biases : b_.scales;
                 if (s <= 1) {
