@@ -10,8 +10,8 @@
 // Partition outputs: O [B, Nq, Sq, P, Hd], m and l [B, Nq, Sq, P] (f32).
 //
 // Layout for gfx950 (fast path, flash_decoding_partial_<t>_l<LPK>_c<CPL>_g<G>):
-//  * one block (4 waves) per (partition, batch x KV head x head group, query
-//    row): the G query heads that share a KV head (GQA) are processed
+//  * one block (NW = 4 or 8 waves) per (partition, batch x KV head x head
+//    group, query row): the G query heads that share a KV head (GQA) are processed
 //    together, so each K/V byte is read once per block, not once per head;
 //  * a key row is split across LPK lanes, each holding CPL 16-byte chunks, so
 //    one wave-wide load instruction covers 64/LPK whole key rows (1 KB);
@@ -19,7 +19,7 @@
 //    lane in flight, dot products reduced within the LPK-lane group by DPP,
 //    tile max across the wave, then p = exp(s - m) and O += p V on the
 //    lane's own dims; l and O stay group-local until the end of the range;
-//  * waves take interleaved tiles of the partition's key range; the 4 wave
+//  * waves take interleaved tiles of the partition's key range; the NW wave
 //    states are merged in LDS and written as the partition's (O, m, l).
 // Host names: flash_decoding_partial_<t>, flash_decoding_reduce_<t> and the
 // plain flash_attention* keep the reference's names, parameter lists
@@ -142,10 +142,10 @@ struct NoFresh {};
 // heads (and, in the block owning key posQ, the key and value heads) in LDS,
 // applies the per-head RMSNorms and RoPE with the reference's rounding after
 // each step, writes the new K/V row to the caches (head group 0 only), and
-// turns the new key into a fifth softmax state (m = q.k, l = 1, O = v) that
-// the merge folds in with the four waves' states. The key loop covers keys
+// turns the new key into one more softmax state (m = q.k, l = 1, O = v) that
+// the merge folds in with the NW waves' states. The key loop covers keys
 // below posQ only.
-template <typename T, int LPK, int CPL, int GMAX, int U, bool FRESH = false, typename FA = NoFresh>
+template <typename T, int LPK, int CPL, int GMAX, int U, bool FRESH = false, typename FA = NoFresh, int NW = kWaves>
 __device__ void fd_partial_fast(const typename T::storage *__restrict__ Q, const typename T::storage *__restrict__ K,
                                 const typename T::storage *__restrict__ V, float *__restrict__ pO,
                                 float *__restrict__ pM, float *__restrict__ pL, const int32_t *__restrict__ position,
@@ -155,7 +155,7 @@ __device__ void fd_partial_fast(const typename T::storage *__restrict__ Q, const
     constexpr int HD = LPK * DL;   // head dim
     constexpr int KPW = 64 / LPK;  // key rows per wave-wide load
     constexpr int TILE = KPW * U;  // keys per wave step
-    constexpr int NSLOTS = kWaves + (FRESH ? 1 : 0);
+    constexpr int NSLOTS = NW + (FRESH ? 1 : 0);
     constexpr int kUnits = FRESH ? GMAX + 2 : 1;  // query heads, key head, value head
 
     __shared__ float sm_m[NSLOTS][GMAX];
@@ -186,7 +186,7 @@ __device__ void fd_partial_fast(const typename T::storage *__restrict__ Q, const
             if (live(u)) sm_x[u][d] = T::load(src(u)[d]);
         }
         __syncthreads();
-        for (uint32_t u = wave; u < (uint32_t)kUnits; u += kWaves) {
+        for (uint32_t u = wave; u < (uint32_t)kUnits; u += NW) {
             if (!live(u)) continue;
             float acc = 0.0f;
             for (uint32_t d = lane; d < (uint32_t)HD; d += 64) acc += sm_x[u][d] * sm_x[u][d];
@@ -238,7 +238,7 @@ __device__ void fd_partial_fast(const typename T::storage *__restrict__ Q, const
         }
         __syncthreads();
         // the new key's state per query head: m = q.k, l = 1, O = v
-        for (uint32_t g = wave; g < (uint32_t)GMAX; g += kWaves) {
+        for (uint32_t g = wave; g < (uint32_t)GMAX; g += NW) {
             const bool has = geo.owner && g < geo.gcount;
             float acc = 0.0f;
             if (has) {
@@ -246,10 +246,10 @@ __device__ void fd_partial_fast(const typename T::storage *__restrict__ Q, const
                 acc = pk::wave_sum(acc);
             }
             if (lane == 0) {
-                sm_m[kWaves][g] = has ? acc : -INFINITY;
-                sm_l[kWaves][g] = has ? 1.0f : 0.0f;
+                sm_m[NW][g] = has ? acc : -INFINITY;
+                sm_l[NW][g] = has ? 1.0f : 0.0f;
             }
-            for (uint32_t d = lane; d < (uint32_t)HD; d += 64) sm_o[kWaves][g][d] = has ? sm_x[GMAX + 1][d] : 0.0f;
+            for (uint32_t d = lane; d < (uint32_t)HD; d += 64) sm_o[NW][g][d] = has ? sm_x[GMAX + 1][d] : 0.0f;
         }
     }
 
@@ -286,7 +286,7 @@ __device__ void fd_partial_fast(const typename T::storage *__restrict__ Q, const
     const uint32_t nkeys = geo.jHi - geo.jLo;
     const uint32_t ntiles = (nkeys + TILE - 1) / TILE;
 
-    for (uint32_t t = wave; t < ntiles; t += kWaves) {
+    for (uint32_t t = wave; t < ntiles; t += NW) {
         const uint32_t j0 = geo.jLo + t * TILE;
         pk::Vec<T> kv[U][CPL], vv[U][CPL];
         bool valid[U];
@@ -728,20 +728,20 @@ __device__ void fd_reduce_ref(const float *__restrict__ pO, const float *__restr
 
 }  // namespace
 
-#define FD_FAST(name, T, LPK, CPL, G, U)                                                                   \
-    POPCORN_KERNEL void __launch_bounds__(256)                                                             \
+#define FD_FAST(name, T, LPK, CPL, G, U, NW)                                                               \
+    POPCORN_KERNEL void __launch_bounds__(64 * NW)                                                         \
         name(const T::storage *q, const T::storage *k, const T::storage *v, float *pO, float *pM, float *pL, \
              const int32_t *position, FlashDecodingPartialExtConstants p) {                                    \
-        fd_partial_fast<T, LPK, CPL, G, U>(q, k, v, pO, pM, pL, position, p);                               \
+        fd_partial_fast<T, LPK, CPL, G, U, false, NoFresh, NW>(q, k, v, pO, pM, pL, position, p);           \
     }
 
-#define FD_FRESH(name, T, LPK, CPL, G, U)                                                                  \
-    POPCORN_KERNEL void __launch_bounds__(256)                                                             \
+#define FD_FRESH(name, T, LPK, CPL, G, U, NW)                                                              \
+    POPCORN_KERNEL void __launch_bounds__(64 * NW)                                                         \
         name(const T::storage *qkv, T::storage *k, T::storage *v, float *pO, float *pM, float *pL,          \
              const int32_t *position, const float *wq, const float *wk, const float *invFreq,                \
              FlashDecodingPartialExtConstants p, DecodeAttentionConstants c) {                                 \
         FreshArgs<T> fa{k, v, wq, wk, invFreq, c};                                                          \
-        fd_partial_fast<T, LPK, CPL, G, U, true>(qkv, k, v, pO, pM, pL, position, p, fa);                   \
+        fd_partial_fast<T, LPK, CPL, G, U, true, FreshArgs<T>, NW>(qkv, k, v, pO, pM, pL, position, p, fa);  \
     }
 
 #define FD_GENERIC(name, T)                                                                                 \
@@ -803,9 +803,21 @@ FD_REF(flash_decoding_partial_f16, flash_decoding_reduce_f16, F16)
 // the per-lane state (q, o for G heads) within the register file.
 // Each partial kernel has a fresh-key twin (flash_decoding_fresh_*) for the
 // decode attention block.
+// The 2-byte types also get 8-wave twins (suffix _w8): the host gives them
+// half the partitions of the 4-wave kernels, so the grid keeps its waves in
+// half as many blocks, each covering twice the keys.
+#define FD_W8_ON(T, t, LPK, CPL, G, U)                                                          \
+    FD_FAST(flash_decoding_partial_##t##_l##LPK##_c##CPL##_g##G##_w8, T, LPK, CPL, G, U, 8)     \
+    FD_FRESH(flash_decoding_fresh_##t##_l##LPK##_c##CPL##_g##G##_w8, T, LPK, CPL, G, U, 8)
+#define FD_W8_OFF(T, t, LPK, CPL, G, U)
+#define FD_W8_BF16 FD_W8_ON
+#define FD_W8_F16 FD_W8_ON
+#define FD_W8_F32 FD_W8_OFF
+#define FD_W8(T, t, LPK, CPL, G, U) FD_W8_##T(T, t, LPK, CPL, G, U)
 #define FD_BOTH(T, t, LPK, CPL, G, U)                                                \
-    FD_FAST(flash_decoding_partial_##t##_l##LPK##_c##CPL##_g##G, T, LPK, CPL, G, U)  \
-    FD_FRESH(flash_decoding_fresh_##t##_l##LPK##_c##CPL##_g##G, T, LPK, CPL, G, U)
+    FD_FAST(flash_decoding_partial_##t##_l##LPK##_c##CPL##_g##G, T, LPK, CPL, G, U, 4)  \
+    FD_FRESH(flash_decoding_fresh_##t##_l##LPK##_c##CPL##_g##G, T, LPK, CPL, G, U, 4)  \
+    FD_W8(T, t, LPK, CPL, G, U)
 #define FD_FAST_G4(T, t, LPK, CPL, U1, U2, U4) \
     FD_BOTH(T, t, LPK, CPL, 1, U1)              \
     FD_BOTH(T, t, LPK, CPL, 2, U2)              \

@@ -95,6 +95,12 @@ int fdMinKeys() {
     static const int v = envInt("POPCORN_FD_MIN_KEYS", 1, 4096, 64);
     return v;
 }
+// Waves per block of the 16-bit split-KV kernels: 0 (chosen per shape, the
+// default), or forced to 4 or 8 for tuning.
+int fdWaves16() {
+    static const int v = envInt("POPCORN_FD_WAVES", 4, 8, 0);
+    return v == 4 || v == 8 ? v : 0;
+}
 
 struct AttnDims {
     int64_t B, Nq, Nkv, Sq, Sk, Hd, cap;
@@ -104,11 +110,13 @@ struct AttnDims {
 // generic kernel), chunks per lane, query heads per block, head groups per
 // KV head and partitions per query row.
 struct FdPlan {
-    int lpk = 0, cpl = 1, gmax = 1;
+    int lpk = 0, cpl = 1, gmax = 1, waves = 4;
     int64_t ngroups = 1, P = 1;
-    std::string suffix() const {  // "<t>_l<LPK>_c<CPL>_g<G>" without the dtype
-        return "_l" + std::to_string(lpk) + "_c" + std::to_string(cpl) + "_g" + std::to_string(gmax);
+    std::string suffix() const {  // "<t>_l<LPK>_c<CPL>_g<G>[_w8]" without the dtype
+        return "_l" + std::to_string(lpk) + "_c" + std::to_string(cpl) + "_g" + std::to_string(gmax) +
+               (waves == 8 ? "_w8" : "");
     }
+    int64_t block() const { return 64 * waves; }
 };
 
 FdPlan fdPlan(DataType t, const AttnDims &d, bool alignedOk, int64_t keys) {
@@ -136,6 +144,20 @@ FdPlan fdPlan(DataType t, const AttnDims &d, bool alignedOk, int64_t keys) {
     const int64_t want = cdiv(fdBlocksPerCU() * deviceCUs(), base);
     const int64_t maxByKeys = cdiv(std::max<int64_t>(keys, 1), fdMinKeys());
     f.P = std::clamp<int64_t>(std::min(want, maxByKeys), 1, 1024);
+    // 16-bit kernels: 8 waves per block over half the partitions (the same
+    // waves, each block twice the keys) when the keys set P and the 4-wave
+    // grid would put more than one block on some CU. Measured at config 4
+    // (68 -> 34 partitions): 6.85-7.07 us against 7.57-7.75 in the decode
+    // step; where the 4-wave grid fits the CUs (B 1, 2048 keys) or P is set
+    // by the CU count, 8 waves measured no faster or slower.
+    if (f.lpk && t != DataType::f32) {
+        const int forced = fdWaves16();
+        const bool pick = forced ? forced == 8 : maxByKeys < want && base * f.P > deviceCUs();
+        if (pick) {
+            f.waves = 8;
+            f.P = cdiv(f.P, 2);
+        }
+    }
     return f;
 }
 
@@ -330,7 +352,7 @@ public:
         pc.keyLenFromPosition = hasPos_ ? 1u : 0u;
         DispatchSize ds;
         ds.grid = dim3((unsigned)P_, (unsigned)(d_.B * d_.Nkv * ngroups_), (unsigned)d_.Sq);
-        ds.block = dim3(kBlock, 1, 1);
+        ds.block = dim3((unsigned)partialBlock_, 1, 1);
         // the position binding is read only when keyLenFromPosition
         Tensor posOrDummy = hasPos_ ? pos_ : q_;
         FixedDispatch partial(partialName_,
@@ -401,6 +423,7 @@ private:
         const bool alignedOk = aligned16(q_.data) && aligned16(k_.data) && aligned16(v_.data);
         const FdPlan f = fdPlan(t, d_, alignedOk, hasPos_ ? d_.cap : d_.Sk);
         partialName_ = std::string("flash_decoding_partial_") + tag(t) + (f.lpk ? f.suffix() : std::string("_ext"));
+        partialBlock_ = f.lpk ? f.block() : kBlock;
         reduceName_ = std::string("flash_decoding_reduce_") + tag(out_.dataType) + "_ext";
         ngroups_ = f.ngroups;
         P_ = f.P;
@@ -413,6 +436,7 @@ private:
     bool hasPos_;
     Kernels::AttentionPath path_ = Kernels::AttentionPath::plain;
     std::string partialName_, reduceName_, tiledName_, mergeName_;
+    int64_t partialBlock_ = kBlock;
     int64_t nSplit_ = 0;
     bool pairTiles_ = false;
     bool rows16_ = false;  // the 16-rows-per-wave kernel: 8 waves per 128-row tile (4 per 64 at Hd 512 and in f32)
@@ -529,7 +553,7 @@ public:
                     pc.keyLenFromPosition = 1;
                     DispatchSize ds;
                     ds.grid = dim3((unsigned)P, (unsigned)(d_.B * d_.Nkv * plan_.ngroups), 1);
-                    ds.block = dim3(kBlock, 1, 1);
+                    ds.block = dim3((unsigned)plan_.block(), 1, 1);
                     FixedDispatch partial(partialName_,
                                           {{qkv_, kRead}, {k_, kReadWrite}, {v_, kReadWrite}, {pO, kWrite}, {pM, kWrite},
                                            {pL, kWrite}, {pos_, kRead}, {wq_, kRead}, {wk_, kRead}, {invf_, kRead}},

@@ -151,7 +151,17 @@ def test_flash_attention_routing_names():
     k = T([1, 4, 4352, 256])
     kern = pa.Kernels.FlashAttention(q, k, k, out=o, scale=1 / 16, batch=1, query_heads=8, kv_heads=4,
                                      query_len=1, key_len=4097, head_dim=256, key_capacity=4352)
-    assert kern.function_names == ["flash_decoding_partial_bf16_l32_c1_g2", "flash_decoding_reduce_bf16_ext"]
+    assert kern.function_names == ["flash_decoding_partial_bf16_l32_c1_g2_w8", "flash_decoding_reduce_bf16_ext"]
+    # 8 waves only where the keys set P and 4-wave blocks would overflow the
+    # CUs: 2048 keys (32 partitions x 4 KV heads) and batch 8 (P set by the
+    # CU count) keep 4 waves
+    short = pa.Kernels.FlashAttention(q, T([1, 4, 2048, 256]), T([1, 4, 2048, 256]), out=o, scale=1 / 16, batch=1,
+                                      query_heads=8, kv_heads=4, query_len=1, key_len=2048, head_dim=256)
+    assert short.function_names[0] == "flash_decoding_partial_bf16_l32_c1_g2"
+    k8 = T([8, 4, 8192, 256], "f16")
+    wide = pa.Kernels.FlashAttention(T([8, 8, 1, 256], "f16"), k8, k8, out=T([8, 8, 1, 256], "f16"), scale=1 / 16,
+                                     batch=8, query_heads=8, kv_heads=4, query_len=1, key_len=8192, head_dim=256)
+    assert wide.function_names[0] == "flash_decoding_partial_f16_l32_c1_g2"
     f = pa.Kernels.FlashAttention(T([1, 4, 1, 64], "f32"), T([1, 1, 129, 64], "f32"), T([1, 1, 129, 64], "f32"),
                                   T([1, 4, 1, 64], "f32"), scale=0.125)
     assert f.function_names[0] == "flash_decoding_partial_f32_l16_c1_g4"

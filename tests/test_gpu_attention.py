@@ -52,7 +52,7 @@ def test_gemma_decode_bf16_with_capacity(env):
     # config 4 shape: 8 q heads, 4 KV heads (GQA 2:1), Hd 256, cache capacity 4352, 4097 keys used
     q, k, v = _inputs(200, 1, 8, 4, 1, 4352, 256, "bf16")
     got, kern = _attend(env, q, k, v, "bf16", "bf16", 1 / 16, key_len=4097)
-    assert kern.function_names == ["flash_decoding_partial_bf16_l32_c1_g2", "flash_decoding_reduce_bf16_ext"]
+    assert kern.function_names == ["flash_decoding_partial_bf16_l32_c1_g2_w8", "flash_decoding_reduce_bf16_ext"]
     assert_out(got, O.attention_naive(q, k, v, 1 / 16, key_len=4097), EPS["bf16"], "bf16", "gemma decode")
 
 
